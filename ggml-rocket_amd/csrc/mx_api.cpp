@@ -1,0 +1,156 @@
+// SPDX-License-Identifier: MIT
+// The C ABI of the kernel library (include/mi355x_kernels.h): argument checks, HIP error
+// mapping and launches. Nothing here allocates device memory.
+
+#include "../../include/mi355x_kernels.h"
+
+#include <hip/hip_runtime.h>
+#include <stdio.h>
+#include <string.h>
+
+#include "mx_kernels_impl.h"
+#include "mx_weights.h"
+
+namespace {
+
+inline hipStream_t S(void * s) { return (hipStream_t)s; }
+
+inline int hip_status(hipError_t e) {
+    if (e == hipSuccess) return MI355X_OK;
+    fprintf(stderr, "[mi355x] HIP error: %s\n", hipGetErrorString(e));
+    return MI355X_E_DEVICE;
+}
+
+inline bool known_wtype(int wt) {
+    return wt == mx::T_F16 || wt == mx::T_Q8_0 || wt == mx::T_Q4_K || wt == mx::T_Q6_K;
+}
+
+inline int64_t blck(int wt) { return (wt == mx::T_Q4_K || wt == mx::T_Q6_K) ? 256 : (wt == mx::T_Q8_0 ? 32 : 1); }
+
+inline bool aligned(const void * p, size_t a) { return ((uintptr_t)p % a) == 0; }
+
+}  // namespace
+
+extern "C" {
+
+MI355X_API const char * mi355x_status_str(int st) {
+    switch (st) {
+        case MI355X_OK: return "ok";
+        case MI355X_E_ARG: return "invalid argument";
+        case MI355X_E_DEVICE: return "device error";
+        case MI355X_E_UNSUPPORTED: return "unsupported";
+        case MI355X_E_NOMEM: return "workspace too small";
+        case MI355X_E_IDS: return "expert id out of range";
+        default: return "unknown status";
+    }
+}
+
+MI355X_API int mi355x_get_device_info(mi355x_device_info * out) {
+    if (!out) return MI355X_E_ARG;
+    memset(out, 0, sizeof(*out));
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return hip_status(e);
+    hipDeviceProp_t p;
+    e = hipGetDeviceProperties(&p, dev);
+    if (e != hipSuccess) return hip_status(e);
+    snprintf(out->name, sizeof(out->name), "%s", p.gcnArchName);
+    out->compute_units = p.multiProcessorCount;
+    out->lds_bytes_per_block = (int)p.sharedMemPerBlock;
+    out->clock_khz = p.clockRate;
+    size_t fr = 0, tot = 0;
+    if (hipMemGetInfo(&fr, &tot) == hipSuccess) {
+        out->hbm_free = fr;
+        out->hbm_total = tot;
+    }
+    return MI355X_OK;
+}
+
+MI355X_API int64_t mi355x_weight_bytes(int wtype, int64_t rows, int64_t K) {
+    if (!known_wtype(wtype) || rows < 0 || K <= 0 || K % blck(wtype)) return -1;
+    return mx::packed_weight_bytes(wtype, rows, K);
+}
+
+MI355X_API int mi355x_weight_pack(int wtype, const void * src_dev, int64_t rows, int64_t K,
+                                  void * dst_dev, void * stream) {
+    if (!known_wtype(wtype) || rows < 0 || K <= 0 || K % blck(wtype) || K % 32) return MI355X_E_ARG;
+    if (rows == 0) return MI355X_OK;
+    if (!src_dev || !dst_dev) return MI355X_E_ARG;
+    if ((wtype == mx::T_Q8_0 || wtype == mx::T_Q6_K) && src_dev == dst_dev) return MI355X_E_ARG;
+    return hip_status(mx::launch_pack_weight(wtype, src_dev, rows, K, dst_dev, S(stream)));
+}
+
+MI355X_API int mi355x_weight_dequant_f16(int wtype, const void * w_dev, int64_t rows, int64_t K,
+                                         uint16_t * out_dev, void * stream) {
+    if (!known_wtype(wtype) || rows < 0 || K <= 0 || K % blck(wtype) || K % 64) return MI355X_E_ARG;
+    if (rows == 0) return MI355X_OK;
+    if (!w_dev || !out_dev || !aligned(w_dev, 16) || !aligned(out_dev, 16)) return MI355X_E_ARG;
+    return hip_status(mx::launch_dequant_f16(wtype, w_dev, rows, K, out_dev, S(stream)));
+}
+
+MI355X_API int mi355x_pack_act(const float * x_dev, int64_t ldx, int64_t M, int64_t K,
+                               uint16_t * a16_dev, float * scales_dev, void * stream) {
+    if (M < 0 || K <= 0 || K % 4 || ldx < K || ldx % 4 || M > INT32_MAX || K > INT32_MAX) return MI355X_E_ARG;
+    if (M == 0) return MI355X_OK;
+    if (!x_dev || !a16_dev || !scales_dev || !aligned(x_dev, 16) || !aligned(a16_dev, 8)) return MI355X_E_ARG;
+    return hip_status(mx::launch_pack_act(x_dev, ldx, (int)M, (int)K, a16_dev, K, scales_dev, S(stream)));
+}
+
+MI355X_API int mi355x_gemm(int wtype, const uint16_t * a16_dev, const float * scales_dev,
+                           int64_t M, int64_t K, const mi355x_gemm_out * outs, int n_out,
+                           void * stream) {
+    if (!known_wtype(wtype) || M < 0 || K <= 0 || K % 32 || K % blck(wtype) || M > INT32_MAX || K > INT32_MAX)
+        return MI355X_E_ARG;
+    if (n_out < 1 || n_out > mx::GEMM_MAX_GROUPS || !outs) return MI355X_E_ARG;
+    if (M == 0) return MI355X_OK;
+    if (!a16_dev || !scales_dev || !aligned(a16_dev, 16)) return MI355X_E_ARG;
+    mx::GemmArgs a;
+    memset(&a, 0, sizeof(a));
+    a.A = a16_dev;
+    a.scales = scales_dev;
+    a.lda = K;
+    a.M = (int)M;
+    a.K = (int)K;
+    a.m_tiles = (int)((M + 127) / 128);
+    a.ng = n_out;
+    int nt = 0;
+    for (int i = 0; i < n_out; i++) {
+        const mi355x_gemm_out & o = outs[i];
+        if (!o.w_dev || !o.c_dev || o.N <= 0 || o.N % 16 || o.N > INT32_MAX || o.ldc < o.N || o.row0 < 0 ||
+            o.rows_total < o.row0 + o.N || !aligned(o.w_dev, 16))
+            return MI355X_E_ARG;
+        a.g[i].W = o.w_dev;
+        a.g[i].rows_total = o.rows_total;
+        a.g[i].row0 = o.row0;
+        a.g[i].N = (int)o.N;
+        a.g[i].C = o.c_dev;
+        a.g[i].ldc = o.ldc;
+        a.g[i].ntile_begin = nt;
+        nt += (int)((o.N + 127) / 128);
+    }
+    return hip_status(mx::launch_gemm(wtype, a, nt, S(stream)));
+}
+
+MI355X_API size_t mi355x_mul_mat_workspace(int64_t M, int64_t K) {
+    if (M <= 0 || K <= 0) return 0;
+    const size_t a16 = ((size_t)M * (size_t)K * 2 + 255) & ~(size_t)255;
+    return a16 + (size_t)M * 4;
+}
+
+MI355X_API int mi355x_mul_mat(int wtype, const void * w_dev, int64_t N, int64_t K,
+                              const float * x_dev, int64_t ldx, int64_t M,
+                              float * dst_dev, int64_t ldd,
+                              void * workspace_dev, size_t workspace_bytes, void * stream) {
+    if (M == 0) return MI355X_OK;
+    const size_t need = mi355x_mul_mat_workspace(M, K);
+    if (need == 0) return MI355X_E_ARG;
+    if (!workspace_dev || workspace_bytes < need) return MI355X_E_NOMEM;
+    uint16_t * a16 = (uint16_t *)workspace_dev;
+    float * scales = (float *)((char *)workspace_dev + (((size_t)M * (size_t)K * 2 + 255) & ~(size_t)255));
+    int st = mi355x_pack_act(x_dev, ldx, M, K, a16, scales, stream);
+    if (st != MI355X_OK) return st;
+    mi355x_gemm_out o = {w_dev, N, 0, N, dst_dev, ldd};
+    return mi355x_gemm(wtype, a16, scales, M, K, &o, 1, stream);
+}
+
+}  // extern "C"

@@ -1,0 +1,74 @@
+// SPDX-License-Identifier: MIT
+// Device-side helpers shared by the gfx950 kernels: vector types, MFMA wrappers, the LDS
+// swizzle, fp16 conversion and the exact-rounding arithmetic the weight decoders use.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace mx {
+
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef _Float16 half4 __attribute__((ext_vector_type(4)));
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+typedef float float16v __attribute__((ext_vector_type(16)));
+typedef float float4v __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+constexpr int WAVE = 64;
+
+// ggml type ids (ggml.h enum ggml_type) for the weight formats this path decodes.
+enum : int { T_F32 = 0, T_F16 = 1, T_Q8_0 = 8, T_Q4_K = 12, T_Q6_K = 14, T_I32 = 26, T_BF16 = 30 };
+
+// D(32x32, f32) += A(32x16, f16) . B(16x32, f16). Lane l holds A row (l % 32) and B column
+// (l % 32), K slots 8*(l/32)+0..7. D: lane l, element i -> row 8*(i/4) + 4*(l/32) + (i%4),
+// column l % 32.
+__device__ __forceinline__ float16v mfma32(const half8 & a, const half8 & b, const float16v & c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+}
+
+// Byte offset of the 16-byte chunk `c` of row `r` in an LDS tile whose rows hold `chunks`
+// 16-byte chunks (chunks a power of two >= 8). The chunk index is XORed with the row's low
+// three bits, so the 32 rows one MFMA fragment read touches spread over every bank.
+template <int CHUNKS>
+__device__ __forceinline__ int swz(int r, int c) {
+    return r * (CHUNKS * 16) + ((c ^ (r & 7)) << 4);
+}
+
+__device__ __forceinline__ uint16_t f2h_bits(float f) {
+    _Float16 h = (_Float16)f;   // v_cvt_f16_f32, round to nearest even
+    return __builtin_bit_cast(uint16_t, h);
+}
+__device__ __forceinline__ float h2f_bits(uint16_t b) {
+    return (float)__builtin_bit_cast(_Float16, b);
+}
+__device__ __forceinline__ uint32_t pack2h(float a, float b) {
+    return (uint32_t)f2h_bits(a) | ((uint32_t)f2h_bits(b) << 16);
+}
+
+// Separately rounded multiply and subtract: the decoders must not fuse d*q - m into one FMA,
+// because the CPU dequantizer rounds the product before the subtraction.
+__device__ __forceinline__ float mul_rn(float a, float b) { return __fmul_rn(a, b); }
+__device__ __forceinline__ float sub_rn(float a, float b) { return __fsub_rn(a, b); }
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, WAVE));
+    return v;
+}
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, WAVE);
+    return v;
+}
+
+// Blocks are handed to the 8 XCDs round-robin by linear id. Renumber so that each XCD gets a
+// contiguous run of tile ids: tiles that share a weight panel then share one L2.
+__device__ __forceinline__ int xcd_tile(int bid, int nblocks) {
+    const int per = nblocks / 8;
+    if (per == 0 || (nblocks % 8)) return bid;
+    return (bid % 8) * per + bid / 8;
+}
+
+}  // namespace mx

@@ -1,0 +1,40 @@
+// SPDX-License-Identifier: MIT
+// Launch interfaces between the C ABI (mx_api.cpp) and the kernel translation units.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace mx {
+
+constexpr int GEMM_MAX_GROUPS = 4;
+
+// One weight of a (possibly fused) GEMM launch: its panel, its output, and where its N tiles
+// start in the launch's concatenated N.
+struct GemmGroup {
+    const void * W;        // HBM weight, layout per mx_weights.h
+    int64_t rows_total;    // rows of the whole panel W (the split layouts index planes by it)
+    int64_t row0;          // first row of this weight inside the panel
+    int N;                 // rows used (output columns)
+    float * C;             // output [M][ldc]
+    int64_t ldc;
+    int ntile_begin;       // first global N tile of this group
+};
+
+struct GemmArgs {
+    const uint16_t * A;    // fp16 activations [M][lda], row-scaled
+    const float * scales;  // [M]
+    int64_t lda;
+    int M, K;
+    int m_tiles;
+    int ng;
+    GemmGroup g[GEMM_MAX_GROUPS];
+};
+
+hipError_t launch_pack_act(const float * X, int64_t ldx, int M, int K, uint16_t * A16, int64_t lda,
+                           float * scales, hipStream_t st);
+hipError_t launch_gemm(int wt, const GemmArgs & a, int n_tiles_total, hipStream_t st);
+hipError_t launch_dequant_f16(int wt, const void * W, int64_t rows, int64_t K, uint16_t * out, hipStream_t st);
+hipError_t launch_pack_weight(int wt, const void * src, int64_t rows, int64_t K, void * dst, hipStream_t st);
+
+}  // namespace mx

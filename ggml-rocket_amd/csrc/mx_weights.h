@@ -1,0 +1,210 @@
+// SPDX-License-Identifier: MIT
+// Weight formats in HBM and their on-the-fly decoders.
+//
+// A weight panel is `rows` rows of K values. The layouts are:
+//   F16   [rows][K] fp16, the ggml payload unchanged (zero copy).
+//   Q4_K  [rows][K/256] blocks of 144 B, the ggml payload unchanged: { fp16 d, fp16 dmin,
+//         u8 scales[12], u8 qs[128] }. Every block starts on a 16-byte boundary.
+//   Q8_0  split into two planes so every load is 16-byte aligned (a 34-byte ggml block is only
+//         2-byte aligned): qs int8 [rows][K] at 0, then d fp16 [rows][K/32].
+//   Q6_K  split into four planes for the same reason (a ggml block is 210 B): ql [rows][K/2]
+//         at 0, qh [rows][K/4] at rows*K/2, scales int8 [rows][K/16] at rows*K*3/4, then
+//         d fp16 [rows][K/256] at rows*K*13/16.
+// The split layouts hold exactly the ggml bytes, re-ordered; their size equals the ggml size.
+//
+// Decoding follows ggml's dequantizers value for value (the to_float contract the reference
+// uses at ggml-rocket.cpp:3894-3906): Q8_0 y = d*q; Q4_K y = (d*sc)*q - dmin*m; Q6_K
+// y = (d*sc)*(q-32). Each product and difference is rounded on its own, then the f32 result is
+// rounded once to fp16 (ggml_fp32_to_fp16_row, 3907).
+#pragma once
+
+#include "mx_common.h"
+
+namespace mx {
+
+__host__ __device__ inline int64_t packed_weight_bytes(int wt, int64_t rows, int64_t K) {
+    switch (wt) {
+        case T_F16: return rows * K * 2;
+        case T_Q8_0: return rows * K + rows * (K / 32) * 2;
+        case T_Q4_K: return rows * (K / 256) * 144;
+        case T_Q6_K: return rows * (K / 256) * 210;
+        default: return -1;
+    }
+}
+
+// The 6-bit (scale, min) pair j of a Q4_K block, from its 12 packed bytes held as three
+// little-endian words s0 (bytes 0-3), s1 (4-7), s2 (8-11).
+__device__ __forceinline__ void q4k_sm(int j, uint32_t s0, uint32_t s1, uint32_t s2, int & sc, int & mn) {
+    auto byte = [&](int i) -> uint32_t {
+        const uint32_t w = i < 4 ? s0 : (i < 8 ? s1 : s2);
+        return (w >> (8 * (i & 3))) & 0xFFu;
+    };
+    if (j < 4) {
+        sc = (int)(byte(j) & 63u);
+        mn = (int)(byte(j + 4) & 63u);
+    } else {
+        sc = (int)((byte(j + 4) & 0x0Fu) | ((byte(j - 4) >> 6) << 4));
+        mn = (int)((byte(j + 4) >> 4) | ((byte(j) >> 6) << 4));
+    }
+}
+
+// Global-load stage of one thread's share of a BK=64 weight tile: 32 consecutive-in-format
+// values of one row. `u` (0/1) selects which half of the row's 64 values the thread takes.
+template <int WT> struct WLoad;
+
+template <> struct WLoad<T_F16> {
+    u32x4 v[4];   // 32 fp16 values, k = k0 + 32u + 0..31
+    __device__ __forceinline__ void load(const uint8_t * W, int64_t rows, int64_t K, int64_t row,
+                                         int64_t k0, int u, bool ok) {
+        const int64_t k = k0 + 32 * u;
+        ok = ok && k < K;
+        const u32x4 * p = (const u32x4 *)(W + (row * K + k) * 2);
+#pragma unroll
+        for (int i = 0; i < 4; i++) v[i] = ok ? p[i] : u32x4{0, 0, 0, 0};
+    }
+    // Writes the two 16-value runs: run0 at k_local = 32u, run1 at 32u + 16.
+    __device__ __forceinline__ void decode(int u, u32x4 out[4], int & run0, int & run1) const {
+#pragma unroll
+        for (int i = 0; i < 4; i++) out[i] = v[i];
+        run0 = 32 * u;
+        run1 = 32 * u + 16;
+    }
+};
+
+template <> struct WLoad<T_Q8_0> {
+    u32x4 q[2];
+    uint16_t d;
+    __device__ __forceinline__ void load(const uint8_t * W, int64_t rows, int64_t K, int64_t row,
+                                         int64_t k0, int u, bool ok) {
+        const int64_t k = k0 + 32 * u;   // one 32-value block
+        ok = ok && k < K;
+        const u32x4 * p = (const u32x4 *)(W + row * K + k);
+        const uint16_t * dp = (const uint16_t *)(W + rows * K) + row * (K / 32) + k / 32;
+        q[0] = ok ? p[0] : u32x4{0, 0, 0, 0};
+        q[1] = ok ? p[1] : u32x4{0, 0, 0, 0};
+        d = ok ? *dp : (uint16_t)0;
+    }
+    __device__ __forceinline__ void decode(int u, u32x4 out[4], int & run0, int & run1) const {
+        const float df = h2f_bits(d);
+        uint32_t o[16];
+#pragma unroll
+        for (int w = 0; w < 8; w++) {
+            const uint32_t word = q[w / 4][w % 4];
+            float f[4];
+#pragma unroll
+            for (int b = 0; b < 4; b++) f[b] = mul_rn(df, (float)(int8_t)((word >> (8 * b)) & 0xFFu));
+            o[2 * w] = pack2h(f[0], f[1]);
+            o[2 * w + 1] = pack2h(f[2], f[3]);
+        }
+#pragma unroll
+        for (int i = 0; i < 4; i++) out[i] = u32x4{o[4 * i], o[4 * i + 1], o[4 * i + 2], o[4 * i + 3]};
+        run0 = 32 * u;
+        run1 = 32 * u + 16;
+    }
+};
+
+template <> struct WLoad<T_Q4_K> {
+    u32x4 hdr;   // d, dmin, scales[12]
+    u32x4 qs;    // 16 bytes of nibbles
+    int j;       // quarter of the block (0..3)
+    __device__ __forceinline__ void load(const uint8_t * W, int64_t rows, int64_t K, int64_t row,
+                                         int64_t k0, int u, bool ok) {
+        const int64_t blk = k0 / 256;
+        j = (int)((k0 % 256) / 64);
+        const uint8_t * b = W + (row * (K / 256) + blk) * 144;
+        hdr = ok ? *(const u32x4 *)b : u32x4{0, 0, 0, 0};
+        qs = ok ? *(const u32x4 *)(b + 16 + 32 * j + 16 * u) : u32x4{0, 0, 0, 0};
+    }
+    // Byte b of qs (b = 0..15) is q[32j + 16u + b]: its low nibble is weight 64j + 16u + b
+    // (sub-block 2j), its high nibble weight 64j + 32 + 16u + b (sub-block 2j+1).
+    __device__ __forceinline__ void decode(int u, u32x4 out[4], int & run0, int & run1) const {
+        const float d = h2f_bits((uint16_t)(hdr[0] & 0xFFFFu));
+        const float dmin = h2f_bits((uint16_t)(hdr[0] >> 16));
+        int s0, m0, s1, m1;
+        q4k_sm(2 * j, hdr[1], hdr[2], hdr[3], s0, m0);
+        q4k_sm(2 * j + 1, hdr[1], hdr[2], hdr[3], s1, m1);
+        const float d0 = mul_rn(d, (float)s0), mm0 = mul_rn(dmin, (float)m0);
+        const float d1 = mul_rn(d, (float)s1), mm1 = mul_rn(dmin, (float)m1);
+        uint32_t lo[8], hi[8];
+#pragma unroll
+        for (int w = 0; w < 4; w++) {
+            const uint32_t word = qs[w];
+#pragma unroll
+            for (int p = 0; p < 2; p++) {
+                const uint32_t b0 = (word >> (16 * p)) & 0xFFu, b1 = (word >> (16 * p + 8)) & 0xFFu;
+                lo[2 * w + p] = pack2h(sub_rn(mul_rn(d0, (float)(b0 & 15u)), mm0),
+                                       sub_rn(mul_rn(d0, (float)(b1 & 15u)), mm0));
+                hi[2 * w + p] = pack2h(sub_rn(mul_rn(d1, (float)(b0 >> 4)), mm1),
+                                       sub_rn(mul_rn(d1, (float)(b1 >> 4)), mm1));
+            }
+        }
+        out[0] = u32x4{lo[0], lo[1], lo[2], lo[3]};
+        out[1] = u32x4{lo[4], lo[5], lo[6], lo[7]};
+        out[2] = u32x4{hi[0], hi[1], hi[2], hi[3]};
+        out[3] = u32x4{hi[4], hi[5], hi[6], hi[7]};
+        run0 = 16 * u;
+        run1 = 32 + 16 * u;
+    }
+};
+
+template <> struct WLoad<T_Q6_K> {
+    u32x4 qla, qlb, qh;   // ql[l], ql[l+32], qh[l] for the thread's 16 l
+    uint32_t sc;          // the 4 int8 scales it needs, packed
+    uint16_t d;
+    int hi;               // 0: weights l, l+32 of the half; 1: l+64, l+96
+    __device__ __forceinline__ void load(const uint8_t * W, int64_t rows, int64_t K, int64_t row,
+                                         int64_t k0, int u, bool ok) {
+        const int64_t blk = k0 / 256;
+        const int q4 = (int)((k0 % 256) / 64);
+        const int h = q4 >> 1;
+        hi = q4 & 1;
+        const int l0 = 16 * u;
+        const uint8_t * ql = W + row * (K / 2) + blk * 128 + 64 * h + l0;
+        const uint8_t * qhp = W + rows * (K / 2) + row * (K / 4) + blk * 64 + 32 * h + l0;
+        const int8_t * scp = (const int8_t *)(W + rows * (K / 2) + rows * (K / 4)) + row * (K / 16) + blk * 16 + 8 * h;
+        const uint16_t * dp = (const uint16_t *)(W + rows * (K / 2) + rows * (K / 4) + rows * (K / 16)) + row * (K / 256) + blk;
+        qla = ok ? *(const u32x4 *)ql : u32x4{0, 0, 0, 0};
+        qlb = ok ? *(const u32x4 *)(ql + 32) : u32x4{0, 0, 0, 0};
+        qh = ok ? *(const u32x4 *)qhp : u32x4{0, 0, 0, 0};
+        // scales for sub-blocks (l/16) + {0,2} (hi=0) or + {4,6} (hi=1), l/16 = u
+        const int i0 = u + 4 * hi;
+        sc = ok ? ((uint32_t)(uint8_t)scp[i0] | ((uint32_t)(uint8_t)scp[i0 + 2] << 8)) : 0u;
+        d = ok ? *dp : (uint16_t)0;
+    }
+    __device__ __forceinline__ void decode(int u, u32x4 out[4], int & run0, int & run1) const {
+        const float df = h2f_bits(d);
+        const float da = mul_rn(df, (float)(int8_t)(sc & 0xFFu));
+        const float db = mul_rn(df, (float)(int8_t)((sc >> 8) & 0xFFu));
+        const int sn = 4 * hi;   // nibble of ql
+        const int sh = 4 * hi;   // bit pair base in qh
+        uint32_t a[8], b[8];
+#pragma unroll
+        for (int w = 0; w < 4; w++) {
+#pragma unroll
+            for (int p = 0; p < 2; p++) {
+                float fa[2], fb[2];
+#pragma unroll
+                for (int e = 0; e < 2; e++) {
+                    const int bi = 2 * p + e;   // byte within the word
+                    const uint32_t la = (qla[w] >> (8 * bi)) & 0xFFu;
+                    const uint32_t lb = (qlb[w] >> (8 * bi)) & 0xFFu;
+                    const uint32_t hh = (qh[w] >> (8 * bi)) & 0xFFu;
+                    const int qa = (int)(((la >> sn) & 15u) | (((hh >> sh) & 3u) << 4)) - 32;
+                    const int qb = (int)(((lb >> sn) & 15u) | (((hh >> (sh + 2)) & 3u) << 4)) - 32;
+                    fa[e] = mul_rn(da, (float)qa);
+                    fb[e] = mul_rn(db, (float)qb);
+                }
+                a[2 * w + p] = pack2h(fa[0], fa[1]);
+                b[2 * w + p] = pack2h(fb[0], fb[1]);
+            }
+        }
+        out[0] = u32x4{a[0], a[1], a[2], a[3]};
+        out[1] = u32x4{a[4], a[5], a[6], a[7]};
+        out[2] = u32x4{b[0], b[1], b[2], b[3]};
+        out[3] = u32x4{b[4], b[5], b[6], b[7]};
+        run0 = 16 * u;
+        run1 = 32 + 16 * u;
+    }
+};
+
+}  // namespace mx

@@ -1,0 +1,121 @@
+/* SPDX-License-Identifier: MIT
+ *
+ * mi355x_kernels.h -- the C ABI of the gfx950 prefill kernels (libggml-mi355x.so).
+ *
+ * This is the device library of the backend: what librocketnpu is to the reference (its call
+ * sites in ggml-rocket.cpp are cited per entry). Plain pointers, sizes and an opaque stream;
+ * no ggml or torch types cross it. Every pointer named *_dev is device memory (HBM) that the
+ * caller owns; the library allocates nothing inside these calls unless a comment says so.
+ * `stream` is a hipStream_t (NULL = the legacy default stream). Every call is asynchronous on
+ * that stream and returns a status (MI355X_OK = 0, or a negative code below).
+ *
+ * Layouts follow ggml's contiguous tensors:
+ *   MUL_MAT      W [N][K] (src0 ne=[K,N]), X [M][K] F32 (src1 ne=[K,M]), dst [M][N] F32.
+ *   FLASH_ATTN   q [H][T][D] F32, k [HK][KV][D] fp16, v [HK][KV][DV] fp16,
+ *                mask [T'][KV'] fp16 (T' >= T, KV' >= KV), dst [T][H][DV] F32.
+ *   MUL_MAT_ID   as [E][N][K], b [T][ne11][K] F32, ids [T][n_used] I32, dst [T][n_used][N] F32.
+ *
+ * Weight types are ggml type ids: F16 = 1, Q8_0 = 8, Q4_K = 12, Q6_K = 14. A weight reaches a
+ * GEMM in its HBM layout: F16 and Q4_K are the ggml payload unchanged; Q8_0 and Q6_K are
+ * re-laid out once by mi355x_weight_pack (same bytes, split into 16-byte-aligned planes).
+ */
+#ifndef MI355X_KERNELS_H
+#define MI355X_KERNELS_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MI355X_API __attribute__((visibility("default")))
+
+enum mi355x_status {
+    MI355X_OK = 0,
+    MI355X_E_ARG = -1,          /* a shape, stride, alignment or type the entry does not take */
+    MI355X_E_DEVICE = -2,       /* a HIP error: launch, copy or allocation failure */
+    MI355X_E_UNSUPPORTED = -3,  /* a structural decline (like ROCKET_E_UNSUPPORTED) */
+    MI355X_E_NOMEM = -4,        /* workspace too small */
+    MI355X_E_IDS = -5,          /* MUL_MAT_ID: an expert id outside [0, n_expert) */
+};
+
+enum mi355x_wtype { MI355X_F16 = 1, MI355X_Q8_0 = 8, MI355X_Q4_K = 12, MI355X_Q6_K = 14 };
+
+typedef struct mi355x_device_info {
+    char name[64];              /* e.g. "gfx950" */
+    int  compute_units;
+    int  lds_bytes_per_block;
+    int  clock_khz;
+    size_t hbm_total;
+    size_t hbm_free;
+} mi355x_device_info;
+
+/* The current device's properties. Replaces rocket_hw_current() (ggml-rocket.cpp:4402, 7262)
+ * and rocket_driver_name() (7273), which describe the NPU part and its driver. */
+MI355X_API int mi355x_get_device_info(mi355x_device_info * out);
+
+/* Human-readable text for a status code. */
+MI355X_API const char * mi355x_status_str(int status);
+
+/* ---- weights ------------------------------------------------------------------------------ */
+
+/* Bytes of `rows` rows of K values of `wtype` in HBM layout (equal to the ggml payload size),
+ * or -1 if K is not a whole number of the type's blocks. */
+MI355X_API int64_t mi355x_weight_bytes(int wtype, int64_t rows, int64_t K);
+
+/* ggml payload (device) -> HBM layout (device). For F16 and Q4_K this is a copy (or nothing,
+ * when src_dev == dst_dev). Replaces the resident pack rocket_weights_pack (ggml-rocket.cpp:
+ * 4362) and its segment form rocket_weights_pack_seg (5121). */
+MI355X_API int mi355x_weight_pack(int wtype, const void * src_dev, int64_t rows, int64_t K,
+                                  void * dst_dev, void * stream);
+
+/* A weight in HBM layout -> fp16 [rows][K]: each value decoded exactly as ggml's dequantizer
+ * does, then rounded once to fp16. The on-device form of rocket_weight_to_fp16 (ggml-rocket.cpp:
+ * 3843-3931), used for the resident-fp16 ("prepacked-q") cache. */
+MI355X_API int mi355x_weight_dequant_f16(int wtype, const void * w_dev, int64_t rows, int64_t K,
+                                         uint16_t * out_dev, void * stream);
+
+/* ---- MUL_MAT ----------------------------------------------------------------------------- */
+
+/* F32 activations [M][ldx] -> fp16 [M][K] divided by each row's max |x| (1 for a zero row),
+ * and the row scales [M]. The device form of rocket_pack_activations (ggml-rocket.cpp:
+ * 1451-1502). K % 4 == 0, ldx % 4 == 0, x 16-byte aligned. */
+MI355X_API int mi355x_pack_act(const float * x_dev, int64_t ldx, int64_t M, int64_t K,
+                               uint16_t * a16_dev, float * scales_dev, void * stream);
+
+/* One output of a (fused) GEMM launch. */
+typedef struct mi355x_gemm_out {
+    const void * w_dev;     /* weight panel in HBM layout */
+    int64_t rows_total;     /* rows of the whole panel (the split layouts index planes by it) */
+    int64_t row0;           /* first row of this weight in the panel */
+    int64_t N;              /* rows of this weight = output columns; N % 16 == 0 */
+    float * c_dev;          /* output [M][ldc] F32 */
+    int64_t ldc;
+} mi355x_gemm_out;
+
+/* c[m][n] = scales[m] * sum_k a16[m][k] * w[row0 + n][k], for each of `n_out` (1..4) weights of
+ * one type that share the activation, in ONE launch over their concatenated N. fp16 MFMA, fp32
+ * accumulation, F32 output. K % 32 == 0 (and a whole number of the type's blocks).
+ * Replaces rocket_matmul_fp16_prepacked (ggml-rocket.cpp:4449, 5144),
+ * rocket_matmul_fp16_stream (4834), rocket_matmul_fp16_mt (4844) and the fused
+ * rocket_matmul_fp16_stream_fused (5004). */
+MI355X_API int mi355x_gemm(int wtype, const uint16_t * a16_dev, const float * scales_dev,
+                           int64_t M, int64_t K, const mi355x_gemm_out * outs, int n_out,
+                           void * stream);
+
+/* Workspace bytes mi355x_mul_mat needs for M rows of K. */
+MI355X_API size_t mi355x_mul_mat_workspace(int64_t M, int64_t K);
+
+/* dst[M][ldd] = x[M][ldx] . w[N][K]^T: mi355x_pack_act then mi355x_gemm, the activation pack
+ * in `workspace_dev`. The whole MUL_MAT of ggml-rocket.cpp:4548-4871 on device. */
+MI355X_API int mi355x_mul_mat(int wtype, const void * w_dev, int64_t N, int64_t K,
+                              const float * x_dev, int64_t ldx, int64_t M,
+                              float * dst_dev, int64_t ldd,
+                              void * workspace_dev, size_t workspace_bytes, void * stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MI355X_KERNELS_H */

@@ -1,0 +1,188 @@
+"""MUL_MAT on the GPU against the CPU oracle, through the C ABI.
+
+Cases follow test-rocket-matmul.cpp: its F16 shapes (incl. M not a multiple of 4), the
+outlier-row case, the fused shared-src1 groups, its quantized shapes, plus the BASELINE shapes:
+the F16 [8192 x 2048] x [512 x 2048] case and the Q8_0 / Q4_K / Q6_K sweep. Bars (tests/bars.py):
+the element bar, worst-column cosine >= 0.999, and max|d|/max|ref| <= 1e-2.
+"""
+import numpy as np
+import pytest
+
+from oracle import oracle as O
+from bars import compare, worst_col_cos, amp_for
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def mx(torch_cuda):
+    import ggml_mi355x
+    ggml_mi355x.lib()
+    return ggml_mi355x
+
+
+def _dev(a):
+    import torch
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def _run_mul_mat(mx, wtype, payload, N, K, X):
+    import torch
+    w = mx.upload_weight(wtype, payload, N, K)
+    out = mx.mul_mat(wtype, w, N, K, _dev(X))
+    torch.cuda.synchronize()
+    return out.cpu().numpy()
+
+
+def _assert_bars(ref, got, M, N, label, cos_floor=0.999, range_tol=1e-2):
+    r = compare(ref, got)
+    wc = worst_col_cos(ref.reshape(M, N), got.reshape(M, N))
+    print(f"{label}: nbad={r['nbad']} max_abs={r['max_abs']:.4g} range_err={r['range_err']:.3g} "
+          f"worst_col_cos={wc:.6f}")
+    assert r["nonfinite"] == 0, label
+    assert r["nbad"] == 0, label
+    assert wc >= cos_floor, label
+    assert r["range_err"] <= range_tol, label
+
+
+def test_pack_act_bitexact(mx):
+    X = O.fill_normal((67, 512), 7)
+    X[3] *= 3000.0                 # outlier row
+    X[5] = 0.0                     # zero row -> scale 1
+    X[9, 17] = 1e6                 # a value past fp16 range before scaling
+    a16, sc = mx.pack_act(_dev(X))
+    want_a, want_s = O.pack_act(X)
+    got_a = a16.cpu().numpy().view(np.uint16)
+    assert np.array_equal(sc.cpu().numpy(), want_s)
+    assert np.array_equal(got_a, want_a)
+
+
+@pytest.mark.parametrize("wtype", [O.F16, O.Q8_0, O.Q4_K, O.Q6_K])
+def test_dequant_f16_bitexact(mx, wtype):
+    N, K = 96, 1024
+    W = O.fill_normal((N, K), 11 + wtype, 0.0, 0.02)
+    W[0, :256] *= 50.0             # a wide block
+    W[1, :] = 0.0                  # an all-zero row
+    W[2, 5] = -3.0                 # one extreme value
+    if wtype == O.F16:
+        payload = O.f32_to_f16_bits(W)
+        want = payload
+    else:
+        payload = O.quantize(wtype, W)
+        want = O.dequantize_f16(wtype, payload, K)
+    w = mx.upload_weight(wtype, payload, N, K)
+    got = mx.dequant_f16(wtype, w, N, K).cpu().numpy().view(np.uint16)
+    assert np.array_equal(got, want.reshape(N, K))
+
+
+F16_SHAPES = [(64, 32, 8), (384, 256, 256), (3840, 4096, 512), (64, 64, 7), (384, 256, 130),
+              (3840, 4096, 250)]
+
+
+@pytest.mark.parametrize("K,N,M", F16_SHAPES)
+def test_mul_mat_f16_shapes(mx, K, N, M):
+    Wf = O.fill_uniform((N, K), 101 + K, 1.0)
+    Xf = O.fill_uniform((M, K), 202 + M, amp_for(K, 1.0))
+    W16 = O.f32_to_f16_bits(Wf)
+    ref = O.mul_mat(O.F16, W16, Xf, N, K)
+    got = _run_mul_mat(mx, O.F16, W16, N, K, Xf)
+    _assert_bars(ref, got, M, N, f"F16 K={K} N={N} M={M}")
+
+
+def test_outlier_row(mx):
+    """test-rocket-matmul.cpp:181-221: an outlier row must not crush the other rows."""
+    K, N, M = 256, 64, 8
+    i = np.arange(K * N)
+    Wf = ((((i * 7) % 13) - 6) * 0.05).astype(np.float32).reshape(N, K)
+    j = np.arange(K * M)
+    Xf = ((((j * 5) % 11) - 5) * 0.02).astype(np.float32).reshape(M, K)
+    Xf[3] = ((np.arange(K) % 7) - 3) * 300.0
+    W16 = O.f32_to_f16_bits(Wf)
+    ref = O.mul_mat(O.F16, W16, Xf, N, K)
+    got = _run_mul_mat(mx, O.F16, W16, N, K, Xf)
+    assert np.isfinite(got).all()
+    small = np.delete(np.arange(M), 3)
+    rd = np.abs(got[small] - ref[small]) / (np.abs(ref[small]) + 1e-6)
+    assert rd.max() < 0.05
+
+
+def test_cfg_f16_8192x2048_m512(mx):
+    """F16 weight [N=8192, K=2048] ~N(0,0.02), F32 activations [512, 2048] ~N(0,1)."""
+    K, N, M = 2048, 8192, 512
+    W16 = O.f32_to_f16_bits(O.fill_normal((N, K), 0x5EED0000 + 16, 0.0, 0.02))
+    Xf = O.fill_normal((M, K), 0x5EED0000 + 16 + 8)
+    ref = O.mul_mat(O.F16, W16, Xf, N, K)
+    got = _run_mul_mat(mx, O.F16, W16, N, K, Xf)
+    _assert_bars(ref, got, M, N, "F16 cfg 8192x2048 M=512")
+
+
+QSHAPES = [(256, 128, 64, O.Q8_0), (3840, 256, 128, O.Q8_0), (256, 128, 64, O.Q4_K),
+           (3840, 256, 128, O.Q4_K), (512, 256, 128, O.Q6_K)]
+
+
+@pytest.mark.parametrize("K,N,M,wtype", QSHAPES)
+def test_mul_mat_quant_reference_shapes(mx, K, N, M, wtype):
+    """test-rocket-matmul.cpp:316-366: golden = fp64 dot of the dequantized weight."""
+    i = np.arange(N * K, dtype=np.float32)
+    Wf = (np.sin(i * np.float32(0.013)) * np.float32(0.5)).astype(np.float32).reshape(N, K)
+    Xf = O.fill_uniform((M, K), 505 + K, amp_for(K, 0.61))
+    Q = O.quantize(wtype, Wf)
+    ref = O.mul_mat(wtype, Q, Xf, N, K)
+    got = _run_mul_mat(mx, wtype, Q, N, K, Xf)
+    r = compare(ref, got)
+    assert r["nbad"] == 0 and r["nonfinite"] == 0
+    assert r["range_err"] <= 1e-2
+
+
+# The quantized sweep at its full sizes. The oracle runs on a sample of 48 activation rows (an
+# exact subset of the output), so the check stays seconds long at M = 2048.
+SWEEP = [(K, N, M, t) for t in (O.Q8_0, O.Q4_K, O.Q6_K)
+         for (K, N) in ((3072, 3072), (3072, 8192), (8192, 3072)) for M in (32, 128, 512, 2048)]
+
+
+@pytest.mark.parametrize("K,N,M,wtype", SWEEP)
+def test_mul_mat_quant_sweep(mx, K, N, M, wtype):
+    W = O.fill_normal((N, K), 0x5EED0000 + 32 + wtype, 0.0, 0.02)
+    Xf = O.fill_normal((M, K), 0x5EED0000 + 40 + M)
+    Q = O.quantize(wtype, W)
+    got = _run_mul_mat(mx, wtype, Q, N, K, Xf)
+    rows = np.unique(np.linspace(0, M - 1, min(M, 48)).astype(int))
+    ref = O.mul_mat(wtype, Q, Xf[rows], N, K)
+    _assert_bars(ref, got[rows], len(rows), N, f"{O.TYPE_NAMES[wtype]} K={K} N={N} M={M}")
+
+
+@pytest.mark.parametrize("Ns", [(4096, 4096), (4096, 2048, 2048)])
+def test_fused_group(mx, Ns):
+    """test-rocket-matmul.cpp:259-314: members sharing src1 in one launch over concatenated N."""
+    import torch
+    K, M = 3840, 128
+    Xf = O.fill_uniform((M, K), 303, amp_for(K, 1.0))
+    a16, sc = mx.pack_act(_dev(Xf))
+    outs, refs = [], []
+    for g, N in enumerate(Ns):
+        W16 = O.f32_to_f16_bits(O.fill_uniform((N, K), 404 + g, 1.0))
+        refs.append(O.mul_mat(O.F16, W16, Xf, N, K))
+        w = mx.upload_weight(O.F16, W16, N, K)
+        c = torch.empty((M, N), dtype=torch.float32, device="cuda")
+        outs.append((w, N, 0, N, c))
+    mx.gemm(O.F16, a16, sc, K, outs)
+    torch.cuda.synchronize()
+    for (w, _, _, N, c), ref in zip(outs, refs):
+        _assert_bars(ref, c.cpu().numpy(), M, N, f"fused N={N}")
+
+
+def test_gemm_rows_of_a_panel(mx):
+    """row0/rows_total: a weight addressed inside a larger split-layout panel (the expert stacks)."""
+    import torch
+    K, N, E, M = 512, 128, 3, 40
+    W = O.fill_normal((E * N, K), 77, 0.0, 0.02)
+    for wtype in (O.Q8_0, O.Q6_K, O.Q4_K):
+        Q = O.quantize(wtype, W)
+        w = mx.upload_weight(wtype, Q, E * N, K)
+        Xf = O.fill_normal((M, K), 78)
+        a16, sc = mx.pack_act(_dev(Xf))
+        c = torch.empty((M, N), dtype=torch.float32, device="cuda")
+        mx.gemm(wtype, a16, sc, K, [(w, E * N, 2 * N, N, c)])
+        torch.cuda.synchronize()
+        ref = O.mul_mat(wtype, Q[2 * N:3 * N], Xf, N, K)
+        _assert_bars(ref, c.cpu().numpy(), M, N, f"panel {O.TYPE_NAMES[wtype]}")
