@@ -153,4 +153,73 @@ MI355X_API int mi355x_mul_mat(int wtype, const void * w_dev, int64_t N, int64_t 
     return mi355x_gemm(wtype, a16, scales, M, K, &o, 1, stream);
 }
 
+// ---- FLASH_ATTN_EXT ---------------------------------------------------------------------------
+
+static int fa_check(const mi355x_fa_args * a) {
+    if (!a || !a->q_dev || !a->k_dev || !a->v_dev || !a->dst_dev) return MI355X_E_ARG;
+    if (a->D != a->DV || (a->D != 64 && a->D != 128)) return MI355X_E_UNSUPPORTED;
+    if (a->max_bias != 0.0f) return MI355X_E_UNSUPPORTED;
+    if (a->T < 0 || a->H <= 0 || a->HK <= 0 || a->KV < 0 || a->H % a->HK) return MI355X_E_ARG;
+    if (a->q_nb1 % 4 || a->q_nb2 % 4 || !aligned(a->q_dev, 16)) return MI355X_E_ARG;
+    if (a->k_nb1 % 8 || a->k_nb2 % 8 || a->v_nb1 % 8 || a->v_nb2 % 8) return MI355X_E_ARG;
+    if (!aligned(a->k_dev, 16) || !aligned(a->v_dev, 16)) return MI355X_E_ARG;
+    if (a->dst_nb1 % 4 || a->dst_nb2 % 4 || !aligned(a->dst_dev, 16)) return MI355X_E_ARG;
+    if (a->mask_dev && (a->mask_nb1 % 4 || a->mask_nb1 < a->KV || !aligned(a->mask_dev, 8))) return MI355X_E_ARG;
+    return MI355X_OK;
+}
+
+static mx::FaArgs fa_lower(const mi355x_fa_args * a, int nsplit) {
+    mx::FaArgs f;
+    memset(&f, 0, sizeof(f));
+    f.q = a->q_dev; f.k = a->k_dev; f.v = a->v_dev; f.mask = a->mask_dev; f.dst = a->dst_dev;
+    f.q_nb1 = a->q_nb1; f.q_nb2 = a->q_nb2; f.k_nb1 = a->k_nb1; f.k_nb2 = a->k_nb2;
+    f.v_nb1 = a->v_nb1; f.v_nb2 = a->v_nb2; f.mask_nb1 = a->mask_nb1;
+    f.dst_nb1 = a->dst_nb1; f.dst_nb2 = a->dst_nb2;
+    f.D = a->D; f.T = a->T; f.H = a->H; f.HK = a->HK; f.KV = a->KV; f.nsplit = nsplit;
+    f.scale = a->scale; f.softcap = a->softcap;
+    return f;
+}
+
+MI355X_API int mi355x_flash_attn_auto_split(const mi355x_fa_args * a) {
+    if (fa_check(a) != MI355X_OK) return 1;
+    const mx::FaArgs f = fa_lower(a, 1);
+    const int nb = mx::fa_blocks_per_split(f);
+    const int ntiles = (a->KV + 63) / 64;
+    int cus = 256;
+    mi355x_device_info di;
+    if (mi355x_get_device_info(&di) == MI355X_OK && di.compute_units > 0) cus = di.compute_units;
+    // fill about two blocks per CU, keeping at least 8 key tiles per split
+    int ns = nb > 0 ? (2 * cus + nb - 1) / nb : 1;
+    const int max_by_len = ntiles / 8 > 0 ? ntiles / 8 : 1;
+    if (ns > max_by_len) ns = max_by_len;
+    if (ns > 16) ns = 16;
+    return ns < 1 ? 1 : ns;
+}
+
+MI355X_API size_t mi355x_flash_attn_workspace(const mi355x_fa_args * a, int nsplit) {
+    if (fa_check(a) != MI355X_OK) return 0;
+    if (nsplit <= 0) nsplit = mi355x_flash_attn_auto_split(a);
+    if (nsplit <= 1) return 0;
+    const size_t rows = (size_t)a->T * a->H * nsplit;
+    return ((rows * a->DV * 4 + 255) & ~(size_t)255) + rows * 8;
+}
+
+MI355X_API int mi355x_flash_attn(const mi355x_fa_args * a, int nsplit,
+                                 void * workspace_dev, size_t workspace_bytes, void * stream) {
+    const int st = fa_check(a);
+    if (st != MI355X_OK) return st;
+    if (a->T == 0) return MI355X_OK;
+    if (nsplit <= 0) nsplit = mi355x_flash_attn_auto_split(a);
+    if (nsplit > 64) return MI355X_E_ARG;
+    mx::FaArgs f = fa_lower(a, nsplit);
+    if (nsplit > 1) {
+        const size_t need = mi355x_flash_attn_workspace(a, nsplit);
+        if (!workspace_dev || workspace_bytes < need) return MI355X_E_NOMEM;
+        const size_t rows = (size_t)a->T * a->H * nsplit;
+        f.part_o = (float *)workspace_dev;
+        f.part_ml = (float *)((char *)workspace_dev + ((rows * a->DV * 4 + 255) & ~(size_t)255));
+    }
+    return hip_status(mx::launch_fa(f, S(stream)));
+}
+
 }  // extern "C"

@@ -31,6 +31,23 @@ struct GemmArgs {
     GemmGroup g[GEMM_MAX_GROUPS];
 };
 
+// FLASH_ATTN_EXT launch: strides in elements.
+struct FaArgs {
+    const float * q;           // [H][T][D] via q_nb2 (head), q_nb1 (token)
+    const uint16_t * k;        // [HK][KV][D] via k_nb2, k_nb1
+    const uint16_t * v;        // [HK][KV][D] via v_nb2, v_nb1
+    const uint16_t * mask;     // [T'][KV'] via mask_nb1, or null
+    float * dst;               // [T][H][D] via dst_nb2 (token), dst_nb1 (head)
+    float * part_o;            // [nsplit][T][H][D] when nsplit > 1
+    float * part_ml;           // [nsplit][T][H][2]
+    int64_t q_nb1, q_nb2, k_nb1, k_nb2, v_nb1, v_nb2, mask_nb1, dst_nb1, dst_nb2;
+    int D, T, H, HK, KV, nsplit;
+    float scale, softcap;
+};
+
+int fa_blocks_per_split(const FaArgs & a);
+hipError_t launch_fa(const FaArgs & a, hipStream_t st);
+
 hipError_t launch_pack_act(const float * X, int64_t ldx, int M, int K, uint16_t * A16, int64_t lda,
                            float * scales, hipStream_t st);
 hipError_t launch_gemm(int wt, const GemmArgs & a, int n_tiles_total, hipStream_t st);

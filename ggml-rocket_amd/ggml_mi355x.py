@@ -39,6 +39,17 @@ class DeviceInfo(ctypes.Structure):
                 ("hbm_total", ctypes.c_size_t), ("hbm_free", ctypes.c_size_t)]
 
 
+class FaArgs(ctypes.Structure):
+    _fields_ = [("q_dev", ctypes.c_void_p), ("q_nb1", ctypes.c_int64), ("q_nb2", ctypes.c_int64),
+                ("k_dev", ctypes.c_void_p), ("k_nb1", ctypes.c_int64), ("k_nb2", ctypes.c_int64),
+                ("v_dev", ctypes.c_void_p), ("v_nb1", ctypes.c_int64), ("v_nb2", ctypes.c_int64),
+                ("mask_dev", ctypes.c_void_p), ("mask_nb1", ctypes.c_int64),
+                ("dst_dev", ctypes.c_void_p), ("dst_nb1", ctypes.c_int64), ("dst_nb2", ctypes.c_int64),
+                ("D", ctypes.c_int), ("DV", ctypes.c_int), ("T", ctypes.c_int), ("H", ctypes.c_int),
+                ("KV", ctypes.c_int), ("HK", ctypes.c_int),
+                ("scale", ctypes.c_float), ("max_bias", ctypes.c_float), ("softcap", ctypes.c_float)]
+
+
 def lib():
     """Load the built backend library. Raises if it has not been built."""
     global _lib
@@ -70,11 +81,13 @@ def lib():
 def _bind_optional(L):
     """Entry points of later kernel families; bound when the library exports them."""
     i64, i32, vp, sz, f32 = ctypes.c_int64, ctypes.c_int, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_float
-    if hasattr(L, "mi355x_flash_attn_workspace"):
+    if hasattr(L, "mi355x_flash_attn"):
+        pa = ctypes.POINTER(FaArgs)
+        L.mi355x_flash_attn_auto_split.restype = i32
+        L.mi355x_flash_attn_auto_split.argtypes = [pa]
         L.mi355x_flash_attn_workspace.restype = sz
-        L.mi355x_flash_attn_workspace.argtypes = [i32, i32, i32, i32, i32]
-        L.mi355x_flash_attn.argtypes = [vp, vp, vp, vp, i64, vp, i32, i32, i32, i32, i32, i32,
-                                        f32, f32, vp, sz, vp]
+        L.mi355x_flash_attn_workspace.argtypes = [pa, i32]
+        L.mi355x_flash_attn.argtypes = [pa, i32, vp, sz, vp]
     if hasattr(L, "mi355x_mul_mat_id_workspace"):
         L.mi355x_mul_mat_id_workspace.restype = sz
         L.mi355x_mul_mat_id_workspace.argtypes = [i64, i64, i64, i64, i64, i64]
@@ -176,4 +189,27 @@ def mul_mat(wtype: int, w_dev, N: int, K: int, x, out=None, workspace=None):
         workspace = torch.empty(max(need, 1), dtype=torch.uint8, device=x.device)
     check(lib().mi355x_mul_mat(wtype, _ptr(w_dev), N, K, _ptr(x), x.stride(0), M, _ptr(out), out.stride(0),
                                _ptr(workspace), workspace.numel(), stream_handle()), "mul_mat")
+    return out
+
+
+def flash_attn(q, k, v, mask, scale: float, softcap: float = 0.0, nsplit: int = 0, out=None,
+               workspace=None, max_bias: float = 0.0):
+    """q [H, T, D] f32 (any strides with unit last-dim stride), k/v [HK, KV, D] fp16, mask
+    [T', KV'] fp16 or None. Returns dst [T, H, D] f32."""
+    torch = _torch()
+    H, T, D = q.shape
+    HK, KV, DV = v.shape
+    if out is None:
+        out = torch.empty((T, H, DV), dtype=torch.float32, device=q.device)
+    a = FaArgs(q.data_ptr(), q.stride(1), q.stride(0),
+               k.data_ptr(), k.stride(1), k.stride(0),
+               v.data_ptr(), v.stride(1), v.stride(0),
+               mask.data_ptr() if mask is not None else None, mask.stride(0) if mask is not None else 0,
+               out.data_ptr(), out.stride(1), out.stride(0),
+               D, DV, T, H, KV, HK, scale, max_bias, softcap)
+    need = int(lib().mi355x_flash_attn_workspace(ctypes.byref(a), nsplit))
+    if need and (workspace is None or workspace.numel() < need):
+        workspace = torch.empty(need, dtype=torch.uint8, device=q.device)
+    wp = workspace.data_ptr() if need else None
+    check(lib().mi355x_flash_attn(ctypes.byref(a), nsplit, wp, need, stream_handle()), "flash_attn")
     return out

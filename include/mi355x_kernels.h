@@ -114,6 +114,35 @@ MI355X_API int mi355x_mul_mat(int wtype, const void * w_dev, int64_t N, int64_t 
                               float * dst_dev, int64_t ldd,
                               void * workspace_dev, size_t workspace_bytes, void * stream);
 
+/* ---- FLASH_ATTN_EXT ---------------------------------------------------------------------- */
+
+/* One attention op. Strides are in ELEMENTS, so strided ggml views (a KV-cache slice, a
+ * permuted Q) are read in place. */
+typedef struct mi355x_fa_args {
+    const float * q_dev;      int64_t q_nb1, q_nb2;      /* token, head strides */
+    const uint16_t * k_dev;   int64_t k_nb1, k_nb2;      /* key, kv-head strides (fp16) */
+    const uint16_t * v_dev;   int64_t v_nb1, v_nb2;      /* key, kv-head strides (fp16) */
+    const uint16_t * mask_dev; int64_t mask_nb1;         /* token stride; NULL = unmasked */
+    float * dst_dev;          int64_t dst_nb1, dst_nb2;  /* head, token strides */
+    int D, DV, T, H, KV, HK;
+    float scale, max_bias, softcap;
+} mi355x_fa_args;
+
+/* The KV-split count mi355x_flash_attn uses when called with nsplit = 0. */
+MI355X_API int mi355x_flash_attn_auto_split(const mi355x_fa_args * a);
+
+/* Workspace bytes for `nsplit` KV splits (0 = auto): the partial outputs of a split launch. */
+MI355X_API size_t mi355x_flash_attn_workspace(const mi355x_fa_args * a, int nsplit);
+
+/* dst = softmax(cap(scale * q.k) + mask) . v for every (token, head); head h reads KV head
+ * h / (H / HK). D == DV in {64, 128}; H % HK == 0; max_bias must be 0 (no ALiBi); the mask
+ * covers [T][KV] with mask_nb1 % 4 == 0; q rows and dst rows 16-byte aligned; k/v rows 16-byte
+ * aligned. Rows whose every key is masked are written as zeros. Replaces
+ * rocket_flash_attn_fp16_ctx / _mt (ggml-rocket.cpp:5589-5606) and, because no fp16 score
+ * surface exists here, the range fallback rocket_fa_ref_f32 (5617-5626) as well. */
+MI355X_API int mi355x_flash_attn(const mi355x_fa_args * a, int nsplit,
+                                 void * workspace_dev, size_t workspace_bytes, void * stream);
+
 #ifdef __cplusplus
 }
 #endif

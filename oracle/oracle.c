@@ -502,6 +502,14 @@ ORC_API int orc_flash_attn(const float * q, const uint16_t * k, const uint16_t *
     if (HK <= 0 || H % HK) return -1;
     if (nthreads > 0) omp_set_num_threads(nthreads);
     const int g = H / HK;
+    /* K and V decoded once (exact: every fp16 is a double) */
+    double * Kd = (double *)malloc((size_t)HK * KV * D * sizeof(double));
+    double * Vd = (double *)malloc((size_t)HK * KV * DV * sizeof(double));
+    if (!Kd || !Vd) { free(Kd); free(Vd); return -2; }
+    #pragma omp parallel for schedule(static)
+    for (int64_t i = 0; i < (int64_t)HK * KV * D; i++) Kd[i] = (double)orc_f16_to_f32(k[i]);
+    #pragma omp parallel for schedule(static)
+    for (int64_t i = 0; i < (int64_t)HK * KV * DV; i++) Vd[i] = (double)orc_f16_to_f32(v[i]);
     #pragma omp parallel
     {
         double * qd = (double *)malloc((size_t)D * sizeof(double));
@@ -513,16 +521,16 @@ ORC_API int orc_flash_attn(const float * q, const uint16_t * k, const uint16_t *
             const float * qr = q + ((size_t)h * T + t) * D;
             for (int c = 0; c < D; c++)
                 qd[c] = q_mode ? (double)qr[c] : (double)orc_f16_to_f32(orc_f32_to_f16(qr[c]));
-            const uint16_t * Kh = k + (size_t)hk * KV * D;
-            const uint16_t * Vh = v + (size_t)hk * KV * DV;
+            const double * Kh = Kd + (size_t)hk * KV * D;
+            const double * Vh = Vd + (size_t)hk * KV * DV;
             const uint16_t * mr = mask ? mask + (size_t)t * mask_stride : NULL;
             double mx = -INFINITY;
             for (int j = 0; j < KV; j++) {
                 const double mv = mr ? (double)orc_f16_to_f32(mr[j]) : 0.0;
                 if (mv == -INFINITY) { sc[j] = -INFINITY; continue; }
-                const uint16_t * kr = Kh + (size_t)j * D;
+                const double * kr = Kh + (size_t)j * D;
                 double dd = 0.0;
-                for (int c = 0; c < D; c++) dd += qd[c] * (double)orc_f16_to_f32(kr[c]);
+                for (int c = 0; c < D; c++) dd += qd[c] * kr[c];
                 double s = dd * (double)scale;
                 if (softcap != 0.0f) s = (double)softcap * tanh(s / (double)softcap);
                 s += mv;
@@ -537,8 +545,8 @@ ORC_API int orc_flash_attn(const float * q, const uint16_t * k, const uint16_t *
             for (int c = 0; c < DV; c++) acc[c] = 0.0;
             for (int j = 0; j < KV; j++) {
                 if (sc[j] == 0.0) continue;
-                const uint16_t * vr = Vh + (size_t)j * DV;
-                for (int c = 0; c < DV; c++) acc[c] += sc[j] * (double)orc_f16_to_f32(vr[c]);
+                const double * vr = Vh + (size_t)j * DV;
+                for (int c = 0; c < DV; c++) acc[c] += sc[j] * vr[c];
             }
             const double inv = sum > 0.0 ? 1.0 / sum : 0.0;
             float * dr = dst + ((size_t)t * H + h) * DV;
@@ -546,6 +554,8 @@ ORC_API int orc_flash_attn(const float * q, const uint16_t * k, const uint16_t *
         }
         free(qd); free(sc); free(acc);
     }
+    free(Kd);
+    free(Vd);
     return 0;
 }
 

@@ -1,0 +1,125 @@
+"""FLASH_ATTN_EXT on the GPU against the double oracle, through the C ABI.
+
+The reference's cases (test-rocket-fa.cpp): overflow (one-hot softmax, raw q.k past 65504),
+typical (random, causal), scaled (scaled logits past 65504) and q range (scaled Q past 65504).
+The reference sends the last two to its host fallback because its NPU keeps an fp16 score
+surface; here scores stay in fp32 registers and a Q row past fp16 range is divided by a per-row
+factor, so all four run on the device, scored against the same oracle and tolerances.
+Plus the BASELINE shapes: 32 query / 8 KV heads, d 128, 512 tokens, n_kv 1024/4096/8192,
+N(0,1) inputs, causal mask, scale 1/sqrt(128); scored on sampled query rows.
+"""
+import numpy as np
+import pytest
+
+from oracle import oracle as O
+from fa_cases import REFERENCE_CASES, fill_case, causal_mask, TYPICAL, SCALED, QRANGE
+from bars import compare
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def mx(torch_cuda):
+    import ggml_mi355x
+    ggml_mi355x.lib()
+    return ggml_mi355x
+
+
+def _run(mx, Q, K16, V16, M16, scale, softcap=0.0, nsplit=0):
+    import torch
+    q = torch.from_numpy(Q).cuda()
+    k = torch.from_numpy(K16.view(np.float16)).cuda()
+    v = torch.from_numpy(V16.view(np.float16)).cuda()
+    m = torch.from_numpy(M16.view(np.float16)).cuda() if M16 is not None else None
+    out = mx.flash_attn(q, k, v, m, scale, softcap=softcap, nsplit=nsplit)
+    torch.cuda.synchronize()
+    return out.cpu().numpy()
+
+
+@pytest.mark.parametrize("case", REFERENCE_CASES, ids=[c[0] for c in REFERENCE_CASES])
+@pytest.mark.parametrize("nsplit", [1, 0])
+def test_fa_reference_cases(mx, case, nsplit):
+    name, D, T, H, KV, HK, kind, tol = case
+    Q, K, V, M = fill_case(D, T, H, KV, HK, kind)
+    K16, V16, M16 = O.f32_to_f16_bits(K), O.f32_to_f16_bits(V), O.f32_to_f16_bits(M)
+    scale = float(np.float32(1.0) / np.sqrt(np.float32(D)))
+    q_mode = 1 if kind in (SCALED, QRANGE) else 0
+    want = O.flash_attn(Q, K16, V16, M16, scale, q_mode=q_mode)
+    got = _run(mx, Q, K16, V16, M16, scale, nsplit=nsplit)
+    assert np.isfinite(got).all(), name
+    err = float(np.abs(got.astype(np.float64) - want).max())
+    print(f"{name} nsplit={nsplit}: max abs err {err:.3g} (tol {tol})")
+    assert err <= tol, name
+
+
+def test_fa_fully_masked_rows_are_zero(mx):
+    """A row whose every key is masked is written as zeros (ggml-rocket.cpp:5395-5397)."""
+    D, T, H, KV, HK = 64, 40, 4, 300, 2
+    Q, K, V, _ = fill_case(D, T, H, KV, HK, TYPICAL)
+    M = causal_mask(T, KV)
+    M[5, :] = -np.inf
+    M[33, :] = -np.inf
+    K16, V16, M16 = O.f32_to_f16_bits(K), O.f32_to_f16_bits(V), O.f32_to_f16_bits(M)
+    for ns in (1, 3):
+        got = _run(mx, Q, K16, V16, M16, 0.125, nsplit=ns)
+        assert np.all(got[5] == 0.0) and np.all(got[33] == 0.0)
+        want = O.flash_attn(Q, K16, V16, M16, 0.125)
+        assert float(np.abs(got - want).max()) <= 2e-2
+
+
+def test_fa_softcap_unmasked_ragged(mx):
+    """Soft-cap, no mask, and T / KV that are not multiples of the tiles."""
+    D, T, H, KV, HK = 128, 45, 6, 333, 3
+    Q = O.fill_normal((H, T, D), 901)
+    K16 = O.f32_to_f16_bits(O.fill_normal((HK, KV, D), 902))
+    V16 = O.f32_to_f16_bits(O.fill_normal((HK, KV, D), 903))
+    scale = 0.3
+    for softcap in (0.0, 5.0):
+        want = O.flash_attn(Q, K16, V16, None, scale, softcap=softcap)
+        for ns in (1, 2):
+            got = _run(mx, Q, K16, V16, None, scale, softcap=softcap, nsplit=ns)
+            r = compare(want, got)
+            assert r["nonfinite"] == 0 and r["range_err"] <= 1e-2, (softcap, ns, r)
+
+
+def test_fa_strided_views(mx):
+    """Q as a permuted [T][H][D] buffer and K/V as KV-cache slices [KV][HK][D] (llama.cpp's
+    layouts), read in place through the strides."""
+    import torch
+    import ggml_mi355x as mxm
+    D, T, H, KV, HK = 128, 64, 8, 512, 2
+    Qthd = O.fill_normal((T, H, D), 911)
+    Kc = O.f32_to_f16_bits(O.fill_normal((KV, HK, D), 912))
+    Vc = O.f32_to_f16_bits(O.fill_normal((KV, HK, D), 913))
+    M = causal_mask(T, KV)
+    q = torch.from_numpy(Qthd).cuda().permute(1, 0, 2)           # [H][T][D] view
+    k = torch.from_numpy(Kc.view(np.float16)).cuda().permute(1, 0, 2)
+    v = torch.from_numpy(Vc.view(np.float16)).cuda().permute(1, 0, 2)
+    m = torch.from_numpy(O.f32_to_f16_bits(M).view(np.float16)).cuda()
+    got = mxm.flash_attn(q, k, v, m, 0.088)
+    torch.cuda.synchronize()
+    want = O.flash_attn(np.ascontiguousarray(Qthd.transpose(1, 0, 2)),
+                        np.ascontiguousarray(Kc.transpose(1, 0, 2)),
+                        np.ascontiguousarray(Vc.transpose(1, 0, 2)), O.f32_to_f16_bits(M), 0.088)
+    r = compare(want, got.cpu().numpy())
+    assert r["nonfinite"] == 0 and r["range_err"] <= 1e-2, r
+
+
+@pytest.mark.parametrize("KV", [1024, 4096, 8192])
+def test_fa_baseline_shapes(mx, KV):
+    """32 query heads, 8 KV heads, d 128, 512 tokens; K/V ~N(0,1) fp16; causal F16 mask;
+    scale 1/sqrt(128). Scored on 48 sampled tokens (all heads) against the double oracle."""
+    D, T, H, HK = 128, 512, 32, 8
+    Q = O.fill_normal((H, T, D), 0x5EED0000 + 48)
+    K16 = O.f32_to_f16_bits(O.fill_normal((HK, KV, D), 0x5EED0000 + 49))
+    V16 = O.f32_to_f16_bits(O.fill_normal((HK, KV, D), 0x5EED0000 + 50))
+    M16 = O.f32_to_f16_bits(causal_mask(T, KV))
+    scale = float(1.0 / np.sqrt(128.0))
+    got = _run(mx, Q, K16, V16, M16, scale)
+    rows = np.unique(np.linspace(0, T - 1, 48).astype(int))
+    want = O.flash_attn(np.ascontiguousarray(Q[:, rows, :]), K16, V16,
+                        np.ascontiguousarray(M16[rows]), scale)
+    r = compare(want, got[rows])
+    print(f"FA KV={KV}: max abs {r['max_abs']:.3g} range_err {r['range_err']:.3g}")
+    assert r["nonfinite"] == 0
+    assert r["max_abs"] <= 2e-2 and r["range_err"] <= 1e-2
