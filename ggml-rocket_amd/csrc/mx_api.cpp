@@ -222,4 +222,69 @@ MI355X_API int mi355x_flash_attn(const mi355x_fa_args * a, int nsplit,
     return hip_status(mx::launch_fa(f, S(stream)));
 }
 
+// ---- MUL_MAT_ID -------------------------------------------------------------------------------
+
+namespace {
+
+struct MoeLayout {
+    size_t a16, scales, off, rows, tiles, n_tiles, err, total;
+};
+
+inline size_t up256(size_t x) { return (x + 255) & ~(size_t)255; }
+
+bool moe_layout(const mi355x_moe_args * a, MoeLayout & L) {
+    if (!a || a->n_tokens < 0 || a->n_used <= 0 || a->ne11 <= 0 || a->n_expert <= 0 || a->K <= 0 || a->N <= 0)
+        return false;
+    const size_t rows_b = (size_t)a->n_tokens * a->ne11;
+    const size_t R = (size_t)a->n_tokens * a->n_used;
+    const size_t tiles = (size_t)mx::moe_max_tiles((int)a->n_tokens, (int)a->n_used, (int)a->n_expert);
+    size_t o = 0;
+    L.a16 = o;     o += up256(rows_b * a->K * 2);
+    L.scales = o;  o += up256(rows_b * 4);
+    L.off = o;     o += up256(((size_t)a->n_expert + 1) * 4);
+    L.rows = o;    o += up256((R > 0 ? R : 1) * 4);
+    L.tiles = o;   o += up256(tiles * 8);
+    L.n_tiles = o; o += 256;
+    L.err = o;     o += 256;
+    L.total = o;
+    return true;
+}
+
+}  // namespace
+
+MI355X_API size_t mi355x_mul_mat_id_workspace(const mi355x_moe_args * a) {
+    MoeLayout L;
+    return moe_layout(a, L) ? L.total : 0;
+}
+
+MI355X_API int mi355x_mul_mat_id(const mi355x_moe_args * a, void * workspace_dev, size_t workspace_bytes,
+                                 int32_t * err_dev, void * stream) {
+    MoeLayout L;
+    if (!moe_layout(a, L)) return MI355X_E_ARG;
+    if (!known_wtype(a->wtype) || a->K % 32 || a->K % blck(a->wtype) || a->N % 16) return MI355X_E_ARG;
+    if (!a->as_dev || !a->b_dev || !a->ids_dev || !a->dst_dev || !aligned(a->as_dev, 16) || !aligned(a->b_dev, 16))
+        return MI355X_E_ARG;
+    if (a->b_nb1 < a->K || a->b_nb1 % 4 || a->b_nb2 != a->ne11 * a->b_nb1) return MI355X_E_ARG;
+    if (a->n_expert * a->N > INT32_MAX || a->n_tokens * a->n_used > INT32_MAX || a->n_expert > 8192 ||
+        a->n_tokens * a->ne11 > INT32_MAX || a->K > INT32_MAX)
+        return MI355X_E_ARG;
+    if (a->n_tokens == 0) return MI355X_OK;
+    if (!workspace_dev || workspace_bytes < L.total) return MI355X_E_NOMEM;
+    char * ws = (char *)workspace_dev;
+    mx::MoeArgs m;
+    memset(&m, 0, sizeof(m));
+    m.w = a->as_dev; m.E = (int)a->n_expert; m.N = (int)a->N; m.K = (int)a->K;
+    m.b = a->b_dev; m.b_nb1 = a->b_nb1; m.ne11 = (int)a->ne11; m.T = (int)a->n_tokens; m.U = (int)a->n_used;
+    m.ids = a->ids_dev; m.ids_nb0 = a->ids_nb0; m.ids_nb1 = a->ids_nb1;
+    m.dst = a->dst_dev; m.dst_nb1 = a->dst_nb1; m.dst_nb2 = a->dst_nb2;
+    m.a16 = (uint16_t *)(ws + L.a16);
+    m.scales = (float *)(ws + L.scales);
+    m.off = (int32_t *)(ws + L.off);
+    m.rows = (int32_t *)(ws + L.rows);
+    m.tiles = (int32_t *)(ws + L.tiles);
+    m.n_tiles = (int32_t *)(ws + L.n_tiles);
+    m.err = err_dev ? err_dev : (int32_t *)(ws + L.err);
+    return hip_status(mx::launch_moe(a->wtype, m, S(stream)));
+}
+
 }  // extern "C"

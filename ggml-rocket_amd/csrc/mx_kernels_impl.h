@@ -45,6 +45,29 @@ struct FaArgs {
     float scale, softcap;
 };
 
+// MUL_MAT_ID launch: strides in elements; scratch pointers carved from the caller's workspace.
+struct MoeArgs {
+    const void * w;            // expert panel, E*N rows of K, HBM layout
+    int E, N, K;
+    const float * b;           // [T][ne11][K], row stride b_nb1 (rows contiguous)
+    int64_t b_nb1;
+    int ne11, T, U;
+    const int32_t * ids;       // ids[t][s] at t*ids_nb1 + s*ids_nb0
+    int64_t ids_nb0, ids_nb1;
+    float * dst;               // dst[t][s][:] at t*dst_nb2 + s*dst_nb1
+    int64_t dst_nb1, dst_nb2;
+    uint16_t * a16;            // [T*ne11][K] packed activations
+    float * scales;            // [T*ne11]
+    int32_t * off;             // [E+1] bucket offsets
+    int32_t * rows;            // [T*U] bucketed row ids (t*U + s)
+    int32_t * tiles;           // [2*max_tiles] (expert, first row)
+    int32_t * n_tiles;         // [1]
+    int32_t * err;             // [1] set when an id is out of range
+};
+
+int moe_max_tiles(int T, int U, int E);
+hipError_t launch_moe(int wt, const MoeArgs & a, hipStream_t st);
+
 int fa_blocks_per_split(const FaArgs & a);
 hipError_t launch_fa(const FaArgs & a, hipStream_t st);
 

@@ -50,6 +50,18 @@ class FaArgs(ctypes.Structure):
                 ("scale", ctypes.c_float), ("max_bias", ctypes.c_float), ("softcap", ctypes.c_float)]
 
 
+class MoeArgs(ctypes.Structure):
+    _fields_ = [("wtype", ctypes.c_int),
+                ("as_dev", ctypes.c_void_p), ("n_expert", ctypes.c_int64), ("N", ctypes.c_int64),
+                ("K", ctypes.c_int64),
+                ("b_dev", ctypes.c_void_p), ("ne11", ctypes.c_int64), ("b_nb1", ctypes.c_int64),
+                ("b_nb2", ctypes.c_int64),
+                ("ids_dev", ctypes.c_void_p), ("n_used", ctypes.c_int64), ("ids_nb0", ctypes.c_int64),
+                ("ids_nb1", ctypes.c_int64),
+                ("n_tokens", ctypes.c_int64),
+                ("dst_dev", ctypes.c_void_p), ("dst_nb1", ctypes.c_int64), ("dst_nb2", ctypes.c_int64)]
+
+
 def lib():
     """Load the built backend library. Raises if it has not been built."""
     global _lib
@@ -88,11 +100,11 @@ def _bind_optional(L):
         L.mi355x_flash_attn_workspace.restype = sz
         L.mi355x_flash_attn_workspace.argtypes = [pa, i32]
         L.mi355x_flash_attn.argtypes = [pa, i32, vp, sz, vp]
-    if hasattr(L, "mi355x_mul_mat_id_workspace"):
+    if hasattr(L, "mi355x_mul_mat_id"):
+        pm = ctypes.POINTER(MoeArgs)
         L.mi355x_mul_mat_id_workspace.restype = sz
-        L.mi355x_mul_mat_id_workspace.argtypes = [i64, i64, i64, i64, i64, i64]
-        L.mi355x_mul_mat_id.argtypes = [i32, vp, i64, i64, i64, vp, i64, vp, i64, i64, vp,
-                                        vp, sz, vp]
+        L.mi355x_mul_mat_id_workspace.argtypes = [pm]
+        L.mi355x_mul_mat_id.argtypes = [pm, vp, sz, vp, vp]
 
 
 def check(status: int, what: str = "call"):
@@ -212,4 +224,24 @@ def flash_attn(q, k, v, mask, scale: float, softcap: float = 0.0, nsplit: int = 
         workspace = torch.empty(need, dtype=torch.uint8, device=q.device)
     wp = workspace.data_ptr() if need else None
     check(lib().mi355x_flash_attn(ctypes.byref(a), nsplit, wp, need, stream_handle()), "flash_attn")
+    return out
+
+
+def mul_mat_id(wtype: int, as_dev, n_expert: int, N: int, K: int, b, ids, out=None, workspace=None,
+               err=None):
+    """as_dev: expert panel in HBM layout (n_expert*N rows); b [T, ne11, K] f32; ids [T, n_used]
+    int32. Returns dst [T, n_used, N] f32."""
+    torch = _torch()
+    T, ne11, _ = b.shape
+    n_used = ids.shape[1]
+    if out is None:
+        out = torch.empty((T, n_used, N), dtype=torch.float32, device=b.device)
+    a = MoeArgs(wtype, as_dev.data_ptr(), n_expert, N, K, b.data_ptr(), ne11, b.stride(1), b.stride(0),
+                ids.data_ptr(), n_used, ids.stride(1), ids.stride(0), T,
+                out.data_ptr(), out.stride(1), out.stride(0))
+    need = int(lib().mi355x_mul_mat_id_workspace(ctypes.byref(a)))
+    if workspace is None or workspace.numel() < need:
+        workspace = torch.empty(max(need, 1), dtype=torch.uint8, device=b.device)
+    check(lib().mi355x_mul_mat_id(ctypes.byref(a), _ptr(workspace), workspace.numel(),
+                                  _ptr(err) if err is not None else None, stream_handle()), "mul_mat_id")
     return out

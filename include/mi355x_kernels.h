@@ -143,6 +143,32 @@ MI355X_API size_t mi355x_flash_attn_workspace(const mi355x_fa_args * a, int nspl
 MI355X_API int mi355x_flash_attn(const mi355x_fa_args * a, int nsplit,
                                  void * workspace_dev, size_t workspace_bytes, void * stream);
 
+/* ---- MUL_MAT_ID --------------------------------------------------------------------------- */
+
+/* One expert-GEMM op. Strides in ELEMENTS. */
+typedef struct mi355x_moe_args {
+    int wtype;
+    const void * as_dev;      int64_t n_expert, N, K;     /* experts [E][N][K], HBM layout over E*N rows */
+    const float * b_dev;      int64_t ne11, b_nb1, b_nb2; /* activations [T][ne11][K]; rows contiguous */
+    const int32_t * ids_dev;  int64_t n_used, ids_nb0, ids_nb1;  /* ids[t][s] */
+    int64_t n_tokens;
+    float * dst_dev;          int64_t dst_nb1, dst_nb2;   /* dst[t][s][:] */
+} mi355x_moe_args;
+
+/* Workspace bytes of mi355x_mul_mat_id for this op. */
+MI355X_API size_t mi355x_mul_mat_id_workspace(const mi355x_moe_args * a);
+
+/* dst[t][s][:] = as[ids[t][s]] . b[t][s % ne11][:] for every token t and slot s, in one device
+ * pipeline with no host synchronisation: the distinct activation rows are packed once, the rows
+ * are bucketed by expert on the device, and one grouped launch runs every (expert tile, N block)
+ * with the expert's weight dequantized in LDS. An id outside [0, n_expert) leaves its row
+ * unwritten and sets *err_dev (a device int32, may be NULL) to 1; the host-buffer path checks ids
+ * before calling. K % 32 == 0 and a whole number of blocks, N % 16 == 0.
+ * Replaces the per-expert loop of ggml-rocket.cpp:6783-6941 and its device calls
+ * rocket_matmul_int8_prepacked_gw (6833) / rocket_matmul_fp16_mt (6922). */
+MI355X_API int mi355x_mul_mat_id(const mi355x_moe_args * a, void * workspace_dev, size_t workspace_bytes,
+                                 int32_t * err_dev, void * stream);
+
 #ifdef __cplusplus
 }
 #endif
