@@ -1,0 +1,367 @@
+#!/usr/bin/env python3
+"""Prefill benchmark: the backend-claimed ops of an 8B-shape Q4_K prefill on one MI355X.
+
+Workload (BASELINE metric "prefill tok/s (8B-shape Q4_K, 2048 tok)"): a Llama-3-8B-shaped stack
+(32 layers, d 4096, FFN 14336, 32 query / 8 KV heads, head dim 128) with random-init Q4_K
+weights (quantized from N(0, 0.02); every layer distinct), prefilling 2048 tokens in 4
+micro-batches of 512. One step runs, per micro-batch and layer, exactly the ops this backend
+claims in such a prefill: the fused Q/K/V projection group, FLASH_ATTN_EXT over the causal KV
+prefix (n_kv = 512, 1024, 1536, 2048), the output projection, the fused gate/up group and the
+down projection. Ops the backend never claims (norms, RoPE, SiLU-mul, residual adds, the
+last-token lm_head at M=1) are not in the step. Inputs are resident in HBM when timing starts.
+
+Routes: "prepacked-q" (default; the reference's ROCKET_QUANT_RESIDENT route): each Q4_K weight
+is decoded once to an fp16 HBM copy and the GEMMs read fp16. "mt": the GEMMs read the Q4_K
+blocks and dequantize them in LDS on every call.
+
+Prints ONE JSON line (rank 0). `value` is tokens/s of the whole step; `roofline` is the dominant
+kernel's (the GEMM) live HIP-event figure; `cpu_baseline` is the CPU oracle timed on a bounded
+sample of the same workload on this host.
+"""
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+sys.path.insert(0, os.path.join(ROOT, "ggml-rocket_amd"))
+
+METRIC = "prefill tok/s (8B-shape Q4_K, 2048 tok); MUL_MAT/FA TFLOP/s vs MFMA peak"
+PEAK_F16_TFLOPS = 2500.0
+PEAK_HBM_GBS = 8000.0
+
+L_LAYERS, D_MODEL, FFN, NH, NKV, HD = 32, 4096, 14336, 32, 8, 128
+TOKENS, UBATCH = 2048, 512
+
+
+def parse():
+    p = argparse.ArgumentParser()
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=10)
+    p.add_argument("--warmup", type=int, default=2)
+    p.add_argument("--route", choices=["prepacked-q", "mt"], default="prepacked-q")
+    p.add_argument("--layers", type=int, default=L_LAYERS)
+    p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--cpu-threads", type=int, default=0)
+    return p.parse_args()
+
+
+class Prefill:
+    def __init__(self, route, n_layers):
+        import numpy as np
+        import torch
+        import ggml_mi355x as mx
+        from oracle import oracle as O
+        self.mx, self.torch, self.np = mx, torch, np
+        self.route = route
+        self.wt = mx.F16 if route == "prepacked-q" else mx.Q4_K
+        dev = "cuda"
+        t0 = time.time()
+        shapes = {"q": (D_MODEL, D_MODEL), "k": (NKV * HD, D_MODEL), "v": (NKV * HD, D_MODEL),
+                  "o": (D_MODEL, D_MODEL), "gate": (FFN, D_MODEL), "up": (FFN, D_MODEL),
+                  "down": (D_MODEL, FFN)}
+        self.shapes = shapes
+        # layer 0: quantized on the host from N(0, 0.02); the other layers get fresh random
+        # nibbles under layer 0's block headers (valid Q4_K, distinct bytes per layer)
+        self.host_q4 = {}
+        base = {}
+        for i, (name, (N, K)) in enumerate(shapes.items()):
+            W = O.fill_normal((N, K), 0x5EED0000 + 80 + i, 0.0, 0.02)
+            self.host_q4[name] = O.quantize(O.Q4_K, W)
+            base[name] = torch.from_numpy(self.host_q4[name].reshape(-1)).to(dev)
+            del W
+        g = torch.Generator(device=dev)
+        g.manual_seed(1234)
+        self.layers = []
+        for li in range(n_layers):
+            lw = {}
+            for name, (N, K) in shapes.items():
+                q = base[name].clone() if li == 0 else base[name].clone()
+                if li > 0:
+                    blk = q.view(-1, 144)
+                    blk[:, 16:] = torch.randint(0, 256, (blk.shape[0], 128), dtype=torch.uint8, device=dev,
+                                                generator=g)
+                if self.wt == mx.F16:
+                    lw[name] = mx.dequant_f16(mx.Q4_K, q, N, K).view(torch.uint8).reshape(-1)
+                    del q
+                else:
+                    lw[name] = q
+            self.layers.append(lw)
+        torch.cuda.synchronize()
+        self.setup_s = time.time() - t0
+        # activations / scratch
+        f32 = torch.float32
+        T = UBATCH
+        self.x = torch.randn(T, D_MODEL, device=dev, dtype=f32)
+        self.qo = torch.empty(T, D_MODEL, device=dev, dtype=f32)
+        self.ko = torch.empty(T, NKV * HD, device=dev, dtype=f32)
+        self.vo = torch.empty(T, NKV * HD, device=dev, dtype=f32)
+        self.attn = torch.empty(T, NH * HD, device=dev, dtype=f32)
+        self.oo = torch.empty(T, D_MODEL, device=dev, dtype=f32)
+        self.go = torch.empty(T, FFN, device=dev, dtype=f32)
+        self.uo = torch.empty(T, FFN, device=dev, dtype=f32)
+        self.act = torch.randn(T, FFN, device=dev, dtype=f32)
+        self.do = torch.empty(T, D_MODEL, device=dev, dtype=f32)
+        self.a16 = torch.empty(T, FFN, device=dev, dtype=torch.float16)
+        self.scales = torch.empty(T, device=dev, dtype=f32)
+        self.kc = torch.randn(TOKENS, NKV, HD, device=dev).half()
+        self.vc = torch.randn(TOKENS, NKV, HD, device=dev).half()
+        self.masks = []
+        for u in range(TOKENS // UBATCH):
+            n_kv = UBATCH * (u + 1)
+            j = torch.arange(n_kv, device=dev)[None, :]
+            t = torch.arange(T, device=dev)[:, None]
+            m = torch.zeros(T, n_kv, device=dev)
+            m[j > UBATCH * u + t] = float("-inf")
+            self.masks.append(m.half())
+        self.fa_ws = torch.empty(64 << 20, dtype=torch.uint8, device=dev)
+        self.timing = None
+
+    # ---- op launchers (optionally bracketed by events on the launch stream) ----
+    def _ev(self, kind, fn):
+        if self.timing is None:
+            fn()
+            return
+        torch = self.torch
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s.record()
+        fn()
+        e.record()
+        self.timing.append((kind, s, e))
+
+    def _pack(self, x, K):
+        a16 = self.a16[:, :K]
+        self._ev("pack", lambda: self.mx.check(self.mx.lib().mi355x_pack_act(
+            self.mx._ptr(x), x.stride(0), x.shape[0], K, self.mx._ptr(self.a16),
+            self.mx._ptr(self.scales), self.mx.stream_handle()), "pack"))
+        return a16
+
+    def _gemm(self, K, outs, flops):
+        mx = self.mx
+        arr = (mx.GemmOut * len(outs))()
+        for i, (w, N, c) in enumerate(outs):
+            arr[i] = mx.GemmOut(w.data_ptr(), N, 0, N, c.data_ptr(), c.stride(0))
+        self._ev("gemm", lambda: mx.check(mx.lib().mi355x_gemm(
+            self.wt, mx._ptr(self.a16), mx._ptr(self.scales), UBATCH, K, arr, len(outs),
+            mx.stream_handle()), "gemm"))
+        self.flops["gemm"] += flops
+
+    def _fa(self, u):
+        n_kv = UBATCH * (u + 1)
+        mx = self.mx
+        q = self.qo.view(UBATCH, NH, HD).permute(1, 0, 2)
+        k = self.kc[:n_kv].permute(1, 0, 2)
+        v = self.vc[:n_kv].permute(1, 0, 2)
+        m = self.masks[u]
+        out = self.attn.view(UBATCH, NH, HD)
+        self._ev("fa", lambda: mx.flash_attn(q, k, v, m, 1.0 / math.sqrt(HD), out=out, workspace=self.fa_ws))
+        self.flops["fa"] += 4.0 * NH * UBATCH * n_kv * HD
+
+    def step(self):
+        sh = self.shapes
+        for u in range(TOKENS // UBATCH):
+            for lw in self.layers:
+                M = UBATCH
+                self._pack(self.x, D_MODEL)
+                self._gemm(D_MODEL, [(lw["q"], sh["q"][0], self.qo), (lw["k"], sh["k"][0], self.ko),
+                                     (lw["v"], sh["v"][0], self.vo)],
+                           2.0 * M * D_MODEL * (D_MODEL + 2 * NKV * HD))
+                self._fa(u)
+                self._pack(self.attn, D_MODEL)
+                self._gemm(D_MODEL, [(lw["o"], D_MODEL, self.oo)], 2.0 * M * D_MODEL * D_MODEL)
+                self._pack(self.x, D_MODEL)
+                self._gemm(D_MODEL, [(lw["gate"], FFN, self.go), (lw["up"], FFN, self.uo)],
+                           2.0 * M * D_MODEL * 2 * FFN)
+                self._pack(self.act, FFN)
+                self._gemm(FFN, [(lw["down"], D_MODEL, self.do)], 2.0 * M * FFN * D_MODEL)
+
+    def reset_counters(self, timing):
+        self.flops = {"gemm": 0.0, "fa": 0.0}
+        self.timing = [] if timing else None
+
+
+def gemm_weight_bytes(route):
+    per_w = 2.0 if route == "prepacked-q" else 144.0 / 256.0
+    n = D_MODEL * D_MODEL * 2 + 2 * NKV * HD * D_MODEL + 3 * FFN * D_MODEL
+    return n * per_w
+
+
+def cpu_baseline(prefill, threads):
+    """The oracle (fp64 GEMM from the Q4_K payload, double attention) on a bounded sample of the
+    same workload: layer 0, S tokens of the last micro-batch (n_kv 2048), all seven projections
+    and the attention of those tokens; tokens/s = S / (sample time * 32 layers)."""
+    import numpy as np
+    from oracle import oracle as O
+    O.lib()
+    nt = threads or min(16, os.cpu_count() or 1)
+    S = 128
+    X = O.fill_normal((S, D_MODEL), 5)
+    Xf = O.fill_normal((S, FFN), 6)
+    Qh = O.fill_normal((NH, S, HD), 7)
+    K16 = O.f32_to_f16_bits(O.fill_normal((NKV, TOKENS, HD), 8))
+    V16 = O.f32_to_f16_bits(O.fill_normal((NKV, TOKENS, HD), 9))
+    t = np.arange(S)[:, None] + (TOKENS - S)
+    M16 = O.f32_to_f16_bits(np.where(np.arange(TOKENS)[None, :] > t, -np.inf, 0.0).astype(np.float32))
+    O.mul_mat(O.Q4_K, prefill.host_q4["k"], X, NKV * HD, D_MODEL, nthreads=nt)   # warm
+    reps, t0 = 0, time.time()
+    while True:   # repeat the sample until about 10 s of CPU work (at most 30 s)
+        for name, (N, K) in prefill.shapes.items():
+            O.mul_mat(O.Q4_K, prefill.host_q4[name], Xf if K == FFN else X, N, K, nthreads=nt)
+        O.flash_attn(Qh, K16, V16, M16, 1.0 / math.sqrt(HD), nthreads=nt)
+        reps += 1
+        el = time.time() - t0
+        if el >= 10.0 or el * (reps + 1) / reps > 30.0:
+            break
+    dt = (time.time() - t0) / reps
+    return {"value": S / (dt * L_LAYERS), "unit": "tok/s", "cores": nt, "kind": "port",
+            "sample": f"CPU oracle restatement (not ggml-cpu): layer 0 of the workload, {S} tokens "
+                      f"of the last 512-token micro-batch (n_kv 2048): 7 Q4_K projections as fp64 "
+                      f"GEMM + double attention, {dt:.2f} s per pass (mean of {reps}), "
+                      f"scaled x{L_LAYERS} layers"}
+
+
+def time_ops(pf, reps=20):
+    """Live HIP-event timing of each distinct launch of the step: events bracket `reps`
+    back-to-back launches of the same op on its stream (each launch runs longer than the host
+    needs to enqueue the next, so the events see GPU time, not launch overhead)."""
+    torch = pf.torch
+    lw = pf.layers[0]
+    sh = pf.shapes
+    M = UBATCH
+    ops = [
+        ("pack", 0.0, 4 * L_LAYERS * 4, lambda: pf._pack(pf.x, D_MODEL)),
+        ("gemm", 2.0 * M * D_MODEL * (D_MODEL + 2 * NKV * HD), L_LAYERS * 4,
+         lambda: pf._gemm(D_MODEL, [(lw["q"], sh["q"][0], pf.qo), (lw["k"], sh["k"][0], pf.ko),
+                                    (lw["v"], sh["v"][0], pf.vo)], 0.0)),
+        ("gemm", 2.0 * M * D_MODEL * D_MODEL, L_LAYERS * 4,
+         lambda: pf._gemm(D_MODEL, [(lw["o"], D_MODEL, pf.oo)], 0.0)),
+        ("gemm", 2.0 * M * D_MODEL * 2 * FFN, L_LAYERS * 4,
+         lambda: pf._gemm(D_MODEL, [(lw["gate"], FFN, pf.go), (lw["up"], FFN, pf.uo)], 0.0)),
+        ("gemm", 2.0 * M * FFN * D_MODEL, L_LAYERS * 4,
+         lambda: pf._gemm(FFN, [(lw["down"], D_MODEL, pf.do)], 0.0)),
+    ]
+    for u in range(TOKENS // UBATCH):
+        ops.append(("fa", 4.0 * NH * UBATCH * UBATCH * (u + 1) * HD, L_LAYERS, (lambda uu=u: pf._fa(uu))))
+    pf.reset_counters(False)
+    out = []
+    for kind, flops, per_step, fn in ops:
+        for _ in range(3):
+            fn()
+        torch.cuda.synchronize()
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s.record()
+        for _ in range(reps):
+            fn()
+        e.record()
+        torch.cuda.synchronize()
+        out.append((kind, flops, per_step, s.elapsed_time(e) * 1e-3 / reps))
+    return out
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); "
+              f"the multi-GPU sharding is a design note, not a benchmark.", file=sys.stderr)
+        sys.exit(2)
+    import torch
+    torch.cuda.set_device(0)
+    pf = Prefill(args.route, args.layers)
+
+    pf.reset_counters(False)
+    for _ in range(args.warmup):
+        pf.step()
+    torch.cuda.synchronize()
+
+    # the step is captured once into a HIP graph and replayed: ~1300 launches per step would
+    # otherwise be bound by host launch overhead, not by the GPU
+    graph = None
+    try:
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            pf.step()
+        torch.cuda.current_stream().wait_stream(side)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            pf.step()
+        graph.replay()
+        torch.cuda.synchronize()
+    except Exception as exc:  # eager steps still measure the same work
+        print(f"bench.py: graph capture unavailable ({exc}); timing eager steps", file=sys.stderr)
+        graph = None
+
+    steps = args.steps
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        if graph is not None:
+            graph.replay()
+        else:
+            pf.step()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms = wall / steps * 1e3
+    scale_layers = L_LAYERS / args.layers
+    tok_s = TOKENS / (wall / steps) / scale_layers
+
+    ops = time_ops(pf)
+    per = {}
+    for kind, flops, per_step, sec in ops:
+        d = per.setdefault(kind, {"flops": 0.0, "sec": 0.0, "launches": 0})
+        d["flops"] += flops * per_step
+        d["sec"] += sec * per_step
+        d["launches"] += per_step
+    gemm, fa = per["gemm"], per["fa"]
+    gemm_tf = gemm["flops"] / gemm["sec"] / 1e12
+    fa_tf = fa["flops"] / fa["sec"] / 1e12
+    wbytes = gemm_weight_bytes(args.route) * L_LAYERS * (TOKENS // UBATCH)
+    kern_ms = sum(d["sec"] for d in per.values()) * 1e3
+    res = {
+        "metric": METRIC,
+        "value": round(tok_s, 1),
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 3),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16",
+        "data": "synthetic (random-init Q4_K weights from N(0,0.02), N(0,1) activations and KV)",
+        "config": {"workload": "llama3-8b-shape Q4_K prefill, 2048 tokens in 4 micro-batches of 512: "
+                               "the backend-claimed ops (fused QKV, FLASH_ATTN_EXT, O, fused gate/up, "
+                               "down) x 32 layers",
+                   "layers": args.layers, "route": args.route, "global_batch": TOKENS,
+                   "ubatch": UBATCH, "parallelism": "none (1 GPU)",
+                   "replay": "hip graph" if graph is not None else "eager"},
+        "roofline": {"bound": "mfma", "achieved": round(gemm_tf, 1), "peak": PEAK_F16_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(gemm_tf / PEAK_F16_TFLOPS, 4), "traffic": None,
+                     "kernel": "gemm_kernel (fp16 MFMA 32x32x16)",
+                     "avg_launch_us": round(gemm["sec"] / gemm["launches"] * 1e6, 2),
+                     "flop_per_launch": round(gemm["flops"] / gemm["launches"])},
+        "kernels": {
+            "gemm": {"tflops": round(gemm_tf, 1), "frac_peak": round(gemm_tf / PEAK_F16_TFLOPS, 4),
+                     "ms_per_step": round(gemm["sec"] * 1e3, 3), "launches_per_step": gemm["launches"],
+                     "weight_GBps": round(wbytes / gemm["sec"] / 1e9, 1)},
+            "flash_attn": {"tflops": round(fa_tf, 1), "frac_peak": round(fa_tf / PEAK_F16_TFLOPS, 4),
+                           "ms_per_step": round(fa["sec"] * 1e3, 3), "launches_per_step": fa["launches"],
+                           "flop_count": "dense rectangle 4*H*T*n_kv*d"},
+            "pack_act": {"ms_per_step": round(per["pack"]["sec"] * 1e3, 3)},
+            "kernel_sum_ms_per_step": round(kern_ms, 3),
+            "per_op_us": {f"{k}:{i}": round(sec * 1e6, 2) for i, (k, _, _, sec) in enumerate(ops)},
+        },
+        "setup_s": round(pf.setup_s, 1),
+    }
+    if not args.no_cpu_baseline:
+        res["cpu_baseline"] = cpu_baseline(pf, args.cpu_threads)
+    print(json.dumps(res), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -185,9 +185,13 @@ MI355X_API int mi355x_flash_attn_auto_split(const mi355x_fa_args * a) {
     const mx::FaArgs f = fa_lower(a, 1);
     const int nb = mx::fa_blocks_per_split(f);
     const int ntiles = (a->KV + 63) / 64;
-    int cus = 256;
-    mi355x_device_info di;
-    if (mi355x_get_device_info(&di) == MI355X_OK && di.compute_units > 0) cus = di.compute_units;
+    static int cus = 0;   // read once: this may run while a stream is being captured
+    if (cus == 0) {
+        int dev = 0;
+        hipDeviceProp_t p;
+        cus = (hipGetDevice(&dev) == hipSuccess && hipGetDeviceProperties(&p, dev) == hipSuccess &&
+               p.multiProcessorCount > 0) ? p.multiProcessorCount : 256;
+    }
     // fill about two blocks per CU, keeping at least 8 key tiles per split
     int ns = nb > 0 ? (2 * cus + nb - 1) / nb : 1;
     const int max_by_len = ntiles / 8 > 0 ? ntiles / 8 : 1;

@@ -28,12 +28,15 @@ __device__ __forceinline__ float16v mfma32(const half8 & a, const half8 & b, con
     return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
 }
 
-// Byte offset of the 16-byte chunk `c` of row `r` in an LDS tile whose rows hold `chunks`
-// 16-byte chunks (chunks a power of two >= 8). The chunk index is XORed with the row's low
-// three bits, so the 32 rows one MFMA fragment read touches spread over every bank.
+// Byte offset of the 16-byte chunk `c` of row `r` in an LDS tile whose rows hold CHUNKS 16-byte
+// chunks (CHUNKS a power of two, 4..16). LDS has 64 banks of 4 bytes, so a 256-byte window
+// holds 16 chunk slots and 16 / CHUNKS rows. The chunk index is XORed with the row's index
+// within each group of CHUNKS windows, so 16 consecutive rows read at one logical chunk (what an
+// MFMA fragment read does) land on 16 distinct slots: no bank conflict.
 template <int CHUNKS>
 __device__ __forceinline__ int swz(int r, int c) {
-    return r * (CHUNKS * 16) + ((c ^ (r & 7)) << 4);
+    constexpr int RPW = 16 / CHUNKS;   // rows per 256-byte window
+    return r * (CHUNKS * 16) + ((c ^ ((r / RPW) & (CHUNKS - 1))) << 4);
 }
 
 __device__ __forceinline__ uint16_t f2h_bits(float f) {

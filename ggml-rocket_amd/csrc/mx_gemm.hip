@@ -22,168 +22,269 @@
 namespace mx {
 
 // ---------------------------------------------------------------------------------------------
-// activation pack: one wave per row
+// activation pack: one 256-thread block per row. A row of up to PACK_REG_MAX floats is read
+// once into registers (all loads in flight together), reduced, scaled and written; longer rows
+// take a second pass over memory.
 // ---------------------------------------------------------------------------------------------
-__global__ void __launch_bounds__(256) pack_act_kernel(const float * __restrict__ X, int64_t ldx,
-                                                       int M, int K, uint16_t * __restrict__ A16,
-                                                       int64_t lda, float * __restrict__ scales) {
-    const int wave = threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
-    const int m = blockIdx.x * 4 + wave;
-    if (m >= M) return;
+constexpr int PACK_THREADS = 256;
+constexpr int PACK_VEC = 16;                                 // float4 per thread held in registers
+constexpr int PACK_REG_MAX = PACK_THREADS * PACK_VEC * 4;    // 16384 floats
+
+__global__ void __launch_bounds__(PACK_THREADS) pack_act_kernel(const float * __restrict__ X, int64_t ldx,
+                                                                int M, int K, uint16_t * __restrict__ A16,
+                                                                int64_t lda, float * __restrict__ scales) {
+    __shared__ float red[PACK_THREADS / WAVE];
+    const int t = threadIdx.x, lane = t % WAVE, wave = t / WAVE;
+    const int m = blockIdx.x;
     const float * x = X + (int64_t)m * ldx;
+    uint16_t * a = A16 + (int64_t)m * lda;
+    const int n4 = K / 4;
+    float4v v[PACK_VEC];
     float amax = 0.0f;
-    for (int k = lane * 4; k < K; k += WAVE * 4) {
-        const float4v v = *(const float4v *)(x + k);
-        amax = fmaxf(amax, fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3]))));
+#pragma unroll
+    for (int i = 0; i < PACK_VEC; i++) {
+        const int c = t + i * PACK_THREADS;
+        v[i] = c < n4 ? *(const float4v *)(x + 4 * c) : float4v{0, 0, 0, 0};
+        amax = fmaxf(amax, fmaxf(fmaxf(fabsf(v[i][0]), fabsf(v[i][1])), fmaxf(fabsf(v[i][2]), fabsf(v[i][3]))));
+    }
+    for (int c = t + PACK_VEC * PACK_THREADS; c < n4; c += PACK_THREADS) {
+        const float4v w = *(const float4v *)(x + 4 * c);
+        amax = fmaxf(amax, fmaxf(fmaxf(fabsf(w[0]), fabsf(w[1])), fmaxf(fabsf(w[2]), fabsf(w[3]))));
     }
     amax = wave_max(amax);
+    if (lane == 0) red[wave] = amax;
+    __syncthreads();
+    amax = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
     const float s = amax > 0.0f ? amax : 1.0f;
     const float inv = 1.0f / s;
-    uint16_t * a = A16 + (int64_t)m * lda;
-    for (int k = lane * 4; k < K; k += WAVE * 4) {
-        const float4v v = *(const float4v *)(x + k);
-        u32x2 o;
-        o[0] = pack2h(v[0] * inv, v[1] * inv);
-        o[1] = pack2h(v[2] * inv, v[3] * inv);
-        *(u32x2 *)(a + k) = o;
+#pragma unroll
+    for (int i = 0; i < PACK_VEC; i++) {
+        const int c = t + i * PACK_THREADS;
+        if (c < n4) {
+            u32x2 o;
+            o[0] = pack2h(v[i][0] * inv, v[i][1] * inv);
+            o[1] = pack2h(v[i][2] * inv, v[i][3] * inv);
+            *(u32x2 *)(a + 4 * c) = o;
+        }
     }
-    if (lane == 0) scales[m] = s;
+    for (int c = t + PACK_VEC * PACK_THREADS; c < n4; c += PACK_THREADS) {
+        const float4v w = *(const float4v *)(x + 4 * c);
+        u32x2 o;
+        o[0] = pack2h(w[0] * inv, w[1] * inv);
+        o[1] = pack2h(w[2] * inv, w[3] * inv);
+        *(u32x2 *)(a + 4 * c) = o;
+    }
+    if (t == 0) scales[m] = s;
 }
 
 // ---------------------------------------------------------------------------------------------
 // GEMM
+//
+// Block = 256 threads (4 waves in a WM x WN grid), output tile BM x BN, K staged BK = 64 at a
+// time through a double-buffered, XOR-swizzled LDS tile. Global loads run R slabs ahead in a ring
+// of register sets (the loop is unrolled by R so the sets are static registers): slab k+R is
+// requested while slab k is multiplied, and slab k+1 is written to LDS only after that, which
+// hides HBM latency behind R-1 slabs of MFMA work.
+// KSPLIT = 2 splits K between two blocks that add their halves atomically into a zeroed output:
+// with exactly two addends the sum is the same in either order, so the result is deterministic.
 // ---------------------------------------------------------------------------------------------
-constexpr int BM = 128, BN = 128, BK = 64;
+constexpr int BK = 64;
 constexpr int GEMM_THREADS = 256;
-constexpr int TILE_BYTES = BM * BK * 2;   // 16 KiB, A and B tiles alike (BM == BN)
 
-// A-tile load stage: thread t takes row t/2, values 32*(t%2) .. +31 of the 64-wide K slab.
-struct ALoad {
-    u32x4 v[4];
-    __device__ __forceinline__ void load(const uint16_t * A, int64_t lda, int M, int K, int m0,
-                                         int64_t k0, int t) {
-        const int r = m0 + t / 2;
-        const int64_t k = k0 + 32 * (t % 2);
-        const bool ok = r < M && k < K;
-        const u32x4 * p = (const u32x4 *)(A + (int64_t)r * lda + k);
-#pragma unroll
-        for (int i = 0; i < 4; i++) v[i] = ok ? p[i] : u32x4{0, 0, 0, 0};
-    }
-    __device__ __forceinline__ void store(uint8_t * lds, int t) const {
-        const int r = t / 2, c0 = 4 * (t % 2);
-#pragma unroll
-        for (int i = 0; i < 4; i++) *(u32x4 *)(lds + swz<8>(r, c0 + i)) = v[i];
-    }
+template <int BM, int BN, int WM, int WN, int R>
+struct GemmCfg {
+    static constexpr int TM = BM / WM, TN = BN / WN;        // wave tile
+    static constexpr int MI = TM / 32, NJ = TN / 32;        // MFMA blocks per wave
+    static constexpr int A_CHUNKS = BM * (BK / 8) / GEMM_THREADS;   // 16-byte chunks per thread
+    static constexpr int B_ITEMS = BN * 2 / GEMM_THREADS;           // (row, half) items per thread
+    static constexpr int A_BYTES = BM * BK * 2, B_BYTES = BN * BK * 2;
+    static constexpr int STAGE = A_BYTES + B_BYTES;
+    static constexpr int LDS = 2 * STAGE;
+    static_assert(WM * WN == 4, "4 waves");
+    static_assert(A_CHUNKS >= 1 && B_ITEMS >= 1, "tile too small");
 };
 
-template <int WT>
-__device__ __forceinline__ void store_w(uint8_t * lds, int t, const WLoad<WT> & w) {
-    u32x4 out[4];
-    int run0, run1;
-    w.decode(t % 2, out, run0, run1);
-    const int r = t / 2;
-    *(u32x4 *)(lds + swz<8>(r, run0 / 8)) = out[0];
-    *(u32x4 *)(lds + swz<8>(r, run0 / 8 + 1)) = out[1];
-    *(u32x4 *)(lds + swz<8>(r, run1 / 8)) = out[2];
-    *(u32x4 *)(lds + swz<8>(r, run1 / 8 + 1)) = out[3];
+// One pipeline stage in registers: raw loads plus whether each item is real; the masking is
+// applied when the stage is written to LDS, so the loads stay in flight until then.
+template <int WT, int NA, int NB>
+struct Slab {
+    u32x4 a[NA];
+    bool a_ok[NA];
+    WLoad<WT> b[NB];
+};
+
+template <int WT, class C>
+__device__ __forceinline__ void slab_load(Slab<WT, C::A_CHUNKS, C::B_ITEMS> & s, const GemmArgs & args,
+                                          const GemmGroup & G, int m0, int n0, int64_t k0, int t) {
+    const int M = args.M, K = args.K;
+#pragma unroll
+    for (int i = 0; i < C::A_CHUNKS; i++) {
+        const int c = t + i * GEMM_THREADS;
+        const int r = m0 + c / 8;
+        const int64_t k = k0 + 8 * (c % 8);
+        s.a_ok[i] = r < M && k < K;
+        s.a[i] = *(const u32x4 *)(args.A + (int64_t)(r < M ? r : M - 1) * args.lda + (k < K ? k : 0));
+    }
+    const uint8_t * W = (const uint8_t *)G.W;
+#pragma unroll
+    for (int i = 0; i < C::B_ITEMS; i++) {
+        const int it = t + i * GEMM_THREADS;
+        const int n = n0 + it / 2;
+        const bool ok = n < G.N;
+        s.b[i].load(W, G.rows_total, K, G.row0 + (ok ? n : G.N - 1), k0, it % 2, ok);
+    }
 }
 
-// One K slab (64) of MFMA work for a wave's 64x64 quadrant.
-__device__ __forceinline__ void mma_slab(const uint8_t * As, const uint8_t * Bs, int wm, int wn,
-                                         int lane, float16v acc[2][2]) {
+template <int WT, class C>
+__device__ __forceinline__ void slab_store(const Slab<WT, C::A_CHUNKS, C::B_ITEMS> & s, uint8_t * st, int t) {
+#pragma unroll
+    for (int i = 0; i < C::A_CHUNKS; i++) {
+        const int c = t + i * GEMM_THREADS;
+        *(u32x4 *)(st + swz<8>(c / 8, c % 8)) = s.a_ok[i] ? s.a[i] : u32x4{0, 0, 0, 0};
+    }
+    uint8_t * bs = st + C::A_BYTES;
+#pragma unroll
+    for (int i = 0; i < C::B_ITEMS; i++) {
+        const int it = t + i * GEMM_THREADS;
+        const int r = it / 2;
+        u32x4 out[4];
+        int run0, run1;
+        s.b[i].decode(it % 2, out, run0, run1);
+        *(u32x4 *)(bs + swz<8>(r, run0 / 8)) = out[0];
+        *(u32x4 *)(bs + swz<8>(r, run0 / 8 + 1)) = out[1];
+        *(u32x4 *)(bs + swz<8>(r, run1 / 8)) = out[2];
+        *(u32x4 *)(bs + swz<8>(r, run1 / 8 + 1)) = out[3];
+    }
+}
+
+template <class C>
+__device__ __forceinline__ void mma_slab(const uint8_t * st, int wm, int wn, int lane,
+                                         float16v (&acc)[C::MI][C::NJ]) {
+    const uint8_t * As = st;
+    const uint8_t * Bs = st + C::A_BYTES;
     const int lr = lane % 32, lg = lane / 32;
 #pragma unroll
     for (int ks = 0; ks < BK / 16; ks++) {
         const int c = 2 * ks + lg;
-        half8 a[2], b[2];
+        half8 a[C::MI], b[C::NJ];
 #pragma unroll
-        for (int i = 0; i < 2; i++) {
-            a[i] = *(const half8 *)(As + swz<8>(wm * 64 + i * 32 + lr, c));
-            b[i] = *(const half8 *)(Bs + swz<8>(wn * 64 + i * 32 + lr, c));
-        }
+        for (int i = 0; i < C::MI; i++) a[i] = *(const half8 *)(As + swz<8>(wm * C::TM + i * 32 + lr, c));
 #pragma unroll
-        for (int i = 0; i < 2; i++)
+        for (int j = 0; j < C::NJ; j++) b[j] = *(const half8 *)(Bs + swz<8>(wn * C::TN + j * 32 + lr, c));
 #pragma unroll
-            for (int j = 0; j < 2; j++) acc[i][j] = mfma32(a[i], b[j], acc[i][j]);
+        for (int i = 0; i < C::MI; i++)
+#pragma unroll
+            for (int j = 0; j < C::NJ; j++) acc[i][j] = mfma32(a[i], b[j], acc[i][j]);
     }
 }
 
-template <int WT>
-__global__ void __launch_bounds__(GEMM_THREADS) gemm_kernel(GemmArgs args) {
+template <int WT, int BM, int BN, int WM, int WN, int R, int KSPLIT>
+__global__ void __launch_bounds__(GEMM_THREADS)
+__attribute__((amdgpu_waves_per_eu((BM == 128 && BN == 128) ? 2 : 1, (BM == 128 && BN == 128) ? 2 : 1)))
+gemm_kernel(GemmArgs args) {
+    // waves_per_eu pins the register budget to the occupancy the LDS allows anyway (2 blocks of
+    // a 128x128 tile per CU, 1 of the larger tiles), so the scheduler does not sink the prefetch
+    // loads next to their use to save registers.
+    using C = GemmCfg<BM, BN, WM, WN, R>;
     extern __shared__ __align__(16) uint8_t smem[];
-    // stage s: A tile at smem + s*TILE_BYTES, B tile at smem + (2+s)*TILE_BYTES
 
     const int t = threadIdx.x, lane = t % WAVE, wave = t / WAVE;
-    const int wm = wave / 2, wn = wave % 2;
+    const int wm = wave / WN, wn = wave % WN;
 
-    // tile id -> (global n tile, m tile); m is the fast index so the blocks that share a
-    // weight panel are neighbours (and, after xcd_tile, on one XCD).
+    // block -> (k split, global n tile, m tile); m is the fast index so the blocks that share a
+    // weight panel are neighbours (and, after xcd_tile, on one XCD)
     const int nblocks = gridDim.x;
-    const int tile = xcd_tile(blockIdx.x, nblocks);
+    int tile = xcd_tile(blockIdx.x, nblocks);
+    const int split = tile % KSPLIT;
+    tile /= KSPLIT;
     const int mt = tile % args.m_tiles, nt = tile / args.m_tiles;
     int g = 0;
 #pragma unroll
     for (int i = 1; i < GEMM_MAX_GROUPS; i++)
         if (i < args.ng && nt >= args.g[i].ntile_begin) g = i;
-    const GemmGroup & G = args.g[g];
+    GemmGroup G;
+    G.W = args.g[0].W; G.rows_total = args.g[0].rows_total; G.row0 = args.g[0].row0; G.N = args.g[0].N;
+    G.C = args.g[0].C; G.ldc = args.g[0].ldc; G.ntile_begin = args.g[0].ntile_begin;
+#pragma unroll
+    for (int i = 1; i < GEMM_MAX_GROUPS; i++)
+        if (i == g) {
+            G.W = args.g[i].W; G.rows_total = args.g[i].rows_total; G.row0 = args.g[i].row0; G.N = args.g[i].N;
+            G.C = args.g[i].C; G.ldc = args.g[i].ldc; G.ntile_begin = args.g[i].ntile_begin;
+        }
     const int n0 = (nt - G.ntile_begin) * BN;
     const int m0 = mt * BM;
-    const int M = args.M, K = args.K;
 
-    const uint8_t * W = (const uint8_t *)G.W;
-    const int64_t wrow = G.row0 + n0 + t / 2;
-    const bool wok = (n0 + t / 2) < G.N;
+    const int nk_all = (args.K + BK - 1) / BK;
+    const int per = (nk_all + KSPLIT - 1) / KSPLIT;
+    const int kb = split * per;
+    const int nk = max(0, min(nk_all, kb + per) - kb);
 
-    float16v acc[2][2];
+    float16v acc[C::MI][C::NJ];
 #pragma unroll
-    for (int i = 0; i < 2; i++)
+    for (int i = 0; i < C::MI; i++)
 #pragma unroll
-        for (int j = 0; j < 2; j++)
+        for (int j = 0; j < C::NJ; j++)
 #pragma unroll
             for (int e = 0; e < 16; e++) acc[i][j][e] = 0.0f;
 
-    const int nk = (K + BK - 1) / BK;
-    ALoad al;
-    WLoad<WT> wl;
-    al.load(args.A, args.lda, M, K, m0, 0, t);
-    wl.load(W, G.rows_total, K, wrow, 0, t % 2, wok);
-    al.store(smem, t);
-    store_w<WT>(smem + 2 * TILE_BYTES, t, wl);
-    __syncthreads();
-
-    for (int kt = 0; kt < nk; kt++) {
-        const int cur = kt & 1;
-        const bool more = kt + 1 < nk;
-        if (more) {
-            const int64_t k0 = (int64_t)(kt + 1) * BK;
-            al.load(args.A, args.lda, M, K, m0, k0, t);
-            wl.load(W, G.rows_total, K, wrow, k0, t % 2, wok);
-        }
-        mma_slab(smem + cur * TILE_BYTES, smem + (2 + cur) * TILE_BYTES, wm, wn, lane, acc);
-        if (more) {
-            al.store(smem + (cur ^ 1) * TILE_BYTES, t);
-            store_w<WT>(smem + (2 + (cur ^ 1)) * TILE_BYTES, t, wl);
-        }
+    // Two register stages. Step kk: request slab kk+2 into ring[kk&1] (its previous contents,
+    // slab kk, are already in LDS), multiply slab kk from LDS, then write slab kk+1 (requested a
+    // step earlier) into the other LDS buffer. Slab indices past the end are clamped to the last
+    // slab, so every step issues the same loads and stores with no branch around them (a load
+    // behind a branch makes the compiler wait for every outstanding load); the extra slab written
+    // on the last step lands in the buffer nobody reads again.
+    static_assert(R == 2, "two register stages");
+    Slab<WT, C::A_CHUNKS, C::B_ITEMS> ring[2];
+    const int last = kb + (nk > 0 ? nk - 1 : 0);
+    auto slab_k0 = [&](int kk) -> int64_t { return (int64_t)min(kb + kk, last) * BK; };
+    auto step = [&](int kk, Slab<WT, C::A_CHUNKS, C::B_ITEMS> & mine, Slab<WT, C::A_CHUNKS, C::B_ITEMS> & next) {
+        slab_load<WT, C>(mine, args, G, m0, n0, slab_k0(kk + 2), t);
+        mma_slab<C>(smem + (kk & 1) * C::STAGE, wm, wn, lane, acc);
+        slab_store<WT, C>(next, smem + ((kk + 1) & 1) * C::STAGE, t);
         __syncthreads();
+    };
+    if (nk > 0) {
+        slab_load<WT, C>(ring[0], args, G, m0, n0, slab_k0(0), t);
+        slab_load<WT, C>(ring[1], args, G, m0, n0, slab_k0(1), t);
+        slab_store<WT, C>(ring[0], smem, t);
+        __syncthreads();
+        int kk = 0;
+        for (; kk + 2 <= nk; kk += 2) {
+            step(kk, ring[0], ring[1]);
+            step(kk + 1, ring[1], ring[0]);
+        }
+        if (kk < nk) step(kk, ring[0], ring[1]);
     }
 
     // epilogue: C = scale[m] * acc
     const int lr = lane % 32, lg = lane / 32;
 #pragma unroll
-    for (int i = 0; i < 2; i++) {
+    for (int i = 0; i < C::MI; i++) {
 #pragma unroll
         for (int e = 0; e < 16; e++) {
-            const int r = m0 + wm * 64 + i * 32 + 8 * (e / 4) + 4 * lg + (e % 4);
-            if (r >= M) continue;
+            const int r = m0 + wm * C::TM + i * 32 + 8 * (e / 4) + 4 * lg + (e % 4);
+            if (r >= args.M) continue;
             const float s = args.scales[r];
             float * crow = G.C + (int64_t)r * G.ldc;
 #pragma unroll
-            for (int j = 0; j < 2; j++) {
-                const int n = n0 + wn * 64 + j * 32 + lr;
-                if (n < G.N) crow[n] = acc[i][j][e] * s;
+            for (int j = 0; j < C::NJ; j++) {
+                const int n = n0 + wn * C::TN + j * 32 + lr;
+                if (n < G.N) {
+                    if (KSPLIT == 1) crow[n] = acc[i][j][e] * s;
+                    else unsafeAtomicAdd(crow + n, acc[i][j][e] * s);
+                }
             }
         }
     }
+}
+
+// Zero the outputs of a split-K launch (a fill kernel rather than a memset, so the launch
+// sequence stays capturable).
+__global__ void zero_rows_kernel(GemmArgs args) {
+    const GemmGroup & G = args.g[blockIdx.y];
+    const int64_t n = (int64_t)args.M * G.N;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
+        G.C[(i / G.N) * G.ldc + i % G.N] = 0.0f;
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -253,22 +354,113 @@ __global__ void pack_q6_k_kernel(const uint8_t * __restrict__ src, int64_t rows,
 hipError_t launch_pack_act(const float * X, int64_t ldx, int M, int K, uint16_t * A16, int64_t lda,
                            float * scales, hipStream_t st) {
     if (M <= 0) return hipSuccess;
-    hipLaunchKernelGGL(pack_act_kernel, dim3((M + 3) / 4), dim3(256), 0, st, X, ldx, M, K, A16, lda, scales);
+    hipLaunchKernelGGL(pack_act_kernel, dim3(M), dim3(PACK_THREADS), 0, st, X, ldx, M, K, A16, lda, scales);
     return hipGetLastError();
 }
 
-hipError_t launch_gemm(int wt, const GemmArgs & a, int n_tiles_total, hipStream_t st) {
-    const int nblocks = n_tiles_total * a.m_tiles;
-    if (nblocks <= 0) return hipSuccess;
-    const size_t lds = 4 * TILE_BYTES;
-    switch (wt) {
-        case T_F16: hipLaunchKernelGGL(gemm_kernel<T_F16>, dim3(nblocks), dim3(GEMM_THREADS), lds, st, a); break;
-        case T_Q8_0: hipLaunchKernelGGL(gemm_kernel<T_Q8_0>, dim3(nblocks), dim3(GEMM_THREADS), lds, st, a); break;
-        case T_Q4_K: hipLaunchKernelGGL(gemm_kernel<T_Q4_K>, dim3(nblocks), dim3(GEMM_THREADS), lds, st, a); break;
-        case T_Q6_K: hipLaunchKernelGGL(gemm_kernel<T_Q6_K>, dim3(nblocks), dim3(GEMM_THREADS), lds, st, a); break;
+// Tile configurations. The launcher picks one per call from the output shape (see choose_cfg);
+// MI355X_GEMM_CFG=<id> forces one (for tuning).
+struct CfgDesc { int bm, bn, ksplit; };
+static const CfgDesc kCfgs[] = {
+    {128, 128, 1},   // 0: 4 waves of 64x64, 3-slab prefetch
+    {128, 128, 2},   // 1: same, K split in two
+    {256, 128, 1},   // 2: 4 waves of 128x64, 2-slab prefetch
+    {128, 256, 1},   // 3: 4 waves of 64x128, 2-slab prefetch
+};
+constexpr int N_CFGS = sizeof(kCfgs) / sizeof(kCfgs[0]);
+
+template <int WT, int BM, int BN, int WM, int WN, int R, int KS>
+static hipError_t launch_one(const GemmArgs & a, int nblocks, hipStream_t st) {
+    using C = GemmCfg<BM, BN, WM, WN, R>;
+    auto kern = gemm_kernel<WT, BM, BN, WM, WN, R, KS>;
+    static bool attr = false;
+    if (!attr) {
+        hipError_t e = hipFuncSetAttribute((const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize, C::LDS);
+        if (e != hipSuccess) return e;
+        attr = true;
+    }
+    hipLaunchKernelGGL(kern, dim3(nblocks), dim3(GEMM_THREADS), C::LDS, st, a);
+    return hipGetLastError();
+}
+
+template <int WT>
+static hipError_t launch_cfg(int cfg, const GemmArgs & a, int nblocks, hipStream_t st) {
+    switch (cfg) {
+        case 0: return launch_one<WT, 128, 128, 2, 2, 2, 1>(a, nblocks, st);
+        case 1: return launch_one<WT, 128, 128, 2, 2, 2, 2>(a, nblocks, st);
+        case 2: return launch_one<WT, 256, 128, 2, 2, 2, 1>(a, nblocks, st);
+        case 3: return launch_one<WT, 128, 256, 2, 2, 2, 1>(a, nblocks, st);
         default: return hipErrorInvalidValue;
     }
-    return hipGetLastError();
+}
+
+static int cu_count() {
+    static int n = 0;
+    if (n == 0) {
+        int dev = 0;
+        hipDeviceProp_t p;
+        n = (hipGetDevice(&dev) == hipSuccess && hipGetDeviceProperties(&p, dev) == hipSuccess) ? p.multiProcessorCount : 256;
+    }
+    return n;
+}
+
+static int tiles_of(const GemmArgs & a, int bm, int bn) {
+    int nt = 0;
+    for (int i = 0; i < a.ng; i++) nt += (a.g[i].N + bn - 1) / bn;
+    return nt * ((a.M + bm - 1) / bm);
+}
+
+// Pick the configuration with the best estimated throughput: the fraction of the chip the grid
+// keeps busy over its waves of blocks, times the tile's relative per-CU efficiency (bigger wave
+// tiles read LDS less per MFMA). Split-K only when the unsplit grid leaves most CUs idle.
+static int choose_cfg(const GemmArgs & a) {
+    if (const char * e = getenv("MI355X_GEMM_CFG")) {
+        if (*e) {
+            const int c = atoi(e);
+            if (c >= 0 && c < N_CFGS) return c;
+        }
+    }
+    const int cus = cu_count();
+    const double tile_eff[N_CFGS] = {1.0, 0.97, 1.25, 1.25};
+    int best = 0;
+    double best_score = -1.0;
+    for (int c = 0; c < N_CFGS; c++) {
+        if (kCfgs[c].ksplit > 1 && (a.K / BK) < 16) continue;
+        const int blocks = tiles_of(a, kCfgs[c].bm, kCfgs[c].bn) * kCfgs[c].ksplit;
+        const int waves = (blocks + cus - 1) / cus;
+        const double fill = (double)blocks / ((double)waves * cus);
+        const double score = fill * tile_eff[c];
+        if (score > best_score + 1e-9) { best_score = score; best = c; }
+    }
+    return best;
+}
+
+__global__ void zero_rows_kernel(GemmArgs args);
+
+hipError_t launch_gemm(int wt, const GemmArgs & a_in, int /*unused*/, hipStream_t st) {
+    GemmArgs a = a_in;
+    const int cfg = choose_cfg(a);
+    const CfgDesc & d = kCfgs[cfg];
+    a.m_tiles = (a.M + d.bm - 1) / d.bm;
+    int nt = 0;
+    for (int i = 0; i < a.ng; i++) {
+        a.g[i].ntile_begin = nt;
+        nt += (a.g[i].N + d.bn - 1) / d.bn;
+    }
+    const int nblocks = nt * a.m_tiles * d.ksplit;
+    if (nblocks <= 0) return hipSuccess;
+    if (d.ksplit > 1) {
+        hipLaunchKernelGGL(zero_rows_kernel, dim3(256, a.ng), dim3(256), 0, st, a);
+        hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+    }
+    switch (wt) {
+        case T_F16: return launch_cfg<T_F16>(cfg, a, nblocks, st);
+        case T_Q8_0: return launch_cfg<T_Q8_0>(cfg, a, nblocks, st);
+        case T_Q4_K: return launch_cfg<T_Q4_K>(cfg, a, nblocks, st);
+        case T_Q6_K: return launch_cfg<T_Q6_K>(cfg, a, nblocks, st);
+        default: return hipErrorInvalidValue;
+    }
 }
 
 hipError_t launch_dequant_f16(int wt, const void * W, int64_t rows, int64_t K, uint16_t * out, hipStream_t st) {

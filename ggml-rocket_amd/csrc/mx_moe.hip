@@ -114,7 +114,7 @@ __global__ void __launch_bounds__(MOE_THREADS) moe_gemm_kernel(MoeArgs a) {
     const uint8_t * W = (const uint8_t *)a.w;
     const int64_t rows_total = (int64_t)a.E * a.N;
     // weight rows: thread t stages row n0 + t (both 32-value halves of each slab)
-    const int64_t wrow = (int64_t)e * a.N + n0 + t;
+    const int64_t wrow = (int64_t)e * a.N + min(n0 + t, a.N - 1);   // clamped: loads are unconditional
     const bool wok = n0 + t < a.N;
     // A: thread t stages row t / 8, chunk t % 8
     const int ar = t / 8, ac = t % 8;

@@ -16,6 +16,11 @@
 // uses at ggml-rocket.cpp:3894-3906): Q8_0 y = d*q; Q4_K y = (d*sc)*q - dmin*m; Q6_K
 // y = (d*sc)*(q-32). Each product and difference is rounded on its own, then the f32 result is
 // rounded once to fp16 (ggml_fp32_to_fp16_row, 3907).
+//
+// Every loader issues its loads unconditionally from an address inside the panel (the caller
+// passes a valid row; a K position past the end reads position 0 instead) and remembers whether
+// the item is real. The zeroing of an unreal item happens in decode(), when the data is used, so
+// a pipeline can keep all of a stage's loads in flight until then.
 #pragma once
 
 #include "mx_common.h"
@@ -48,24 +53,33 @@ __device__ __forceinline__ void q4k_sm(int j, uint32_t s0, uint32_t s1, uint32_t
     }
 }
 
+__device__ __forceinline__ void zero_out(bool ok, u32x4 out[4]) {
+    if (!ok) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) out[i] = u32x4{0, 0, 0, 0};
+    }
+}
+
 // Global-load stage of one thread's share of a BK=64 weight tile: 32 consecutive-in-format
 // values of one row. `u` (0/1) selects which half of the row's 64 values the thread takes.
+// decode() produces them as fp16 in two runs of 16, at K offsets run0 and run1 of the slab.
 template <int WT> struct WLoad;
 
 template <> struct WLoad<T_F16> {
     u32x4 v[4];   // 32 fp16 values, k = k0 + 32u + 0..31
+    bool ok;
     __device__ __forceinline__ void load(const uint8_t * W, int64_t rows, int64_t K, int64_t row,
-                                         int64_t k0, int u, bool ok) {
+                                         int64_t k0, int u, bool ok_row) {
         const int64_t k = k0 + 32 * u;
-        ok = ok && k < K;
-        const u32x4 * p = (const u32x4 *)(W + (row * K + k) * 2);
+        ok = ok_row && k < K;
+        const u32x4 * p = (const u32x4 *)(W + (row * K + (k < K ? k : 0)) * 2);
 #pragma unroll
-        for (int i = 0; i < 4; i++) v[i] = ok ? p[i] : u32x4{0, 0, 0, 0};
+        for (int i = 0; i < 4; i++) v[i] = p[i];
     }
-    // Writes the two 16-value runs: run0 at k_local = 32u, run1 at 32u + 16.
     __device__ __forceinline__ void decode(int u, u32x4 out[4], int & run0, int & run1) const {
 #pragma unroll
         for (int i = 0; i < 4; i++) out[i] = v[i];
+        zero_out(ok, out);
         run0 = 32 * u;
         run1 = 32 * u + 16;
     }
@@ -74,15 +88,17 @@ template <> struct WLoad<T_F16> {
 template <> struct WLoad<T_Q8_0> {
     u32x4 q[2];
     uint16_t d;
+    bool ok;
     __device__ __forceinline__ void load(const uint8_t * W, int64_t rows, int64_t K, int64_t row,
-                                         int64_t k0, int u, bool ok) {
-        const int64_t k = k0 + 32 * u;   // one 32-value block
-        ok = ok && k < K;
+                                         int64_t k0, int u, bool ok_row) {
+        int64_t k = k0 + 32 * u;   // one 32-value block
+        ok = ok_row && k < K;
+        k = k < K ? k : 0;
         const u32x4 * p = (const u32x4 *)(W + row * K + k);
         const uint16_t * dp = (const uint16_t *)(W + rows * K) + row * (K / 32) + k / 32;
-        q[0] = ok ? p[0] : u32x4{0, 0, 0, 0};
-        q[1] = ok ? p[1] : u32x4{0, 0, 0, 0};
-        d = ok ? *dp : (uint16_t)0;
+        q[0] = p[0];
+        q[1] = p[1];
+        d = *dp;
     }
     __device__ __forceinline__ void decode(int u, u32x4 out[4], int & run0, int & run1) const {
         const float df = h2f_bits(d);
@@ -98,6 +114,7 @@ template <> struct WLoad<T_Q8_0> {
         }
 #pragma unroll
         for (int i = 0; i < 4; i++) out[i] = u32x4{o[4 * i], o[4 * i + 1], o[4 * i + 2], o[4 * i + 3]};
+        zero_out(ok, out);
         run0 = 32 * u;
         run1 = 32 * u + 16;
     }
@@ -107,13 +124,15 @@ template <> struct WLoad<T_Q4_K> {
     u32x4 hdr;   // d, dmin, scales[12]
     u32x4 qs;    // 16 bytes of nibbles
     int j;       // quarter of the block (0..3)
+    bool ok;
     __device__ __forceinline__ void load(const uint8_t * W, int64_t rows, int64_t K, int64_t row,
-                                         int64_t k0, int u, bool ok) {
+                                         int64_t k0, int u, bool ok_row) {
         const int64_t blk = k0 / 256;
         j = (int)((k0 % 256) / 64);
+        ok = ok_row;
         const uint8_t * b = W + (row * (K / 256) + blk) * 144;
-        hdr = ok ? *(const u32x4 *)b : u32x4{0, 0, 0, 0};
-        qs = ok ? *(const u32x4 *)(b + 16 + 32 * j + 16 * u) : u32x4{0, 0, 0, 0};
+        hdr = *(const u32x4 *)b;
+        qs = *(const u32x4 *)(b + 16 + 32 * j + 16 * u);
     }
     // Byte b of qs (b = 0..15) is q[32j + 16u + b]: its low nibble is weight 64j + 16u + b
     // (sub-block 2j), its high nibble weight 64j + 32 + 16u + b (sub-block 2j+1).
@@ -142,6 +161,7 @@ template <> struct WLoad<T_Q4_K> {
         out[1] = u32x4{lo[4], lo[5], lo[6], lo[7]};
         out[2] = u32x4{hi[0], hi[1], hi[2], hi[3]};
         out[3] = u32x4{hi[4], hi[5], hi[6], hi[7]};
+        zero_out(ok, out);
         run0 = 16 * u;
         run1 = 32 + 16 * u;
     }
@@ -152,24 +172,26 @@ template <> struct WLoad<T_Q6_K> {
     uint32_t sc;          // the 4 int8 scales it needs, packed
     uint16_t d;
     int hi;               // 0: weights l, l+32 of the half; 1: l+64, l+96
+    bool ok;
     __device__ __forceinline__ void load(const uint8_t * W, int64_t rows, int64_t K, int64_t row,
-                                         int64_t k0, int u, bool ok) {
+                                         int64_t k0, int u, bool ok_row) {
         const int64_t blk = k0 / 256;
         const int q4 = (int)((k0 % 256) / 64);
         const int h = q4 >> 1;
         hi = q4 & 1;
+        ok = ok_row;
         const int l0 = 16 * u;
         const uint8_t * ql = W + row * (K / 2) + blk * 128 + 64 * h + l0;
         const uint8_t * qhp = W + rows * (K / 2) + row * (K / 4) + blk * 64 + 32 * h + l0;
         const int8_t * scp = (const int8_t *)(W + rows * (K / 2) + rows * (K / 4)) + row * (K / 16) + blk * 16 + 8 * h;
         const uint16_t * dp = (const uint16_t *)(W + rows * (K / 2) + rows * (K / 4) + rows * (K / 16)) + row * (K / 256) + blk;
-        qla = ok ? *(const u32x4 *)ql : u32x4{0, 0, 0, 0};
-        qlb = ok ? *(const u32x4 *)(ql + 32) : u32x4{0, 0, 0, 0};
-        qh = ok ? *(const u32x4 *)qhp : u32x4{0, 0, 0, 0};
+        qla = *(const u32x4 *)ql;
+        qlb = *(const u32x4 *)(ql + 32);
+        qh = *(const u32x4 *)qhp;
         // scales for sub-blocks (l/16) + {0,2} (hi=0) or + {4,6} (hi=1), l/16 = u
         const int i0 = u + 4 * hi;
-        sc = ok ? ((uint32_t)(uint8_t)scp[i0] | ((uint32_t)(uint8_t)scp[i0 + 2] << 8)) : 0u;
-        d = ok ? *dp : (uint16_t)0;
+        sc = (uint32_t)(uint8_t)scp[i0] | ((uint32_t)(uint8_t)scp[i0 + 2] << 8);
+        d = *dp;
     }
     __device__ __forceinline__ void decode(int u, u32x4 out[4], int & run0, int & run1) const {
         const float df = h2f_bits(d);
@@ -202,6 +224,7 @@ template <> struct WLoad<T_Q6_K> {
         out[1] = u32x4{a[4], a[5], a[6], a[7]};
         out[2] = u32x4{b[0], b[1], b[2], b[3]};
         out[3] = u32x4{b[4], b[5], b[6], b[7]};
+        zero_out(ok, out);
         run0 = 16 * u;
         run1 = 32 + 16 * u;
     }
