@@ -1,0 +1,637 @@
+// SPDX-License-Identifier: MIT
+// The backend instance: the device and its stream, the HBM weight cache, the graph_compute
+// node loop and its three op handlers, the per-route circuit breaker, the CPU fallback and the
+// counters. The reference's equivalents: context 322-692, graph_compute 7050-7200, MUL_MAT
+// 4548-4871 (+ fused groups 4873-5160), FLASH_ATTN_EXT 5444-5691, MUL_MAT_ID 6651-6944, free
+// 5172-5326, breaker 263-307 (all ggml-rocket.cpp).
+//
+// Data flow (the host-buffer contract, ggml-rocket.cpp:7326-7331): tensors live in host memory;
+// each claimed op uploads its activations, runs on the device and writes dst back before
+// graph_compute returns. Weights are uploaded once into the HBM weight cache, keyed by
+// weight_key (name + content fingerprint), in the layout the kernels read:
+//   F16 / Q4_K   the ggml payload as-is;   Q8_0 / Q6_K   split into aligned planes;
+//   F32 / BF16   converted to fp16;        QUANT_RESIDENT=1   quant weights decoded to fp16.
+
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <map>
+#include <mutex>
+#include <string>
+#include <unordered_map>
+#include <unordered_set>
+#include <vector>
+
+#include <hip/hip_runtime.h>
+
+#include "../../../include/mi355x_kernels.h"
+#include "host.h"
+
+using namespace mxh;
+
+namespace {
+
+// ---- circuit breaker (ggml-rocket.cpp:263-307) ----------------------------------------------
+// Three consecutive device failures open a route: its fallback runs directly for 64 calls, then
+// one call probes the device again; a failed probe doubles the interval, up to 4096 calls; a
+// success closes it. Structural declines (MI355X_E_ARG / _UNSUPPORTED) do not count.
+struct Breaker {
+    int fails = 0;
+    long skip = 0;
+    long open_len = 0;
+    long attempts = 0, failures = 0, bypassed = 0;
+    int inject = 0;   // host-side fault injection for tests
+};
+
+bool breaker_allow(Breaker & b) {
+    if (b.skip > 0) {
+        b.skip--;
+        b.bypassed++;
+        return false;
+    }
+    return true;
+}
+
+bool device_failure(int rc) {
+    return rc != MI355X_OK && rc != MI355X_E_ARG && rc != MI355X_E_UNSUPPORTED;
+}
+
+void breaker_note(Breaker & b, int rc, const char * route) {
+    if (!device_failure(rc)) {
+        if (rc == MI355X_OK) {
+            b.fails = 0;
+            b.open_len = 0;
+        }
+        return;
+    }
+    b.failures++;
+    if (++b.fails < 3) return;
+    const long OPEN0 = 64, OPEN_MAX = 4096;
+    b.open_len = b.open_len ? (b.open_len * 2 > OPEN_MAX ? OPEN_MAX : b.open_len * 2) : OPEN0;
+    b.skip = b.open_len;
+    logw("%s: %d consecutive device failures (last status %d): its CPU fallback runs directly for "
+         "the next %ld calls, then the route is retried once\n", route, b.fails, rc, b.skip);
+}
+
+// A grow-only device buffer.
+struct DevBuf {
+    void * p = nullptr;
+    size_t cap = 0;
+    int ensure(size_t n) {
+        if (n <= cap) return MI355X_OK;
+        if (p) {
+            (void)hipDeviceSynchronize();   // queued work may still read the old buffer
+            (void)hipFree(p);
+        }
+        p = nullptr;
+        cap = 0;
+        const size_t want = (n + ((size_t)1 << 20) - 1) & ~(((size_t)1 << 20) - 1);
+        if (hipMalloc(&p, want) != hipSuccess) {
+            (void)hipGetLastError();
+            p = nullptr;
+            return MI355X_E_DEVICE;
+        }
+        cap = want;
+        return MI355X_OK;
+    }
+    void release() {
+        if (p) (void)hipFree(p);
+        p = nullptr;
+        cap = 0;
+    }
+};
+
+struct WEntry {
+    void * dev = nullptr;
+    size_t bytes = 0;
+    int dev_type = 0;   // layout the kernels read: F16, Q8_0, Q4_K or Q6_K
+    int64_t rows = 0, K = 0;
+};
+
+const uint64_t GUID[2] = {0x4d49333535584d49ULL, 0x2d70726566696c6cULL};
+
+}  // namespace
+
+struct ggml_backend_mi355x {
+    uint64_t guid[2] = {GUID[0], GUID[1]};
+    int n_threads = 5;
+    bool started = false;
+    int quant_resident = -1;   // -1: the QUANT_RESIDENT knob; 0 / 1: this instance's choice
+
+    bool dev_checked = false, dev_ok = false;
+    hipStream_t stream = nullptr;
+
+    DevBuf act, a16, scales, out, wstage, wconv, fa_q, fa_k, fa_v, fa_m, fa_o, fa_ws, moe_b, moe_ids, moe_o, moe_ws;
+    DevBuf wscratch[4], moe_wscratch;   // per-call weights: unnamed, or over the cache budget
+
+    std::unordered_map<std::string, WEntry> wcache;
+    size_t cache_used = 0, cache_budget = 0;
+
+    std::map<std::string, long> routes;
+    long n_cpu_fallbacks = 0;
+    long moe_resident = 0, moe_streamed = 0;
+    std::unordered_set<std::string> moe_claimed;
+    std::unordered_set<std::string> moe_counted;   // stacks whose experts were counted resident
+
+    Breaker brk_gemm, brk_fa, brk_moe;
+};
+
+namespace {
+
+using Ctx = ggml_backend_mi355x;
+
+bool ensure_device(Ctx * c) {
+    if (c->dev_checked) return c->dev_ok;
+    c->dev_checked = true;
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess || n <= 0) {
+        (void)hipGetLastError();
+        logw("no HIP device: every claimed op will run on the CPU fallback\n");
+        return false;
+    }
+    if (hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking) != hipSuccess) {
+        (void)hipGetLastError();
+        c->stream = nullptr;
+        return false;
+    }
+    size_t fr = 0, tot = 0;
+    (void)hipMemGetInfo(&fr, &tot);
+    size_t b = 0;
+    const char * e = knob_env("CACHE_MB");
+    if (e && parse_mb(e, &b)) c->cache_budget = b ? b : (size_t)-1;
+    else c->cache_budget = fr > ((size_t)16 << 30) ? fr - ((size_t)16 << 30) : fr / 2;
+    c->dev_ok = true;
+    return true;
+}
+
+int sync(Ctx * c) {
+    return hipStreamSynchronize(c->stream) == hipSuccess ? MI355X_OK : MI355X_E_DEVICE;
+}
+
+int h2d(Ctx * c, void * dst, const void * src, size_t n) {
+    if (!n) return MI355X_OK;
+    return hipMemcpyAsync(dst, src, n, hipMemcpyHostToDevice, c->stream) == hipSuccess ? MI355X_OK : MI355X_E_DEVICE;
+}
+
+int d2h(Ctx * c, void * dst, const void * src, size_t n) {
+    if (!n) return MI355X_OK;
+    return hipMemcpyAsync(dst, src, n, hipMemcpyDeviceToHost, c->stream) == hipSuccess ? MI355X_OK : MI355X_E_DEVICE;
+}
+
+#define TRY(x) do { const int _rc = (x); if (_rc != MI355X_OK) return _rc; } while (0)
+
+// The device layout a weight of ggml type `t` is read in (F32/BF16 become fp16; fp16 when the
+// resident-fp16 form is asked for).
+int dev_layout(int t, bool want_f16) {
+    if (want_f16 || t == MI355X_TYPE_F16 || t == MI355X_TYPE_F32 || t == MI355X_TYPE_BF16) return MI355X_F16;
+    return t;   // Q8_0, Q4_K, Q6_K
+}
+
+// Builds the device form of `rows` rows of K values of ggml type `t` (host bytes `src`) at
+// `dst` (capacity `dst_bytes`). Uses wstage / wconv as staging.
+int build_weight(Ctx * c, int t, const void * src, int64_t rows, int64_t K, bool want_f16, void * dst) {
+    const size_t raw = (size_t)row_bytes(t, K) * (size_t)rows;
+    const int lay = dev_layout(t, want_f16);
+    if ((t == MI355X_TYPE_F16 || t == MI355X_TYPE_Q4_K) && lay == t) return h2d(c, dst, src, raw);
+    TRY(c->wstage.ensure(raw));
+    TRY(h2d(c, c->wstage.p, src, raw));
+    if (t == MI355X_TYPE_F32 || t == MI355X_TYPE_BF16)
+        return mi355x_convert_f16(t, c->wstage.p, rows * K, (uint16_t *)dst, c->stream);
+    if (lay != MI355X_F16) return mi355x_weight_pack(t, c->wstage.p, rows, K, dst, c->stream);
+    // quantized -> resident fp16: into the HBM layout first when that differs from the ggml one
+    const void * q = c->wstage.p;
+    if (t == MI355X_TYPE_Q8_0 || t == MI355X_TYPE_Q6_K) {
+        TRY(c->wconv.ensure(raw));
+        TRY(mi355x_weight_pack(t, c->wstage.p, rows, K, c->wconv.p, c->stream));
+        q = c->wconv.p;
+    }
+    return mi355x_weight_dequant_f16(t, q, rows, K, (uint16_t *)dst, c->stream);
+}
+
+// A weight in device form: from the cache, or built into it, or (no key / over budget) built
+// into per-call scratch. `resident` tells which.
+int get_weight(Ctx * c, const mi355x_tensor * a, int64_t rows, int64_t K, bool want_f16, DevBuf & scratch,
+               WEntry & out, bool & resident) {
+    const int lay = dev_layout(a->type, want_f16);
+    const int64_t dbytes = mi355x_weight_bytes(lay, rows, K);
+    if (dbytes < 0) return MI355X_E_ARG;
+    std::string key = weight_key(a);
+    if (!key.empty()) {
+        key += want_f16 ? "|f16" : "|dev";
+        auto it = c->wcache.find(key);
+        if (it != c->wcache.end() && it->second.rows == rows && it->second.K == K && it->second.dev_type == lay) {
+            out = it->second;
+            resident = true;
+            return MI355X_OK;
+        }
+        if (c->cache_used + (size_t)dbytes <= c->cache_budget) {
+            void * p = nullptr;
+            if (hipMalloc(&p, (size_t)dbytes) == hipSuccess) {
+                const int rc = build_weight(c, a->type, a->data, rows, K, want_f16, p);
+                if (rc != MI355X_OK) {
+                    (void)hipFree(p);
+                    return rc;
+                }
+                WEntry e;
+                e.dev = p;
+                e.bytes = (size_t)dbytes;
+                e.dev_type = lay;
+                e.rows = rows;
+                e.K = K;
+                c->wcache[key] = e;
+                c->cache_used += e.bytes;
+                out = e;
+                resident = true;
+                return MI355X_OK;
+            }
+            (void)hipGetLastError();
+        }
+    }
+    TRY(scratch.ensure((size_t)dbytes));
+    TRY(build_weight(c, a->type, a->data, rows, K, want_f16, scratch.p));
+    out.dev = scratch.p;
+    out.bytes = (size_t)dbytes;
+    out.dev_type = lay;
+    out.rows = rows;
+    out.K = K;
+    resident = false;
+    return MI355X_OK;
+}
+
+// ---- MUL_MAT (one node or a fused group sharing src1) ---------------------------------------
+int mul_mat_device(Ctx * c, const std::vector<mi355x_tensor *> & grp, bool want_f16, bool & all_resident) {
+    if (!ensure_device(c)) return MI355X_E_DEVICE;
+    const mi355x_tensor * b = grp[0]->src[1];
+    const int64_t K = b->ne[0], M = b->ne[1] * b->ne[2] * b->ne[3];
+    TRY(c->act.ensure((size_t)M * K * 4));
+    TRY(c->a16.ensure((size_t)M * K * 2));
+    TRY(c->scales.ensure((size_t)M * 4));
+    int64_t ntot = 0;
+    for (auto * d : grp) ntot += d->src[0]->ne[1];
+    TRY(c->out.ensure((size_t)M * ntot * 4));
+    TRY(h2d(c, c->act.p, b->data, (size_t)M * K * 4));
+    TRY(mi355x_pack_act((const float *)c->act.p, K, M, K, (uint16_t *)c->a16.p, (float *)c->scales.p, c->stream));
+    std::vector<WEntry> ws(grp.size());
+    all_resident = true;
+    mi355x_gemm_out outs[4];
+    int64_t col = 0;
+    for (size_t i = 0; i < grp.size(); i++) {
+        const mi355x_tensor * a = grp[i]->src[0];
+        bool res = false;
+        TRY(get_weight(c, a, a->ne[1], K, want_f16, c->wscratch[i], ws[i], res));
+        all_resident = all_resident && res;
+        outs[i].w_dev = ws[i].dev;
+        outs[i].rows_total = a->ne[1];
+        outs[i].row0 = 0;
+        outs[i].N = a->ne[1];
+        outs[i].c_dev = (float *)c->out.p + col;
+        outs[i].ldc = ntot;
+        col += a->ne[1];
+    }
+    TRY(mi355x_gemm(ws[0].dev_type, (const uint16_t *)c->a16.p, (const float *)c->scales.p, M, K, outs, (int)grp.size(),
+                    c->stream));
+    // dst[i] is [N_i, M] contiguous: copy its column block row by row
+    col = 0;
+    for (auto * d : grp) {
+        const int64_t N = d->src[0]->ne[1];
+        if (grp.size() == 1) {
+            TRY(d2h(c, d->data, c->out.p, (size_t)M * N * 4));
+        } else if (hipMemcpy2DAsync(d->data, (size_t)N * 4, (const float *)c->out.p + col, (size_t)ntot * 4,
+                                    (size_t)N * 4, (size_t)M, hipMemcpyDeviceToHost, c->stream) != hipSuccess) {
+            return MI355X_E_DEVICE;
+        }
+        col += N;
+    }
+    return sync(c);
+}
+
+// ---- FLASH_ATTN_EXT ---------------------------------------------------------------------------
+int flash_attn_device(Ctx * c, mi355x_tensor * dst) {
+    if (!ensure_device(c)) return MI355X_E_DEVICE;
+    const mi355x_tensor * q = dst->src[0];
+    const mi355x_tensor * k = dst->src[1];
+    const mi355x_tensor * v = dst->src[2];
+    const mi355x_tensor * m = dst->src[3];
+    const size_t qb = nbytes(q), kb = nbytes(k), vb = nbytes(v), mb = m ? nbytes(m) : 0, ob = nbytes(dst);
+    TRY(c->fa_q.ensure(qb));
+    TRY(c->fa_k.ensure(kb));
+    TRY(c->fa_v.ensure(vb));
+    if (m) TRY(c->fa_m.ensure(mb));
+    TRY(c->fa_o.ensure(ob));
+    TRY(h2d(c, c->fa_q.p, q->data, qb));
+    TRY(h2d(c, c->fa_k.p, k->data, kb));
+    TRY(h2d(c, c->fa_v.p, v->data, vb));
+    if (m) TRY(h2d(c, c->fa_m.p, m->data, mb));
+    mi355x_fa_args a;
+    memset(&a, 0, sizeof a);
+    a.q_dev = (const float *)c->fa_q.p;
+    a.q_nb1 = (int64_t)(q->nb[1] / 4);
+    a.q_nb2 = (int64_t)(q->nb[2] / 4);
+    a.k_dev = (const uint16_t *)c->fa_k.p;
+    a.k_nb1 = (int64_t)(k->nb[1] / 2);
+    a.k_nb2 = (int64_t)(k->nb[2] / 2);
+    a.v_dev = (const uint16_t *)c->fa_v.p;
+    a.v_nb1 = (int64_t)(v->nb[1] / 2);
+    a.v_nb2 = (int64_t)(v->nb[2] / 2);
+    a.mask_dev = m ? (const uint16_t *)c->fa_m.p : nullptr;
+    a.mask_nb1 = m ? (int64_t)(m->nb[1] / 2) : 0;
+    a.dst_dev = (float *)c->fa_o.p;
+    a.dst_nb1 = (int64_t)(dst->nb[1] / 4);
+    a.dst_nb2 = (int64_t)(dst->nb[2] / 4);
+    a.D = (int)q->ne[0];
+    a.DV = (int)v->ne[0];
+    a.T = (int)q->ne[1];
+    a.H = (int)q->ne[2];
+    a.KV = (int)k->ne[1];
+    a.HK = (int)k->ne[2];
+    memcpy(&a.scale, &dst->op_params[0], 4);
+    memcpy(&a.max_bias, &dst->op_params[1], 4);
+    memcpy(&a.softcap, &dst->op_params[2], 4);
+    const size_t ws = mi355x_flash_attn_workspace(&a, 0);
+    if (ws) TRY(c->fa_ws.ensure(ws));
+    TRY(mi355x_flash_attn(&a, 0, ws ? c->fa_ws.p : nullptr, ws, c->stream));
+    TRY(d2h(c, dst->data, c->fa_o.p, ob));
+    return sync(c);
+}
+
+// ---- MUL_MAT_ID -------------------------------------------------------------------------------
+int mul_mat_id_device(Ctx * c, mi355x_tensor * dst, bool & resident) {
+    if (!ensure_device(c)) return MI355X_E_DEVICE;
+    const mi355x_tensor * as = dst->src[0];
+    const mi355x_tensor * b = dst->src[1];
+    const mi355x_tensor * ids = dst->src[2];
+    const int64_t K = as->ne[0], N = as->ne[1], E = as->ne[2];
+    const int64_t ne11 = b->ne[1], T = ids->ne[1], U = ids->ne[0];
+    // the whole stack is one weight panel of E*N rows
+    mi355x_tensor panel = *as;
+    panel.ne[1] = N * E;
+    panel.ne[2] = 1;
+    WEntry w;
+    TRY(get_weight(c, &panel, N * E, K, false, c->moe_wscratch, w, resident));
+    const size_t bb = (size_t)T * ne11 * K * 4, ib = (size_t)T * U * 4, ob = (size_t)T * U * N * 4;
+    TRY(c->moe_b.ensure(bb));
+    TRY(c->moe_ids.ensure(ib));
+    TRY(c->moe_o.ensure(ob));
+    TRY(h2d(c, c->moe_b.p, b->data, bb));
+    // ids may be a strided view: pack it to [T][U] on the host side of the copy
+    std::vector<int32_t> idh((size_t)T * U);
+    for (int64_t t = 0; t < T; t++)
+        for (int64_t s = 0; s < U; s++)
+            idh[t * U + s] = *(const int32_t *)((const char *)ids->data + t * ids->nb[1] + s * ids->nb[0]);
+    TRY(h2d(c, c->moe_ids.p, idh.data(), ib));
+    mi355x_moe_args a;
+    memset(&a, 0, sizeof a);
+    a.wtype = w.dev_type;
+    a.as_dev = w.dev;
+    a.n_expert = E;
+    a.N = N;
+    a.K = K;
+    a.b_dev = (const float *)c->moe_b.p;
+    a.ne11 = ne11;
+    a.b_nb1 = K;
+    a.b_nb2 = ne11 * K;
+    a.ids_dev = (const int32_t *)c->moe_ids.p;
+    a.n_used = U;
+    a.ids_nb0 = 1;
+    a.ids_nb1 = U;
+    a.n_tokens = T;
+    a.dst_dev = (float *)c->moe_o.p;
+    a.dst_nb1 = N;
+    a.dst_nb2 = U * N;
+    const size_t ws = mi355x_mul_mat_id_workspace(&a);
+    TRY(c->moe_ws.ensure(ws));
+    TRY(mi355x_mul_mat_id(&a, c->moe_ws.p, ws, nullptr, c->stream));
+    TRY(d2h(c, dst->data, c->moe_o.p, ob));
+    return sync(c);
+}
+
+// Runs a device job under a breaker; on a device failure (or an open breaker) runs `fallback`.
+template <class Dev, class Fb>
+void guarded(Ctx * c, Breaker & brk, const char * route, Dev && dev, Fb && fallback) {
+    int rc = MI355X_E_DEVICE;
+    if (breaker_allow(brk)) {
+        brk.attempts++;
+        if (brk.inject > 0) {
+            brk.inject--;
+            rc = MI355X_E_DEVICE;
+        } else {
+            rc = dev();
+        }
+        breaker_note(brk, rc, route);
+    }
+    if (rc != MI355X_OK) {
+        fallback();
+        c->n_cpu_fallbacks++;
+    }
+}
+
+bool is_view_op(int op) {
+    return op == MI355X_OP_NONE || op == MI355X_OP_RESHAPE || op == MI355X_OP_VIEW ||
+           op == MI355X_OP_PERMUTE || op == MI355X_OP_TRANSPOSE;
+}
+
+bool fusable(const mi355x_tensor * n) {
+    return n->op == MI355X_OP_MUL_MAT && n->src[0] && n->src[1] && n->src[0]->ne[2] == 1 && n->src[0]->ne[3] == 1;
+}
+
+}  // namespace
+
+extern "C" {
+
+MI355X_API const char * ggml_backend_mi355x_name(void) { return "MI355X"; }
+
+MI355X_API const char * ggml_backend_mi355x_description(void) {
+    static char desc[160];
+    static std::once_flag once;
+    std::call_once(once, [] {
+        int n = 0, dev = 0, rt = 0;
+        hipDeviceProp_t p;
+        if (hipGetDeviceCount(&n) == hipSuccess && n > 0 && hipGetDevice(&dev) == hipSuccess &&
+            hipGetDeviceProperties(&p, dev) == hipSuccess) {
+            (void)hipRuntimeGetVersion(&rt);
+            snprintf(desc, sizeof desc, "%s (%d CUs, HIP runtime %d)", p.gcnArchName, p.multiProcessorCount, rt);
+        } else {
+            (void)hipGetLastError();
+            snprintf(desc, sizeof desc, "MI355X backend (no HIP device visible)");
+        }
+    });
+    return desc;
+}
+
+MI355X_API void ggml_backend_mi355x_get_memory(size_t * fr, size_t * tot) {
+    size_t f = 0, t = 0;
+    int n = 0;
+    if (!(hipGetDeviceCount(&n) == hipSuccess && n > 0 && hipMemGetInfo(&f, &t) == hipSuccess)) {
+        (void)hipGetLastError();
+        f = t = 0;
+    }
+    if (fr) *fr = f;
+    if (tot) *tot = t;
+}
+
+MI355X_API ggml_backend_mi355x_t ggml_backend_mi355x_init(void) {
+    Ctx * c = new Ctx();
+    int nt = knob_int("N_THREADS", 5);
+    c->n_threads = nt < 1 ? 1 : (nt > 8 ? 8 : nt);
+    moe_preflight_open();
+    return c;
+}
+
+MI355X_API bool ggml_backend_is_mi355x(ggml_backend_mi355x_t c) {
+    return c && c->guid[0] == GUID[0] && c->guid[1] == GUID[1];
+}
+
+MI355X_API void ggml_backend_mi355x_free(ggml_backend_mi355x_t c) {
+    if (!c) return;
+    if (c->stream) (void)hipStreamSynchronize(c->stream);
+    for (auto & kv : c->wcache) (void)hipFree(kv.second.dev);
+    if (!c->wcache.empty())
+        logi("[weights] %zu weights resident, %.1f MB of HBM\n", c->wcache.size(), (double)c->cache_used / (1 << 20));
+    c->wcache.clear();
+    for (DevBuf * b : {&c->act, &c->a16, &c->scales, &c->out, &c->wstage, &c->wconv, &c->fa_q, &c->fa_k, &c->fa_v,
+                       &c->fa_m, &c->fa_o, &c->fa_ws, &c->moe_b, &c->moe_ids, &c->moe_o, &c->moe_ws,
+                       &c->wscratch[0], &c->wscratch[1], &c->wscratch[2], &c->wscratch[3], &c->moe_wscratch})
+        b->release();
+    if (c->stream) (void)hipStreamDestroy(c->stream);
+    for (const auto & k : c->moe_claimed) moe_preflight_release(k);
+    moe_preflight_close();
+    c->guid[0] = c->guid[1] = 0;
+    delete c;
+}
+
+MI355X_API void ggml_backend_mi355x_set_n_threads(ggml_backend_mi355x_t c, int n) {
+    if (!ggml_backend_is_mi355x(c)) return;
+    if (c->started) {
+        logw("set_n_threads(%d) after the first compute changes nothing\n", n);
+        return;
+    }
+    if (n < 1 || n > 8) logw("set_n_threads(%d) clamped to 1..8\n", n);
+    c->n_threads = n < 1 ? 1 : (n > 8 ? 8 : n);
+}
+
+MI355X_API void ggml_backend_mi355x_set_quant_resident(ggml_backend_mi355x_t c, int mode) {
+    if (ggml_backend_is_mi355x(c)) c->quant_resident = mode < 0 ? -1 : (mode > 0 ? 1 : 0);
+}
+
+MI355X_API int ggml_backend_mi355x_get_n_threads(ggml_backend_mi355x_t c) {
+    return ggml_backend_is_mi355x(c) ? c->n_threads : 0;
+}
+
+MI355X_API long ggml_backend_mi355x_route_ops(ggml_backend_mi355x_t c, const char * route) {
+    if (!ggml_backend_is_mi355x(c)) return 0;
+    if (!route) {
+        long s = 0;
+        for (const auto & kv : c->routes) s += kv.second;
+        return s;
+    }
+    auto it = c->routes.find(route);
+    return it == c->routes.end() ? 0 : it->second;
+}
+
+MI355X_API long ggml_backend_mi355x_cpu_fallbacks(ggml_backend_mi355x_t c) {
+    return ggml_backend_is_mi355x(c) ? c->n_cpu_fallbacks : 0;
+}
+
+MI355X_API void ggml_backend_mi355x_moe_stats(ggml_backend_mi355x_t c, long * n_resident, long * n_streamed) {
+    if (n_resident) *n_resident = ggml_backend_is_mi355x(c) ? c->moe_resident : 0;
+    if (n_streamed) *n_streamed = ggml_backend_is_mi355x(c) ? c->moe_streamed : 0;
+}
+
+static Breaker * breaker_of(ggml_backend_mi355x_t c, const char * g) {
+    if (!ggml_backend_is_mi355x(c) || !g) return nullptr;
+    if (!strcmp(g, "gemm")) return &c->brk_gemm;
+    if (!strcmp(g, "fa")) return &c->brk_fa;
+    if (!strcmp(g, "moe")) return &c->brk_moe;
+    return nullptr;
+}
+
+MI355X_API void ggml_backend_mi355x_route_stats(ggml_backend_mi355x_t c, const char * g, long * attempts,
+                                                long * failures, long * bypassed) {
+    Breaker * b = breaker_of(c, g);
+    if (attempts) *attempts = b ? b->attempts : 0;
+    if (failures) *failures = b ? b->failures : 0;
+    if (bypassed) *bypassed = b ? b->bypassed : 0;
+}
+
+MI355X_API void ggml_backend_mi355x_inject_faults(ggml_backend_mi355x_t c, const char * g, int n) {
+    Breaker * b = breaker_of(c, g);
+    if (b) b->inject = n < 0 ? 0 : n;
+}
+
+MI355X_API int ggml_backend_mi355x_graph_compute(ggml_backend_mi355x_t c, mi355x_tensor * const * nodes, int n_nodes) {
+    if (!ggml_backend_is_mi355x(c) || (n_nodes > 0 && !nodes)) return MI355X_STATUS_FAILED;
+    c->started = true;
+    std::vector<bool> done((size_t)(n_nodes > 0 ? n_nodes : 0), false);
+    for (int i = 0; i < n_nodes; i++) {
+        if (done[i]) continue;
+        mi355x_tensor * node = nodes[i];
+        if (!node) continue;
+        if (is_view_op(node->op)) continue;
+        switch (node->op) {
+            case MI355X_OP_MUL_MAT: {
+                std::vector<mi355x_tensor *> grp{node};
+                if (fusion_on() && fusable(node)) {
+                    for (int j = i + 1; j < n_nodes && grp.size() < 4; j++) {
+                        mi355x_tensor * o = nodes[j];
+                        if (!o || done[j] || !fusable(o)) continue;
+                        if (o->src[1] == node->src[1] && o->src[0]->type == node->src[0]->type &&
+                            o->src[0]->ne[0] == node->src[0]->ne[0]) {
+                            grp.push_back(o);
+                            done[j] = true;
+                        }
+                    }
+                }
+                const bool quant = type_is_quantized(node->src[0]->type);
+                const bool qres = c->quant_resident < 0 ? quant_resident_on() : c->quant_resident > 0;
+                const bool want_f16 = quant && qres;
+                bool resident = false;
+                guarded(c, c->brk_gemm, "MUL_MAT",
+                        [&] { return mul_mat_device(c, grp, want_f16, resident); },
+                        [&] { for (auto * d : grp) cpu_mul_mat(d); });
+                const char * label;
+                if (grp.size() > 1) label = (resident && (!quant || want_f16)) ? "fused-resident" : "fused";
+                else if (!resident) label = "mt";
+                else label = quant ? (want_f16 ? "prepacked-q" : "mt") : "prepacked";
+                c->routes[label] += (long)grp.size();
+                break;
+            }
+            case MI355X_OP_FLASH_ATTN_EXT: {
+                guarded(c, c->brk_fa, "FLASH_ATTN_EXT", [&] { return flash_attn_device(c, node); },
+                        [&] { cpu_flash_attn(node); });
+                c->routes["fa"]++;
+                break;
+            }
+            case MI355X_OP_MUL_MAT_ID: {
+                const mi355x_tensor * as = node->src[0];
+                const mi355x_tensor * ids = node->src[2];
+                // an id outside [0, n_expert) is a malformed graph (ggml-rocket.cpp:6719)
+                for (int64_t t = 0; t < ids->ne[1]; t++)
+                    for (int64_t s = 0; s < ids->ne[0]; s++) {
+                        const int32_t e = *(const int32_t *)((const char *)ids->data + t * ids->nb[1] + s * ids->nb[0]);
+                        if (e < 0 || e >= as->ne[2]) return MI355X_STATUS_FAILED;
+                    }
+                const std::string key = weight_key(as);
+                if (!key.empty() && !c->moe_claimed.count(key) && moe_preflight_claim(key) == MOE_CLAIMED)
+                    c->moe_claimed.insert(key);
+                bool resident = false;
+                bool ok = true;
+                guarded(c, c->brk_moe, "MUL_MAT_ID", [&] { return mul_mat_id_device(c, node, resident); },
+                        [&] { ok = cpu_mul_mat_id(node); });
+                if (!ok) return MI355X_STATUS_FAILED;
+                if (resident) {
+                    if (c->moe_counted.insert(key).second) c->moe_resident += as->ne[2];
+                } else {
+                    c->moe_streamed += as->ne[2];
+                }
+                c->routes["moe"]++;
+                break;
+            }
+            default:
+                return MI355X_STATUS_FAILED;
+        }
+    }
+    return MI355X_STATUS_SUCCESS;
+}
+
+}  // extern "C"

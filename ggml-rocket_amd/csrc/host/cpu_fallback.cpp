@@ -1,0 +1,211 @@
+// SPDX-License-Identifier: MIT
+// The degraded path: an op whose device job failed is computed here, on the host, in fp64,
+// from the op's original inputs (ggml-rocket.cpp:4048-4084 for MUL_MAT, 5392-5442 for
+// FLASH_ATTN_EXT, 6927-6939 for an expert). Slow and rare by design: the route counters and
+// cpu_fallbacks() say when it ran. Rows of the output are spread over a few host threads.
+
+#include <math.h>
+#include <string.h>
+
+#include <algorithm>
+#include <thread>
+#include <vector>
+
+#include "host.h"
+
+namespace mxh {
+
+static float h2f(uint16_t h) {
+    const uint32_t s = (uint32_t)(h & 0x8000u) << 16, e = (h >> 10) & 0x1fu, m = h & 0x3ffu;
+    uint32_t x;
+    if (e == 0) {
+        if (m == 0) x = s;
+        else {
+            float f = (float)m * (1.0f / 16777216.0f);
+            memcpy(&x, &f, 4);
+            x |= s;
+        }
+    } else if (e == 31) {
+        x = s | 0x7f800000u | (m << 13);
+    } else {
+        x = s | ((e + 112u) << 23) | (m << 13);
+    }
+    float f;
+    memcpy(&f, &x, 4);
+    return f;
+}
+static inline uint16_t rd16(const uint8_t * p) { return (uint16_t)(p[0] | (p[1] << 8)); }
+
+// One row of n values of a weight type to f32, as ggml's dequantizers define them.
+bool decode_row_f32(int type, const void * src, float * y, int64_t n) {
+    const uint8_t * x = (const uint8_t *)src;
+    switch (type) {
+        case MI355X_TYPE_F32: memcpy(y, src, (size_t)n * 4); return true;
+        case MI355X_TYPE_F16: for (int64_t i = 0; i < n; i++) y[i] = h2f(rd16(x + 2 * i)); return true;
+        case MI355X_TYPE_BF16:
+            for (int64_t i = 0; i < n; i++) {
+                const uint32_t b = (uint32_t)rd16(x + 2 * i) << 16;
+                memcpy(&y[i], &b, 4);
+            }
+            return true;
+        case MI355X_TYPE_Q8_0:
+            for (int64_t b = 0; b < n / 32; b++, x += 34) {
+                const float d = h2f(rd16(x));
+                for (int l = 0; l < 32; l++) *y++ = d * (float)(int8_t)x[2 + l];
+            }
+            return true;
+        case MI355X_TYPE_Q4_K:
+            for (int64_t b = 0; b < n / 256; b++, x += 144) {
+                const float d = h2f(rd16(x)), dmin = h2f(rd16(x + 2));
+                const uint8_t * s = x + 4;
+                const uint8_t * q = x + 16;
+                for (int j = 0; j < 8; j++) {
+                    int sc, mn;
+                    if (j < 4) { sc = s[j] & 63; mn = s[j + 4] & 63; }
+                    else { sc = (s[j + 4] & 15) | ((s[j - 4] >> 6) << 4); mn = (s[j + 4] >> 4) | ((s[j] >> 6) << 4); }
+                    const float dd = d * (float)sc, mm = dmin * (float)mn;
+                    const uint8_t * qq = q + 32 * (j / 2);
+                    const int sh = (j % 2) * 4;
+                    for (int l = 0; l < 32; l++) *y++ = dd * (float)((qq[l] >> sh) & 15) - mm;
+                }
+            }
+            return true;
+        case MI355X_TYPE_Q6_K:
+            for (int64_t b = 0; b < n / 256; b++, x += 210) {
+                const float d = h2f(rd16(x + 208));
+                const int8_t * sc = (const int8_t *)(x + 192);
+                for (int p = 0; p < 256; p++) {
+                    const int half = p / 128, r = p % 128, quarter = r / 32, l = r % 32;
+                    const uint8_t lq = x[64 * half + l + (quarter & 1) * 32];
+                    const int lo = (quarter >= 2) ? (lq >> 4) : (lq & 15);
+                    const int hi = (x[128 + 32 * half + l] >> (2 * quarter)) & 3;
+                    *y++ = d * (float)sc[p / 16] * (float)((lo | (hi << 4)) - 32);
+                }
+            }
+            return true;
+        default: return false;
+    }
+}
+
+template <class F>
+static void parallel_rows(int64_t n, F && f) {
+    const int nt = (int)std::max<int64_t>(1, std::min<int64_t>(8, n / 4));
+    if (nt <= 1) { f((int64_t)0, n); return; }
+    std::vector<std::thread> th;
+    const int64_t per = (n + nt - 1) / nt;
+    for (int i = 0; i < nt; i++) {
+        const int64_t a = i * per, b = std::min(n, a + per);
+        if (a < b) th.emplace_back([&f, a, b] { f(a, b); });
+    }
+    for (auto & t : th) t.join();
+}
+
+// dst[..., n] = sum_k src1[..., k] * W[n, k], the weight decoded row by row.
+void cpu_mul_mat(const mi355x_tensor * dst) {
+    const mi355x_tensor * a = dst->src[0];
+    const mi355x_tensor * b = dst->src[1];
+    const int64_t K = a->ne[0], N = a->ne[1];
+    const int64_t rows = b->ne[1] * b->ne[2] * b->ne[3];
+    const size_t rb = (size_t)row_bytes(a->type, K);
+    std::vector<double> W((size_t)N * K);
+    parallel_rows(N, [&](int64_t n0, int64_t n1) {
+        std::vector<float> r((size_t)K);
+        for (int64_t n = n0; n < n1; n++) {
+            decode_row_f32(a->type, (const uint8_t *)a->data + n * rb, r.data(), K);
+            for (int64_t k = 0; k < K; k++) W[n * K + k] = r[k];
+        }
+    });
+    const float * X = (const float *)b->data;
+    float * D = (float *)dst->data;
+    parallel_rows(rows, [&](int64_t m0, int64_t m1) {
+        for (int64_t m = m0; m < m1; m++)
+            for (int64_t n = 0; n < N; n++) {
+                double acc = 0.0;
+                const double * w = &W[n * K];
+                const float * x = X + m * K;
+                for (int64_t k = 0; k < K; k++) acc += (double)x[k] * w[k];
+                D[m * N + n] = (float)acc;
+            }
+    });
+}
+
+// The full-precision attention of ggml-rocket.cpp:5392-5442: Q read as F32, the scale, soft-cap,
+// mask and softmax in double, a fully masked row written as zeros.
+void cpu_flash_attn(const mi355x_tensor * dst) {
+    const mi355x_tensor * q = dst->src[0];
+    const mi355x_tensor * k = dst->src[1];
+    const mi355x_tensor * v = dst->src[2];
+    const mi355x_tensor * m = dst->src[3];
+    const int64_t D = q->ne[0], T = q->ne[1], H = q->ne[2], KV = k->ne[1], HK = k->ne[2], DV = v->ne[0];
+    float scale, softcap;
+    memcpy(&scale, &dst->op_params[0], 4);
+    memcpy(&softcap, &dst->op_params[2], 4);
+    const int64_t g = H / HK;
+    parallel_rows(H * T, [&](int64_t r0, int64_t r1) {
+        std::vector<double> sc((size_t)KV), acc((size_t)DV), qd((size_t)D);
+        for (int64_t r = r0; r < r1; r++) {
+            const int64_t h = r / T, t = r % T, hk = h / g;
+            const char * qr = (const char *)q->data + t * q->nb[1] + h * q->nb[2];
+            for (int64_t c = 0; c < D; c++) qd[c] = *(const float *)(qr + c * q->nb[0]);
+            double mx = -INFINITY;
+            for (int64_t j = 0; j < KV; j++) {
+                const double mv = m ? (double)h2f(*(const uint16_t *)((const char *)m->data + t * m->nb[1] + j * 2)) : 0.0;
+                if (mv == -INFINITY) { sc[j] = -INFINITY; continue; }
+                const char * kr = (const char *)k->data + j * k->nb[1] + hk * k->nb[2];
+                double d = 0.0;
+                for (int64_t c = 0; c < D; c++) d += qd[c] * (double)h2f(*(const uint16_t *)(kr + c * 2));
+                double s = d * (double)scale;
+                if (softcap != 0.0f) s = (double)softcap * tanh(s / (double)softcap);
+                sc[j] = s + mv;
+                mx = std::max(mx, sc[j]);
+            }
+            double sum = 0.0;
+            for (int64_t j = 0; j < KV; j++) {
+                sc[j] = (mx == -INFINITY || sc[j] == -INFINITY) ? 0.0 : exp(sc[j] - mx);
+                sum += sc[j];
+            }
+            std::fill(acc.begin(), acc.end(), 0.0);
+            for (int64_t j = 0; j < KV; j++) {
+                if (sc[j] == 0.0) continue;
+                const char * vr = (const char *)v->data + j * v->nb[1] + hk * v->nb[2];
+                for (int64_t c = 0; c < DV; c++) acc[c] += sc[j] * (double)h2f(*(const uint16_t *)(vr + c * 2));
+            }
+            const double inv = sum > 0.0 ? 1.0 / sum : 0.0;
+            float * o = (float *)((char *)dst->data + h * dst->nb[1] + t * dst->nb[2]);
+            for (int64_t c = 0; c < DV; c++) o[c] = (float)(acc[c] * inv);
+        }
+    });
+}
+
+// dst[:, s, t] = as[:, :, ids[s, t]] . b[:, s % ne11, t]
+bool cpu_mul_mat_id(const mi355x_tensor * dst) {
+    const mi355x_tensor * as = dst->src[0];
+    const mi355x_tensor * b = dst->src[1];
+    const mi355x_tensor * ids = dst->src[2];
+    const int64_t K = as->ne[0], N = as->ne[1], E = as->ne[2];
+    const int64_t ne11 = b->ne[1], U = ids->ne[0], T = ids->ne[1];
+    for (int64_t t = 0; t < T; t++)
+        for (int64_t s = 0; s < U; s++) {
+            const int32_t e = *(const int32_t *)((const char *)ids->data + t * ids->nb[1] + s * ids->nb[0]);
+            if (e < 0 || e >= E) return false;
+        }
+    const size_t rb = (size_t)row_bytes(as->type, K);
+    parallel_rows(T, [&](int64_t t0, int64_t t1) {
+        std::vector<float> w((size_t)K);
+        for (int64_t t = t0; t < t1; t++)
+            for (int64_t s = 0; s < U; s++) {
+                const int32_t e = *(const int32_t *)((const char *)ids->data + t * ids->nb[1] + s * ids->nb[0]);
+                const float * x = (const float *)((const char *)b->data + t * b->nb[2] + (s % ne11) * b->nb[1]);
+                float * d = (float *)((char *)dst->data + t * dst->nb[2] + s * dst->nb[1]);
+                for (int64_t n = 0; n < N; n++) {
+                    decode_row_f32(as->type, (const uint8_t *)as->data + e * as->nb[2] + n * rb, w.data(), K);
+                    double acc = 0.0;
+                    for (int64_t k = 0; k < K; k++) acc += (double)x[k] * (double)w[k];
+                    d[n] = (float)acc;
+                }
+            }
+    });
+    return true;
+}
+
+}  // namespace mxh

@@ -88,6 +88,13 @@ MI355X_API int mi355x_weight_dequant_f16(int wtype, const void * w_dev, int64_t 
     return hip_status(mx::launch_dequant_f16(wtype, w_dev, rows, K, out_dev, S(stream)));
 }
 
+MI355X_API int mi355x_convert_f16(int type, const void * src_dev, int64_t n, uint16_t * dst_dev, void * stream) {
+    if ((type != mx::T_F32 && type != mx::T_BF16) || n < 0) return MI355X_E_ARG;
+    if (n == 0) return MI355X_OK;
+    if (!src_dev || !dst_dev || !aligned(src_dev, type == mx::T_F32 ? 4 : 2) || !aligned(dst_dev, 2)) return MI355X_E_ARG;
+    return hip_status(mx::launch_convert_f16(type, src_dev, n, dst_dev, S(stream)));
+}
+
 MI355X_API int mi355x_pack_act(const float * x_dev, int64_t ldx, int64_t M, int64_t K,
                                uint16_t * a16_dev, float * scales_dev, void * stream) {
     if (M < 0 || K <= 0 || K % 4 || ldx < K || ldx % 4 || M > INT32_MAX || K > INT32_MAX) return MI355X_E_ARG;

@@ -313,6 +313,17 @@ __global__ void __launch_bounds__(256) dequant_f16_kernel(const uint8_t * __rest
     *(u32x4 *)(d + run1 + 8) = o[3];
 }
 
+// F32 or BF16 values -> fp16 (round to nearest even): the resident form of an F32 / BF16 weight,
+// as rocket_weight_to_fp16 makes it (ggml-rocket.cpp:3855-3890).
+__global__ void convert_f16_kernel(int type, const void * __restrict__ src, int64_t n, uint16_t * __restrict__ dst) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    float f;
+    if (type == T_F32) f = ((const float *)src)[i];
+    else f = __builtin_bit_cast(float, (uint32_t)((const uint16_t *)src)[i] << 16);
+    dst[i] = f2h_bits(f);
+}
+
 // ggml Q8_0 -> split planes. One thread per block.
 __global__ void pack_q8_0_kernel(const uint8_t * __restrict__ src, int64_t rows, int64_t K,
                                  uint8_t * __restrict__ dst) {
@@ -475,6 +486,12 @@ hipError_t launch_dequant_f16(int wt, const void * W, int64_t rows, int64_t K, u
         case T_Q6_K: hipLaunchKernelGGL(dequant_f16_kernel<T_Q6_K>, grid, dim3(256), 0, st, w, rows, K, out); break;
         default: return hipErrorInvalidValue;
     }
+    return hipGetLastError();
+}
+
+hipError_t launch_convert_f16(int type, const void * src, int64_t n, uint16_t * dst, hipStream_t st) {
+    if (n <= 0) return hipSuccess;
+    hipLaunchKernelGGL(convert_f16_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, type, src, n, dst);
     return hipGetLastError();
 }
 

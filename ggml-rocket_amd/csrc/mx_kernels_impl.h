@@ -76,5 +76,6 @@ hipError_t launch_pack_act(const float * X, int64_t ldx, int M, int K, uint16_t 
 hipError_t launch_gemm(int wt, const GemmArgs & a, int n_tiles_total, hipStream_t st);
 hipError_t launch_dequant_f16(int wt, const void * W, int64_t rows, int64_t K, uint16_t * out, hipStream_t st);
 hipError_t launch_pack_weight(int wt, const void * src, int64_t rows, int64_t K, void * dst, hipStream_t st);
+hipError_t launch_convert_f16(int type, const void * src, int64_t n, uint16_t * dst, hipStream_t st);
 
 }  // namespace mx

@@ -245,3 +245,226 @@ def mul_mat_id(wtype: int, as_dev, n_expert: int, N: int, K: int, b, ids, out=No
     check(lib().mi355x_mul_mat_id(ctypes.byref(a), _ptr(workspace), workspace.numel(),
                                   _ptr(err) if err is not None else None, stream_handle()), "mul_mat_id")
     return out
+
+
+# ==== the backend host layer (include/ggml-mi355x.h) =========================================
+# A numpy-backed stand-in for the few ggml graph constructors the reference's tests use
+# (ggml_new_tensor_*, ggml_mul_mat, ggml_mul_mat_id, ggml_flash_attn_ext, permute / view), with
+# ggml's ne / nb conventions, so the host-layer tests read like the reference's.
+
+OP_NONE, OP_MUL_MAT, OP_MUL_MAT_ID, OP_FLASH_ATTN_EXT, OP_RESHAPE, OP_VIEW, OP_PERMUTE, \
+    OP_TRANSPOSE, OP_ADD, OP_SCALE, OP_OTHER = range(11)
+BUF_NONE, BUF_HOST, BUF_REPACK, BUF_OTHER = range(4)
+STATUS_SUCCESS, STATUS_FAILED = 0, -1
+_TYPE_SIZE_ALL = {0: (1, 4), 1: (1, 2), 8: (32, 34), 12: (256, 144), 14: (256, 210), 26: (1, 4),
+                  30: (1, 2), 2: (32, 18), 13: (256, 176), 39: (32, 17)}
+
+
+class Tensor(ctypes.Structure):
+    pass
+
+
+Tensor._fields_ = [("type", ctypes.c_int32), ("op", ctypes.c_int32),
+                   ("ne", ctypes.c_int64 * 4), ("nb", ctypes.c_size_t * 4),
+                   ("op_params", ctypes.c_int32 * 16), ("src", ctypes.POINTER(Tensor) * 10),
+                   ("data", ctypes.c_void_p), ("name", ctypes.c_char * 64),
+                   ("buffer_kind", ctypes.c_int32), ("buffer_id", ctypes.c_void_p),
+                   ("buffer_size", ctypes.c_size_t)]
+
+
+def _bind_host(L):
+    if getattr(L, "_host_bound", False):
+        return L
+    vp, i32, lng, sz = ctypes.c_void_p, ctypes.c_int, ctypes.c_long, ctypes.c_size_t
+    pt = ctypes.POINTER(Tensor)
+    L.ggml_backend_mi355x_name.restype = ctypes.c_char_p
+    L.ggml_backend_mi355x_description.restype = ctypes.c_char_p
+    L.ggml_backend_mi355x_get_memory.argtypes = [ctypes.POINTER(sz), ctypes.POINTER(sz)]
+    L.ggml_backend_mi355x_supports_op.restype = ctypes.c_bool
+    L.ggml_backend_mi355x_supports_op.argtypes = [pt]
+    L.ggml_backend_mi355x_offload_op.restype = ctypes.c_bool
+    L.ggml_backend_mi355x_offload_op.argtypes = [pt]
+    L.ggml_backend_mi355x_supports_buft.restype = ctypes.c_bool
+    L.ggml_backend_mi355x_supports_buft.argtypes = [i32]
+    L.ggml_backend_mi355x_init.restype = vp
+    L.ggml_backend_mi355x_free.argtypes = [vp]
+    L.ggml_backend_is_mi355x.restype = ctypes.c_bool
+    L.ggml_backend_is_mi355x.argtypes = [vp]
+    L.ggml_backend_mi355x_set_n_threads.argtypes = [vp, i32]
+    L.ggml_backend_mi355x_get_n_threads.argtypes = [vp]
+    L.ggml_backend_mi355x_set_quant_resident.argtypes = [vp, i32]
+    L.ggml_backend_mi355x_graph_compute.argtypes = [vp, ctypes.POINTER(pt), i32]
+    L.ggml_backend_mi355x_route_ops.restype = lng
+    L.ggml_backend_mi355x_route_ops.argtypes = [vp, ctypes.c_char_p]
+    L.ggml_backend_mi355x_cpu_fallbacks.restype = lng
+    L.ggml_backend_mi355x_cpu_fallbacks.argtypes = [vp]
+    L.ggml_backend_mi355x_moe_stats.argtypes = [vp, ctypes.POINTER(lng), ctypes.POINTER(lng)]
+    L.ggml_backend_mi355x_route_stats.argtypes = [vp, ctypes.c_char_p, ctypes.POINTER(lng), ctypes.POINTER(lng),
+                                                  ctypes.POINTER(lng)]
+    L.ggml_backend_mi355x_inject_faults.argtypes = [vp, ctypes.c_char_p, i32]
+    L.ggml_backend_mi355x_weight_key.argtypes = [pt, ctypes.c_char_p, i32]
+    L.ggml_backend_mi355x_parse_mb.restype = ctypes.c_bool
+    L.ggml_backend_mi355x_parse_mb.argtypes = [ctypes.c_char_p, ctypes.POINTER(sz)]
+    L._host_bound = True
+    return L
+
+
+def host():
+    return _bind_host(lib())
+
+
+class Graph:
+    """Owns the descriptors and numpy buffers of one graph (a ggml_context stand-in). With
+    alloc=False (a no_alloc context) tensors have no data, as in a supports_op probe."""
+
+    def __init__(self, alloc=True):
+        self.alloc = alloc
+        self.tensors = []
+        self.keep = []
+
+    def _new(self, ttype, ne, name=None, op=OP_NONE, srcs=(), data=None):
+        import numpy as np
+        t = Tensor()
+        t.type = ttype
+        t.op = op
+        ne = list(ne) + [1] * (4 - len(ne))
+        blk, bsz = _TYPE_SIZE_ALL[ttype]
+        for i in range(4):
+            t.ne[i] = ne[i]
+        t.nb[0] = bsz
+        t.nb[1] = bsz * (ne[0] // blk)
+        t.nb[2] = t.nb[1] * ne[1]
+        t.nb[3] = t.nb[2] * ne[2]
+        for i, s in enumerate(srcs):
+            if s is not None:
+                t.src[i] = ctypes.pointer(s)
+        if name:
+            t.name = name.encode()[:63]
+        nbytes = t.nb[3] * ne[3]
+        if self.alloc and op in (OP_NONE, OP_MUL_MAT, OP_MUL_MAT_ID, OP_FLASH_ATTN_EXT, OP_OTHER, OP_ADD, OP_SCALE):
+            buf = np.zeros(max(nbytes, 1), dtype=np.uint8) if data is None else data
+            self.keep.append(buf)
+            t.data = buf.ctypes.data
+            t.buffer_kind = BUF_HOST
+            t.buffer_size = buf.nbytes
+            t.buffer_id = buf.ctypes.data
+        self.tensors.append(t)
+        return t
+
+    def new_tensor(self, ttype, ne, name=None):
+        return self._new(ttype, ne, name)
+
+    def set(self, t, arr):
+        import numpy as np
+        a = np.ascontiguousarray(arr).view(np.uint8).reshape(-1)
+        n = min(a.nbytes, t.buffer_size)
+        ctypes.memmove(t.data, a.ctypes.data, n)
+
+    def get(self, t, dtype, shape):
+        import numpy as np
+        n = int(np.prod(shape)) * np.dtype(dtype).itemsize
+        out = np.empty(shape, dtype=dtype)
+        ctypes.memmove(out.ctypes.data, t.data, n)
+        return out
+
+    def mul_mat(self, a, b):
+        return self._new(F32, [a.ne[1], b.ne[1], b.ne[2], b.ne[3]], op=OP_MUL_MAT, srcs=(a, b))
+
+    def mul_mat_id(self, a, b, ids):
+        return self._new(F32, [a.ne[1], ids.ne[0], b.ne[2], 1], op=OP_MUL_MAT_ID, srcs=(a, b, ids))
+
+    def flash_attn_ext(self, q, k, v, mask, scale, max_bias=0.0, softcap=0.0, acc_prec=0):
+        t = self._new(F32, [v.ne[0], q.ne[2], q.ne[1], q.ne[3]], op=OP_FLASH_ATTN_EXT, srcs=(q, k, v, mask))
+        fp = (ctypes.c_float * 3)(scale, max_bias, softcap)
+        ctypes.memmove(ctypes.addressof(t.op_params), fp, 12)
+        if acc_prec:
+            t.op_params[3] = acc_prec
+        return t
+
+    def op(self, ttype, ne, op, srcs=()):
+        """A node of any other op (e.g. an ADD or a SCALE) for placement probes."""
+        return self._new(ttype, ne, op=op, srcs=srcs)
+
+    def permute_view(self, src, ne, nb, offset=0):
+        """A strided view of `src` (ggml_view_* / ggml_permute): same bytes, new ne / nb."""
+        t = Tensor()
+        t.type = src.type
+        t.op = OP_VIEW
+        for i in range(4):
+            t.ne[i] = ne[i]
+            t.nb[i] = nb[i]
+        t.src[0] = ctypes.pointer(src)
+        if src.data:
+            t.data = src.data + offset
+            t.buffer_kind = src.buffer_kind
+            t.buffer_size = src.buffer_size
+            t.buffer_id = src.buffer_id
+        self.tensors.append(t)
+        return t
+
+
+class Backend:
+    """One backend instance (ggml_backend_mi355x_init .. free)."""
+
+    def __init__(self):
+        self.L = host()
+        self.h = self.L.ggml_backend_mi355x_init()
+        if not self.h:
+            raise MI355XError("init failed")
+
+    def free(self):
+        if self.h:
+            self.L.ggml_backend_mi355x_free(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+    def compute(self, nodes):
+        arr = (ctypes.POINTER(Tensor) * len(nodes))(*[ctypes.pointer(n) for n in nodes])
+        return self.L.ggml_backend_mi355x_graph_compute(self.h, arr, len(nodes))
+
+    def route_ops(self, route=None):
+        return self.L.ggml_backend_mi355x_route_ops(self.h, route.encode() if route else None)
+
+    def cpu_fallbacks(self):
+        return self.L.ggml_backend_mi355x_cpu_fallbacks(self.h)
+
+    def moe_stats(self):
+        a, b = ctypes.c_long(), ctypes.c_long()
+        self.L.ggml_backend_mi355x_moe_stats(self.h, ctypes.byref(a), ctypes.byref(b))
+        return a.value, b.value
+
+    def route_stats(self, group):
+        a, b, c = ctypes.c_long(), ctypes.c_long(), ctypes.c_long()
+        self.L.ggml_backend_mi355x_route_stats(self.h, group.encode(), ctypes.byref(a), ctypes.byref(b), ctypes.byref(c))
+        return a.value, b.value, c.value
+
+    def set_quant_resident(self, mode):
+        self.L.ggml_backend_mi355x_set_quant_resident(self.h, mode)
+
+    def inject_faults(self, group, n):
+        self.L.ggml_backend_mi355x_inject_faults(self.h, group.encode(), n)
+
+
+def supports_op(t):
+    return bool(host().ggml_backend_mi355x_supports_op(ctypes.byref(t)))
+
+
+def offload_op(t):
+    return bool(host().ggml_backend_mi355x_offload_op(ctypes.byref(t)))
+
+
+def weight_key(t):
+    buf = ctypes.create_string_buffer(256)
+    host().ggml_backend_mi355x_weight_key(ctypes.byref(t), buf, 256)
+    return buf.value.decode()
+
+
+def parse_mb(text):
+    v = ctypes.c_size_t(12345)
+    ok = host().ggml_backend_mi355x_parse_mb(text.encode(), ctypes.byref(v))
+    return ok, v.value

@@ -76,6 +76,11 @@ MI355X_API int mi355x_weight_pack(int wtype, const void * src_dev, int64_t rows,
 MI355X_API int mi355x_weight_dequant_f16(int wtype, const void * w_dev, int64_t rows, int64_t K,
                                          uint16_t * out_dev, void * stream);
 
+/* F32 (type 0) or BF16 (type 30) values -> fp16, round to nearest even: the resident form of an
+ * F32 / BF16 weight (the F32 and BF16 branches of rocket_weight_to_fp16, ggml-rocket.cpp:
+ * 3855-3890). n values; src 4- or 2-byte aligned, dst 2-byte aligned. */
+MI355X_API int mi355x_convert_f16(int type, const void * src_dev, int64_t n, uint16_t * dst_dev, void * stream);
+
 /* ---- MUL_MAT ----------------------------------------------------------------------------- */
 
 /* F32 activations [M][ldx] -> fp16 [M][K] divided by each row's max |x| (1 for a zero row),

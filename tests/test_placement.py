@@ -1,0 +1,120 @@
+"""The placement gate (CPU only): every CHECK of test-rocket-placement.cpp on this backend's
+supports_op / offload_op, with the RK3588 expectations of the reference except where the
+MI355X route is wider or narrower; each such row says why.
+
+Knob-dependent modes run in a child process with their environment (knobs are read once per
+process), as the reference forks a child per mode.
+"""
+import json
+import os
+import subprocess
+import sys
+
+import pytest
+
+import ggml_mi355x as mx
+from placement_probes import (mm_supported, mm_computed_w_supported, add_offloaded, mm_offloaded,
+                              fa_supported, PREC_F32, PREC_BF16, PREC_F16, PREC_Q8)
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+K, N, M, MQ = 256, 128, 256, 512
+
+CASES = [
+    ("F16 leaf weight, valid shape -> offload", True, lambda: mm_supported(K, N, M, mx.F16)),
+    ("F32 leaf weight, valid shape -> offload", True, lambda: mm_supported(K, N, M, mx.F32)),
+    ("BF16 leaf weight -> offload (converted to fp16)", True, lambda: mm_supported(K, N, M, mx.BF16)),
+    ("Q8_0 leaf, M >= quant floor -> offload", True, lambda: mm_supported(K, N, MQ, mx.Q8_0)),
+    ("Q4_K leaf, M >= quant floor -> offload", True, lambda: mm_supported(K, N, MQ, mx.Q4_K)),
+    ("Q6_K leaf, M >= quant floor -> offload", True, lambda: mm_supported(K, N, MQ, mx.Q6_K)),
+    ("Q4_K leaf, M(256) < quant floor -> CPU", False, lambda: mm_supported(K, N, M, mx.Q4_K)),
+    ("K%32 != 0 (K=80) -> CPU", False, lambda: mm_supported(80, N, M, mx.F16)),
+    ("N%16 != 0 (N=70) -> CPU", False, lambda: mm_supported(K, 70, M, mx.F16)),
+    ("N=112 (N%16 == 0) -> offload", True, lambda: mm_supported(K, 112, M, mx.F16)),
+    ("K<64 (K=32) -> CPU", False, lambda: mm_supported(32, N, M, mx.F16)),
+    ("N<64 (N=48) -> CPU", False, lambda: mm_supported(K, 48, M, mx.F16)),
+    ("M=1 decode GEMV -> CPU", False, lambda: mm_supported(K, N, 1, mx.F16)),
+    ("computed (non-leaf) src0 -> CPU", False, lambda: mm_computed_w_supported(K, N, M)),
+    ("offload_op: valid GEMM -> offload", True, lambda: mm_offloaded(K, N, M)),
+    ("offload_op: ADD -> CPU", False, lambda: add_offloaded(K, M)),
+    # The accumulator declaration: the reference's NPU route writes an fp16 C, so it declines
+    # F32 / BF16 (ggml-rocket.cpp:7372-7380). This device accumulates in fp32 and writes F32,
+    # which meets both declarations.
+    ("acc F32 declared -> offload (fp32 accumulation here)", True, lambda: mm_supported(K, N, M, mx.F16, 0, PREC_F32)),
+    ("acc BF16 declared -> offload (fp32 accumulation here)", True, lambda: mm_supported(K, N, M, mx.F16, 0, PREC_BF16)),
+    ("acc F16 declared -> offload", True, lambda: mm_supported(K, N, M, mx.F16, 0, PREC_F16)),
+    ("src1 F32 declared -> CPU (the activation is converted to fp16)", False,
+     lambda: mm_supported(K, N, M, mx.F16, 3, PREC_F32)),
+    ("src1 BF16 declared -> CPU", False, lambda: mm_supported(K, N, M, mx.F16, 3, PREC_BF16)),
+    ("src1 F16 declared -> offload", True, lambda: mm_supported(K, N, M, mx.F16, 3, PREC_F16)),
+    ("src1 Q8 declared -> offload", True, lambda: mm_supported(K, N, M, mx.F16, 3, PREC_Q8)),
+    ("128x128 F32 leaf -> offload", True, lambda: mm_supported(128, 128, M, mx.F32)),
+    ("same, SRC0_IS_HADAMARD hint -> CPU", False, lambda: mm_supported(128, 128, M, mx.F32, 1, 1)),
+    ("FA: F16 KV, n_tokens >= min_t, n_kv >= min_kv -> offload", True,
+     lambda: fa_supported(64, 256, 8, 1024, 2, mx.F16, 0.0)),
+    ("FA: acc F32 declared -> offload (read, not enforced)", True,
+     lambda: fa_supported(64, 256, 8, 1024, 2, mx.F16, 0.0, PREC_F32)),
+    ("FA: decode (n_tokens=1 < min_t) -> CPU", False, lambda: fa_supported(64, 1, 8, 1024, 2, mx.F16, 0.0)),
+    ("FA: short context (n_kv=512 < min_kv) -> CPU", False, lambda: fa_supported(64, 256, 8, 512, 2, mx.F16, 0.0)),
+    ("FA: head_dim%32 != 0 (48) -> CPU", False, lambda: fa_supported(48, 256, 8, 1024, 2, mx.F16, 0.0)),
+    ("FA: K/V not F16 -> CPU", False, lambda: fa_supported(64, 256, 8, 1024, 2, mx.F32, 0.0)),
+    ("FA: ALiBi (max_bias > 0) -> CPU", False, lambda: fa_supported(64, 256, 8, 1024, 2, mx.F16, 8.0)),
+    # Narrower than the reference: the kernel covers head dims 64 and 128 with dk == dv; the
+    # reference also takes any dk%32 / dv%16, MLA included (ggml-rocket.cpp:7740-7760).
+    ("FA: head_dim 128 -> offload", True, lambda: fa_supported(128, 512, 32, 4096, 8, mx.F16, 0.0)),
+    ("FA: head_dim 96 -> CPU (kernel covers 64 / 128)", False, lambda: fa_supported(96, 256, 8, 1024, 2, mx.F16, 0.0)),
+    ("FA: dk 192 / dv 128 (MLA) -> CPU", False, lambda: fa_supported(192, 256, 8, 1024, 2, mx.F16, 0.0, 0, 128)),
+    # Narrower: a quantized type without a device decoder is declined (the reference takes any
+    # type with a ggml to_float, 7452-7455).
+    ("Q4_0 leaf -> CPU (no device decoder)", False, lambda: mm_supported(K, N, MQ, 2)),
+    ("Q5_K leaf -> CPU (no device decoder)", False, lambda: mm_supported(K, N, MQ, 13)),
+]
+
+
+@pytest.mark.parametrize("label,want,fn", CASES, ids=[c[0] for c in CASES])
+def test_placement(label, want, fn):
+    assert fn() == want, label
+
+
+def test_supports_buft():
+    assert mx.host().ggml_backend_mi355x_supports_buft(mx.BUF_HOST)
+    assert not mx.host().ggml_backend_mi355x_supports_buft(mx.BUF_REPACK)
+    assert not mx.host().ggml_backend_mi355x_supports_buft(mx.BUF_OTHER)
+
+
+def test_repacked_weight_declined():
+    g = mx.Graph(alloc=False)
+    W = g.new_tensor(mx.Q4_K, [K, N])
+    W.buffer_kind = mx.BUF_REPACK
+    X = g.new_tensor(mx.F32, [K, MQ])
+    assert not mx.supports_op(g.mul_mat(W, X))
+
+
+def _child(mode, env):
+    e = {k: v for k, v in os.environ.items() if not k.startswith(("MI355X_", "ROCKET_"))}
+    e.update(env)
+    r = subprocess.run([sys.executable, os.path.join(HERE, "placement_probes.py"), mode], env=e,
+                       capture_output=True, text=True, timeout=120)
+    assert r.returncode == 0, r.stderr
+    return json.loads(r.stdout.strip().splitlines()[-1])
+
+
+@pytest.mark.parametrize("mode,env", [("auto", {}), ("budget", {"MI355X_MOE_CACHE_MB": "1"}),
+                                      ("off", {"MI355X_MOE": "0"}), ("forced", {"MI355X_MOE": "1"}),
+                                      ("prec_quant", {"ROCKET_INT8": "1", "ROCKET_INT4": "1"})])
+def test_moe_and_knob_modes(mode, env):
+    bad = [row for row in _child(mode, env) if row[1] != row[2]]
+    assert not bad, bad
+
+
+def test_reference_knob_spelling_is_honoured():
+    """A ROCKET_* knob means what it means for the reference (MOE=0 under its own name)."""
+    bad = [row for row in _child("off", {"ROCKET_MOE": "0"}) if row[1] != row[2]]
+    assert not bad, bad
+
+
+def test_moe_charge_all_source():
+    """Same budget, same four stacks in one buffer: charging the mapped source admits fewer
+    (test-rocket-placement.cpp:302-372, 527-538)."""
+    n_default = _child("src_admitted", {})
+    n_all_src = _child("src_admitted", {"MI355X_MOE_CHARGE_ALL_SOURCE": "1"})
+    assert n_all_src < n_default, (n_default, n_all_src)
