@@ -32,6 +32,12 @@ sys.path.insert(0, os.path.join(ROOT, "ggml-rocket_amd"))
 METRIC = "prefill tok/s (8B-shape Q4_K, 2048 tok); MUL_MAT/FA TFLOP/s vs MFMA peak"
 PEAK_F16_TFLOPS = 2500.0
 PEAK_HBM_GBS = 8000.0
+# HBM bytes per GEMM launch, mean over a layer's four launches (qkv, o, gate/up, down) at M = 512
+# on the fp16-resident route: rocprofv3 FETCH_SIZE and WRITE_SIZE of `bench.py --pmc-probe`, each
+# scaled by what the counter reads for a plain 1 GiB device copy (x2.000 and x1.000). Hardware
+# counters cannot be read inside the timed run, so the figure is the last measurement of this
+# kernel (profiles/prefill_8b_hbm_traffic_pmc.md) and must be re-measured when the kernel changes.
+GEMM_TRAFFIC_BYTES = {"prepacked-q": 198.5e6, "mt": None}
 
 L_LAYERS, D_MODEL, FFN, NH, NKV, HD = 32, 4096, 14336, 32, 8, 128
 TOKENS, UBATCH = 2048, 512
@@ -46,6 +52,9 @@ def parse():
     p.add_argument("--layers", type=int, default=L_LAYERS)
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-threads", type=int, default=0)
+    p.add_argument("--pmc-probe", action="store_true",
+                   help="for hardware-counter runs: launch each distinct op of one layer once, "
+                        "eagerly, then a plain 1 GiB device copy (the calibration kernel), and exit")
     return p.parse_args()
 
 
@@ -261,6 +270,40 @@ def time_ops(pf, reps=20):
     return out
 
 
+def pmc_probe(pf):
+    """One eager launch of each distinct op of the step (after one warm-up pass), then a plain
+    device copy of 1 GiB, whose FETCH_SIZE / WRITE_SIZE read against its known 1 GiB in and out
+    give the counters' scale. Prints the launch order so counter rows can be matched to ops."""
+    torch = pf.torch
+    lw, sh = pf.layers[0], pf.shapes
+    pf.reset_counters(False)
+    ops = [
+        ("pack x[512,4096]", lambda: pf._pack(pf.x, D_MODEL)),
+        ("gemm qkv 512x4096x6144", lambda: pf._gemm(D_MODEL, [(lw["q"], sh["q"][0], pf.qo),
+                                                             (lw["k"], sh["k"][0], pf.ko),
+                                                             (lw["v"], sh["v"][0], pf.vo)], 0.0)),
+        ("gemm o 512x4096x4096", lambda: pf._gemm(D_MODEL, [(lw["o"], D_MODEL, pf.oo)], 0.0)),
+        ("gemm gate/up 512x4096x28672", lambda: pf._gemm(D_MODEL, [(lw["gate"], FFN, pf.go),
+                                                                  (lw["up"], FFN, pf.uo)], 0.0)),
+        ("pack act[512,14336]", lambda: pf._pack(pf.act, FFN)),
+        ("gemm down 512x14336x4096", lambda: pf._gemm(FFN, [(lw["down"], D_MODEL, pf.do)], 0.0)),
+        ("fa n_kv 2048", lambda: pf._fa(3)),
+    ]
+    for _, fn in ops:
+        fn()
+    torch.cuda.synchronize()
+    for name, fn in ops:
+        print(f"pmc-probe: {name}", flush=True)
+        fn()
+        torch.cuda.synchronize()
+    src = torch.ones(1 << 28, device="cuda", dtype=torch.float32)
+    dst = torch.empty_like(src)
+    print("pmc-probe: copy 1 GiB -> 1 GiB", flush=True)
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    print("pmc-probe: done", flush=True)
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -269,6 +312,9 @@ def main():
         sys.exit(2)
     import torch
     torch.cuda.set_device(0)
+    if args.pmc_probe:
+        pmc_probe(Prefill(args.route, 1))
+        return
     pf = Prefill(args.route, args.layers)
 
     pf.reset_counters(False)
@@ -341,7 +387,8 @@ def main():
                    "ubatch": UBATCH, "parallelism": "none (1 GPU)",
                    "replay": "hip graph" if graph is not None else "eager"},
         "roofline": {"bound": "mfma", "achieved": round(gemm_tf, 1), "peak": PEAK_F16_TFLOPS,
-                     "unit": "TFLOP/s", "frac": round(gemm_tf / PEAK_F16_TFLOPS, 4), "traffic": None,
+                     "unit": "TFLOP/s", "frac": round(gemm_tf / PEAK_F16_TFLOPS, 4),
+                     "traffic": GEMM_TRAFFIC_BYTES[args.route],
                      "kernel": "gemm_kernel (fp16 MFMA 32x32x16)",
                      "avg_launch_us": round(gemm["sec"] / gemm["launches"] * 1e6, 2),
                      "flop_per_launch": round(gemm["flops"] / gemm["launches"])},
