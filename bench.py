@@ -37,7 +37,7 @@ PEAK_HBM_GBS = 8000.0
 # scaled by what the counter reads for a plain 1 GiB device copy (x2.000 and x1.000). Hardware
 # counters cannot be read inside the timed run, so the figure is the last measurement of this
 # kernel (profiles/prefill_8b_hbm_traffic_pmc.md) and must be re-measured when the kernel changes.
-GEMM_TRAFFIC_BYTES = {"prepacked-q": 198.5e6, "mt": None}
+GEMM_TRAFFIC_BYTES = {"prepacked-q": 187.9e6, "mt": None}
 
 L_LAYERS, D_MODEL, FFN, NH, NKV, HD = 32, 4096, 14336, 32, 8, 128
 TOKENS, UBATCH = 2048, 512
@@ -389,7 +389,7 @@ def main():
         "roofline": {"bound": "mfma", "achieved": round(gemm_tf, 1), "peak": PEAK_F16_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(gemm_tf / PEAK_F16_TFLOPS, 4),
                      "traffic": GEMM_TRAFFIC_BYTES[args.route],
-                     "kernel": "gemm_kernel (fp16 MFMA 32x32x16)",
+                     "kernel": "gemm_f16_kernel (LDS-DMA, fp16 MFMA 32x32x16)",
                      "avg_launch_us": round(gemm["sec"] / gemm["launches"] * 1e6, 2),
                      "flop_per_launch": round(gemm["flops"] / gemm["launches"])},
         "kernels": {

@@ -13,8 +13,9 @@
 //   dequant_f16   a weight panel -> fp16 [rows][K] (the resident-fp16 form, "prepacked-q").
 //   pack_weight   a ggml Q8_0 / Q6_K payload -> its split HBM layout (mx_weights.h).
 //
-// Tiling: 256 threads (4 waves) per block, a 128x128 output tile, K staged 64 at a time through
-// a double-buffered, XOR-swizzled LDS tile; each wave owns a 64x64 quadrant (2x2 MFMA blocks).
+// Two GEMM kernels: a register-staged one that decodes any weight format into LDS (gemm_kernel),
+// and for fp16 weights one that moves both operands into LDS by DMA (gemm_f16_kernel). The
+// launcher picks a tile configuration of either per call from the output shape.
 
 #include "mx_weights.h"
 #include "mx_kernels_impl.h"
@@ -278,6 +279,221 @@ gemm_kernel(GemmArgs args) {
     }
 }
 
+// ---------------------------------------------------------------------------------------------
+// fp16-weight GEMM with LDS DMA
+//
+// For fp16 weights nothing has to be decoded between HBM and LDS, so both operands go straight
+// into LDS with global_load_lds_dwordx4 (gfx950): no staging registers, no ds_write. K is staged
+// DK (32, 64 or 128) values at a time through a ring of NS LDS stages; while one stage is
+// multiplied the next NS-1 are landing. A block is WGM x WGN waves, each owning a
+// (BM/WGM) x (BN/WGN) tile of 32x32x16 MFMAs with its accumulators in AGPRs. With 8 waves two
+// share each SIMD, so one wave's MFMAs cover the other's LDS reads and barrier waits.
+//
+// A DMA instruction writes 64 lanes x 16 bytes to 1 KB of consecutive LDS; lane l lands at
+// base + 16 l. Each lane therefore fetches the global chunk that belongs at its LDS slot under
+// the swizzle: a row of DK values holds CH = DK/8 chunks, and slot (row, p) holds logical chunk
+// p ^ ((row / (16/CH)) & (CH-1)), so the 16 rows of an MFMA fragment read hit 16 distinct bank
+// groups. With DK >= 64 every DMA instruction covers whole 128-byte lines of A and W, which
+// halves the cache-line lookups per byte against DK = 32 (the limit of this path when all its
+// data hits in L2). Rows past M or N are clamped to the last real row (their results are never
+// stored); K must be a multiple of DK, so there is no K tail.
+//
+// The waits are explicit, and the compiler is kept from adding its own around the DMA:
+//   * before every barrier, s_waitcnt on this wave's DMA count (the stage about to be read has
+//     landed, the NS-2 behind it may still be in flight) and on lgkmcnt (this wave's LDS reads of
+//     the stage about to be overwritten are done);
+//   * every iteration issues exactly one stage of DMA (past the last stage it re-fetches the last
+//     one into a buffer nobody reads again), so those counts are the same every time and the loop
+//     body has no branch;
+//   * the compiler waits for all outstanding LDS reads before an MFMA whose fragment is still in
+//     flight (it cannot order them against the DMA), so each fragment read is issued after the
+//     first MFMA that would otherwise wait for it, and scheduling barriers keep that order.
+// KSPLIT = 2 splits K between two blocks that add their halves atomically into a zeroed output
+// (two addends: the sum is the same in either order).
+// ---------------------------------------------------------------------------------------------
+template <int BM, int BN, int WGM, int WGN, int DK, int NS>
+struct F16Cfg {
+    static constexpr int NW = WGM * WGN, THREADS = WAVE * NW;
+    static constexpr int TM = BM / WGM, TN = BN / WGN, MI = TM / 32, NJ = TN / 32;
+    static constexpr int CH = DK / 8, RPW = 16 / CH, RB = DK * 2;
+    static constexpr int A_BYTES = BM * RB, B_BYTES = BN * RB, STAGE = A_BYTES + B_BYTES;
+    static constexpr int LDS = NS * STAGE;
+    static constexpr int PA = A_BYTES / (THREADS * 16), PB = B_BYTES / (THREADS * 16);   // DMA per wave
+    static constexpr int PER = PA + PB;
+    static_assert(MI >= 1 && NJ >= 1 && TM % 32 == 0 && TN % 32 == 0, "wave tile");
+    static_assert(PA >= 1 && PB >= 1 && PA * THREADS * 16 == A_BYTES && PB * THREADS * 16 == B_BYTES, "DMA split");
+    static_assert(NS >= 2 && (NS - 1) * PER <= 63, "vmcnt range");
+    static_assert(LDS <= 160 * 1024, "LDS");
+};
+
+typedef const void __attribute__((address_space(1))) * gptr_t;
+typedef void __attribute__((address_space(3))) * lptr_t;
+
+__device__ __forceinline__ void dma16(const void * g, void * l) {
+    __builtin_amdgcn_global_load_lds((gptr_t)g, (lptr_t)l, 16, 0, 0);
+}
+
+// s_waitcnt with vmcnt(N), expcnt(7) (no wait), lgkmcnt(0): gfx9 encoding.
+template <int N>
+__device__ __forceinline__ void wait_vm_lgkm0() {
+    static_assert(N >= 0 && N <= 63, "vmcnt");
+    __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (0 << 8) | ((N >> 4) << 14));
+}
+
+template <int BM, int BN, int WGM, int WGN, int DK, int NS, int KSPLIT>
+__global__ void __launch_bounds__(WAVE * WGM * WGN)
+__attribute__((amdgpu_waves_per_eu(WGM * WGN / 4, WGM * WGN / 4)))
+gemm_f16_kernel(GemmArgs args) {
+    using C = F16Cfg<BM, BN, WGM, WGN, DK, NS>;
+    extern __shared__ __align__(16) uint8_t smem[];
+    const int t = threadIdx.x, lane = t % WAVE, wave = t / WAVE;
+    const int wm = wave / WGN, wn = wave % WGN;
+
+    int tile = xcd_tile(blockIdx.x, gridDim.x);
+    const int split = tile % KSPLIT;
+    tile /= KSPLIT;
+    const int mt = tile % args.m_tiles, nt = tile / args.m_tiles;
+    int g = 0;
+#pragma unroll
+    for (int i = 1; i < GEMM_MAX_GROUPS; i++)
+        if (i < args.ng && nt >= args.g[i].ntile_begin) g = i;
+    const uint16_t * W = (const uint16_t *)args.g[0].W;
+    int64_t row0 = args.g[0].row0;
+    int N = args.g[0].N, ntb = args.g[0].ntile_begin;
+    float * Cp = args.g[0].C;
+    int64_t ldc = args.g[0].ldc;
+#pragma unroll
+    for (int i = 1; i < GEMM_MAX_GROUPS; i++)
+        if (i == g) {
+            W = (const uint16_t *)args.g[i].W; row0 = args.g[i].row0; N = args.g[i].N;
+            ntb = args.g[i].ntile_begin; Cp = args.g[i].C; ldc = args.g[i].ldc;
+        }
+    const int n0 = (nt - ntb) * BN, m0 = mt * BM;
+    const int M = args.M, K = args.K;
+    const int nk_all = K / DK;
+    const int per = (nk_all + KSPLIT - 1) / KSPLIT;
+    const int kb = split * per;
+    const int nk = max(0, min(nk_all, kb + per) - kb);
+
+    // this lane's global sources, one row chunk per DMA instruction, advanced by DK per stage
+    const uint16_t * asrc[C::PA];
+    const uint16_t * bsrc[C::PB];
+#pragma unroll
+    for (int q = 0; q < C::PA; q++) {
+        const int slot = (q * C::NW + wave) * WAVE + lane;
+        const int r = slot / C::CH, c = (slot % C::CH) ^ ((r / C::RPW) & (C::CH - 1));
+        asrc[q] = args.A + (int64_t)min(m0 + r, M - 1) * args.lda + (int64_t)kb * DK + 8 * c;
+    }
+#pragma unroll
+    for (int q = 0; q < C::PB; q++) {
+        const int slot = (q * C::NW + wave) * WAVE + lane;
+        const int r = slot / C::CH, c = (slot % C::CH) ^ ((r / C::RPW) & (C::CH - 1));
+        bsrc[q] = W + (row0 + min(n0 + r, N - 1)) * (int64_t)K + (int64_t)kb * DK + 8 * c;
+    }
+    // the LDS destination of a DMA instruction must be wave-uniform (it goes to M0): take the
+    // wave index from an SGPR so the address arithmetic stays scalar
+    const int wave_s = __builtin_amdgcn_readfirstlane(wave);
+    auto issue = [&](int s) {
+        s = min(s, nk - 1);
+        uint8_t * st = smem + (s % NS) * C::STAGE;
+        const int64_t off = (int64_t)s * DK;
+#pragma unroll
+        for (int q = 0; q < C::PA; q++) dma16(asrc[q] + off, st + (q * C::NW + wave_s) * 1024);
+#pragma unroll
+        for (int q = 0; q < C::PB; q++) dma16(bsrc[q] + off, st + C::A_BYTES + (q * C::NW + wave_s) * 1024);
+    };
+
+    float16v acc[C::MI][C::NJ];
+#pragma unroll
+    for (int i = 0; i < C::MI; i++)
+#pragma unroll
+        for (int j = 0; j < C::NJ; j++)
+#pragma unroll
+            for (int e = 0; e < 16; e++) acc[i][j][e] = 0.0f;
+
+    // fragment rows (w*T + i*32 + lr), logical chunk (2 ks + lg); the row part of the swizzle
+    // depends on lr only, because w*T + i*32 is a multiple of 16
+    const int lr = lane % 32, lg = lane / 32, x = (lr / C::RPW) & (C::CH - 1);
+    const int a_off = (wm * C::TM + lr) * C::RB, b_off = C::A_BYTES + (wn * C::TN + lr) * C::RB;
+    struct Frags {
+        half8 a[C::MI], b[C::NJ];
+    };
+    auto read_frags = [&](int s, int ks, Frags & f) {
+        const uint8_t * st = smem + (s % NS) * C::STAGE;
+        const int co = ((2 * ks + lg) ^ x) * 16;
+#pragma unroll
+        for (int i = 0; i < C::MI; i++) f.a[i] = *(const half8 *)(st + a_off + i * 32 * C::RB + co);
+#pragma unroll
+        for (int j = 0; j < C::NJ; j++) f.b[j] = *(const half8 *)(st + b_off + j * 32 * C::RB + co);
+    };
+    // the MFMAs of one 16-deep K step; `part` 0 = only the first, 1 = all but the first
+    auto mma = [&](const Frags & f, int part) {
+#pragma unroll
+        for (int i = 0; i < C::MI; i++)
+#pragma unroll
+            for (int j = 0; j < C::NJ; j++)
+                if ((part == 0) == (i == 0 && j == 0)) acc[i][j] = mfma32(f.a[i], f.b[j], acc[i][j]);
+    };
+
+    // Software pipeline over the 16-deep K steps of each stage, fragments alternating between f0
+    // and f1: the next step's fragments are read while this step's MFMAs run. At the last step of
+    // a stage: one barrier (the next stage has landed for every wave, and every wave is done
+    // reading this one), the next stage's first fragments, and the DMA of the stage NS ahead
+    // into the buffer just freed.
+    if (nk > 0) {
+        Frags f0, f1;
+#pragma unroll
+        for (int p = 0; p < NS; p++) issue(p);
+        wait_vm_lgkm0<(NS - 1) * C::PER>();
+        __builtin_amdgcn_s_barrier();
+        read_frags(0, 0, f0);
+        constexpr int KS = DK / 16;
+        for (int s = 0; s < nk; s++) {
+#pragma unroll
+            for (int ks = 0; ks < KS; ks++) {
+                Frags & F = (ks % 2 == 0) ? f0 : f1;
+                Frags & G = (ks % 2 == 0) ? f1 : f0;
+                mma(F, 0);
+                __builtin_amdgcn_sched_barrier(0);
+                if (ks + 1 < KS) {
+                    read_frags(s, ks + 1, G);
+                    __builtin_amdgcn_sched_barrier(0);
+                } else {
+                    wait_vm_lgkm0<(NS - 2) * C::PER>();
+                    __builtin_amdgcn_s_barrier();
+                    read_frags(s + 1, 0, G);
+                    __builtin_amdgcn_sched_barrier(0);
+                    issue(s + NS);
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+                mma(F, 1);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        }
+        wait_vm_lgkm0<0>();   // no DMA may still be writing this block's LDS when it exits
+    }
+
+    // epilogue: C = scale[m] * acc
+#pragma unroll
+    for (int i = 0; i < C::MI; i++) {
+#pragma unroll
+        for (int e = 0; e < 16; e++) {
+            const int r = m0 + wm * C::TM + i * 32 + 8 * (e / 4) + 4 * lg + (e % 4);
+            if (r >= M) continue;
+            const float sc = args.scales[r];
+            float * crow = Cp + (int64_t)r * ldc;
+#pragma unroll
+            for (int j = 0; j < C::NJ; j++) {
+                const int n = n0 + wn * C::TN + j * 32 + lr;
+                if (n < N) {
+                    if (KSPLIT == 1) crow[n] = acc[i][j][e] * sc;
+                    else unsafeAtomicAdd(crow + n, acc[i][j][e] * sc);
+                }
+            }
+        }
+    }
+}
+
 // Zero the outputs of a split-K launch (a fill kernel rather than a memset, so the launch
 // sequence stays capturable).
 __global__ void zero_rows_kernel(GemmArgs args) {
@@ -369,15 +585,33 @@ hipError_t launch_pack_act(const float * X, int64_t ldx, int M, int K, uint16_t 
     return hipGetLastError();
 }
 
-// Tile configurations. The launcher picks one per call from the output shape (see choose_cfg);
-// MI355X_GEMM_CFG=<id> forces one (for tuning).
-struct CfgDesc { int bm, bn, ksplit; };
-static const CfgDesc kCfgs[] = {
-    {128, 128, 1},   // 0: 4 waves of 64x64, 3-slab prefetch
-    {128, 128, 2},   // 1: same, K split in two
-    {256, 128, 1},   // 2: 4 waves of 128x64, 2-slab prefetch
-    {128, 256, 1},   // 3: 4 waves of 64x128, 2-slab prefetch
+// Tile configurations. The launcher picks one per call (choose_cfg); MI355X_GEMM_CFG=<id>
+// forces one (for tuning and for the tests, which run every configuration).
+//   0-3  register-staged kernel with the weight decoded into LDS: every weight type.
+//   4-10 LDS-DMA kernel: fp16 weights only. The cost model of choose_cfg times one block as
+//        ov_us + (its MFMA work) / tf_cu: a fixed part (pipeline fill, epilogue, for split-K the
+//        atomics) and a per-CU rate, both fitted to measurements of each configuration at
+//        M = 512 with K = 2048-14336.
+struct CfgDesc {
+    int bm, bn, ksplit;
+    int dk;          // K per LDS stage of the DMA kernel; 0 for the register-staged kernel
+    double tf_cu;    // TFLOP/s per CU
+    double ov_us;    // fixed microseconds per block
 };
+static const CfgDesc kCfgs[] = {
+    {128, 128, 1, 0, 0.0, 0.0},      // 0: 4 waves of 64x64
+    {128, 128, 2, 0, 0.0, 0.0},      // 1: same, K split in two
+    {256, 128, 1, 0, 0.0, 0.0},      // 2: 4 waves of 128x64
+    {128, 256, 1, 0, 0.0, 0.0},      // 3: 4 waves of 64x128
+    {256, 256, 1, 64, 4.2, 0.0},     // 4: 8 waves of 64x128, 2 stages of 64
+    {128, 128, 1, 64, 4.8, 10.0},    // 5: 8 waves of 32x64, 4 stages of 64
+    {64, 128, 1, 128, 2.4, 8.0},     // 6: 4 waves of 32x64, 3 stages of 128
+    {128, 64, 1, 128, 2.4, 8.0},     // 7: 4 waves of 64x32, 3 stages of 128
+    {128, 128, 2, 64, 3.7, 26.0},    // 8: as 5, K split in two
+    {64, 128, 2, 128, 2.56, 17.7},   // 9: as 6, K split in two
+    {128, 128, 1, 32, 4.3, 7.0},     // 10: 8 waves of 32x64, 4 stages of 32 (any K)
+};
+constexpr int FIRST_DMA_CFG = 4;
 constexpr int N_CFGS = sizeof(kCfgs) / sizeof(kCfgs[0]);
 
 template <int WT, int BM, int BN, int WM, int WN, int R, int KS>
@@ -394,8 +628,35 @@ static hipError_t launch_one(const GemmArgs & a, int nblocks, hipStream_t st) {
     return hipGetLastError();
 }
 
+template <int BM, int BN, int WGM, int WGN, int DK, int NS, int KS>
+static hipError_t launch_f16(const GemmArgs & a, int nblocks, hipStream_t st) {
+    using C = F16Cfg<BM, BN, WGM, WGN, DK, NS>;
+    auto kern = gemm_f16_kernel<BM, BN, WGM, WGN, DK, NS, KS>;
+    static bool attr = false;
+    if (!attr) {
+        hipError_t e = hipFuncSetAttribute((const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize, C::LDS);
+        if (e != hipSuccess) return e;
+        attr = true;
+    }
+    hipLaunchKernelGGL(kern, dim3(nblocks), dim3(C::THREADS), C::LDS, st, a);
+    return hipGetLastError();
+}
+
 template <int WT>
 static hipError_t launch_cfg(int cfg, const GemmArgs & a, int nblocks, hipStream_t st) {
+    if (cfg >= FIRST_DMA_CFG) {
+        if (WT != T_F16) return hipErrorInvalidValue;
+        switch (cfg) {
+            case 4: return launch_f16<256, 256, 4, 2, 64, 2, 1>(a, nblocks, st);
+            case 5: return launch_f16<128, 128, 4, 2, 64, 4, 1>(a, nblocks, st);
+            case 6: return launch_f16<64, 128, 2, 2, 128, 3, 1>(a, nblocks, st);
+            case 7: return launch_f16<128, 64, 2, 2, 128, 3, 1>(a, nblocks, st);
+            case 8: return launch_f16<128, 128, 4, 2, 64, 4, 2>(a, nblocks, st);
+            case 9: return launch_f16<64, 128, 2, 2, 128, 3, 2>(a, nblocks, st);
+            case 10: return launch_f16<128, 128, 4, 2, 32, 4, 1>(a, nblocks, st);
+            default: return hipErrorInvalidValue;
+        }
+    }
     switch (cfg) {
         case 0: return launch_one<WT, 128, 128, 2, 2, 2, 1>(a, nblocks, st);
         case 1: return launch_one<WT, 128, 128, 2, 2, 2, 2>(a, nblocks, st);
@@ -421,21 +682,45 @@ static int tiles_of(const GemmArgs & a, int bm, int bn) {
     return nt * ((a.M + bm - 1) / bm);
 }
 
-// Pick the configuration with the best estimated throughput: the fraction of the chip the grid
-// keeps busy over its waves of blocks, times the tile's relative per-CU efficiency (bigger wave
-// tiles read LDS less per MFMA). Split-K only when the unsplit grid leaves most CUs idle.
-static int choose_cfg(const GemmArgs & a) {
+static bool cfg_fits(int c, int wt, int K) {
+    const CfgDesc & d = kCfgs[c];
+    if (d.dk == 0) return true;
+    if (wt != T_F16 || K % d.dk) return false;
+    return d.ksplit == 1 || K / d.dk >= 2;
+}
+
+// fp16 weights: the DMA configuration with the least estimated time. Every block has a CU to
+// itself (their LDS rings take 128-144 KB), so a launch runs in ceil(blocks / CUs) rounds, each
+// as long as one block (ov_us + MFMA work / tf_cu).
+// Other weights: the register-staged configuration with the best grid fill times its tile's
+// relative per-CU efficiency (bigger wave tiles read LDS less per MFMA); split-K only when the
+// unsplit grid leaves most CUs idle.
+static int choose_cfg(int wt, const GemmArgs & a) {
     if (const char * e = getenv("MI355X_GEMM_CFG")) {
         if (*e) {
             const int c = atoi(e);
-            if (c >= 0 && c < N_CFGS) return c;
+            if (c >= 0 && c < N_CFGS && cfg_fits(c, wt, a.K)) return c;
         }
     }
     const int cus = cu_count();
-    const double tile_eff[N_CFGS] = {1.0, 0.97, 1.25, 1.25};
+    if (wt == T_F16) {
+        int best = -1;
+        double best_us = 0.0;
+        for (int c = FIRST_DMA_CFG; c < N_CFGS; c++) {
+            if (!cfg_fits(c, wt, a.K)) continue;
+            const CfgDesc & d = kCfgs[c];
+            const int blocks = tiles_of(a, d.bm, d.bn) * d.ksplit;
+            const int rounds = (blocks + cus - 1) / cus;
+            double us = rounds * (d.ov_us + 2.0 * d.bm * d.bn * ((double)a.K / d.ksplit) / (d.tf_cu * 1e6));
+            if (d.ksplit > 1) us += 3.0;   // the zero fill of the output
+            if (best < 0 || us < best_us - 1e-9) { best = c; best_us = us; }
+        }
+        if (best >= 0) return best;
+    }
+    const double tile_eff[FIRST_DMA_CFG] = {1.0, 0.97, 1.25, 1.25};
     int best = 0;
     double best_score = -1.0;
-    for (int c = 0; c < N_CFGS; c++) {
+    for (int c = 0; c < FIRST_DMA_CFG; c++) {
         if (kCfgs[c].ksplit > 1 && (a.K / BK) < 16) continue;
         const int blocks = tiles_of(a, kCfgs[c].bm, kCfgs[c].bn) * kCfgs[c].ksplit;
         const int waves = (blocks + cus - 1) / cus;
@@ -450,7 +735,7 @@ __global__ void zero_rows_kernel(GemmArgs args);
 
 hipError_t launch_gemm(int wt, const GemmArgs & a_in, int /*unused*/, hipStream_t st) {
     GemmArgs a = a_in;
-    const int cfg = choose_cfg(a);
+    const int cfg = choose_cfg(wt, a);
     const CfgDesc & d = kCfgs[cfg];
     a.m_tiles = (a.M + d.bm - 1) / d.bm;
     int nt = 0;

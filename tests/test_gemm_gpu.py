@@ -186,3 +186,45 @@ def test_gemm_rows_of_a_panel(mx):
         torch.cuda.synchronize()
         ref = O.mul_mat(wtype, Q[2 * N:3 * N], Xf, N, K)
         _assert_bars(ref, c.cpu().numpy(), M, N, f"panel {O.TYPE_NAMES[wtype]}")
+
+
+# Every tile configuration of mi355x_gemm, forced through MI355X_GEMM_CFG, on a ragged fused
+# launch (M and both N not multiples of any tile). Configurations 4-10 are the LDS-DMA kernels,
+# which take fp16 weights only.
+N_GEMM_CFGS = 11
+FIRST_DMA_CFG = 4
+
+
+@pytest.mark.parametrize("cfg", list(range(N_GEMM_CFGS)))
+@pytest.mark.parametrize("wtype", [O.F16, O.Q4_K])
+def test_gemm_every_tile_config(mx, monkeypatch, cfg, wtype):
+    import torch
+    if cfg >= FIRST_DMA_CFG and wtype != O.F16:
+        pytest.skip("the LDS-DMA configurations take fp16 weights only")
+    monkeypatch.setenv("MI355X_GEMM_CFG", str(cfg))
+    K, M, Ns = 1280, 300, (528, 144)
+    Xf = O.fill_normal((M, K), 900 + cfg)
+    a16, sc = mx.pack_act(_dev(Xf))
+    outs, refs = [], []
+    for g, N in enumerate(Ns):
+        W = O.fill_normal((N, K), 910 + g, 0.0, 0.02)
+        payload = O.f32_to_f16_bits(W) if wtype == O.F16 else O.quantize(wtype, W)
+        refs.append(O.mul_mat(wtype, payload, Xf, N, K))
+        w = mx.upload_weight(wtype, payload, N, K)
+        c = torch.full((M, N), float("nan"), dtype=torch.float32, device="cuda")
+        outs.append((w, N, 0, N, c))
+    mx.gemm(wtype, a16, sc, K, outs)
+    torch.cuda.synchronize()
+    for (w, _, _, N, c), ref in zip(outs, refs):
+        _assert_bars(ref, c.cpu().numpy(), M, N, f"cfg {cfg} {O.TYPE_NAMES[wtype]} N={N}")
+
+
+@pytest.mark.parametrize("K", [1312, 96])
+def test_f16_k_not_multiple_of_64(mx, K):
+    """K % 64 != 0: only the 32-deep DMA configuration (or the register-staged kernel) takes it."""
+    N, M = 272, 130
+    W16 = O.f32_to_f16_bits(O.fill_normal((N, K), 930, 0.0, 0.02))
+    Xf = O.fill_normal((M, K), 931)
+    ref = O.mul_mat(O.F16, W16, Xf, N, K)
+    got = _run_mul_mat(mx, O.F16, W16, N, K, Xf)
+    _assert_bars(ref, got, M, N, f"F16 K={K}")
