@@ -172,6 +172,7 @@ static int fa_check(const mi355x_fa_args * a) {
     if (!aligned(a->k_dev, 16) || !aligned(a->v_dev, 16)) return MI355X_E_ARG;
     if (a->dst_nb1 % 4 || a->dst_nb2 % 4 || !aligned(a->dst_dev, 16)) return MI355X_E_ARG;
     if (a->mask_dev && (a->mask_nb1 % 4 || a->mask_nb1 < a->KV || !aligned(a->mask_dev, 8))) return MI355X_E_ARG;
+    if ((size_t)a->KV > mx::fa_max_kv()) return MI355X_E_UNSUPPORTED;
     return MI355X_OK;
 }
 
@@ -183,8 +184,29 @@ static mx::FaArgs fa_lower(const mi355x_fa_args * a, int nsplit) {
     f.v_nb1 = a->v_nb1; f.v_nb2 = a->v_nb2; f.mask_nb1 = a->mask_nb1;
     f.dst_nb1 = a->dst_nb1; f.dst_nb2 = a->dst_nb2;
     f.D = a->D; f.T = a->T; f.H = a->H; f.HK = a->HK; f.KV = a->KV; f.nsplit = nsplit;
+    f.kvp = (int)((a->KV + 63) / 64 * 64);
+    f.cls_stride = (f.kvp / 64 + 15) / 16 * 16;
     f.scale = a->scale; f.softcap = a->softcap;
     return f;
+}
+
+static size_t align256(size_t n) { return (n + 255) & ~(size_t)255; }
+
+// Workspace: V^T [HK][D][KVp] fp16 | mask classes [T/32][cls_stride] | partial O
+// [nsplit][T][H][D] f32 and (max, sum) [nsplit][T][H][2] f32 when nsplit > 1.
+struct FaLayout {
+    size_t vt, cls, po, pml, total;
+};
+static FaLayout fa_layout(const mx::FaArgs & f) {
+    FaLayout L;
+    const size_t nqt = (size_t)(f.T + 31) / 32;
+    const size_t rows = (size_t)f.T * f.H * f.nsplit;
+    L.vt = 0;
+    L.cls = L.vt + align256((size_t)f.HK * f.D * f.kvp * 2);
+    L.po = L.cls + align256(nqt * (size_t)f.cls_stride);
+    L.pml = L.po + (f.nsplit > 1 ? align256(rows * f.D * 4) : 0);
+    L.total = L.pml + (f.nsplit > 1 ? align256(rows * 8) : 0);
+    return L;
 }
 
 MI355X_API int mi355x_flash_attn_auto_split(const mi355x_fa_args * a) {
@@ -199,9 +221,9 @@ MI355X_API int mi355x_flash_attn_auto_split(const mi355x_fa_args * a) {
         cus = (hipGetDevice(&dev) == hipSuccess && hipGetDeviceProperties(&p, dev) == hipSuccess &&
                p.multiProcessorCount > 0) ? p.multiProcessorCount : 256;
     }
-    // fill about two blocks per CU, keeping at least 8 key tiles per split
-    int ns = nb > 0 ? (2 * cus + nb - 1) / nb : 1;
-    const int max_by_len = ntiles / 8 > 0 ? ntiles / 8 : 1;
+    // one block per CU (their LDS rings take 128 KB); fill the chip, at least 4 key tiles a split
+    int ns = nb > 0 ? (cus + nb - 1) / nb : 1;
+    const int max_by_len = ntiles / 4 > 0 ? ntiles / 4 : 1;
     if (ns > max_by_len) ns = max_by_len;
     if (ns > 16) ns = 16;
     return ns < 1 ? 1 : ns;
@@ -210,9 +232,8 @@ MI355X_API int mi355x_flash_attn_auto_split(const mi355x_fa_args * a) {
 MI355X_API size_t mi355x_flash_attn_workspace(const mi355x_fa_args * a, int nsplit) {
     if (fa_check(a) != MI355X_OK) return 0;
     if (nsplit <= 0) nsplit = mi355x_flash_attn_auto_split(a);
-    if (nsplit <= 1) return 0;
-    const size_t rows = (size_t)a->T * a->H * nsplit;
-    return ((rows * a->DV * 4 + 255) & ~(size_t)255) + rows * 8;
+    if (nsplit > 64) return 0;
+    return fa_layout(fa_lower(a, nsplit)).total;
 }
 
 MI355X_API int mi355x_flash_attn(const mi355x_fa_args * a, int nsplit,
@@ -223,12 +244,14 @@ MI355X_API int mi355x_flash_attn(const mi355x_fa_args * a, int nsplit,
     if (nsplit <= 0) nsplit = mi355x_flash_attn_auto_split(a);
     if (nsplit > 64) return MI355X_E_ARG;
     mx::FaArgs f = fa_lower(a, nsplit);
+    const FaLayout L = fa_layout(f);
+    if (!workspace_dev || workspace_bytes < L.total || !aligned(workspace_dev, 256)) return MI355X_E_NOMEM;
+    char * ws = (char *)workspace_dev;
+    f.vt = (uint16_t *)(ws + L.vt);
+    f.cls = (uint8_t *)(ws + L.cls);
     if (nsplit > 1) {
-        const size_t need = mi355x_flash_attn_workspace(a, nsplit);
-        if (!workspace_dev || workspace_bytes < need) return MI355X_E_NOMEM;
-        const size_t rows = (size_t)a->T * a->H * nsplit;
-        f.part_o = (float *)workspace_dev;
-        f.part_ml = (float *)((char *)workspace_dev + ((rows * a->DV * 4 + 255) & ~(size_t)255));
+        f.part_o = (float *)(ws + L.po);
+        f.part_ml = (float *)(ws + L.pml);
     }
     return hip_status(mx::launch_fa(f, S(stream)));
 }

@@ -1,5 +1,6 @@
 // SPDX-License-Identifier: MIT
-// FLASH_ATTN_EXT prefill for gfx950: one fused kernel, online softmax in fp32 registers.
+// FLASH_ATTN_EXT prefill for gfx950: online softmax in fp32 registers, K and V^T streamed into
+// LDS by DMA.
 //
 // Semantics (ggml-rocket.cpp:5444-5691 and its reference rocket_fa_ref_f32, 5392-5442):
 //   O[t,h,:] = softmax_j( cap(scale * q[h,t].k[hk,j]) + mask[t,j] ) . v[hk,j,:],  hk = h / (H/HK)
@@ -10,85 +11,184 @@
 // never leave fp32 registers (there is no fp16 score surface to overflow), P is rounded to fp16
 // for the P.V MFMA, both contractions accumulate in fp32.
 //
-// Work decomposition: a block is 4 waves; each wave owns 32 query rows of one head. The 4 waves
-// of a block share one KV head, so each K/V tile staged in LDS serves all of them (GQA reuse).
-// The scores are computed transposed, S^T = K . Q^T, so each lane owns one query: the row max
-// and row sum need one exchange with the partner lane (l ^ 32) only, and O^T = V^T . P^T keeps
-// the same ownership, so the rescale by exp(m_old - m_new) is lane-local.
-// The KV range may be split across blocks; each split then writes an unnormalised partial O with
-// its (max, sum), and a combine kernel merges them.
+// One op is two launches:
+//   fa_prep   V -> V^T [HK][D][KVp] (keys padded to a multiple of 64 with zeros, and permuted
+//             within each 16-key group so that each lane's P^T operand keys are one 16-byte
+//             chunk, see vt_pos); the mask tile classes (per 32-query x 64-key tile: every key
+//             masked / no key masked / mixed).
+//   fa        a block is 4 waves, each owning 32 query rows of one head, all 4 on one KV head
+//             (GQA reuse of the LDS tiles). Per 64-key tile: K [64][D] and V^T [D][64] arrive
+//             in LDS by global_load_lds (a 4-deep ring, three tiles landing while one is used);
+//             tiles whose mask is -inf for all the block's queries are skipped, tiles with
+//             no mask entry read no mask. Scores are computed transposed, S^T = K . Q^T, so each
+//             lane owns one query: the row max and sum need one exchange with the partner lane
+//             (l ^ 32), and O^T = V^T . P^T keeps the same ownership, so the rescale by
+//             exp(m_old - m_new) is lane-local.
+// The KV range may be split across blocks; every split writes an unnormalised partial O with
+// its (max, sum), and a third launch, fa_combine, merges them.
 
 #include "mx_common.h"
 #include "mx_kernels_impl.h"
 
 namespace mx {
 
-constexpr int FA_BKV = 64;         // keys per LDS tile
-constexpr int FA_QW = 32;          // query rows per wave
+constexpr int FA_BKV = 64;      // keys per tile
+constexpr int FA_QW = 32;       // query rows per wave
 constexpr int FA_WAVES = 4;
-constexpr int FA_VT_STRIDE = 136;  // bytes per V^T row (64 keys * 2 B + 8 B pad)
+constexpr int FA_THREADS = FA_WAVES * WAVE;
+constexpr int FA_NS = 4;        // LDS ring depth
 
 template <int D>
-struct FaSmem {
-    static constexpr int K_BYTES = FA_BKV * D * 2;
-    static constexpr int V_BYTES = D * FA_VT_STRIDE;
+struct FaCfg {
+    static constexpr int KCH = D / 8;                        // 16-byte chunks per K row
+    static constexpr int KRPW = 16 / KCH;                    // K rows per 256-byte bank window
+    static constexpr int K_BYTES = FA_BKV * D * 2;           // [64 keys][D]
+    static constexpr int V_BYTES = D * FA_BKV * 2;           // [D][64 key slots], 128-byte rows
     static constexpr int STAGE = K_BYTES + V_BYTES;
-    static constexpr int TOTAL = 2 * STAGE;
+    static constexpr int LDS = FA_NS * STAGE;
+    static constexpr int PK = K_BYTES / (FA_THREADS * 16);   // DMA instructions per wave
+    static constexpr int PV = V_BYTES / (FA_THREADS * 16);
+    static constexpr int PER = PK + PV;
+    static_assert(PK >= 1 && PV >= 1 && PK * FA_THREADS * 16 == K_BYTES && PV * FA_THREADS * 16 == V_BYTES, "DMA split");
 };
 
-__device__ __forceinline__ float fa_cap(float s, float softcap, float inv_softcap) {
-    return softcap != 0.0f ? softcap * tanhf(s * inv_softcap) : s;
+typedef const void __attribute__((address_space(1))) * fa_gptr_t;
+typedef void __attribute__((address_space(3))) * fa_lptr_t;
+
+__device__ __forceinline__ void fa_dma16(const void * g, void * l) {
+    __builtin_amdgcn_global_load_lds((fa_gptr_t)g, (fa_lptr_t)l, 16, 0, 0);
 }
 
-// Stage keys [j0, j0+64) of K (row-major [key][D]) and V (transposed into [d][key]) into LDS.
+// s_waitcnt with vmcnt(N), expcnt(7) (no wait), lgkmcnt(0): gfx9 encoding.
+template <int N>
+__device__ __forceinline__ void fa_wait_vm_lgkm0() {
+    static_assert(N >= 0 && N <= 63, "vmcnt");
+    __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (0 << 8) | ((N >> 4) << 14));
+}
+
+// Position of key r (0..15) of a 16-key group in V^T. The S^T accumulator gives lane group lg
+// the keys {4lg..4lg+3, 8+4lg..8+4lg+3} of each 16 (the MFMA D layout), so the groups are stored
+// as [0-3 | 8-11 | 4-7 | 12-15]: each lane's 8 keys of a K step are then one 16-byte chunk.
+__device__ __forceinline__ int vt_pos(int r) {
+    const int q = r / 4;
+    return 4 * ((q == 1) ? 2 : (q == 2) ? 1 : q) + (r % 4);
+}
+
+// ---------------------------------------------------------------------------------------------
+// prep: V^T and the mask classes
+// ---------------------------------------------------------------------------------------------
+enum : uint8_t { FA_TILE_SKIP = 0, FA_TILE_FULL = 1, FA_TILE_MIXED = 2 };
+
 template <int D>
-__device__ __forceinline__ void fa_load_kv(const FaArgs & a, int hk, int j0, uint8_t * ks, uint8_t * vt, int t) {
-    constexpr int KCH = D / 8;   // 16-byte chunks per K row
-    const uint16_t * K = a.k + (int64_t)hk * a.k_nb2;
-    const uint16_t * V = a.v + (int64_t)hk * a.v_nb2;
-    // K: 64 rows x KCH chunks
+__global__ void __launch_bounds__(256) fa_prep_kernel(FaArgs a) {
+    __shared__ uint16_t tile[FA_BKV][D + 2];   // +2: row stride 4 bytes off the bank period
+    const int t = threadIdx.x;
+    const int nkt = a.kvp / FA_BKV;
+    const int nvt = a.HK * nkt;
+    const int b = blockIdx.x;
+    if (b < nvt) {
+        // V^T for (hk, key tile)
+        const int hk = b / nkt, j0 = (b % nkt) * FA_BKV;
+        const uint16_t * V = a.v + (int64_t)hk * a.v_nb2;
+        constexpr int CH = D / 8;
 #pragma unroll
-    for (int i = 0; i < (FA_BKV * KCH) / (FA_WAVES * WAVE); i++) {
-        const int c = t + i * FA_WAVES * WAVE;
-        const int r = c / KCH, ch = c % KCH;
-        const int j = j0 + r;
-        u32x4 v = {0, 0, 0, 0};
-        if (j < a.KV) v = *(const u32x4 *)(K + (int64_t)j * a.k_nb1 + ch * 8);
-        *(u32x4 *)(ks + swz<KCH>(r, ch)) = v;
+        for (int i = 0; i < FA_BKV * CH / 256; i++) {
+            const int c = t + i * 256, r = c / CH, ch = c % CH;
+            const int j = j0 + r;
+            u32x4 v = {0, 0, 0, 0};
+            if (j < a.KV) v = *(const u32x4 *)(V + (int64_t)j * a.v_nb1 + 8 * ch);
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                tile[r][8 * ch + 2 * e] = (uint16_t)(v[e] & 0xFFFFu);
+                tile[r][8 * ch + 2 * e + 1] = (uint16_t)(v[e] >> 16);
+            }
+        }
+        __syncthreads();
+        // output: row d, 8 chunks of 8 key slots; slot p holds the key r with vt_pos(r) = p
+        uint16_t * out = a.vt + ((int64_t)hk * D) * a.kvp + j0;
+#pragma unroll
+        for (int i = 0; i < D * 8 / 256; i++) {
+            const int c = t + i * 256, d = c / 8, ch = c % 8;
+            uint32_t w[4];
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                uint32_t pair = 0;
+#pragma unroll
+                for (int h = 0; h < 2; h++) {
+                    const int p = 8 * ch + 2 * e + h;          // slot
+                    const int g16 = p / 16, s16 = p % 16;
+                    const int q = s16 / 4;                     // inverse of vt_pos within 16
+                    const int r = 16 * g16 + 4 * ((q == 1) ? 2 : (q == 2) ? 1 : q) + s16 % 4;
+                    pair |= (uint32_t)tile[r][d] << (16 * h);
+                }
+                w[e] = pair;
+            }
+            *(u32x4 *)(out + (int64_t)d * a.kvp + 8 * ch) = u32x4{w[0], w[1], w[2], w[3]};
+        }
+        return;
     }
-    // V: thread takes 4 keys x 8 dims, writes 8 transposed 4-key runs
-    constexpr int DCH = D / 8;
-    constexpr int ITEMS = 16 * DCH;   // (key group, d chunk) pairs
+    const int nqt = (a.T + FA_QW - 1) / FA_QW;
+    const int nct = nqt * a.cls_stride;   // rows padded to cls_stride entries (padding: skip)
+    const int cb = b - nvt;
+    if (cb * FA_WAVES < nct) {
+        // one wave per (query tile, key tile): lane l scans row l/2, keys 32*(l%2) .. +31
+        const int wave = t / WAVE, lane = t % WAVE;
+        const int ct = cb * FA_WAVES + wave;
+        if (ct >= nct) return;
+        const int qt = ct / a.cls_stride, kt = ct % a.cls_stride;
+        bool vis = false, nz = false;
+        if (kt >= nkt) {
+            vis = false;                              // padding entry
+        } else if (a.mask) {
+            const int tq = qt * FA_QW + lane / 2;
+            const int jb = kt * FA_BKV + 32 * (lane % 2);
+            if (tq < a.T) {
+                const uint16_t * mr = a.mask + (int64_t)tq * a.mask_nb1 + jb;
+                if (jb + 32 <= a.KV) {
+                    // 8 independent 8-byte loads (rows are 8-byte aligned)
+                    u32x2 w[8];
 #pragma unroll
-    for (int i = 0; i < (ITEMS + FA_WAVES * WAVE - 1) / (FA_WAVES * WAVE); i++) {
-        const int it = t + i * FA_WAVES * WAVE;
-        if (it >= ITEMS) break;
-        const int kg = it % 16, dc = it / 16;
-        u32x4 rows[4];
+                    for (int i = 0; i < 8; i++) w[i] = *(const u32x2 *)(mr + 4 * i);
 #pragma unroll
-        for (int r = 0; r < 4; r++) {
-            const int j = j0 + 4 * kg + r;
-            rows[r] = u32x4{0, 0, 0, 0};
-            if (j < a.KV) rows[r] = *(const u32x4 *)(V + (int64_t)j * a.v_nb1 + dc * 8);
+                    for (int i = 0; i < 8; i++)
+#pragma unroll
+                        for (int e = 0; e < 4; e++) {
+                            const float m = h2f_bits((uint16_t)((w[i][e / 2] >> (16 * (e % 2))) & 0xFFFFu));
+                            vis |= (m != -INFINITY);
+                            nz |= (m != 0.0f);
+                        }
+                } else {
+                    for (int j = 0; j < 32; j++) {
+                        if (jb + j < a.KV) {
+                            const float m = h2f_bits(mr[j]);
+                            vis |= (m != -INFINITY);
+                            nz |= (m != 0.0f);
+                        }
+                    }
+                }
+            }
+        } else {
+            vis = true;
         }
-#pragma unroll
-        for (int e = 0; e < 8; e++) {
-            const int w = e / 2, sh = (e % 2) * 16;
-            const uint32_t h0 = (rows[0][w] >> sh) & 0xFFFFu, h1 = (rows[1][w] >> sh) & 0xFFFFu;
-            const uint32_t h2 = (rows[2][w] >> sh) & 0xFFFFu, h3 = (rows[3][w] >> sh) & 0xFFFFu;
-            *(u32x2 *)(vt + (dc * 8 + e) * FA_VT_STRIDE + kg * 8) = u32x2{h0 | (h1 << 16), h2 | (h3 << 16)};
-        }
+        const bool any_vis = __any(vis), any_nz = __any(nz);
+        if (lane == 0) a.cls[ct] = !any_vis ? FA_TILE_SKIP : (any_nz ? FA_TILE_MIXED : FA_TILE_FULL);
+        return;
     }
 }
 
-template <int D>
-__global__ void __launch_bounds__(FA_WAVES * WAVE) fa_kernel(FaArgs a) {
+// ---------------------------------------------------------------------------------------------
+// main kernel
+// ---------------------------------------------------------------------------------------------
+template <int D, bool SOFTCAP>
+__global__ void __launch_bounds__(FA_THREADS) fa_kernel(FaArgs a) {
+    using C = FaCfg<D>;
     extern __shared__ __align__(16) uint8_t smem[];
     constexpr int KSTEPS = D / 16;   // QK contraction steps
-    constexpr int DBLK = D / 32;     // output column blocks of the PV product
+    constexpr int DBLK = D / 32;     // output row blocks of O^T
 
     const int t = threadIdx.x, lane = t % WAVE, wave = t / WAVE;
     const int lq = lane % 32, lg = lane / 32;
+    const int wave_s = __builtin_amdgcn_readfirstlane(wave);
 
     // block -> (kv head, group of 4 wave tasks, kv split)
     const int g = a.H / a.HK;
@@ -97,26 +197,54 @@ __global__ void __launch_bounds__(FA_WAVES * WAVE) fa_kernel(FaArgs a) {
     const int bph = (tasks + FA_WAVES - 1) / FA_WAVES;   // blocks per kv head
     int b = blockIdx.x;
     const int split = b % a.nsplit;
-    b /= a.nsplit;
+    b /= a.nsplit;                                       // the merge group of this block
     const int hk = b / bph;
-    const int task = (b % bph) * FA_WAVES + wave;
+    const int task0 = (b % bph) * FA_WAVES;
+    const int task = task0 + wave;
     const bool active = task < tasks;
     const int h = hk * g + (active ? task % g : 0);
-    const int t0 = (active ? task / g : 0) * FA_QW;
-    const int tq = t0 + lq;               // this lane's query token
+    const int qt = active ? task / g : 0;
+    const int tq = qt * FA_QW + lq;                      // this lane's query token
     const bool qok = active && tq < a.T;
+    const int nkt = a.kvp / FA_BKV;
 
-    // KV range of this split, in whole tiles
-    const int ntiles = (a.KV + FA_BKV - 1) / FA_BKV;
-    const int per = (ntiles + a.nsplit - 1) / a.nsplit;
-    const int tile0 = split * per;
-    const int tile1 = min(ntiles, tile0 + per);
+    // the block's key tiles: the union of its waves' non-skipped ranges (a cooperative scan of
+    // the class rows, 16 entries per load), then this split's share
+    const int qt_first = task0 / g, qt_last = min(tasks - 1, task0 + FA_WAVES - 1) / g;
+    __shared__ int range_lo, range_hi;
+    if (t == 0) { range_lo = nkt; range_hi = 0; }
+    __syncthreads();
+    {
+        const int nchunk = a.cls_stride / 16;
+        const int items = (qt_last - qt_first + 1) * nchunk;
+        int mylo = nkt, myhi = 0;
+        for (int it = t; it < items; it += FA_THREADS) {
+            const int q = qt_first + it / nchunk, c = it % nchunk;
+            const u32x4 w = *(const u32x4 *)(a.cls + (int64_t)q * a.cls_stride + 16 * c);
+            *(u32x4 *)(smem + C::LDS + (q - qt_first) * a.cls_stride + 16 * c) = w;   // kept for the loop
+#pragma unroll
+            for (int e = 0; e < 16; e++)
+                if ((w[e / 4] >> (8 * (e % 4))) & 0xFFu) {
+                    mylo = min(mylo, 16 * c + e);
+                    myhi = max(myhi, 16 * c + e + 1);
+                }
+        }
+        if (mylo < nkt) atomicMin(&range_lo, mylo);
+        if (myhi > 0) atomicMax(&range_hi, myhi);
+    }
+    __syncthreads();
+    const int lo = range_lo, hi = range_hi;
+    const int span = max(0, hi - lo);
+    const int per = (span + a.nsplit - 1) / a.nsplit;
+    const int tile0 = lo + split * per;
+    const int tile1 = min(hi, tile0 + per);
+    const int ntl = max(0, tile1 - tile0);
 
     // ---- Q: scaled, range-guarded, converted to fp16 in the B-operand layout ----
     half8 qf[KSTEPS];
     float qfac = 1.0f;
     {
-        const float * q = a.q + (int64_t)h * a.q_nb2 + (int64_t)tq * a.q_nb1;
+        const float * q = a.q + (int64_t)h * a.q_nb2 + (int64_t)(qok ? tq : 0) * a.q_nb1;
         float amax = 0.0f;
         float qv[KSTEPS][8];
 #pragma unroll
@@ -150,115 +278,191 @@ __global__ void __launch_bounds__(FA_WAVES * WAVE) fa_kernel(FaArgs a) {
 #pragma unroll
         for (int e = 0; e < 16; e++) o[i][e] = 0.0f;
     float m_run = -INFINITY, l_run = 0.0f;
-    const float inv_cap = a.softcap != 0.0f ? 1.0f / a.softcap : 0.0f;
+    const float inv_cap = SOFTCAP ? 1.0f / a.softcap : 0.0f;
+    const bool q_scaled = __any(qfac != 1.0f);   // a row of this wave needed the Q range factor
     const float LOG2E = 1.4426950408889634f;
     const uint16_t * mrow = (a.mask && qok) ? a.mask + (int64_t)tq * a.mask_nb1 : nullptr;
+    // this wave's class row, copied into LDS behind the ring by the range scan above
+    const uint8_t * cls_w = smem + C::LDS + (qt - qt_first) * a.cls_stride;
 
-    if (tile0 < tile1) {
-        fa_load_kv<D>(a, hk, tile0 * FA_BKV, smem, smem + FaSmem<D>::K_BYTES, t);
+    // DMA sources: K rows (keys, clamped to the last key) and V^T rows (dims)
+    const uint16_t * ksrc[C::PK];
+    const uint16_t * vsrc[C::PV];
+#pragma unroll
+    for (int q = 0; q < C::PK; q++) {
+        const int slot = (q * FA_WAVES + wave) * WAVE + lane;
+        const int r = slot / C::KCH, c = (slot % C::KCH) ^ ((r / C::KRPW) & (C::KCH - 1));
+        ksrc[q] = a.k + (int64_t)hk * a.k_nb2 + 8 * c + (int64_t)r * a.k_nb1;   // + j0 * k_nb1 per tile
     }
-    __syncthreads();
-
-    for (int tile = tile0; tile < tile1; tile++) {
-        const int cur = (tile - tile0) & 1;
-        uint8_t * ks = smem + cur * FaSmem<D>::STAGE;
-        uint8_t * vt = ks + FaSmem<D>::K_BYTES;
-        const int j0 = tile * FA_BKV;
-        // stage the next tile into the other buffer while this one is consumed
-        if (tile + 1 < tile1) {
-            uint8_t * ks2 = smem + (cur ^ 1) * FaSmem<D>::STAGE;
-            fa_load_kv<D>(a, hk, j0 + FA_BKV, ks2, ks2 + FaSmem<D>::K_BYTES, t);
+#pragma unroll
+    for (int q = 0; q < C::PV; q++) {
+        const int slot = (q * FA_WAVES + wave) * WAVE + lane;
+        const int r = slot / 8, c = (slot % 8) ^ ((r / 2) & 7);
+        vsrc[q] = a.vt + ((int64_t)hk * D + r) * a.kvp + 8 * c;                  // + j0 per tile
+    }
+    const int kv_last = max(a.KV - 1, 0);
+    // tile i into ring buffer i % FA_NS; past the last tile the last one is fetched again into
+    // the buffer just freed (nobody reads it), so every iteration issues the same DMA count
+    auto issue = [&](int i) {
+        uint8_t * st = smem + (i % FA_NS) * C::STAGE;
+        i = min(i, max(ntl - 1, 0));
+        const int j0 = (tile0 + i) * FA_BKV;
+#pragma unroll
+        for (int q = 0; q < C::PK; q++) {
+            // key row of this lane's chunk: clamp past the last key (masked out below)
+            const int slot = (q * FA_WAVES + wave) * WAVE + lane;
+            const int r = slot / C::KCH;
+            const int64_t jr = (int64_t)min(j0 + r, kv_last) - r;
+            fa_dma16(ksrc[q] + jr * a.k_nb1, st + (q * FA_WAVES + wave_s) * 1024);
         }
-        if (active) {
+#pragma unroll
+        for (int q = 0; q < C::PV; q++) fa_dma16(vsrc[q] + j0, st + C::K_BYTES + (q * FA_WAVES + wave_s) * 1024);
+    };
+
+    const int xk = (lq / C::KRPW) & (C::KCH - 1);   // K row swizzle: rows kb*32 + lq
+    const int xv = (lq / 2) & 7;                    // V^T row swizzle: rows db*32 + lq
+
+    if (ntl > 0) {
+#pragma unroll
+        for (int p = 0; p < FA_NS; p++) issue(p);
+        fa_wait_vm_lgkm0<(FA_NS - 1) * C::PER>();
+        __builtin_amdgcn_s_barrier();
+    }
+    for (int i = 0; i < ntl; i++) {
+        const int tile = tile0 + i;
+        const int j0 = tile * FA_BKV;
+        const uint8_t * ks = smem + (i % FA_NS) * C::STAGE;
+        const uint8_t * vt = ks + C::K_BYTES;
+        // the class is the same in every lane of the wave: read it into an SGPR, so the branch
+        // below is a scalar one
+        const uint32_t cls = __builtin_amdgcn_readfirstlane(active ? (uint32_t)cls_w[tile] : (uint32_t)FA_TILE_SKIP);
+        if (cls != FA_TILE_SKIP) {
             // ---- S^T = K . Q^T for 64 keys: two 32-key blocks ----
-            float16v sacc[2];
+            // All K fragments are read before the first MFMA (one wait instead of one per MFMA),
+            // and the d range is split over two accumulators per key block so that four MFMA
+            // chains are in flight.
+            half8 kf[2][KSTEPS];
 #pragma unroll
-            for (int kb = 0; kb < 2; kb++) {
+            for (int kb = 0; kb < 2; kb++)
 #pragma unroll
-                for (int e = 0; e < 16; e++) sacc[kb][e] = 0.0f;
+                for (int s2 = 0; s2 < KSTEPS; s2++)
+                    kf[kb][s2] = *(const half8 *)(ks + (kb * 32 + lq) * (D * 2) + (((2 * s2 + lg) ^ xk) << 4));
+            __builtin_amdgcn_sched_barrier(0);
+            float16v sacc[2], sacc2[2];
 #pragma unroll
-                for (int s = 0; s < KSTEPS; s++) {
-                    const half8 kf = *(const half8 *)(ks + swz<D / 8>(kb * 32 + lq, 2 * s + lg));
-                    sacc[kb] = mfma32(kf, qf[s], sacc[kb]);
+            for (int kb = 0; kb < 2; kb++)
+#pragma unroll
+                for (int e = 0; e < 16; e++) { sacc[kb][e] = 0.0f; sacc2[kb][e] = 0.0f; }
+#pragma unroll
+            for (int s2 = 0; s2 < KSTEPS; s2 += 2)
+#pragma unroll
+                for (int kb = 0; kb < 2; kb++) {
+                    sacc[kb] = mfma32(kf[kb][s2], qf[s2], sacc[kb]);
+                    sacc2[kb] = mfma32(kf[kb][s2 + 1], qf[s2 + 1], sacc2[kb]);
+                }
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int kb = 0; kb < 2; kb++)
+#pragma unroll
+                for (int e = 0; e < 16; e++) sacc[kb][e] += sacc2[kb][e];
+            // ---- scores: scale back, cap, mask, key bound (each a wave-uniform case) ----
+            if (q_scaled) {
+#pragma unroll
+                for (int kb = 0; kb < 2; kb++)
+#pragma unroll
+                    for (int ii = 0; ii < 16; ii++) sacc[kb][ii] *= qfac;
+            }
+            if (SOFTCAP) {
+#pragma unroll
+                for (int kb = 0; kb < 2; kb++)
+#pragma unroll
+                    for (int ii = 0; ii < 16; ii++) sacc[kb][ii] = a.softcap * tanhf(sacc[kb][ii] * inv_cap);
+            }
+            if (cls == FA_TILE_MIXED) {
+                if (mrow) {
+#pragma unroll
+                    for (int kb = 0; kb < 2; kb++)
+#pragma unroll
+                        for (int q4 = 0; q4 < 4; q4++) {
+                            const int jb = j0 + kb * 32 + 8 * q4 + 4 * lg;   // first of 4 keys
+                            float mk[4];
+                            if (jb + 3 < a.KV) {
+                                const u32x2 mm = *(const u32x2 *)(mrow + jb);
+                                mk[0] = h2f_bits((uint16_t)(mm[0] & 0xFFFFu));
+                                mk[1] = h2f_bits((uint16_t)(mm[0] >> 16));
+                                mk[2] = h2f_bits((uint16_t)(mm[1] & 0xFFFFu));
+                                mk[3] = h2f_bits((uint16_t)(mm[1] >> 16));
+                            } else {
+#pragma unroll
+                                for (int e = 0; e < 4; e++) mk[e] = (jb + e < a.KV) ? h2f_bits(mrow[jb + e]) : 0.0f;
+                            }
+#pragma unroll
+                            for (int e = 0; e < 4; e++) sacc[kb][4 * q4 + e] += mk[e];
+                        }
                 }
             }
-            // ---- scores: scale back, cap, mask, key bound ----
+            if (j0 + FA_BKV > a.KV) {
+#pragma unroll
+                for (int kb = 0; kb < 2; kb++)
+#pragma unroll
+                    for (int ii = 0; ii < 16; ii++)
+                        if (j0 + kb * 32 + 8 * (ii / 4) + 4 * lg + (ii % 4) >= a.KV) sacc[kb][ii] = -INFINITY;
+            }
             float mt = -INFINITY;
 #pragma unroll
-            for (int kb = 0; kb < 2; kb++) {
+            for (int kb = 0; kb < 2; kb++)
 #pragma unroll
-                for (int q4 = 0; q4 < 4; q4++) {
-                    const int jb = j0 + kb * 32 + 8 * q4 + 4 * lg;   // first of 4 keys
-                    float mk[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-                    if (mrow && jb + 3 < a.KV) {
-                        const u32x2 mm = *(const u32x2 *)(mrow + jb);
-                        mk[0] = h2f_bits((uint16_t)(mm[0] & 0xFFFFu));
-                        mk[1] = h2f_bits((uint16_t)(mm[0] >> 16));
-                        mk[2] = h2f_bits((uint16_t)(mm[1] & 0xFFFFu));
-                        mk[3] = h2f_bits((uint16_t)(mm[1] >> 16));
-                    } else if (mrow) {
-#pragma unroll
-                        for (int e = 0; e < 4; e++) mk[e] = (jb + e < a.KV) ? h2f_bits(mrow[jb + e]) : 0.0f;
-                    }
-#pragma unroll
-                    for (int e = 0; e < 4; e++) {
-                        const int i = 4 * q4 + e;
-                        float s = fa_cap(sacc[kb][i] * qfac, a.softcap, inv_cap) + mk[e];
-                        if (jb + e >= a.KV) s = -INFINITY;
-                        sacc[kb][i] = s;
-                        mt = fmaxf(mt, s);
-                    }
-                }
-            }
+                for (int ii = 0; ii < 16; ii++) mt = fmaxf(mt, sacc[kb][ii]);
             mt = fmaxf(mt, __shfl_xor(mt, 32, WAVE));
             const float m_new = fmaxf(m_run, mt);
             // No lane-divergent branch here: the P.V MFMA reads every lane's operands, so a
             // lane whose keys are all masked so far must still supply finite P (zeros).
-            {
-                const float m_use = (m_new == -INFINITY) ? 0.0f : m_new;
-                const float alpha = (m_run == -INFINITY) ? 0.0f : exp2f((m_run - m_use) * LOG2E);
-                const float mb = m_use * LOG2E;
-                float psum = 0.0f;
+            const float m_use = (m_new == -INFINITY) ? 0.0f : m_new;
+            const float alpha = (m_run == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f((m_run - m_use) * LOG2E);
+            const float mb = m_use * LOG2E;
+            float psum = 0.0f;
 #pragma unroll
-                for (int kb = 0; kb < 2; kb++)
+            for (int kb = 0; kb < 2; kb++)
 #pragma unroll
-                    for (int i = 0; i < 16; i++) {
-                        const float p = exp2f(sacc[kb][i] * LOG2E - mb);   // exp(-inf) = 0
-                        sacc[kb][i] = p;
-                        psum += p;
-                    }
-                l_run = l_run * alpha + psum;
-                m_run = m_new;
-#pragma unroll
-                for (int i = 0; i < DBLK; i++)
-#pragma unroll
-                    for (int e = 0; e < 16; e++) o[i][e] *= alpha;
-                // ---- O^T += V^T . P^T, 4 steps of 16 keys ----
-#pragma unroll
-                for (int s = 0; s < 4; s++) {
-                    const int kb = s / 2, hs = s % 2;
-                    half8 pf;
-#pragma unroll
-                    for (int e = 0; e < 8; e++) pf[e] = (_Float16)sacc[kb][8 * hs + e];
-                    const int kofs = (kb * 32 + 16 * hs + 4 * lg) * 2;   // bytes
-#pragma unroll
-                    for (int db = 0; db < DBLK; db++) {
-                        const uint8_t * row = vt + (db * 32 + lq) * FA_VT_STRIDE;
-                        const u32x2 lo = *(const u32x2 *)(row + kofs);
-                        const u32x2 hi = *(const u32x2 *)(row + kofs + 16);
-                        const u32x4 vv = {lo[0], lo[1], hi[0], hi[1]};
-                        o[db] = mfma32(__builtin_bit_cast(half8, vv), pf, o[db]);
-                    }
+                for (int ii = 0; ii < 16; ii++) {
+                    // v_exp_f32: exp2(-inf) = 0; results below the fp32 normal range flush to 0
+                    const float p = __builtin_amdgcn_exp2f(fmaf(sacc[kb][ii], LOG2E, -mb));
+                    sacc[kb][ii] = p;
+                    psum += p;
                 }
+            l_run = l_run * alpha + psum;
+            m_run = m_new;
+            if (__any(alpha != 1.0f)) {   // once the running max settles, most tiles skip this
+#pragma unroll
+                for (int db = 0; db < DBLK; db++)
+#pragma unroll
+                    for (int e = 0; e < 16; e++) o[db][e] *= alpha;
+            }
+            // ---- O^T += V^T . P^T, 4 steps of 16 keys; V^T's key slots follow vt_pos ----
+#pragma unroll
+            for (int s2 = 0; s2 < 4; s2++) {
+                const int kb = s2 / 2, hs = s2 % 2;
+                half8 pf;
+#pragma unroll
+                for (int e = 0; e < 8; e++) pf[e] = (_Float16)sacc[kb][8 * hs + e];
+                half8 vf[DBLK];
+#pragma unroll
+                for (int db = 0; db < DBLK; db++)
+                    vf[db] = *(const half8 *)(vt + (db * 32 + lq) * 128 + (((2 * s2 + lg) ^ xv) << 4));
+#pragma unroll
+                for (int db = 0; db < DBLK; db++) o[db] = mfma32(vf[db], pf, o[db]);
             }
         }
-        __syncthreads();
+        // the next tile has landed for every wave, and every wave is done with this one
+        fa_wait_vm_lgkm0<(FA_NS - 2) * C::PER>();
+        __builtin_amdgcn_s_barrier();
+        issue(i + FA_NS);
     }
+    if (ntl > 0) fa_wait_vm_lgkm0<0>();   // no DMA may still be writing this block's LDS at exit
 
-    if (!qok) return;
-    // ---- epilogue ----
     const float l_tot = l_run + __shfl_xor(l_run, 32, WAVE);
     if (a.nsplit == 1) {
+        if (!qok) return;
         const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
         float * dst = a.dst + (int64_t)tq * a.dst_nb2 + (int64_t)h * a.dst_nb1;
 #pragma unroll
@@ -271,51 +475,61 @@ __global__ void __launch_bounds__(FA_WAVES * WAVE) fa_kernel(FaArgs a) {
                 for (int e = 0; e < 4; e++) v[e] = o[db][4 * q4 + e] * inv;
                 *(float4v *)(dst + d) = v;
             }
-    } else {
-        // partial: O unnormalised [split][T][H][D], (m, l) [split][T][H]
-        const int64_t row = ((int64_t)split * a.T + tq) * a.H + h;
-        float * po = a.part_o + row * D;
+        return;
+    }
+
+    // partial: O unnormalised [split][T][H][D], (m, l) [split][T][H]; fa_combine merges them
+    if (!qok) return;
+    const int64_t rows = (int64_t)a.T * a.H;
+    const int64_t row = (int64_t)split * rows + (int64_t)tq * a.H + h;
+    float * po = a.part_o + row * D;
 #pragma unroll
-        for (int db = 0; db < DBLK; db++)
+    for (int db = 0; db < DBLK; db++)
 #pragma unroll
-            for (int q4 = 0; q4 < 4; q4++) {
-                const int d = db * 32 + 8 * q4 + 4 * lg;
-                float4v v;
+        for (int q4 = 0; q4 < 4; q4++) {
+            const int d = db * 32 + 8 * q4 + 4 * lg;
+            float4v v;
 #pragma unroll
-                for (int e = 0; e < 4; e++) v[e] = o[db][4 * q4 + e];
-                *(float4v *)(po + d) = v;
-            }
-        if (lg == 0) {
-            a.part_ml[2 * row] = m_run;
-            a.part_ml[2 * row + 1] = l_tot;
+            for (int e = 0; e < 4; e++) v[e] = o[db][4 * q4 + e];
+            *(float4v *)(po + d) = v;
         }
+    if (lg == 0) {
+        a.part_ml[2 * row] = m_run;
+        a.part_ml[2 * row + 1] = l_tot;
     }
 }
 
-// Merge nsplit partials: O = sum_s exp(m_s - M) O_s / sum_s exp(m_s - M) l_s. One thread per
-// output element, D threads per (t, h) row.
+// Merge the nsplit partials of every (token, head) row:
+// O = sum_s exp(m_s - M) O_s / sum_s exp(m_s - M) l_s. D/4 threads per row, a float4 each.
 template <int D>
 __global__ void __launch_bounds__(256) fa_combine_kernel(FaArgs a) {
-    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    constexpr int TPR = D / 4;
     const int64_t rows = (int64_t)a.T * a.H;
-    if (i >= rows * D) return;
-    const int64_t r = i / D;
-    const int d = (int)(i % D);
-    const int tq = (int)(r / a.H), h = (int)(r % a.H);
+    const int64_t r = (int64_t)blockIdx.x * (256 / TPR) + threadIdx.x / TPR;
+    if (r >= rows) return;
+    const int c = threadIdx.x % TPR;
     float M = -INFINITY;
     for (int s = 0; s < a.nsplit; s++) M = fmaxf(M, a.part_ml[2 * ((int64_t)s * rows + r)]);
-    float num = 0.0f, den = 0.0f;
+    float4v num = {0, 0, 0, 0};
+    float den = 0.0f;
     if (M != -INFINITY) {
         for (int s = 0; s < a.nsplit; s++) {
             const int64_t pr = (int64_t)s * rows + r;
             const float ms = a.part_ml[2 * pr];
             if (ms == -INFINITY) continue;
             const float w = __expf(ms - M);
-            num += w * a.part_o[pr * D + d];
             den += w * a.part_ml[2 * pr + 1];
+            const float4v v = *(const float4v *)(a.part_o + pr * D + 4 * c);
+#pragma unroll
+            for (int e = 0; e < 4; e++) num[e] += w * v[e];
         }
     }
-    a.dst[(int64_t)tq * a.dst_nb2 + (int64_t)h * a.dst_nb1 + d] = den > 0.0f ? num / den : 0.0f;
+    const float inv = den > 0.0f ? 1.0f / den : 0.0f;
+    const int tq = (int)(r / a.H), h = (int)(r % a.H);
+    float4v out;
+#pragma unroll
+    for (int e = 0; e < 4; e++) out[e] = num[e] * inv;
+    *(float4v *)(a.dst + (int64_t)tq * a.dst_nb2 + (int64_t)h * a.dst_nb1 + 4 * c) = out;
 }
 
 int fa_blocks_per_split(const FaArgs & a) {
@@ -324,22 +538,58 @@ int fa_blocks_per_split(const FaArgs & a) {
     return a.HK * ((g * n_ttiles + FA_WAVES - 1) / FA_WAVES);
 }
 
+int fa_prep_blocks(const FaArgs & a) {
+    const int nkt = a.kvp / FA_BKV;
+    const int nqt = (a.T + FA_QW - 1) / FA_QW;
+    return a.HK * nkt + (nqt * a.cls_stride + FA_WAVES - 1) / FA_WAVES;
+}
+
+// the ring plus the class rows of up to FA_WAVES query tiles
+static size_t fa_lds_bytes(const FaArgs & a) {
+    const size_t ring = a.D == 64 ? FaCfg<64>::LDS : FaCfg<128>::LDS;
+    return ring + (size_t)FA_WAVES * a.cls_stride;
+}
+constexpr int FA_LDS_MAX = 160 * 1024;
+
+size_t fa_max_kv() {
+    // class rows of FA_WAVES query tiles must fit beside the larger ring
+    return (size_t)(FA_LDS_MAX - FaCfg<128>::LDS - 64) / FA_WAVES / 16 * 16 * FA_BKV;
+}
+
+template <int D, bool SC>
+static hipError_t fa_launch_main(const FaArgs & a, int nb, hipStream_t st) {
+    static bool done = false;
+    if (!done) {
+        hipError_t e = hipFuncSetAttribute((const void *)fa_kernel<D, SC>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                           FA_LDS_MAX - 64);
+        if (e != hipSuccess) return e;
+        done = true;
+    }
+    hipLaunchKernelGGL((fa_kernel<D, SC>), dim3(nb), dim3(FA_THREADS), fa_lds_bytes(a), st, a);
+    return hipGetLastError();
+}
+
 hipError_t launch_fa(const FaArgs & a, hipStream_t st) {
     const int nb = fa_blocks_per_split(a) * a.nsplit;
     if (nb <= 0) return hipSuccess;
     switch (a.D) {
         case 64:
-            hipLaunchKernelGGL(fa_kernel<64>, dim3(nb), dim3(FA_WAVES * WAVE), FaSmem<64>::TOTAL, st, a);
+            hipLaunchKernelGGL(fa_prep_kernel<64>, dim3(fa_prep_blocks(a)), dim3(256), 0, st, a);
             break;
         case 128:
-            hipLaunchKernelGGL(fa_kernel<128>, dim3(nb), dim3(FA_WAVES * WAVE), FaSmem<128>::TOTAL, st, a);
+            hipLaunchKernelGGL(fa_prep_kernel<128>, dim3(fa_prep_blocks(a)), dim3(256), 0, st, a);
             break;
         default: return hipErrorInvalidValue;
     }
     hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    const bool sc = a.softcap != 0.0f;
+    if (a.D == 64) e = sc ? fa_launch_main<64, true>(a, nb, st) : fa_launch_main<64, false>(a, nb, st);
+    else e = sc ? fa_launch_main<128, true>(a, nb, st) : fa_launch_main<128, false>(a, nb, st);
     if (e != hipSuccess || a.nsplit == 1) return e;
-    const int64_t n = (int64_t)a.T * a.H * a.D;
-    const dim3 grid((unsigned)((n + 255) / 256));
+    const int64_t rows = (int64_t)a.T * a.H;
+    const int rpb = 256 / (a.D / 4);
+    const dim3 grid((unsigned)((rows + rpb - 1) / rpb));
     if (a.D == 64) hipLaunchKernelGGL(fa_combine_kernel<64>, grid, dim3(256), 0, st, a);
     else hipLaunchKernelGGL(fa_combine_kernel<128>, grid, dim3(256), 0, st, a);
     return hipGetLastError();

@@ -393,9 +393,11 @@ gemm_f16_kernel(GemmArgs args) {
     // the LDS destination of a DMA instruction must be wave-uniform (it goes to M0): take the
     // wave index from an SGPR so the address arithmetic stays scalar
     const int wave_s = __builtin_amdgcn_readfirstlane(wave);
+    // stage s into ring buffer s % NS; past the last stage the last one is fetched again into
+    // the buffer just freed (nobody reads it again)
     auto issue = [&](int s) {
-        s = min(s, nk - 1);
         uint8_t * st = smem + (s % NS) * C::STAGE;
+        s = min(s, nk - 1);
         const int64_t off = (int64_t)s * DK;
 #pragma unroll
         for (int q = 0; q < C::PA; q++) dma16(asrc[q] + off, st + (q * C::NW + wave_s) * 1024);

@@ -123,3 +123,26 @@ def test_fa_baseline_shapes(mx, KV):
     print(f"FA KV={KV}: max abs {r['max_abs']:.3g} range_err {r['range_err']:.3g}")
     assert r["nonfinite"] == 0
     assert r["max_abs"] <= 2e-2 and r["range_err"] <= 1e-2
+
+
+@pytest.mark.parametrize("H,HK", [(3, 3), (6, 3), (8, 2)])
+def test_fa_mask_holes_and_skipped_tiles(mx, H, HK):
+    """A mask with scattered -inf entries, a 128-key band masked for every query (whole key tiles
+    skipped inside the visible range), fully masked rows, and a tail masked for the first query
+    tile only; GQA groups of 1, 2 and 4 (a block's waves on different query tiles when < 4)."""
+    D, T, KV = 64, 96, 640
+    Q = O.fill_normal((H, T, D), 940)
+    K16 = O.f32_to_f16_bits(O.fill_normal((HK, KV, D), 941))
+    V16 = O.f32_to_f16_bits(O.fill_normal((HK, KV, D), 942))
+    rnd = O.fill_uniform((T, KV), 943, 1.0)
+    M = np.where(rnd > 0.4, -np.inf, 0.0).astype(np.float32)
+    M[:, 128:256] = -np.inf
+    M[40:48, :] = -np.inf
+    M[:32, 576:] = -np.inf
+    M16 = O.f32_to_f16_bits(M)
+    want = O.flash_attn(Q, K16, V16, M16, 0.125)
+    for ns in (1, 2, 5):
+        got = _run(mx, Q, K16, V16, M16, 0.125, nsplit=ns)
+        assert np.all(got[40:48] == 0.0), ns
+        r = compare(want, got)
+        assert r["nonfinite"] == 0 and r["max_abs"] <= 2e-2 and r["range_err"] <= 1e-2, (ns, r)
