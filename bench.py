@@ -233,9 +233,9 @@ def cpu_baseline(prefill, threads):
 
 
 def time_ops(pf, reps=20):
-    """Live HIP-event timing of each distinct launch of the step: events bracket `reps`
-    back-to-back launches of the same op on its stream (each launch runs longer than the host
-    needs to enqueue the next, so the events see GPU time, not launch overhead)."""
+    """Live HIP-event timing of each distinct launch of the step: `reps` launches of the same op
+    are captured into a HIP graph, and events on the launch stream bracket replays of it, so the
+    figure is GPU time per launch without host launch overhead (as in the replayed step)."""
     torch = pf.torch
     lw = pf.layers[0]
     sh = pf.shapes
@@ -260,13 +260,25 @@ def time_ops(pf, reps=20):
         for _ in range(3):
             fn()
         torch.cuda.synchronize()
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            fn()
+        torch.cuda.current_stream().wait_stream(side)
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            for _ in range(reps):
+                fn()
+        g.replay()
+        torch.cuda.synchronize()
         s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         s.record()
-        for _ in range(reps):
-            fn()
+        for _ in range(3):
+            g.replay()
         e.record()
         torch.cuda.synchronize()
-        out.append((kind, flops, per_step, s.elapsed_time(e) * 1e-3 / reps))
+        out.append((kind, flops, per_step, s.elapsed_time(e) * 1e-3 / (3 * reps)))
     return out
 
 

@@ -221,9 +221,10 @@ MI355X_API int mi355x_flash_attn_auto_split(const mi355x_fa_args * a) {
         cus = (hipGetDevice(&dev) == hipSuccess && hipGetDeviceProperties(&p, dev) == hipSuccess &&
                p.multiProcessorCount > 0) ? p.multiProcessorCount : 256;
     }
-    // one block per CU (their LDS rings take 128 KB); fill the chip, at least 4 key tiles a split
+    // one block per CU (their LDS rings take 128 KB); fill the chip, but keep at least 12 key
+    // tiles a split: a split costs a partial-output round trip and a combine launch
     int ns = nb > 0 ? (cus + nb - 1) / nb : 1;
-    const int max_by_len = ntiles / 4 > 0 ? ntiles / 4 : 1;
+    const int max_by_len = ntiles / 12 > 0 ? ntiles / 12 : 1;
     if (ns > max_by_len) ns = max_by_len;
     if (ns > 16) ns = 16;
     return ns < 1 ? 1 : ns;

@@ -33,10 +33,12 @@
 namespace mx {
 
 constexpr int FA_BKV = 64;      // keys per tile
-constexpr int FA_QW = 32;       // query rows per wave
-constexpr int FA_WAVES = 4;
+constexpr int FA_QW = 32;       // query rows per wave task
+constexpr int FA_TASKS = 4;     // wave tasks (head, 32-query tile) per block
+constexpr int FA_PAR = 2;       // waves per task, taking alternate key tiles
+constexpr int FA_WAVES = FA_TASKS * FA_PAR;
 constexpr int FA_THREADS = FA_WAVES * WAVE;
-constexpr int FA_NS = 4;        // LDS ring depth
+constexpr int FA_NS = 4;        // LDS ring depth (two tiles consumed per step)
 
 template <int D>
 struct FaCfg {
@@ -130,10 +132,10 @@ __global__ void __launch_bounds__(256) fa_prep_kernel(FaArgs a) {
     const int nqt = (a.T + FA_QW - 1) / FA_QW;
     const int nct = nqt * a.cls_stride;   // rows padded to cls_stride entries (padding: skip)
     const int cb = b - nvt;
-    if (cb * FA_WAVES < nct) {
+    if (cb * 4 < nct) {
         // one wave per (query tile, key tile): lane l scans row l/2, keys 32*(l%2) .. +31
         const int wave = t / WAVE, lane = t % WAVE;
-        const int ct = cb * FA_WAVES + wave;
+        const int ct = cb * 4 + wave;
         if (ct >= nct) return;
         const int qt = ct / a.cls_stride, kt = ct % a.cls_stride;
         bool vis = false, nz = false;
@@ -180,7 +182,8 @@ __global__ void __launch_bounds__(256) fa_prep_kernel(FaArgs a) {
 // main kernel
 // ---------------------------------------------------------------------------------------------
 template <int D, bool SOFTCAP>
-__global__ void __launch_bounds__(FA_THREADS) fa_kernel(FaArgs a) {
+__global__ void __launch_bounds__(FA_THREADS) __attribute__((amdgpu_waves_per_eu(2, 2)))
+fa_kernel(FaArgs a) {
     using C = FaCfg<D>;
     extern __shared__ __align__(16) uint8_t smem[];
     constexpr int KSTEPS = D / 16;   // QK contraction steps
@@ -189,18 +192,19 @@ __global__ void __launch_bounds__(FA_THREADS) fa_kernel(FaArgs a) {
     const int t = threadIdx.x, lane = t % WAVE, wave = t / WAVE;
     const int lq = lane % 32, lg = lane / 32;
     const int wave_s = __builtin_amdgcn_readfirstlane(wave);
+    const int slot_task = wave % FA_TASKS, par = wave / FA_TASKS;
 
-    // block -> (kv head, group of 4 wave tasks, kv split)
+    // block -> (kv head, group of 4 wave tasks, kv split); two waves per task
     const int g = a.H / a.HK;
     const int n_ttiles = (a.T + FA_QW - 1) / FA_QW;
     const int tasks = g * n_ttiles;
-    const int bph = (tasks + FA_WAVES - 1) / FA_WAVES;   // blocks per kv head
+    const int bph = (tasks + FA_TASKS - 1) / FA_TASKS;   // blocks per kv head
     int b = blockIdx.x;
     const int split = b % a.nsplit;
-    b /= a.nsplit;                                       // the merge group of this block
+    b /= a.nsplit;
     const int hk = b / bph;
-    const int task0 = (b % bph) * FA_WAVES;
-    const int task = task0 + wave;
+    const int task0 = (b % bph) * FA_TASKS;
+    const int task = task0 + slot_task;
     const bool active = task < tasks;
     const int h = hk * g + (active ? task % g : 0);
     const int qt = active ? task / g : 0;
@@ -208,9 +212,9 @@ __global__ void __launch_bounds__(FA_THREADS) fa_kernel(FaArgs a) {
     const bool qok = active && tq < a.T;
     const int nkt = a.kvp / FA_BKV;
 
-    // the block's key tiles: the union of its waves' non-skipped ranges (a cooperative scan of
+    // the block's key tiles: the union of its tasks' non-skipped ranges (a cooperative scan of
     // the class rows, 16 entries per load), then this split's share
-    const int qt_first = task0 / g, qt_last = min(tasks - 1, task0 + FA_WAVES - 1) / g;
+    const int qt_first = task0 / g, qt_last = min(tasks - 1, task0 + FA_TASKS - 1) / g;
     __shared__ int range_lo, range_hi;
     if (t == 0) { range_lo = nkt; range_hi = 0; }
     __syncthreads();
@@ -240,6 +244,62 @@ __global__ void __launch_bounds__(FA_THREADS) fa_kernel(FaArgs a) {
     const int tile1 = min(hi, tile0 + per);
     const int ntl = max(0, tile1 - tile0);
 
+    float16v o[DBLK];
+#pragma unroll
+    for (int i = 0; i < DBLK; i++)
+#pragma unroll
+        for (int e = 0; e < 16; e++) o[i][e] = 0.0f;
+    float m_run = -INFINITY, l_run = 0.0f;
+    const float inv_cap = SOFTCAP ? 1.0f / a.softcap : 0.0f;
+    const float LOG2E = 1.4426950408889634f;
+    const uint16_t * mrow = (a.mask && qok) ? a.mask + (int64_t)tq * a.mask_nb1 : nullptr;
+    // this task's class row, copied into LDS behind the ring by the range scan above
+    const uint8_t * cls_w = smem + C::LDS + (qt - qt_first) * a.cls_stride;
+
+    // DMA sources: K rows (keys, clamped to the last key) and V^T rows (dims)
+    const uint16_t * ksrc[C::PK];
+    const uint16_t * vsrc[C::PV];
+#pragma unroll
+    for (int q = 0; q < C::PK; q++) {
+        const int slot = (q * FA_WAVES + wave) * WAVE + lane;
+        const int r = slot / C::KCH, c = (slot % C::KCH) ^ ((r / C::KRPW) & (C::KCH - 1));
+        ksrc[q] = a.k + (int64_t)hk * a.k_nb2 + 8 * c + (int64_t)r * a.k_nb1;   // + j0 * k_nb1 per tile
+    }
+#pragma unroll
+    for (int q = 0; q < C::PV; q++) {
+        const int slot = (q * FA_WAVES + wave) * WAVE + lane;
+        const int r = slot / 8, c = (slot % 8) ^ ((r / 2) & 7);
+        vsrc[q] = a.vt + ((int64_t)hk * D + r) * a.kvp + 8 * c;                  // + j0 per tile
+    }
+    const int kv_last = max(a.KV - 1, 0);
+    // tile i into ring buffer i % FA_NS; past the last tile the last one is fetched again into
+    // the buffer just freed (nobody reads it), so every step issues the same DMA count
+    auto issue = [&](int i) {
+        uint8_t * st = smem + (i % FA_NS) * C::STAGE;
+        i = min(i, max(ntl - 1, 0));
+        const int j0 = (tile0 + i) * FA_BKV;
+#pragma unroll
+        for (int q = 0; q < C::PK; q++) {
+            const int slot = (q * FA_WAVES + wave) * WAVE + lane;
+            const int r = slot / C::KCH;
+            const int64_t jr = (int64_t)min(j0 + r, kv_last) - r;
+            fa_dma16(ksrc[q] + jr * a.k_nb1, st + (q * FA_WAVES + wave_s) * 1024);
+        }
+#pragma unroll
+        for (int q = 0; q < C::PV; q++) fa_dma16(vsrc[q] + j0, st + C::K_BYTES + (q * FA_WAVES + wave_s) * 1024);
+    };
+
+    const int xk = (lq / C::KRPW) & (C::KCH - 1);   // K row swizzle: rows kb*32 + lq
+    const int xv = (lq / 2) & 7;                    // V^T row swizzle: rows db*32 + lq
+
+    // Each step consumes two tiles: parity-0 waves take the even one, parity-1 waves the odd one
+    // (the same query rows), and both land in the ring during the step before.
+    const int nsteps = (ntl + 1) / 2;
+    if (ntl > 0) {
+#pragma unroll
+        for (int p = 0; p < FA_NS; p++) issue(p);
+    }
+    // the Q load runs while the first tiles land
     // ---- Q: scaled, range-guarded, converted to fp16 in the B-operand layout ----
     half8 qf[KSTEPS];
     float qfac = 1.0f;
@@ -272,99 +332,35 @@ __global__ void __launch_bounds__(FA_THREADS) fa_kernel(FaArgs a) {
             for (int e = 0; e < 8; e++) qf[s][e] = (_Float16)(qfac == 1.0f ? qv[s][e] : qv[s][e] * inv);
     }
 
-    float16v o[DBLK];
-#pragma unroll
-    for (int i = 0; i < DBLK; i++)
-#pragma unroll
-        for (int e = 0; e < 16; e++) o[i][e] = 0.0f;
-    float m_run = -INFINITY, l_run = 0.0f;
-    const float inv_cap = SOFTCAP ? 1.0f / a.softcap : 0.0f;
     const bool q_scaled = __any(qfac != 1.0f);   // a row of this wave needed the Q range factor
-    const float LOG2E = 1.4426950408889634f;
-    const uint16_t * mrow = (a.mask && qok) ? a.mask + (int64_t)tq * a.mask_nb1 : nullptr;
-    // this wave's class row, copied into LDS behind the ring by the range scan above
-    const uint8_t * cls_w = smem + C::LDS + (qt - qt_first) * a.cls_stride;
-
-    // DMA sources: K rows (keys, clamped to the last key) and V^T rows (dims)
-    const uint16_t * ksrc[C::PK];
-    const uint16_t * vsrc[C::PV];
-#pragma unroll
-    for (int q = 0; q < C::PK; q++) {
-        const int slot = (q * FA_WAVES + wave) * WAVE + lane;
-        const int r = slot / C::KCH, c = (slot % C::KCH) ^ ((r / C::KRPW) & (C::KCH - 1));
-        ksrc[q] = a.k + (int64_t)hk * a.k_nb2 + 8 * c + (int64_t)r * a.k_nb1;   // + j0 * k_nb1 per tile
-    }
-#pragma unroll
-    for (int q = 0; q < C::PV; q++) {
-        const int slot = (q * FA_WAVES + wave) * WAVE + lane;
-        const int r = slot / 8, c = (slot % 8) ^ ((r / 2) & 7);
-        vsrc[q] = a.vt + ((int64_t)hk * D + r) * a.kvp + 8 * c;                  // + j0 per tile
-    }
-    const int kv_last = max(a.KV - 1, 0);
-    // tile i into ring buffer i % FA_NS; past the last tile the last one is fetched again into
-    // the buffer just freed (nobody reads it), so every iteration issues the same DMA count
-    auto issue = [&](int i) {
-        uint8_t * st = smem + (i % FA_NS) * C::STAGE;
-        i = min(i, max(ntl - 1, 0));
-        const int j0 = (tile0 + i) * FA_BKV;
-#pragma unroll
-        for (int q = 0; q < C::PK; q++) {
-            // key row of this lane's chunk: clamp past the last key (masked out below)
-            const int slot = (q * FA_WAVES + wave) * WAVE + lane;
-            const int r = slot / C::KCH;
-            const int64_t jr = (int64_t)min(j0 + r, kv_last) - r;
-            fa_dma16(ksrc[q] + jr * a.k_nb1, st + (q * FA_WAVES + wave_s) * 1024);
-        }
-#pragma unroll
-        for (int q = 0; q < C::PV; q++) fa_dma16(vsrc[q] + j0, st + C::K_BYTES + (q * FA_WAVES + wave_s) * 1024);
-    };
-
-    const int xk = (lq / C::KRPW) & (C::KCH - 1);   // K row swizzle: rows kb*32 + lq
-    const int xv = (lq / 2) & 7;                    // V^T row swizzle: rows db*32 + lq
-
     if (ntl > 0) {
-#pragma unroll
-        for (int p = 0; p < FA_NS; p++) issue(p);
-        fa_wait_vm_lgkm0<(FA_NS - 1) * C::PER>();
+        fa_wait_vm_lgkm0<2 * C::PER>();
         __builtin_amdgcn_s_barrier();
     }
-    for (int i = 0; i < ntl; i++) {
+    for (int stp = 0; stp < nsteps; stp++) {
+        const int i = 2 * stp + par;                    // this wave's local tile
         const int tile = tile0 + i;
         const int j0 = tile * FA_BKV;
         const uint8_t * ks = smem + (i % FA_NS) * C::STAGE;
         const uint8_t * vt = ks + C::K_BYTES;
         // the class is the same in every lane of the wave: read it into an SGPR, so the branch
         // below is a scalar one
-        const uint32_t cls = __builtin_amdgcn_readfirstlane(active ? (uint32_t)cls_w[tile] : (uint32_t)FA_TILE_SKIP);
+        const uint32_t cls = __builtin_amdgcn_readfirstlane(
+            (active && i < ntl) ? (uint32_t)cls_w[tile] : (uint32_t)FA_TILE_SKIP);
         if (cls != FA_TILE_SKIP) {
             // ---- S^T = K . Q^T for 64 keys: two 32-key blocks ----
-            // All K fragments are read before the first MFMA (one wait instead of one per MFMA),
-            // and the d range is split over two accumulators per key block so that four MFMA
-            // chains are in flight.
-            half8 kf[2][KSTEPS];
+            float16v sacc[2];
 #pragma unroll
-            for (int kb = 0; kb < 2; kb++)
+            for (int kb = 0; kb < 2; kb++) {
+                half8 kf[KSTEPS];
 #pragma unroll
                 for (int s2 = 0; s2 < KSTEPS; s2++)
-                    kf[kb][s2] = *(const half8 *)(ks + (kb * 32 + lq) * (D * 2) + (((2 * s2 + lg) ^ xk) << 4));
-            __builtin_amdgcn_sched_barrier(0);
-            float16v sacc[2], sacc2[2];
+                    kf[s2] = *(const half8 *)(ks + (kb * 32 + lq) * (D * 2) + (((2 * s2 + lg) ^ xk) << 4));
 #pragma unroll
-            for (int kb = 0; kb < 2; kb++)
+                for (int e = 0; e < 16; e++) sacc[kb][e] = 0.0f;
 #pragma unroll
-                for (int e = 0; e < 16; e++) { sacc[kb][e] = 0.0f; sacc2[kb][e] = 0.0f; }
-#pragma unroll
-            for (int s2 = 0; s2 < KSTEPS; s2 += 2)
-#pragma unroll
-                for (int kb = 0; kb < 2; kb++) {
-                    sacc[kb] = mfma32(kf[kb][s2], qf[s2], sacc[kb]);
-                    sacc2[kb] = mfma32(kf[kb][s2 + 1], qf[s2 + 1], sacc2[kb]);
-                }
-            __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-            for (int kb = 0; kb < 2; kb++)
-#pragma unroll
-                for (int e = 0; e < 16; e++) sacc[kb][e] += sacc2[kb][e];
+                for (int s2 = 0; s2 < KSTEPS; s2++) sacc[kb] = mfma32(kf[s2], qf[s2], sacc[kb]);
+            }
             // ---- scores: scale back, cap, mask, key bound (each a wave-uniform case) ----
             if (q_scaled) {
 #pragma unroll
@@ -453,12 +449,41 @@ __global__ void __launch_bounds__(FA_THREADS) fa_kernel(FaArgs a) {
                 for (int db = 0; db < DBLK; db++) o[db] = mfma32(vf[db], pf, o[db]);
             }
         }
-        // the next tile has landed for every wave, and every wave is done with this one
-        fa_wait_vm_lgkm0<(FA_NS - 2) * C::PER>();
+        // the next two tiles have landed for every wave, and every wave is done with these two
+        fa_wait_vm_lgkm0<0>();
         __builtin_amdgcn_s_barrier();
-        issue(i + FA_NS);
+        if (2 * stp + FA_NS < ntl) {   // block-uniform; the wait above counts nothing issued later
+            issue(2 * stp + FA_NS);
+            issue(2 * stp + FA_NS + 1);
+        }
     }
-    if (ntl > 0) fa_wait_vm_lgkm0<0>();   // no DMA may still be writing this block's LDS at exit
+    fa_wait_vm_lgkm0<0>();   // no DMA may still be writing LDS: the merge below reuses the ring
+    __syncthreads();
+
+    // ---- merge each task's two waves (same rows, disjoint key tiles) through LDS ----
+    float * ob = (float *)smem + (size_t)slot_task * (DBLK * 16 + 2) * WAVE;   // [DBLK*16 + 2][64]
+    if (par == 1) {
+#pragma unroll
+        for (int db = 0; db < DBLK; db++)
+#pragma unroll
+            for (int e = 0; e < 16; e++) ob[(db * 16 + e) * WAVE + lane] = o[db][e];
+        ob[(DBLK * 16) * WAVE + lane] = m_run;
+        ob[(DBLK * 16 + 1) * WAVE + lane] = l_run;
+    }
+    __syncthreads();
+    if (par == 1) return;
+    {
+        const float m1 = ob[(DBLK * 16) * WAVE + lane], l1 = ob[(DBLK * 16 + 1) * WAVE + lane];
+        const float M = fmaxf(m_run, m1);
+        const float a0 = (m_run == -INFINITY) ? 0.0f : __expf(m_run - M);
+        const float a1 = (m1 == -INFINITY) ? 0.0f : __expf(m1 - M);
+#pragma unroll
+        for (int db = 0; db < DBLK; db++)
+#pragma unroll
+            for (int e = 0; e < 16; e++) o[db][e] = o[db][e] * a0 + ob[(db * 16 + e) * WAVE + lane] * a1;
+        l_run = l_run * a0 + l1 * a1;
+        m_run = M;
+    }
 
     const float l_tot = l_run + __shfl_xor(l_run, 32, WAVE);
     if (a.nsplit == 1) {
@@ -535,25 +560,25 @@ __global__ void __launch_bounds__(256) fa_combine_kernel(FaArgs a) {
 int fa_blocks_per_split(const FaArgs & a) {
     const int g = a.H / a.HK;
     const int n_ttiles = (a.T + FA_QW - 1) / FA_QW;
-    return a.HK * ((g * n_ttiles + FA_WAVES - 1) / FA_WAVES);
+    return a.HK * ((g * n_ttiles + FA_TASKS - 1) / FA_TASKS);
 }
 
 int fa_prep_blocks(const FaArgs & a) {
     const int nkt = a.kvp / FA_BKV;
     const int nqt = (a.T + FA_QW - 1) / FA_QW;
-    return a.HK * nkt + (nqt * a.cls_stride + FA_WAVES - 1) / FA_WAVES;
+    return a.HK * nkt + (nqt * a.cls_stride + 3) / 4;
 }
 
-// the ring plus the class rows of up to FA_WAVES query tiles
+// the ring plus the class rows of up to FA_TASKS query tiles
 static size_t fa_lds_bytes(const FaArgs & a) {
     const size_t ring = a.D == 64 ? FaCfg<64>::LDS : FaCfg<128>::LDS;
-    return ring + (size_t)FA_WAVES * a.cls_stride;
+    return ring + (size_t)FA_TASKS * a.cls_stride;
 }
 constexpr int FA_LDS_MAX = 160 * 1024;
 
 size_t fa_max_kv() {
-    // class rows of FA_WAVES query tiles must fit beside the larger ring
-    return (size_t)(FA_LDS_MAX - FaCfg<128>::LDS - 64) / FA_WAVES / 16 * 16 * FA_BKV;
+    // class rows of FA_TASKS query tiles must fit beside the larger ring
+    return (size_t)(FA_LDS_MAX - FaCfg<128>::LDS - 64) / FA_TASKS / 16 * 16 * FA_BKV;
 }
 
 template <int D, bool SC>
