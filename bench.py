@@ -66,7 +66,7 @@ class Prefill:
         from oracle import oracle as O
         self.mx, self.torch, self.np = mx, torch, np
         self.route = route
-        self.wt = mx.F16 if route == "prepacked-q" else mx.Q4_K
+        self.wt = mx.F16_T if route == "prepacked-q" else mx.Q4_K
         dev = "cuda"
         t0 = time.time()
         shapes = {"q": (D_MODEL, D_MODEL), "k": (NKV * HD, D_MODEL), "v": (NKV * HD, D_MODEL),
@@ -93,8 +93,8 @@ class Prefill:
                     blk = q.view(-1, 144)
                     blk[:, 16:] = torch.randint(0, 256, (blk.shape[0], 128), dtype=torch.uint8, device=dev,
                                                 generator=g)
-                if self.wt == mx.F16:
-                    lw[name] = mx.dequant_f16(mx.Q4_K, q, N, K).view(torch.uint8).reshape(-1)
+                if self.wt == mx.F16_T:
+                    lw[name] = mx.tile_f16(mx.Q4_K, q, N, K)
                     del q
                 else:
                     lw[name] = q
@@ -142,11 +142,10 @@ class Prefill:
         self.timing.append((kind, s, e))
 
     def _pack(self, x, K):
-        a16 = self.a16[:, :K]
-        self._ev("pack", lambda: self.mx.check(self.mx.lib().mi355x_pack_act(
+        fn = self.mx.lib().mi355x_pack_act_tiled if self.wt == self.mx.F16_T else self.mx.lib().mi355x_pack_act
+        self._ev("pack", lambda: self.mx.check(fn(
             self.mx._ptr(x), x.stride(0), x.shape[0], K, self.mx._ptr(self.a16),
             self.mx._ptr(self.scales), self.mx.stream_handle()), "pack"))
-        return a16
 
     def _gemm(self, K, outs, flops):
         mx = self.mx
@@ -232,44 +231,47 @@ def cpu_baseline(prefill, threads):
                       f"scaled x{L_LAYERS} layers"}
 
 
-def time_ops(pf, reps=20):
+def time_ops(pf, reps=32):
     """Live HIP-event timing of each distinct launch of the step: `reps` launches of the same op
     are captured into a HIP graph, and events on the launch stream bracket replays of it, so the
-    figure is GPU time per launch without host launch overhead (as in the replayed step)."""
+    figure is GPU time per launch without host launch overhead (as in the replayed step). The
+    GEMM launches cycle through the layers' weights, as the step does, so no launch finds its
+    weight panel still cached by the one before."""
     torch = pf.torch
-    lw = pf.layers[0]
     sh = pf.shapes
     M = UBATCH
+    L = len(pf.layers)
+    lw = lambda i: pf.layers[i % L]
     ops = [
-        ("pack", 0.0, 4 * L_LAYERS * 4, lambda: pf._pack(pf.x, D_MODEL)),
+        ("pack", 0.0, 4 * L_LAYERS * 4, lambda i: pf._pack(pf.x, D_MODEL)),
         ("gemm", 2.0 * M * D_MODEL * (D_MODEL + 2 * NKV * HD), L_LAYERS * 4,
-         lambda: pf._gemm(D_MODEL, [(lw["q"], sh["q"][0], pf.qo), (lw["k"], sh["k"][0], pf.ko),
-                                    (lw["v"], sh["v"][0], pf.vo)], 0.0)),
+         lambda i: pf._gemm(D_MODEL, [(lw(i)["q"], sh["q"][0], pf.qo), (lw(i)["k"], sh["k"][0], pf.ko),
+                                      (lw(i)["v"], sh["v"][0], pf.vo)], 0.0)),
         ("gemm", 2.0 * M * D_MODEL * D_MODEL, L_LAYERS * 4,
-         lambda: pf._gemm(D_MODEL, [(lw["o"], D_MODEL, pf.oo)], 0.0)),
+         lambda i: pf._gemm(D_MODEL, [(lw(i)["o"], D_MODEL, pf.oo)], 0.0)),
         ("gemm", 2.0 * M * D_MODEL * 2 * FFN, L_LAYERS * 4,
-         lambda: pf._gemm(D_MODEL, [(lw["gate"], FFN, pf.go), (lw["up"], FFN, pf.uo)], 0.0)),
+         lambda i: pf._gemm(D_MODEL, [(lw(i)["gate"], FFN, pf.go), (lw(i)["up"], FFN, pf.uo)], 0.0)),
         ("gemm", 2.0 * M * FFN * D_MODEL, L_LAYERS * 4,
-         lambda: pf._gemm(FFN, [(lw["down"], D_MODEL, pf.do)], 0.0)),
+         lambda i: pf._gemm(FFN, [(lw(i)["down"], D_MODEL, pf.do)], 0.0)),
     ]
     for u in range(TOKENS // UBATCH):
-        ops.append(("fa", 4.0 * NH * UBATCH * UBATCH * (u + 1) * HD, L_LAYERS, (lambda uu=u: pf._fa(uu))))
+        ops.append(("fa", 4.0 * NH * UBATCH * UBATCH * (u + 1) * HD, L_LAYERS, (lambda i, uu=u: pf._fa(uu))))
     pf.reset_counters(False)
     out = []
     for kind, flops, per_step, fn in ops:
-        for _ in range(3):
-            fn()
+        for i in range(3):
+            fn(i)
         torch.cuda.synchronize()
         side = torch.cuda.Stream()
         side.wait_stream(torch.cuda.current_stream())
         with torch.cuda.stream(side):
-            fn()
+            fn(0)
         torch.cuda.current_stream().wait_stream(side)
         torch.cuda.synchronize()
         g = torch.cuda.CUDAGraph()
         with torch.cuda.graph(g):
-            for _ in range(reps):
-                fn()
+            for i in range(reps):
+                fn(i)
         g.replay()
         torch.cuda.synchronize()
         s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)

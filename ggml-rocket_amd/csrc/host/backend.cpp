@@ -105,7 +105,7 @@ struct DevBuf {
 struct WEntry {
     void * dev = nullptr;
     size_t bytes = 0;
-    int dev_type = 0;   // layout the kernels read: F16, Q8_0, Q4_K or Q6_K
+    int dev_type = 0;   // layout the kernels read: F16, F16_T, Q8_0, Q4_K or Q6_K
     int64_t rows = 0, K = 0;
 };
 
@@ -181,44 +181,52 @@ int d2h(Ctx * c, void * dst, const void * src, size_t n) {
 
 #define TRY(x) do { const int _rc = (x); if (_rc != MI355X_OK) return _rc; } while (0)
 
-// The device layout a weight of ggml type `t` is read in (F32/BF16 become fp16; fp16 when the
-// resident-fp16 form is asked for).
-int dev_layout(int t, bool want_f16) {
-    if (want_f16 || t == MI355X_TYPE_F16 || t == MI355X_TYPE_F32 || t == MI355X_TYPE_BF16) return MI355X_F16;
+// The device layout a weight of ggml type `t` is read in: fp16 for F16 / F32 / BF16 weights and
+// for quantized ones when the resident-fp16 form is asked for, the quantized HBM layout
+// otherwise. The fp16 form is the tiled one (MI355X_F16_T, the GEMM's fastest input) when the
+// caller reads it through mi355x_gemm (`tiled_ok`) and K % 64 == 0; row-major otherwise (the
+// expert kernel of MUL_MAT_ID reads rows).
+int dev_layout(int t, bool want_f16, bool tiled_ok, int64_t K) {
+    if (want_f16 || t == MI355X_TYPE_F16 || t == MI355X_TYPE_F32 || t == MI355X_TYPE_BF16)
+        return (tiled_ok && K % 64 == 0) ? MI355X_F16_T : MI355X_F16;
     return t;   // Q8_0, Q4_K, Q6_K
 }
 
-// Builds the device form of `rows` rows of K values of ggml type `t` (host bytes `src`) at
-// `dst` (capacity `dst_bytes`). Uses wstage / wconv as staging.
-int build_weight(Ctx * c, int t, const void * src, int64_t rows, int64_t K, bool want_f16, void * dst) {
+// Builds the device form `lay` of `rows` rows of K values of ggml type `t` (host bytes `src`) at
+// `dst`. Uses wstage / wconv as staging.
+int build_weight(Ctx * c, int t, const void * src, int64_t rows, int64_t K, int lay, void * dst) {
     const size_t raw = (size_t)row_bytes(t, K) * (size_t)rows;
-    const int lay = dev_layout(t, want_f16);
     if ((t == MI355X_TYPE_F16 || t == MI355X_TYPE_Q4_K) && lay == t) return h2d(c, dst, src, raw);
     TRY(c->wstage.ensure(raw));
     TRY(h2d(c, c->wstage.p, src, raw));
-    if (t == MI355X_TYPE_F32 || t == MI355X_TYPE_BF16)
-        return mi355x_convert_f16(t, c->wstage.p, rows * K, (uint16_t *)dst, c->stream);
-    if (lay != MI355X_F16) return mi355x_weight_pack(t, c->wstage.p, rows, K, dst, c->stream);
-    // quantized -> resident fp16: into the HBM layout first when that differs from the ggml one
+    if (t == MI355X_TYPE_F32 || t == MI355X_TYPE_BF16) {
+        if (lay == MI355X_F16) return mi355x_convert_f16(t, c->wstage.p, rows * K, (uint16_t *)dst, c->stream);
+        TRY(c->wconv.ensure((size_t)rows * K * 2));
+        TRY(mi355x_convert_f16(t, c->wstage.p, rows * K, (uint16_t *)c->wconv.p, c->stream));
+        return mi355x_weight_f16_tiled(MI355X_F16, c->wconv.p, rows, K, (uint16_t *)dst, c->stream);
+    }
+    if (lay != MI355X_F16 && lay != MI355X_F16_T) return mi355x_weight_pack(t, c->wstage.p, rows, K, dst, c->stream);
+    // -> fp16: from the HBM layout, built first when that differs from the ggml one
     const void * q = c->wstage.p;
     if (t == MI355X_TYPE_Q8_0 || t == MI355X_TYPE_Q6_K) {
         TRY(c->wconv.ensure(raw));
         TRY(mi355x_weight_pack(t, c->wstage.p, rows, K, c->wconv.p, c->stream));
         q = c->wconv.p;
     }
+    if (lay == MI355X_F16_T) return mi355x_weight_f16_tiled(t, q, rows, K, (uint16_t *)dst, c->stream);
     return mi355x_weight_dequant_f16(t, q, rows, K, (uint16_t *)dst, c->stream);
 }
 
 // A weight in device form: from the cache, or built into it, or (no key / over budget) built
 // into per-call scratch. `resident` tells which.
-int get_weight(Ctx * c, const mi355x_tensor * a, int64_t rows, int64_t K, bool want_f16, DevBuf & scratch,
-               WEntry & out, bool & resident) {
-    const int lay = dev_layout(a->type, want_f16);
+int get_weight(Ctx * c, const mi355x_tensor * a, int64_t rows, int64_t K, bool want_f16, bool tiled_ok,
+               DevBuf & scratch, WEntry & out, bool & resident) {
+    const int lay = dev_layout(a->type, want_f16, tiled_ok, K);
     const int64_t dbytes = mi355x_weight_bytes(lay, rows, K);
     if (dbytes < 0) return MI355X_E_ARG;
     std::string key = weight_key(a);
     if (!key.empty()) {
-        key += want_f16 ? "|f16" : "|dev";
+        key += "|L" + std::to_string(lay);
         auto it = c->wcache.find(key);
         if (it != c->wcache.end() && it->second.rows == rows && it->second.K == K && it->second.dev_type == lay) {
             out = it->second;
@@ -228,7 +236,7 @@ int get_weight(Ctx * c, const mi355x_tensor * a, int64_t rows, int64_t K, bool w
         if (c->cache_used + (size_t)dbytes <= c->cache_budget) {
             void * p = nullptr;
             if (hipMalloc(&p, (size_t)dbytes) == hipSuccess) {
-                const int rc = build_weight(c, a->type, a->data, rows, K, want_f16, p);
+                const int rc = build_weight(c, a->type, a->data, rows, K, lay, p);
                 if (rc != MI355X_OK) {
                     (void)hipFree(p);
                     return rc;
@@ -249,7 +257,7 @@ int get_weight(Ctx * c, const mi355x_tensor * a, int64_t rows, int64_t K, bool w
         }
     }
     TRY(scratch.ensure((size_t)dbytes));
-    TRY(build_weight(c, a->type, a->data, rows, K, want_f16, scratch.p));
+    TRY(build_weight(c, a->type, a->data, rows, K, lay, scratch.p));
     out.dev = scratch.p;
     out.bytes = (size_t)dbytes;
     out.dev_type = lay;
@@ -265,13 +273,11 @@ int mul_mat_device(Ctx * c, const std::vector<mi355x_tensor *> & grp, bool want_
     const mi355x_tensor * b = grp[0]->src[1];
     const int64_t K = b->ne[0], M = b->ne[1] * b->ne[2] * b->ne[3];
     TRY(c->act.ensure((size_t)M * K * 4));
-    TRY(c->a16.ensure((size_t)M * K * 2));
+    TRY(c->a16.ensure((size_t)((M + 15) / 16 * 16) * K * 2));
     TRY(c->scales.ensure((size_t)M * 4));
     int64_t ntot = 0;
     for (auto * d : grp) ntot += d->src[0]->ne[1];
     TRY(c->out.ensure((size_t)M * ntot * 4));
-    TRY(h2d(c, c->act.p, b->data, (size_t)M * K * 4));
-    TRY(mi355x_pack_act((const float *)c->act.p, K, M, K, (uint16_t *)c->a16.p, (float *)c->scales.p, c->stream));
     std::vector<WEntry> ws(grp.size());
     all_resident = true;
     mi355x_gemm_out outs[4];
@@ -279,7 +285,7 @@ int mul_mat_device(Ctx * c, const std::vector<mi355x_tensor *> & grp, bool want_
     for (size_t i = 0; i < grp.size(); i++) {
         const mi355x_tensor * a = grp[i]->src[0];
         bool res = false;
-        TRY(get_weight(c, a, a->ne[1], K, want_f16, c->wscratch[i], ws[i], res));
+        TRY(get_weight(c, a, a->ne[1], K, want_f16, true, c->wscratch[i], ws[i], res));
         all_resident = all_resident && res;
         outs[i].w_dev = ws[i].dev;
         outs[i].rows_total = a->ne[1];
@@ -289,6 +295,12 @@ int mul_mat_device(Ctx * c, const std::vector<mi355x_tensor *> & grp, bool want_
         outs[i].ldc = ntot;
         col += a->ne[1];
     }
+    TRY(h2d(c, c->act.p, b->data, (size_t)M * K * 4));
+    if (ws[0].dev_type == MI355X_F16_T)
+        TRY(mi355x_pack_act_tiled((const float *)c->act.p, K, M, K, (uint16_t *)c->a16.p, (float *)c->scales.p,
+                                  c->stream));
+    else
+        TRY(mi355x_pack_act((const float *)c->act.p, K, M, K, (uint16_t *)c->a16.p, (float *)c->scales.p, c->stream));
     TRY(mi355x_gemm(ws[0].dev_type, (const uint16_t *)c->a16.p, (const float *)c->scales.p, M, K, outs, (int)grp.size(),
                     c->stream));
     // dst[i] is [N_i, M] contiguous: copy its column block row by row
@@ -368,7 +380,7 @@ int mul_mat_id_device(Ctx * c, mi355x_tensor * dst, bool & resident) {
     panel.ne[1] = N * E;
     panel.ne[2] = 1;
     WEntry w;
-    TRY(get_weight(c, &panel, N * E, K, false, c->moe_wscratch, w, resident));
+    TRY(get_weight(c, &panel, N * E, K, false, false, c->moe_wscratch, w, resident));
     const size_t bb = (size_t)T * ne11 * K * 4, ib = (size_t)T * U * 4, ob = (size_t)T * U * N * 4;
     TRY(c->moe_b.ensure(bb));
     TRY(c->moe_ids.ensure(ib));

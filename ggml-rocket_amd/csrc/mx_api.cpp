@@ -67,6 +67,7 @@ MI355X_API int mi355x_get_device_info(mi355x_device_info * out) {
 }
 
 MI355X_API int64_t mi355x_weight_bytes(int wtype, int64_t rows, int64_t K) {
+    if (wtype == mx::T_F16T) return (rows < 0 || K <= 0 || K % 32) ? -1 : mx::packed_weight_bytes(wtype, rows, K);
     if (!known_wtype(wtype) || rows < 0 || K <= 0 || K % blck(wtype)) return -1;
     return mx::packed_weight_bytes(wtype, rows, K);
 }
@@ -88,6 +89,15 @@ MI355X_API int mi355x_weight_dequant_f16(int wtype, const void * w_dev, int64_t 
     return hip_status(mx::launch_dequant_f16(wtype, w_dev, rows, K, out_dev, S(stream)));
 }
 
+MI355X_API int mi355x_weight_f16_tiled(int wtype, const void * w_dev, int64_t rows, int64_t K,
+                                       uint16_t * out_dev, void * stream) {
+    if (!known_wtype(wtype) || rows < 0 || K <= 0 || K % blck(wtype) || K % 64) return MI355X_E_ARG;
+    if (rows == 0) return MI355X_OK;
+    if (!w_dev || !out_dev || !aligned(w_dev, 16) || !aligned(out_dev, 16) || w_dev == (const void *)out_dev)
+        return MI355X_E_ARG;
+    return hip_status(mx::launch_f16_tiled(wtype, w_dev, rows, K, out_dev, S(stream)));
+}
+
 MI355X_API int mi355x_convert_f16(int type, const void * src_dev, int64_t n, uint16_t * dst_dev, void * stream) {
     if ((type != mx::T_F32 && type != mx::T_BF16) || n < 0) return MI355X_E_ARG;
     if (n == 0) return MI355X_OK;
@@ -103,10 +113,20 @@ MI355X_API int mi355x_pack_act(const float * x_dev, int64_t ldx, int64_t M, int6
     return hip_status(mx::launch_pack_act(x_dev, ldx, (int)M, (int)K, a16_dev, K, scales_dev, S(stream)));
 }
 
+MI355X_API int mi355x_pack_act_tiled(const float * x_dev, int64_t ldx, int64_t M, int64_t K,
+                                     uint16_t * a16_dev, float * scales_dev, void * stream) {
+    if (M < 0 || K <= 0 || K % 32 || ldx < K || ldx % 4 || M > INT32_MAX - 15 || K > INT32_MAX) return MI355X_E_ARG;
+    if (M == 0) return MI355X_OK;
+    if (!x_dev || !a16_dev || !scales_dev || !aligned(x_dev, 16) || !aligned(a16_dev, 8)) return MI355X_E_ARG;
+    return hip_status(mx::launch_pack_act_tiled(x_dev, ldx, (int)M, (int)K, a16_dev, scales_dev, S(stream)));
+}
+
 MI355X_API int mi355x_gemm(int wtype, const uint16_t * a16_dev, const float * scales_dev,
                            int64_t M, int64_t K, const mi355x_gemm_out * outs, int n_out,
                            void * stream) {
-    if (!known_wtype(wtype) || M < 0 || K <= 0 || K % 32 || K % blck(wtype) || M > INT32_MAX || K > INT32_MAX)
+    const bool tiled = wtype == mx::T_F16T;
+    if ((!known_wtype(wtype) && !tiled) || M < 0 || K <= 0 || K % 32 || K % blck(wtype) || M > INT32_MAX ||
+        K > INT32_MAX)
         return MI355X_E_ARG;
     if (n_out < 1 || n_out > mx::GEMM_MAX_GROUPS || !outs) return MI355X_E_ARG;
     if (M == 0) return MI355X_OK;
@@ -138,10 +158,14 @@ MI355X_API int mi355x_gemm(int wtype, const uint16_t * a16_dev, const float * sc
     return hip_status(mx::launch_gemm(wtype, a, nt, S(stream)));
 }
 
+// M rows rounded up to 16: the tiled layout's padding (the row-major pack uses M rows of it).
+static size_t mul_mat_a16_bytes(int64_t M, int64_t K) {
+    return ((size_t)((M + 15) / 16 * 16) * (size_t)K * 2 + 255) & ~(size_t)255;
+}
+
 MI355X_API size_t mi355x_mul_mat_workspace(int64_t M, int64_t K) {
     if (M <= 0 || K <= 0) return 0;
-    const size_t a16 = ((size_t)M * (size_t)K * 2 + 255) & ~(size_t)255;
-    return a16 + (size_t)M * 4;
+    return mul_mat_a16_bytes(M, K) + (size_t)M * 4;
 }
 
 MI355X_API int mi355x_mul_mat(int wtype, const void * w_dev, int64_t N, int64_t K,
@@ -153,8 +177,9 @@ MI355X_API int mi355x_mul_mat(int wtype, const void * w_dev, int64_t N, int64_t 
     if (need == 0) return MI355X_E_ARG;
     if (!workspace_dev || workspace_bytes < need) return MI355X_E_NOMEM;
     uint16_t * a16 = (uint16_t *)workspace_dev;
-    float * scales = (float *)((char *)workspace_dev + (((size_t)M * (size_t)K * 2 + 255) & ~(size_t)255));
-    int st = mi355x_pack_act(x_dev, ldx, M, K, a16, scales, stream);
+    float * scales = (float *)((char *)workspace_dev + mul_mat_a16_bytes(M, K));
+    int st = wtype == mx::T_F16T ? mi355x_pack_act_tiled(x_dev, ldx, M, K, a16, scales, stream)
+                                 : mi355x_pack_act(x_dev, ldx, M, K, a16, scales, stream);
     if (st != MI355X_OK) return st;
     mi355x_gemm_out o = {w_dev, N, 0, N, dst_dev, ldd};
     return mi355x_gemm(wtype, a16, scales, M, K, &o, 1, stream);

@@ -18,8 +18,20 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 constexpr int WAVE = 64;
 
-// ggml type ids (ggml.h enum ggml_type) for the weight formats this path decodes.
-enum : int { T_F32 = 0, T_F16 = 1, T_Q8_0 = 8, T_Q4_K = 12, T_Q6_K = 14, T_I32 = 26, T_BF16 = 30 };
+// ggml type ids (ggml.h enum ggml_type) for the weight formats this path decodes, and T_F16T,
+// this library's own tiled fp16 layout (tiled_index below), which is no ggml type.
+enum : int { T_F32 = 0, T_F16 = 1, T_Q8_0 = 8, T_Q4_K = 12, T_Q6_K = 14, T_I32 = 26, T_BF16 = 30, T_F16T = 0x101 };
+
+// The tiled fp16 layout of a [rows][K] matrix (K % 32 == 0): 16 x 32 tiles of 1 KB, row-major
+// inside, tile (row / 16, k / 32) at ((row / 16) * (K / 32) + k / 32) * 512 values; rows padded to
+// a multiple of 16 (the padding is never read). One 64-lane, 16-byte-per-lane load reads one
+// tile: 1 KB of consecutive bytes, whatever K-slab width the reader stages, and each 16-row
+// block of a matrix is one sequential run along K.
+__host__ __device__ inline int64_t tiled_rows(int64_t rows) { return (rows + 15) & ~(int64_t)15; }
+
+__host__ __device__ inline int64_t tiled_index(int64_t row, int64_t k, int64_t K) {
+    return ((((row >> 4) * (K >> 5)) + (k >> 5)) << 9) + ((row & 15) << 5) + (k & 31);
+}
 
 // D(32x32, f32) += A(32x16, f16) . B(16x32, f16). Lane l holds A row (l % 32) and B column
 // (l % 32), K slots 8*(l/32)+0..7. D: lane l, element i -> row 8*(i/4) + 4*(l/32) + (i%4),
@@ -51,9 +63,29 @@ __device__ __forceinline__ uint32_t pack2h(float a, float b) {
 }
 
 // Separately rounded multiply and subtract: the decoders must not fuse d*q - m into one FMA,
-// because the CPU dequantizer rounds the product before the subtraction.
-__device__ __forceinline__ float mul_rn(float a, float b) { return __fmul_rn(a, b); }
-__device__ __forceinline__ float sub_rn(float a, float b) { return __fsub_rn(a, b); }
+// because the CPU dequantizer rounds the product before the subtraction, and a result that is
+// then converted to fp16 must not be folded into the conversion: the backend turns
+// fptrunc(a * b) into one v_fma_mix, which rounds once where the CPU rounds to f32 and then to
+// fp16 (it does so even without the contract flag). The empty asm makes the rounded f32 value
+// the only thing the next operation can see.
+__device__ __forceinline__ float mul_rn(float a, float b) {
+    float p;
+    {
+#pragma clang fp contract(off)
+        p = a * b;
+    }
+    asm volatile("" : "+v"(p));
+    return p;
+}
+__device__ __forceinline__ float sub_rn(float a, float b) {
+    float d;
+    {
+#pragma clang fp contract(off)
+        d = a - b;
+    }
+    asm volatile("" : "+v"(d));
+    return d;
+}
 
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll

@@ -31,15 +31,20 @@ constexpr int PACK_THREADS = 256;
 constexpr int PACK_VEC = 16;                                 // float4 per thread held in registers
 constexpr int PACK_REG_MAX = PACK_THREADS * PACK_VEC * 4;    // 16384 floats
 
+// TL: write A16 in the tiled layout (tiled_index over M rows) instead of rows of lda.
+template <bool TL>
 __global__ void __launch_bounds__(PACK_THREADS) pack_act_kernel(const float * __restrict__ X, int64_t ldx,
                                                                 int M, int K, uint16_t * __restrict__ A16,
                                                                 int64_t lda, float * __restrict__ scales) {
     __shared__ float red[PACK_THREADS / WAVE];
     const int t = threadIdx.x, lane = t % WAVE, wave = t / WAVE;
     const int m = blockIdx.x;
-    const float * x = X + (int64_t)m * ldx;
-    uint16_t * a = A16 + (int64_t)m * lda;
     const int n4 = K / 4;
+    // the destination of the 4 values starting at column 4c
+    auto dst = [&](int c) -> uint16_t * {
+        return TL ? A16 + tiled_index(m, 4 * c, K) : A16 + (int64_t)m * lda + 4 * c;
+    };
+    const float * x = X + (int64_t)m * ldx;
     float4v v[PACK_VEC];
     float amax = 0.0f;
 #pragma unroll
@@ -58,22 +63,24 @@ __global__ void __launch_bounds__(PACK_THREADS) pack_act_kernel(const float * __
     amax = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
     const float s = amax > 0.0f ? amax : 1.0f;
     const float inv = 1.0f / s;
+    // x * inv is rounded to f32 and then to fp16, as the CPU pack does: mul_rn keeps the compiler
+    // from folding the product into the conversion (v_fma_mix rounds once)
 #pragma unroll
     for (int i = 0; i < PACK_VEC; i++) {
         const int c = t + i * PACK_THREADS;
         if (c < n4) {
             u32x2 o;
-            o[0] = pack2h(v[i][0] * inv, v[i][1] * inv);
-            o[1] = pack2h(v[i][2] * inv, v[i][3] * inv);
-            *(u32x2 *)(a + 4 * c) = o;
+            o[0] = pack2h(mul_rn(v[i][0], inv), mul_rn(v[i][1], inv));
+            o[1] = pack2h(mul_rn(v[i][2], inv), mul_rn(v[i][3], inv));
+            *(u32x2 *)dst(c) = o;
         }
     }
     for (int c = t + PACK_VEC * PACK_THREADS; c < n4; c += PACK_THREADS) {
         const float4v w = *(const float4v *)(x + 4 * c);
         u32x2 o;
-        o[0] = pack2h(w[0] * inv, w[1] * inv);
-        o[1] = pack2h(w[2] * inv, w[3] * inv);
-        *(u32x2 *)(a + 4 * c) = o;
+        o[0] = pack2h(mul_rn(w[0], inv), mul_rn(w[1], inv));
+        o[1] = pack2h(mul_rn(w[2], inv), mul_rn(w[3], inv));
+        *(u32x2 *)dst(c) = o;
     }
     if (t == 0) scales[m] = s;
 }
@@ -340,7 +347,7 @@ __device__ __forceinline__ void wait_vm_lgkm0() {
     __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (0 << 8) | ((N >> 4) << 14));
 }
 
-template <int BM, int BN, int WGM, int WGN, int DK, int NS, int KSPLIT>
+template <int BM, int BN, int WGM, int WGN, int DK, int NS, int KSPLIT, bool TL>
 __global__ void __launch_bounds__(WAVE * WGM * WGN)
 __attribute__((amdgpu_waves_per_eu(WGM * WGN / 4, WGM * WGN / 4)))
 gemm_f16_kernel(GemmArgs args) {
@@ -375,20 +382,24 @@ gemm_f16_kernel(GemmArgs args) {
     const int kb = split * per;
     const int nk = max(0, min(nk_all, kb + per) - kb);
 
-    // this lane's global sources, one row chunk per DMA instruction, advanced by DK per stage
+    // this lane's global sources, one row chunk per DMA instruction, advanced by one stage's K
+    // per stage: DK values in rows, DK/32 tiles of 512 values in the tiled layout (TL), where the
+    // 16 rows x DK of one instruction are whole 64-byte tile rows
     const uint16_t * asrc[C::PA];
     const uint16_t * bsrc[C::PB];
 #pragma unroll
     for (int q = 0; q < C::PA; q++) {
         const int slot = (q * C::NW + wave) * WAVE + lane;
         const int r = slot / C::CH, c = (slot % C::CH) ^ ((r / C::RPW) & (C::CH - 1));
-        asrc[q] = args.A + (int64_t)min(m0 + r, M - 1) * args.lda + (int64_t)kb * DK + 8 * c;
+        const int64_t row = min(m0 + r, M - 1), k = (int64_t)kb * DK + 8 * c;
+        asrc[q] = args.A + (TL ? tiled_index(row, k, K) : row * args.lda + k);
     }
 #pragma unroll
     for (int q = 0; q < C::PB; q++) {
         const int slot = (q * C::NW + wave) * WAVE + lane;
         const int r = slot / C::CH, c = (slot % C::CH) ^ ((r / C::RPW) & (C::CH - 1));
-        bsrc[q] = W + (row0 + min(n0 + r, N - 1)) * (int64_t)K + (int64_t)kb * DK + 8 * c;
+        const int64_t row = row0 + min(n0 + r, N - 1), k = (int64_t)kb * DK + 8 * c;
+        bsrc[q] = W + (TL ? tiled_index(row, k, K) : row * K + k);
     }
     // the LDS destination of a DMA instruction must be wave-uniform (it goes to M0): take the
     // wave index from an SGPR so the address arithmetic stays scalar
@@ -398,7 +409,7 @@ gemm_f16_kernel(GemmArgs args) {
     auto issue = [&](int s) {
         uint8_t * st = smem + (s % NS) * C::STAGE;
         s = min(s, nk - 1);
-        const int64_t off = (int64_t)s * DK;
+        const int64_t off = (int64_t)s * (TL ? DK * 16 : DK);
 #pragma unroll
         for (int q = 0; q < C::PA; q++) dma16(asrc[q] + off, st + (q * C::NW + wave_s) * 1024);
 #pragma unroll
@@ -510,7 +521,8 @@ __global__ void zero_rows_kernel(GemmArgs args) {
 // ---------------------------------------------------------------------------------------------
 
 // One thread per (row, 32-value half of a 64-wide slab): the same decoders the GEMM uses.
-template <int WT>
+// TL: write the tiled layout (tiled_index); every 16-value run stays inside one 32-wide slab.
+template <int WT, bool TL>
 __global__ void __launch_bounds__(256) dequant_f16_kernel(const uint8_t * __restrict__ W, int64_t rows,
                                                           int64_t K, uint16_t * __restrict__ out) {
     const int64_t per_row = K / 32;   // thread items per row
@@ -524,6 +536,13 @@ __global__ void __launch_bounds__(256) dequant_f16_kernel(const uint8_t * __rest
     u32x4 o[4];
     int run0, run1;
     wl.decode(u, o, run0, run1);
+    if (TL) {
+        *(u32x4 *)(out + tiled_index(row, k0 + run0, K)) = o[0];
+        *(u32x4 *)(out + tiled_index(row, k0 + run0 + 8, K)) = o[1];
+        *(u32x4 *)(out + tiled_index(row, k0 + run1, K)) = o[2];
+        *(u32x4 *)(out + tiled_index(row, k0 + run1 + 8, K)) = o[3];
+        return;
+    }
     uint16_t * d = out + row * K + k0;
     *(u32x4 *)(d + run0) = o[0];
     *(u32x4 *)(d + run0 + 8) = o[1];
@@ -583,35 +602,52 @@ __global__ void pack_q6_k_kernel(const uint8_t * __restrict__ src, int64_t rows,
 hipError_t launch_pack_act(const float * X, int64_t ldx, int M, int K, uint16_t * A16, int64_t lda,
                            float * scales, hipStream_t st) {
     if (M <= 0) return hipSuccess;
-    hipLaunchKernelGGL(pack_act_kernel, dim3(M), dim3(PACK_THREADS), 0, st, X, ldx, M, K, A16, lda, scales);
+    hipLaunchKernelGGL(pack_act_kernel<false>, dim3(M), dim3(PACK_THREADS), 0, st, X, ldx, M, K, A16, lda, scales);
+    return hipGetLastError();
+}
+
+hipError_t launch_pack_act_tiled(const float * X, int64_t ldx, int M, int K, uint16_t * A16, float * scales,
+                                 hipStream_t st) {
+    if (M <= 0) return hipSuccess;
+    hipLaunchKernelGGL(pack_act_kernel<true>, dim3(M), dim3(PACK_THREADS), 0, st, X, ldx, M, K, A16, (int64_t)K,
+                       scales);
     return hipGetLastError();
 }
 
 // Tile configurations. The launcher picks one per call (choose_cfg); MI355X_GEMM_CFG=<id>
 // forces one (for tuning and for the tests, which run every configuration).
 //   0-3  register-staged kernel with the weight decoded into LDS: every weight type.
-//   4-10 LDS-DMA kernel: fp16 weights only. The cost model of choose_cfg times one block as
-//        ov_us + (its MFMA work) / tf_cu: a fixed part (pipeline fill, epilogue, for split-K the
-//        atomics) and a per-CU rate, both fitted to measurements of each configuration at
-//        M = 512 with K = 2048-14336.
+//   4-14 LDS-DMA kernel: fp16 weights only (row-major or tiled). choose_cfg prices a launch as
+//        max(rounds * (ov_us + MFMA work of a block / tf_cu), L2->CU bytes of all blocks / bw):
+//        a block's own pace (pipeline fill and epilogue, then its per-CU MFMA rate) or the
+//        aggregate rate at which the L2s feed the CUs for that tile shape (bigger tiles fetch
+//        less per FLOP but keep fewer bytes in flight per CU). All three were fitted to
+//        measurements of each configuration on tiled weights at M = 512, K = 2048-14336, each
+//        launch on a weight panel no earlier launch left in the caches (worst error 9%, most
+//        under 5%).
 struct CfgDesc {
     int bm, bn, ksplit;
     int dk;          // K per LDS stage of the DMA kernel; 0 for the register-staged kernel
     double tf_cu;    // TFLOP/s per CU
     double ov_us;    // fixed microseconds per block
+    double bw;       // aggregate L2 -> CU TB/s
 };
 static const CfgDesc kCfgs[] = {
-    {128, 128, 1, 0, 0.0, 0.0},      // 0: 4 waves of 64x64
-    {128, 128, 2, 0, 0.0, 0.0},      // 1: same, K split in two
-    {256, 128, 1, 0, 0.0, 0.0},      // 2: 4 waves of 128x64
-    {128, 256, 1, 0, 0.0, 0.0},      // 3: 4 waves of 64x128
-    {256, 256, 1, 64, 4.2, 0.0},     // 4: 8 waves of 64x128, 2 stages of 64
-    {128, 128, 1, 64, 4.8, 10.0},    // 5: 8 waves of 32x64, 4 stages of 64
-    {64, 128, 1, 128, 2.4, 8.0},     // 6: 4 waves of 32x64, 3 stages of 128
-    {128, 64, 1, 128, 2.4, 8.0},     // 7: 4 waves of 64x32, 3 stages of 128
-    {128, 128, 2, 64, 3.7, 26.0},    // 8: as 5, K split in two
-    {64, 128, 2, 128, 2.56, 17.7},   // 9: as 6, K split in two
-    {128, 128, 1, 32, 4.3, 7.0},     // 10: 8 waves of 32x64, 4 stages of 32 (any K)
+    {128, 128, 1, 0, 0.0, 0.0, 0.0},        // 0: 4 waves of 64x64
+    {128, 128, 2, 0, 0.0, 0.0, 0.0},        // 1: same, K split in two
+    {256, 128, 1, 0, 0.0, 0.0, 0.0},        // 2: 4 waves of 128x64
+    {128, 256, 1, 0, 0.0, 0.0, 0.0},        // 3: 4 waves of 64x128
+    {256, 256, 1, 64, 6.4, 19.0, 6.75},     // 4: 8 waves of 64x128, 2 stages of 64
+    {128, 128, 1, 64, 3.5, 0.0, 9.75},      // 5: 8 waves of 32x64, 4 stages of 64
+    {64, 128, 1, 128, 2.5, 7.0, 13.25},     // 6: 4 waves of 32x64, 3 stages of 128
+    {128, 64, 1, 128, 2.6, 7.0, 13.5},      // 7: 4 waves of 64x32, 3 stages of 128
+    {128, 128, 2, 64, 6.3, 29.0, 10.0},     // 8: as 5, K split in two
+    {64, 128, 2, 128, 3.0, 17.0, 11.25},    // 9: as 6, K split in two
+    {128, 128, 1, 32, 4.0, 0.0, 10.0},      // 10: 8 waves of 32x64, 4 stages of 32 (any K)
+    {128, 128, 1, 32, 4.0, 0.0, 10.0},      // 11: 8 waves of 32x64, 8 stages of 32
+    {256, 128, 1, 64, 5.8, 16.0, 8.75},     // 12: 8 waves of 64x64, 3 stages of 64
+    {128, 256, 1, 64, 5.6, 15.0, 8.75},     // 13: 8 waves of 64x64, 3 stages of 64
+    {64, 128, 1, 64, 2.4, 5.0, 12.5},       // 14: 4 waves of 32x64, 6 stages of 64
 };
 constexpr int FIRST_DMA_CFG = 4;
 constexpr int N_CFGS = sizeof(kCfgs) / sizeof(kCfgs[0]);
@@ -630,10 +666,10 @@ static hipError_t launch_one(const GemmArgs & a, int nblocks, hipStream_t st) {
     return hipGetLastError();
 }
 
-template <int BM, int BN, int WGM, int WGN, int DK, int NS, int KS>
+template <int BM, int BN, int WGM, int WGN, int DK, int NS, int KS, bool TL>
 static hipError_t launch_f16(const GemmArgs & a, int nblocks, hipStream_t st) {
     using C = F16Cfg<BM, BN, WGM, WGN, DK, NS>;
-    auto kern = gemm_f16_kernel<BM, BN, WGM, WGN, DK, NS, KS>;
+    auto kern = gemm_f16_kernel<BM, BN, WGM, WGN, DK, NS, KS, TL>;
     static bool attr = false;
     if (!attr) {
         hipError_t e = hipFuncSetAttribute((const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize, C::LDS);
@@ -644,22 +680,32 @@ static hipError_t launch_f16(const GemmArgs & a, int nblocks, hipStream_t st) {
     return hipGetLastError();
 }
 
+template <bool TL>
+static hipError_t launch_dma_cfg(int cfg, const GemmArgs & a, int nblocks, hipStream_t st) {
+    switch (cfg) {
+        case 4: return launch_f16<256, 256, 4, 2, 64, 2, 1, TL>(a, nblocks, st);
+        case 5: return launch_f16<128, 128, 4, 2, 64, 4, 1, TL>(a, nblocks, st);
+        case 6: return launch_f16<64, 128, 2, 2, 128, 3, 1, TL>(a, nblocks, st);
+        case 7: return launch_f16<128, 64, 2, 2, 128, 3, 1, TL>(a, nblocks, st);
+        case 8: return launch_f16<128, 128, 4, 2, 64, 4, 2, TL>(a, nblocks, st);
+        case 9: return launch_f16<64, 128, 2, 2, 128, 3, 2, TL>(a, nblocks, st);
+        case 10: return launch_f16<128, 128, 4, 2, 32, 4, 1, TL>(a, nblocks, st);
+        case 11: return launch_f16<128, 128, 4, 2, 32, 8, 1, TL>(a, nblocks, st);
+        case 12: return launch_f16<256, 128, 4, 2, 64, 3, 1, TL>(a, nblocks, st);
+        case 13: return launch_f16<128, 256, 2, 4, 64, 3, 1, TL>(a, nblocks, st);
+        case 14: return launch_f16<64, 128, 2, 2, 64, 6, 1, TL>(a, nblocks, st);
+        default: return hipErrorInvalidValue;
+    }
+}
+
 template <int WT>
 static hipError_t launch_cfg(int cfg, const GemmArgs & a, int nblocks, hipStream_t st) {
     if (cfg >= FIRST_DMA_CFG) {
-        if (WT != T_F16) return hipErrorInvalidValue;
-        switch (cfg) {
-            case 4: return launch_f16<256, 256, 4, 2, 64, 2, 1>(a, nblocks, st);
-            case 5: return launch_f16<128, 128, 4, 2, 64, 4, 1>(a, nblocks, st);
-            case 6: return launch_f16<64, 128, 2, 2, 128, 3, 1>(a, nblocks, st);
-            case 7: return launch_f16<128, 64, 2, 2, 128, 3, 1>(a, nblocks, st);
-            case 8: return launch_f16<128, 128, 4, 2, 64, 4, 2>(a, nblocks, st);
-            case 9: return launch_f16<64, 128, 2, 2, 128, 3, 2>(a, nblocks, st);
-            case 10: return launch_f16<128, 128, 4, 2, 32, 4, 1>(a, nblocks, st);
-            default: return hipErrorInvalidValue;
-        }
+        if (WT != T_F16 && WT != T_F16T) return hipErrorInvalidValue;
+        return launch_dma_cfg<WT == T_F16T>(cfg, a, nblocks, st);
     }
-    switch (cfg) {
+    if constexpr (WT == T_F16T) return hipErrorInvalidValue;
+    else switch (cfg) {
         case 0: return launch_one<WT, 128, 128, 2, 2, 2, 1>(a, nblocks, st);
         case 1: return launch_one<WT, 128, 128, 2, 2, 2, 2>(a, nblocks, st);
         case 2: return launch_one<WT, 256, 128, 2, 2, 2, 1>(a, nblocks, st);
@@ -686,14 +732,13 @@ static int tiles_of(const GemmArgs & a, int bm, int bn) {
 
 static bool cfg_fits(int c, int wt, int K) {
     const CfgDesc & d = kCfgs[c];
-    if (d.dk == 0) return true;
-    if (wt != T_F16 || K % d.dk) return false;
+    if (d.dk == 0) return wt != T_F16T;
+    if ((wt != T_F16 && wt != T_F16T) || K % d.dk) return false;
     return d.ksplit == 1 || K / d.dk >= 2;
 }
 
-// fp16 weights: the DMA configuration with the least estimated time. Every block has a CU to
-// itself (their LDS rings take 128-144 KB), so a launch runs in ceil(blocks / CUs) rounds, each
-// as long as one block (ov_us + MFMA work / tf_cu).
+// fp16 weights: the DMA configuration with the least estimated time (the CfgDesc model; every
+// DMA block has a CU to itself, so a launch runs in ceil(blocks / CUs) rounds).
 // Other weights: the register-staged configuration with the best grid fill times its tile's
 // relative per-CU efficiency (bigger wave tiles read LDS less per MFMA); split-K only when the
 // unsplit grid leaves most CUs idle.
@@ -705,7 +750,7 @@ static int choose_cfg(int wt, const GemmArgs & a) {
         }
     }
     const int cus = cu_count();
-    if (wt == T_F16) {
+    if (wt == T_F16 || wt == T_F16T) {
         int best = -1;
         double best_us = 0.0;
         for (int c = FIRST_DMA_CFG; c < N_CFGS; c++) {
@@ -713,7 +758,10 @@ static int choose_cfg(int wt, const GemmArgs & a) {
             const CfgDesc & d = kCfgs[c];
             const int blocks = tiles_of(a, d.bm, d.bn) * d.ksplit;
             const int rounds = (blocks + cus - 1) / cus;
-            double us = rounds * (d.ov_us + 2.0 * d.bm * d.bn * ((double)a.K / d.ksplit) / (d.tf_cu * 1e6));
+            const double kb = (double)a.K / d.ksplit;
+            const double pace = rounds * (d.ov_us + 2.0 * d.bm * d.bn * kb / (d.tf_cu * 1e6));
+            const double feed = (double)blocks * (d.bm + d.bn) * kb * 2.0 / (d.bw * 1e6);
+            double us = pace > feed ? pace : feed;
             if (d.ksplit > 1) us += 3.0;   // the zero fill of the output
             if (best < 0 || us < best_us - 1e-9) { best = c; best_us = us; }
         }
@@ -754,6 +802,7 @@ hipError_t launch_gemm(int wt, const GemmArgs & a_in, int /*unused*/, hipStream_
     }
     switch (wt) {
         case T_F16: return launch_cfg<T_F16>(cfg, a, nblocks, st);
+        case T_F16T: return launch_cfg<T_F16T>(cfg, a, nblocks, st);
         case T_Q8_0: return launch_cfg<T_Q8_0>(cfg, a, nblocks, st);
         case T_Q4_K: return launch_cfg<T_Q4_K>(cfg, a, nblocks, st);
         case T_Q6_K: return launch_cfg<T_Q6_K>(cfg, a, nblocks, st);
@@ -761,19 +810,28 @@ hipError_t launch_gemm(int wt, const GemmArgs & a_in, int /*unused*/, hipStream_
     }
 }
 
-hipError_t launch_dequant_f16(int wt, const void * W, int64_t rows, int64_t K, uint16_t * out, hipStream_t st) {
+template <bool TL>
+static hipError_t launch_dequant(int wt, const void * W, int64_t rows, int64_t K, uint16_t * out, hipStream_t st) {
     const int64_t items = rows * (K / 32);
     if (items <= 0) return hipSuccess;
     const dim3 grid((unsigned)((items + 255) / 256));
     const uint8_t * w = (const uint8_t *)W;
     switch (wt) {
-        case T_F16: hipLaunchKernelGGL(dequant_f16_kernel<T_F16>, grid, dim3(256), 0, st, w, rows, K, out); break;
-        case T_Q8_0: hipLaunchKernelGGL(dequant_f16_kernel<T_Q8_0>, grid, dim3(256), 0, st, w, rows, K, out); break;
-        case T_Q4_K: hipLaunchKernelGGL(dequant_f16_kernel<T_Q4_K>, grid, dim3(256), 0, st, w, rows, K, out); break;
-        case T_Q6_K: hipLaunchKernelGGL(dequant_f16_kernel<T_Q6_K>, grid, dim3(256), 0, st, w, rows, K, out); break;
+        case T_F16: hipLaunchKernelGGL((dequant_f16_kernel<T_F16, TL>), grid, dim3(256), 0, st, w, rows, K, out); break;
+        case T_Q8_0: hipLaunchKernelGGL((dequant_f16_kernel<T_Q8_0, TL>), grid, dim3(256), 0, st, w, rows, K, out); break;
+        case T_Q4_K: hipLaunchKernelGGL((dequant_f16_kernel<T_Q4_K, TL>), grid, dim3(256), 0, st, w, rows, K, out); break;
+        case T_Q6_K: hipLaunchKernelGGL((dequant_f16_kernel<T_Q6_K, TL>), grid, dim3(256), 0, st, w, rows, K, out); break;
         default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
+}
+
+hipError_t launch_dequant_f16(int wt, const void * W, int64_t rows, int64_t K, uint16_t * out, hipStream_t st) {
+    return launch_dequant<false>(wt, W, rows, K, out, st);
+}
+
+hipError_t launch_f16_tiled(int wt, const void * W, int64_t rows, int64_t K, uint16_t * out, hipStream_t st) {
+    return launch_dequant<true>(wt, W, rows, K, out, st);
 }
 
 hipError_t launch_convert_f16(int type, const void * src, int64_t n, uint16_t * dst, hipStream_t st) {

@@ -22,7 +22,7 @@ struct GemmGroup {
 };
 
 struct GemmArgs {
-    const uint16_t * A;    // fp16 activations [M][lda], row-scaled
+    const uint16_t * A;    // fp16 activations [M][lda], row-scaled (tiled for T_F16T weights)
     const float * scales;  // [M]
     int64_t lda;
     int M, K;
@@ -78,7 +78,10 @@ hipError_t launch_fa(const FaArgs & a, hipStream_t st);
 hipError_t launch_pack_act(const float * X, int64_t ldx, int M, int K, uint16_t * A16, int64_t lda,
                            float * scales, hipStream_t st);
 hipError_t launch_gemm(int wt, const GemmArgs & a, int n_tiles_total, hipStream_t st);
+hipError_t launch_pack_act_tiled(const float * X, int64_t ldx, int M, int K, uint16_t * A16, float * scales,
+                                 hipStream_t st);
 hipError_t launch_dequant_f16(int wt, const void * W, int64_t rows, int64_t K, uint16_t * out, hipStream_t st);
+hipError_t launch_f16_tiled(int wt, const void * W, int64_t rows, int64_t K, uint16_t * out, hipStream_t st);
 hipError_t launch_pack_weight(int wt, const void * src, int64_t rows, int64_t K, void * dst, hipStream_t st);
 hipError_t launch_convert_f16(int type, const void * src, int64_t n, uint16_t * dst, hipStream_t st);
 

@@ -3,6 +3,8 @@
 //
 // A weight panel is `rows` rows of K values. The layouts are:
 //   F16   [rows][K] fp16, the ggml payload unchanged (zero copy).
+//   F16T  fp16 in 16 x 32 tiles of 1 KB (tiled_index, mx_common.h): the resident fp16 form the
+//         LDS-DMA GEMM streams, one contiguous kilobyte per load instruction.
 //   Q4_K  [rows][K/256] blocks of 144 B, the ggml payload unchanged: { fp16 d, fp16 dmin,
 //         u8 scales[12], u8 qs[128] }. Every block starts on a 16-byte boundary.
 //   Q8_0  split into two planes so every load is 16-byte aligned (a 34-byte ggml block is only
@@ -30,6 +32,7 @@ namespace mx {
 __host__ __device__ inline int64_t packed_weight_bytes(int wt, int64_t rows, int64_t K) {
     switch (wt) {
         case T_F16: return rows * K * 2;
+        case T_F16T: return tiled_rows(rows) * K * 2;
         case T_Q8_0: return rows * K + rows * (K / 32) * 2;
         case T_Q4_K: return rows * (K / 256) * 144;
         case T_Q6_K: return rows * (K / 256) * 210;

@@ -17,6 +17,7 @@ _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "lib", "libggml-mi355x.so")
 
 F32, F16, Q8_0, Q4_K, Q6_K, I32, BF16 = 0, 1, 8, 12, 14, 26, 30
+F16_T = 0x101   # the library's tiled fp16 layout (16 x 32 tiles of 1 KB); not a ggml type
 BLOCK = {F16: 1, F32: 1, BF16: 1, Q8_0: 32, Q4_K: 256, Q6_K: 256}
 TYPE_SIZE = {F16: 2, F32: 4, BF16: 2, Q8_0: 34, Q4_K: 144, Q6_K: 210}
 
@@ -80,7 +81,9 @@ def lib():
     L.mi355x_weight_bytes.argtypes = [i32, i64, i64]
     L.mi355x_weight_pack.argtypes = [i32, vp, i64, i64, vp, vp]
     L.mi355x_weight_dequant_f16.argtypes = [i32, vp, i64, i64, vp, vp]
+    L.mi355x_weight_f16_tiled.argtypes = [i32, vp, i64, i64, vp, vp]
     L.mi355x_pack_act.argtypes = [vp, i64, i64, i64, vp, vp, vp]
+    L.mi355x_pack_act_tiled.argtypes = [vp, i64, i64, i64, vp, vp, vp]
     L.mi355x_gemm.argtypes = [i32, vp, vp, i64, i64, ctypes.POINTER(GemmOut), i32, vp]
     L.mi355x_mul_mat_workspace.restype = sz
     L.mi355x_mul_mat_workspace.argtypes = [i64, i64]
@@ -172,21 +175,34 @@ def dequant_f16(wtype: int, w_dev, rows: int, K: int):
     return out
 
 
-def pack_act(x):
+def tile_f16(wtype: int, w_dev, rows: int, K: int):
+    """A weight in HBM layout -> the tiled fp16 layout (F16_T), as a uint8 device tensor."""
+    torch = _torch()
+    out = torch.empty(weight_bytes(F16_T, rows, K), dtype=torch.uint8, device=w_dev.device)
+    check(lib().mi355x_weight_f16_tiled(wtype, _ptr(w_dev), rows, K, _ptr(out), stream_handle()),
+          "weight_f16_tiled")
+    return out
+
+
+def pack_act(x, tiled: bool = False):
+    """F32 [M, K] -> (fp16 activations, row scales [M]). tiled: the F16_T layout over M rows,
+    returned as [ceil(M/16)*16, K] (the padding rows are never read)."""
     torch = _torch()
     M, K = x.shape
-    a16 = torch.empty((M, K), dtype=torch.float16, device=x.device)
+    rows = (M + 15) // 16 * 16 if tiled else M
+    a16 = torch.empty((rows, K), dtype=torch.float16, device=x.device)
     sc = torch.empty((M,), dtype=torch.float32, device=x.device)
-    check(lib().mi355x_pack_act(_ptr(x), x.stride(0), M, K, _ptr(a16), _ptr(sc), stream_handle()), "pack_act")
+    fn = lib().mi355x_pack_act_tiled if tiled else lib().mi355x_pack_act
+    check(fn(_ptr(x), x.stride(0), M, K, _ptr(a16), _ptr(sc), stream_handle()), "pack_act")
     return a16, sc
 
 
 def gemm(wtype: int, a16, scales, K: int, outs):
-    """outs: list of (w_dev, rows_total, row0, N, c_tensor)."""
+    """outs: list of (w_dev, rows_total, row0, N, c_tensor). M = len(scales)."""
     arr = (GemmOut * len(outs))()
     for i, (w, rows_total, row0, N, c) in enumerate(outs):
         arr[i] = GemmOut(w.data_ptr(), rows_total, row0, N, c.data_ptr(), c.stride(0))
-    M = a16.shape[0]
+    M = scales.shape[0]
     check(lib().mi355x_gemm(wtype, _ptr(a16), _ptr(scales), M, K, arr, len(outs), stream_handle()), "gemm")
 
 

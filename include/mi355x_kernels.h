@@ -40,7 +40,12 @@ enum mi355x_status {
     MI355X_E_IDS = -5,          /* MUL_MAT_ID: an expert id outside [0, n_expert) */
 };
 
-enum mi355x_wtype { MI355X_F16 = 1, MI355X_Q8_0 = 8, MI355X_Q4_K = 12, MI355X_Q6_K = 14 };
+enum mi355x_wtype { MI355X_F16 = 1, MI355X_Q8_0 = 8, MI355X_Q4_K = 12, MI355X_Q6_K = 14,
+                    /* not a ggml type: fp16 [rows][K] in 16 x 32 tiles of 1 KB, row-major inside,
+                     * tile (r/16, k/32) at element ((r/16)*(K/32) + k/32)*512; rows padded to a
+                     * multiple of 16 (padding never read). The resident fp16 form the GEMM streams
+                     * fastest: each 64-lane load instruction reads one whole tile. */
+                    MI355X_F16_T = 0x101 };
 
 typedef struct mi355x_device_info {
     char name[64];              /* e.g. "gfx950" */
@@ -76,6 +81,13 @@ MI355X_API int mi355x_weight_pack(int wtype, const void * src_dev, int64_t rows,
 MI355X_API int mi355x_weight_dequant_f16(int wtype, const void * w_dev, int64_t rows, int64_t K,
                                          uint16_t * out_dev, void * stream);
 
+/* A weight in HBM layout (F16, Q8_0, Q4_K, Q6_K) -> MI355X_F16_T, decoded exactly as
+ * mi355x_weight_dequant_f16 decodes it (the same fp16 values, tiled). K % 64 == 0; out_dev holds
+ * mi355x_weight_bytes(MI355X_F16_T, rows, K) bytes and does not alias w_dev. The tiled resident
+ * form of rocket_weight_to_fp16 + the resident pack (ggml-rocket.cpp:3843-3931, 4362). */
+MI355X_API int mi355x_weight_f16_tiled(int wtype, const void * w_dev, int64_t rows, int64_t K,
+                                       uint16_t * out_dev, void * stream);
+
 /* F32 (type 0) or BF16 (type 30) values -> fp16, round to nearest even: the resident form of an
  * F32 / BF16 weight (the F32 and BF16 branches of rocket_weight_to_fp16, ggml-rocket.cpp:
  * 3855-3890). n values; src 4- or 2-byte aligned, dst 2-byte aligned. */
@@ -89,6 +101,12 @@ MI355X_API int mi355x_convert_f16(int type, const void * src_dev, int64_t n, uin
 MI355X_API int mi355x_pack_act(const float * x_dev, int64_t ldx, int64_t M, int64_t K,
                                uint16_t * a16_dev, float * scales_dev, void * stream);
 
+/* mi355x_pack_act with the fp16 output in the MI355X_F16_T layout (ceil(M/16)*16 rows; the
+ * padding rows are never read), for a GEMM on MI355X_F16_T weights. K % 32 == 0. Same values and
+ * scales as mi355x_pack_act (rocket_pack_activations, ggml-rocket.cpp:1451-1502). */
+MI355X_API int mi355x_pack_act_tiled(const float * x_dev, int64_t ldx, int64_t M, int64_t K,
+                                     uint16_t * a16_dev, float * scales_dev, void * stream);
+
 /* One output of a (fused) GEMM launch. */
 typedef struct mi355x_gemm_out {
     const void * w_dev;     /* weight panel in HBM layout */
@@ -101,7 +119,8 @@ typedef struct mi355x_gemm_out {
 
 /* c[m][n] = scales[m] * sum_k a16[m][k] * w[row0 + n][k], for each of `n_out` (1..4) weights of
  * one type that share the activation, in ONE launch over their concatenated N. fp16 MFMA, fp32
- * accumulation, F32 output. K % 32 == 0 (and a whole number of the type's blocks).
+ * accumulation, F32 output. K % 32 == 0 (and a whole number of the type's blocks). For
+ * MI355X_F16_T weights a16 is tiled too (mi355x_pack_act_tiled).
  * Replaces rocket_matmul_fp16_prepacked (ggml-rocket.cpp:4449, 5144),
  * rocket_matmul_fp16_stream (4834), rocket_matmul_fp16_mt (4844) and the fused
  * rocket_matmul_fp16_stream_fused (5004). */
@@ -112,8 +131,8 @@ MI355X_API int mi355x_gemm(int wtype, const uint16_t * a16_dev, const float * sc
 /* Workspace bytes mi355x_mul_mat needs for M rows of K. */
 MI355X_API size_t mi355x_mul_mat_workspace(int64_t M, int64_t K);
 
-/* dst[M][ldd] = x[M][ldx] . w[N][K]^T: mi355x_pack_act then mi355x_gemm, the activation pack
- * in `workspace_dev`. The whole MUL_MAT of ggml-rocket.cpp:4548-4871 on device. */
+/* dst[M][ldd] = x[M][ldx] . w[N][K]^T: mi355x_pack_act (mi355x_pack_act_tiled for MI355X_F16_T)
+ * then mi355x_gemm, the activation pack in `workspace_dev`. The whole MUL_MAT of ggml-rocket.cpp:4548-4871 on device. */
 MI355X_API int mi355x_mul_mat(int wtype, const void * w_dev, int64_t N, int64_t K,
                               const float * x_dev, int64_t ldx, int64_t M,
                               float * dst_dev, int64_t ldd,

@@ -188,35 +188,78 @@ def test_gemm_rows_of_a_panel(mx):
         _assert_bars(ref, c.cpu().numpy(), M, N, f"panel {O.TYPE_NAMES[wtype]}")
 
 
+def _untile(buf, rows, K):
+    """The tiled fp16 layout (16 x 32 tiles of 1 KB, tile (r/16, k/32) at ((r/16)*(K/32) + k/32)
+    * 512 values, row-major inside, rows padded to 16) back to [rows][K]."""
+    rp = (rows + 15) // 16 * 16
+    t = np.asarray(buf).view(np.uint16).reshape(-1)[:rp * K].reshape(rp // 16, K // 32, 16, 32)
+    return t.transpose(0, 2, 1, 3).reshape(rp, K)[:rows]
+
+
+@pytest.mark.parametrize("wtype", [O.F16, O.Q8_0, O.Q4_K, O.Q6_K])
+def test_f16_tiled_bitexact(mx, wtype):
+    """The tiled resident form holds exactly the fp16 values of the row-major one (rows not a
+    multiple of 16: padded, the padding never read)."""
+    N, K = 300, 1024                # rows padded to 304
+    W = O.fill_normal((N, K), 21 + wtype, 0.0, 0.02)
+    W[0, :256] *= 50.0
+    W[1, :] = 0.0
+    payload = O.f32_to_f16_bits(W) if wtype == O.F16 else O.quantize(wtype, W)
+    want = payload if wtype == O.F16 else O.dequantize_f16(wtype, payload, K)
+    w = mx.upload_weight(wtype, payload, N, K)
+    t = mx.tile_f16(wtype, w, N, K)
+    assert t.numel() == mx.weight_bytes(mx.F16_T, N, K) == 304 * K * 2
+    assert np.array_equal(_untile(t.cpu().numpy(), N, K), want.reshape(N, K))
+
+
+def test_pack_act_tiled_bitexact(mx):
+    X = O.fill_normal((67, 512), 8)
+    X[3] *= 3000.0
+    X[5] = 0.0
+    X[9, 17] = 1e6
+    a16, sc = mx.pack_act(_dev(X), tiled=True)
+    want_a, want_s = O.pack_act(X)
+    got = _untile(a16.cpu().numpy(), 67, 512)
+    assert np.array_equal(sc.cpu().numpy(), want_s)
+    bad = np.argwhere(got != want_a)
+    assert len(bad) == 0, f"{len(bad)} differ, first {[(int(r), int(c), int(got[r, c]), int(want_a[r, c])) for r, c in bad[:8]]}"
+
+
 # Every tile configuration of mi355x_gemm, forced through MI355X_GEMM_CFG, on a ragged fused
-# launch (M and both N not multiples of any tile). Configurations 4-10 are the LDS-DMA kernels,
-# which take fp16 weights only.
-N_GEMM_CFGS = 11
+# launch (M and both N not multiples of any tile). Configurations 4-14 are the LDS-DMA kernels,
+# which take fp16 weights only, row-major (F16) or tiled (F16_T).
+N_GEMM_CFGS = 15
 FIRST_DMA_CFG = 4
+F16_T = 0x101
 
 
 @pytest.mark.parametrize("cfg", list(range(N_GEMM_CFGS)))
-@pytest.mark.parametrize("wtype", [O.F16, O.Q4_K])
+@pytest.mark.parametrize("wtype", [O.F16, O.Q4_K, F16_T])
 def test_gemm_every_tile_config(mx, monkeypatch, cfg, wtype):
     import torch
-    if cfg >= FIRST_DMA_CFG and wtype != O.F16:
+    if cfg >= FIRST_DMA_CFG and wtype == O.Q4_K:
         pytest.skip("the LDS-DMA configurations take fp16 weights only")
+    if cfg < FIRST_DMA_CFG and wtype == F16_T:
+        pytest.skip("the register-staged configurations do not read the tiled layout")
     monkeypatch.setenv("MI355X_GEMM_CFG", str(cfg))
     K, M, Ns = 1280, 300, (528, 144)
     Xf = O.fill_normal((M, K), 900 + cfg)
-    a16, sc = mx.pack_act(_dev(Xf))
+    a16, sc = mx.pack_act(_dev(Xf), tiled=wtype == F16_T)
     outs, refs = [], []
     for g, N in enumerate(Ns):
         W = O.fill_normal((N, K), 910 + g, 0.0, 0.02)
-        payload = O.f32_to_f16_bits(W) if wtype == O.F16 else O.quantize(wtype, W)
-        refs.append(O.mul_mat(wtype, payload, Xf, N, K))
-        w = mx.upload_weight(wtype, payload, N, K)
+        payload = O.quantize(wtype, W) if wtype == O.Q4_K else O.f32_to_f16_bits(W)
+        refs.append(O.mul_mat(O.Q4_K if wtype == O.Q4_K else O.F16, payload, Xf, N, K))
+        if wtype == F16_T:
+            w = mx.tile_f16(O.F16, mx.upload_weight(O.F16, payload, N, K), N, K)
+        else:
+            w = mx.upload_weight(wtype, payload, N, K)
         c = torch.full((M, N), float("nan"), dtype=torch.float32, device="cuda")
         outs.append((w, N, 0, N, c))
     mx.gemm(wtype, a16, sc, K, outs)
     torch.cuda.synchronize()
     for (w, _, _, N, c), ref in zip(outs, refs):
-        _assert_bars(ref, c.cpu().numpy(), M, N, f"cfg {cfg} {O.TYPE_NAMES[wtype]} N={N}")
+        _assert_bars(ref, c.cpu().numpy(), M, N, f"cfg {cfg} {O.TYPE_NAMES.get(wtype, 'F16_T')} N={N}")
 
 
 @pytest.mark.parametrize("K", [1312, 96])
@@ -228,3 +271,33 @@ def test_f16_k_not_multiple_of_64(mx, K):
     ref = O.mul_mat(O.F16, W16, Xf, N, K)
     got = _run_mul_mat(mx, O.F16, W16, N, K, Xf)
     _assert_bars(ref, got, M, N, f"F16 K={K}")
+
+
+@pytest.mark.parametrize("K,N,M", [(1024, 512, 7), (4096, 1024, 130), (2048, 8192, 512)])
+def test_mul_mat_f16_tiled(mx, K, N, M):
+    """mi355x_mul_mat on a tiled resident weight (the tiled activation pack inside), M ragged."""
+    import torch
+    W16 = O.f32_to_f16_bits(O.fill_normal((N, K), 940 + M, 0.0, 0.02))
+    Xf = O.fill_normal((M, K), 941 + M)
+    w = mx.tile_f16(O.F16, mx.upload_weight(O.F16, W16, N, K), N, K)
+    out = mx.mul_mat(F16_T, w, N, K, _dev(Xf))
+    torch.cuda.synchronize()
+    rows = np.unique(np.linspace(0, M - 1, min(M, 48)).astype(int))
+    ref = O.mul_mat(O.F16, W16, Xf[rows], N, K)
+    _assert_bars(ref, out.cpu().numpy()[rows], len(rows), N, f"F16_T K={K} N={N} M={M}")
+
+
+def test_gemm_tiled_rows_of_a_panel(mx):
+    """row0 inside a tiled panel (not a multiple of 16): the slabs are rows_total rows long."""
+    import torch
+    K, N, M = 512, 96, 33
+    W16 = O.f32_to_f16_bits(O.fill_normal((3 * N, K), 950, 0.0, 0.02))
+    w = mx.tile_f16(O.F16, mx.upload_weight(O.F16, W16, 3 * N, K), 3 * N, K)
+    Xf = O.fill_normal((M, K), 951)
+    a16, sc = mx.pack_act(_dev(Xf), tiled=True)
+    c = torch.empty((M, N), dtype=torch.float32, device="cuda")
+    for row0 in (2 * N, 40):
+        mx.gemm(F16_T, a16, sc, K, [(w, 3 * N, row0, N, c)])
+        torch.cuda.synchronize()
+        ref = O.mul_mat(O.F16, W16.reshape(3 * N, K)[row0:row0 + N], Xf, N, K)
+        _assert_bars(ref, c.cpu().numpy(), M, N, f"tiled panel row0={row0}")
