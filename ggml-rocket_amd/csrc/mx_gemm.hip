@@ -507,6 +507,178 @@ gemm_f16_kernel(GemmArgs args) {
     }
 }
 
+// ---------------------------------------------------------------------------------------------
+// The same LDS-DMA pipeline with a block tile whose two wave columns differ in width: BN0 + BN1
+// columns (e.g. 128 + 96 = 224), 8 waves in a 4 x 2 grid. A 256 x 224 tile cuts an N of 28672
+// (the fused gate/up of an 8B model) into 128 x 2 = 256 blocks, one per CU, where 256 x 256
+// leaves 32 CUs idle. Wave w takes column w / 4, so each SIMD (w % 4) holds one wave of each
+// width. Each column's four waves fetch that column's B rows, so the DMA count per stage, and
+// with it the vmcnt of every wait, is a per-column constant; the body below is instantiated once
+// per column width, and both instances meet at the same barriers (one before the loop, one per
+// stage).
+// ---------------------------------------------------------------------------------------------
+template <int BM_, int BN0, int BN1, int DK, int NS>
+struct ColsCfg {
+    static constexpr int NW = 8, THREADS = WAVE * NW, WGM = 4;
+    static constexpr int BM = BM_, BN = BN0 + BN1, TM = BM / WGM, MI = TM / 32;
+    static constexpr int CH = DK / 8, RPW = 16 / CH, RB = DK * 2, NSTAGES = NS;
+    static constexpr int A_BYTES = BM * RB, B_BYTES = BN * RB, STAGE = A_BYTES + B_BYTES;
+    static constexpr int LDS = NS * STAGE;
+    static constexpr int PA = A_BYTES / (THREADS * 16);
+    static_assert(MI >= 1 && TM % 32 == 0 && BN0 % 32 == 0 && BN1 % 32 == 0 && BN0 % 16 == 0, "wave tile");
+    static_assert(PA * THREADS * 16 == A_BYTES, "A DMA split");
+    static_assert((BN0 * RB) % (4 * 1024) == 0 && (BN1 * RB) % (4 * 1024) == 0, "B DMA split");
+    static_assert(NS >= 2 && (NS - 1) * (PA + BN0 * RB / 4096) <= 63, "vmcnt range");
+    static_assert(LDS <= 160 * 1024, "LDS");
+};
+
+template <class C, int TNW, int COL0, bool TL>
+__device__ __forceinline__ void cols_body(const GemmArgs & args, uint8_t * smem, int wm) {
+    constexpr int DK = C::RB / 2, NS = C::NSTAGES, NJ = TNW / 32;
+    constexpr int PB = TNW * C::RB / 4096;        // this column's B DMA per wave
+    constexpr int PER = C::PA + PB;
+    const int t = threadIdx.x, lane = t % WAVE, wave = t / WAVE;
+
+    const int tile = xcd_tile(blockIdx.x, gridDim.x);
+    const int mt = tile % args.m_tiles, nt = tile / args.m_tiles;
+    int g = 0;
+#pragma unroll
+    for (int i = 1; i < GEMM_MAX_GROUPS; i++)
+        if (i < args.ng && nt >= args.g[i].ntile_begin) g = i;
+    const uint16_t * W = (const uint16_t *)args.g[0].W;
+    int64_t row0 = args.g[0].row0;
+    int N = args.g[0].N, ntb = args.g[0].ntile_begin;
+    float * Cp = args.g[0].C;
+    int64_t ldc = args.g[0].ldc;
+#pragma unroll
+    for (int i = 1; i < GEMM_MAX_GROUPS; i++)
+        if (i == g) {
+            W = (const uint16_t *)args.g[i].W; row0 = args.g[i].row0; N = args.g[i].N;
+            ntb = args.g[i].ntile_begin; Cp = args.g[i].C; ldc = args.g[i].ldc;
+        }
+    const int n0 = (nt - ntb) * C::BN, m0 = mt * C::BM;
+    const int M = args.M, K = args.K;
+    const int nk = K / DK;
+
+    const uint16_t * asrc[C::PA];
+    const uint16_t * bsrc[PB];
+#pragma unroll
+    for (int q = 0; q < C::PA; q++) {
+        const int slot = (q * C::NW + wave) * WAVE + lane;
+        const int r = slot / C::CH, c = (slot % C::CH) ^ ((r / C::RPW) & (C::CH - 1));
+        const int64_t row = min(m0 + r, M - 1), k = 8 * c;
+        asrc[q] = args.A + (TL ? tiled_index(row, k, K) : row * args.lda + k);
+    }
+#pragma unroll
+    for (int q = 0; q < PB; q++) {
+        // rows COL0 .. COL0 + TNW of the B tile, fetched by this column's four waves; COL0 is a
+        // multiple of 16, so the swizzle of a row depends on its offset inside the column only
+        const int slot = (q * 4 + wm) * WAVE + lane;
+        const int r = slot / C::CH, c = (slot % C::CH) ^ ((r / C::RPW) & (C::CH - 1));
+        const int64_t row = row0 + min(n0 + COL0 + r, N - 1), k = 8 * c;
+        bsrc[q] = W + (TL ? tiled_index(row, k, K) : row * K + k);
+    }
+    const int wave_s = __builtin_amdgcn_readfirstlane(wave), wm_s = __builtin_amdgcn_readfirstlane(wm);
+    auto issue = [&](int s) {
+        uint8_t * st = smem + (s % NS) * C::STAGE;
+        s = min(s, nk - 1);
+        const int64_t off = (int64_t)s * (TL ? DK * 16 : DK);
+#pragma unroll
+        for (int q = 0; q < C::PA; q++) dma16(asrc[q] + off, st + (q * C::NW + wave_s) * 1024);
+#pragma unroll
+        for (int q = 0; q < PB; q++) dma16(bsrc[q] + off, st + C::A_BYTES + COL0 * C::RB + (q * 4 + wm_s) * 1024);
+    };
+
+    float16v acc[C::MI][NJ];
+#pragma unroll
+    for (int i = 0; i < C::MI; i++)
+#pragma unroll
+        for (int j = 0; j < NJ; j++)
+#pragma unroll
+            for (int e = 0; e < 16; e++) acc[i][j][e] = 0.0f;
+
+    const int lr = lane % 32, lg = lane / 32, x = (lr / C::RPW) & (C::CH - 1);
+    const int a_off = (wm * C::TM + lr) * C::RB, b_off = C::A_BYTES + (COL0 + lr) * C::RB;
+    struct Frags {
+        half8 a[C::MI], b[NJ];
+    };
+    auto read_frags = [&](int s, int ks, Frags & f) {
+        const uint8_t * st = smem + (s % NS) * C::STAGE;
+        const int co = ((2 * ks + lg) ^ x) * 16;
+#pragma unroll
+        for (int i = 0; i < C::MI; i++) f.a[i] = *(const half8 *)(st + a_off + i * 32 * C::RB + co);
+#pragma unroll
+        for (int j = 0; j < NJ; j++) f.b[j] = *(const half8 *)(st + b_off + j * 32 * C::RB + co);
+    };
+    auto mma = [&](const Frags & f, int part) {
+#pragma unroll
+        for (int i = 0; i < C::MI; i++)
+#pragma unroll
+            for (int j = 0; j < NJ; j++)
+                if ((part == 0) == (i == 0 && j == 0)) acc[i][j] = mfma32(f.a[i], f.b[j], acc[i][j]);
+    };
+
+    // the pipeline of gemm_f16_kernel, stage for stage (same barriers, same DMA order)
+    if (nk > 0) {
+        Frags f0, f1;
+#pragma unroll
+        for (int p = 0; p < NS; p++) issue(p);
+        wait_vm_lgkm0<(NS - 1) * PER>();
+        __builtin_amdgcn_s_barrier();
+        read_frags(0, 0, f0);
+        constexpr int KS = DK / 16;
+        for (int s = 0; s < nk; s++) {
+#pragma unroll
+            for (int ks = 0; ks < KS; ks++) {
+                Frags & F = (ks % 2 == 0) ? f0 : f1;
+                Frags & G = (ks % 2 == 0) ? f1 : f0;
+                mma(F, 0);
+                __builtin_amdgcn_sched_barrier(0);
+                if (ks + 1 < KS) {
+                    read_frags(s, ks + 1, G);
+                    __builtin_amdgcn_sched_barrier(0);
+                } else {
+                    wait_vm_lgkm0<(NS - 2) * PER>();
+                    __builtin_amdgcn_s_barrier();
+                    read_frags(s + 1, 0, G);
+                    __builtin_amdgcn_sched_barrier(0);
+                    issue(s + NS);
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+                mma(F, 1);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        }
+        wait_vm_lgkm0<0>();
+    }
+
+#pragma unroll
+    for (int i = 0; i < C::MI; i++) {
+#pragma unroll
+        for (int e = 0; e < 16; e++) {
+            const int r = m0 + wm * C::TM + i * 32 + 8 * (e / 4) + 4 * lg + (e % 4);
+            if (r >= M) continue;
+            const float sc = args.scales[r];
+            float * crow = Cp + (int64_t)r * ldc;
+#pragma unroll
+            for (int j = 0; j < NJ; j++) {
+                const int n = n0 + COL0 + j * 32 + lr;
+                if (n < N) crow[n] = acc[i][j][e] * sc;
+            }
+        }
+    }
+}
+
+template <int BM, int BN0, int BN1, int DK, int NS, bool TL>
+__global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
+gemm_f16_cols_kernel(GemmArgs args) {
+    using C = ColsCfg<BM, BN0, BN1, DK, NS>;
+    extern __shared__ __align__(16) uint8_t smem[];
+    const int wave = threadIdx.x / WAVE;
+    if (wave / 4 == 0) cols_body<C, BN0, 0, TL>(args, smem, wave % 4);
+    else cols_body<C, BN1, BN0, TL>(args, smem, wave % 4);
+}
+
 // Zero the outputs of a split-K launch (a fill kernel rather than a memset, so the launch
 // sequence stays capturable).
 __global__ void zero_rows_kernel(GemmArgs args) {
@@ -617,7 +789,8 @@ hipError_t launch_pack_act_tiled(const float * X, int64_t ldx, int M, int K, uin
 // Tile configurations. The launcher picks one per call (choose_cfg); MI355X_GEMM_CFG=<id>
 // forces one (for tuning and for the tests, which run every configuration).
 //   0-3  register-staged kernel with the weight decoded into LDS: every weight type.
-//   4-14 LDS-DMA kernel: fp16 weights only (row-major or tiled). choose_cfg prices a launch as
+//   4-15 LDS-DMA kernel: fp16 weights only (row-major or tiled); 15 has wave columns of two
+//        widths (gemm_f16_cols_kernel). choose_cfg prices a launch as
 //        max(rounds * (ov_us + MFMA work of a block / tf_cu), L2->CU bytes of all blocks / bw):
 //        a block's own pace (pipeline fill and epilogue, then its per-CU MFMA rate) or the
 //        aggregate rate at which the L2s feed the CUs for that tile shape (bigger tiles fetch
@@ -648,6 +821,7 @@ static const CfgDesc kCfgs[] = {
     {256, 128, 1, 64, 5.8, 16.0, 8.75},     // 12: 8 waves of 64x64, 3 stages of 64
     {128, 256, 1, 64, 5.6, 15.0, 8.75},     // 13: 8 waves of 64x64, 3 stages of 64
     {64, 128, 1, 64, 2.4, 5.0, 12.5},       // 14: 4 waves of 32x64, 6 stages of 64
+    {256, 224, 1, 64, 6.4, 19.0, 7.4},      // 15: 8 waves of 64x128 and 64x96, 2 stages of 64
 };
 constexpr int FIRST_DMA_CFG = 4;
 constexpr int N_CFGS = sizeof(kCfgs) / sizeof(kCfgs[0]);
@@ -680,9 +854,24 @@ static hipError_t launch_f16(const GemmArgs & a, int nblocks, hipStream_t st) {
     return hipGetLastError();
 }
 
+template <int BM, int BN0, int BN1, int DK, int NS, bool TL>
+static hipError_t launch_cols(const GemmArgs & a, int nblocks, hipStream_t st) {
+    using C = ColsCfg<BM, BN0, BN1, DK, NS>;
+    auto kern = gemm_f16_cols_kernel<BM, BN0, BN1, DK, NS, TL>;
+    static bool attr = false;
+    if (!attr) {
+        hipError_t e = hipFuncSetAttribute((const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize, C::LDS);
+        if (e != hipSuccess) return e;
+        attr = true;
+    }
+    hipLaunchKernelGGL(kern, dim3(nblocks), dim3(C::THREADS), C::LDS, st, a);
+    return hipGetLastError();
+}
+
 template <bool TL>
 static hipError_t launch_dma_cfg(int cfg, const GemmArgs & a, int nblocks, hipStream_t st) {
     switch (cfg) {
+        case 15: return launch_cols<256, 128, 96, 64, 2, TL>(a, nblocks, st);
         case 4: return launch_f16<256, 256, 4, 2, 64, 2, 1, TL>(a, nblocks, st);
         case 5: return launch_f16<128, 128, 4, 2, 64, 4, 1, TL>(a, nblocks, st);
         case 6: return launch_f16<64, 128, 2, 2, 128, 3, 1, TL>(a, nblocks, st);

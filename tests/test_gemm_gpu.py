@@ -226,9 +226,9 @@ def test_pack_act_tiled_bitexact(mx):
 
 
 # Every tile configuration of mi355x_gemm, forced through MI355X_GEMM_CFG, on a ragged fused
-# launch (M and both N not multiples of any tile). Configurations 4-14 are the LDS-DMA kernels,
+# launch (M and both N not multiples of any tile). Configurations 4-15 are the LDS-DMA kernels,
 # which take fp16 weights only, row-major (F16) or tiled (F16_T).
-N_GEMM_CFGS = 15
+N_GEMM_CFGS = 16
 FIRST_DMA_CFG = 4
 F16_T = 0x101
 
