@@ -7,7 +7,8 @@
 //
 // Data flow (the host-buffer contract, ggml-rocket.cpp:7326-7331): tensors live in host memory;
 // each claimed op uploads its activations, runs on the device and writes dst back before
-// graph_compute returns. Weights are uploaded once into the HBM weight cache, keyed by
+// graph_compute returns. Large copies go through pinned staging slots, filled and drained by
+// n_threads copy workers while the DMA engine moves the neighbouring chunk. Weights are uploaded once into the HBM weight cache, keyed by
 // weight_key (name + content fingerprint), in the layout the kernels read:
 //   F16 / Q4_K   the ggml payload as-is;   Q8_0 / Q6_K   split into aligned planes;
 //   F32 / BF16   converted to fp16;        QUANT_RESIDENT=1   quant weights decoded to fp16.
@@ -16,9 +17,14 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <atomic>
+#include <condition_variable>
+#include <functional>
 #include <map>
+#include <memory>
 #include <mutex>
 #include <string>
+#include <thread>
 #include <unordered_map>
 #include <unordered_set>
 #include <vector>
@@ -102,6 +108,129 @@ struct DevBuf {
     }
 };
 
+// Host copy workers: one memcpy (or any job over disjoint parts) split across n threads, the
+// caller being one of them. Persistent threads, because a copy of one staging chunk takes about
+// as long as starting a thread.
+class CopyPool {
+public:
+    explicit CopyPool(int n) {
+        for (int i = 1; i < n; i++) th_.emplace_back([this] { work(); });
+    }
+    ~CopyPool() {
+        {
+            std::lock_guard<std::mutex> lk(mu_);
+            stop_ = true;
+        }
+        cv_.notify_all();
+        for (auto & t : th_) t.join();
+    }
+    int threads() const { return (int)th_.size() + 1; }
+    // part(i) for i in [0, parts), spread over the workers and the calling thread
+    void run(int parts, const std::function<void(int)> & part) {
+        if (th_.empty() || parts <= 1) {
+            for (int i = 0; i < parts; i++) part(i);
+            return;
+        }
+        {
+            std::lock_guard<std::mutex> lk(mu_);
+            job_ = &part;
+            parts_ = parts;
+            next_.store(0);
+            left_ = parts;
+            gen_++;
+        }
+        cv_.notify_all();
+        drain();
+        std::unique_lock<std::mutex> lk(mu_);
+        done_.wait(lk, [this] { return left_ == 0; });
+        job_ = nullptr;
+    }
+    void copy(void * dst, const void * src, size_t n) {
+        const size_t MIN_PART = (size_t)1 << 20;
+        const int parts = (int)std::min<size_t>((size_t)threads(), (n + MIN_PART - 1) / MIN_PART);
+        const size_t per = ((n + parts - 1) / parts + 63) & ~(size_t)63;
+        run(parts, [&](int i) {
+            const size_t o = (size_t)i * per;
+            if (o < n) memcpy((char *)dst + o, (const char *)src + o, std::min(per, n - o));
+        });
+    }
+
+private:
+    void drain() {
+        for (;;) {
+            const int i = next_.fetch_add(1);
+            if (i >= parts_) return;
+            (*job_)(i);
+            std::lock_guard<std::mutex> lk(mu_);
+            if (--left_ == 0) done_.notify_all();
+        }
+    }
+    void work() {
+        uint64_t seen = 0;
+        for (;;) {
+            {
+                std::unique_lock<std::mutex> lk(mu_);
+                cv_.wait(lk, [&] { return stop_ || gen_ != seen; });
+                if (stop_) return;
+                seen = gen_;
+            }
+            drain();
+        }
+    }
+    std::vector<std::thread> th_;
+    std::mutex mu_;
+    std::condition_variable cv_, done_;
+    const std::function<void(int)> * job_ = nullptr;
+    int parts_ = 0, left_ = 0;
+    std::atomic<int> next_{0};
+    uint64_t gen_ = 0;
+    bool stop_ = false;
+};
+
+// Pinned staging for the host <-> device copies of graph_compute. Host tensors are pageable
+// (ggml's CPU buffers), and a copy from pageable memory crawls through the runtime's own small
+// bounce buffer. A large copy is cut into CHUNK-sized pieces that cycle through NSLOT pinned
+// slots: the copy workers fill (or drain) one slot while the DMA engine moves another. Slots are
+// reused only after the event of their last DMA has completed.
+struct Stager {
+    static constexpr size_t CHUNK = (size_t)8 << 20;
+    static constexpr int NSLOT = 3;
+    void * slot[NSLOT] = {};
+    hipEvent_t ev[NSLOT] = {};
+    bool pending[NSLOT] = {};
+    bool ready = false;
+    int init() {
+        if (ready) return MI355X_OK;
+        for (int i = 0; i < NSLOT; i++) {
+            if (hipHostMalloc(&slot[i], CHUNK, hipHostMallocDefault) != hipSuccess ||
+                hipEventCreateWithFlags(&ev[i], hipEventDisableTiming) != hipSuccess) {
+                (void)hipGetLastError();
+                release();
+                return MI355X_E_DEVICE;
+            }
+        }
+        ready = true;
+        return MI355X_OK;
+    }
+    // wait until slot i's last DMA is done
+    int settle(int i) {
+        if (!pending[i]) return MI355X_OK;
+        pending[i] = false;
+        return hipEventSynchronize(ev[i]) == hipSuccess ? MI355X_OK : MI355X_E_DEVICE;
+    }
+    void release() {
+        for (int i = 0; i < NSLOT; i++) {
+            if (pending[i] && ev[i]) (void)hipEventSynchronize(ev[i]);
+            if (ev[i]) (void)hipEventDestroy(ev[i]);
+            if (slot[i]) (void)hipHostFree(slot[i]);
+            slot[i] = nullptr;
+            ev[i] = nullptr;
+            pending[i] = false;
+        }
+        ready = false;
+    }
+};
+
 struct WEntry {
     void * dev = nullptr;
     size_t bytes = 0;
@@ -135,6 +264,9 @@ struct ggml_backend_mi355x {
     std::unordered_set<std::string> moe_counted;   // stacks whose experts were counted resident
 
     Breaker brk_gemm, brk_fa, brk_moe;
+
+    Stager stage;                        // pinned slots of the host <-> device copies
+    std::unique_ptr<CopyPool> pool;      // n_threads copy workers, started with the device
 };
 
 namespace {
@@ -169,14 +301,87 @@ int sync(Ctx * c) {
     return hipStreamSynchronize(c->stream) == hipSuccess ? MI355X_OK : MI355X_E_DEVICE;
 }
 
-int h2d(Ctx * c, void * dst, const void * src, size_t n) {
-    if (!n) return MI355X_OK;
-    return hipMemcpyAsync(dst, src, n, hipMemcpyHostToDevice, c->stream) == hipSuccess ? MI355X_OK : MI355X_E_DEVICE;
+#define TRY_RC(x) do { const int _r = (x); if (_r != MI355X_OK) return _r; } while (0)
+
+// Copies below STAGE_MIN bytes go straight from pageable memory (the runtime's path is fine
+// there); larger ones through the pinned slots.
+constexpr size_t STAGE_MIN = (size_t)1 << 20;
+
+bool staging_on(Ctx * c) {
+    if (!c->pool) c->pool.reset(new CopyPool(c->n_threads));
+    return c->stage.init() == MI355X_OK;
 }
 
+// host -> device, enqueued on the stream; the host buffer may be reused once this returns
+int h2d(Ctx * c, void * dst, const void * src, size_t n) {
+    if (!n) return MI355X_OK;
+    if (n < STAGE_MIN || !staging_on(c))
+        return hipMemcpyAsync(dst, src, n, hipMemcpyHostToDevice, c->stream) == hipSuccess ? MI355X_OK
+                                                                                          : MI355X_E_DEVICE;
+    Stager & S = c->stage;
+    for (size_t o = 0, i = 0; o < n; o += Stager::CHUNK, i++) {
+        const int k = (int)(i % Stager::NSLOT);
+        const size_t len = std::min(Stager::CHUNK, n - o);
+        TRY_RC(S.settle(k));
+        c->pool->copy(S.slot[k], (const char *)src + o, len);
+        if (hipMemcpyAsync((char *)dst + o, S.slot[k], len, hipMemcpyHostToDevice, c->stream) != hipSuccess ||
+            hipEventRecord(S.ev[k], c->stream) != hipSuccess)
+            return MI355X_E_DEVICE;
+        S.pending[k] = true;
+    }
+    return MI355X_OK;
+}
+
+// Rows [0, rows) of a device matrix with row pitch `pitch` bytes, `width` bytes used per row,
+// to host memory through the pinned slots, handing each landed block of rows to `take(r0, r1,
+// host_rows)` (host_rows = the staged rows, `width` bytes apart). Returns when all rows are in.
+int d2h_rows(Ctx * c, const void * src, size_t pitch, size_t width, int64_t rows,
+             const std::function<void(int64_t, int64_t, const char *)> & take) {
+    Stager & S = c->stage;
+    const int64_t per = std::max<int64_t>(1, (int64_t)(Stager::CHUNK / width));
+    const int64_t nchunk = (rows + per - 1) / per;
+    auto launch = [&](int64_t i) -> int {
+        const int k = (int)(i % Stager::NSLOT);
+        const int64_t r0 = i * per, r1 = std::min(rows, r0 + per);
+        const hipError_t e = pitch == width
+            ? hipMemcpyAsync(S.slot[k], (const char *)src + r0 * pitch, (size_t)(r1 - r0) * width,
+                             hipMemcpyDeviceToHost, c->stream)
+            : hipMemcpy2DAsync(S.slot[k], width, (const char *)src + r0 * pitch, pitch, width, (size_t)(r1 - r0),
+                               hipMemcpyDeviceToHost, c->stream);
+        if (e != hipSuccess || hipEventRecord(S.ev[k], c->stream) != hipSuccess) return MI355X_E_DEVICE;
+        S.pending[k] = true;
+        return MI355X_OK;
+    };
+    for (int64_t i = 0; i < std::min<int64_t>(nchunk, Stager::NSLOT); i++) TRY_RC(launch(i));
+    for (int64_t i = 0; i < nchunk; i++) {
+        const int k = (int)(i % Stager::NSLOT);
+        TRY_RC(S.settle(k));
+        const int64_t r0 = i * per, r1 = std::min(rows, r0 + per);
+        take(r0, r1, (const char *)S.slot[k]);
+        if (i + Stager::NSLOT < nchunk) TRY_RC(launch(i + Stager::NSLOT));
+    }
+    return MI355X_OK;
+}
+
+// device -> host; returns when the bytes are in `dst` (it synchronizes on the copies)
 int d2h(Ctx * c, void * dst, const void * src, size_t n) {
     if (!n) return MI355X_OK;
-    return hipMemcpyAsync(dst, src, n, hipMemcpyDeviceToHost, c->stream) == hipSuccess ? MI355X_OK : MI355X_E_DEVICE;
+    if (n < STAGE_MIN || !staging_on(c)) {
+        if (hipMemcpyAsync(dst, src, n, hipMemcpyDeviceToHost, c->stream) != hipSuccess) return MI355X_E_DEVICE;
+        return hipStreamSynchronize(c->stream) == hipSuccess ? MI355X_OK : MI355X_E_DEVICE;
+    }
+    const size_t W = 1 << 16;   // stage as rows of 64 KB (+ one short tail)
+    const int64_t full = (int64_t)(n / W);
+    TRY_RC(d2h_rows(c, src, W, W, full, [&](int64_t r0, int64_t r1, const char * h) {
+        c->pool->copy((char *)dst + r0 * W, h, (size_t)(r1 - r0) * W);
+    }));
+    if (n % W) {
+        if (hipMemcpyAsync((char *)dst + full * W, (const char *)src + full * W, n % W, hipMemcpyDeviceToHost,
+                           c->stream) != hipSuccess)
+            return MI355X_E_DEVICE;
+        return hipStreamSynchronize(c->stream) == hipSuccess ? MI355X_OK : MI355X_E_DEVICE;
+    }
+    return MI355X_OK;
 }
 
 #define TRY(x) do { const int _rc = (x); if (_rc != MI355X_OK) return _rc; } while (0)
@@ -303,18 +508,39 @@ int mul_mat_device(Ctx * c, const std::vector<mi355x_tensor *> & grp, bool want_
         TRY(mi355x_pack_act((const float *)c->act.p, K, M, K, (uint16_t *)c->a16.p, (float *)c->scales.p, c->stream));
     TRY(mi355x_gemm(ws[0].dev_type, (const uint16_t *)c->a16.p, (const float *)c->scales.p, M, K, outs, (int)grp.size(),
                     c->stream));
-    // dst[i] is [N_i, M] contiguous: copy its column block row by row
-    col = 0;
-    for (auto * d : grp) {
-        const int64_t N = d->src[0]->ne[1];
-        if (grp.size() == 1) {
-            TRY(d2h(c, d->data, c->out.p, (size_t)M * N * 4));
-        } else if (hipMemcpy2DAsync(d->data, (size_t)N * 4, (const float *)c->out.p + col, (size_t)ntot * 4,
-                                    (size_t)N * 4, (size_t)M, hipMemcpyDeviceToHost, c->stream) != hipSuccess) {
-            return MI355X_E_DEVICE;
-        }
-        col += N;
+    // dst[i] is [N_i, M] contiguous: one member takes the output as is; a group's outputs come
+    // back as whole rows of the concatenated [M][ntot] and are split into the members' column
+    // blocks on the host
+    if (grp.size() == 1) {
+        TRY(d2h(c, grp[0]->data, c->out.p, (size_t)M * ntot * 4));
+        return sync(c);
     }
+    if ((size_t)M * ntot * 4 < STAGE_MIN || (size_t)ntot * 4 > Stager::CHUNK || !staging_on(c)) {
+        col = 0;
+        for (auto * d : grp) {
+            const int64_t N = d->src[0]->ne[1];
+            if (hipMemcpy2DAsync(d->data, (size_t)N * 4, (const float *)c->out.p + col, (size_t)ntot * 4,
+                                 (size_t)N * 4, (size_t)M, hipMemcpyDeviceToHost, c->stream) != hipSuccess)
+                return MI355X_E_DEVICE;
+            col += N;
+        }
+        return sync(c);
+    }
+    TRY(d2h_rows(c, c->out.p, (size_t)ntot * 4, (size_t)ntot * 4, M, [&](int64_t r0, int64_t r1, const char * h) {
+        const int64_t nr = r1 - r0;
+        const int parts = (int)std::min<int64_t>(c->pool->threads(), nr);
+        c->pool->run(parts, [&](int pi) {
+            for (int64_t r = r0 + nr * pi / parts; r < r0 + nr * (pi + 1) / parts; r++) {
+                int64_t cc = 0;
+                for (auto * d : grp) {
+                    const int64_t N = d->src[0]->ne[1];
+                    memcpy((char *)d->data + (size_t)r * N * 4, h + (size_t)(r - r0) * ntot * 4 + (size_t)cc * 4,
+                           (size_t)N * 4);
+                    cc += N;
+                }
+            }
+        });
+    }));
     return sync(c);
 }
 
@@ -497,6 +723,8 @@ MI355X_API bool ggml_backend_is_mi355x(ggml_backend_mi355x_t c) {
 MI355X_API void ggml_backend_mi355x_free(ggml_backend_mi355x_t c) {
     if (!c) return;
     if (c->stream) (void)hipStreamSynchronize(c->stream);
+    c->stage.release();
+    c->pool.reset();
     for (auto & kv : c->wcache) (void)hipFree(kv.second.dev);
     if (!c->wcache.empty())
         logi("[weights] %zu weights resident, %.1f MB of HBM\n", c->wcache.size(), (double)c->cache_used / (1 << 20));

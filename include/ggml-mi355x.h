@@ -105,9 +105,10 @@ MI355X_API ggml_backend_mi355x_t ggml_backend_mi355x_init(void);
 MI355X_API void ggml_backend_mi355x_free(ggml_backend_mi355x_t backend);
 /* True if `backend` is an instance of this backend (GUID check, 7241-7246). */
 MI355X_API bool ggml_backend_is_mi355x(ggml_backend_mi355x_t backend);
-/* Kept for API compatibility with ggml_backend_rocket_set_n_threads: the value (clamped to
- * 1-8, with a warning) is stored and reported; the GPU path does not fan out host workers. A
- * call after the first compute warns and changes nothing, as the reference's does. */
+/* ggml_backend_rocket_set_n_threads (ggml-rocket.cpp:8185-8217): the number of host threads
+ * (clamped to 1-8, with a warning) that fill and drain the pinned staging of host <-> device
+ * copies, as the reference's value sizes its host worker pool. A call after the first compute
+ * warns and changes nothing, as the reference's does. */
 MI355X_API void ggml_backend_mi355x_set_n_threads(ggml_backend_mi355x_t backend, int n_threads);
 MI355X_API int  ggml_backend_mi355x_get_n_threads(ggml_backend_mi355x_t backend);
 
