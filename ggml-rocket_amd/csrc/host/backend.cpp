@@ -799,8 +799,53 @@ MI355X_API void ggml_backend_mi355x_inject_faults(ggml_backend_mi355x_t c, const
     if (b) b->inject = n < 0 ? 0 : n;
 }
 
+static int graph_compute_nodes(ggml_backend_mi355x_t c, mi355x_tensor * const * nodes, int n_nodes);
+
+// Repacked weights with registered original bytes (ggml-rocket.cpp:7005-7047): for this call,
+// each such source descriptor reads the registered bytes (a view at its offset). Only the
+// descriptors change, never the host's tensors, so a CPU split running meanwhile still reads its
+// repacked copy. A source that needs bytes and has none fails the call before any route reads
+// it; a view node reads nothing and does not count as a check of its source.
 MI355X_API int ggml_backend_mi355x_graph_compute(ggml_backend_mi355x_t c, mi355x_tensor * const * nodes, int n_nodes) {
     if (!ggml_backend_is_mi355x(c) || (n_nodes > 0 && !nodes)) return MI355X_STATUS_FAILED;
+    if (registered_sources() == 0) return graph_compute_nodes(c, nodes, n_nodes);
+    struct Saved {
+        mi355x_tensor * t;
+        void * data;
+        int32_t kind;
+    };
+    std::vector<Saved> swapped;
+    std::unordered_set<const mi355x_tensor *> seen;
+    auto restore = [&] {
+        for (auto it = swapped.rbegin(); it != swapped.rend(); ++it) {
+            it->t->data = it->data;
+            it->t->buffer_kind = it->kind;
+        }
+    };
+    for (int i = 0; i < n_nodes; i++) {
+        mi355x_tensor * node = nodes[i];
+        if (!node || node->op == MI355X_OP_NONE || is_view_op(node->op)) continue;
+        for (int j = 0; j < MI355X_MAX_SRC; j++) {
+            mi355x_tensor * s = node->src[j];
+            if (!s || !tensor_needs_source(s) || !seen.insert(s).second) continue;
+            const void * p = tensor_source(s);
+            if (!p) {
+                logw("source %s of %s lives in a buffer this backend cannot read and has no registered "
+                     "original bytes\n", s->name, node->name);
+                restore();
+                return MI355X_STATUS_FAILED;
+            }
+            swapped.push_back({s, s->data, s->buffer_kind});
+            s->data = const_cast<void *>(p);
+            s->buffer_kind = MI355X_BUF_HOST;
+        }
+    }
+    const int st = graph_compute_nodes(c, nodes, n_nodes);
+    restore();
+    return st;
+}
+
+static int graph_compute_nodes(ggml_backend_mi355x_t c, mi355x_tensor * const * nodes, int n_nodes) {
     c->started = true;
     std::vector<bool> done((size_t)(n_nodes > 0 ? n_nodes : 0), false);
     for (int i = 0; i < n_nodes; i++) {

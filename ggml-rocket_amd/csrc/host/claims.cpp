@@ -10,8 +10,10 @@
 //     types are declined rather than claimed and then computed on the host;
 //   * FLASH_ATTN_EXT: head dims 64 and 128 with D == DV, and the strides the kernel reads.
 
+#include <atomic>
 #include <mutex>
 #include <string.h>
+#include <string>
 #include <unordered_map>
 #include <unordered_set>
 
@@ -39,12 +41,68 @@ bool prec_declines(const mi355x_tensor * op) {
     return false;
 }
 
+// ---- repacked-weight sources (ggml-rocket.cpp:6965-7047, API.md:280-314) ----------------------
+// ggml-cpu's CPU_REPACK buffer holds a quantized weight in an interleaved layout no route here
+// reads. A host that keeps the original bytes (its mapped GGUF range) registers them for the
+// tensor; ops on it are then claimed and computed from those bytes, and the CPU keeps its
+// repacked copy for decode. The registry is process-wide, as placement has no backend handle.
+// An entry is keyed by the tensor's own data address (its place in the repack buffer) and is
+// used only while the tensor's name and byte size still match it, which catches a tensor struct
+// reused for another weight, not the same model reloaded into it: the host unregisters first.
+namespace {
+struct WSrc {
+    const void * src;
+    size_t nbytes;
+    std::string name;
+};
+std::mutex g_wsrc_mu;
+std::unordered_map<const void *, WSrc> g_wsrc;
+std::atomic<size_t> g_wsrc_count{0};
+
+bool is_view_op(int op) {
+    return op == MI355X_OP_VIEW || op == MI355X_OP_RESHAPE || op == MI355X_OP_PERMUTE || op == MI355X_OP_TRANSPOSE;
+}
+
+// the tensor a view reads, and the byte offset of the view in it
+const mi355x_tensor * view_base(const mi355x_tensor * t, size_t * offs) {
+    const mi355x_tensor * b = t;
+    while (is_view_op(b->op) && b->src[0]) b = b->src[0];
+    *offs = (b->data && t->data) ? (size_t)((const char *)t->data - (const char *)b->data) : 0;
+    return b;
+}
+
+}  // namespace
+
+bool tensor_needs_source(const mi355x_tensor * t) {
+    size_t offs;
+    const mi355x_tensor * b = view_base(t, &offs);
+    return b->buffer_kind == MI355X_BUF_REPACK || b->buffer_kind == MI355X_BUF_OTHER;
+}
+
+const void * tensor_source(const mi355x_tensor * t) {
+    if (g_wsrc_count.load(std::memory_order_acquire) == 0) return nullptr;
+    size_t offs;
+    const mi355x_tensor * b = view_base(t, &offs);
+    std::lock_guard<std::mutex> lk(g_wsrc_mu);
+    auto it = g_wsrc.find(b->data);
+    if (it == g_wsrc.end()) return nullptr;
+    if (it->second.nbytes != nbytes(b) || it->second.name != std::string(b->name, strnlen(b->name, MI355X_MAX_NAME)))
+        return nullptr;
+    if (offs + nbytes(t) > it->second.nbytes) return nullptr;
+    return (const char *)it->second.src + offs;
+}
+
+size_t registered_sources() { return g_wsrc_count.load(std::memory_order_acquire); }
+
 // ---- weight identity ---------------------------------------------------------------------------
 // A sampled content fingerprint: sixteen 64-byte windows spread over the tensor (all of it when
-// smaller), mixed with the byte size and type. Changes when a weight's bytes are replaced.
+// smaller), mixed with the byte size and type. Changes when a weight's bytes are replaced. A
+// repacked weight is fingerprinted over its registered original bytes, so placement (data at the
+// repacked copy) and compute (data pointed at the original) agree on its key.
 static uint64_t fingerprint(const mi355x_tensor * t) {
     const size_t n = nbytes(t);
-    const unsigned char * p = (const unsigned char *)t->data;
+    const void * src = tensor_needs_source(t) ? tensor_source(t) : nullptr;
+    const unsigned char * p = (const unsigned char *)(src ? src : t->data);
     uint64_t h = 0xcbf29ce484222325ULL ^ ((uint64_t)n * 0x9E3779B97F4A7C15ULL) ^ ((uint64_t)(uint32_t)t->type << 48);
     auto mix = [&h](uint64_t x) {
         h ^= x + 0x632BE59BD9B4E019ULL + (h << 6) + (h >> 2);
@@ -317,9 +375,10 @@ extern "C" {
 
 MI355X_API bool ggml_backend_mi355x_supports_op(const mi355x_tensor * op) {
     if (!op) return false;
-    // a weight in a buffer this backend cannot read as ggml blocks stays on the CPU
+    // a source in a buffer this backend cannot read as ggml blocks (CPU_REPACK, another device)
+    // stays on the CPU unless its original bytes are registered (ggml-rocket.cpp:7036-7043)
     for (int i = 0; i < MI355X_MAX_SRC; i++)
-        if (op->src[i] && op->src[i]->buffer_kind == MI355X_BUF_REPACK) return false;
+        if (op->src[i] && tensor_needs_source(op->src[i]) && !tensor_source(op->src[i])) return false;
     switch (op->op) {
         case MI355X_OP_NONE:
         case MI355X_OP_RESHAPE:
@@ -340,7 +399,15 @@ MI355X_API bool ggml_backend_mi355x_offload_op(const mi355x_tensor * op) {
 }
 
 MI355X_API bool ggml_backend_mi355x_supports_buft(int buffer_kind) {
-    return buffer_kind == MI355X_BUF_HOST;
+    return buffer_kind == MI355X_BUF_HOST || buffer_kind == MI355X_BUF_REPACK;
+}
+
+MI355X_API void ggml_backend_mi355x_register_weight_source(const mi355x_tensor * t, const void * data, size_t nbytes) {
+    if (!t || !t->data) return;
+    std::lock_guard<std::mutex> lk(g_wsrc_mu);
+    if (!data) g_wsrc.erase(t->data);
+    else g_wsrc[t->data] = WSrc{data, nbytes, std::string(t->name, strnlen(t->name, MI355X_MAX_NAME))};
+    g_wsrc_count.store(g_wsrc.size(), std::memory_order_release);
 }
 
 MI355X_API int ggml_backend_mi355x_weight_key(const mi355x_tensor * t, char * out, int cap) {

@@ -20,6 +20,11 @@ int64_t row_bytes(int type, int64_t n);   // bytes of n values, -1 if n is not w
 bool is_contiguous(const mi355x_tensor * t);
 int64_t nelements(const mi355x_tensor * t);
 size_t nbytes(const mi355x_tensor * t);
+// repacked-weight sources (claims.cpp): whether t's bytes are in a buffer no route reads, the
+// registered original bytes for it (nullptr if none match), and how many are registered
+bool tensor_needs_source(const mi355x_tensor * t);
+const void * tensor_source(const mi355x_tensor * t);
+size_t registered_sources();
 // The weight types the device path decodes (HBM layouts of mx_weights.h, after a conversion to
 // fp16 for F32 and BF16).
 bool device_weight_type(int type);

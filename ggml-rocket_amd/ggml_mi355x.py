@@ -319,6 +319,7 @@ def _bind_host(L):
                                                   ctypes.POINTER(lng)]
     L.ggml_backend_mi355x_inject_faults.argtypes = [vp, ctypes.c_char_p, i32]
     L.ggml_backend_mi355x_weight_key.argtypes = [pt, ctypes.c_char_p, i32]
+    L.ggml_backend_mi355x_register_weight_source.argtypes = [pt, vp, sz]
     L.ggml_backend_mi355x_parse_mb.restype = ctypes.c_bool
     L.ggml_backend_mi355x_parse_mb.argtypes = [ctypes.c_char_p, ctypes.POINTER(sz)]
     L._host_bound = True
@@ -464,6 +465,23 @@ class Backend:
 
     def inject_faults(self, group, n):
         self.L.ggml_backend_mi355x_inject_faults(self.h, group.encode(), n)
+
+
+_registered = {}
+
+
+def register_weight_source(t, src):
+    """The original bytes of a weight whose tensor sits in CPU_REPACK (numpy array, or None to
+    unregister); the array is kept alive while registered."""
+    import numpy as np
+    key = ctypes.addressof(t)
+    if src is None:
+        host().ggml_backend_mi355x_register_weight_source(ctypes.byref(t), None, 0)
+        _registered.pop(key, None)
+        return
+    a = np.ascontiguousarray(src).view(np.uint8).reshape(-1)
+    _registered[key] = a
+    host().ggml_backend_mi355x_register_weight_source(ctypes.byref(t), ctypes.c_void_p(a.ctypes.data), a.nbytes)
 
 
 def supports_op(t):

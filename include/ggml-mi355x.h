@@ -91,10 +91,19 @@ MI355X_API void ggml_backend_mi355x_get_memory(size_t * free, size_t * total);
  * supports_op: the claim rules of ggml-rocket.cpp:7415-7772 (MUL_MAT 7424-7496, precision
  * declarations 7334-7404, MUL_MAT_ID 7497-7653 with the MoE residency pre-flight 6198-6289,
  * FLASH_ATTN_EXT 7654-7768). offload_op: (MUL_MAT or MUL_MAT_ID) and supports_op (7820-7827).
- * supports_buft: host buffers (7795-7797). */
+ * supports_buft: host buffers and CPU_REPACK (7795-7797). */
 MI355X_API bool ggml_backend_mi355x_supports_op(const mi355x_tensor * op);
 MI355X_API bool ggml_backend_mi355x_offload_op(const mi355x_tensor * op);
 MI355X_API bool ggml_backend_mi355x_supports_buft(int buffer_kind);
+
+/* ggml_backend_rocket_register_weight_source (ggml-rocket.cpp:6993-7003, the registry's
+ * "…register_weight_source" proc address, API.md:280-314): registers the original (GGUF) bytes
+ * of a weight whose tensor lives in CPU_REPACK; data == NULL unregisters it. `t` describes the
+ * tensor as placement sees it (its data = its place in the repack buffer, its name, its ne/nb).
+ * While registered with a matching name and byte size, supports_buft / supports_op claim ops
+ * on it and graph_compute reads the registered bytes (through a view too, at its offset). The
+ * host keeps the bytes mapped while the tensor lives and unregisters before freeing it. */
+MI355X_API void ggml_backend_mi355x_register_weight_source(const mi355x_tensor * t, const void * data, size_t nbytes);
 
 /* ---- backend instance (ggml-rocket.h:25-91) ------------------------------------------------ */
 

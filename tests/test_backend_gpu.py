@@ -261,3 +261,39 @@ def test_injected_device_failure_falls_back(be):
     got2 = run_mul_mat(be, mx.F16, K, N, M, W16, Xf, "blk.inject.weight")
     mk.check("after the injected failure")
     bars(ref, got2, M, N, "device again")
+
+
+def test_repacked_weight_computes_from_registered_bytes(be):
+    """test-rocket-internals.cpp:564-655 and API.md:280-314 on the device: a Q4_K weight whose
+    tensor bytes are ggml-cpu's repacked copy (here: bytes no decoder would accept as the weight)
+    computes from its registered original bytes; unregistered, the split fails before any route
+    reads the repacked layout, also when a view node of the weight comes first."""
+    K, N, M = 512, 256, 512
+    W = O.fill_normal((N, K), 960, 0.0, 0.02)
+    Q = O.quantize(O.Q4_K, W)
+    Xf = O.fill_normal((M, K), 961)
+    ref = O.mul_mat(O.Q4_K, Q, Xf, N, K)
+    g = mx.Graph()
+    Wt = g._new(mx.Q4_K, [K, N], name="blk.r.ffn_down.weight",
+                data=np.full(Q.nbytes, 0x5A, dtype=np.uint8))          # the "repacked" copy
+    Wt.buffer_kind = mx.BUF_REPACK
+    Xt = g.new_tensor(mx.F32, [K, M])
+    g.set(Xt, Xf)
+    d = g.mul_mat(Wt, Xt)
+    other = g.new_tensor(mx.F32, [64, 64], "x")
+    try:
+        mx.register_weight_source(Wt, Q)
+        assert mx.supports_op(d)
+        mk = Mark(be)
+        assert be.compute([d]) == mx.STATUS_SUCCESS
+        mk.check("repacked weight, registered source")
+        got = g.get(d, np.float32, (M, N))
+        assert Wt.buffer_kind == mx.BUF_REPACK and Wt.data == g.keep[0].ctypes.data   # restored
+        bars(ref, got, M, N, "repacked Q4_K from registered bytes")
+        mx.register_weight_source(Wt, None)
+        mx.register_weight_source(other, np.zeros(64 * 64, dtype=np.float32))   # registry not empty
+        view = g.permute_view(Wt, [K, N // 2, 1, 1], [Wt.nb[0], Wt.nb[1], Wt.nb[1] * N, Wt.nb[1] * N])
+        assert be.compute([view, d]) == mx.STATUS_FAILED
+    finally:
+        mx.register_weight_source(Wt, None)
+        mx.register_weight_source(other, None)

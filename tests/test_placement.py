@@ -76,17 +76,57 @@ def test_placement(label, want, fn):
 
 
 def test_supports_buft():
+    """ggml-rocket.cpp:7795-7797: host buffers and CPU_REPACK (whose weights are claimed only
+    through registered original bytes)."""
     assert mx.host().ggml_backend_mi355x_supports_buft(mx.BUF_HOST)
-    assert not mx.host().ggml_backend_mi355x_supports_buft(mx.BUF_REPACK)
+    assert mx.host().ggml_backend_mi355x_supports_buft(mx.BUF_REPACK)
     assert not mx.host().ggml_backend_mi355x_supports_buft(mx.BUF_OTHER)
 
 
-def test_repacked_weight_declined():
-    g = mx.Graph(alloc=False)
-    W = g.new_tensor(mx.Q4_K, [K, N])
+def _repacked_q4k(g, name="blk.0.ffn_down.weight"):
+    """A Q4_K weight in a CPU_REPACK buffer: its own bytes (the repacked copy) differ from the
+    original bytes a host would register."""
+    import numpy as np
+    nb = K // 256 * 144 * N
+    W = g._new(mx.Q4_K, [K, N], name=name, data=np.full(nb, 0x5A, dtype=np.uint8))
     W.buffer_kind = mx.BUF_REPACK
+    orig = np.random.default_rng(7).integers(0, 256, nb, dtype=np.uint8)
+    return W, orig
+
+
+def test_repacked_weight_sources():
+    """test-rocket-internals.cpp:564-655: a repacked weight is claimed only through its
+    registered original bytes; name and size must match; unregistering declines it again; the
+    weight key is the same in placement and in compute."""
+    import ctypes
+    g = mx.Graph()
+    W, orig = _repacked_q4k(g)
     X = g.new_tensor(mx.F32, [K, MQ])
-    assert not mx.supports_op(g.mul_mat(W, X))
+    mm = g.mul_mat(W, X)
+    try:
+        assert not mx.supports_op(mm), "an unregistered repacked weight's MUL_MAT is declined"
+        mx.register_weight_source(W, orig)
+        assert mx.supports_op(mm), "a registered weight's MUL_MAT is claimed"
+        k_place = mx.weight_key(W)
+        repacked, kind = W.data, W.buffer_kind
+        W.data, W.buffer_kind = orig.ctypes.data, mx.BUF_HOST      # what graph_compute does
+        k_compute = mx.weight_key(W)
+        W.data, W.buffer_kind = repacked, kind
+        assert k_place and k_place == k_compute, "one key in placement and in compute"
+        W.name = b"blk.1.ffn_down.weight"
+        assert not mx.supports_op(mm), "a renamed tensor does not use the old registration"
+        W.name = b"blk.0.ffn_down.weight"
+        assert mx.supports_op(mm)
+        mx.register_weight_source(W, orig[:-1])
+        assert not mx.supports_op(mm), "a registration of another size is not used"
+        mx.register_weight_source(W, orig)
+        half = g.permute_view(W, [K, N // 2, 1, 1], [W.nb[0], W.nb[1], W.nb[1] * (N // 2), W.nb[1] * (N // 2)],
+                              offset=W.nb[1] * (N // 2))
+        assert mx.supports_op(g.mul_mat(half, X)) is False   # a view is not a leaf weight
+        mx.register_weight_source(W, None)
+        assert not mx.supports_op(mm), "unregistered: declined again"
+    finally:
+        mx.register_weight_source(W, None)
 
 
 def _child(mode, env):
