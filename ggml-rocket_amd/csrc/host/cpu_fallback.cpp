@@ -83,6 +83,17 @@ bool decode_row_f32(int type, const void * src, float * y, int64_t n) {
                 }
             }
             return true;
+        case MI355X_TYPE_MXFP4:   // kvalues_mxfp4 (E2M1 doubled) times 2^(e-128), ggml-common.h
+            for (int64_t b = 0; b < n / 32; b++, x += 17) {
+                static const int8_t kv[16] = {0, 1, 2, 3, 4, 6, 8, 12, 0, -1, -2, -3, -4, -6, -8, -12};
+                const uint32_t eb = x[0] < 2 ? (0x00200000u << x[0]) : ((uint32_t)(x[0] - 1) << 23);
+                float d;
+                memcpy(&d, &eb, 4);
+                for (int l = 0; l < 16; l++) y[l] = (float)kv[x[1 + l] & 15] * d;
+                for (int l = 0; l < 16; l++) y[16 + l] = (float)kv[x[1 + l] >> 4] * d;
+                y += 32;
+            }
+            return true;
         default: return false;
     }
 }

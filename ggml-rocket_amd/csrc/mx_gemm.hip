@@ -11,7 +11,7 @@
 //                 Up to four weights that share A run in one launch over their concatenated N
 //                 (the fused QKV / gate-up groups of ggml-rocket.cpp:4956-5160).
 //   dequant_f16   a weight panel -> fp16 [rows][K] (the resident-fp16 form, "prepacked-q").
-//   pack_weight   a ggml Q8_0 / Q6_K payload -> its split HBM layout (mx_weights.h).
+//   pack_weight   a ggml Q8_0 / Q6_K / MXFP4 payload -> its split HBM layout (mx_weights.h).
 //
 // Two GEMM kernels: a register-staged one that decodes any weight format into LDS (gemm_kernel),
 // and for fp16 weights one that moves both operands into LDS by DMA (gemm_f16_kernel). The
@@ -748,6 +748,19 @@ __global__ void pack_q8_0_kernel(const uint8_t * __restrict__ src, int64_t rows,
     d[1] = s[1];
 }
 
+// ggml MXFP4 -> split planes. One thread per 17-byte block.
+__global__ void pack_mxfp4_kernel(const uint8_t * __restrict__ src, int64_t rows, int64_t K,
+                                  uint8_t * __restrict__ dst) {
+    const int64_t nb = K / 32;
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= rows * nb) return;
+    const int64_t row = i / nb, b = i % nb;
+    const uint8_t * s = src + i * 17;
+    uint8_t * qs = dst + row * (K / 2) + b * 16;
+    for (int l = 0; l < 16; l++) qs[l] = s[1 + l];
+    dst[rows * (K / 2) + row * nb + b] = s[0];
+}
+
 // ggml Q6_K -> split planes. One thread per block.
 __global__ void pack_q6_k_kernel(const uint8_t * __restrict__ src, int64_t rows, int64_t K,
                                  uint8_t * __restrict__ dst) {
@@ -995,6 +1008,7 @@ hipError_t launch_gemm(int wt, const GemmArgs & a_in, int /*unused*/, hipStream_
         case T_Q8_0: return launch_cfg<T_Q8_0>(cfg, a, nblocks, st);
         case T_Q4_K: return launch_cfg<T_Q4_K>(cfg, a, nblocks, st);
         case T_Q6_K: return launch_cfg<T_Q6_K>(cfg, a, nblocks, st);
+        case T_MXFP4: return launch_cfg<T_MXFP4>(cfg, a, nblocks, st);
         default: return hipErrorInvalidValue;
     }
 }
@@ -1010,6 +1024,7 @@ static hipError_t launch_dequant(int wt, const void * W, int64_t rows, int64_t K
         case T_Q8_0: hipLaunchKernelGGL((dequant_f16_kernel<T_Q8_0, TL>), grid, dim3(256), 0, st, w, rows, K, out); break;
         case T_Q4_K: hipLaunchKernelGGL((dequant_f16_kernel<T_Q4_K, TL>), grid, dim3(256), 0, st, w, rows, K, out); break;
         case T_Q6_K: hipLaunchKernelGGL((dequant_f16_kernel<T_Q6_K, TL>), grid, dim3(256), 0, st, w, rows, K, out); break;
+        case T_MXFP4: hipLaunchKernelGGL((dequant_f16_kernel<T_MXFP4, TL>), grid, dim3(256), 0, st, w, rows, K, out); break;
         default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
@@ -1049,6 +1064,12 @@ hipError_t launch_pack_weight(int wt, const void * src, int64_t rows, int64_t K,
             const int64_t n = rows * (K / 256);
             if (n <= 0) return hipSuccess;
             hipLaunchKernelGGL(pack_q6_k_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, s, rows, K, d);
+            return hipGetLastError();
+        }
+        case T_MXFP4: {
+            const int64_t n = rows * (K / 32);
+            if (n <= 0) return hipSuccess;
+            hipLaunchKernelGGL(pack_mxfp4_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, s, rows, K, d);
             return hipGetLastError();
         }
         default: return hipErrorInvalidValue;

@@ -218,6 +218,7 @@ hipError_t launch_moe(int wt, const MoeArgs & a, hipStream_t st) {
         case T_Q8_0: hipLaunchKernelGGL(moe_gemm_kernel<T_Q8_0>, dim3((unsigned)nb), dim3(MOE_THREADS), lds, st, a); break;
         case T_Q4_K: hipLaunchKernelGGL(moe_gemm_kernel<T_Q4_K>, dim3((unsigned)nb), dim3(MOE_THREADS), lds, st, a); break;
         case T_Q6_K: hipLaunchKernelGGL(moe_gemm_kernel<T_Q6_K>, dim3((unsigned)nb), dim3(MOE_THREADS), lds, st, a); break;
+        case T_MXFP4: hipLaunchKernelGGL(moe_gemm_kernel<T_MXFP4>, dim3((unsigned)nb), dim3(MOE_THREADS), lds, st, a); break;
         default: return hipErrorInvalidValue;
     }
     return hipGetLastError();

@@ -12,12 +12,15 @@
 //   Q6_K  split into four planes for the same reason (a ggml block is 210 B): ql [rows][K/2]
 //         at 0, qh [rows][K/4] at rows*K/2, scales int8 [rows][K/16] at rows*K*3/4, then
 //         d fp16 [rows][K/256] at rows*K*13/16.
+//   MXFP4 split into two planes (a ggml block is 17 B: { u8 e; u8 qs[16]; } per 32 values):
+//         qs [rows][K/2] at 0 (16 bytes per block), then e [rows][K/32] at rows*K/2.
 // The split layouts hold exactly the ggml bytes, re-ordered; their size equals the ggml size.
 //
 // Decoding follows ggml's dequantizers value for value (the to_float contract the reference
 // uses at ggml-rocket.cpp:3894-3906): Q8_0 y = d*q; Q4_K y = (d*sc)*q - dmin*m; Q6_K
-// y = (d*sc)*(q-32). Each product and difference is rounded on its own, then the f32 result is
-// rounded once to fp16 (ggml_fp32_to_fp16_row, 3907).
+// y = (d*sc)*(q-32); MXFP4 y = kvalues_mxfp4[code] * 2^(e-128) (E2M1 codes doubled to integers,
+// the E8M0 scale halved: GGML_E8M0_TO_FP32_HALF), exact in f32. Each product and difference is
+// rounded on its own, then the f32 result is rounded once to fp16 (ggml_fp32_to_fp16_row, 3907).
 //
 // Every loader issues its loads unconditionally from an address inside the panel (the caller
 // passes a valid row; a K position past the end reads position 0 instead) and remembers whether
@@ -36,6 +39,7 @@ __host__ __device__ inline int64_t packed_weight_bytes(int wt, int64_t rows, int
         case T_Q8_0: return rows * K + rows * (K / 32) * 2;
         case T_Q4_K: return rows * (K / 256) * 144;
         case T_Q6_K: return rows * (K / 256) * 210;
+        case T_MXFP4: return rows * (K / 32) * 17;
         default: return -1;
     }
 }
@@ -61,6 +65,13 @@ __device__ __forceinline__ void zero_out(bool ok, u32x4 out[4]) {
 #pragma unroll
         for (int i = 0; i < 4; i++) out[i] = u32x4{0, 0, 0, 0};
     }
+}
+
+// The E2M1 value of an MXFP4 code, doubled (kvalues_mxfp4 of ggml-common.h): bit 3 is the sign,
+// the low 3 bits index 0 1 2 3 4 6 8 12.
+__device__ __forceinline__ int mxfp4_code(uint32_t c) {
+    const int mag = (int)((0xC8643210u >> (4 * (c & 7u))) & 15u);
+    return (c & 8u) ? -mag : mag;
 }
 
 // Global-load stage of one thread's share of a BK=64 weight tile: 32 consecutive-in-format
@@ -114,6 +125,46 @@ template <> struct WLoad<T_Q8_0> {
             for (int b = 0; b < 4; b++) f[b] = mul_rn(df, (float)(int8_t)((word >> (8 * b)) & 0xFFu));
             o[2 * w] = pack2h(f[0], f[1]);
             o[2 * w + 1] = pack2h(f[2], f[3]);
+        }
+#pragma unroll
+        for (int i = 0; i < 4; i++) out[i] = u32x4{o[4 * i], o[4 * i + 1], o[4 * i + 2], o[4 * i + 3]};
+        zero_out(ok, out);
+        run0 = 32 * u;
+        run1 = 32 * u + 16;
+    }
+};
+
+// MXFP4: one 32-value block per item (the same slab halves as Q8_0).
+template <> struct WLoad<T_MXFP4> {
+    u32x4 qs;    // 16 bytes: weight j in the low nibble of byte j, weight j + 16 in the high one
+    uint8_t e;
+    bool ok;
+    __device__ __forceinline__ void load(const uint8_t * W, int64_t rows, int64_t K, int64_t row,
+                                         int64_t k0, int u, bool ok_row) {
+        int64_t k = k0 + 32 * u;
+        ok = ok_row && k < K;
+        k = k < K ? k : 0;
+        qs = *(const u32x4 *)(W + row * (K / 2) + k / 2);
+        e = W[rows * (K / 2) + row * (K / 32) + k / 32];
+    }
+    __device__ __forceinline__ void decode(int u, u32x4 out[4], int & run0, int & run1) const {
+        // 2^(e-128) from its bits: a subnormal for e < 2
+        const uint32_t eb = e < 2 ? (0x00200000u << e) : ((uint32_t)(e - 1) << 23);
+        const float d = __builtin_bit_cast(float, eb);
+        uint32_t o[16];
+#pragma unroll
+        for (int w = 0; w < 4; w++) {
+            const uint32_t word = qs[w];
+            float lo[4], hi[4];
+#pragma unroll
+            for (int b = 0; b < 4; b++) {
+                lo[b] = mul_rn(d, (float)mxfp4_code((word >> (8 * b)) & 15u));
+                hi[b] = mul_rn(d, (float)mxfp4_code((word >> (8 * b + 4)) & 15u));
+            }
+            o[2 * w] = pack2h(lo[0], lo[1]);          // weights 4w .. 4w+3
+            o[2 * w + 1] = pack2h(lo[2], lo[3]);
+            o[8 + 2 * w] = pack2h(hi[0], hi[1]);      // weights 16 + 4w .. 16 + 4w+3
+            o[8 + 2 * w + 1] = pack2h(hi[2], hi[3]);
         }
 #pragma unroll
         for (int i = 0; i < 4; i++) out[i] = u32x4{o[4 * i], o[4 * i + 1], o[4 * i + 2], o[4 * i + 3]};

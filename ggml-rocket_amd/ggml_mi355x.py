@@ -16,10 +16,10 @@ import os
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "lib", "libggml-mi355x.so")
 
-F32, F16, Q8_0, Q4_K, Q6_K, I32, BF16 = 0, 1, 8, 12, 14, 26, 30
+F32, F16, Q8_0, Q4_K, Q6_K, I32, BF16, MXFP4 = 0, 1, 8, 12, 14, 26, 30, 39
 F16_T = 0x101   # the library's tiled fp16 layout (16 x 32 tiles of 1 KB); not a ggml type
-BLOCK = {F16: 1, F32: 1, BF16: 1, Q8_0: 32, Q4_K: 256, Q6_K: 256}
-TYPE_SIZE = {F16: 2, F32: 4, BF16: 2, Q8_0: 34, Q4_K: 144, Q6_K: 210}
+BLOCK = {F16: 1, F32: 1, BF16: 1, Q8_0: 32, Q4_K: 256, Q6_K: 256, MXFP4: 32}
+TYPE_SIZE = {F16: 2, F32: 4, BF16: 2, Q8_0: 34, Q4_K: 144, Q6_K: 210, MXFP4: 17}
 
 _lib = None
 

@@ -15,9 +15,10 @@
  *                mask [T'][KV'] fp16 (T' >= T, KV' >= KV), dst [T][H][DV] F32.
  *   MUL_MAT_ID   as [E][N][K], b [T][ne11][K] F32, ids [T][n_used] I32, dst [T][n_used][N] F32.
  *
- * Weight types are ggml type ids: F16 = 1, Q8_0 = 8, Q4_K = 12, Q6_K = 14. A weight reaches a
- * GEMM in its HBM layout: F16 and Q4_K are the ggml payload unchanged; Q8_0 and Q6_K are
- * re-laid out once by mi355x_weight_pack (same bytes, split into 16-byte-aligned planes).
+ * Weight types are ggml type ids: F16 = 1, Q8_0 = 8, Q4_K = 12, Q6_K = 14, MXFP4 = 39. A weight
+ * reaches a GEMM in its HBM layout: F16 and Q4_K are the ggml payload unchanged; Q8_0, Q6_K and
+ * MXFP4 are re-laid out once by mi355x_weight_pack (same bytes, split into 16-byte-aligned
+ * planes).
  */
 #ifndef MI355X_KERNELS_H
 #define MI355X_KERNELS_H
@@ -40,7 +41,7 @@ enum mi355x_status {
     MI355X_E_IDS = -5,          /* MUL_MAT_ID: an expert id outside [0, n_expert) */
 };
 
-enum mi355x_wtype { MI355X_F16 = 1, MI355X_Q8_0 = 8, MI355X_Q4_K = 12, MI355X_Q6_K = 14,
+enum mi355x_wtype { MI355X_F16 = 1, MI355X_Q8_0 = 8, MI355X_Q4_K = 12, MI355X_Q6_K = 14, MI355X_MXFP4 = 39,
                     /* not a ggml type: fp16 [rows][K] in 16 x 32 tiles of 1 KB, row-major inside,
                      * tile (r/16, k/32) at element ((r/16)*(K/32) + k/32)*512; rows padded to a
                      * multiple of 16 (padding never read). The resident fp16 form the GEMM streams

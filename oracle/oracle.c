@@ -9,7 +9,7 @@
  *   - fp16 <-> fp32 conversion, round-to-nearest-even (the semantics of ggml_fp32_to_fp16 that
  *     ggml-rocket.cpp:1473, 1516, 3860, 3907 rely on);
  *   - the splitmix64 fills of test-common.h:181-193 and a Box-Muller normal fill on top of them;
- *   - the Q8_0 / Q4_K / Q6_K block decoders that ggml_get_type_traits(t)->to_float provides
+ *   - the Q8_0 / Q4_K / Q6_K / MXFP4 block decoders that ggml_get_type_traits(t)->to_float provides
  *     (ggml-rocket.cpp:3894-3906). ggml is an un-vendored third-party dependency of the
  *     reference (CMakeLists.txt:176-186, compatible range llama.cpp b10558-b11539 per
  *     README.md:380-391); the decoders here are written from ggml's published block formats;
@@ -35,7 +35,7 @@
 #define ORC_API __attribute__((visibility("default")))
 
 /* ggml type ids (ggml.h enum ggml_type); the formats this path carries. */
-enum { T_F32 = 0, T_F16 = 1, T_Q8_0 = 8, T_Q4_K = 12, T_Q6_K = 14, T_BF16 = 30 };
+enum { T_F32 = 0, T_F16 = 1, T_Q8_0 = 8, T_Q4_K = 12, T_Q6_K = 14, T_BF16 = 30, T_MXFP4 = 39 };
 
 /* ------------------------------------------------------------------------------------------ */
 /* fp16                                                                                        */
@@ -132,12 +132,15 @@ ORC_API void orc_fill_normal(float * v, int64_t n, uint64_t seed, float mean, fl
 /*   Q8_0: { fp16 d; int8 qs[32]; }                                       34 B / 32 weights     */
 /*   Q4_K: { fp16 d; fp16 dmin; u8 scales[12]; u8 qs[128]; }             144 B / 256 weights    */
 /*   Q6_K: { u8 ql[128]; u8 qh[64]; int8 scales[16]; fp16 d; }           210 B / 256 weights    */
+/*   MXFP4: { u8 e; u8 qs[16]; }                                           17 B / 32 weights     */
+/*     (the OCP microscaling FP4 block ggml stores for gpt-oss: an E8M0 power-of-two scale and  */
+/*     32 E2M1 codes, qs[j] low nibble = weight j, high nibble = weight j + 16)                 */
 /* ------------------------------------------------------------------------------------------ */
 
 ORC_API int64_t orc_block_size(int type) {
     switch (type) {
         case T_F32: case T_F16: case T_BF16: return 1;
-        case T_Q8_0: return 32;
+        case T_Q8_0: case T_MXFP4: return 32;
         case T_Q4_K: case T_Q6_K: return 256;
         default: return 0;
     }
@@ -149,6 +152,7 @@ ORC_API int64_t orc_type_size(int type) {
         case T_Q8_0: return 34;
         case T_Q4_K: return 144;
         case T_Q6_K: return 210;
+        case T_MXFP4: return 17;
         default: return 0;
     }
 }
@@ -221,6 +225,29 @@ static void dequant_q6_k(const uint8_t * x, float * y, int64_t K) {
     }
 }
 
+/* MXFP4: E2M1 values (kvalues_mxfp4 of ggml-common.h: 0 1 2 3 4 6 8 12 and their negatives,
+ * doubled so they are integers) times the E8M0 scale 2^(e-128) (GGML_E8M0_TO_FP32_HALF: the
+ * block exponent minus the bias 127, halved). Every product is exact in f32. */
+static const int8_t MXFP4_K[16] = {0, 1, 2, 3, 4, 6, 8, 12, 0, -1, -2, -3, -4, -6, -8, -12};
+
+static inline float e8m0_half(uint8_t e) {
+    /* 2^(e-128) as f32 bits: a subnormal for e < 2 */
+    const uint32_t bits = e < 2 ? (uint32_t)0x00200000u << e : (uint32_t)(e - 1) << 23;
+    float f;
+    memcpy(&f, &bits, 4);
+    return f;
+}
+
+static void dequant_mxfp4(const uint8_t * x, float * y, int64_t K) {
+    for (int64_t b = 0; b < K / 32; b++, x += 17, y += 32) {
+        const float d = e8m0_half(x[0]);
+        for (int j = 0; j < 16; j++) {
+            y[j] = (float)MXFP4_K[x[1 + j] & 0x0F] * d;
+            y[j + 16] = (float)MXFP4_K[x[1 + j] >> 4] * d;
+        }
+    }
+}
+
 /* One [K] row of `type` to f32: the to_float contract of ggml-rocket.cpp:3894-3906. */
 ORC_API int orc_dequant_row(int type, const void * src, float * dst, int64_t K) {
     const uint8_t * x = (const uint8_t *)src;
@@ -231,6 +258,7 @@ ORC_API int orc_dequant_row(int type, const void * src, float * dst, int64_t K) 
         case T_Q8_0: if (K % 32) return -1; dequant_q8_0(x, dst, K); return 0;
         case T_Q4_K: if (K % 256) return -1; dequant_q4_k(x, dst, K); return 0;
         case T_Q6_K: if (K % 256) return -1; dequant_q6_k(x, dst, K); return 0;
+        case T_MXFP4: if (K % 32) return -1; dequant_mxfp4(x, dst, K); return 0;
         default: return -1;
     }
 }
@@ -359,6 +387,30 @@ static void quant_q6_k(const float * x, uint8_t * y, int64_t K) {
     }
 }
 
+/* MXFP4 quantizer for synthetic weights (this repository's own: the smallest scale 2^(e-128)
+ * with amax <= 6 * 2^(e-127), i.e. the largest code fits, then each value to the nearest code). */
+static void quant_mxfp4(const float * x, uint8_t * y, int64_t K) {
+    for (int64_t b = 0; b < K / 32; b++, x += 32, y += 17) {
+        float amax = 0.0f;
+        for (int l = 0; l < 32; l++) amax = fmaxf(amax, fabsf(x[l]));
+        int e = 0;
+        while (e < 254 && 12.0f * e8m0_half((uint8_t)e) < amax) e++;
+        y[0] = (uint8_t)e;
+        const float d = e8m0_half((uint8_t)e);
+        uint8_t code[32];
+        for (int l = 0; l < 32; l++) {
+            int best = 0;
+            float bd = INFINITY;
+            for (int c = 0; c < 16; c++) {
+                const float dv = fabsf((float)MXFP4_K[c] * d - x[l]);
+                if (dv < bd) { bd = dv; best = c; }
+            }
+            code[l] = (uint8_t)best;
+        }
+        for (int j = 0; j < 16; j++) y[1 + j] = (uint8_t)(code[j] | (code[j + 16] << 4));
+    }
+}
+
 ORC_API int orc_quantize_rows(int type, const float * src, void * dst, int64_t nrows, int64_t K) {
     const int64_t rb = orc_row_size(type, K);
     if (rb < 0) return -1;
@@ -372,6 +424,7 @@ ORC_API int orc_quantize_rows(int type, const float * src, void * dst, int64_t n
             case T_Q8_0: quant_q8_0(x, y, K); break;
             case T_Q4_K: quant_q4_k(x, y, K); break;
             case T_Q6_K: quant_q6_k(x, y, K); break;
+            case T_MXFP4: quant_mxfp4(x, y, K); break;
             default: break;
         }
     }

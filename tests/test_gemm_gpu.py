@@ -57,7 +57,7 @@ def test_pack_act_bitexact(mx):
     assert np.array_equal(got_a, want_a)
 
 
-@pytest.mark.parametrize("wtype", [O.F16, O.Q8_0, O.Q4_K, O.Q6_K])
+@pytest.mark.parametrize("wtype", [O.F16, O.Q8_0, O.Q4_K, O.Q6_K, O.MXFP4])
 def test_dequant_f16_bitexact(mx, wtype):
     N, K = 96, 1024
     W = O.fill_normal((N, K), 11 + wtype, 0.0, 0.02)
@@ -117,7 +117,7 @@ def test_cfg_f16_8192x2048_m512(mx):
 
 
 QSHAPES = [(256, 128, 64, O.Q8_0), (3840, 256, 128, O.Q8_0), (256, 128, 64, O.Q4_K),
-           (3840, 256, 128, O.Q4_K), (512, 256, 128, O.Q6_K)]
+           (3840, 256, 128, O.Q4_K), (512, 256, 128, O.Q6_K), (2880, 256, 128, O.MXFP4)]
 
 
 @pytest.mark.parametrize("K,N,M,wtype", QSHAPES)
@@ -196,7 +196,7 @@ def _untile(buf, rows, K):
     return t.transpose(0, 2, 1, 3).reshape(rp, K)[:rows]
 
 
-@pytest.mark.parametrize("wtype", [O.F16, O.Q8_0, O.Q4_K, O.Q6_K])
+@pytest.mark.parametrize("wtype", [O.F16, O.Q8_0, O.Q4_K, O.Q6_K, O.MXFP4])
 def test_f16_tiled_bitexact(mx, wtype):
     """The tiled resident form holds exactly the fp16 values of the row-major one (rows not a
     multiple of 16: padded, the padding never read)."""
@@ -234,10 +234,10 @@ F16_T = 0x101
 
 
 @pytest.mark.parametrize("cfg", list(range(N_GEMM_CFGS)))
-@pytest.mark.parametrize("wtype", [O.F16, O.Q4_K, F16_T])
+@pytest.mark.parametrize("wtype", [O.F16, O.Q4_K, F16_T, O.MXFP4])
 def test_gemm_every_tile_config(mx, monkeypatch, cfg, wtype):
     import torch
-    if cfg >= FIRST_DMA_CFG and wtype == O.Q4_K:
+    if cfg >= FIRST_DMA_CFG and wtype in (O.Q4_K, O.MXFP4):
         pytest.skip("the LDS-DMA configurations take fp16 weights only")
     if cfg < FIRST_DMA_CFG and wtype == F16_T:
         pytest.skip("the register-staged configurations do not read the tiled layout")
@@ -248,8 +248,8 @@ def test_gemm_every_tile_config(mx, monkeypatch, cfg, wtype):
     outs, refs = [], []
     for g, N in enumerate(Ns):
         W = O.fill_normal((N, K), 910 + g, 0.0, 0.02)
-        payload = O.quantize(wtype, W) if wtype == O.Q4_K else O.f32_to_f16_bits(W)
-        refs.append(O.mul_mat(O.Q4_K if wtype == O.Q4_K else O.F16, payload, Xf, N, K))
+        payload = O.quantize(wtype, W) if wtype in (O.Q4_K, O.MXFP4) else O.f32_to_f16_bits(W)
+        refs.append(O.mul_mat(wtype if wtype in (O.Q4_K, O.MXFP4) else O.F16, payload, Xf, N, K))
         if wtype == F16_T:
             w = mx.tile_f16(O.F16, mx.upload_weight(O.F16, payload, N, K), N, K)
         else:

@@ -4,8 +4,9 @@ Cases follow test-rocket-moe.cpp (F16 and quantized expert stacks, both b forms 
 ne11 = n_used, pad rows, 16 experts / 4 used, skewed routing with the last expert empty,
 outlier activation channels, one weight upload serving several token counts) plus the BASELINE
 shape: 128 experts, top-8 routing from a softmax over seeded N(0,1) router logits, 512 tokens,
-d_model 2048, expert FFN 768, gate/up/down Q4_K. MXFP4 stacks (the reference's gpt-oss cases)
-are not supported by this backend yet and are left out.
+d_model 2048, expert FFN 768, gate/up/down Q4_K, and the reference's MXFP4 (gpt-oss) stacks,
+decoded exactly to fp16 here (the reference merges block exponents onto int8 codes instead, so
+its bars hold with room).
 Bars: the element bar, aggregate cosine, worst row / column cosine at 1 - 10 (1 - floor)
 (test-rocket-moe.cpp:200-219, 279-289), and max|d|/max|ref| <= 1e-2.
 """
@@ -37,8 +38,12 @@ def make_input(T, ne11, K):
     return X
 
 
-def expert_payload(wtype, E, N, K, seed0=1000):
+def expert_payload(wtype, E, N, K, seed0=1000, wide=False):
     W = np.stack([O.fill_uniform((N, K), seed0 + e, 0.3) for e in range(E)])
+    if wide:   # a 9-octave spread of block magnitudes (test-rocket-moe.cpp's WIDE weights)
+        oct_ = (np.arange(E * N * K // 32).reshape(E, N, K // 32) * 7919) % 9
+        W = (W.reshape(E, N, K // 32, 32) * np.exp2(-oct_.astype(np.float32))[..., None]).reshape(E, N, K)
+        W = W.astype(np.float32)
     if wtype == O.F16:
         return O.f32_to_f16_bits(W)
     return O.quantize(wtype, W)
@@ -74,21 +79,26 @@ def check_bars(ref, got, N, floor, label):
     assert r["range_err"] <= 1e-2, label
 
 
-# (K, N, E, ne11, U, T, wtype, floor) -- test-rocket-moe.cpp:240-262 without the MXFP4 rows
+# (K, N, E, ne11, U, T, wtype, floor, wide) -- test-rocket-moe.cpp:200-219
 CASES = [
-    (256, 128, 8, 1, 2, 64, O.F16, 0.9999),
-    (256, 128, 8, 2, 2, 64, O.F16, 0.9999),
-    (256, 128, 8, 1, 2, 66, O.F16, 0.9999),
-    (256, 128, 16, 1, 4, 96, O.F16, 0.9999),
-    (1024, 128, 8, 1, 2, 64, O.Q4_K, 0.9990),
-    (1152, 128, 8, 2, 2, 64, O.Q8_0, 0.9990),
-    (512, 256, 8, 2, 4, 80, O.Q6_K, 0.9990),
+    (256, 128, 8, 1, 2, 64, O.F16, 0.9999, False),
+    (256, 128, 8, 2, 2, 64, O.F16, 0.9999, False),
+    (256, 128, 8, 1, 2, 66, O.F16, 0.9999, False),
+    (256, 128, 16, 1, 4, 96, O.F16, 0.9999, False),
+    (256, 128, 8, 1, 2, 64, O.MXFP4, 0.9990, False),
+    (256, 128, 8, 2, 2, 64, O.MXFP4, 0.9990, False),
+    (1152, 128, 8, 1, 2, 64, O.MXFP4, 0.9990, False),
+    (2048, 128, 8, 1, 2, 66, O.MXFP4, 0.9990, False),
+    (1152, 128, 8, 1, 2, 64, O.MXFP4, 0.9985, True),
+    (1024, 128, 8, 1, 2, 64, O.Q4_K, 0.9990, False),
+    (1152, 128, 8, 2, 2, 64, O.Q8_0, 0.9990, False),
+    (512, 256, 8, 2, 4, 80, O.Q6_K, 0.9990, False),
 ]
 
 
-@pytest.mark.parametrize("K,N,E,ne11,U,T,wtype,floor", CASES)
-def test_moe_reference_cases(mx, K, N, E, ne11, U, T, wtype, floor):
-    P = expert_payload(wtype, E, N, K)
+@pytest.mark.parametrize("K,N,E,ne11,U,T,wtype,floor,wide", CASES)
+def test_moe_reference_cases(mx, K, N, E, ne11, U, T, wtype, floor, wide):
+    P = expert_payload(wtype, E, N, K, wide=wide)
     X = make_input(T, ne11, K)
     ids = make_ids(T, U, E)
     got, _ = run(mx, wtype, P, E, N, K, X, ids)

@@ -154,6 +154,50 @@ def test_quant_roundtrip(wtype):
 def test_row_size():
     assert O.row_size(O.Q8_0, 64) == 68 and O.row_size(O.Q4_K, 512) == 288
     assert O.row_size(O.Q6_K, 256) == 210 and O.row_size(O.Q4_K, 100) == -1
+    assert O.row_size(O.MXFP4, 64) == 34 and O.row_size(O.MXFP4, 48) == -1
+
+
+# The OCP microscaling FP4 definition the MXFP4 decoder restates: an E2M1 code is
+# sign * {0, 0.5, 1, 1.5, 2, 3, 4, 6}[low 3 bits] (bit 3 = sign), the E8M0 byte e scales the
+# block by 2^(e-127), and ggml puts weight j in the low nibble of qs[j], weight j+16 in the high.
+E2M1 = np.array([0, 0.5, 1, 1.5, 2, 3, 4, 6, -0.0, -0.5, -1, -1.5, -2, -3, -4, -6], dtype=np.float64)
+
+
+def _mxfp4_block(e, codes):
+    codes = np.asarray(codes, dtype=np.uint8)
+    return np.concatenate([[np.uint8(e)], (codes[:16] | (codes[16:] << 4)).astype(np.uint8)]).astype(np.uint8)
+
+
+def test_mxfp4_known_answer():
+    """Every code at unit scale (e = 127), the nibble order, the bias, doubling per exponent
+    step, and the two subnormal scales (e = 0, 1 -> 2^-127, 2^-126 times the E2M1 value)."""
+    codes = np.array(list(range(16)) + list(range(15, -1, -1)), dtype=np.uint8)
+    for e in (0, 1, 2, 100, 126, 127, 128, 140):
+        y = O.dequantize(O.MXFP4, _mxfp4_block(e, codes), 32)
+        want = E2M1[codes] * np.ldexp(1.0, e - 127)
+        assert np.array_equal(y.astype(np.float64), want), e
+    # low nibble -> weight j, high nibble -> weight j + 16
+    one = np.zeros(32, dtype=np.uint8)
+    one[3], one[16 + 9] = 7, 12         # 6.0 at weight 3, -2.0 at weight 25
+    y = O.dequantize(O.MXFP4, _mxfp4_block(127, one), 32)
+    assert y[3] == 6.0 and y[25] == -2.0 and np.count_nonzero(y) == 2
+
+
+def test_mxfp4_quant_roundtrip():
+    """Values that are E2M1 codes times the block scale come back exactly; others within half
+    the widest code gap (2 units of the scale, between 4 and 6) of each block."""
+    rng = np.random.default_rng(11)
+    codes = rng.integers(0, 16, (8, 64)).astype(np.uint8)
+    exps = rng.integers(110, 140, (8, 2))
+    W = (E2M1[codes].reshape(8, 2, 32) * np.ldexp(1.0, exps - 127)[..., None]).reshape(8, 64)
+    W[:, 0] = 6.0 * np.ldexp(1.0, exps[:, 0] - 127)      # each block's largest code is present
+    W[:, 32] = -6.0 * np.ldexp(1.0, exps[:, 1] - 127)
+    W = W.astype(np.float32)
+    assert np.array_equal(O.dequantize(O.MXFP4, O.quantize(O.MXFP4, W), 64), W)
+    X = O.fill_normal((16, 256), 12, 0.0, 0.02)
+    d = O.dequantize(O.MXFP4, O.quantize(O.MXFP4, X), 256)
+    scale = np.abs(X.reshape(16, -1, 32)).max(-1, keepdims=True) / 6.0
+    assert np.all(np.abs(d - X).reshape(16, -1, 32) <= 2.0 * scale + 1e-12)
 
 
 # ---- ops --------------------------------------------------------------------------------------

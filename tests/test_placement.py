@@ -26,6 +26,10 @@ CASES = [
     ("Q8_0 leaf, M >= quant floor -> offload", True, lambda: mm_supported(K, N, MQ, mx.Q8_0)),
     ("Q4_K leaf, M >= quant floor -> offload", True, lambda: mm_supported(K, N, MQ, mx.Q4_K)),
     ("Q6_K leaf, M >= quant floor -> offload", True, lambda: mm_supported(K, N, MQ, mx.Q6_K)),
+    # MXFP4 (gpt-oss): the reference claims it for its MoE route; decoded exactly to fp16 here,
+    # so MUL_MAT takes it as it takes the other quant types
+    ("MXFP4 leaf, M >= quant floor -> offload", True, lambda: mm_supported(K, N, MQ, mx.MXFP4)),
+    ("MXFP4 leaf, M(256) < quant floor -> CPU", False, lambda: mm_supported(K, N, M, mx.MXFP4)),
     ("Q4_K leaf, M(256) < quant floor -> CPU", False, lambda: mm_supported(K, N, M, mx.Q4_K)),
     ("K%32 != 0 (K=80) -> CPU", False, lambda: mm_supported(80, N, M, mx.F16)),
     ("N%16 != 0 (N=70) -> CPU", False, lambda: mm_supported(K, 70, M, mx.F16)),
