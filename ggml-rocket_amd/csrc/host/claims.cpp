@@ -8,7 +8,8 @@
 //     BF16 accumulator declaration is met (the NPU route could not, 7372-7380);
 //   * the weight types: the device decodes F16, F32, BF16, Q8_0, Q4_K, Q6_K and MXFP4; other ggml quant
 //     types are declined rather than claimed and then computed on the host;
-//   * FLASH_ATTN_EXT: head dims 64 and 128 with D == DV, and the strides the kernel reads.
+//   * FLASH_ATTN_EXT: head dims (64, 64), (128, 128) and the MLA (192, 128), and the strides the
+//     kernel reads.
 
 #include <atomic>
 #include <mutex>
@@ -358,8 +359,10 @@ static bool claim_flash_attn(const mi355x_tensor * op) {
         && n_tokens >= flash_attn_min_t()
         && n_kv >= flash_attn_min_kv();
     if (!ref_rules) return false;
-    // what the kernel reads: D == DV in {64, 128}; element strides; 16-byte rows
-    const bool dims = head_dim == dv && (head_dim == 64 || head_dim == 128);
+    // what the kernel reads: (D, DV) = (64, 64), (128, 128) or the MLA shape (192, 128);
+    // element strides; 16-byte rows
+    const bool dims = (head_dim == 64 && dv == 64) || (head_dim == 128 && dv == 128) ||
+                      (head_dim == 192 && dv == 128);
     const bool q_ok = q->nb[0] == 4 && q->nb[1] % 16 == 0 && q->nb[2] % 16 == 0;
     const bool kv_ok = k->nb[0] == 2 && v->nb[0] == 2 && k->nb[1] % 16 == 0 && k->nb[2] % 16 == 0 &&
                        v->nb[1] % 16 == 0 && v->nb[2] % 16 == 0;

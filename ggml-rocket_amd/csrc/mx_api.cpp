@@ -191,7 +191,7 @@ MI355X_API int mi355x_mul_mat(int wtype, const void * w_dev, int64_t N, int64_t 
 
 static int fa_check(const mi355x_fa_args * a) {
     if (!a || !a->q_dev || !a->k_dev || !a->v_dev || !a->dst_dev) return MI355X_E_ARG;
-    if (a->D != a->DV || (a->D != 64 && a->D != 128)) return MI355X_E_UNSUPPORTED;
+    if (!mx::fa_dims_supported(a->D, a->DV)) return MI355X_E_UNSUPPORTED;   // (64,64) (128,128) (192,128)
     if (a->max_bias != 0.0f) return MI355X_E_UNSUPPORTED;
     if (a->T < 0 || a->H <= 0 || a->HK <= 0 || a->KV < 0 || a->H % a->HK) return MI355X_E_ARG;
     if (a->q_nb1 % 4 || a->q_nb2 % 4 || !aligned(a->q_dev, 16)) return MI355X_E_ARG;
@@ -199,7 +199,7 @@ static int fa_check(const mi355x_fa_args * a) {
     if (!aligned(a->k_dev, 16) || !aligned(a->v_dev, 16)) return MI355X_E_ARG;
     if (a->dst_nb1 % 4 || a->dst_nb2 % 4 || !aligned(a->dst_dev, 16)) return MI355X_E_ARG;
     if (a->mask_dev && (a->mask_nb1 % 4 || a->mask_nb1 < a->KV || !aligned(a->mask_dev, 8))) return MI355X_E_ARG;
-    if ((size_t)a->KV > mx::fa_max_kv()) return MI355X_E_UNSUPPORTED;
+    if ((size_t)a->KV > mx::fa_max_kv(a->D, a->DV)) return MI355X_E_UNSUPPORTED;
     return MI355X_OK;
 }
 
@@ -210,7 +210,7 @@ static mx::FaArgs fa_lower(const mi355x_fa_args * a, int nsplit) {
     f.q_nb1 = a->q_nb1; f.q_nb2 = a->q_nb2; f.k_nb1 = a->k_nb1; f.k_nb2 = a->k_nb2;
     f.v_nb1 = a->v_nb1; f.v_nb2 = a->v_nb2; f.mask_nb1 = a->mask_nb1;
     f.dst_nb1 = a->dst_nb1; f.dst_nb2 = a->dst_nb2;
-    f.D = a->D; f.T = a->T; f.H = a->H; f.HK = a->HK; f.KV = a->KV; f.nsplit = nsplit;
+    f.D = a->D; f.DV = a->DV; f.T = a->T; f.H = a->H; f.HK = a->HK; f.KV = a->KV; f.nsplit = nsplit;
     f.kvp = (int)((a->KV + 63) / 64 * 64);
     f.cls_stride = (f.kvp / 64 + 15) / 16 * 16;
     f.scale = a->scale; f.softcap = a->softcap;
@@ -229,9 +229,9 @@ static FaLayout fa_layout(const mx::FaArgs & f) {
     const size_t nqt = (size_t)(f.T + 31) / 32;
     const size_t rows = (size_t)f.T * f.H * f.nsplit;
     L.vt = 0;
-    L.cls = L.vt + align256((size_t)f.HK * f.D * f.kvp * 2);
+    L.cls = L.vt + align256((size_t)f.HK * f.DV * f.kvp * 2);
     L.po = L.cls + align256(nqt * (size_t)f.cls_stride);
-    L.pml = L.po + (f.nsplit > 1 ? align256(rows * f.D * 4) : 0);
+    L.pml = L.po + (f.nsplit > 1 ? align256(rows * f.DV * 4) : 0);
     L.total = L.pml + (f.nsplit > 1 ? align256(rows * 8) : 0);
     return L;
 }

@@ -12,13 +12,14 @@
 // for the P.V MFMA, both contractions accumulate in fp32.
 //
 // One op is two launches:
-//   fa_prep   V -> V^T [HK][D][KVp] (keys padded to a multiple of 64 with zeros, and permuted
+//   fa_prep   V -> V^T [HK][DV][KVp] (keys padded to a multiple of 64 with zeros, and permuted
 //             within each 16-key group so that each lane's P^T operand keys are one 16-byte
 //             chunk, see vt_pos); the mask tile classes (per 32-query x 64-key tile: every key
 //             masked / no key masked / mixed).
 //   fa        a block is 4 waves, each owning 32 query rows of one head, all 4 on one KV head
-//             (GQA reuse of the LDS tiles). Per 64-key tile: K [64][D] and V^T [D][64] arrive
-//             in LDS by global_load_lds (a 4-deep ring, three tiles landing while one is used);
+//             (GQA reuse of the LDS tiles). Per 64-key tile: K [64][DK] and V^T [DV][64] arrive
+//             in LDS by global_load_lds (a 4-deep ring, two tiles landing while two are used;
+//             2-deep when four stages do not fit, for DK 192);
 //             tiles whose mask is -inf for all the block's queries are skipped, tiles with
 //             no mask entry read no mask. Scores are computed transposed, S^T = K . Q^T, so each
 //             lane owns one query: the row max and sum need one exchange with the partner lane
@@ -38,20 +39,41 @@ constexpr int FA_TASKS = 4;     // wave tasks (head, 32-query tile) per block
 constexpr int FA_PAR = 2;       // waves per task, taking alternate key tiles
 constexpr int FA_WAVES = FA_TASKS * FA_PAR;
 constexpr int FA_THREADS = FA_WAVES * WAVE;
-constexpr int FA_NS = 4;        // LDS ring depth (two tiles consumed per step)
+constexpr int FA_LDS_MAX = 160 * 1024;
+constexpr int FA_CLS_RESERVE = 2048;   // LDS kept beside the ring for the class rows (KV <= 32768)
 
-template <int D>
+// DK: the Q.K contraction (Q and K head dim), DV: the V and output head dim (DK > DV for the
+// non-absorbed MLA of DeepSeek-style models, 192 / 128).
+template <int DK, int DV>
 struct FaCfg {
-    static constexpr int KCH = D / 8;                        // 16-byte chunks per K row
-    static constexpr int KRPW = 16 / KCH;                    // K rows per 256-byte bank window
-    static constexpr int K_BYTES = FA_BKV * D * 2;           // [64 keys][D]
-    static constexpr int V_BYTES = D * FA_BKV * 2;           // [D][64 key slots], 128-byte rows
+    static constexpr int KCH = DK / 8;                       // 16-byte chunks per K row
+    // K rows swizzle their chunks by XOR when KCH is a power of two (conflict free), else by a
+    // rotation of one chunk per row
+    static constexpr bool KXOR = (KCH & (KCH - 1)) == 0;
+    static constexpr int KRPW = KCH >= 16 ? 1 : 16 / KCH;    // K rows per 256-byte bank window
+    static constexpr int K_BYTES = FA_BKV * DK * 2;          // [64 keys][DK]
+    static constexpr int V_BYTES = DV * FA_BKV * 2;          // [DV][64 key slots], 128-byte rows
     static constexpr int STAGE = K_BYTES + V_BYTES;
-    static constexpr int LDS = FA_NS * STAGE;
+    // ring depth: two tiles land while two are used, when four stages fit; else two stages and
+    // the next pair is fetched between the steps
+    static constexpr int NS = 4 * STAGE + FA_CLS_RESERVE <= FA_LDS_MAX - 64 ? 4 : 2;
+    static constexpr int LDS = NS * STAGE;
     static constexpr int PK = K_BYTES / (FA_THREADS * 16);   // DMA instructions per wave
     static constexpr int PV = V_BYTES / (FA_THREADS * 16);
     static constexpr int PER = PK + PV;
     static_assert(PK >= 1 && PV >= 1 && PK * FA_THREADS * 16 == K_BYTES && PV * FA_THREADS * 16 == V_BYTES, "DMA split");
+    static_assert(DK % 64 == 0 && DV % 64 == 0, "head dims");
+    static_assert(NS * STAGE + FA_CLS_RESERVE <= FA_LDS_MAX - 64, "LDS");
+    // physical 16-byte chunk of logical chunk c in K row r
+    __device__ static __forceinline__ int kchunk(int r, int c) {
+        if constexpr (KXOR) return c ^ ((r / KRPW) & (KCH - 1));
+        else return (c + r) % KCH;
+    }
+    // logical chunk stored at physical chunk p of K row r
+    __device__ static __forceinline__ int kchunk_inv(int r, int p) {
+        if constexpr (KXOR) return p ^ ((r / KRPW) & (KCH - 1));
+        else return (p + KCH - r % KCH) % KCH;
+    }
 };
 
 typedef const void __attribute__((address_space(1))) * fa_gptr_t;
@@ -81,7 +103,7 @@ __device__ __forceinline__ int vt_pos(int r) {
 // ---------------------------------------------------------------------------------------------
 enum : uint8_t { FA_TILE_SKIP = 0, FA_TILE_FULL = 1, FA_TILE_MIXED = 2 };
 
-template <int D>
+template <int D>   // D = DV, the V head dim
 __global__ void __launch_bounds__(256) fa_prep_kernel(FaArgs a) {
     __shared__ uint16_t tile[FA_BKV][D + 2];   // +2: row stride 4 bytes off the bank period
     const int t = threadIdx.x;
@@ -181,13 +203,14 @@ __global__ void __launch_bounds__(256) fa_prep_kernel(FaArgs a) {
 // ---------------------------------------------------------------------------------------------
 // main kernel
 // ---------------------------------------------------------------------------------------------
-template <int D, bool SOFTCAP>
+template <int DK, int DV, bool SOFTCAP>
 __global__ void __launch_bounds__(FA_THREADS) __attribute__((amdgpu_waves_per_eu(2, 2)))
 fa_kernel(FaArgs a) {
-    using C = FaCfg<D>;
+    using C = FaCfg<DK, DV>;
     extern __shared__ __align__(16) uint8_t smem[];
-    constexpr int KSTEPS = D / 16;   // QK contraction steps
-    constexpr int DBLK = D / 32;     // output row blocks of O^T
+    constexpr int FA_NS = C::NS;
+    constexpr int KSTEPS = DK / 16;  // QK contraction steps
+    constexpr int DBLK = DV / 32;    // output row blocks of O^T
 
     const int t = threadIdx.x, lane = t % WAVE, wave = t / WAVE;
     const int lq = lane % 32, lg = lane / 32;
@@ -262,14 +285,14 @@ fa_kernel(FaArgs a) {
 #pragma unroll
     for (int q = 0; q < C::PK; q++) {
         const int slot = (q * FA_WAVES + wave) * WAVE + lane;
-        const int r = slot / C::KCH, c = (slot % C::KCH) ^ ((r / C::KRPW) & (C::KCH - 1));
+        const int r = slot / C::KCH, c = C::kchunk_inv(r, slot % C::KCH);
         ksrc[q] = a.k + (int64_t)hk * a.k_nb2 + 8 * c + (int64_t)r * a.k_nb1;   // + j0 * k_nb1 per tile
     }
 #pragma unroll
     for (int q = 0; q < C::PV; q++) {
         const int slot = (q * FA_WAVES + wave) * WAVE + lane;
         const int r = slot / 8, c = (slot % 8) ^ ((r / 2) & 7);
-        vsrc[q] = a.vt + ((int64_t)hk * D + r) * a.kvp + 8 * c;                  // + j0 per tile
+        vsrc[q] = a.vt + ((int64_t)hk * DV + r) * a.kvp + 8 * c;                 // + j0 per tile
     }
     const int kv_last = max(a.KV - 1, 0);
     // tile i into ring buffer i % FA_NS; past the last tile the last one is fetched again into
@@ -289,7 +312,6 @@ fa_kernel(FaArgs a) {
         for (int q = 0; q < C::PV; q++) fa_dma16(vsrc[q] + j0, st + C::K_BYTES + (q * FA_WAVES + wave_s) * 1024);
     };
 
-    const int xk = (lq / C::KRPW) & (C::KCH - 1);   // K row swizzle: rows kb*32 + lq
     const int xv = (lq / 2) & 7;                    // V^T row swizzle: rows db*32 + lq
 
     // Each step consumes two tiles: parity-0 waves take the even one, parity-1 waves the odd one
@@ -309,7 +331,7 @@ fa_kernel(FaArgs a) {
         float qv[KSTEPS][8];
 #pragma unroll
         for (int s = 0; s < KSTEPS; s++) {
-            const int d = 16 * s + 8 * lg;
+            const int d = 16 * s + 8 * lg;   // < DK
             float4v x0 = {0, 0, 0, 0}, x1 = {0, 0, 0, 0};
             if (qok) {
                 x0 = *(const float4v *)(q + d);
@@ -334,7 +356,7 @@ fa_kernel(FaArgs a) {
 
     const bool q_scaled = __any(qfac != 1.0f);   // a row of this wave needed the Q range factor
     if (ntl > 0) {
-        fa_wait_vm_lgkm0<2 * C::PER>();
+        fa_wait_vm_lgkm0<(FA_NS - 2) * C::PER>();
         __builtin_amdgcn_s_barrier();
     }
     for (int stp = 0; stp < nsteps; stp++) {
@@ -355,7 +377,7 @@ fa_kernel(FaArgs a) {
                 half8 kf[KSTEPS];
 #pragma unroll
                 for (int s2 = 0; s2 < KSTEPS; s2++)
-                    kf[s2] = *(const half8 *)(ks + (kb * 32 + lq) * (D * 2) + (((2 * s2 + lg) ^ xk) << 4));
+                    kf[s2] = *(const half8 *)(ks + (kb * 32 + lq) * (DK * 2) + (C::kchunk(kb * 32 + lq, 2 * s2 + lg) << 4));
 #pragma unroll
                 for (int e = 0; e < 16; e++) sacc[kb][e] = 0.0f;
 #pragma unroll
@@ -455,6 +477,10 @@ fa_kernel(FaArgs a) {
         if (2 * stp + FA_NS < ntl) {   // block-uniform; the wait above counts nothing issued later
             issue(2 * stp + FA_NS);
             issue(2 * stp + FA_NS + 1);
+            if constexpr (FA_NS == 2) {   // no tiles in flight behind these: wait for them here
+                fa_wait_vm_lgkm0<0>();
+                __builtin_amdgcn_s_barrier();
+            }
         }
     }
     fa_wait_vm_lgkm0<0>();   // no DMA may still be writing LDS: the merge below reuses the ring
@@ -507,7 +533,7 @@ fa_kernel(FaArgs a) {
     if (!qok) return;
     const int64_t rows = (int64_t)a.T * a.H;
     const int64_t row = (int64_t)split * rows + (int64_t)tq * a.H + h;
-    float * po = a.part_o + row * D;
+    float * po = a.part_o + row * DV;
 #pragma unroll
     for (int db = 0; db < DBLK; db++)
 #pragma unroll
@@ -525,7 +551,8 @@ fa_kernel(FaArgs a) {
 }
 
 // Merge the nsplit partials of every (token, head) row:
-// O = sum_s exp(m_s - M) O_s / sum_s exp(m_s - M) l_s. D/4 threads per row, a float4 each.
+// O = sum_s exp(m_s - M) O_s / sum_s exp(m_s - M) l_s. D/4 threads per row, a float4 each
+// (D = DV, the output head dim).
 template <int D>
 __global__ void __launch_bounds__(256) fa_combine_kernel(FaArgs a) {
     constexpr int TPR = D / 4;
@@ -570,54 +597,56 @@ int fa_prep_blocks(const FaArgs & a) {
 }
 
 // the ring plus the class rows of up to FA_TASKS query tiles
-static size_t fa_lds_bytes(const FaArgs & a) {
-    const size_t ring = a.D == 64 ? FaCfg<64>::LDS : FaCfg<128>::LDS;
-    return ring + (size_t)FA_TASKS * a.cls_stride;
+static size_t fa_ring_bytes(int D, int DV) {
+    if (D == 64 && DV == 64) return FaCfg<64, 64>::LDS;
+    if (D == 128 && DV == 128) return FaCfg<128, 128>::LDS;
+    if (D == 192 && DV == 128) return FaCfg<192, 128>::LDS;
+    return 0;
 }
-constexpr int FA_LDS_MAX = 160 * 1024;
+static size_t fa_lds_bytes(const FaArgs & a) { return fa_ring_bytes(a.D, a.DV) + (size_t)FA_TASKS * a.cls_stride; }
 
-size_t fa_max_kv() {
-    // class rows of FA_TASKS query tiles must fit beside the larger ring
-    return (size_t)(FA_LDS_MAX - FaCfg<128>::LDS - 64) / FA_TASKS / 16 * 16 * FA_BKV;
+bool fa_dims_supported(int D, int DV) { return fa_ring_bytes(D, DV) != 0; }
+
+size_t fa_max_kv(int D, int DV) {
+    const size_t ring = fa_ring_bytes(D, DV);
+    if (!ring) return 0;
+    // class rows of FA_TASKS query tiles (one byte per 64-key tile, rows of a multiple of 16)
+    return (size_t)(FA_LDS_MAX - ring - 64) / FA_TASKS / 16 * 16 * FA_BKV;
 }
 
-template <int D, bool SC>
+template <int DK, int DV, bool SC>
 static hipError_t fa_launch_main(const FaArgs & a, int nb, hipStream_t st) {
     static bool done = false;
     if (!done) {
-        hipError_t e = hipFuncSetAttribute((const void *)fa_kernel<D, SC>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                           FA_LDS_MAX - 64);
+        hipError_t e = hipFuncSetAttribute((const void *)fa_kernel<DK, DV, SC>,
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, FA_LDS_MAX - 64);
         if (e != hipSuccess) return e;
         done = true;
     }
-    hipLaunchKernelGGL((fa_kernel<D, SC>), dim3(nb), dim3(FA_THREADS), fa_lds_bytes(a), st, a);
+    hipLaunchKernelGGL((fa_kernel<DK, DV, SC>), dim3(nb), dim3(FA_THREADS), fa_lds_bytes(a), st, a);
+    return hipGetLastError();
+}
+
+template <int DK, int DV>
+static hipError_t fa_launch_all(const FaArgs & a, int nb, hipStream_t st) {
+    hipLaunchKernelGGL(fa_prep_kernel<DV>, dim3(fa_prep_blocks(a)), dim3(256), 0, st, a);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    e = a.softcap != 0.0f ? fa_launch_main<DK, DV, true>(a, nb, st) : fa_launch_main<DK, DV, false>(a, nb, st);
+    if (e != hipSuccess || a.nsplit == 1) return e;
+    const int64_t rows = (int64_t)a.T * a.H;
+    const int rpb = 256 / (DV / 4);
+    hipLaunchKernelGGL(fa_combine_kernel<DV>, dim3((unsigned)((rows + rpb - 1) / rpb)), dim3(256), 0, st, a);
     return hipGetLastError();
 }
 
 hipError_t launch_fa(const FaArgs & a, hipStream_t st) {
     const int nb = fa_blocks_per_split(a) * a.nsplit;
     if (nb <= 0) return hipSuccess;
-    switch (a.D) {
-        case 64:
-            hipLaunchKernelGGL(fa_prep_kernel<64>, dim3(fa_prep_blocks(a)), dim3(256), 0, st, a);
-            break;
-        case 128:
-            hipLaunchKernelGGL(fa_prep_kernel<128>, dim3(fa_prep_blocks(a)), dim3(256), 0, st, a);
-            break;
-        default: return hipErrorInvalidValue;
-    }
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return e;
-    const bool sc = a.softcap != 0.0f;
-    if (a.D == 64) e = sc ? fa_launch_main<64, true>(a, nb, st) : fa_launch_main<64, false>(a, nb, st);
-    else e = sc ? fa_launch_main<128, true>(a, nb, st) : fa_launch_main<128, false>(a, nb, st);
-    if (e != hipSuccess || a.nsplit == 1) return e;
-    const int64_t rows = (int64_t)a.T * a.H;
-    const int rpb = 256 / (a.D / 4);
-    const dim3 grid((unsigned)((rows + rpb - 1) / rpb));
-    if (a.D == 64) hipLaunchKernelGGL(fa_combine_kernel<64>, grid, dim3(256), 0, st, a);
-    else hipLaunchKernelGGL(fa_combine_kernel<128>, grid, dim3(256), 0, st, a);
-    return hipGetLastError();
+    if (a.D == 64 && a.DV == 64) return fa_launch_all<64, 64>(a, nb, st);
+    if (a.D == 128 && a.DV == 128) return fa_launch_all<128, 128>(a, nb, st);
+    if (a.D == 192 && a.DV == 128) return fa_launch_all<192, 128>(a, nb, st);
+    return hipErrorInvalidValue;
 }
 
 }  // namespace mx

@@ -156,14 +156,15 @@ typedef struct mi355x_fa_args {
 /* The KV-split count mi355x_flash_attn uses when called with nsplit = 0. */
 MI355X_API int mi355x_flash_attn_auto_split(const mi355x_fa_args * a);
 
-/* Workspace bytes for `nsplit` KV splits (0 = auto): V transposed into [HK][D][KV rounded up to
+/* Workspace bytes for `nsplit` KV splits (0 = auto): V transposed into [HK][DV][KV rounded up to
  * 64], the per-tile mask classes, the split-merge counters and, for nsplit > 1, the partial
  * outputs. Always non-zero for a valid op; the workspace must be 256-byte aligned. */
 MI355X_API size_t mi355x_flash_attn_workspace(const mi355x_fa_args * a, int nsplit);
 
 /* dst = softmax(cap(scale * q.k) + mask) . v for every (token, head); head h reads KV head
  * h / (H / HK). Two kernels on `stream`: a prep pass over V and the mask, then the attention.
- * Concurrent calls must not share a workspace. D == DV in {64, 128}; H % HK == 0; max_bias
+ * Concurrent calls must not share a workspace. (D, DV) is (64, 64), (128, 128) or (192, 128)
+ * (MLA); H % HK == 0; max_bias
  * must be 0 (no ALiBi); the mask
  * covers [T][KV] with mask_nb1 % 4 == 0; q rows and dst rows 16-byte aligned; k/v rows 16-byte
  * aligned. Rows whose every key is masked are written as zeros. Replaces

@@ -8,7 +8,7 @@ import pytest
 import ggml_mi355x as mx
 from oracle import oracle as O
 from bars import compare, worst_col_cos, worst_row_cos, amp_for
-from fa_cases import REFERENCE_CASES, fill_case, SCALED, QRANGE
+from fa_cases import REFERENCE_CASES, fill_case, causal_mask, SCALED, QRANGE
 
 pytestmark = pytest.mark.gpu
 
@@ -177,6 +177,32 @@ def test_flash_attn_cases(be, case):
     err = float(np.abs(got.astype(np.float64) - want).max())
     print(f"{name}: max abs err {err:.3g} (tol {tol})")
     assert np.isfinite(got).all() and err <= tol
+
+
+def test_flash_attn_mla_graph(be):
+    """FLASH_ATTN_EXT with keys of 192 and values of 128 through graph_compute: dst takes its
+    row width from V (ne0 = dv), the device kernel runs, causal mask at n_kv 1024."""
+    D, DV, T, H, KV, HK = 192, 128, 128, 16, 1024, 2
+    Q = O.fill_normal((H, T, D), 960)
+    K16 = O.f32_to_f16_bits(O.fill_normal((HK, KV, D), 961))
+    V16 = O.f32_to_f16_bits(O.fill_normal((HK, KV, DV), 962))
+    M16 = O.f32_to_f16_bits(causal_mask(T, KV))
+    scale = float(np.float32(1.0) / np.sqrt(np.float32(D)))
+    want = O.flash_attn(Q, K16, V16, M16, scale)
+    g = mx.Graph()
+    q = g.new_tensor(mx.F32, [D, T, H])
+    k = g.new_tensor(mx.F16, [D, KV, HK])
+    v = g.new_tensor(mx.F16, [DV, KV, HK])
+    m = g.new_tensor(mx.F16, [KV, T])
+    g.set(q, Q), g.set(k, K16), g.set(v, V16), g.set(m, M16)
+    o = g.flash_attn_ext(q, k, v, m, scale)
+    mk = Mark(be, "fa")
+    assert be.compute([o]) == mx.STATUS_SUCCESS
+    mk.check("mla")
+    got = g.get(o, np.float32, (T, H, DV))
+    r = compare(want, got)
+    print(f"MLA graph: {r}")
+    assert r["nonfinite"] == 0 and r["max_abs"] <= 2e-2 and r["range_err"] <= 1e-2
 
 
 def _moe_graph(g, wt, K, N, E, ne11, U, T, payload, X, ids, name):

@@ -146,3 +146,30 @@ def test_fa_mask_holes_and_skipped_tiles(mx, H, HK):
         assert np.all(got[40:48] == 0.0), ns
         r = compare(want, got)
         assert r["nonfinite"] == 0 and r["max_abs"] <= 2e-2 and r["range_err"] <= 1e-2, (ns, r)
+
+
+@pytest.mark.parametrize("H,HK,softcap", [(16, 2, 0.0), (8, 8, 0.0), (16, 2, 30.0)])
+def test_fa_mla_k192_v128(mx, H, HK, softcap):
+    """Keys of 192 and values of 128 (DeepSeek-style MLA heads after decompression): causal
+    mask with scattered holes and a fully masked row, a ragged n_kv under a padded mask row,
+    GQA groups of 8 and 1, softcap; split-K off, on, and chosen by the library."""
+    D, DV, T, KV = 192, 128, 96, 601
+    Q = O.fill_normal((H, T, D), 950)
+    K16 = O.f32_to_f16_bits(O.fill_normal((HK, KV, D), 951))
+    V16 = O.f32_to_f16_bits(O.fill_normal((HK, KV, DV), 952))
+    # mask rows padded to 608 halves as ggml pads them; the columns past n_kv are never read
+    M = np.full((T, 608), 7.0, np.float32)
+    M[:, :KV] = causal_mask(T, KV)
+    rnd = O.fill_uniform((T, KV), 953, 1.0)
+    M[:, :KV][rnd > 0.7] = -np.inf
+    M[17, :] = -np.inf
+    M16 = O.f32_to_f16_bits(M)
+    scale = float(np.float32(1.0) / np.sqrt(np.float32(D)))
+    want = O.flash_attn(Q, K16, V16, M16, scale, softcap=softcap)
+    for ns in (1, 2, 0):
+        got = _run(mx, Q, K16, V16, M16, scale, softcap=softcap, nsplit=ns)
+        assert got.shape == (T, H, DV)
+        assert np.all(got[17] == 0.0), ns
+        r = compare(want, got)
+        print(f"MLA H={H} HK={HK} softcap={softcap} nsplit={ns}: {r}")
+        assert r["nonfinite"] == 0 and r["max_abs"] <= 2e-2 and r["range_err"] <= 1e-2, (ns, r)

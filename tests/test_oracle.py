@@ -310,3 +310,17 @@ def test_flash_attn_uniform_is_mean():
     for t in range(T):
         vis = KV - T + t + 1
         assert np.allclose(got[t, 0], Vf[0, :vis].astype(np.float64).mean(0), rtol=1e-6, atol=1e-7)
+
+
+def test_flash_attn_value_width_differs_from_key_width():
+    """K rows of 48 and V rows of 24 (the MLA shape family: keys wider than values); a wrong
+    stride on either operand breaks the match with the float64 softmax."""
+    D, DV, T, H, KV, HK = 48, 24, 7, 4, 33, 2
+    Q = O.fill_normal((H, T, D), 11)
+    K16 = O.f32_to_f16_bits(O.fill_normal((HK, KV, D), 12))
+    V16 = O.f32_to_f16_bits(O.fill_normal((HK, KV, DV), 13))
+    M16 = O.f32_to_f16_bits(causal_mask(T, KV))
+    Kf, Vf, Mf = O.f16_bits_to_f32(K16), O.f16_bits_to_f32(V16), O.f16_bits_to_f32(M16)
+    got = O.flash_attn(Q, K16, V16, M16, 0.15)
+    assert got.shape == (T, H, DV)
+    assert np.allclose(got, _np_attn(Q, Kf, Vf, Mf, 0.15), rtol=1e-5, atol=1e-6)
