@@ -107,4 +107,33 @@ __device__ __forceinline__ int xcd_tile(int bid, int nblocks) {
     return (bid % 8) * per + bid / 8;
 }
 
+// Multiplies a wave's MI x NJ accumulator tiles (32x32 MFMA output layout: element e of tile
+// row i is row base + 32 i + 8 (e / 4) + 4 lg + e % 4) by their row scales, loading every scale
+// and applying it before the caller's first output store. Loads and stores retire through one
+// in-order counter, so a scale loaded, or first used, between stores would wait for every
+// store issued before it: one memory round trip per row, which a row-by-row epilogue costs.
+template <int MI, int NJ, class Acc>
+__device__ __forceinline__ void scale_rows(Acc (&acc)[MI][NJ], const float * scales, int base, int lg,
+                                           int M) {
+    float rs[MI][16];
+#pragma unroll
+    for (int i = 0; i < MI; i++)
+#pragma unroll
+        for (int e = 0; e < 16; e++)
+            rs[i][e] = scales[min(base + i * 32 + 8 * (e / 4) + 4 * lg + (e % 4), M - 1)];
+#pragma unroll
+    for (int i = 0; i < MI; i++)
+#pragma unroll
+        for (int j = 0; j < NJ; j++)
+#pragma unroll
+            for (int e = 0; e < 16; e++) acc[i][j][e] *= rs[i][e];
+    // the empty asm keeps the products here: left alone, the compiler sinks each multiply into
+    // the bounds-checked store that consumes it, after earlier stores
+#pragma unroll
+    for (int i = 0; i < MI; i++)
+#pragma unroll
+        for (int j = 0; j < NJ; j++) asm volatile("" : "+v"(acc[i][j]));
+    __builtin_amdgcn_sched_barrier(0);
+}
+
 }  // namespace mx

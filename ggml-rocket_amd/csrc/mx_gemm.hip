@@ -17,6 +17,8 @@
 // and for fp16 weights one that moves both operands into LDS by DMA (gemm_f16_kernel). The
 // launcher picks a tile configuration of either per call from the output shape.
 
+#include <cmath>
+
 #include "mx_weights.h"
 #include "mx_kernels_impl.h"
 
@@ -266,20 +268,20 @@ gemm_kernel(GemmArgs args) {
 
     // epilogue: C = scale[m] * acc
     const int lr = lane % 32, lg = lane / 32;
+    scale_rows(acc, args.scales, m0 + wm * C::TM, lg, args.M);
 #pragma unroll
     for (int i = 0; i < C::MI; i++) {
 #pragma unroll
         for (int e = 0; e < 16; e++) {
             const int r = m0 + wm * C::TM + i * 32 + 8 * (e / 4) + 4 * lg + (e % 4);
             if (r >= args.M) continue;
-            const float s = args.scales[r];
             float * crow = G.C + (int64_t)r * G.ldc;
 #pragma unroll
             for (int j = 0; j < C::NJ; j++) {
                 const int n = n0 + wn * C::TN + j * 32 + lr;
                 if (n < G.N) {
-                    if (KSPLIT == 1) crow[n] = acc[i][j][e] * s;
-                    else unsafeAtomicAdd(crow + n, acc[i][j][e] * s);
+                    if (KSPLIT == 1) crow[n] = acc[i][j][e];
+                    else unsafeAtomicAdd(crow + n, acc[i][j][e]);
                 }
             }
         }
@@ -487,20 +489,20 @@ gemm_f16_kernel(GemmArgs args) {
     }
 
     // epilogue: C = scale[m] * acc
+    scale_rows(acc, args.scales, m0 + wm * C::TM, lg, M);
 #pragma unroll
     for (int i = 0; i < C::MI; i++) {
 #pragma unroll
         for (int e = 0; e < 16; e++) {
             const int r = m0 + wm * C::TM + i * 32 + 8 * (e / 4) + 4 * lg + (e % 4);
             if (r >= M) continue;
-            const float sc = args.scales[r];
             float * crow = Cp + (int64_t)r * ldc;
 #pragma unroll
             for (int j = 0; j < C::NJ; j++) {
                 const int n = n0 + wn * C::TN + j * 32 + lr;
                 if (n < N) {
-                    if (KSPLIT == 1) crow[n] = acc[i][j][e] * sc;
-                    else unsafeAtomicAdd(crow + n, acc[i][j][e] * sc);
+                    if (KSPLIT == 1) crow[n] = acc[i][j][e];
+                    else unsafeAtomicAdd(crow + n, acc[i][j][e]);
                 }
             }
         }
@@ -532,32 +534,30 @@ struct ColsCfg {
     static_assert(LDS <= 160 * 1024, "LDS");
 };
 
+// The weight group a block's N tile falls in, resolved once per block from the kernel
+// arguments (a select chain: indexing args.g with a runtime value would copy the array to
+// scratch).
+struct ColsTile {
+    const uint16_t * W;
+    int64_t row0;
+    float * C;
+    int64_t ldc;
+    int N, n0, m0;
+};
+
 template <class C, int TNW, int COL0, bool TL>
-__device__ __forceinline__ void cols_body(const GemmArgs & args, uint8_t * smem, int wm) {
+__device__ __forceinline__ void cols_body(const uint16_t * __restrict__ Ap, const float * __restrict__ scales,
+                                          int64_t lda, int M, int K, ColsTile tb, uint8_t * smem, int wm) {
     constexpr int DK = C::RB / 2, NS = C::NSTAGES, NJ = TNW / 32;
     constexpr int PB = TNW * C::RB / 4096;        // this column's B DMA per wave
     constexpr int PER = C::PA + PB;
     const int t = threadIdx.x, lane = t % WAVE, wave = t / WAVE;
-
-    const int tile = xcd_tile(blockIdx.x, gridDim.x);
-    const int mt = tile % args.m_tiles, nt = tile / args.m_tiles;
-    int g = 0;
-#pragma unroll
-    for (int i = 1; i < GEMM_MAX_GROUPS; i++)
-        if (i < args.ng && nt >= args.g[i].ntile_begin) g = i;
-    const uint16_t * W = (const uint16_t *)args.g[0].W;
-    int64_t row0 = args.g[0].row0;
-    int N = args.g[0].N, ntb = args.g[0].ntile_begin;
-    float * Cp = args.g[0].C;
-    int64_t ldc = args.g[0].ldc;
-#pragma unroll
-    for (int i = 1; i < GEMM_MAX_GROUPS; i++)
-        if (i == g) {
-            W = (const uint16_t *)args.g[i].W; row0 = args.g[i].row0; N = args.g[i].N;
-            ntb = args.g[i].ntile_begin; Cp = args.g[i].C; ldc = args.g[i].ldc;
-        }
-    const int n0 = (nt - ntb) * C::BN, m0 = mt * C::BM;
-    const int M = args.M, K = args.K;
+    const uint16_t * W = tb.W;
+    const int64_t row0 = tb.row0;
+    const int N = tb.N;
+    float * Cp = tb.C;
+    const int64_t ldc = tb.ldc;
+    const int n0 = tb.n0, m0 = tb.m0;
     const int nk = K / DK;
 
     const uint16_t * asrc[C::PA];
@@ -567,7 +567,7 @@ __device__ __forceinline__ void cols_body(const GemmArgs & args, uint8_t * smem,
         const int slot = (q * C::NW + wave) * WAVE + lane;
         const int r = slot / C::CH, c = (slot % C::CH) ^ ((r / C::RPW) & (C::CH - 1));
         const int64_t row = min(m0 + r, M - 1), k = 8 * c;
-        asrc[q] = args.A + (TL ? tiled_index(row, k, K) : row * args.lda + k);
+        asrc[q] = Ap + (TL ? tiled_index(row, k, K) : row * lda + k);
     }
 #pragma unroll
     for (int q = 0; q < PB; q++) {
@@ -652,18 +652,18 @@ __device__ __forceinline__ void cols_body(const GemmArgs & args, uint8_t * smem,
         wait_vm_lgkm0<0>();
     }
 
+    scale_rows(acc, scales, m0 + wm * C::TM, lg, M);
 #pragma unroll
     for (int i = 0; i < C::MI; i++) {
 #pragma unroll
         for (int e = 0; e < 16; e++) {
             const int r = m0 + wm * C::TM + i * 32 + 8 * (e / 4) + 4 * lg + (e % 4);
             if (r >= M) continue;
-            const float sc = args.scales[r];
             float * crow = Cp + (int64_t)r * ldc;
 #pragma unroll
             for (int j = 0; j < NJ; j++) {
                 const int n = n0 + COL0 + j * 32 + lr;
-                if (n < N) crow[n] = acc[i][j][e] * sc;
+                if (n < N) crow[n] = acc[i][j][e];
             }
         }
     }
@@ -675,8 +675,22 @@ gemm_f16_cols_kernel(GemmArgs args) {
     using C = ColsCfg<BM, BN0, BN1, DK, NS>;
     extern __shared__ __align__(16) uint8_t smem[];
     const int wave = threadIdx.x / WAVE;
-    if (wave / 4 == 0) cols_body<C, BN0, 0, TL>(args, smem, wave % 4);
-    else cols_body<C, BN1, BN0, TL>(args, smem, wave % 4);
+    const int tile = xcd_tile(blockIdx.x, gridDim.x);
+    const int mt = tile % args.m_tiles, nt = tile / args.m_tiles;
+    ColsTile tb;
+    tb.W = (const uint16_t *)args.g[0].W; tb.row0 = args.g[0].row0; tb.N = args.g[0].N;
+    tb.C = args.g[0].C; tb.ldc = args.g[0].ldc;
+    int ntb = args.g[0].ntile_begin;
+#pragma unroll
+    for (int i = 1; i < GEMM_MAX_GROUPS; i++)
+        if (i < args.ng && nt >= args.g[i].ntile_begin) {
+            tb.W = (const uint16_t *)args.g[i].W; tb.row0 = args.g[i].row0; tb.N = args.g[i].N;
+            tb.C = args.g[i].C; tb.ldc = args.g[i].ldc; ntb = args.g[i].ntile_begin;
+        }
+    tb.n0 = (nt - ntb) * C::BN;
+    tb.m0 = mt * C::BM;
+    if (wave / 4 == 0) cols_body<C, BN0, 0, TL>(args.A, args.scales, args.lda, args.M, args.K, tb, smem, wave % 4);
+    else cols_body<C, BN1, BN0, TL>(args.A, args.scales, args.lda, args.M, args.K, tb, smem, wave % 4);
 }
 
 // Zero the outputs of a split-K launch (a fill kernel rather than a memset, so the launch
@@ -803,38 +817,43 @@ hipError_t launch_pack_act_tiled(const float * X, int64_t ldx, int M, int K, uin
 // forces one (for tuning and for the tests, which run every configuration).
 //   0-3  register-staged kernel with the weight decoded into LDS: every weight type.
 //   4-15 LDS-DMA kernel: fp16 weights only (row-major or tiled); 15 has wave columns of two
-//        widths (gemm_f16_cols_kernel). choose_cfg prices a launch as
-//        max(rounds * (ov_us + MFMA work of a block / tf_cu), L2->CU bytes of all blocks / bw):
-//        a block's own pace (pipeline fill and epilogue, then its per-CU MFMA rate) or the
-//        aggregate rate at which the L2s feed the CUs for that tile shape (bigger tiles fetch
-//        less per FLOP but keep fewer bytes in flight per CU). All three were fitted to
-//        measurements of each configuration on tiled weights at M = 512, K = 2048-14336, each
-//        launch on a weight panel no earlier launch left in the caches (worst error 9%, most
-//        under 5%).
+//        widths (gemm_f16_cols_kernel). choose_cfg prices a launch from two rates: a block's
+//        own pace, rounds * (ov_us + MFMA work of a block / tf_cu) (pipeline fill and epilogue,
+//        then its per-CU MFMA rate), and the aggregate rate at which the L2s feed the CUs for
+//        that tile shape, L2->CU bytes of all blocks / bw (bigger tiles fetch less per FLOP but
+//        keep fewer bytes in flight per CU). The two overlap, so the estimate is their 4-norm
+//        (pace^4 + feed^4)^(1/4), which follows the measured transition between the regimes
+//        better than the max; a split-K launch adds zc microseconds per MB of output (the zero
+//        fill and the second addend's atomics). The four were fitted per configuration to
+//        measurements on tiled weights at M = 128-2048, N = 1024-28672, K = 2880-14336, each
+//        launch on a weight panel no earlier launch left in the caches: mean error 3-9% per
+//        configuration, and over 50 shapes the chosen configurations cost 0.3% more than the
+//        best measured ones.
 struct CfgDesc {
     int bm, bn, ksplit;
     int dk;          // K per LDS stage of the DMA kernel; 0 for the register-staged kernel
     double tf_cu;    // TFLOP/s per CU
     double ov_us;    // fixed microseconds per block
     double bw;       // aggregate L2 -> CU TB/s
+    double zc;       // split-K: microseconds per MB of output
 };
 static const CfgDesc kCfgs[] = {
-    {128, 128, 1, 0, 0.0, 0.0, 0.0},        // 0: 4 waves of 64x64
-    {128, 128, 2, 0, 0.0, 0.0, 0.0},        // 1: same, K split in two
-    {256, 128, 1, 0, 0.0, 0.0, 0.0},        // 2: 4 waves of 128x64
-    {128, 256, 1, 0, 0.0, 0.0, 0.0},        // 3: 4 waves of 64x128
-    {256, 256, 1, 64, 6.4, 19.0, 6.75},     // 4: 8 waves of 64x128, 2 stages of 64
-    {128, 128, 1, 64, 3.5, 0.0, 9.75},      // 5: 8 waves of 32x64, 4 stages of 64
-    {64, 128, 1, 128, 2.5, 7.0, 13.25},     // 6: 4 waves of 32x64, 3 stages of 128
-    {128, 64, 1, 128, 2.6, 7.0, 13.5},      // 7: 4 waves of 64x32, 3 stages of 128
-    {128, 128, 2, 64, 6.3, 29.0, 10.0},     // 8: as 5, K split in two
-    {64, 128, 2, 128, 3.0, 17.0, 11.25},    // 9: as 6, K split in two
-    {128, 128, 1, 32, 4.0, 0.0, 10.0},      // 10: 8 waves of 32x64, 4 stages of 32 (any K)
-    {128, 128, 1, 32, 4.0, 0.0, 10.0},      // 11: 8 waves of 32x64, 8 stages of 32
-    {256, 128, 1, 64, 5.8, 16.0, 8.75},     // 12: 8 waves of 64x64, 3 stages of 64
-    {128, 256, 1, 64, 5.6, 15.0, 8.75},     // 13: 8 waves of 64x64, 3 stages of 64
-    {64, 128, 1, 64, 2.4, 5.0, 12.5},       // 14: 4 waves of 32x64, 6 stages of 64
-    {256, 224, 1, 64, 6.4, 19.0, 7.4},      // 15: 8 waves of 64x128 and 64x96, 2 stages of 64
+    {128, 128, 1, 0, 0.0, 0.0, 0.0, 0.0},        // 0: 4 waves of 64x64
+    {128, 128, 2, 0, 0.0, 0.0, 0.0, 0.0},        // 1: same, K split in two
+    {256, 128, 1, 0, 0.0, 0.0, 0.0, 0.0},        // 2: 4 waves of 128x64
+    {128, 256, 1, 0, 0.0, 0.0, 0.0, 0.0},        // 3: 4 waves of 64x128
+    {256, 256, 1, 64, 6.32, 5.8, 8.01, 0.00},   // 4: 8 waves of 64x128, 2 stages of 64
+    {128, 128, 1, 64, 4.00, 0.0, 13.04, 0.00},  // 5: 8 waves of 32x64, 4 stages of 64
+    {64, 128, 1, 128, 2.68, 4.6, 16.76, 0.00},  // 6: 4 waves of 32x64, 3 stages of 128
+    {128, 64, 1, 128, 2.92, 5.6, 17.65, 0.00},  // 7: 4 waves of 64x32, 3 stages of 128
+    {128, 128, 2, 64, 3.51, 0.0, 24.93, 2.22},  // 8: as 5, K split in two
+    {64, 128, 2, 128, 2.47, 6.0, 40.00, 1.15},  // 9: as 6, K split in two
+    {128, 128, 1, 32, 4.37, 0.0, 12.94, 0.00},  // 10: 8 waves of 32x64, 4 stages of 32 (any K)
+    {128, 128, 1, 32, 4.34, 0.0, 12.96, 0.00},  // 11: 8 waves of 32x64, 8 stages of 32
+    {256, 128, 1, 64, 5.64, 8.9, 10.91, 0.00},  // 12: 8 waves of 64x64, 3 stages of 64
+    {128, 256, 1, 64, 5.30, 5.1, 11.29, 0.00},  // 13: 8 waves of 64x64, 3 stages of 64
+    {64, 128, 1, 64, 2.54, 1.7, 17.37, 0.00},   // 14: 4 waves of 32x64, 6 stages of 64
+    {256, 224, 1, 64, 5.74, 0.8, 8.79, 0.00},   // 15: 8 waves of 64x128 and 64x96, 2 stages of 64
 };
 constexpr int FIRST_DMA_CFG = 4;
 constexpr int N_CFGS = sizeof(kCfgs) / sizeof(kCfgs[0]);
@@ -932,6 +951,12 @@ static int tiles_of(const GemmArgs & a, int bm, int bn) {
     return nt * ((a.M + bm - 1) / bm);
 }
 
+static int64_t tiles_n_cols(const GemmArgs & a) {
+    int64_t n = 0;
+    for (int i = 0; i < a.ng; i++) n += a.g[i].N;
+    return n;
+}
+
 static bool cfg_fits(int c, int wt, int K) {
     const CfgDesc & d = kCfgs[c];
     if (d.dk == 0) return wt != T_F16T;
@@ -963,8 +988,9 @@ static int choose_cfg(int wt, const GemmArgs & a) {
             const double kb = (double)a.K / d.ksplit;
             const double pace = rounds * (d.ov_us + 2.0 * d.bm * d.bn * kb / (d.tf_cu * 1e6));
             const double feed = (double)blocks * (d.bm + d.bn) * kb * 2.0 / (d.bw * 1e6);
-            double us = pace > feed ? pace : feed;
-            if (d.ksplit > 1) us += 3.0;   // the zero fill of the output
+            const double p2 = pace * pace, f2 = feed * feed;
+            double us = std::sqrt(std::sqrt(p2 * p2 + f2 * f2));
+            if (d.ksplit > 1) us += d.zc * (double)a.M * tiles_n_cols(a) * 4.0 / 1e6;
             if (best < 0 || us < best_us - 1e-9) { best = c; best_us = us; }
         }
         if (best >= 0) return best;

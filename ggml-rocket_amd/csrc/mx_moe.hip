@@ -182,18 +182,27 @@ __global__ void __launch_bounds__(MOE_THREADS) moe_gemm_kernel(MoeArgs a) {
         __syncthreads();
     }
 
-    // scatter: tile row i -> dst[t][s][:], scaled back by the row's activation scale
+    // scatter: tile row i -> dst[t][s][:], scaled back by the row's activation scale. Every
+    // scale is loaded and applied before the first store: a load issued, or first used, after a
+    // store waits for that store too (one in-order counter).
+    float rs[16];
+#pragma unroll
+    for (int i = 0; i < 16; i++) rs[i] = a.scales[max(arow[8 * (i / 4) + 4 * lg + (i % 4)], 0)];
+#pragma unroll
+    for (int j = 0; j < 2; j++)
+#pragma unroll
+        for (int i = 0; i < 16; i++) acc[j][i] *= rs[i];
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int i = 0; i < 16; i++) {
         const int rl = 8 * (i / 4) + 4 * lg + (i % 4);
         const int r = orow[rl];
         if (r < 0) continue;
-        const float s = a.scales[arow[rl]];
         float * d = a.dst + (int64_t)(r / a.U) * a.dst_nb2 + (int64_t)(r % a.U) * a.dst_nb1;
 #pragma unroll
         for (int j = 0; j < 2; j++) {
             const int n = n0 + wave * 64 + j * 32 + lr;
-            if (n < a.N) d[n] = acc[j][i] * s;
+            if (n < a.N) d[n] = acc[j][i];
         }
     }
 }
