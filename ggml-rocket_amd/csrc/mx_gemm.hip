@@ -695,11 +695,18 @@ gemm_f16_cols_kernel(GemmArgs args) {
 
 // Zero the outputs of a split-K launch (a fill kernel rather than a memset, so the launch
 // sequence stays capturable).
-__global__ void zero_rows_kernel(GemmArgs args) {
+// Zeroes the outputs a split-K launch adds into: one block per (row, weight group), 16-byte
+// stores where the row start allows them.
+__global__ void __launch_bounds__(256) zero_rows_kernel(GemmArgs args) {
     const GemmGroup & G = args.g[blockIdx.y];
-    const int64_t n = (int64_t)args.M * G.N;
-    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
-        G.C[(i / G.N) * G.ldc + i % G.N] = 0.0f;
+    float * row = G.C + (int64_t)blockIdx.x * G.ldc;
+    const int N = G.N;
+    int c0 = 0;
+    if ((reinterpret_cast<uintptr_t>(row) & 15) == 0) {
+        for (int c = 4 * threadIdx.x; c + 3 < N; c += 4 * blockDim.x) *(float4v *)(row + c) = float4v{0, 0, 0, 0};
+        c0 = N & ~3;
+    }
+    for (int c = c0 + threadIdx.x; c < N; c += blockDim.x) row[c] = 0.0f;
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -842,18 +849,18 @@ static const CfgDesc kCfgs[] = {
     {128, 128, 2, 0, 0.0, 0.0, 0.0, 0.0},        // 1: same, K split in two
     {256, 128, 1, 0, 0.0, 0.0, 0.0, 0.0},        // 2: 4 waves of 128x64
     {128, 256, 1, 0, 0.0, 0.0, 0.0, 0.0},        // 3: 4 waves of 64x128
-    {256, 256, 1, 64, 6.32, 5.8, 8.01, 0.00},   // 4: 8 waves of 64x128, 2 stages of 64
-    {128, 128, 1, 64, 4.00, 0.0, 13.04, 0.00},  // 5: 8 waves of 32x64, 4 stages of 64
-    {64, 128, 1, 128, 2.68, 4.6, 16.76, 0.00},  // 6: 4 waves of 32x64, 3 stages of 128
-    {128, 64, 1, 128, 2.92, 5.6, 17.65, 0.00},  // 7: 4 waves of 64x32, 3 stages of 128
-    {128, 128, 2, 64, 3.51, 0.0, 24.93, 2.22},  // 8: as 5, K split in two
-    {64, 128, 2, 128, 2.47, 6.0, 40.00, 1.15},  // 9: as 6, K split in two
-    {128, 128, 1, 32, 4.37, 0.0, 12.94, 0.00},  // 10: 8 waves of 32x64, 4 stages of 32 (any K)
-    {128, 128, 1, 32, 4.34, 0.0, 12.96, 0.00},  // 11: 8 waves of 32x64, 8 stages of 32
-    {256, 128, 1, 64, 5.64, 8.9, 10.91, 0.00},  // 12: 8 waves of 64x64, 3 stages of 64
-    {128, 256, 1, 64, 5.30, 5.1, 11.29, 0.00},  // 13: 8 waves of 64x64, 3 stages of 64
-    {64, 128, 1, 64, 2.54, 1.7, 17.37, 0.00},   // 14: 4 waves of 32x64, 6 stages of 64
-    {256, 224, 1, 64, 5.74, 0.8, 8.79, 0.00},   // 15: 8 waves of 64x128 and 64x96, 2 stages of 64
+    {256, 256, 1, 64, 6.31, 5.6, 8.23, 0.00},   // 4: 8 waves of 64x128, 2 stages of 64
+    {128, 128, 1, 64, 3.99, 0.0, 13.35, 0.00},  // 5: 8 waves of 32x64, 4 stages of 64
+    {64, 128, 1, 128, 2.73, 5.1, 17.03, 0.00},  // 6: 4 waves of 32x64, 3 stages of 128
+    {128, 64, 1, 128, 2.88, 5.3, 17.64, 0.00},  // 7: 4 waves of 64x32, 3 stages of 128
+    {128, 128, 2, 64, 3.44, 0.0, 38.45, 1.70},  // 8: as 5, K split in two
+    {64, 128, 2, 128, 2.54, 6.8, 40.00, 0.60},  // 9: as 6, K split in two
+    {128, 128, 1, 32, 4.34, 0.0, 13.23, 0.00},  // 10: 8 waves of 32x64, 4 stages of 32 (any K)
+    {128, 128, 1, 32, 4.29, 0.0, 13.28, 0.00},  // 11: 8 waves of 32x64, 8 stages of 32
+    {256, 128, 1, 64, 5.60, 8.8, 11.29, 0.00},  // 12: 8 waves of 64x64, 3 stages of 64
+    {128, 256, 1, 64, 5.27, 4.9, 11.57, 0.00},  // 13: 8 waves of 64x64, 3 stages of 64
+    {64, 128, 1, 64, 2.53, 1.7, 18.04, 0.00},   // 14: 4 waves of 32x64, 6 stages of 64
+    {256, 224, 1, 64, 5.73, 0.5, 8.77, 0.00},   // 15: 8 waves of 64x128 and 64x96, 2 stages of 64
 };
 constexpr int FIRST_DMA_CFG = 4;
 constexpr int N_CFGS = sizeof(kCfgs) / sizeof(kCfgs[0]);
@@ -1024,7 +1031,7 @@ hipError_t launch_gemm(int wt, const GemmArgs & a_in, int /*unused*/, hipStream_
     const int nblocks = nt * a.m_tiles * d.ksplit;
     if (nblocks <= 0) return hipSuccess;
     if (d.ksplit > 1) {
-        hipLaunchKernelGGL(zero_rows_kernel, dim3(256, a.ng), dim3(256), 0, st, a);
+        hipLaunchKernelGGL(zero_rows_kernel, dim3(a.M, a.ng), dim3(256), 0, st, a);
         hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
     }
