@@ -59,8 +59,11 @@ __device__ __forceinline__ uint16_t f2h_bits(float f) {
 __device__ __forceinline__ float h2f_bits(uint16_t b) {
     return (float)__builtin_bit_cast(_Float16, b);
 }
+typedef float float2v __attribute__((ext_vector_type(2)));
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+// two f32 -> packed fp16, each rounded to nearest even (one v_cvt_pk_f16_f32)
 __device__ __forceinline__ uint32_t pack2h(float a, float b) {
-    return (uint32_t)f2h_bits(a) | ((uint32_t)f2h_bits(b) << 16);
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(float2v{a, b}, half2v));
 }
 
 // Separately rounded multiply and subtract: the decoders must not fuse d*q - m into one FMA,
@@ -86,6 +89,13 @@ __device__ __forceinline__ float sub_rn(float a, float b) {
     }
     asm volatile("" : "+v"(d));
     return d;
+}
+// a * b + c rounded once to f32, pinned there like mul_rn (no fold into an f16 conversion). Only
+// for operands whose product is exact in f32, where it equals sub_rn(mul_rn(a, b), -c).
+__device__ __forceinline__ float fma_rn(float a, float b, float c) {
+    float r = __builtin_fmaf(a, b, c);
+    asm volatile("" : "+v"(r));
+    return r;
 }
 
 __device__ __forceinline__ float wave_max(float v) {

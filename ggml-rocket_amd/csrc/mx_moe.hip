@@ -22,23 +22,51 @@
 
 namespace mx {
 
-constexpr int MOE_BM = 32;            // rows per tile (an expert receives ~32 rows at 512 tokens, top-8 of 128)
+constexpr int MOE_BM = 64;            // rows per tile: an expert receives ~32 rows (20-45) at 512 tokens, top-8
+                                      // of 128, so one tile each and every weight is decoded once
 constexpr int MOE_BN = 256;           // output columns per block: 4 waves x 64
 constexpr int MOE_BK = 64;
 constexpr int MOE_THREADS = 256;
-constexpr int MOE_A_BYTES = MOE_BM * MOE_BK * 2;   // 4 KiB
+constexpr int MOE_A_BYTES = MOE_BM * MOE_BK * 2;   // 8 KiB
 constexpr int MOE_B_BYTES = MOE_BN * MOE_BK * 2;   // 32 KiB
-constexpr int MOE_STAGE = MOE_A_BYTES + MOE_B_BYTES;
+constexpr int MOE_STAGE = MOE_A_BYTES + MOE_B_BYTES;   // two stages: 80 KiB, two blocks per CU
 constexpr int MOE_SORT_THREADS = 1024;
 
 // ---------------------------------------------------------------------------------------------
 // bucketing
 // ---------------------------------------------------------------------------------------------
+// Exclusive prefix sums of (x, y) over the block's threads, in thread order; returns the totals.
+__device__ __forceinline__ int2 block_scan2(int & x, int & y, int2 * wsum) {
+    const int t = threadIdx.x, lane = t % WAVE, wave = t / WAVE;
+    constexpr int NWAVES = MOE_SORT_THREADS / WAVE;
+    int ix = x, iy = y;   // inclusive within the wave
+#pragma unroll
+    for (int o = 1; o < WAVE; o <<= 1) {
+        const int px = __shfl_up(ix, o, WAVE), py = __shfl_up(iy, o, WAVE);
+        if (lane >= o) { ix += px; iy += py; }
+    }
+    if (lane == WAVE - 1) wsum[wave] = make_int2(ix, iy);
+    __syncthreads();
+    int bx = 0, by = 0, tx = 0, ty = 0;
+    for (int w = 0; w < NWAVES; w++) {
+        const int2 v = wsum[w];
+        if (w < wave) { bx += v.x; by += v.y; }
+        tx += v.x;
+        ty += v.y;
+    }
+    x = bx + ix - x;
+    y = by + iy - y;
+    return make_int2(tx, ty);
+}
+
+// One block: counts the (token, slot) rows of every expert, lays the experts' rows out
+// contiguously (bucket offsets off[e]) and lists the tiles of MOE_BM rows as (expert, first row).
+// Both prefix sums run across the block; rows are placed with LDS cursors.
 __global__ void __launch_bounds__(MOE_SORT_THREADS) moe_sort_kernel(MoeArgs a) {
     extern __shared__ __align__(16) int32_t sh[];
-    int32_t * cnt = sh;              // [E]
-    int32_t * cur = sh + a.E;        // [E]
+    int32_t * cnt = sh;              // [E] rows per expert, then the placement cursor
     __shared__ int32_t bad;
+    __shared__ int2 wsum[MOE_SORT_THREADS / WAVE];
     const int t = threadIdx.x;
     const int R = a.T * a.U;
     for (int e = t; e < a.E; e += MOE_SORT_THREADS) cnt[e] = 0;
@@ -51,21 +79,28 @@ __global__ void __launch_bounds__(MOE_SORT_THREADS) moe_sort_kernel(MoeArgs a) {
         else atomicAdd(&cnt[e], 1);
     }
     __syncthreads();
-    if (t == 0) {
-        int32_t o = 0, tl = 0;
-        for (int e = 0; e < a.E; e++) {
-            const int c = cnt[e];
-            a.off[e] = o;
-            cur[e] = o;
-            for (int m0 = 0; m0 < c; m0 += MOE_BM) {
-                a.tiles[2 * tl] = e;
-                a.tiles[2 * tl + 1] = m0;
-                tl++;
-            }
-            o += c;
+    // thread t owns experts [t * per, (t + 1) * per)
+    const int per = (a.E + MOE_SORT_THREADS - 1) / MOE_SORT_THREADS;
+    const int e0 = min(t * per, a.E), e1 = min(e0 + per, a.E);
+    int rows = 0, tiles = 0;
+    for (int e = e0; e < e1; e++) {
+        rows += cnt[e];
+        tiles += (cnt[e] + MOE_BM - 1) / MOE_BM;
+    }
+    const int2 tot = block_scan2(rows, tiles, wsum);   // rows, tiles: this thread's first offsets
+    for (int e = e0; e < e1; e++) {
+        const int c = cnt[e];
+        a.off[e] = rows;
+        for (int m0 = 0; m0 < c; m0 += MOE_BM, tiles++) {
+            a.tiles[2 * tiles] = e;
+            a.tiles[2 * tiles + 1] = m0;
         }
-        a.off[a.E] = o;
-        a.n_tiles[0] = tl;
+        cnt[e] = rows;   // placement cursor
+        rows += c;
+    }
+    if (t == 0) {
+        a.off[a.E] = tot.x;
+        a.n_tiles[0] = tot.y;
         a.err[0] = bad;
     }
     __syncthreads();
@@ -73,7 +108,7 @@ __global__ void __launch_bounds__(MOE_SORT_THREADS) moe_sort_kernel(MoeArgs a) {
         const int tok = r / a.U, s = r % a.U;
         const int e = a.ids[(int64_t)tok * a.ids_nb1 + (int64_t)s * a.ids_nb0];
         if (e < 0 || e >= a.E) continue;
-        const int p = atomicAdd(&cur[e], 1);
+        const int p = atomicAdd(&cnt[e], 1);
         a.rows[p] = r;
     }
 }
@@ -81,130 +116,168 @@ __global__ void __launch_bounds__(MOE_SORT_THREADS) moe_sort_kernel(MoeArgs a) {
 // ---------------------------------------------------------------------------------------------
 // grouped expert GEMM
 // ---------------------------------------------------------------------------------------------
+// Block = (tile of MOE_BM rows of one expert, MOE_BN output columns); wave w owns columns
+// w*64 .. w*64+63 of the block for all MOE_BM rows (2 x 2 MFMA tiles of 32x32). Thread t stages
+// weight row n0 + t (decoded to fp16 on its way into LDS, as in the dense register-staged
+// GEMM) and two 16-byte chunks of the tile's gathered activation rows; loads run two K slabs
+// ahead of the MFMAs, so an HBM round trip has two slabs of work to hide behind.
 template <int WT>
-__global__ void __launch_bounds__(MOE_THREADS) moe_gemm_kernel(MoeArgs a) {
+__global__ void __launch_bounds__(MOE_THREADS) __attribute__((amdgpu_waves_per_eu(2, 2)))
+moe_gemm_kernel(MoeArgs a) {
     extern __shared__ __align__(16) uint8_t smem[];
-    __shared__ int32_t arow[MOE_BM];   // A16 row of each tile row (-1 = pad)
-    __shared__ int32_t orow[MOE_BM];   // flattened (t * U + s) of each tile row
 
     const int n_nt = (a.N + MOE_BN - 1) / MOE_BN;
     const int tile = blockIdx.x / n_nt, nt = blockIdx.x % n_nt;
     if (tile >= a.n_tiles[0]) return;   // uniform for the block
     const int e = a.tiles[2 * tile], m0 = a.tiles[2 * tile + 1];
     const int base = a.off[e];
-    const int cnt = a.off[e + 1] - base;
-    const int rows_here = min(MOE_BM, cnt - m0);
+    const int rows_here = min(MOE_BM, a.off[e + 1] - base - m0);
+    const int32_t * trows = a.rows + base + m0;   // the tile's bucketed rows (t * U + s)
 
     const int t = threadIdx.x, lane = t % WAVE, wave = t / WAVE;
-    if (t < MOE_BM) {
-        if (t < rows_here) {
-            const int r = a.rows[base + m0 + t];
-            const int tok = r / a.U, s = r % a.U;
-            arow[t] = tok * a.ne11 + (s % a.ne11);
-            orow[t] = r;
-        } else {
-            arow[t] = -1;
-            orow[t] = -1;
-        }
-    }
-    __syncthreads();
+    // the packed activation row of tile row r (-1: pad row)
+    auto act_row = [&](int r) -> int {
+        if (r >= rows_here) return -1;
+        const int rr = trows[r];
+        const int tok = rr / a.U, s = rr % a.U;
+        return tok * a.ne11 + (s % a.ne11);
+    };
 
     const int K = a.K;
     const int n0 = nt * MOE_BN;
     const uint8_t * W = (const uint8_t *)a.w;
     const int64_t rows_total = (int64_t)a.E * a.N;
-    // weight rows: thread t stages row n0 + t (both 32-value halves of each slab)
     const int64_t wrow = (int64_t)e * a.N + min(n0 + t, a.N - 1);   // clamped: loads are unconditional
     const bool wok = n0 + t < a.N;
-    // A: thread t stages row t / 8, chunk t % 8
+    // A: thread t stages rows t / 8 and 32 + t / 8, chunk t % 8
     const int ar = t / 8, ac = t % 8;
-    const int arow_t = arow[ar];
+    const int arow0 = act_row(ar), arow1 = act_row(ar + 32);
 
-    float16v acc[2];
+    float16v acc[2][2];
 #pragma unroll
-    for (int j = 0; j < 2; j++)
+    for (int i = 0; i < 2; i++)
 #pragma unroll
-        for (int i = 0; i < 16; i++) acc[j][i] = 0.0f;
+        for (int j = 0; j < 2; j++)
+#pragma unroll
+            for (int q = 0; q < 16; q++) acc[i][j][q] = 0.0f;
 
-    auto load_a = [&](int64_t k0) -> u32x4 {
-        const int64_t k = k0 + 8 * ac;
-        if (arow_t < 0 || k >= K) return u32x4{0, 0, 0, 0};
-        return *(const u32x4 *)(a.a16 + (int64_t)arow_t * K + k);
+    struct Stage {
+        u32x4 a0, a1;
+        WLoad<WT> w0, w1;
     };
-    auto store_stage = [&](uint8_t * st, const u32x4 & av, const WLoad<WT> & w0, const WLoad<WT> & w1) {
-        *(u32x4 *)(st + swz<8>(ar, ac)) = av;
+    auto load_a = [&](int arow, int64_t k0) -> u32x4 {
+        const int64_t k = k0 + 8 * ac;
+        if (arow < 0 || k >= K) return u32x4{0, 0, 0, 0};
+        return *(const u32x4 *)(a.a16 + (int64_t)arow * K + k);
+    };
+    const int nk = (K + MOE_BK - 1) / MOE_BK;
+    auto load = [&](Stage & g, int kt) {
+        const int64_t k0 = (int64_t)min(kt, nk - 1) * MOE_BK;   // past the end: a repeat nobody uses
+        g.a0 = load_a(arow0, k0);
+        g.a1 = load_a(arow1, k0);
+        g.w0.load(W, rows_total, K, wrow, k0, 0, wok);
+        g.w1.load(W, rows_total, K, wrow, k0, 1, wok);
+    };
+    auto store = [&](uint8_t * st, const Stage & g) {
+        *(u32x4 *)(st + swz<8>(ar, ac)) = g.a0;
+        *(u32x4 *)(st + swz<8>(ar + 32, ac)) = g.a1;
         uint8_t * bs = st + MOE_A_BYTES;
         u32x4 o[4];
         int r0, r1;
-        w0.decode(0, o, r0, r1);
+        g.w0.decode(0, o, r0, r1);
         *(u32x4 *)(bs + swz<8>(t, r0 / 8)) = o[0];
         *(u32x4 *)(bs + swz<8>(t, r0 / 8 + 1)) = o[1];
         *(u32x4 *)(bs + swz<8>(t, r1 / 8)) = o[2];
         *(u32x4 *)(bs + swz<8>(t, r1 / 8 + 1)) = o[3];
-        w1.decode(1, o, r0, r1);
+        g.w1.decode(1, o, r0, r1);
         *(u32x4 *)(bs + swz<8>(t, r0 / 8)) = o[0];
         *(u32x4 *)(bs + swz<8>(t, r0 / 8 + 1)) = o[1];
         *(u32x4 *)(bs + swz<8>(t, r1 / 8)) = o[2];
         *(u32x4 *)(bs + swz<8>(t, r1 / 8 + 1)) = o[3];
     };
 
-    const int nk = (K + MOE_BK - 1) / MOE_BK;
-    WLoad<WT> w0, w1;
-    u32x4 av = load_a(0);
-    w0.load(W, rows_total, K, wrow, 0, 0, wok);
-    w1.load(W, rows_total, K, wrow, 0, 1, wok);
-    store_stage(smem, av, w0, w1);
-    __syncthreads();
-
     const int lr = lane % 32, lg = lane / 32;
-    for (int kt = 0; kt < nk; kt++) {
-        const int cur = kt & 1;
-        const bool more = kt + 1 < nk;
-        if (more) {
-            const int64_t k0 = (int64_t)(kt + 1) * MOE_BK;
-            av = load_a(k0);
-            w0.load(W, rows_total, K, wrow, k0, 0, wok);
-            w1.load(W, rows_total, K, wrow, k0, 1, wok);
-        }
-        const uint8_t * As = smem + cur * MOE_STAGE;
-        const uint8_t * Bs = As + MOE_A_BYTES;
+    auto mma = [&](const uint8_t * st) {
+        const uint8_t * Bs = st + MOE_A_BYTES;
 #pragma unroll
         for (int ks = 0; ks < MOE_BK / 16; ks++) {
             const int c = 2 * ks + lg;
-            const half8 af = *(const half8 *)(As + swz<8>(lr, c));
+            half8 af[2], bf[2];
 #pragma unroll
-            for (int j = 0; j < 2; j++) {
-                const half8 bf = *(const half8 *)(Bs + swz<8>(wave * 64 + j * 32 + lr, c));
-                acc[j] = mfma32(af, bf, acc[j]);
-            }
+            for (int i = 0; i < 2; i++) af[i] = *(const half8 *)(st + swz<8>(i * 32 + lr, c));
+#pragma unroll
+            for (int j = 0; j < 2; j++) bf[j] = *(const half8 *)(Bs + swz<8>(wave * 64 + j * 32 + lr, c));
+#pragma unroll
+            for (int i = 0; i < 2; i++)
+#pragma unroll
+                for (int j = 0; j < 2; j++) acc[i][j] = mfma32(af[i], bf[j], acc[i][j]);
         }
-        if (more) store_stage(smem + (cur ^ 1) * MOE_STAGE, av, w0, w1);
-        __syncthreads();
-    }
+    };
 
-    // scatter: tile row i -> dst[t][s][:], scaled back by the row's activation scale. Every
-    // scale is loaded and applied before the first store: a load issued, or first used, after a
-    // store waits for that store too (one in-order counter).
-    float rs[16];
+    // Two register stages, as in gemm_kernel: step kk requests slab kk+2 into the stage slab kk
+    // came from (already in LDS), multiplies slab kk, then writes slab kk+1 into the other LDS
+    // buffer. The same loads and stores every step, no branch around them.
+    Stage g0, g1;
+    load(g0, 0);
+    load(g1, 1);
+    store(smem, g0);
+    __syncthreads();
+    auto step = [&](int kk, Stage & mine, Stage & next) {
+        load(mine, kk + 2);
+        mma(smem + (kk & 1) * MOE_STAGE);
+        store(smem + ((kk + 1) & 1) * MOE_STAGE, next);
+        __syncthreads();
+    };
+    int kk = 0;
+    for (; kk + 2 <= nk; kk += 2) {
+        step(kk, g0, g1);
+        step(kk + 1, g1, g0);
+    }
+    if (kk < nk) step(kk, g0, g1);
+
+    // scatter: tile row -> dst[t][s][:], scaled back by the row's activation scale. The rows and
+    // scales are loaded, and the scales applied, before the first store: a load issued, or first
+    // used, after a store waits for that store too (one in-order counter).
+    int orow[2][16];
+    float rs[2][16];
 #pragma unroll
-    for (int i = 0; i < 16; i++) rs[i] = a.scales[max(arow[8 * (i / 4) + 4 * lg + (i % 4)], 0)];
+    for (int i = 0; i < 2; i++)
 #pragma unroll
-    for (int j = 0; j < 2; j++)
+        for (int q = 0; q < 16; q++) {
+            const int rl = i * 32 + 8 * (q / 4) + 4 * lg + (q % 4);
+            orow[i][q] = rl < rows_here ? trows[rl] : -1;
+        }
 #pragma unroll
-        for (int i = 0; i < 16; i++) acc[j][i] *= rs[i];
+    for (int i = 0; i < 2; i++)
+#pragma unroll
+        for (int q = 0; q < 16; q++) {
+            const int r = max(orow[i][q], 0);
+            rs[i][q] = a.scales[(r / a.U) * a.ne11 + (r % a.U) % a.ne11];
+        }
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+#pragma unroll
+        for (int j = 0; j < 2; j++)
+#pragma unroll
+            for (int q = 0; q < 16; q++) acc[i][j][q] *= rs[i][q];
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+#pragma unroll
+        for (int j = 0; j < 2; j++) asm volatile("" : "+v"(acc[i][j]));
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (int i = 0; i < 16; i++) {
-        const int rl = 8 * (i / 4) + 4 * lg + (i % 4);
-        const int r = orow[rl];
-        if (r < 0) continue;
-        float * d = a.dst + (int64_t)(r / a.U) * a.dst_nb2 + (int64_t)(r % a.U) * a.dst_nb1;
+    for (int i = 0; i < 2; i++)
 #pragma unroll
-        for (int j = 0; j < 2; j++) {
-            const int n = n0 + wave * 64 + j * 32 + lr;
-            if (n < a.N) d[n] = acc[j][i];
+        for (int q = 0; q < 16; q++) {
+            const int r = orow[i][q];
+            if (r < 0) continue;
+            float * d = a.dst + (int64_t)(r / a.U) * a.dst_nb2 + (int64_t)(r % a.U) * a.dst_nb1;
+#pragma unroll
+            for (int j = 0; j < 2; j++) {
+                const int n = n0 + wave * 64 + j * 32 + lr;
+                if (n < a.N) d[n] = acc[i][j][q];
+            }
         }
-    }
 }
 
 int moe_max_tiles(int T, int U, int E) { return (T * U + MOE_BM - 1) / MOE_BM + E; }
@@ -215,7 +288,7 @@ hipError_t launch_moe(int wt, const MoeArgs & a, hipStream_t st) {
     hipError_t e = launch_pack_act(a.b, a.b_nb1, a.T * a.ne11, a.K, a.a16, a.K, a.scales, st);
     if (e != hipSuccess) return e;
     // 2. bucket
-    hipLaunchKernelGGL(moe_sort_kernel, dim3(1), dim3(MOE_SORT_THREADS), (size_t)2 * a.E * sizeof(int32_t), st, a);
+    hipLaunchKernelGGL(moe_sort_kernel, dim3(1), dim3(MOE_SORT_THREADS), (size_t)a.E * sizeof(int32_t), st, a);
     e = hipGetLastError();
     if (e != hipSuccess || R == 0) return e;
     // 3. grouped GEMM over an upper bound of tiles

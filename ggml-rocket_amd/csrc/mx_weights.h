@@ -196,20 +196,28 @@ template <> struct WLoad<T_Q4_K> {
         int s0, m0, s1, m1;
         q4k_sm(2 * j, hdr[1], hdr[2], hdr[3], s0, m0);
         q4k_sm(2 * j + 1, hdr[1], hdr[2], hdr[3], s1, m1);
-        const float d0 = mul_rn(d, (float)s0), mm0 = mul_rn(dmin, (float)m0);
-        const float d1 = mul_rn(d, (float)s1), mm1 = mul_rn(dmin, (float)m1);
+        // d * sc and dmin * m have at most 17 significant bits and d * sc * q at most 21: all
+        // exact in f32, so one fma rounds d*sc*q - dmin*m exactly as the CPU's rounded product
+        // followed by the difference does
+        const float d0 = d * (float)s0, mm0 = dmin * (float)m0;
+        const float d1 = d * (float)s1, mm1 = dmin * (float)m1;
         uint32_t lo[8], hi[8];
 #pragma unroll
         for (int w = 0; w < 4; w++) {
-            const uint32_t word = qs[w];
+            uint32_t l4 = qs[w] & 0x0F0F0F0Fu, h4 = (qs[w] >> 4) & 0x0F0F0F0Fu;   // nibbles as bytes
+            // opaque to the compiler, so each byte converts with one v_cvt_f32_ubyteN instead of
+            // a 4-bit extract folded from the mask plus a conversion
+            asm volatile("" : "+v"(l4), "+v"(h4));
+            float fl[4], fh[4];
 #pragma unroll
-            for (int p = 0; p < 2; p++) {
-                const uint32_t b0 = (word >> (16 * p)) & 0xFFu, b1 = (word >> (16 * p + 8)) & 0xFFu;
-                lo[2 * w + p] = pack2h(sub_rn(mul_rn(d0, (float)(b0 & 15u)), mm0),
-                                       sub_rn(mul_rn(d0, (float)(b1 & 15u)), mm0));
-                hi[2 * w + p] = pack2h(sub_rn(mul_rn(d1, (float)(b0 >> 4)), mm1),
-                                       sub_rn(mul_rn(d1, (float)(b1 >> 4)), mm1));
+            for (int i = 0; i < 4; i++) {
+                fl[i] = fma_rn(d0, (float)((l4 >> (8 * i)) & 0xFFu), -mm0);
+                fh[i] = fma_rn(d1, (float)((h4 >> (8 * i)) & 0xFFu), -mm1);
             }
+            lo[2 * w] = pack2h(fl[0], fl[1]);
+            lo[2 * w + 1] = pack2h(fl[2], fl[3]);
+            hi[2 * w] = pack2h(fh[0], fh[1]);
+            hi[2 * w + 1] = pack2h(fh[2], fh[3]);
         }
         out[0] = u32x4{lo[0], lo[1], lo[2], lo[3]};
         out[1] = u32x4{lo[4], lo[5], lo[6], lo[7]};
