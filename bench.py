@@ -44,6 +44,39 @@ L_LAYERS, D_MODEL, FFN, NH, NKV, HD = 32, 4096, 14336, 32, 8, 128
 TOKENS, UBATCH = 2048, 512
 
 
+def synth_q4k(N, K, seed, sigma=0.02):
+    """Synthetic workload weights: an [N, K] matrix drawn from N(0, sigma) and quantized to ggml's
+    Q4_K blocks (144 bytes per 256 weights: fp16 d, fp16 dmin, 12 bytes of packed 6-bit
+    sub-block scales and mins, 128 bytes of nibbles). A plain min/max quantizer: every sub-block
+    of 32 spans [min(0, lo), hi] in 15 steps, the block's d / dmin are the largest sub-block
+    scale / min over 63. Returns the payload as flat uint8."""
+    import numpy as np
+    rng = np.random.default_rng(seed)
+    out = np.empty((N, K // 256, 144), dtype=np.uint8)
+    for r0 in range(0, N, 512):   # row chunks keep the temporaries cache-sized
+        n = min(512, N - r0)
+        B = (rng.standard_normal((n, K), dtype=np.float32) * np.float32(sigma)).reshape(n, K // 256, 8, 32)
+        lo = np.minimum(B.min(axis=3), np.float32(0))
+        sub_scale = (B.max(axis=3) - lo) * np.float32(1 / 15)
+        sub_min = -lo
+        d = (sub_scale.max(axis=2) * np.float32(1 / 63)).astype(np.float16)
+        dmin = (sub_min.max(axis=2) * np.float32(1 / 63)).astype(np.float16)
+        df = np.maximum(d.astype(np.float32), np.float32(1e-30))[..., None]
+        dmf = np.maximum(dmin.astype(np.float32), np.float32(1e-30))[..., None]
+        sc = np.clip(np.rint(sub_scale / df), 0, 63).astype(np.uint8)
+        mn = np.clip(np.rint(sub_min / dmf), 0, 63).astype(np.uint8)
+        step = np.maximum(df * sc, np.float32(1e-30))[..., None]
+        q = np.clip(np.rint((B + (dmf * mn)[..., None]) / step), 0, 15).astype(np.uint8)
+        o = out[r0:r0 + n]
+        o[..., 0:2] = d[..., None].view(np.uint8)
+        o[..., 2:4] = dmin[..., None].view(np.uint8)
+        o[..., 4:8] = sc[..., :4] | ((sc[..., 4:] >> 4) << 6)
+        o[..., 8:12] = mn[..., :4] | ((mn[..., 4:] >> 4) << 6)
+        o[..., 12:16] = (sc[..., 4:] & 15) | ((mn[..., 4:] & 15) << 4)
+        q = q.reshape(n, K // 256, 4, 2, 32)   # (64-weight group, low / high nibble, 32)
+        o[..., 16:] = (q[..., 0, :] | (q[..., 1, :] << 4)).reshape(n, K // 256, 128)
+    return out.reshape(-1)
+
 def parse():
     p = argparse.ArgumentParser()
     p.add_argument("--gpus", type=int, default=1)
@@ -56,6 +89,9 @@ def parse():
     p.add_argument("--host-path", action="store_true",
                    help="run the prefill through graph_compute with host tensors (the plugin "
                         "boundary, PCIe-inclusive) and print that rate instead")
+    p.add_argument("--moe", action="store_true",
+                   help="time MUL_MAT_ID at the 128-expert / top-8 / 512-token / d 2048 / FFN 768 Q4_K "
+                        "shape (gate/up and down, cold expert stacks) and print one JSON line")
     p.add_argument("--pmc-probe", action="store_true",
                    help="for hardware-counter runs: launch each distinct op of one layer once, "
                         "eagerly, then a plain 1 GiB device copy (the calibration kernel), and exit")
@@ -67,7 +103,6 @@ class Prefill:
         import numpy as np
         import torch
         import ggml_mi355x as mx
-        from oracle import oracle as O
         self.mx, self.torch, self.np = mx, torch, np
         self.route = route
         self.wt = mx.F16_T if route == "prepacked-q" else mx.Q4_K
@@ -82,10 +117,8 @@ class Prefill:
         self.host_q4 = {}
         base = {}
         for i, (name, (N, K)) in enumerate(shapes.items()):
-            W = O.fill_normal((N, K), 0x5EED0000 + 80 + i, 0.0, 0.02)
-            self.host_q4[name] = O.quantize(O.Q4_K, W)
-            base[name] = torch.from_numpy(self.host_q4[name].reshape(-1)).to(dev)
-            del W
+            self.host_q4[name] = synth_q4k(N, K, 0x5EED0000 + 80 + i)
+            base[name] = torch.from_numpy(self.host_q4[name]).to(dev)
         g = torch.Generator(device=dev)
         g.manual_seed(1234)
         self.layers = []
@@ -335,7 +368,6 @@ def host_path(args):
     import numpy as np
     os.environ.setdefault("MI355X_FLASH_ATTN_MIN_KV", str(UBATCH))   # claim every micro-batch's FA
     import ggml_mi355x as mx
-    from oracle import oracle as O
     be = mx.Backend()
     be.set_quant_resident(1)
     L, T = args.layers, UBATCH
@@ -345,7 +377,7 @@ def host_path(args):
     t0 = time.time()
     base = {}
     for i, (name, (N, K)) in enumerate(shapes.items()):
-        base[name] = O.quantize(O.Q4_K, O.fill_normal((N, K), 0x5EED0000 + 80 + i, 0.0, 0.02)).reshape(-1)
+        base[name] = synth_q4k(N, K, 0x5EED0000 + 80 + i)
     wg = mx.Graph()
     wts = []
     for li in range(L):
@@ -415,6 +447,81 @@ def host_path(args):
     print(json.dumps(out), flush=True)
 
 
+def moe_bench(args):
+    """MUL_MAT_ID expert GEMM at the mixture-of-experts prefill shape: 128 experts, top-8 routing
+    from a softmax over N(0, 1) router logits (ties to the lower index), 512 tokens, d_model 2048,
+    expert FFN 768; gate/up [128 x 768 x 2048] (b: one row per token) and down [128 x 2048 x 768]
+    (b: one row per token and slot), Q4_K experts quantized from N(0, 0.02), F32 activations.
+    Each op is timed through mi355x_mul_mat_id (pack, bucketing and grouped GEMM) on three
+    copies of its expert stack, cycled so no launch finds its weights in the 256 MB last-level
+    cache, 8 calls per captured HIP graph, HIP events around the replays on the launch stream.
+    The bound is HBM: bytes = expert weights at their stored size + F32 activations in + F32
+    outputs, each counted once."""
+    import numpy as np
+    import torch
+    import ggml_mi355x as mx
+    E, U, T, DM, FF = 128, 8, 512, 2048, 768
+    logits = np.random.default_rng(0x5EED0000 + 64).standard_normal((T, E), dtype=np.float32)
+    ids = np.argsort(-logits, axis=1, kind="stable")[:, :U].astype(np.int32)   # softmax is monotone
+    idt = torch.from_numpy(ids).cuda()
+    ops = {}
+    tot_us = tot_bytes = 0.0
+    for i, (name, N, K, ne11) in enumerate((("gate/up", FF, DM, 1), ("down", DM, FF, U))):
+        P = synth_q4k(E * N, K, 0x5EED0000 + 65 + i)
+        copies = [mx.upload_weight(mx.Q4_K, P, E * N, K) for _ in range(3)]
+        X = torch.randn(T, ne11, K, device="cuda")
+        out = torch.empty(T, U, N, device="cuda")
+        ws = torch.empty(1 << 26, dtype=torch.uint8, device="cuda")
+        cyc = [0]
+
+        def run():
+            w = copies[cyc[0] % 3]
+            cyc[0] += 1
+            mx.mul_mat_id(mx.Q4_K, w, E, N, K, X, idt, out=out, workspace=ws)
+        for _ in range(3):
+            run()
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            run()
+        torch.cuda.current_stream().wait_stream(side)
+        torch.cuda.synchronize()
+        with torch.cuda.graph(g):
+            for _ in range(8):
+                run()
+        g.replay()
+        torch.cuda.synchronize()
+        reps = max(2, args.steps // 2)
+        s0, s1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s0.record()
+        for _ in range(reps):
+            g.replay()
+        s1.record()
+        torch.cuda.synchronize()
+        us = s0.elapsed_time(s1) * 1e3 / (8 * reps)
+        nbytes = P.nbytes + X.numel() * 4 + out.numel() * 4
+        flop = 2.0 * T * U * N * K
+        ops[name] = {"us": round(us, 2), "GBps": round(nbytes / us / 1e3, 1), "tflops": round(flop / us / 1e6, 1),
+                     "weight_MB": round(P.nbytes / 1e6, 1)}
+        tot_us += us
+        tot_bytes += nbytes
+        del copies, X, out, ws, g
+        torch.cuda.empty_cache()
+    gbs = tot_bytes / tot_us / 1e3
+    print(json.dumps({
+        "metric": "MUL_MAT_ID expert GEMM GB/s (128 experts, top-8, 512 tok, d 2048, FFN 768, Q4_K)",
+        "value": round(gbs, 1), "unit": "GB/s", "n_gpus": 1, "higher_is_better": True,
+        "dtype": "f16", "data": "synthetic (Q4_K experts from N(0,0.02), N(0,1) activations and router logits)",
+        "config": {"workload": "MoE prefill expert GEMMs: gate/up and down, cold expert stacks",
+                   "experts": E, "top_k": U, "tokens": T, "d_model": DM, "ffn": FF},
+        "ops": ops,
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                     "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": None},
+    }))
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -425,6 +532,9 @@ def main():
     torch.cuda.set_device(0)
     if args.pmc_probe:
         pmc_probe(Prefill(args.route, 1))
+        return
+    if args.moe:
+        moe_bench(args)
         return
     if args.host_path:
         host_path(args)

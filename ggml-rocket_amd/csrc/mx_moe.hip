@@ -119,11 +119,18 @@ __global__ void __launch_bounds__(MOE_SORT_THREADS) moe_sort_kernel(MoeArgs a) {
 // Block = (tile of MOE_BM rows of one expert, MOE_BN output columns); wave w owns columns
 // w*64 .. w*64+63 of the block for all MOE_BM rows (2 x 2 MFMA tiles of 32x32). Thread t stages
 // weight row n0 + t (decoded to fp16 on its way into LDS, as in the dense register-staged
-// GEMM) and two 16-byte chunks of the tile's gathered activation rows; loads run two K slabs
-// ahead of the MFMAs, so an HBM round trip has two slabs of work to hide behind.
+// GEMM) and two 16-byte chunks of the tile's gathered activation rows; loads run R K slabs
+// ahead of the MFMAs, so an HBM round trip has R - 1 slabs of work to hide behind before its
+// data is decoded. The slab loop is bound by the decode's VALU work (about 5 instructions per
+// weight) once two blocks share a CU.
+// Two register stages for every type: one block per CU (one wave per SIMD) with 4 stages of
+// Q4_K lookahead ran at the same speed as with 2, so the slabs are not waiting on memory.
+template <int WT> constexpr int moe_stages() { return 2; }
+
 template <int WT>
 __global__ void __launch_bounds__(MOE_THREADS) __attribute__((amdgpu_waves_per_eu(2, 2)))
 moe_gemm_kernel(MoeArgs a) {
+    constexpr int R = moe_stages<WT>();
     extern __shared__ __align__(16) uint8_t smem[];
 
     const int n_nt = (a.N + MOE_BN - 1) / MOE_BN;
@@ -214,26 +221,43 @@ moe_gemm_kernel(MoeArgs a) {
         }
     };
 
-    // Two register stages, as in gemm_kernel: step kk requests slab kk+2 into the stage slab kk
-    // came from (already in LDS), multiplies slab kk, then writes slab kk+1 into the other LDS
-    // buffer. The same loads and stores every step, no branch around them.
-    Stage g0, g1;
-    load(g0, 0);
-    load(g1, 1);
-    store(smem, g0);
+    // R register stages: step kk requests slab kk+R into the stage slab kk came from (already in
+    // LDS), multiplies slab kk, then writes slab kk+1 into the other LDS buffer. The same loads
+    // and stores every step, no branch around them; the ring index of every step is a constant
+    // (loop unrolled by R, the remainder by a switch), so the stages stay in registers.
+    Stage g[R];
+#pragma unroll
+    for (int q = 0; q < R; q++) load(g[q], q);
+    store(smem, g[0]);
     __syncthreads();
     auto step = [&](int kk, Stage & mine, Stage & next) {
-        load(mine, kk + 2);
+        load(mine, kk + R);
         mma(smem + (kk & 1) * MOE_STAGE);
         store(smem + ((kk + 1) & 1) * MOE_STAGE, next);
         __syncthreads();
     };
     int kk = 0;
-    for (; kk + 2 <= nk; kk += 2) {
-        step(kk, g0, g1);
-        step(kk + 1, g1, g0);
+    for (; kk + R <= nk; kk += R) {
+#pragma unroll
+        for (int q = 0; q < R; q++) step(kk + q, g[q], g[(q + 1) % R]);
     }
-    if (kk < nk) step(kk, g0, g1);
+    switch (nk - kk) {   // 0 .. R-1 steps left, ring positions 0 .. R-2
+        case 3:
+            if constexpr (R > 3) {
+                step(kk, g[0], g[1]);
+                step(kk + 1, g[1], g[2]);
+                step(kk + 2, g[2], g[3 % R]);
+            }
+            break;
+        case 2:
+            if constexpr (R > 2) {
+                step(kk, g[0], g[1]);
+                step(kk + 1, g[1], g[2 % R]);
+            }
+            break;
+        case 1: step(kk, g[0], g[1]); break;
+        default: break;
+    }
 
     // scatter: tile row -> dst[t][s][:], scaled back by the row's activation scale. The rows and
     // scales are loaded, and the scales applied, before the first store: a load issued, or first
