@@ -24,12 +24,12 @@ namespace mx {
 
 constexpr int MOE_BM = 64;            // rows per tile: an expert receives ~32 rows (20-45) at 512 tokens, top-8
                                       // of 128, so one tile each and every weight is decoded once
-constexpr int MOE_BN = 256;           // output columns per block: 4 waves x 64
+constexpr int MOE_BN = 128;           // output columns per block: 4 waves x 32
 constexpr int MOE_BK = 64;
 constexpr int MOE_THREADS = 256;
 constexpr int MOE_A_BYTES = MOE_BM * MOE_BK * 2;   // 8 KiB
-constexpr int MOE_B_BYTES = MOE_BN * MOE_BK * 2;   // 32 KiB
-constexpr int MOE_STAGE = MOE_A_BYTES + MOE_B_BYTES;   // two stages: 80 KiB, two blocks per CU
+constexpr int MOE_B_BYTES = MOE_BN * MOE_BK * 2;   // 16 KiB
+constexpr int MOE_STAGE = MOE_A_BYTES + MOE_B_BYTES;   // two stages: 48 KiB, three blocks per CU
 constexpr int MOE_SORT_THREADS = 1024;
 
 // ---------------------------------------------------------------------------------------------
@@ -117,18 +117,20 @@ __global__ void __launch_bounds__(MOE_SORT_THREADS) moe_sort_kernel(MoeArgs a) {
 // grouped expert GEMM
 // ---------------------------------------------------------------------------------------------
 // Block = (tile of MOE_BM rows of one expert, MOE_BN output columns); wave w owns columns
-// w*64 .. w*64+63 of the block for all MOE_BM rows (2 x 2 MFMA tiles of 32x32). Thread t stages
-// weight row n0 + t (decoded to fp16 on its way into LDS, as in the dense register-staged
-// GEMM) and two 16-byte chunks of the tile's gathered activation rows; loads run R K slabs
-// ahead of the MFMAs, so an HBM round trip has R - 1 slabs of work to hide behind before its
-// data is decoded. The slab loop is bound by the decode's VALU work (about 5 instructions per
-// weight) once two blocks share a CU.
+// w*32 .. w*32+31 of the block for all MOE_BM rows (2 MFMA tiles of 32x32). Threads 2n and 2n+1
+// stage the two 32-value halves of weight row n0 + n (decoded to fp16 on their way into LDS, as
+// in the dense register-staged GEMM), and every thread two 16-byte chunks of the tile's
+// gathered activation rows; loads run R K slabs ahead of the MFMAs, so an HBM round trip has
+// R - 1 slabs of work to hide behind before its data is decoded. The slab loop is bound by the
+// decode's VALU work (about 5 instructions per weight); 128-column blocks fit three to a CU
+// (48 KiB of LDS each), so 768 of them (128 experts x 6 column blocks of a 768-wide gate/up)
+// are one even round over 256 CUs, where 256-column blocks left half the CUs with double work.
 // Two register stages for every type: one block per CU (one wave per SIMD) with 4 stages of
 // Q4_K lookahead ran at the same speed as with 2, so the slabs are not waiting on memory.
 template <int WT> constexpr int moe_stages() { return 2; }
 
 template <int WT>
-__global__ void __launch_bounds__(MOE_THREADS) __attribute__((amdgpu_waves_per_eu(2, 2)))
+__global__ void __launch_bounds__(MOE_THREADS) __attribute__((amdgpu_waves_per_eu(3, 3)))
 moe_gemm_kernel(MoeArgs a) {
     constexpr int R = moe_stages<WT>();
     extern __shared__ __align__(16) uint8_t smem[];
@@ -149,28 +151,43 @@ moe_gemm_kernel(MoeArgs a) {
         const int tok = rr / a.U, s = rr % a.U;
         return tok * a.ne11 + (s % a.ne11);
     };
+    // each tile row's output row offset in dst (-1: pad row) and activation scale, worked out
+    // once per block (the epilogue would otherwise divide by U for each of a lane's 32 rows)
+    __shared__ int64_t row_dst[MOE_BM];
+    __shared__ float row_sc[MOE_BM];
+    if (t < MOE_BM) {
+        int64_t off = -1;
+        float sc = 0.0f;
+        if (t < rows_here) {
+            const int rr = trows[t];
+            const int tok = rr / a.U, s = rr % a.U;
+            off = (int64_t)tok * a.dst_nb2 + (int64_t)s * a.dst_nb1;
+            sc = a.scales[tok * a.ne11 + (s % a.ne11)];
+        }
+        row_dst[t] = off;
+        row_sc[t] = sc;
+    }
 
     const int K = a.K;
     const int n0 = nt * MOE_BN;
     const uint8_t * W = (const uint8_t *)a.w;
     const int64_t rows_total = (int64_t)a.E * a.N;
-    const int64_t wrow = (int64_t)e * a.N + min(n0 + t, a.N - 1);   // clamped: loads are unconditional
-    const bool wok = n0 + t < a.N;
+    const int wr = t / 2, wu = t % 2;   // this thread's weight row in the block, and its half
+    const int64_t wrow = (int64_t)e * a.N + min(n0 + wr, a.N - 1);   // clamped: loads are unconditional
+    const bool wok = n0 + wr < a.N;
     // A: thread t stages rows t / 8 and 32 + t / 8, chunk t % 8
     const int ar = t / 8, ac = t % 8;
     const int arow0 = act_row(ar), arow1 = act_row(ar + 32);
 
-    float16v acc[2][2];
+    float16v acc[2];
 #pragma unroll
     for (int i = 0; i < 2; i++)
 #pragma unroll
-        for (int j = 0; j < 2; j++)
-#pragma unroll
-            for (int q = 0; q < 16; q++) acc[i][j][q] = 0.0f;
+        for (int q = 0; q < 16; q++) acc[i][q] = 0.0f;
 
     struct Stage {
         u32x4 a0, a1;
-        WLoad<WT> w0, w1;
+        WLoad<WT> w;
     };
     auto load_a = [&](int arow, int64_t k0) -> u32x4 {
         const int64_t k = k0 + 8 * ac;
@@ -182,8 +199,7 @@ moe_gemm_kernel(MoeArgs a) {
         const int64_t k0 = (int64_t)min(kt, nk - 1) * MOE_BK;   // past the end: a repeat nobody uses
         g.a0 = load_a(arow0, k0);
         g.a1 = load_a(arow1, k0);
-        g.w0.load(W, rows_total, K, wrow, k0, 0, wok);
-        g.w1.load(W, rows_total, K, wrow, k0, 1, wok);
+        g.w.load(W, rows_total, K, wrow, k0, wu, wok);
     };
     auto store = [&](uint8_t * st, const Stage & g) {
         *(u32x4 *)(st + swz<8>(ar, ac)) = g.a0;
@@ -191,16 +207,11 @@ moe_gemm_kernel(MoeArgs a) {
         uint8_t * bs = st + MOE_A_BYTES;
         u32x4 o[4];
         int r0, r1;
-        g.w0.decode(0, o, r0, r1);
-        *(u32x4 *)(bs + swz<8>(t, r0 / 8)) = o[0];
-        *(u32x4 *)(bs + swz<8>(t, r0 / 8 + 1)) = o[1];
-        *(u32x4 *)(bs + swz<8>(t, r1 / 8)) = o[2];
-        *(u32x4 *)(bs + swz<8>(t, r1 / 8 + 1)) = o[3];
-        g.w1.decode(1, o, r0, r1);
-        *(u32x4 *)(bs + swz<8>(t, r0 / 8)) = o[0];
-        *(u32x4 *)(bs + swz<8>(t, r0 / 8 + 1)) = o[1];
-        *(u32x4 *)(bs + swz<8>(t, r1 / 8)) = o[2];
-        *(u32x4 *)(bs + swz<8>(t, r1 / 8 + 1)) = o[3];
+        g.w.decode(wu, o, r0, r1);
+        *(u32x4 *)(bs + swz<8>(wr, r0 / 8)) = o[0];
+        *(u32x4 *)(bs + swz<8>(wr, r0 / 8 + 1)) = o[1];
+        *(u32x4 *)(bs + swz<8>(wr, r1 / 8)) = o[2];
+        *(u32x4 *)(bs + swz<8>(wr, r1 / 8 + 1)) = o[3];
     };
 
     const int lr = lane % 32, lg = lane / 32;
@@ -209,15 +220,12 @@ moe_gemm_kernel(MoeArgs a) {
 #pragma unroll
         for (int ks = 0; ks < MOE_BK / 16; ks++) {
             const int c = 2 * ks + lg;
-            half8 af[2], bf[2];
+            half8 af[2];
 #pragma unroll
             for (int i = 0; i < 2; i++) af[i] = *(const half8 *)(st + swz<8>(i * 32 + lr, c));
+            const half8 bf = *(const half8 *)(Bs + swz<8>(wave * 32 + lr, c));
 #pragma unroll
-            for (int j = 0; j < 2; j++) bf[j] = *(const half8 *)(Bs + swz<8>(wave * 64 + j * 32 + lr, c));
-#pragma unroll
-            for (int i = 0; i < 2; i++)
-#pragma unroll
-                for (int j = 0; j < 2; j++) acc[i][j] = mfma32(af[i], bf[j], acc[i][j]);
+            for (int i = 0; i < 2; i++) acc[i] = mfma32(af[i], bf, acc[i]);
         }
     };
 
@@ -259,48 +267,24 @@ moe_gemm_kernel(MoeArgs a) {
         default: break;
     }
 
-    // scatter: tile row -> dst[t][s][:], scaled back by the row's activation scale. The rows and
-    // scales are loaded, and the scales applied, before the first store: a load issued, or first
-    // used, after a store waits for that store too (one in-order counter).
-    int orow[2][16];
-    float rs[2][16];
+    // scatter: tile row -> dst[t][s][:], scaled back by the row's activation scale (both from
+    // the block's row table in LDS, written before the loop's first barrier)
 #pragma unroll
     for (int i = 0; i < 2; i++)
 #pragma unroll
-        for (int q = 0; q < 16; q++) {
-            const int rl = i * 32 + 8 * (q / 4) + 4 * lg + (q % 4);
-            orow[i][q] = rl < rows_here ? trows[rl] : -1;
-        }
+        for (int q = 0; q < 16; q++) acc[i][q] *= row_sc[i * 32 + 8 * (q / 4) + 4 * lg + (q % 4)];
 #pragma unroll
-    for (int i = 0; i < 2; i++)
-#pragma unroll
-        for (int q = 0; q < 16; q++) {
-            const int r = max(orow[i][q], 0);
-            rs[i][q] = a.scales[(r / a.U) * a.ne11 + (r % a.U) % a.ne11];
-        }
-#pragma unroll
-    for (int i = 0; i < 2; i++)
-#pragma unroll
-        for (int j = 0; j < 2; j++)
-#pragma unroll
-            for (int q = 0; q < 16; q++) acc[i][j][q] *= rs[i][q];
-#pragma unroll
-    for (int i = 0; i < 2; i++)
-#pragma unroll
-        for (int j = 0; j < 2; j++) asm volatile("" : "+v"(acc[i][j]));
+    for (int i = 0; i < 2; i++) asm volatile("" : "+v"(acc[i]));
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int i = 0; i < 2; i++)
 #pragma unroll
         for (int q = 0; q < 16; q++) {
-            const int r = orow[i][q];
-            if (r < 0) continue;
-            float * d = a.dst + (int64_t)(r / a.U) * a.dst_nb2 + (int64_t)(r % a.U) * a.dst_nb1;
-#pragma unroll
-            for (int j = 0; j < 2; j++) {
-                const int n = n0 + wave * 64 + j * 32 + lr;
-                if (n < a.N) d[n] = acc[i][j][q];
-            }
+            const int64_t off = row_dst[i * 32 + 8 * (q / 4) + 4 * lg + (q % 4)];
+            if (off < 0) continue;
+            float * d = a.dst + off;
+            const int n = n0 + wave * 32 + lr;
+            if (n < a.N) d[n] = acc[i][q];
         }
 }
 
