@@ -613,7 +613,8 @@ def main():
         "roofline": {"bound": "mfma", "achieved": round(gemm_tf, 1), "peak": PEAK_F16_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(gemm_tf / PEAK_F16_TFLOPS, 4),
                      "traffic": GEMM_TRAFFIC_BYTES[args.route],
-                     "kernel": "gemm_f16_kernel (LDS-DMA, fp16 MFMA 32x32x16)",
+                     "kernel": ("gemm_f16_kernel / gemm_f16_cols_kernel (LDS-DMA, fp16 MFMA 32x32x16)" if args.route == "prepacked-q"
+                                else "gemm_kernel<Q4_K> (register-staged, Q4_K decoded into LDS, fp16 MFMA 32x32x16)"),
                      "avg_launch_us": round(gemm["sec"] / gemm["launches"] * 1e6, 2),
                      "flop_per_launch": round(gemm["flops"] / gemm["launches"])},
         "kernels": {
