@@ -89,6 +89,11 @@ def parse():
     p.add_argument("--host-path", action="store_true",
                    help="run the prefill through graph_compute with host tensors (the plugin "
                         "boundary, PCIe-inclusive) and print that rate instead")
+    p.add_argument("--configs", action="store_true",
+                   help="time the single-op configurations (F16 MUL_MAT 8192x2048 at M 512; Q8_0 / Q4_K / "
+                        "Q6_K MUL_MAT at K,N in {3072x3072, 3072x8192, 8192x3072}, M in {32, 128, 512, "
+                        "2048}; FLASH_ATTN_EXT 32/8 heads, d 128, 512 queries, n_kv 1024/4096/8192) against "
+                        "their rooflines and print one JSON line")
     p.add_argument("--moe", action="store_true",
                    help="time MUL_MAT_ID at the 128-expert / top-8 / 512-token / d 2048 / FFN 768 Q4_K "
                         "shape (gate/up and down, cold expert stacks) and print one JSON line")
@@ -447,6 +452,122 @@ def host_path(args):
     print(json.dumps(out), flush=True)
 
 
+def graph_time_us(fn_of_i, n_calls, reps=3):
+    """Mean device time of fn_of_i(i), i = 0 .. n_calls-1, captured once into a HIP graph and
+    replayed `reps` times between HIP events on the launch stream."""
+    import torch
+    for i in range(min(n_calls, 3)):
+        fn_of_i(i)
+    torch.cuda.synchronize()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        fn_of_i(0)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for i in range(n_calls):
+            fn_of_i(i)
+    g.replay()
+    torch.cuda.synchronize()
+    s0, s1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s0.record()
+    for _ in range(reps):
+        g.replay()
+    s1.record()
+    torch.cuda.synchronize()
+    return s0.elapsed_time(s1) * 1e3 / (reps * n_calls)
+
+
+def synth_blocks(wtype, N, K, seed):
+    """Random but well-formed ggml blocks for a timing run: random codes under a fixed small
+    fp16 scale (Q8_0: d | qs[32]; Q6_K: ql[128] qh[64] scales[16] | d; Q4_K from synth_q4k)."""
+    import numpy as np
+    if wtype == 12:
+        return synth_q4k(N, K, seed)
+    bs, bb = {8: (32, 34), 14: (256, 210)}[wtype]
+    blk = np.random.default_rng(seed).integers(0, 256, size=(N * K // bs, bb), dtype=np.uint8)
+    d = np.array([0.0005], dtype=np.float16).view(np.uint8)
+    if wtype == 8:
+        blk[:, 0:2] = d
+    else:
+        blk[:, 208:210] = d
+    return blk.reshape(-1)
+
+
+def configs_bench(args):
+    """The single-op configurations, each through the C ABI entry the backend uses for it and
+    against the roofline that bounds it (arithmetic intensity against the 2.5 PFLOP/s / 8 TB/s
+    ridge of ~312 FLOP/byte). MUL_MAT: mi355x_mul_mat (activation pack + GEMM) on an HBM-resident
+    weight (F16 in the tiled fp16 layout; quantized types as ggml blocks, decoded in the GEMM),
+    bytes = weight at its stored size + F32 activations + F32 output; the weight rotates over
+    enough copies (>= 320 MB) that no call finds it in the 256 MB last-level cache.
+    FLASH_ATTN_EXT: mi355x_flash_attn, causal mask, FLOP = the dense rectangle 4 H T n_kv d (the
+    causal-visible share is reported beside it)."""
+    import numpy as np
+    import torch
+    import ggml_mi355x as mx
+    cases = {}
+
+    def record(name, us, flop, nbytes, extra=None):
+        ai = flop / nbytes
+        tf, gbs = flop / us / 1e6, nbytes / us / 1e3
+        bound = "mfma" if ai >= PEAK_F16_TFLOPS * 1e12 / (PEAK_HBM_GBS * 1e9) else "hbm"
+        frac = tf / PEAK_F16_TFLOPS if bound == "mfma" else gbs / PEAK_HBM_GBS
+        cases[name] = {"us": round(us, 2), "tflops": round(tf, 1), "GBps": round(gbs, 1),
+                       "ai": round(ai, 1), "bound": bound, "frac": round(frac, 4), **(extra or {})}
+        print(f"{name}: {us:8.2f} us  {tf:7.1f} TFLOP/s  {gbs:7.1f} GB/s  ({bound}, frac {frac:.3f})",
+              file=sys.stderr, flush=True)
+
+    def mul_mat_case(name, wtype, dev_type, payload, N, K, Ms):
+        w0 = mx.upload_weight(wtype, payload, N, K)
+        if dev_type == mx.F16_T:
+            w0 = mx.tile_f16(wtype, w0, N, K)
+        ncopy = max(3, min(64, math.ceil(320e6 / w0.numel())))
+        ws = [w0] + [w0.clone() for _ in range(ncopy - 1)]
+        for M in Ms:
+            x = torch.randn(M, K, device="cuda")
+            out = torch.empty(M, N, device="cuda")
+            wsp = torch.empty(max(1, int(mx.lib().mi355x_mul_mat_workspace(M, K))), dtype=torch.uint8,
+                              device="cuda")
+            us = graph_time_us(lambda i: mx.mul_mat(dev_type, ws[i % ncopy], N, K, x, out, wsp), ncopy)
+            record(f"{name} M={M}", us, 2.0 * M * N * K, payload.nbytes + M * K * 4 + M * N * 4)
+        del ws
+        torch.cuda.empty_cache()
+
+    # F16 weight [8192, 2048], activations [512, 2048]
+    W = (np.random.default_rng(0x5EED0000 + 16).standard_normal((8192, 2048), dtype=np.float32) * 0.02)
+    mul_mat_case("MUL_MAT F16 N=8192 K=2048", mx.F16, mx.F16_T, W.astype(np.float16).view(np.uint16),
+                 8192, 2048, [512])
+    # quantized sweep, decoded inside the GEMM (the per-call route)
+    for ti, (wt, tn) in enumerate(((mx.Q8_0, "Q8_0"), (mx.Q4_K, "Q4_K"), (mx.Q6_K, "Q6_K"))):
+        for si, (K, N) in enumerate(((3072, 3072), (3072, 8192), (8192, 3072))):
+            P = synth_blocks(wt, N, K, 0x5EED0000 + 32 + 4 * ti + si)
+            mul_mat_case(f"MUL_MAT {tn} N={N} K={K}", wt, wt, P, N, K, [32, 128, 512, 2048])
+    # FLASH_ATTN_EXT prefill: 32 query / 8 KV heads, d 128, 512 queries, causal
+    T, H, HK, D = 512, 32, 8, 128
+    for n_kv in (1024, 4096, 8192):
+        q = torch.randn(T, H, D, device="cuda")
+        kc = torch.randn(n_kv, HK, D, device="cuda").half()
+        vc = torch.randn(n_kv, HK, D, device="cuda").half()
+        j = torch.arange(n_kv, device="cuda")[None, :]
+        t = torch.arange(T, device="cuda")[:, None]
+        m = torch.where(j > n_kv - T + t, float("-inf"), 0.0).half()
+        out = torch.empty(T, H, D, device="cuda")
+        wsp = torch.empty(256 << 20, dtype=torch.uint8, device="cuda")
+        us = graph_time_us(lambda i: mx.flash_attn(q.permute(1, 0, 2), kc.permute(1, 0, 2), vc.permute(1, 0, 2),
+                                                   m, 1.0 / math.sqrt(D), out=out, workspace=wsp), 8)
+        visible = 4.0 * H * D * sum(n_kv - T + tt + 1 for tt in range(T))
+        record(f"FLASH_ATTN_EXT n_kv={n_kv}", us, 4.0 * H * T * n_kv * D,
+               T * H * D * 4 + 2 * HK * n_kv * D * 2 + T * n_kv * 2 + T * H * D * 4,
+               {"tflops_causal_visible": round(visible / us / 1e6, 1)})
+    print(json.dumps({
+        "metric": "single-op configurations vs their rooflines (MI355X peaks: 2.5 PFLOP/s fp16, 8 TB/s)",
+        "n_gpus": 1, "dtype": "f16", "data": "synthetic (N(0,0.02) / random-code weights, N(0,1) activations)",
+        "cases": cases}))
+
+
 def moe_bench(args):
     """MUL_MAT_ID expert GEMM at the mixture-of-experts prefill shape: 128 experts, top-8 routing
     from a softmax over N(0, 1) router logits (ties to the lower index), 512 tokens, d_model 2048,
@@ -535,6 +656,9 @@ def main():
         return
     if args.moe:
         moe_bench(args)
+        return
+    if args.configs:
+        configs_bench(args)
         return
     if args.host_path:
         host_path(args)

@@ -95,8 +95,11 @@ __global__ void __launch_bounds__(PACK_THREADS) pack_act_kernel(const float * __
 // of register sets (the loop is unrolled by R so the sets are static registers): slab k+R is
 // requested while slab k is multiplied, and slab k+1 is written to LDS only after that, which
 // hides HBM latency behind R-1 slabs of MFMA work.
-// KSPLIT = 2 splits K between two blocks that add their halves atomically into a zeroed output:
-// with exactly two addends the sum is the same in either order, so the result is deterministic.
+// KSPLIT > 1 splits K between that many blocks that add their parts atomically into a zeroed
+// output; KSPLIT = 0 takes the split count from the launcher (args.ksplit), which sizes it to fill
+// the chip when the output has few tiles (a skinny M: 32 rows of a 3072-wide output are 24
+// tiles). Two addends sum the same in either order; with more, the rounding of the sum depends
+// on the order the blocks finish in.
 // ---------------------------------------------------------------------------------------------
 constexpr int BK = 64;
 constexpr int GEMM_THREADS = 256;
@@ -204,9 +207,10 @@ gemm_kernel(GemmArgs args) {
     // block -> (k split, global n tile, m tile); m is the fast index so the blocks that share a
     // weight panel are neighbours (and, after xcd_tile, on one XCD)
     const int nblocks = gridDim.x;
+    const int ks = KSPLIT > 0 ? KSPLIT : args.ksplit;   // 0: the launcher's split count
     int tile = xcd_tile(blockIdx.x, nblocks);
-    const int split = tile % KSPLIT;
-    tile /= KSPLIT;
+    const int split = tile % ks;
+    tile /= ks;
     const int mt = tile % args.m_tiles, nt = tile / args.m_tiles;
     int g = 0;
 #pragma unroll
@@ -225,7 +229,7 @@ gemm_kernel(GemmArgs args) {
     const int m0 = mt * BM;
 
     const int nk_all = (args.K + BK - 1) / BK;
-    const int per = (nk_all + KSPLIT - 1) / KSPLIT;
+    const int per = (nk_all + ks - 1) / ks;
     const int kb = split * per;
     const int nk = max(0, min(nk_all, kb + per) - kb);
 
@@ -280,7 +284,7 @@ gemm_kernel(GemmArgs args) {
             for (int j = 0; j < C::NJ; j++) {
                 const int n = n0 + wn * C::TN + j * 32 + lr;
                 if (n < G.N) {
-                    if (KSPLIT == 1) crow[n] = acc[i][j][e];
+                    if (ks == 1) crow[n] = acc[i][j][e];
                     else unsafeAtomicAdd(crow + n, acc[i][j][e]);
                 }
             }
@@ -846,7 +850,7 @@ struct CfgDesc {
 };
 static const CfgDesc kCfgs[] = {
     {128, 128, 1, 0, 0.0, 0.0, 0.0, 0.0},        // 0: 4 waves of 64x64
-    {128, 128, 2, 0, 0.0, 0.0, 0.0, 0.0},        // 1: same, K split in two
+    {128, 128, 2, 0, 0.0, 0.0, 0.0, 0.0},        // 1: same, K split (launcher-sized, >= 2)
     {256, 128, 1, 0, 0.0, 0.0, 0.0, 0.0},        // 2: 4 waves of 128x64
     {128, 256, 1, 0, 0.0, 0.0, 0.0, 0.0},        // 3: 4 waves of 64x128
     {256, 256, 1, 64, 6.31, 5.6, 8.23, 0.00},   // 4: 8 waves of 64x128, 2 stages of 64
@@ -935,7 +939,7 @@ static hipError_t launch_cfg(int cfg, const GemmArgs & a, int nblocks, hipStream
     if constexpr (WT == T_F16T) return hipErrorInvalidValue;
     else switch (cfg) {
         case 0: return launch_one<WT, 128, 128, 2, 2, 2, 1>(a, nblocks, st);
-        case 1: return launch_one<WT, 128, 128, 2, 2, 2, 2>(a, nblocks, st);
+        case 1: return launch_one<WT, 128, 128, 2, 2, 2, 0>(a, nblocks, st);   // split a.ksplit ways
         case 2: return launch_one<WT, 256, 128, 2, 2, 2, 1>(a, nblocks, st);
         case 3: return launch_one<WT, 128, 256, 2, 2, 2, 1>(a, nblocks, st);
         default: return hipErrorInvalidValue;
@@ -964,6 +968,26 @@ static int64_t tiles_n_cols(const GemmArgs & a) {
     return n;
 }
 
+// The K split of the register-staged split configuration (1). Fitted to the fastest split
+// measured for Q4_K and Q8_0 at M 32-512, N 3072-14336, K 3072-8192 (1% over the best in
+// total): ~6.65 K^0.75 / sqrt(M N). A wider output has more elements to add atomically per
+// split, a deeper K more work to share. At least 2 ways, at most 16 and at least 4 K slabs per
+// split. MI355X_GEMM_KSPLIT=<n> forces n (for tuning).
+static double reg_split_est(const GemmArgs & a) {
+    return 6.65 * std::pow((double)a.K, 0.75) / std::sqrt((double)a.M * (double)tiles_n_cols(a));
+}
+static int reg_split(const GemmArgs & a) {
+    const int nk = (a.K + BK - 1) / BK;
+    if (const char * e = getenv("MI355X_GEMM_KSPLIT")) {
+        const int v = atoi(e);
+        if (v >= 2 && v <= nk) return v;
+    }
+    int ks = (int)std::lround(reg_split_est(a));
+    const int cap = nk / 4 < 16 ? nk / 4 : 16;
+    if (ks > cap) ks = cap;
+    return ks < 2 ? 2 : ks;
+}
+
 static bool cfg_fits(int c, int wt, int K) {
     const CfgDesc & d = kCfgs[c];
     if (d.dk == 0) return wt != T_F16T;
@@ -973,9 +997,9 @@ static bool cfg_fits(int c, int wt, int K) {
 
 // fp16 weights: the DMA configuration with the least estimated time (the CfgDesc model; every
 // DMA block has a CU to itself, so a launch runs in ceil(blocks / CUs) rounds).
-// Other weights: the register-staged configuration with the best grid fill times its tile's
-// relative per-CU efficiency (bigger wave tiles read LDS less per MFMA); split-K only when the
-// unsplit grid leaves most CUs idle.
+// Other weights: split K when the output is skinny for its depth (reg_split), otherwise the
+// unsplit register-staged tile with the best grid fill times its relative per-CU efficiency
+// (bigger wave tiles read LDS less per MFMA).
 static int choose_cfg(int wt, const GemmArgs & a) {
     if (const char * e = getenv("MI355X_GEMM_CFG")) {
         if (*e) {
@@ -1002,12 +1026,15 @@ static int choose_cfg(int wt, const GemmArgs & a) {
         }
         if (best >= 0) return best;
     }
+    // a skinny output: split K (see reg_split); otherwise the unsplit tile with the best fill
+    if (reg_split_est(a) >= 1.5 && (a.K / BK) >= 8) return 1;
     const double tile_eff[FIRST_DMA_CFG] = {1.0, 0.97, 1.25, 1.25};
     int best = 0;
     double best_score = -1.0;
     for (int c = 0; c < FIRST_DMA_CFG; c++) {
-        if (kCfgs[c].ksplit > 1 && (a.K / BK) < 16) continue;
-        const int blocks = tiles_of(a, kCfgs[c].bm, kCfgs[c].bn) * kCfgs[c].ksplit;
+        if (kCfgs[c].ksplit > 1) continue;
+        const int tiles = tiles_of(a, kCfgs[c].bm, kCfgs[c].bn);
+        const int blocks = tiles * kCfgs[c].ksplit;
         const int waves = (blocks + cus - 1) / cus;
         const double fill = (double)blocks / ((double)waves * cus);
         const double score = fill * tile_eff[c];
@@ -1028,7 +1055,8 @@ hipError_t launch_gemm(int wt, const GemmArgs & a_in, int /*unused*/, hipStream_
         a.g[i].ntile_begin = nt;
         nt += (a.g[i].N + d.bn - 1) / d.bn;
     }
-    const int nblocks = nt * a.m_tiles * d.ksplit;
+    a.ksplit = cfg == 1 ? reg_split(a) : d.ksplit;
+    const int nblocks = nt * a.m_tiles * a.ksplit;
     if (nblocks <= 0) return hipSuccess;
     if (d.ksplit > 1) {
         hipLaunchKernelGGL(zero_rows_kernel, dim3(a.M, a.ng), dim3(256), 0, st, a);

@@ -28,6 +28,7 @@ struct GemmArgs {
     int M, K;
     int m_tiles;
     int ng;
+    int ksplit;            // K split of a register-staged split configuration (set by the launcher)
     GemmGroup g[GEMM_MAX_GROUPS];
 };
 
