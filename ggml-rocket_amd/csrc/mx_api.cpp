@@ -107,25 +107,33 @@ MI355X_API int mi355x_convert_f16(int type, const void * src_dev, int64_t n, uin
     return hip_status(mx::launch_convert_f16(type, src_dev, n, dst_dev, S(stream)));
 }
 
-MI355X_API int mi355x_pack_act(const float * x_dev, int64_t ldx, int64_t M, int64_t K,
-                               uint16_t * a16_dev, float * scales_dev, void * stream) {
-    if (M < 0 || K <= 0 || K % 4 || ldx < K || ldx % 4 || M > INT32_MAX || K > INT32_MAX) return MI355X_E_ARG;
+// zc (optional): an output [M][ldzc] whose first zn columns the pack kernel also clears
+static int pack_impl(bool tiled, const float * x_dev, int64_t ldx, int64_t M, int64_t K, uint16_t * a16_dev,
+                     float * scales_dev, void * stream, float * zc, int64_t ldzc, int64_t zn) {
+    if (M < 0 || K <= 0 || K % (tiled ? 32 : 4) || ldx < K || ldx % 4 || M > INT32_MAX - 15 || K > INT32_MAX)
+        return MI355X_E_ARG;
     if (M == 0) return MI355X_OK;
     if (!x_dev || !a16_dev || !scales_dev || !aligned(x_dev, 16) || !aligned(a16_dev, 8)) return MI355X_E_ARG;
-    return hip_status(mx::launch_pack_act(x_dev, ldx, (int)M, (int)K, a16_dev, K, scales_dev, S(stream)));
+    if (zc && (ldzc < zn || zn > INT32_MAX)) return MI355X_E_ARG;
+    return tiled ? hip_status(mx::launch_pack_act_tiled(x_dev, ldx, (int)M, (int)K, a16_dev, scales_dev, S(stream),
+                                                        zc, ldzc, (int)zn))
+                 : hip_status(mx::launch_pack_act(x_dev, ldx, (int)M, (int)K, a16_dev, K, scales_dev, S(stream), zc,
+                                                  ldzc, (int)zn));
+}
+
+MI355X_API int mi355x_pack_act(const float * x_dev, int64_t ldx, int64_t M, int64_t K,
+                               uint16_t * a16_dev, float * scales_dev, void * stream) {
+    return pack_impl(false, x_dev, ldx, M, K, a16_dev, scales_dev, stream, nullptr, 0, 0);
 }
 
 MI355X_API int mi355x_pack_act_tiled(const float * x_dev, int64_t ldx, int64_t M, int64_t K,
                                      uint16_t * a16_dev, float * scales_dev, void * stream) {
-    if (M < 0 || K <= 0 || K % 32 || ldx < K || ldx % 4 || M > INT32_MAX - 15 || K > INT32_MAX) return MI355X_E_ARG;
-    if (M == 0) return MI355X_OK;
-    if (!x_dev || !a16_dev || !scales_dev || !aligned(x_dev, 16) || !aligned(a16_dev, 8)) return MI355X_E_ARG;
-    return hip_status(mx::launch_pack_act_tiled(x_dev, ldx, (int)M, (int)K, a16_dev, scales_dev, S(stream)));
+    return pack_impl(true, x_dev, ldx, M, K, a16_dev, scales_dev, stream, nullptr, 0, 0);
 }
 
-MI355X_API int mi355x_gemm(int wtype, const uint16_t * a16_dev, const float * scales_dev,
-                           int64_t M, int64_t K, const mi355x_gemm_out * outs, int n_out,
-                           void * stream) {
+// c_zeroed: the outputs were cleared by the activation pack (mi355x_mul_mat)
+static int gemm_impl(int wtype, const uint16_t * a16_dev, const float * scales_dev, int64_t M, int64_t K,
+                     const mi355x_gemm_out * outs, int n_out, void * stream, bool c_zeroed) {
     const bool tiled = wtype == mx::T_F16T;
     if ((!known_wtype(wtype) && !tiled) || M < 0 || K <= 0 || K % 32 || K % blck(wtype) || M > INT32_MAX ||
         K > INT32_MAX)
@@ -157,7 +165,13 @@ MI355X_API int mi355x_gemm(int wtype, const uint16_t * a16_dev, const float * sc
         a.g[i].ntile_begin = nt;
         nt += (int)((o.N + 127) / 128);
     }
-    return hip_status(mx::launch_gemm(wtype, a, nt, S(stream)));
+    return hip_status(mx::launch_gemm(wtype, a, nt, S(stream), c_zeroed));
+}
+
+MI355X_API int mi355x_gemm(int wtype, const uint16_t * a16_dev, const float * scales_dev,
+                           int64_t M, int64_t K, const mi355x_gemm_out * outs, int n_out,
+                           void * stream) {
+    return gemm_impl(wtype, a16_dev, scales_dev, M, K, outs, n_out, stream, false);
 }
 
 // M rows rounded up to 16: the tiled layout's padding (the row-major pack uses M rows of it).
@@ -180,11 +194,22 @@ MI355X_API int mi355x_mul_mat(int wtype, const void * w_dev, int64_t N, int64_t 
     if (!workspace_dev || workspace_bytes < need) return MI355X_E_NOMEM;
     uint16_t * a16 = (uint16_t *)workspace_dev;
     float * scales = (float *)((char *)workspace_dev + mul_mat_a16_bytes(M, K));
-    int st = wtype == mx::T_F16T ? mi355x_pack_act_tiled(x_dev, ldx, M, K, a16, scales, stream)
-                                 : mi355x_pack_act(x_dev, ldx, M, K, a16, scales, stream);
+    // a GEMM that adds its K splits into dst has it cleared by the pack, in the same launch
+    bool zero = false;
+    if ((known_wtype(wtype) || wtype == mx::T_F16T) && K > 0 && K <= INT32_MAX && M <= INT32_MAX && N > 0 &&
+        N <= INT32_MAX && dst_dev && ldd >= N) {
+        mx::GemmArgs probe;
+        memset(&probe, 0, sizeof(probe));
+        probe.M = (int)M;
+        probe.K = (int)K;
+        probe.ng = 1;
+        probe.g[0].N = (int)N;
+        zero = mx::gemm_accumulates(wtype, probe);
+    }
+    int st = pack_impl(wtype == mx::T_F16T, x_dev, ldx, M, K, a16, scales, stream, zero ? dst_dev : nullptr, ldd, N);
     if (st != MI355X_OK) return st;
     mi355x_gemm_out o = {w_dev, N, 0, N, dst_dev, ldd};
-    return mi355x_gemm(wtype, a16, scales, M, K, &o, 1, stream);
+    return gemm_impl(wtype, a16, scales, M, K, &o, 1, stream, zero);
 }
 
 // ---- FLASH_ATTN_EXT ---------------------------------------------------------------------------

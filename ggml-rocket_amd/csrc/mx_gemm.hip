@@ -17,6 +17,7 @@
 // and for fp16 weights one that moves both operands into LDS by DMA (gemm_f16_kernel). The
 // launcher picks a tile configuration of either per call from the output shape.
 
+#include <algorithm>
 #include <cmath>
 
 #include "mx_weights.h"
@@ -34,13 +35,25 @@ constexpr int PACK_VEC = 16;                                 // float4 per threa
 constexpr int PACK_REG_MAX = PACK_THREADS * PACK_VEC * 4;    // 16384 floats
 
 // TL: write A16 in the tiled layout (tiled_index over M rows) instead of rows of lda.
+// ZC (optional): an F32 output whose row m (ZN values) the block also clears, for a GEMM that
+// adds its K splits into it; one launch fewer than a separate fill.
 template <bool TL>
 __global__ void __launch_bounds__(PACK_THREADS) pack_act_kernel(const float * __restrict__ X, int64_t ldx,
                                                                 int M, int K, uint16_t * __restrict__ A16,
-                                                                int64_t lda, float * __restrict__ scales) {
+                                                                int64_t lda, float * __restrict__ scales,
+                                                                float * __restrict__ ZC, int64_t ldzc, int ZN) {
     __shared__ float red[PACK_THREADS / WAVE];
     const int t = threadIdx.x, lane = t % WAVE, wave = t / WAVE;
     const int m = blockIdx.x;
+    if (ZC) {
+        float * zrow = ZC + (int64_t)m * ldzc;
+        int c0 = 0;
+        if ((reinterpret_cast<uintptr_t>(zrow) & 15) == 0) {
+            for (int c = 4 * t; c + 3 < ZN; c += 4 * PACK_THREADS) *(float4v *)(zrow + c) = float4v{0, 0, 0, 0};
+            c0 = ZN & ~3;
+        }
+        for (int c = c0 + t; c < ZN; c += PACK_THREADS) zrow[c] = 0.0f;
+    }
     const int n4 = K / 4;
     // the destination of the 4 values starting at column 4c
     auto dst = [&](int c) -> uint16_t * {
@@ -288,6 +301,160 @@ gemm_kernel(GemmArgs args) {
                     else unsafeAtomicAdd(crow + n, acc[i][j][e]);
                 }
             }
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------------------------
+// Skinny GEMM (M <= 128): a launch this narrow is bound by how many weight bytes it keeps in
+// flight, not by MFMA rate, so the weight goes from HBM straight into registers and is decoded
+// there into MFMA operands (no LDS round trip for the weight). A block is SK_NW waves over
+// SK_NW*32 weight rows and a run of K groups of CH 64-deep chunks; lane (r, g) of a wave loads
+// decoder item g of each chunk for weight row r, and the 32 values it decodes (two runs of 16
+// consecutive k) are its B operands for the chunk's four 16-deep MFMA steps, so lane (r, g) of
+// the A operand reads the same k from activation row r. Per group the activation slice
+// [32 MT][64 CH] fp16 sits in LDS (16-byte chunks XOR-swizzled by row), double-buffered, and the
+// weight of the next group is in flight in a second register set while this one is multiplied.
+// Issue order matters: one vmcnt counter covers every load in issue order, so each step issues
+// the next group's activation loads before its weight loads (their LDS store then waits for them
+// alone, not for the weight). Past the block's last group the loads re-fetch it (decoded as
+// zero), so the loop body has no branch between a load and its use. Blocks split K and add their
+// partial sums atomically into a zeroed output.
+// ---------------------------------------------------------------------------------------------
+constexpr int SK_MAX_M = 128;
+constexpr int SK_NW = 4;
+
+// Two waves per SIMD (two blocks per CU) where the two register sets fit in half the register
+// file without spilling, one otherwise.
+template <int WT, int MT>
+constexpr int skinny_occupancy() {
+    return (WT == T_Q4_K || WT == T_MXFP4 || MT == 1) ? 2 : 1;
+}
+
+template <int WT, int MT, int CH>
+__global__ void __launch_bounds__(SK_NW * WAVE)
+__attribute__((amdgpu_waves_per_eu(skinny_occupancy<WT, MT>(), skinny_occupancy<WT, MT>())))
+gemm_skinny_kernel(GemmArgs args, int groups_per_block) {
+    constexpr int NW = SK_NW;
+    constexpr int CPR = 8 * CH;               // 16-byte chunks per activation row of the slice
+    constexpr int ACH = 32 * MT * CPR;        // 16-byte chunks of the slice
+    constexpr int APT = ACH / (NW * WAVE);    // per thread
+    constexpr int SLICE = ACH * 16;
+    static_assert(ACH % (NW * WAVE) == 0, "slice split");
+    __shared__ __align__(16) uint8_t sa[2 * SLICE];
+
+    const int t = threadIdx.x, lane = t % WAVE, wave = t / WAVE;
+    const int lr = lane % 32, lg = lane / 32;
+    const int ks = args.ksplit;
+    const int split = blockIdx.x % ks;
+    const int nt = blockIdx.x / ks;
+    int g = 0;
+#pragma unroll
+    for (int i = 1; i < GEMM_MAX_GROUPS; i++)
+        if (i < args.ng && nt >= args.g[i].ntile_begin) g = i;
+    GemmGroup G;
+    G.W = args.g[0].W; G.rows_total = args.g[0].rows_total; G.row0 = args.g[0].row0; G.N = args.g[0].N;
+    G.C = args.g[0].C; G.ldc = args.g[0].ldc; G.ntile_begin = args.g[0].ntile_begin;
+#pragma unroll
+    for (int i = 1; i < GEMM_MAX_GROUPS; i++)
+        if (i == g) {
+            G.W = args.g[i].W; G.rows_total = args.g[i].rows_total; G.row0 = args.g[i].row0; G.N = args.g[i].N;
+            G.C = args.g[i].C; G.ldc = args.g[i].ldc; G.ntile_begin = args.g[i].ntile_begin;
+        }
+    const int n = (nt - G.ntile_begin) * (32 * NW) + 32 * wave + lr;   // this lane's weight row
+    const bool okn = n < G.N;
+    const int64_t row = G.row0 + (okn ? n : G.N - 1);
+    const int nchunks = (args.K + 63) / 64;
+    const int ngroups = (nchunks + CH - 1) / CH;
+    const int gb = split * groups_per_block;                             // first group of the block
+    const int gn = max(0, min(ngroups, gb + groups_per_block) - gb);    // groups of the block
+    const int glast = gb + max(gn, 1) - 1;
+
+    auto load_a = [&](u32x4 (&av)[APT], int grp) {   // rows past M and k past K read as zero
+        const int64_t kb = (int64_t)min(grp, glast) * CH * 64;
+#pragma unroll
+        for (int i = 0; i < APT; i++) {
+            const int q = t + i * NW * WAVE, r = q / CPR, c = q % CPR;
+            const int64_t k = kb + 8 * c;
+            const bool ok = r < args.M && k < args.K;
+            av[i] = *(const u32x4 *)(args.A + (ok ? (int64_t)r * args.lda + k : 0));
+            if (!ok) av[i] = u32x4{0, 0, 0, 0};
+        }
+    };
+    auto store_a = [&](const u32x4 (&av)[APT], int buf) {
+#pragma unroll
+        for (int i = 0; i < APT; i++) {
+            const int q = t + i * NW * WAVE, r = q / CPR, c = q % CPR;
+            *(u32x4 *)(sa + buf * SLICE + (r * CPR + (c ^ (r & 7))) * 16) = av[i];
+        }
+    };
+    auto load_w = [&](WLoad<WT> (&w)[CH], int grp) {
+        const bool live = okn && grp <= glast && gn > 0;
+        const int c0 = min(grp, glast) * CH;
+#pragma unroll
+        for (int c = 0; c < CH; c++) {
+            const int cc = c0 + c;
+            w[c].load((const uint8_t *)G.W, G.rows_total, args.K, row, (int64_t)min(cc, nchunks - 1) * 64, lg,
+                      live && cc < nchunks);
+        }
+    };
+    float16v acc[MT][1];
+#pragma unroll
+    for (int i = 0; i < MT; i++)
+#pragma unroll
+        for (int e = 0; e < 16; e++) acc[i][0][e] = 0.0f;
+    auto compute = [&](const WLoad<WT> (&w)[CH], int buf) {
+#pragma unroll
+        for (int c = 0; c < CH; c++) {
+            u32x4 b[4];
+            int run0, run1;
+            w[c].decode(lg, b, run0, run1);
+#pragma unroll
+            for (int s = 0; s < 4; s++) {
+                const int ch = 8 * c + (s < 2 ? run0 + 8 * s : run1 + 8 * (s - 2)) / 8;   // slice chunk
+                const half8 bf = __builtin_bit_cast(half8, b[s]);
+#pragma unroll
+                for (int i = 0; i < MT; i++) {
+                    const int r = 32 * i + lr;
+                    const half8 af = *(const half8 *)(sa + buf * SLICE + (r * CPR + (ch ^ (r & 7))) * 16);
+                    acc[i][0] = mfma32(af, bf, acc[i][0]);
+                }
+            }
+        }
+    };
+
+    WLoad<WT> w0[CH], w1[CH];
+    u32x4 av[APT];
+    load_a(av, gb);
+    load_w(w0, gb);
+    store_a(av, 0);
+    __syncthreads();
+    int q = 0;
+    for (; q + 2 <= gn; q += 2) {
+        load_a(av, gb + q + 1);
+        load_w(w1, gb + q + 1);
+        compute(w0, 0);
+        store_a(av, 1);
+        __syncthreads();
+        load_a(av, gb + q + 2);
+        load_w(w0, gb + q + 2);
+        compute(w1, 1);
+        store_a(av, 0);
+        __syncthreads();
+    }
+    if (q < gn) compute(w0, 0);
+
+    scale_rows(acc, args.scales, 0, lg, args.M);
+    if (!okn || gn == 0) return;
+#pragma unroll
+    for (int i = 0; i < MT; i++) {
+#pragma unroll
+        for (int e = 0; e < 16; e++) {
+            const int r = i * 32 + 8 * (e / 4) + 4 * lg + (e % 4);
+            if (r >= args.M) continue;
+            float * p = G.C + (int64_t)r * G.ldc + n;
+            if (ks == 1) *p = acc[i][0][e];
+            else unsafeAtomicAdd(p, acc[i][0][e]);
         }
     }
 }
@@ -810,17 +977,18 @@ __global__ void pack_q6_k_kernel(const uint8_t * __restrict__ src, int64_t rows,
 // ---------------------------------------------------------------------------------------------
 
 hipError_t launch_pack_act(const float * X, int64_t ldx, int M, int K, uint16_t * A16, int64_t lda,
-                           float * scales, hipStream_t st) {
+                           float * scales, hipStream_t st, float * zc, int64_t ldzc, int zn) {
     if (M <= 0) return hipSuccess;
-    hipLaunchKernelGGL(pack_act_kernel<false>, dim3(M), dim3(PACK_THREADS), 0, st, X, ldx, M, K, A16, lda, scales);
+    hipLaunchKernelGGL(pack_act_kernel<false>, dim3(M), dim3(PACK_THREADS), 0, st, X, ldx, M, K, A16, lda, scales,
+                       zc, ldzc, zn);
     return hipGetLastError();
 }
 
 hipError_t launch_pack_act_tiled(const float * X, int64_t ldx, int M, int K, uint16_t * A16, float * scales,
-                                 hipStream_t st) {
+                                 hipStream_t st, float * zc, int64_t ldzc, int zn) {
     if (M <= 0) return hipSuccess;
     hipLaunchKernelGGL(pack_act_kernel<true>, dim3(M), dim3(PACK_THREADS), 0, st, X, ldx, M, K, A16, (int64_t)K,
-                       scales);
+                       scales, zc, ldzc, zn);
     return hipGetLastError();
 }
 
@@ -1045,8 +1213,88 @@ static int choose_cfg(int wt, const GemmArgs & a) {
 
 __global__ void zero_rows_kernel(GemmArgs args);
 
-hipError_t launch_gemm(int wt, const GemmArgs & a_in, int /*unused*/, hipStream_t st) {
+// The skinny kernel (configuration 16 for MI355X_GEMM_CFG): every weight format but the tiled
+// fp16 one, M <= SK_MAX_M. Chunk depth CH by M tiles (LDS 32 KB per block, double-buffered). The
+// K split aims at ~240 blocks, about one per CU: fewer leave weight bytes unrequested, more add
+// atomic traffic (the fastest splits measured for Q4_K / Q8_0 at M 32-128, N 3072-14336,
+// K 3072-14336 launch 144-256 blocks).
+constexpr int SKINNY_CFG = N_CFGS;
+
+static bool use_skinny(int wt, const GemmArgs & a) {
+    if (wt == T_F16T || a.M > SK_MAX_M) return false;
+    if (const char * e = getenv("MI355X_GEMM_CFG"))
+        if (*e) return atoi(e) == SKINNY_CFG;
+    return true;
+}
+
+static int skinny_ch(int M) { return M <= 64 ? 4 : 2; }
+
+static int skinny_ntiles(const GemmArgs & a) {
+    int nt = 0;
+    for (int i = 0; i < a.ng; i++) nt += (a.g[i].N + 32 * SK_NW - 1) / (32 * SK_NW);
+    return nt;
+}
+
+// K groups per block; the split count is ceil(groups / that)
+static int skinny_gpb(const GemmArgs & a) {
+    const int ngroups = ((a.K + 63) / 64 + skinny_ch(a.M) - 1) / skinny_ch(a.M);
+    double blocks = 240.0;
+    if (const char * e = getenv("MI355X_SKINNY_BLOCKS")) {   // tuning override
+        const int v = atoi(e);
+        if (v > 0) blocks = v;
+    }
+    const double target = blocks / skinny_ntiles(a);
+    const int ks = std::max(1, (int)std::lround(target));
+    return (ngroups + ks - 1) / ks;
+}
+
+static int skinny_split(const GemmArgs & a) {
+    const int ngroups = ((a.K + 63) / 64 + skinny_ch(a.M) - 1) / skinny_ch(a.M);
+    const int gpb = skinny_gpb(a);
+    return (ngroups + gpb - 1) / gpb;
+}
+
+template <int WT>
+static hipError_t launch_skinny(const GemmArgs & a, int nblocks, hipStream_t st) {
+    const int mt = (a.M + 31) / 32, gpb = skinny_gpb(a);
+    if (mt == 1) hipLaunchKernelGGL((gemm_skinny_kernel<WT, 1, 4>), dim3(nblocks), dim3(SK_NW * WAVE), 0, st, a, gpb);
+    else if (mt == 2) hipLaunchKernelGGL((gemm_skinny_kernel<WT, 2, 4>), dim3(nblocks), dim3(SK_NW * WAVE), 0, st, a, gpb);
+    else hipLaunchKernelGGL((gemm_skinny_kernel<WT, 4, 2>), dim3(nblocks), dim3(SK_NW * WAVE), 0, st, a, gpb);
+    return hipGetLastError();
+}
+
+bool gemm_accumulates(int wt, const GemmArgs & a) {
+    if (use_skinny(wt, a)) return skinny_split(a) > 1;
+    return kCfgs[choose_cfg(wt, a)].ksplit > 1;
+}
+
+hipError_t launch_gemm(int wt, const GemmArgs & a_in, int /*unused*/, hipStream_t st, bool c_zeroed) {
     GemmArgs a = a_in;
+    if (use_skinny(wt, a)) {
+        const int bn = 32 * SK_NW;
+        int nt = 0;
+        for (int i = 0; i < a.ng; i++) {
+            a.g[i].ntile_begin = nt;
+            nt += (a.g[i].N + bn - 1) / bn;
+        }
+        a.m_tiles = 1;
+        a.ksplit = skinny_split(a);
+        const int nblocks = nt * a.ksplit;
+        if (nblocks <= 0) return hipSuccess;
+        if (a.ksplit > 1 && !c_zeroed) {
+            hipLaunchKernelGGL(zero_rows_kernel, dim3(a.M, a.ng), dim3(256), 0, st, a);
+            hipError_t e = hipGetLastError();
+            if (e != hipSuccess) return e;
+        }
+        switch (wt) {
+            case T_F16: return launch_skinny<T_F16>(a, nblocks, st);
+            case T_Q8_0: return launch_skinny<T_Q8_0>(a, nblocks, st);
+            case T_Q4_K: return launch_skinny<T_Q4_K>(a, nblocks, st);
+            case T_Q6_K: return launch_skinny<T_Q6_K>(a, nblocks, st);
+            case T_MXFP4: return launch_skinny<T_MXFP4>(a, nblocks, st);
+            default: return hipErrorInvalidValue;
+        }
+    }
     const int cfg = choose_cfg(wt, a);
     const CfgDesc & d = kCfgs[cfg];
     a.m_tiles = (a.M + d.bm - 1) / d.bm;
@@ -1058,7 +1306,7 @@ hipError_t launch_gemm(int wt, const GemmArgs & a_in, int /*unused*/, hipStream_
     a.ksplit = cfg == 1 ? reg_split(a) : d.ksplit;
     const int nblocks = nt * a.m_tiles * a.ksplit;
     if (nblocks <= 0) return hipSuccess;
-    if (d.ksplit > 1) {
+    if (d.ksplit > 1 && !c_zeroed) {
         hipLaunchKernelGGL(zero_rows_kernel, dim3(a.M, a.ng), dim3(256), 0, st, a);
         hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;

@@ -77,11 +77,16 @@ bool fa_dims_supported(int D, int DV);   // (D, DV) = (64, 64), (128, 128) or (1
 size_t fa_max_kv(int D, int DV);          // the longest KV range one launch takes
 hipError_t launch_fa(const FaArgs & a, hipStream_t st);
 
+// zc (optional): an F32 output [M][ldzc] whose first zn columns the pack also clears
 hipError_t launch_pack_act(const float * X, int64_t ldx, int M, int K, uint16_t * A16, int64_t lda,
-                           float * scales, hipStream_t st);
-hipError_t launch_gemm(int wt, const GemmArgs & a, int n_tiles_total, hipStream_t st);
+                           float * scales, hipStream_t st, float * zc = nullptr, int64_t ldzc = 0, int zn = 0);
 hipError_t launch_pack_act_tiled(const float * X, int64_t ldx, int M, int K, uint16_t * A16, float * scales,
-                                 hipStream_t st);
+                                 hipStream_t st, float * zc = nullptr, int64_t ldzc = 0, int zn = 0);
+// c_zeroed: the outputs are already zero (the pack cleared them), so a launch that adds its K
+// splits into them needs no fill of its own
+hipError_t launch_gemm(int wt, const GemmArgs & a, int n_tiles_total, hipStream_t st, bool c_zeroed = false);
+// whether launch_gemm would add into its outputs (a K split) rather than write them
+bool gemm_accumulates(int wt, const GemmArgs & a);
 hipError_t launch_dequant_f16(int wt, const void * W, int64_t rows, int64_t K, uint16_t * out, hipStream_t st);
 hipError_t launch_f16_tiled(int wt, const void * W, int64_t rows, int64_t K, uint16_t * out, hipStream_t st);
 hipError_t launch_pack_weight(int wt, const void * src, int64_t rows, int64_t K, void * dst, hipStream_t st);

@@ -301,3 +301,48 @@ def test_gemm_tiled_rows_of_a_panel(mx):
         torch.cuda.synchronize()
         ref = O.mul_mat(O.F16, W16.reshape(3 * N, K)[row0:row0 + N], Xf, N, K)
         _assert_bars(ref, c.cpu().numpy(), M, N, f"tiled panel row0={row0}")
+
+
+# The skinny kernel (M <= 128, every format but the tiled fp16 one): each M-tile count, a ragged
+# N (not a multiple of the 128-row block), a K with a 32-value tail where the format allows one,
+# K splits added atomically into an output cleared by the pack (mi355x_mul_mat) or by the GEMM
+# launch itself (mi355x_gemm on NaN-filled outputs, two fused weights).
+SKINNY_TYPES = [O.F16, O.Q8_0, O.Q4_K, O.Q6_K, O.MXFP4]
+
+
+@pytest.mark.parametrize("M", [1, 33, 96, 128])
+@pytest.mark.parametrize("wtype", SKINNY_TYPES)
+def test_skinny_mul_mat(mx, wtype, M):
+    K = 2560 if wtype in (O.Q4_K, O.Q6_K) else 1312
+    N = 400
+    W = O.fill_normal((N, K), 960 + wtype, 0.0, 0.02)
+    Xf = O.fill_normal((M, K), 961 + M)
+    payload = O.f32_to_f16_bits(W) if wtype == O.F16 else O.quantize(wtype, W)
+    import torch
+    ref = O.mul_mat(wtype, payload, Xf, N, K)
+    w = mx.upload_weight(wtype, payload, N, K)
+    out = torch.full((M, N), float("nan"), dtype=torch.float32, device="cuda")
+    mx.mul_mat(wtype, w, N, K, _dev(Xf), out)
+    torch.cuda.synchronize()
+    _assert_bars(ref, out.cpu().numpy(), M, N, f"skinny {O.TYPE_NAMES[wtype]} M={M}")
+
+
+@pytest.mark.parametrize("wtype", SKINNY_TYPES)
+def test_skinny_gemm_fused_nan_outputs(mx, wtype):
+    import torch
+    K = 1536 if wtype in (O.Q4_K, O.Q6_K) else 1248
+    M, Ns = 70, (144, 272)
+    Xf = O.fill_normal((M, K), 970)
+    a16, sc = mx.pack_act(_dev(Xf))
+    outs, refs = [], []
+    for g, N in enumerate(Ns):
+        W = O.fill_normal((N, K), 971 + g, 0.0, 0.02)
+        payload = O.f32_to_f16_bits(W) if wtype == O.F16 else O.quantize(wtype, W)
+        refs.append(O.mul_mat(wtype, payload, Xf, N, K))
+        w = mx.upload_weight(wtype, payload, N, K)
+        c = torch.full((M, N), float("nan"), dtype=torch.float32, device="cuda")
+        outs.append((w, N, 0, N, c))
+    mx.gemm(wtype, a16, sc, K, outs)
+    torch.cuda.synchronize()
+    for (w, _, _, N, c), ref in zip(outs, refs):
+        _assert_bars(ref, c.cpu().numpy(), M, N, f"skinny fused {O.TYPE_NAMES[wtype]} N={N}")
