@@ -8,6 +8,7 @@
 #include <stdio.h>
 #include <string.h>
 
+#include "mx_fa_dims.h"
 #include "mx_kernels_impl.h"
 #include "mx_weights.h"
 
@@ -216,7 +217,7 @@ MI355X_API int mi355x_mul_mat(int wtype, const void * w_dev, int64_t N, int64_t 
 
 static int fa_check(const mi355x_fa_args * a) {
     if (!a || !a->q_dev || !a->k_dev || !a->v_dev || !a->dst_dev) return MI355X_E_ARG;
-    if (!mx::fa_dims_supported(a->D, a->DV)) return MI355X_E_UNSUPPORTED;   // (64,64) (128,128) (192,128)
+    if (!mx::fa_dims_supported(a->D, a->DV)) return MI355X_E_UNSUPPORTED;   // D <= 192, DV <= 128, % 8
     if (a->max_bias != 0.0f) return MI355X_E_UNSUPPORTED;
     if (a->T < 0 || a->H <= 0 || a->HK <= 0 || a->KV < 0 || a->H % a->HK) return MI355X_E_ARG;
     if (a->q_nb1 % 4 || a->q_nb2 % 4 || !aligned(a->q_dev, 16)) return MI355X_E_ARG;
@@ -235,7 +236,9 @@ static mx::FaArgs fa_lower(const mi355x_fa_args * a, int nsplit) {
     f.q_nb1 = a->q_nb1; f.q_nb2 = a->q_nb2; f.k_nb1 = a->k_nb1; f.k_nb2 = a->k_nb2;
     f.v_nb1 = a->v_nb1; f.v_nb2 = a->v_nb2; f.mask_nb1 = a->mask_nb1;
     f.dst_nb1 = a->dst_nb1; f.dst_nb2 = a->dst_nb2;
-    f.D = a->D; f.DV = a->DV; f.T = a->T; f.H = a->H; f.HK = a->HK; f.KV = a->KV; f.nsplit = nsplit;
+    f.dk = a->D; f.dv = a->DV;
+    mx::fa_pad_dims(a->D, a->DV, f.D, f.DV);   // the kernel's dims (checked by fa_check)
+    f.T = a->T; f.H = a->H; f.HK = a->HK; f.KV = a->KV; f.nsplit = nsplit;
     f.kvp = (int)((a->KV + 63) / 64 * 64);
     f.cls_stride = (f.kvp / 64 + 15) / 16 * 16;
     f.scale = a->scale; f.softcap = a->softcap;
@@ -244,10 +247,11 @@ static mx::FaArgs fa_lower(const mi355x_fa_args * a, int nsplit) {
 
 static size_t align256(size_t n) { return (n + 255) & ~(size_t)255; }
 
-// Workspace: V^T [HK][D][KVp] fp16 | mask classes [T/32][cls_stride] | partial O
-// [nsplit][T][H][D] f32 and (max, sum) [nsplit][T][H][2] f32 when nsplit > 1.
+// Workspace: V^T [HK][DV][KVp] fp16 | mask classes [T/32][cls_stride] | 256 bytes, the first 16
+// zeroed by the prep kernel | partial O [nsplit][T][H][DV] f32 and (max, sum) [nsplit][T][H][2]
+// f32 when nsplit > 1 (DV as the kernel is built).
 struct FaLayout {
-    size_t vt, cls, po, pml, total;
+    size_t vt, cls, zero, po, pml, total;
 };
 static FaLayout fa_layout(const mx::FaArgs & f) {
     FaLayout L;
@@ -255,7 +259,8 @@ static FaLayout fa_layout(const mx::FaArgs & f) {
     const size_t rows = (size_t)f.T * f.H * f.nsplit;
     L.vt = 0;
     L.cls = L.vt + align256((size_t)f.HK * f.DV * f.kvp * 2);
-    L.po = L.cls + align256(nqt * (size_t)f.cls_stride);
+    L.zero = L.cls + align256(nqt * (size_t)f.cls_stride);
+    L.po = L.zero + 256;
     L.pml = L.po + (f.nsplit > 1 ? align256(rows * f.DV * 4) : 0);
     L.total = L.pml + (f.nsplit > 1 ? align256(rows * 8) : 0);
     return L;
@@ -302,6 +307,7 @@ MI355X_API int mi355x_flash_attn(const mi355x_fa_args * a, int nsplit,
     char * ws = (char *)workspace_dev;
     f.vt = (uint16_t *)(ws + L.vt);
     f.cls = (uint8_t *)(ws + L.cls);
+    f.kzero = (uint16_t *)(ws + L.zero);
     if (nsplit > 1) {
         f.part_o = (float *)(ws + L.po);
         f.part_ml = (float *)(ws + L.pml);

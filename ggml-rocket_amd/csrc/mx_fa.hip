@@ -25,10 +25,14 @@
 //             lane owns one query: the row max and sum need one exchange with the partner lane
 //             (l ^ 32), and O^T = V^T . P^T keeps the same ownership, so the rescale by
 //             exp(m_old - m_new) is lane-local.
+// Head dims between the built ones (mx_fa_dims.h) run on the next larger build: K chunks past dk
+// are fetched from 16 zero bytes of the workspace (row stride 0), Q columns past dk and V columns
+// past dv are read as zero, output columns past dv are not stored.
 // The KV range may be split across blocks; every split writes an unnormalised partial O with
 // its (max, sum), and a third launch, fa_combine, merges them.
 
 #include "mx_common.h"
+#include "mx_fa_dims.h"
 #include "mx_kernels_impl.h"
 
 namespace mx {
@@ -110,6 +114,7 @@ __global__ void __launch_bounds__(256) fa_prep_kernel(FaArgs a) {
     const int nkt = a.kvp / FA_BKV;
     const int nvt = a.HK * nkt;
     const int b = blockIdx.x;
+    if (b == 0 && t < 8) a.kzero[t] = 0;   // the K source of the padded columns
     if (b < nvt) {
         // V^T for (hk, key tile)
         const int hk = b / nkt, j0 = (b % nkt) * FA_BKV;
@@ -120,7 +125,7 @@ __global__ void __launch_bounds__(256) fa_prep_kernel(FaArgs a) {
             const int c = t + i * 256, r = c / CH, ch = c % CH;
             const int j = j0 + r;
             u32x4 v = {0, 0, 0, 0};
-            if (j < a.KV) v = *(const u32x4 *)(V + (int64_t)j * a.v_nb1 + 8 * ch);
+            if (j < a.KV && 8 * ch < a.dv) v = *(const u32x4 *)(V + (int64_t)j * a.v_nb1 + 8 * ch);
 #pragma unroll
             for (int e = 0; e < 4; e++) {
                 tile[r][8 * ch + 2 * e] = (uint16_t)(v[e] & 0xFFFFu);
@@ -280,13 +285,17 @@ fa_kernel(FaArgs a) {
     const uint8_t * cls_w = smem + C::LDS + (qt - qt_first) * a.cls_stride;
 
     // DMA sources: K rows (keys, clamped to the last key) and V^T rows (dims)
+    // (chunks past dk, padding, read the zero bytes for every key: row stride 0)
     const uint16_t * ksrc[C::PK];
+    int64_t kstr[C::PK];
     const uint16_t * vsrc[C::PV];
 #pragma unroll
     for (int q = 0; q < C::PK; q++) {
         const int slot = (q * FA_WAVES + wave) * WAVE + lane;
         const int r = slot / C::KCH, c = C::kchunk_inv(r, slot % C::KCH);
-        ksrc[q] = a.k + (int64_t)hk * a.k_nb2 + 8 * c + (int64_t)r * a.k_nb1;   // + j0 * k_nb1 per tile
+        const bool real = 8 * c < a.dk;
+        kstr[q] = real ? a.k_nb1 : 0;
+        ksrc[q] = real ? a.k + (int64_t)hk * a.k_nb2 + 8 * c + (int64_t)r * a.k_nb1 : a.kzero;   // + j0 * kstr per tile
     }
 #pragma unroll
     for (int q = 0; q < C::PV; q++) {
@@ -306,7 +315,7 @@ fa_kernel(FaArgs a) {
             const int slot = (q * FA_WAVES + wave) * WAVE + lane;
             const int r = slot / C::KCH;
             const int64_t jr = (int64_t)min(j0 + r, kv_last) - r;
-            fa_dma16(ksrc[q] + jr * a.k_nb1, st + (q * FA_WAVES + wave_s) * 1024);
+            fa_dma16(ksrc[q] + jr * kstr[q], st + (q * FA_WAVES + wave_s) * 1024);
         }
 #pragma unroll
         for (int q = 0; q < C::PV; q++) fa_dma16(vsrc[q] + j0, st + C::K_BYTES + (q * FA_WAVES + wave_s) * 1024);
@@ -333,7 +342,7 @@ fa_kernel(FaArgs a) {
         for (int s = 0; s < KSTEPS; s++) {
             const int d = 16 * s + 8 * lg;   // < DK
             float4v x0 = {0, 0, 0, 0}, x1 = {0, 0, 0, 0};
-            if (qok) {
+            if (qok && d < a.dk) {
                 x0 = *(const float4v *)(q + d);
                 x1 = *(const float4v *)(q + d + 4);
             }
@@ -524,7 +533,7 @@ fa_kernel(FaArgs a) {
                 float4v v;
 #pragma unroll
                 for (int e = 0; e < 4; e++) v[e] = o[db][4 * q4 + e] * inv;
-                *(float4v *)(dst + d) = v;
+                if (d < a.dv) *(float4v *)(dst + d) = v;
             }
         return;
     }
@@ -581,7 +590,7 @@ __global__ void __launch_bounds__(256) fa_combine_kernel(FaArgs a) {
     float4v out;
 #pragma unroll
     for (int e = 0; e < 4; e++) out[e] = num[e] * inv;
-    *(float4v *)(a.dst + (int64_t)tq * a.dst_nb2 + (int64_t)h * a.dst_nb1 + 4 * c) = out;
+    if (4 * c < a.dv) *(float4v *)(a.dst + (int64_t)tq * a.dst_nb2 + (int64_t)h * a.dst_nb1 + 4 * c) = out;
 }
 
 int fa_blocks_per_split(const FaArgs & a) {
@@ -605,9 +614,14 @@ static size_t fa_ring_bytes(int D, int DV) {
 }
 static size_t fa_lds_bytes(const FaArgs & a) { return fa_ring_bytes(a.D, a.DV) + (size_t)FA_TASKS * a.cls_stride; }
 
-bool fa_dims_supported(int D, int DV) { return fa_ring_bytes(D, DV) != 0; }
+bool fa_dims_supported(int dk, int dv) {
+    int D = 0, DV = 0;
+    return fa_pad_dims(dk, dv, D, DV) && fa_ring_bytes(D, DV) != 0;
+}
 
-size_t fa_max_kv(int D, int DV) {
+size_t fa_max_kv(int dk, int dv) {
+    int D = 0, DV = 0;
+    if (!fa_pad_dims(dk, dv, D, DV)) return 0;
     const size_t ring = fa_ring_bytes(D, DV);
     if (!ring) return 0;
     // class rows of FA_TASKS query tiles (one byte per 64-key tile, rows of a multiple of 16)

@@ -44,7 +44,11 @@ struct FaArgs {
     uint16_t * vt;             // workspace: V^T [HK][D][kvp], written by the prep kernel
     uint8_t * cls;             // workspace: mask class per (32-query tile, 64-key tile), rows of cls_stride
     int64_t q_nb1, q_nb2, k_nb1, k_nb2, v_nb1, v_nb2, mask_nb1, dst_nb1, dst_nb2;
-    int D, DV, T, H, HK, KV, kvp, cls_stride, nsplit;   // D: Q / K head dim, DV: V / output
+    uint16_t * kzero;          // workspace: 16 zero bytes (written by the prep kernel), the K
+                               // source of the padded columns
+    int D, DV, T, H, HK, KV, kvp, cls_stride, nsplit;   // D: Q / K head dim, DV: V / output, as
+                                                        // the kernel is built (fa_pad_dims)
+    int dk, dv;                // the op's head dims (<= D, DV): columns past them are padding
     float scale, softcap;
 };
 
@@ -73,8 +77,8 @@ hipError_t launch_moe(int wt, const MoeArgs & a, hipStream_t st);
 
 int fa_blocks_per_split(const FaArgs & a);
 int fa_prep_blocks(const FaArgs & a);
-bool fa_dims_supported(int D, int DV);   // (D, DV) = (64, 64), (128, 128) or (192, 128)
-size_t fa_max_kv(int D, int DV);          // the longest KV range one launch takes
+bool fa_dims_supported(int dk, int dv);   // fa_pad_dims: dk <= 192, dv <= 128, multiples of 8
+size_t fa_max_kv(int dk, int dv);          // the longest KV range one launch takes
 hipError_t launch_fa(const FaArgs & a, hipStream_t st);
 
 // zc (optional): an F32 output [M][ldzc] whose first zn columns the pack also clears

@@ -173,3 +173,41 @@ def test_fa_mla_k192_v128(mx, H, HK, softcap):
         r = compare(want, got)
         print(f"MLA H={H} HK={HK} softcap={softcap} nsplit={ns}: {r}")
         assert r["nonfinite"] == 0 and r["max_abs"] <= 2e-2 and r["range_err"] <= 1e-2, (ns, r)
+
+
+@pytest.mark.parametrize("D,DV", [(32, 32), (96, 96), (128, 64), (64, 128), (160, 80), (192, 64)])
+def test_fa_padded_head_dims(mx, D, DV):
+    """Head dims between the built kernels (64/64, 128/128, 192/128) run zero-padded onto the
+    smallest that holds them: Q and K columns past dk and V columns past dv read as zero, output
+    columns past dv are not written (checked on a NaN-filled output with a row stride wider than
+    dv). Causal mask with holes and a fully masked row, GQA 4:1, ragged T and n_kv; split-K off,
+    on, and chosen by the library."""
+    import torch
+    H, HK, T, KV = 8, 2, 70, 389
+    Q = O.fill_normal((H, T, D), 990 + D)
+    K16 = O.f32_to_f16_bits(O.fill_normal((HK, KV, D), 991 + D))
+    V16 = O.f32_to_f16_bits(O.fill_normal((HK, KV, DV), 992 + DV))
+    M = np.full((T, 392), 7.0, np.float32)
+    M[:, :KV] = causal_mask(T, KV)
+    rnd = O.fill_uniform((T, KV), 993, 1.0)
+    M[:, :KV][rnd > 0.8] = -np.inf
+    M[5, :] = -np.inf
+    M16 = O.f32_to_f16_bits(M)
+    scale = float(np.float32(1.0) / np.sqrt(np.float32(D)))
+    want = O.flash_attn(Q, K16, V16, M16, scale)
+    q = torch.from_numpy(Q).cuda()
+    k = torch.from_numpy(K16.view(np.float16)).cuda()
+    v = torch.from_numpy(V16.view(np.float16)).cuda()
+    m = torch.from_numpy(M16.view(np.float16)).cuda()
+    for ns in (1, 3, 0):
+        wide = torch.full((T, H, DV + 16), float("nan"), dtype=torch.float32, device="cuda")
+        out = wide[:, :, :DV]
+        mx.flash_attn(q, k, v, m, scale, nsplit=ns, out=out)
+        torch.cuda.synchronize()
+        w = wide.cpu().numpy()
+        assert np.isnan(w[:, :, DV:]).all(), ("wrote past dv", ns)
+        got = w[:, :, :DV]
+        assert np.all(got[5] == 0.0), ns
+        r = compare(want, got)
+        print(f"padded D={D} DV={DV} nsplit={ns}: {r}")
+        assert r["nonfinite"] == 0 and r["max_abs"] <= 2e-2 and r["range_err"] <= 1e-2, (ns, r)
