@@ -16,10 +16,12 @@
 //             within each 16-key group so that each lane's P^T operand keys are one 16-byte
 //             chunk, see vt_pos); the mask tile classes (per 32-query x 64-key tile: every key
 //             masked / no key masked / mixed).
-//   fa        a block is 4 waves, each owning 32 query rows of one head, all 4 on one KV head
-//             (GQA reuse of the LDS tiles). Per 64-key tile: K [64][DK] and V^T [DV][64] arrive
+//   fa        a block is 4 tasks, each 32 query rows of one head, all 4 on one KV head (GQA
+//             reuse of the LDS tiles); two waves per task take alternate key tiles and merge at
+//             the end (one wave per task, alone on its SIMD, for DV 256, whose O tile takes 128
+//             accumulators). Per 64-key tile: K [64][DK] and V^T [DV][64] arrive
 //             in LDS by global_load_lds (a 4-deep ring, two tiles landing while two are used;
-//             2-deep when four stages do not fit, for DK 192);
+//             2-deep when four stages do not fit, for DK 192 and 256);
 //             tiles whose mask is -inf for all the block's queries are skipped, tiles with
 //             no mask entry read no mask. Scores are computed transposed, S^T = K . Q^T, so each
 //             lane owns one query: the row max and sum need one exchange with the partner lane
@@ -40,9 +42,6 @@ namespace mx {
 constexpr int FA_BKV = 64;      // keys per tile
 constexpr int FA_QW = 32;       // query rows per wave task
 constexpr int FA_TASKS = 4;     // wave tasks (head, 32-query tile) per block
-constexpr int FA_PAR = 2;       // waves per task, taking alternate key tiles
-constexpr int FA_WAVES = FA_TASKS * FA_PAR;
-constexpr int FA_THREADS = FA_WAVES * WAVE;
 constexpr int FA_LDS_MAX = 160 * 1024;
 constexpr int FA_CLS_RESERVE = 2048;   // LDS kept beside the ring for the class rows (KV <= 32768)
 
@@ -62,10 +61,15 @@ struct FaCfg {
     // the next pair is fetched between the steps
     static constexpr int NS = 4 * STAGE + FA_CLS_RESERVE <= FA_LDS_MAX - 64 ? 4 : 2;
     static constexpr int LDS = NS * STAGE;
-    static constexpr int PK = K_BYTES / (FA_THREADS * 16);   // DMA instructions per wave
-    static constexpr int PV = V_BYTES / (FA_THREADS * 16);
+    // waves per task: two taking alternate key tiles (merged at the end), or for DV > 128 one
+    // wave taking every tile, alone on its SIMD so the 128 accumulators of its O tile fit
+    static constexpr int PAR = DV > 128 ? 1 : 2;
+    static constexpr int WAVES = FA_TASKS * PAR;
+    static constexpr int THREADS = WAVES * WAVE;
+    static constexpr int PK = K_BYTES / (THREADS * 16);   // DMA instructions per wave
+    static constexpr int PV = V_BYTES / (THREADS * 16);
     static constexpr int PER = PK + PV;
-    static_assert(PK >= 1 && PV >= 1 && PK * FA_THREADS * 16 == K_BYTES && PV * FA_THREADS * 16 == V_BYTES, "DMA split");
+    static_assert(PK >= 1 && PV >= 1 && PK * THREADS * 16 == K_BYTES && PV * THREADS * 16 == V_BYTES, "DMA split");
     static_assert(DK % 64 == 0 && DV % 64 == 0, "head dims");
     static_assert(NS * STAGE + FA_CLS_RESERVE <= FA_LDS_MAX - 64, "LDS");
     // physical 16-byte chunk of logical chunk c in K row r
@@ -209,7 +213,8 @@ __global__ void __launch_bounds__(256) fa_prep_kernel(FaArgs a) {
 // main kernel
 // ---------------------------------------------------------------------------------------------
 template <int DK, int DV, bool SOFTCAP>
-__global__ void __launch_bounds__(FA_THREADS) __attribute__((amdgpu_waves_per_eu(2, 2)))
+__global__ void __launch_bounds__((FaCfg<DK, DV>::THREADS))
+__attribute__((amdgpu_waves_per_eu(FaCfg<DK, DV>::PAR, FaCfg<DK, DV>::PAR)))
 fa_kernel(FaArgs a) {
     using C = FaCfg<DK, DV>;
     extern __shared__ __align__(16) uint8_t smem[];
@@ -250,7 +255,7 @@ fa_kernel(FaArgs a) {
         const int nchunk = a.cls_stride / 16;
         const int items = (qt_last - qt_first + 1) * nchunk;
         int mylo = nkt, myhi = 0;
-        for (int it = t; it < items; it += FA_THREADS) {
+        for (int it = t; it < items; it += C::THREADS) {
             const int q = qt_first + it / nchunk, c = it % nchunk;
             const u32x4 w = *(const u32x4 *)(a.cls + (int64_t)q * a.cls_stride + 16 * c);
             *(u32x4 *)(smem + C::LDS + (q - qt_first) * a.cls_stride + 16 * c) = w;   // kept for the loop
@@ -291,7 +296,7 @@ fa_kernel(FaArgs a) {
     const uint16_t * vsrc[C::PV];
 #pragma unroll
     for (int q = 0; q < C::PK; q++) {
-        const int slot = (q * FA_WAVES + wave) * WAVE + lane;
+        const int slot = (q * C::WAVES + wave) * WAVE + lane;
         const int r = slot / C::KCH, c = C::kchunk_inv(r, slot % C::KCH);
         const bool real = 8 * c < a.dk;
         kstr[q] = real ? a.k_nb1 : 0;
@@ -299,7 +304,7 @@ fa_kernel(FaArgs a) {
     }
 #pragma unroll
     for (int q = 0; q < C::PV; q++) {
-        const int slot = (q * FA_WAVES + wave) * WAVE + lane;
+        const int slot = (q * C::WAVES + wave) * WAVE + lane;
         const int r = slot / 8, c = (slot % 8) ^ ((r / 2) & 7);
         vsrc[q] = a.vt + ((int64_t)hk * DV + r) * a.kvp + 8 * c;                 // + j0 per tile
     }
@@ -312,13 +317,13 @@ fa_kernel(FaArgs a) {
         const int j0 = (tile0 + i) * FA_BKV;
 #pragma unroll
         for (int q = 0; q < C::PK; q++) {
-            const int slot = (q * FA_WAVES + wave) * WAVE + lane;
+            const int slot = (q * C::WAVES + wave) * WAVE + lane;
             const int r = slot / C::KCH;
             const int64_t jr = (int64_t)min(j0 + r, kv_last) - r;
-            fa_dma16(ksrc[q] + jr * kstr[q], st + (q * FA_WAVES + wave_s) * 1024);
+            fa_dma16(ksrc[q] + jr * kstr[q], st + (q * C::WAVES + wave_s) * 1024);
         }
 #pragma unroll
-        for (int q = 0; q < C::PV; q++) fa_dma16(vsrc[q] + j0, st + C::K_BYTES + (q * FA_WAVES + wave_s) * 1024);
+        for (int q = 0; q < C::PV; q++) fa_dma16(vsrc[q] + j0, st + C::K_BYTES + (q * C::WAVES + wave_s) * 1024);
     };
 
     const int xv = (lq / 2) & 7;                    // V^T row swizzle: rows db*32 + lq
@@ -369,115 +374,118 @@ fa_kernel(FaArgs a) {
         __builtin_amdgcn_s_barrier();
     }
     for (int stp = 0; stp < nsteps; stp++) {
-        const int i = 2 * stp + par;                    // this wave's local tile
-        const int tile = tile0 + i;
-        const int j0 = tile * FA_BKV;
-        const uint8_t * ks = smem + (i % FA_NS) * C::STAGE;
-        const uint8_t * vt = ks + C::K_BYTES;
-        // the class is the same in every lane of the wave: read it into an SGPR, so the branch
-        // below is a scalar one
-        const uint32_t cls = __builtin_amdgcn_readfirstlane(
-            (active && i < ntl) ? (uint32_t)cls_w[tile] : (uint32_t)FA_TILE_SKIP);
-        if (cls != FA_TILE_SKIP) {
-            // ---- S^T = K . Q^T for 64 keys: two 32-key blocks ----
-            float16v sacc[2];
+        // one tile of the step per wave when two share a task, both when one wave has the task
+        for (int sub = 0; sub < 3 - C::PAR; sub++) {
+            const int i = 2 * stp + (C::PAR == 2 ? par : sub);   // this wave's local tile
+            const int tile = tile0 + i;
+            const int j0 = tile * FA_BKV;
+            const uint8_t * ks = smem + (i % FA_NS) * C::STAGE;
+            const uint8_t * vt = ks + C::K_BYTES;
+            // the class is the same in every lane of the wave: read it into an SGPR, so the branch
+            // below is a scalar one
+            const uint32_t cls = __builtin_amdgcn_readfirstlane(
+                (active && i < ntl) ? (uint32_t)cls_w[tile] : (uint32_t)FA_TILE_SKIP);
+            if (cls != FA_TILE_SKIP) {
+                // ---- S^T = K . Q^T for 64 keys: two 32-key blocks ----
+                float16v sacc[2];
 #pragma unroll
-            for (int kb = 0; kb < 2; kb++) {
-                half8 kf[KSTEPS];
+                for (int kb = 0; kb < 2; kb++) {
+                    half8 kf[KSTEPS];
 #pragma unroll
-                for (int s2 = 0; s2 < KSTEPS; s2++)
-                    kf[s2] = *(const half8 *)(ks + (kb * 32 + lq) * (DK * 2) + (C::kchunk(kb * 32 + lq, 2 * s2 + lg) << 4));
+                    for (int s2 = 0; s2 < KSTEPS; s2++)
+                        kf[s2] = *(const half8 *)(ks + (kb * 32 + lq) * (DK * 2) + (C::kchunk(kb * 32 + lq, 2 * s2 + lg) << 4));
 #pragma unroll
-                for (int e = 0; e < 16; e++) sacc[kb][e] = 0.0f;
+                    for (int e = 0; e < 16; e++) sacc[kb][e] = 0.0f;
 #pragma unroll
-                for (int s2 = 0; s2 < KSTEPS; s2++) sacc[kb] = mfma32(kf[s2], qf[s2], sacc[kb]);
-            }
-            // ---- scores: scale back, cap, mask, key bound (each a wave-uniform case) ----
-            if (q_scaled) {
-#pragma unroll
-                for (int kb = 0; kb < 2; kb++)
-#pragma unroll
-                    for (int ii = 0; ii < 16; ii++) sacc[kb][ii] *= qfac;
-            }
-            if (SOFTCAP) {
-#pragma unroll
-                for (int kb = 0; kb < 2; kb++)
-#pragma unroll
-                    for (int ii = 0; ii < 16; ii++) sacc[kb][ii] = a.softcap * tanhf(sacc[kb][ii] * inv_cap);
-            }
-            if (cls == FA_TILE_MIXED) {
-                if (mrow) {
+                    for (int s2 = 0; s2 < KSTEPS; s2++) sacc[kb] = mfma32(kf[s2], qf[s2], sacc[kb]);
+                }
+                // ---- scores: scale back, cap, mask, key bound (each a wave-uniform case) ----
+                if (q_scaled) {
 #pragma unroll
                     for (int kb = 0; kb < 2; kb++)
 #pragma unroll
-                        for (int q4 = 0; q4 < 4; q4++) {
-                            const int jb = j0 + kb * 32 + 8 * q4 + 4 * lg;   // first of 4 keys
-                            float mk[4];
-                            if (jb + 3 < a.KV) {
-                                const u32x2 mm = *(const u32x2 *)(mrow + jb);
-                                mk[0] = h2f_bits((uint16_t)(mm[0] & 0xFFFFu));
-                                mk[1] = h2f_bits((uint16_t)(mm[0] >> 16));
-                                mk[2] = h2f_bits((uint16_t)(mm[1] & 0xFFFFu));
-                                mk[3] = h2f_bits((uint16_t)(mm[1] >> 16));
-                            } else {
-#pragma unroll
-                                for (int e = 0; e < 4; e++) mk[e] = (jb + e < a.KV) ? h2f_bits(mrow[jb + e]) : 0.0f;
-                            }
-#pragma unroll
-                            for (int e = 0; e < 4; e++) sacc[kb][4 * q4 + e] += mk[e];
-                        }
+                        for (int ii = 0; ii < 16; ii++) sacc[kb][ii] *= qfac;
                 }
-            }
-            if (j0 + FA_BKV > a.KV) {
+                if (SOFTCAP) {
+#pragma unroll
+                    for (int kb = 0; kb < 2; kb++)
+#pragma unroll
+                        for (int ii = 0; ii < 16; ii++) sacc[kb][ii] = a.softcap * tanhf(sacc[kb][ii] * inv_cap);
+                }
+                if (cls == FA_TILE_MIXED) {
+                    if (mrow) {
+#pragma unroll
+                        for (int kb = 0; kb < 2; kb++)
+#pragma unroll
+                            for (int q4 = 0; q4 < 4; q4++) {
+                                const int jb = j0 + kb * 32 + 8 * q4 + 4 * lg;   // first of 4 keys
+                                float mk[4];
+                                if (jb + 3 < a.KV) {
+                                    const u32x2 mm = *(const u32x2 *)(mrow + jb);
+                                    mk[0] = h2f_bits((uint16_t)(mm[0] & 0xFFFFu));
+                                    mk[1] = h2f_bits((uint16_t)(mm[0] >> 16));
+                                    mk[2] = h2f_bits((uint16_t)(mm[1] & 0xFFFFu));
+                                    mk[3] = h2f_bits((uint16_t)(mm[1] >> 16));
+                                } else {
+#pragma unroll
+                                    for (int e = 0; e < 4; e++) mk[e] = (jb + e < a.KV) ? h2f_bits(mrow[jb + e]) : 0.0f;
+                                }
+#pragma unroll
+                                for (int e = 0; e < 4; e++) sacc[kb][4 * q4 + e] += mk[e];
+                            }
+                    }
+                }
+                if (j0 + FA_BKV > a.KV) {
+#pragma unroll
+                    for (int kb = 0; kb < 2; kb++)
+#pragma unroll
+                        for (int ii = 0; ii < 16; ii++)
+                            if (j0 + kb * 32 + 8 * (ii / 4) + 4 * lg + (ii % 4) >= a.KV) sacc[kb][ii] = -INFINITY;
+                }
+                float mt = -INFINITY;
 #pragma unroll
                 for (int kb = 0; kb < 2; kb++)
 #pragma unroll
-                    for (int ii = 0; ii < 16; ii++)
-                        if (j0 + kb * 32 + 8 * (ii / 4) + 4 * lg + (ii % 4) >= a.KV) sacc[kb][ii] = -INFINITY;
-            }
-            float mt = -INFINITY;
+                    for (int ii = 0; ii < 16; ii++) mt = fmaxf(mt, sacc[kb][ii]);
+                mt = fmaxf(mt, __shfl_xor(mt, 32, WAVE));
+                const float m_new = fmaxf(m_run, mt);
+                // No lane-divergent branch here: the P.V MFMA reads every lane's operands, so a
+                // lane whose keys are all masked so far must still supply finite P (zeros).
+                const float m_use = (m_new == -INFINITY) ? 0.0f : m_new;
+                const float alpha = (m_run == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f((m_run - m_use) * LOG2E);
+                const float mb = m_use * LOG2E;
+                float psum = 0.0f;
 #pragma unroll
-            for (int kb = 0; kb < 2; kb++)
+                for (int kb = 0; kb < 2; kb++)
 #pragma unroll
-                for (int ii = 0; ii < 16; ii++) mt = fmaxf(mt, sacc[kb][ii]);
-            mt = fmaxf(mt, __shfl_xor(mt, 32, WAVE));
-            const float m_new = fmaxf(m_run, mt);
-            // No lane-divergent branch here: the P.V MFMA reads every lane's operands, so a
-            // lane whose keys are all masked so far must still supply finite P (zeros).
-            const float m_use = (m_new == -INFINITY) ? 0.0f : m_new;
-            const float alpha = (m_run == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f((m_run - m_use) * LOG2E);
-            const float mb = m_use * LOG2E;
-            float psum = 0.0f;
+                    for (int ii = 0; ii < 16; ii++) {
+                        // v_exp_f32: exp2(-inf) = 0; results below the fp32 normal range flush to 0
+                        const float p = __builtin_amdgcn_exp2f(fmaf(sacc[kb][ii], LOG2E, -mb));
+                        sacc[kb][ii] = p;
+                        psum += p;
+                    }
+                l_run = l_run * alpha + psum;
+                m_run = m_new;
+                if (__any(alpha != 1.0f)) {   // once the running max settles, most tiles skip this
 #pragma unroll
-            for (int kb = 0; kb < 2; kb++)
+                    for (int db = 0; db < DBLK; db++)
 #pragma unroll
-                for (int ii = 0; ii < 16; ii++) {
-                    // v_exp_f32: exp2(-inf) = 0; results below the fp32 normal range flush to 0
-                    const float p = __builtin_amdgcn_exp2f(fmaf(sacc[kb][ii], LOG2E, -mb));
-                    sacc[kb][ii] = p;
-                    psum += p;
+                        for (int e = 0; e < 16; e++) o[db][e] *= alpha;
                 }
-            l_run = l_run * alpha + psum;
-            m_run = m_new;
-            if (__any(alpha != 1.0f)) {   // once the running max settles, most tiles skip this
+                // ---- O^T += V^T . P^T, 4 steps of 16 keys; V^T's key slots follow vt_pos ----
 #pragma unroll
-                for (int db = 0; db < DBLK; db++)
+                for (int s2 = 0; s2 < 4; s2++) {
+                    const int kb = s2 / 2, hs = s2 % 2;
+                    half8 pf;
 #pragma unroll
-                    for (int e = 0; e < 16; e++) o[db][e] *= alpha;
-            }
-            // ---- O^T += V^T . P^T, 4 steps of 16 keys; V^T's key slots follow vt_pos ----
+                    for (int e = 0; e < 8; e++) pf[e] = (_Float16)sacc[kb][8 * hs + e];
+                    half8 vf[DBLK];
 #pragma unroll
-            for (int s2 = 0; s2 < 4; s2++) {
-                const int kb = s2 / 2, hs = s2 % 2;
-                half8 pf;
+                    for (int db = 0; db < DBLK; db++)
+                        vf[db] = *(const half8 *)(vt + (db * 32 + lq) * 128 + (((2 * s2 + lg) ^ xv) << 4));
 #pragma unroll
-                for (int e = 0; e < 8; e++) pf[e] = (_Float16)sacc[kb][8 * hs + e];
-                half8 vf[DBLK];
-#pragma unroll
-                for (int db = 0; db < DBLK; db++)
-                    vf[db] = *(const half8 *)(vt + (db * 32 + lq) * 128 + (((2 * s2 + lg) ^ xv) << 4));
-#pragma unroll
-                for (int db = 0; db < DBLK; db++) o[db] = mfma32(vf[db], pf, o[db]);
+                    for (int db = 0; db < DBLK; db++) o[db] = mfma32(vf[db], pf, o[db]);
+                }
             }
         }
         // the next two tiles have landed for every wave, and every wave is done with these two
@@ -496,28 +504,30 @@ fa_kernel(FaArgs a) {
     __syncthreads();
 
     // ---- merge each task's two waves (same rows, disjoint key tiles) through LDS ----
-    float * ob = (float *)smem + (size_t)slot_task * (DBLK * 16 + 2) * WAVE;   // [DBLK*16 + 2][64]
-    if (par == 1) {
+    if constexpr (C::PAR == 2) {
+        float * ob = (float *)smem + (size_t)slot_task * (DBLK * 16 + 2) * WAVE;   // [DBLK*16 + 2][64]
+        if (par == 1) {
 #pragma unroll
-        for (int db = 0; db < DBLK; db++)
+            for (int db = 0; db < DBLK; db++)
 #pragma unroll
-            for (int e = 0; e < 16; e++) ob[(db * 16 + e) * WAVE + lane] = o[db][e];
-        ob[(DBLK * 16) * WAVE + lane] = m_run;
-        ob[(DBLK * 16 + 1) * WAVE + lane] = l_run;
-    }
-    __syncthreads();
-    if (par == 1) return;
-    {
-        const float m1 = ob[(DBLK * 16) * WAVE + lane], l1 = ob[(DBLK * 16 + 1) * WAVE + lane];
-        const float M = fmaxf(m_run, m1);
-        const float a0 = (m_run == -INFINITY) ? 0.0f : __expf(m_run - M);
-        const float a1 = (m1 == -INFINITY) ? 0.0f : __expf(m1 - M);
+                for (int e = 0; e < 16; e++) ob[(db * 16 + e) * WAVE + lane] = o[db][e];
+            ob[(DBLK * 16) * WAVE + lane] = m_run;
+            ob[(DBLK * 16 + 1) * WAVE + lane] = l_run;
+        }
+        __syncthreads();
+        if (par == 1) return;
+        {
+            const float m1 = ob[(DBLK * 16) * WAVE + lane], l1 = ob[(DBLK * 16 + 1) * WAVE + lane];
+            const float M = fmaxf(m_run, m1);
+            const float a0 = (m_run == -INFINITY) ? 0.0f : __expf(m_run - M);
+            const float a1 = (m1 == -INFINITY) ? 0.0f : __expf(m1 - M);
 #pragma unroll
-        for (int db = 0; db < DBLK; db++)
+            for (int db = 0; db < DBLK; db++)
 #pragma unroll
-            for (int e = 0; e < 16; e++) o[db][e] = o[db][e] * a0 + ob[(db * 16 + e) * WAVE + lane] * a1;
-        l_run = l_run * a0 + l1 * a1;
-        m_run = M;
+                for (int e = 0; e < 16; e++) o[db][e] = o[db][e] * a0 + ob[(db * 16 + e) * WAVE + lane] * a1;
+            l_run = l_run * a0 + l1 * a1;
+            m_run = M;
+        }
     }
 
     const float l_tot = l_run + __shfl_xor(l_run, 32, WAVE);
@@ -610,6 +620,7 @@ static size_t fa_ring_bytes(int D, int DV) {
     if (D == 64 && DV == 64) return FaCfg<64, 64>::LDS;
     if (D == 128 && DV == 128) return FaCfg<128, 128>::LDS;
     if (D == 192 && DV == 128) return FaCfg<192, 128>::LDS;
+    if (D == 256 && DV == 256) return FaCfg<256, 256>::LDS;
     return 0;
 }
 static size_t fa_lds_bytes(const FaArgs & a) { return fa_ring_bytes(a.D, a.DV) + (size_t)FA_TASKS * a.cls_stride; }
@@ -637,7 +648,7 @@ static hipError_t fa_launch_main(const FaArgs & a, int nb, hipStream_t st) {
         if (e != hipSuccess) return e;
         done = true;
     }
-    hipLaunchKernelGGL((fa_kernel<DK, DV, SC>), dim3(nb), dim3(FA_THREADS), fa_lds_bytes(a), st, a);
+    hipLaunchKernelGGL((fa_kernel<DK, DV, SC>), dim3(nb), dim3(FaCfg<DK, DV>::THREADS), fa_lds_bytes(a), st, a);
     return hipGetLastError();
 }
 
@@ -660,6 +671,7 @@ hipError_t launch_fa(const FaArgs & a, hipStream_t st) {
     if (a.D == 64 && a.DV == 64) return fa_launch_all<64, 64>(a, nb, st);
     if (a.D == 128 && a.DV == 128) return fa_launch_all<128, 128>(a, nb, st);
     if (a.D == 192 && a.DV == 128) return fa_launch_all<192, 128>(a, nb, st);
+    if (a.D == 256 && a.DV == 256) return fa_launch_all<256, 256>(a, nb, st);
     return hipErrorInvalidValue;
 }
 

@@ -4,12 +4,12 @@
 
 namespace mx {
 
-// The attention kernels are built for (DK, DV) = (64, 64), (128, 128) and (192, 128). Other head
-// dims run on the smallest of them that holds both, zero-padded: Q and K columns past dk and V
-// columns past dv read as zero (they add nothing to Q.K or to P.V), output columns past dv are
-// not written. So every dk <= 192 and dv <= 128 that are multiples of 8 are taken.
+// The attention kernels are built for (DK, DV) = (64, 64), (128, 128), (192, 128) and
+// (256, 256). Other head dims run on the smallest of them that holds both, zero-padded: Q and K
+// columns past dk and V columns past dv read as zero (they add nothing to Q.K or to P.V), output
+// columns past dv are not written. So every dk and dv up to 256 that are multiples of 8 are taken.
 inline bool fa_pad_dims(int dk, int dv, int & D, int & DV) {
-    static const int kDims[3][2] = {{64, 64}, {128, 128}, {192, 128}};
+    static const int kDims[4][2] = {{64, 64}, {128, 128}, {192, 128}, {256, 256}};
     if (dk <= 0 || dv <= 0 || dk % 8 || dv % 8) return false;
     for (const auto & p : kDims)
         if (dk <= p[0] && dv <= p[1]) {

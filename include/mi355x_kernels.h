@@ -163,9 +163,9 @@ MI355X_API size_t mi355x_flash_attn_workspace(const mi355x_fa_args * a, int nspl
 
 /* dst = softmax(cap(scale * q.k) + mask) . v for every (token, head); head h reads KV head
  * h / (H / HK). Two kernels on `stream`: a prep pass over V and the mask, then the attention.
- * Concurrent calls must not share a workspace. D <= 192 and DV <= 128, both multiples of 8 (the
- * kernels are built for (64, 64), (128, 128) and the MLA (192, 128); other dims run zero-padded
- * on the smallest that holds them); H % HK == 0; max_bias
+ * Concurrent calls must not share a workspace. D and DV up to 256, multiples of 8 (the kernels
+ * are built for (64, 64), (128, 128), the MLA (192, 128) and (256, 256); other dims run
+ * zero-padded on the smallest that holds them); H % HK == 0; max_bias
  * must be 0 (no ALiBi); the mask
  * covers [T][KV] with mask_nb1 % 4 == 0; q rows and dst rows 16-byte aligned; k/v rows 16-byte
  * aligned. Rows whose every key is masked are written as zeros. Replaces

@@ -175,9 +175,12 @@ def test_fa_mla_k192_v128(mx, H, HK, softcap):
         assert r["nonfinite"] == 0 and r["max_abs"] <= 2e-2 and r["range_err"] <= 1e-2, (ns, r)
 
 
-@pytest.mark.parametrize("D,DV", [(32, 32), (96, 96), (128, 64), (64, 128), (160, 80), (192, 64)])
-def test_fa_padded_head_dims(mx, D, DV):
-    """Head dims between the built kernels (64/64, 128/128, 192/128) run zero-padded onto the
+@pytest.mark.parametrize("D,DV,softcap", [(32, 32, 0.0), (96, 96, 0.0), (128, 64, 0.0), (64, 128, 0.0),
+                                          (160, 80, 0.0), (192, 64, 0.0), (256, 256, 0.0), (256, 256, 50.0),
+                                          (192, 192, 0.0), (224, 160, 0.0)])
+def test_fa_padded_head_dims(mx, D, DV, softcap):
+    """Head dims between the built kernels (64/64, 128/128, 192/128, 256/256; the last with one
+    wave per query tile) run zero-padded onto the
     smallest that holds them: Q and K columns past dk and V columns past dv read as zero, output
     columns past dv are not written (checked on a NaN-filled output with a row stride wider than
     dv). Causal mask with holes and a fully masked row, GQA 4:1, ragged T and n_kv; split-K off,
@@ -194,7 +197,7 @@ def test_fa_padded_head_dims(mx, D, DV):
     M[5, :] = -np.inf
     M16 = O.f32_to_f16_bits(M)
     scale = float(np.float32(1.0) / np.sqrt(np.float32(D)))
-    want = O.flash_attn(Q, K16, V16, M16, scale)
+    want = O.flash_attn(Q, K16, V16, M16, scale, softcap=softcap)
     q = torch.from_numpy(Q).cuda()
     k = torch.from_numpy(K16.view(np.float16)).cuda()
     v = torch.from_numpy(V16.view(np.float16)).cuda()
@@ -202,12 +205,12 @@ def test_fa_padded_head_dims(mx, D, DV):
     for ns in (1, 3, 0):
         wide = torch.full((T, H, DV + 16), float("nan"), dtype=torch.float32, device="cuda")
         out = wide[:, :, :DV]
-        mx.flash_attn(q, k, v, m, scale, nsplit=ns, out=out)
+        mx.flash_attn(q, k, v, m, scale, softcap=softcap, nsplit=ns, out=out)
         torch.cuda.synchronize()
         w = wide.cpu().numpy()
         assert np.isnan(w[:, :, DV:]).all(), ("wrote past dv", ns)
         got = w[:, :, :DV]
         assert np.all(got[5] == 0.0), ns
         r = compare(want, got)
-        print(f"padded D={D} DV={DV} nsplit={ns}: {r}")
+        print(f"padded D={D} DV={DV} softcap={softcap} nsplit={ns}: {r}")
         assert r["nonfinite"] == 0 and r["max_abs"] <= 2e-2 and r["range_err"] <= 1e-2, (ns, r)

@@ -62,8 +62,8 @@ CASES = [
     ("FA: head_dim%32 != 0 (48) -> CPU", False, lambda: fa_supported(48, 256, 8, 1024, 2, mx.F16, 0.0)),
     ("FA: K/V not F16 -> CPU", False, lambda: fa_supported(64, 256, 8, 1024, 2, mx.F32, 0.0)),
     ("FA: ALiBi (max_bias > 0) -> CPU", False, lambda: fa_supported(64, 256, 8, 1024, 2, mx.F16, 8.0)),
-    # Narrower than the reference: the kernels take dk <= 192 and dv <= 128 (zero-padded onto the
-    # 64/64, 128/128 and 192/128 builds); the reference takes any dk%32 / dv%16
+    # Narrower than the reference: the kernels take dk and dv up to 256 (zero-padded onto the
+    # 64/64, 128/128, 192/128 and 256/256 builds); the reference takes any dk%32 / dv%16
     # (ggml-rocket.cpp:7740-7760).
     ("FA: head_dim 128 -> offload", True, lambda: fa_supported(128, 512, 32, 4096, 8, mx.F16, 0.0)),
     ("FA: head_dim 96 -> offload (padded to 128)", True, lambda: fa_supported(96, 256, 8, 1024, 2, mx.F16, 0.0)),
@@ -71,8 +71,10 @@ CASES = [
     ("FA: dk 192 / dv 128 (MLA) -> offload", True, lambda: fa_supported(192, 256, 8, 1024, 2, mx.F16, 0.0, 0, 128)),
     ("FA: dk 160 / dv 80 -> offload (padded to 192 / 128)", True, lambda: fa_supported(160, 256, 8, 1024, 2, mx.F16, 0.0, 0, 80)),
     ("FA: dk 128 / dv 64 -> offload (dv padded to 128)", True, lambda: fa_supported(128, 256, 8, 1024, 2, mx.F16, 0.0, 0, 64)),
-    ("FA: dk 192 / dv 192 -> CPU (dv > 128)", False, lambda: fa_supported(192, 256, 8, 1024, 2, mx.F16, 0.0)),
-    ("FA: head_dim 256 -> CPU (dk > 192)", False, lambda: fa_supported(256, 256, 8, 1024, 2, mx.F16, 0.0)),
+    ("FA: dk 192 / dv 192 -> offload (padded to 256)", True, lambda: fa_supported(192, 256, 8, 1024, 2, mx.F16, 0.0)),
+    ("FA: head_dim 256 (Gemma) -> offload", True, lambda: fa_supported(256, 256, 8, 1024, 2, mx.F16, 0.0)),
+    ("FA: dk 576 / dv 512 (absorbed MLA) -> CPU", False, lambda: fa_supported(576, 256, 8, 1024, 1, mx.F16, 0.0, 0, 512)),
+    ("FA: head_dim 288 -> CPU (> 256)", False, lambda: fa_supported(288, 256, 8, 1024, 2, mx.F16, 0.0)),
     # Narrower: a quantized type without a device decoder is declined (the reference takes any
     # type with a ggml to_float, 7452-7455).
     ("Q4_0 leaf -> CPU (no device decoder)", False, lambda: mm_supported(K, N, MQ, 2)),
