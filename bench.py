@@ -1,7 +1,7 @@
 #!/usr/bin/env python3
 """Prefill benchmark: the backend-claimed ops of an 8B-shape Q4_K prefill on one MI355X.
 
-Workload (BASELINE metric "prefill tok/s (8B-shape Q4_K, 2048 tok)"): a Llama-3-8B-shaped stack
+Workload (metric "prefill tok/s (8B-shape Q4_K, 2048 tok)"): a Llama-3-8B-shaped stack
 (32 layers, d 4096, FFN 14336, 32 query / 8 KV heads, head dim 128) with random-init Q4_K
 weights (quantized from N(0, 0.02); every layer distinct), prefilling 2048 tokens in 4
 micro-batches of 512. One step runs, per micro-batch and layer, exactly the ops this backend

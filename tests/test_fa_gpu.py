@@ -5,7 +5,7 @@ typical (random, causal), scaled (scaled logits past 65504) and q range (scaled 
 The reference sends the last two to its host fallback because its NPU keeps an fp16 score
 surface; here scores stay in fp32 registers and a Q row past fp16 range is divided by a per-row
 factor, so all four run on the device, scored against the same oracle and tolerances.
-Plus the BASELINE shapes: 32 query / 8 KV heads, d 128, 512 tokens, n_kv 1024/4096/8192,
+Plus the prefill attention shapes: 32 query / 8 KV heads, d 128, 512 tokens, n_kv 1024/4096/8192,
 N(0,1) inputs, causal mask, scale 1/sqrt(128); scored on sampled query rows.
 """
 import numpy as np

@@ -1,7 +1,7 @@
 """MUL_MAT on the GPU against the CPU oracle, through the C ABI.
 
 Cases follow test-rocket-matmul.cpp: its F16 shapes (incl. M not a multiple of 4), the
-outlier-row case, the fused shared-src1 groups, its quantized shapes, plus the BASELINE shapes:
+outlier-row case, the fused shared-src1 groups, its quantized shapes, plus the single-op shapes:
 the F16 [8192 x 2048] x [512 x 2048] case and the Q8_0 / Q4_K / Q6_K sweep. Bars (tests/bars.py):
 the element bar, worst-column cosine >= 0.999, and max|d|/max|ref| <= 1e-2.
 """

@@ -2,7 +2,7 @@
 
 Cases follow test-rocket-moe.cpp (F16 and quantized expert stacks, both b forms ne11 = 1 and
 ne11 = n_used, pad rows, 16 experts / 4 used, skewed routing with the last expert empty,
-outlier activation channels, one weight upload serving several token counts) plus the BASELINE
+outlier activation channels, one weight upload serving several token counts) plus the MoE prefill
 shape: 128 experts, top-8 routing from a softmax over seeded N(0,1) router logits, 512 tokens,
 d_model 2048, expert FFN 768, gate/up/down Q4_K, and the reference's MXFP4 (gpt-oss) stacks,
 decoded exactly to fp16 here (the reference merges block exponents onto int8 codes instead, so
