@@ -321,10 +321,13 @@ def test_skinny_mul_mat(mx, wtype, M):
     import torch
     ref = O.mul_mat(wtype, payload, Xf, N, K)
     w = mx.upload_weight(wtype, payload, N, K)
-    out = torch.full((M, N), float("nan"), dtype=torch.float32, device="cuda")
-    mx.mul_mat(wtype, w, N, K, _dev(Xf), out)
+    # a row stride wider than N: the pack clears only the N columns the GEMM adds into
+    wide = torch.full((M, N + 24), float("nan"), dtype=torch.float32, device="cuda")
+    mx.mul_mat(wtype, w, N, K, _dev(Xf), wide[:, :N])
     torch.cuda.synchronize()
-    _assert_bars(ref, out.cpu().numpy(), M, N, f"skinny {O.TYPE_NAMES[wtype]} M={M}")
+    got = wide.cpu().numpy()
+    assert np.isnan(got[:, N:]).all(), "wrote past N"
+    _assert_bars(ref, got[:, :N], M, N, f"skinny {O.TYPE_NAMES[wtype]} M={M}")
 
 
 @pytest.mark.parametrize("wtype", SKINNY_TYPES)
