@@ -1220,10 +1220,14 @@ __global__ void zero_rows_kernel(GemmArgs args);
 // K 3072-14336 launch 144-256 blocks).
 constexpr int SKINNY_CFG = N_CFGS;
 
+// Row-major fp16 weights also have the DMA kernels: past M = 32 those win unless K is deep for
+// the output width (measured at M 32-128: K 14336 x N 4096 at M 128 50 against 60 us on the
+// skinny kernel; N 14336 x K 4096 at M 128 51 against 44 us on the DMA one).
 static bool use_skinny(int wt, const GemmArgs & a) {
     if (wt == T_F16T || a.M > SK_MAX_M) return false;
     if (const char * e = getenv("MI355X_GEMM_CFG"))
         if (*e) return atoi(e) == SKINNY_CFG;
+    if (wt == T_F16 && a.M > 32 && (int64_t)a.K < 2 * tiles_n_cols(a)) return false;
     return true;
 }
 
