@@ -13,9 +13,11 @@
 //   dequant_f16   a weight panel -> fp16 [rows][K] (the resident-fp16 form, "prepacked-q").
 //   pack_weight   a ggml Q8_0 / Q6_K / MXFP4 payload -> its split HBM layout (mx_weights.h).
 //
-// Two GEMM kernels: a register-staged one that decodes any weight format into LDS (gemm_kernel),
-// and for fp16 weights one that moves both operands into LDS by DMA (gemm_f16_kernel). The
-// launcher picks a tile configuration of either per call from the output shape.
+// Three GEMM kernels: a register-staged one that decodes any weight format into LDS
+// (gemm_kernel), for fp16 weights one that moves both operands into LDS by DMA (gemm_f16_kernel,
+// and its two-width variant gemm_f16_cols_kernel), and for M <= 128 one that decodes the weight
+// straight into MFMA operands (gemm_skinny_kernel). The launcher picks a kernel and tile
+// configuration per call from the output shape.
 
 #include <algorithm>
 #include <cmath>
@@ -1221,8 +1223,8 @@ __global__ void zero_rows_kernel(GemmArgs args);
 constexpr int SKINNY_CFG = N_CFGS;
 
 // Row-major fp16 weights also have the DMA kernels: past M = 32 those win unless K is deep for
-// the output width (measured at M 32-128: K 14336 x N 4096 at M 128 50 against 60 us on the
-// skinny kernel; N 14336 x K 4096 at M 128 51 against 44 us on the DMA one).
+// the output width (measured at M 32-128; at M 128, K 14336 x N 4096: 50 us skinny, 60 us DMA;
+// N 14336 x K 4096: 51 us skinny, 44 us DMA).
 static bool use_skinny(int wt, const GemmArgs & a) {
     if (wt == T_F16T || a.M > SK_MAX_M) return false;
     if (const char * e = getenv("MI355X_GEMM_CFG"))
