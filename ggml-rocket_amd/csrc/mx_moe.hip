@@ -122,8 +122,9 @@ __global__ void __launch_bounds__(MOE_SORT_THREADS) moe_sort_kernel(MoeArgs a) {
 // in the dense register-staged GEMM), and every thread two 16-byte chunks of the tile's
 // gathered activation rows; loads run R K slabs ahead of the MFMAs, so an HBM round trip has
 // R - 1 slabs of work to hide behind before its data is decoded. The slab loop is bound by the
-// decode's VALU work (about 5 instructions per weight); 128-column blocks fit three to a CU
-// (48 KiB of LDS each), so 768 of them (128 experts x 6 column blocks of a 768-wide gate/up)
+// per-slab chain of load, decode, LDS store, barrier and MFMA (a decode with a third of the
+// VALU instructions ran at the same speed, as did four register stages); 128-column blocks fit
+// three to a CU (48 KiB of LDS each), so 768 of them (128 experts x 6 column blocks of a 768-wide gate/up)
 // are one even round over 256 CUs, where 256-column blocks left half the CUs with double work.
 // Two register stages for every type: one block per CU (one wave per SIMD) with 4 stages of
 // Q4_K lookahead ran at the same speed as with 2, so the slabs are not waiting on memory.
