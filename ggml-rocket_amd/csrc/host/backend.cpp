@@ -17,6 +17,7 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <algorithm>
 #include <atomic>
 #include <condition_variable>
 #include <functional>
@@ -38,47 +39,54 @@ using namespace mxh;
 
 namespace {
 
-// ---- circuit breaker (ggml-rocket.cpp:263-307) ----------------------------------------------
-// Three consecutive device failures open a route: its fallback runs directly for 64 calls, then
-// one call probes the device again; a failed probe doubles the interval, up to 4096 calls; a
-// success closes it. Structural declines (MI355X_E_ARG / _UNSUPPORTED) do not count.
-struct Breaker {
-    int fails = 0;
-    long skip = 0;
-    long open_len = 0;
-    long attempts = 0, failures = 0, bypassed = 0;
-    int inject = 0;   // host-side fault injection for tests
-};
+// ---- route health (the contract of ggml-rocket.cpp:263-307) ---------------------------------
+// Each route group keeps a failure streak. When the streak reaches kTrip the route "rests": the
+// CPU fallback serves the next rest_len() calls without a device attempt, then one call tries
+// the device again. Every trip in a row (a failed retry adds one) doubles the rest, from 64
+// calls up to a ceiling of 4096; a device success ends the streak and forgets the trips. A
+// status that only says the shape or type is not taken (MI355X_E_ARG, MI355X_E_UNSUPPORTED)
+// leaves the record as it is.
+class RouteHealth {
+public:
+    static constexpr int kTrip = 3;
+    static constexpr int kRestShift0 = 6;     // first rest: 1 << 6 = 64 calls
+    static constexpr int kRestShiftMax = 12;  // longest rest: 1 << 12 = 4096 calls
 
-bool breaker_allow(Breaker & b) {
-    if (b.skip > 0) {
-        b.skip--;
-        b.bypassed++;
+    // false while the route rests (the call is counted as bypassed)
+    bool try_device() {
+        if (resting_ == 0) return true;
+        resting_--;
+        bypassed++;
         return false;
     }
-    return true;
-}
 
-bool device_failure(int rc) {
-    return rc != MI355X_OK && rc != MI355X_E_ARG && rc != MI355X_E_UNSUPPORTED;
-}
-
-void breaker_note(Breaker & b, int rc, const char * route) {
-    if (!device_failure(rc)) {
-        if (rc == MI355X_OK) {
-            b.fails = 0;
-            b.open_len = 0;
+    void record(int status, const char * route) {
+        if (status == MI355X_OK) {
+            streak_ = 0;
+            trips_ = 0;
+            return;
         }
-        return;
+        if (status == MI355X_E_ARG || status == MI355X_E_UNSUPPORTED) return;
+        failures++;
+        if (++streak_ < kTrip) return;
+        trips_++;
+        resting_ = rest_len();
+        logw("%s failed on the device %d times running (status %d); the CPU serves its next %ld "
+             "calls before the device is tried again\n", route, streak_, status, resting_);
     }
-    b.failures++;
-    if (++b.fails < 3) return;
-    const long OPEN0 = 64, OPEN_MAX = 4096;
-    b.open_len = b.open_len ? (b.open_len * 2 > OPEN_MAX ? OPEN_MAX : b.open_len * 2) : OPEN0;
-    b.skip = b.open_len;
-    logw("%s: %d consecutive device failures (last status %d): its CPU fallback runs directly for "
-         "the next %ld calls, then the route is retried once\n", route, b.fails, rc, b.skip);
-}
+
+    long attempts = 0, failures = 0, bypassed = 0;
+    int inject = 0;   // host-side fault injection for tests: the next `inject` attempts fail
+
+private:
+    long rest_len() const {
+        const int shift = std::min(kRestShift0 + trips_ - 1, kRestShiftMax);
+        return 1L << shift;
+    }
+    int streak_ = 0;    // device failures since the last success
+    int trips_ = 0;     // rests entered since the last success
+    long resting_ = 0;  // calls left in the current rest
+};
 
 // A grow-only device buffer.
 struct DevBuf {
@@ -262,8 +270,9 @@ struct ggml_backend_mi355x {
     long moe_resident = 0, moe_streamed = 0;
     std::unordered_set<std::string> moe_claimed;
     std::unordered_set<std::string> moe_counted;   // stacks whose experts were counted resident
+    std::unordered_set<std::string> moe_streamed_experts;   // "<stack key>/e<index>" run from an upload
 
-    Breaker brk_gemm, brk_fa, brk_moe;
+    RouteHealth brk_gemm, brk_fa, brk_moe;
 
     Stager stage;                        // pinned slots of the host <-> device copies
     std::unique_ptr<CopyPool> pool;      // n_threads copy workers, started with the device
@@ -646,9 +655,9 @@ int mul_mat_id_device(Ctx * c, mi355x_tensor * dst, bool & resident) {
 
 // Runs a device job under a breaker; on a device failure (or an open breaker) runs `fallback`.
 template <class Dev, class Fb>
-void guarded(Ctx * c, Breaker & brk, const char * route, Dev && dev, Fb && fallback) {
+void guarded(Ctx * c, RouteHealth & brk, const char * route, Dev && dev, Fb && fallback) {
     int rc = MI355X_E_DEVICE;
-    if (breaker_allow(brk)) {
+    if (brk.try_device()) {
         brk.attempts++;
         if (brk.inject > 0) {
             brk.inject--;
@@ -656,7 +665,7 @@ void guarded(Ctx * c, Breaker & brk, const char * route, Dev && dev, Fb && fallb
         } else {
             rc = dev();
         }
-        breaker_note(brk, rc, route);
+        brk.record(rc, route);
     }
     if (rc != MI355X_OK) {
         fallback();
@@ -778,7 +787,7 @@ MI355X_API void ggml_backend_mi355x_moe_stats(ggml_backend_mi355x_t c, long * n_
     if (n_streamed) *n_streamed = ggml_backend_is_mi355x(c) ? c->moe_streamed : 0;
 }
 
-static Breaker * breaker_of(ggml_backend_mi355x_t c, const char * g) {
+static RouteHealth * breaker_of(ggml_backend_mi355x_t c, const char * g) {
     if (!ggml_backend_is_mi355x(c) || !g) return nullptr;
     if (!strcmp(g, "gemm")) return &c->brk_gemm;
     if (!strcmp(g, "fa")) return &c->brk_fa;
@@ -788,14 +797,14 @@ static Breaker * breaker_of(ggml_backend_mi355x_t c, const char * g) {
 
 MI355X_API void ggml_backend_mi355x_route_stats(ggml_backend_mi355x_t c, const char * g, long * attempts,
                                                 long * failures, long * bypassed) {
-    Breaker * b = breaker_of(c, g);
+    RouteHealth * b = breaker_of(c, g);
     if (attempts) *attempts = b ? b->attempts : 0;
     if (failures) *failures = b ? b->failures : 0;
     if (bypassed) *bypassed = b ? b->bypassed : 0;
 }
 
 MI355X_API void ggml_backend_mi355x_inject_faults(ggml_backend_mi355x_t c, const char * g, int n) {
-    Breaker * b = breaker_of(c, g);
+    RouteHealth * b = breaker_of(c, g);
     if (b) b->inject = n < 0 ? 0 : n;
 }
 
@@ -891,23 +900,36 @@ static int graph_compute_nodes(ggml_backend_mi355x_t c, mi355x_tensor * const * 
                 const mi355x_tensor * as = node->src[0];
                 const mi355x_tensor * ids = node->src[2];
                 // an id outside [0, n_expert) is a malformed graph (ggml-rocket.cpp:6719)
+                std::vector<bool> routed((size_t)as->ne[2], false);
                 for (int64_t t = 0; t < ids->ne[1]; t++)
                     for (int64_t s = 0; s < ids->ne[0]; s++) {
                         const int32_t e = *(const int32_t *)((const char *)ids->data + t * ids->nb[1] + s * ids->nb[0]);
                         if (e < 0 || e >= as->ne[2]) return MI355X_STATUS_FAILED;
+                        routed[(size_t)e] = true;
                     }
                 const std::string key = weight_key(as);
                 if (!key.empty() && !c->moe_claimed.count(key) && moe_preflight_claim(key) == MOE_CLAIMED)
                     c->moe_claimed.insert(key);
                 bool resident = false;
                 bool ok = true;
-                guarded(c, c->brk_moe, "MUL_MAT_ID", [&] { return mul_mat_id_device(c, node, resident); },
+                bool on_device = false;
+                guarded(c, c->brk_moe, "MUL_MAT_ID",
+                        [&] {
+                            const int rc = mul_mat_id_device(c, node, resident);
+                            on_device = rc == MI355X_OK;
+                            return rc;
+                        },
                         [&] { ok = cpu_mul_mat_id(node); });
                 if (!ok) return MI355X_STATUS_FAILED;
-                if (resident) {
+                // distinct experts over the backend's life (ggml-rocket.h:39-57), device runs only:
+                // a resident stack is ingested whole, so all its experts count once; a streamed
+                // named stack counts each expert the ids routed to (an unnamed one has no identity)
+                if (on_device && resident) {
                     if (c->moe_counted.insert(key).second) c->moe_resident += as->ne[2];
-                } else {
-                    c->moe_streamed += as->ne[2];
+                } else if (on_device && !key.empty()) {
+                    for (size_t e = 0; e < routed.size(); e++)
+                        if (routed[e]) c->moe_streamed_experts.insert(key + "/e" + std::to_string(e));
+                    c->moe_streamed = (long)c->moe_streamed_experts.size();
                 }
                 c->routes["moe"]++;
                 break;

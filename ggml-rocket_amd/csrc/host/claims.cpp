@@ -11,11 +11,11 @@
 //   * FLASH_ATTN_EXT: head dims up to 256, and the strides the kernel reads.
 
 #include <atomic>
+#include <map>
 #include <mutex>
 #include <string.h>
 #include <string>
 #include <unordered_map>
-#include <unordered_set>
 
 #include <hip/hip_runtime.h>
 
@@ -42,235 +42,312 @@ bool prec_declines(const mi355x_tensor * op) {
     return false;
 }
 
-// ---- repacked-weight sources (ggml-rocket.cpp:6965-7047, API.md:280-314) ----------------------
+// ---- repacked-weight sources (the contract of ggml-rocket.cpp:6965-7047, API.md:280-314) ---
 // ggml-cpu's CPU_REPACK buffer holds a quantized weight in an interleaved layout no route here
 // reads. A host that keeps the original bytes (its mapped GGUF range) registers them for the
-// tensor; ops on it are then claimed and computed from those bytes, and the CPU keeps its
-// repacked copy for decode. The registry is process-wide, as placement has no backend handle.
-// An entry is keyed by the tensor's own data address (its place in the repack buffer) and is
-// used only while the tensor's name and byte size still match it, which catches a tensor struct
-// reused for another weight, not the same model reloaded into it: the host unregisters first.
+// tensor; ops on it are then claimed and computed from those bytes while the CPU keeps its
+// repacked copy for decode. Placement has no backend handle, so the table is process-wide.
+// A registration belongs to the tensor's place in the repack buffer and stands only while the
+// tensor there still has the registered name and byte size; a different weight put in that place
+// finds nothing (the same model reloaded into it must be unregistered first, as the host does).
 namespace {
-struct WSrc {
-    const void * src;
-    size_t nbytes;
-    std::string name;
-};
-std::mutex g_wsrc_mu;
-std::unordered_map<const void *, WSrc> g_wsrc;
-std::atomic<size_t> g_wsrc_count{0};
 
-bool is_view_op(int op) {
-    return op == MI355X_OP_VIEW || op == MI355X_OP_RESHAPE || op == MI355X_OP_PERMUTE || op == MI355X_OP_TRANSPOSE;
+class SourceTable {
+public:
+    void put(const mi355x_tensor * t, const void * bytes, size_t n) {
+        std::lock_guard<std::mutex> g(lock_);
+        const uintptr_t at = (uintptr_t)t->data;
+        if (!bytes) rows_.erase(at);
+        else rows_[at] = Row{bytes, n, std::string(t->name, strnlen(t->name, MI355X_MAX_NAME))};
+        count_.store(rows_.size(), std::memory_order_release);
+    }
+    // the original bytes for `base` (a tensor that owns its bytes), or nullptr
+    const char * find(const mi355x_tensor * base) const {
+        std::lock_guard<std::mutex> g(lock_);
+        const auto hit = rows_.find((uintptr_t)base->data);
+        if (hit == rows_.end()) return nullptr;
+        const Row & r = hit->second;
+        const bool same_weight = r.n == nbytes(base) && r.name.size() == strnlen(base->name, MI355X_MAX_NAME) &&
+                                 memcmp(r.name.data(), base->name, r.name.size()) == 0;
+        return same_weight ? (const char *)r.bytes : nullptr;
+    }
+    size_t count() const { return count_.load(std::memory_order_acquire); }
+
+private:
+    struct Row {
+        const void * bytes;
+        size_t n;
+        std::string name;
+    };
+    mutable std::mutex lock_;
+    std::map<uintptr_t, Row> rows_;
+    std::atomic<size_t> count_{0};
+};
+
+SourceTable & sources() {
+    static SourceTable table;
+    return table;
 }
 
-// the tensor a view reads, and the byte offset of the view in it
-const mi355x_tensor * view_base(const mi355x_tensor * t, size_t * offs) {
-    const mi355x_tensor * b = t;
-    while (is_view_op(b->op) && b->src[0]) b = b->src[0];
-    *offs = (b->data && t->data) ? (size_t)((const char *)t->data - (const char *)b->data) : 0;
-    return b;
+// A view op reads (part of) the bytes of the tensor it was made from.
+bool reads_through(int op) {
+    switch (op) {
+        case MI355X_OP_VIEW: case MI355X_OP_RESHAPE: case MI355X_OP_PERMUTE: case MI355X_OP_TRANSPOSE: return true;
+        default: return false;
+    }
+}
+
+// The tensor that owns t's bytes (t itself unless t is a view), and t's byte offset in it.
+const mi355x_tensor * owner_of(const mi355x_tensor * t, size_t & offset) {
+    const mi355x_tensor * o = t;
+    while (reads_through(o->op) && o->src[0] != nullptr) o = o->src[0];
+    offset = (o->data != nullptr && t->data != nullptr) ? (size_t)((const char *)t->data - (const char *)o->data) : 0;
+    return o;
 }
 
 }  // namespace
 
 bool tensor_needs_source(const mi355x_tensor * t) {
-    size_t offs;
-    const mi355x_tensor * b = view_base(t, &offs);
-    return b->buffer_kind == MI355X_BUF_REPACK || b->buffer_kind == MI355X_BUF_OTHER;
+    size_t offset = 0;
+    const int kind = owner_of(t, offset)->buffer_kind;
+    return kind == MI355X_BUF_REPACK || kind == MI355X_BUF_OTHER;
 }
 
 const void * tensor_source(const mi355x_tensor * t) {
-    if (g_wsrc_count.load(std::memory_order_acquire) == 0) return nullptr;
-    size_t offs;
-    const mi355x_tensor * b = view_base(t, &offs);
-    std::lock_guard<std::mutex> lk(g_wsrc_mu);
-    auto it = g_wsrc.find(b->data);
-    if (it == g_wsrc.end()) return nullptr;
-    if (it->second.nbytes != nbytes(b) || it->second.name != std::string(b->name, strnlen(b->name, MI355X_MAX_NAME)))
-        return nullptr;
-    if (offs + nbytes(t) > it->second.nbytes) return nullptr;
-    return (const char *)it->second.src + offs;
+    if (sources().count() == 0) return nullptr;
+    size_t offset = 0;
+    const mi355x_tensor * o = owner_of(t, offset);
+    const char * orig = sources().find(o);
+    if (!orig || offset + nbytes(t) > nbytes(o)) return nullptr;
+    return orig + offset;
 }
 
-size_t registered_sources() { return g_wsrc_count.load(std::memory_order_acquire); }
+size_t registered_sources() { return sources().count(); }
 
-// ---- weight identity ---------------------------------------------------------------------------
-// A sampled content fingerprint: sixteen 64-byte windows spread over the tensor (all of it when
-// smaller), mixed with the byte size and type. Changes when a weight's bytes are replaced. A
-// repacked weight is fingerprinted over its registered original bytes, so placement (data at the
-// repacked copy) and compute (data pointed at the original) agree on its key.
-static uint64_t fingerprint(const mi355x_tensor * t) {
-    const size_t n = nbytes(t);
-    const void * src = tensor_needs_source(t) ? tensor_source(t) : nullptr;
-    const unsigned char * p = (const unsigned char *)(src ? src : t->data);
-    uint64_t h = 0xcbf29ce484222325ULL ^ ((uint64_t)n * 0x9E3779B97F4A7C15ULL) ^ ((uint64_t)(uint32_t)t->type << 48);
-    auto mix = [&h](uint64_t x) {
-        h ^= x + 0x632BE59BD9B4E019ULL + (h << 6) + (h >> 2);
-        h *= 0x100000001B3ULL;
-    };
-    auto span = [&](size_t off, size_t len) {
-        size_t i = 0;
-        for (; i + 8 <= len; i += 8) {
-            uint64_t x;
-            memcpy(&x, p + off + i, 8);
-            mix(x);
+// ---- weight identity (the contract of ggml-rocket.cpp:4124-4222) -------------------------------
+// A weight is identified by its logical name and a sample of its bytes. The sample is sixteen
+// 64-byte windows at evenly spaced offsets from the first to the last byte (the whole tensor when
+// it holds no more than that), so replacing a weight's bytes changes its key. A repacked weight
+// is sampled from its registered original bytes: placement sees its data in the repack buffer,
+// compute sees the original, and both must produce one key.
+namespace {
+
+// 64-bit multiply-xorshift accumulation (a splitmix64-style finalizer per word)
+struct WindowHash {
+    uint64_t s;
+    explicit WindowHash(uint64_t seed) : s(seed) {}
+    void word(uint64_t w) {
+        s += w + 0x9E3779B97F4A7C15ULL;
+        uint64_t z = s;
+        z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ULL;
+        z = (z ^ (z >> 27)) * 0x94D049BB133111EBULL;
+        s = z ^ (z >> 31);
+    }
+    // `len` bytes; a short tail is zero-padded to a word and tagged with its length
+    void bytes(const unsigned char * p, size_t len) {
+        const size_t whole = len / 8;
+        for (size_t i = 0; i < whole; i++) {
+            uint64_t w;
+            memcpy(&w, p + 8 * i, 8);
+            word(w);
         }
-        for (; i < len; i++) mix(0x100u | p[off + i]);
-    };
-    const int NW = 16;
-    const size_t W = 64;
-    if (n <= (size_t)NW * W) span(0, n);
-    else for (int w = 0; w < NW; w++) span((n - W) / (NW - 1) * (size_t)w, W);
-    return h;
+        const size_t rest = len % 8;
+        if (rest) {
+            uint64_t w = 0;
+            memcpy(&w, p + 8 * whole, rest);
+            word(w ^ ((uint64_t)rest << 59));
+        }
+    }
+};
+
+uint64_t content_sample(const mi355x_tensor * t) {
+    const size_t n = nbytes(t);
+    const void * orig = tensor_needs_source(t) ? tensor_source(t) : nullptr;
+    const unsigned char * base = (const unsigned char *)(orig ? orig : t->data);
+    WindowHash h(((uint64_t)n << 8) ^ (uint64_t)(uint32_t)t->type);
+    constexpr size_t kWindows = 16, kWidth = 64;
+    if (n <= kWindows * kWidth) {
+        h.bytes(base, n);
+    } else {
+        for (size_t i = 0; i < kWindows; i++) h.bytes(base + i * (n - kWidth) / (kWindows - 1), kWidth);
+    }
+    return h.s;
 }
+
+bool all_digits(const char * p) {
+    if (*p == 0) return false;
+    for (; *p; p++)
+        if (*p < '0' || *p > '9') return false;
+    return true;
+}
+
+// The logical weight name. ggml-backend-sched names the input copies it makes for a backend
+// "<backend>#<name>#<index>"; only this backend's copies are mapped back to <name>, with the
+// index dropped when it survived the name-length limit. Other names are kept whole.
+std::string logical_name(const char * raw) {
+    static const char kMine[] = "MI355X#";
+    const size_t mine = sizeof kMine - 1;
+    if (strncmp(raw, kMine, mine) != 0 || raw[mine] == 0) return std::string(raw);
+    std::string name(raw + mine);
+    const size_t cut = name.find_last_of('#');
+    if (cut != std::string::npos && cut > 0 && all_digits(name.c_str() + cut + 1)) name.erase(cut);
+    return name;
+}
+
+// "leaf_<n>" / "node_<n>": ggml's names for unnamed tensors, positions in one graph, which
+// several graphs of one host reuse for different weights
+bool positional_name(const std::string & name) {
+    for (const char * p : {"leaf_", "node_"})
+        if (name.rfind(p, 0) == 0 && all_digits(name.c_str() + 5)) return true;
+    return false;
+}
+
+}  // namespace
 
 std::string weight_key(const mi355x_tensor * t) {
     if (!t || !t->name[0]) return std::string();
-    char name[MI355X_MAX_NAME + 1];
-    memcpy(name, t->name, MI355X_MAX_NAME);
-    name[MI355X_MAX_NAME] = 0;
-    // the scheduler's input-copy grammar "<backend>#<name>#<idx>", for this backend only
-    static const char PREFIX[] = "MI355X#";
-    const size_t plen = sizeof(PREFIX) - 1;
-    const bool copy = strncmp(name, PREFIX, plen) == 0 && name[plen];
-    std::string key(copy ? name + plen : name);
-    if (copy) {
-        const size_t h = key.rfind('#');
-        if (h != std::string::npos && h > 0 && h + 1 < key.size() &&
-            key.find_first_not_of("0123456789", h + 1) == std::string::npos)
-            key.resize(h);
-    }
-    // ggml auto-names ("leaf_<n>", "node_<n>") are graph positions, not weight identities
-    for (const char * pre : {"leaf_", "node_"}) {
-        if (key.compare(0, 5, pre) == 0 && key.size() > 5 &&
-            key.find_first_not_of("0123456789", 5) == std::string::npos)
-            return std::string();
-    }
+    char raw[MI355X_MAX_NAME + 1];
+    memcpy(raw, t->name, MI355X_MAX_NAME);
+    raw[MI355X_MAX_NAME] = 0;
+    std::string key = logical_name(raw);
+    if (positional_name(key)) return std::string();
     if (t->data) {
-        char id[24];
-        snprintf(id, sizeof id, "@%016llx", (unsigned long long)fingerprint(t));
-        key += id;
+        // "@" and the sample as 16 hex digits
+        const uint64_t v = content_sample(t);
+        static const char kHex[] = "0123456789abcdef";
+        key.push_back('@');
+        for (int sh = 60; sh >= 0; sh -= 4) key.push_back(kHex[(v >> sh) & 15]);
     }
     return key;
 }
 
-// ---- MoE residency ledger ------------------------------------------------------------------
-// A stack (one expert weight tensor) is admitted whole or not at all, before its first ingest:
-// partial residency is what the pre-flight exists to avoid (ggml-rocket.cpp:6198-6289). The
-// charge is the stack's HBM copy (its packed bytes, equal to the GGUF bytes), plus, under
-// MOE_CHARGE_ALL_SOURCE=1, each distinct mapped source buffer once. The budget is
-// MOE_CACHE_MB (0 = unlimited), by default the device's HBM less an 8 GiB reserve. The ledger is
-// process-wide and cleared when the last backend instance is freed.
+// ---- expert-stack ledger (the contract of ggml-rocket.cpp:5983-6375, without the NPU's IOVA) ---
+// Placement decides per expert stack, once, whether the whole stack fits in HBM: a stack that
+// would only partly fit is declined rather than half ingested. The decision is remembered so a
+// stack never moves between devices from one micro-batch to the next. Each live backend holds
+// its own HBM copy of a placed stack: the placement decision reserves one spare copy, the first
+// backend that runs the stack takes it, and a further backend needs a new copy charged against
+// the budget (or streams the stack when it does not fit). Copies are returned when their backend
+// is freed; the whole ledger is forgotten once no backend is live. The budget is MOE_CACHE_MB
+// (0 = unlimited), by default the device's HBM less an 8 GiB reserve. Under
+// MOE_CHARGE_ALL_SOURCE=1 each distinct host weight buffer is also charged once, in full.
 namespace {
-struct Stack {
-    bool admitted = false;
-    size_t bytes = 0;
-    int copies = 0;
-    int claimed = 0;
-};
-struct Ledger {
-    std::mutex mu;
-    bool frozen = false;
-    size_t budget = 0;    // 0 = unlimited
-    size_t used = 0;
-    size_t src_used = 0;
-    bool all_src = false;
-    int live = 0;
-    std::unordered_set<const void *> src_bufs;
-    std::unordered_map<std::string, Stack> stacks;
-};
-Ledger g_ledger;
 
-size_t default_moe_budget() {
-    size_t fr = 0, tot = 0;
-    int n = 0;
-    if (hipGetDeviceCount(&n) == hipSuccess && n > 0 && hipMemGetInfo(&fr, &tot) == hipSuccess && tot) {
-        const size_t reserve = (size_t)8 << 30;
-        return tot > reserve ? tot - reserve : tot / 2;
+class ExpertLedger {
+public:
+    bool place(const std::string & key, size_t copy_bytes, const void * buf, size_t buf_bytes) {
+        if (key.empty() || copy_bytes == 0) return false;
+        std::lock_guard<std::mutex> g(lock_);
+        const auto known = stacks_.find(key);
+        if (known != stacks_.end()) return known->second.placed;
+        resolve_budget();
+        if (charge_buffers_ && buf != nullptr && buf_bytes != 0) buffers_.emplace(buf, buf_bytes);   // once per buffer
+        Stack s;
+        s.copy_bytes = copy_bytes;
+        s.placed = fits(copy_bytes);
+        s.spare = s.placed ? 1 : 0;
+        stacks_.emplace(key, s);
+        return s.placed;
     }
-    (void)hipGetLastError();
-    return (size_t)4096 << 20;   // no device to ask: a conservative figure
+    bool lookup(const std::string & key, bool & placed) {
+        if (key.empty()) return false;
+        std::lock_guard<std::mutex> g(lock_);
+        const auto known = stacks_.find(key);
+        if (known == stacks_.end()) return false;
+        placed = known->second.placed;
+        return true;
+    }
+    int take(const std::string & key) {
+        if (key.empty()) return MOE_UNDECIDED;
+        std::lock_guard<std::mutex> g(lock_);
+        const auto known = stacks_.find(key);
+        if (known == stacks_.end() || !known->second.placed) return MOE_UNDECIDED;
+        Stack & s = known->second;
+        if (s.spare > 0) {
+            s.spare--;
+        } else {
+            if (!fits(s.copy_bytes)) return MOE_REFUSED;
+        }
+        s.held++;
+        return MOE_CLAIMED;
+    }
+    void give_back(const std::string & key) {
+        std::lock_guard<std::mutex> g(lock_);
+        const auto known = stacks_.find(key);
+        if (known != stacks_.end() && known->second.held > 0) known->second.held--;
+    }
+    void attach() {
+        std::lock_guard<std::mutex> g(lock_);
+        if (live_++ == 0) {
+            stacks_.clear();
+            buffers_.clear();
+            budget_resolved_ = false;
+        }
+    }
+    void detach() {
+        std::lock_guard<std::mutex> g(lock_);
+        if (live_ > 0) live_--;
+    }
+
+private:
+    struct Stack {
+        bool placed = false;
+        size_t copy_bytes = 0;
+        int spare = 0;   // charged copies no backend has taken (the placement's reservation)
+        int held = 0;    // copies live backends hold
+    };
+    // bytes charged now: every spare and held copy, and the charged host buffers
+    size_t charged() const {
+        size_t sum = 0;
+        for (const auto & kv : stacks_) sum += (size_t)(kv.second.spare + kv.second.held) * kv.second.copy_bytes;
+        for (const auto & kv : buffers_) sum += kv.second;
+        return sum;
+    }
+    bool fits(size_t more) const { return budget_ == 0 || charged() + more <= budget_; }
+    void resolve_budget() {
+        if (budget_resolved_) return;
+        budget_resolved_ = true;
+        size_t b = 0;
+        const char * text = knob_env("MOE_CACHE_MB");
+        budget_ = (text && parse_mb(text, &b)) ? b : hbm_less_reserve();
+        charge_buffers_ = knob_int("MOE_CHARGE_ALL_SOURCE", 0) != 0;
+    }
+    static size_t hbm_less_reserve() {
+        const size_t reserve = (size_t)8 << 30;
+        size_t free_b = 0, total_b = 0;
+        int devices = 0;
+        if (hipGetDeviceCount(&devices) != hipSuccess || devices <= 0 || hipMemGetInfo(&free_b, &total_b) != hipSuccess ||
+            total_b == 0) {
+            (void)hipGetLastError();
+            return (size_t)4 << 30;   // no device to ask: a conservative figure
+        }
+        return total_b > reserve ? total_b - reserve : total_b / 2;
+    }
+
+    std::mutex lock_;
+    std::unordered_map<std::string, Stack> stacks_;
+    std::map<const void *, size_t> buffers_;   // host weight buffers charged under MOE_CHARGE_ALL_SOURCE
+    size_t budget_ = 0;                        // 0 = unlimited
+    bool budget_resolved_ = false;
+    bool charge_buffers_ = false;
+    int live_ = 0;
+};
+
+ExpertLedger & ledger() {
+    static ExpertLedger l;
+    return l;
 }
+
 }  // namespace
 
 bool moe_preflight_admit(const std::string & key, size_t stack_bytes, const void * src_buf, size_t src_buf_bytes) {
-    if (key.empty() || stack_bytes == 0) return false;
-    std::lock_guard<std::mutex> lk(g_ledger.mu);
-    auto it = g_ledger.stacks.find(key);
-    if (it != g_ledger.stacks.end()) return it->second.admitted;
-    if (!g_ledger.frozen) {
-        size_t b = 0;
-        const char * e = knob_env("MOE_CACHE_MB");
-        g_ledger.budget = (e && parse_mb(e, &b)) ? b : default_moe_budget();
-        g_ledger.all_src = knob_int("MOE_CHARGE_ALL_SOURCE", 0) != 0;
-        g_ledger.frozen = true;
-    }
-    if (g_ledger.all_src && src_buf && src_buf_bytes && g_ledger.src_bufs.insert(src_buf).second)
-        g_ledger.src_used += src_buf_bytes;
-    Stack st;
-    const bool fits = !g_ledger.budget || g_ledger.used + g_ledger.src_used + stack_bytes <= g_ledger.budget;
-    if (fits) {
-        st.admitted = true;
-        st.bytes = stack_bytes;
-        st.copies = 1;
-        g_ledger.used += stack_bytes;
-    }
-    g_ledger.stacks[key] = st;
-    return fits;
+    return ledger().place(key, stack_bytes, src_buf, src_buf_bytes);
 }
-
-bool moe_preflight_decided(const std::string & key, bool * admitted) {
-    if (key.empty()) return false;
-    std::lock_guard<std::mutex> lk(g_ledger.mu);
-    auto it = g_ledger.stacks.find(key);
-    if (it == g_ledger.stacks.end()) return false;
-    *admitted = it->second.admitted;
-    return true;
-}
-
-int moe_preflight_claim(const std::string & key) {
-    if (key.empty()) return MOE_UNDECIDED;
-    std::lock_guard<std::mutex> lk(g_ledger.mu);
-    auto it = g_ledger.stacks.find(key);
-    if (it == g_ledger.stacks.end() || !it->second.admitted) return MOE_UNDECIDED;
-    Stack & st = it->second;
-    if (st.claimed < st.copies) {
-        st.claimed++;
-        return MOE_CLAIMED;
-    }
-    // a second live backend wants its own copy: charge it if it fits
-    if (g_ledger.budget && g_ledger.used + g_ledger.src_used + st.bytes > g_ledger.budget) return MOE_REFUSED;
-    g_ledger.used += st.bytes;
-    st.copies++;
-    st.claimed++;
-    return MOE_CLAIMED;
-}
-
-void moe_preflight_release(const std::string & key) {
-    std::lock_guard<std::mutex> lk(g_ledger.mu);
-    auto it = g_ledger.stacks.find(key);
-    if (it == g_ledger.stacks.end() || it->second.claimed <= 0) return;
-    it->second.claimed--;
-    it->second.copies--;
-    g_ledger.used -= it->second.bytes;
-}
-
-void moe_preflight_open() {
-    std::lock_guard<std::mutex> lk(g_ledger.mu);
-    if (g_ledger.live == 0) {
-        g_ledger.stacks.clear();
-        g_ledger.src_bufs.clear();
-        g_ledger.used = g_ledger.src_used = 0;
-        g_ledger.frozen = false;
-    }
-    g_ledger.live++;
-}
-
-void moe_preflight_close() {
-    std::lock_guard<std::mutex> lk(g_ledger.mu);
-    if (g_ledger.live > 0) g_ledger.live--;
-}
+bool moe_preflight_decided(const std::string & key, bool * admitted) { return ledger().lookup(key, *admitted); }
+int moe_preflight_claim(const std::string & key) { return ledger().take(key); }
+void moe_preflight_release(const std::string & key) { ledger().give_back(key); }
+void moe_preflight_open() { ledger().attach(); }
+void moe_preflight_close() { ledger().detach(); }
 
 // ---- claim rules -----------------------------------------------------------------------------
 
@@ -406,11 +483,7 @@ MI355X_API bool ggml_backend_mi355x_supports_buft(int buffer_kind) {
 }
 
 MI355X_API void ggml_backend_mi355x_register_weight_source(const mi355x_tensor * t, const void * data, size_t nbytes) {
-    if (!t || !t->data) return;
-    std::lock_guard<std::mutex> lk(g_wsrc_mu);
-    if (!data) g_wsrc.erase(t->data);
-    else g_wsrc[t->data] = WSrc{data, nbytes, std::string(t->name, strnlen(t->name, MI355X_MAX_NAME))};
-    g_wsrc_count.store(g_wsrc.size(), std::memory_order_release);
+    if (t && t->data) sources().put(t, data, nbytes);
 }
 
 MI355X_API int ggml_backend_mi355x_weight_key(const mi355x_tensor * t, char * out, int cap) {

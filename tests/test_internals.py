@@ -1,10 +1,14 @@
 """Host-layer internals (CPU): the MB parser, weight identity, the circuit breaker, the fallback
 counters and instance lifecycle -- test-rocket-internals.cpp's cases on this backend's API."""
+import os
+
 import numpy as np
 import pytest
 
 import ggml_mi355x as mx
 from oracle import oracle as O
+
+HERE = os.path.dirname(os.path.abspath(__file__))
 
 
 @pytest.mark.parametrize("text,ok,want", [
@@ -130,3 +134,24 @@ def test_moe_bad_id_fails_graph():
     g.set(ids, idv)
     assert be.compute([g.mul_mat_id(a, b, ids)]) == mx.STATUS_FAILED
     be.free()
+
+
+def test_expert_ledger_across_backends(tmp_path):
+    """test-rocket-internals.cpp:155-215: the expert-stack ledger with several live backends
+    (placement's spare copy, a second backend's own copy, a refused copy, copies returned on
+    free, the ledger forgotten with the last backend). The ledger has no ABI entry, so a small
+    C++ program links the host sources and calls it directly."""
+    import subprocess
+    root = os.path.dirname(HERE)
+    host = os.path.join(root, "ggml-rocket_amd", "csrc", "host")
+    exe = str(tmp_path / "ledger_test")
+    cmd = ["g++", "-std=c++17", "-O1", "-D__HIP_PLATFORM_AMD__", "-I/opt/rocm/include",
+           os.path.join(HERE, "cpp", "ledger_test.cpp"), os.path.join(host, "claims.cpp"),
+           os.path.join(host, "knobs.cpp"), "-L/opt/rocm/lib", "-lamdhip64", "-Wl,-rpath,/opt/rocm/lib",
+           "-o", exe]
+    subprocess.run(cmd, check=True, capture_output=True)
+    env = {k: v for k, v in os.environ.items() if not k.startswith(("MI355X_", "ROCKET_"))}
+    env["HIP_VISIBLE_DEVICES"] = ""
+    r = subprocess.run([exe], capture_output=True, text=True, env=env, timeout=120)
+    print(r.stdout)
+    assert r.returncode == 0, r.stdout + r.stderr
