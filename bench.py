@@ -5,11 +5,14 @@ Workload (metric "prefill tok/s (8B-shape Q4_K, 2048 tok)"): a Llama-3-8B-shaped
 (32 layers, d 4096, FFN 14336, 32 query / 8 KV heads, head dim 128) with random-init Q4_K
 weights (quantized from N(0, 0.02); every layer distinct), prefilling 2048 tokens in 4
 micro-batches of 512. One step runs, per micro-batch and layer, exactly the ops this backend
-claims in such a prefill: the fused Q/K/V projection group, FLASH_ATTN_EXT over the causal KV
-prefix (n_kv = 512, 1024, 1536, 2048; the first is claimed when FLASH_ATTN_MIN_KV <= 512, the
-reference's default being 1024), the output projection, the fused gate/up group and the down
-projection. Ops the backend never claims (norms, RoPE, SiLU-mul, residual adds, the
-last-token lm_head at M=1) are not in the step. Inputs are resident in HBM when timing starts.
+claims in such a prefill under its default knobs: the fused Q/K/V projection group,
+FLASH_ATTN_EXT over the causal KV prefix where n_kv >= FLASH_ATTN_MIN_KV (1024: micro-batches 2-4,
+n_kv 1024 / 1536 / 2048; the first micro-batch's n_kv 512 attention is declined and runs on the
+host's CPU backend), the output projection, the fused gate/up group and the down projection.
+Ops the backend never claims (norms, RoPE, SiLU-mul, residual adds, the last-token lm_head at
+M=1) are not in the step, so `value` is the rate of the backend's share of the prefill with its
+inputs resident in HBM, not an end-to-end prefill rate; the rate through the plugin boundary with
+host buffers (PCIe-inclusive) is reported beside it under "host_path".
 
 Routes: "prepacked-q" (default; the reference's ROCKET_QUANT_RESIDENT route): each Q4_K weight
 is decoded once to an fp16 HBM copy and the GEMMs read fp16. "mt": the GEMMs read the Q4_K
@@ -33,12 +36,33 @@ sys.path.insert(0, os.path.join(ROOT, "ggml-rocket_amd"))
 METRIC = "prefill tok/s (8B-shape Q4_K, 2048 tok); MUL_MAT/FA TFLOP/s vs MFMA peak"
 PEAK_F16_TFLOPS = 2500.0
 PEAK_HBM_GBS = 8000.0
-# HBM bytes per GEMM launch, mean over a layer's four launches (qkv, o, gate/up, down) at M = 512
-# on the fp16-resident route: rocprofv3 FETCH_SIZE and WRITE_SIZE of `bench.py --pmc-probe`, each
-# scaled by what the counter reads for a plain 1 GiB device copy (x2.000 and x1.000). Hardware
-# counters cannot be read inside the timed run, so the figure is the last measurement of this
-# kernel (profiles/prefill_8b_hbm_traffic_pmc.md) and must be re-measured when the kernel changes.
-GEMM_TRAFFIC_BYTES = {"prepacked-q": 187.9e6, "mt": None}
+# HBM bytes per GEMM launch (mean of a layer's four launches at M = 512, fp16-resident route),
+# from rocprofv3 FETCH_SIZE / WRITE_SIZE runs of `bench.py --pmc-probe` scaled by a plain copy's
+# reading. Counters cannot be read inside the timed run, so the figure comes from the committed
+# profile, which records the SHA-256 of the GEMM source it was measured on: when the source has
+# changed since, the figure is stale and `traffic` is reported as null.
+TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "prefill_8b_hbm_traffic_pmc.md")
+GEMM_SOURCE = os.path.join(ROOT, "ggml-rocket_amd", "csrc", "mx_gemm.hip")
+
+
+def gemm_traffic(route):
+    """(bytes per GEMM launch, provenance) from the traffic profile, or (None, reason)."""
+    import hashlib
+    import re
+    if route != "prepacked-q":
+        return None, "not measured for this route"
+    try:
+        text = open(TRAFFIC_PROFILE).read()
+        src = hashlib.sha256(open(GEMM_SOURCE, "rb").read()).hexdigest()
+    except OSError as exc:
+        return None, f"unavailable ({exc.__class__.__name__})"
+    m = re.search(r"traffic_bytes_per_gemm_launch:\s*([0-9.eE+]+)\s+mx_gemm\.hip sha256:\s*([0-9a-f]{64})", text)
+    if not m:
+        return None, "no machine-readable line in the profile"
+    if m.group(2) != src:
+        return None, "stale: mx_gemm.hip changed since the profile was measured"
+    return float(m.group(1)), "profiles/prefill_8b_hbm_traffic_pmc.md (source hash matches)"
+
 
 L_LAYERS, D_MODEL, FFN, NH, NKV, HD = 32, 4096, 14336, 32, 8, 128
 TOKENS, UBATCH = 2048, 512
@@ -85,7 +109,14 @@ def parse():
     p.add_argument("--route", choices=["prepacked-q", "mt"], default="prepacked-q")
     p.add_argument("--layers", type=int, default=L_LAYERS)
     p.add_argument("--no-cpu-baseline", action="store_true")
-    p.add_argument("--cpu-threads", type=int, default=0)
+    p.add_argument("--cpu-threads", type=int, default=0,
+                   help="threads of the CPU baseline (default: OMP_NUM_THREADS, else every core this "
+                        "process may run on)")
+    p.add_argument("--fa-min-kv", type=int, default=1024,
+                   help="FLASH_ATTN_EXT runs in the step where n_kv >= this (the backend's default claim)")
+    p.add_argument("--quick", action="store_true",
+                   help="only the step and its roofline: no CPU baseline, single-op configurations "
+                        "or host-path run")
     p.add_argument("--host-path", action="store_true",
                    help="run the prefill through graph_compute with host tensors (the plugin "
                         "boundary, PCIe-inclusive) and print that rate instead")
@@ -104,12 +135,13 @@ def parse():
 
 
 class Prefill:
-    def __init__(self, route, n_layers):
+    def __init__(self, route, n_layers, fa_min_kv=1024):
         import numpy as np
         import torch
         import ggml_mi355x as mx
         self.mx, self.torch, self.np = mx, torch, np
         self.route = route
+        self.fa_min_kv = fa_min_kv
         self.wt = mx.F16_T if route == "prepacked-q" else mx.Q4_K
         dev = "cuda"
         t0 = time.time()
@@ -219,7 +251,8 @@ class Prefill:
                 self._gemm(D_MODEL, [(lw["q"], sh["q"][0], self.qo), (lw["k"], sh["k"][0], self.ko),
                                      (lw["v"], sh["v"][0], self.vo)],
                            2.0 * M * D_MODEL * (D_MODEL + 2 * NKV * HD))
-                self._fa(u)
+                if UBATCH * (u + 1) >= self.fa_min_kv:
+                    self._fa(u)
                 self._pack(self.attn, D_MODEL)
                 self._gemm(D_MODEL, [(lw["o"], D_MODEL, self.oo)], 2.0 * M * D_MODEL * D_MODEL)
                 self._pack(self.x, D_MODEL)
@@ -239,14 +272,48 @@ def gemm_weight_bytes(route):
     return n * per_w
 
 
+def host_cpu():
+    """CPU model, logical and physical core counts of this host, and the cores this process may
+    run on (the box's share of the host)."""
+    model, cores = "unknown", set()
+    phys = core = None
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                k, _, v = line.partition(":")
+                k, v = k.strip(), v.strip()
+                if k == "model name" and model == "unknown":
+                    model = v
+                elif k == "physical id":
+                    phys = v
+                elif k == "core id":
+                    core = v
+                elif not k and phys is not None and core is not None:
+                    cores.add((phys, core))
+                    phys = core = None
+    except OSError:
+        pass
+    if phys is not None and core is not None:
+        cores.add((phys, core))
+    try:
+        allowed = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        allowed = os.cpu_count() or 1
+    return {"model": model, "logical_cores": os.cpu_count(), "physical_cores": len(cores) or None,
+            "cores_allowed": allowed}
+
+
 def cpu_baseline(prefill, threads):
-    """The oracle (fp64 GEMM from the Q4_K payload, double attention) on a bounded sample of the
-    same workload: layer 0, S tokens of the last micro-batch (n_kv 2048), all seven projections
-    and the attention of those tokens; tokens/s = S / (sample time * 32 layers)."""
+    """The oracle (fp64 GEMM from the Q4_K payload, double attention; OpenMP) on a bounded sample
+    of the same workload: layer 0, S tokens of the last micro-batch (n_kv 2048), all seven
+    projections and the attention of those tokens. One warm-up pass, then at least 5 timed
+    passes (until ~10 s, at most ~30 s); tokens/s = S / (median pass time * 32 layers)."""
     import numpy as np
     from oracle import oracle as O
     O.lib()
-    nt = threads or min(16, os.cpu_count() or 1)
+    cpu = host_cpu()
+    env_threads = int(os.environ.get("OMP_NUM_THREADS", "0") or 0)
+    nt = threads or env_threads or cpu["cores_allowed"]
     S = 128
     X = O.fill_normal((S, D_MODEL), 5)
     Xf = O.fill_normal((S, FFN), 6)
@@ -255,22 +322,29 @@ def cpu_baseline(prefill, threads):
     V16 = O.f32_to_f16_bits(O.fill_normal((NKV, TOKENS, HD), 9))
     t = np.arange(S)[:, None] + (TOKENS - S)
     M16 = O.f32_to_f16_bits(np.where(np.arange(TOKENS)[None, :] > t, -np.inf, 0.0).astype(np.float32))
-    O.mul_mat(O.Q4_K, prefill.host_q4["k"], X, NKV * HD, D_MODEL, nthreads=nt)   # warm
-    reps, t0 = 0, time.time()
-    while True:   # repeat the sample until about 10 s of CPU work (at most 30 s)
+
+    def one_pass():
+        t0 = time.perf_counter()
         for name, (N, K) in prefill.shapes.items():
             O.mul_mat(O.Q4_K, prefill.host_q4[name], Xf if K == FFN else X, N, K, nthreads=nt)
         O.flash_attn(Qh, K16, V16, M16, 1.0 / math.sqrt(HD), nthreads=nt)
-        reps += 1
-        el = time.time() - t0
-        if el >= 10.0 or el * (reps + 1) / reps > 30.0:
+        return time.perf_counter() - t0
+
+    one_pass()   # warm-up
+    runs, t0 = [], time.perf_counter()
+    while len(runs) < 5 or (time.perf_counter() - t0 < 10.0 and len(runs) < 64):
+        runs.append(one_pass())
+        if len(runs) >= 5 and time.perf_counter() - t0 > 30.0:
             break
-    dt = (time.time() - t0) / reps
-    return {"value": S / (dt * L_LAYERS), "unit": "tok/s", "cores": nt, "kind": "port",
-            "sample": f"CPU oracle restatement (not ggml-cpu): layer 0 of the workload, {S} tokens "
-                      f"of the last 512-token micro-batch (n_kv 2048): 7 Q4_K projections as fp64 "
-                      f"GEMM + double attention, {dt:.2f} s per pass (mean of {reps}), "
-                      f"scaled x{L_LAYERS} layers"}
+    dt = float(np.median(runs))
+    return {"value": round(S / (dt * L_LAYERS), 2), "unit": "tok/s", "cores": nt, "kind": "port",
+            "cpu_model": cpu["model"], "logical_cores": cpu["logical_cores"],
+            "physical_cores": cpu["physical_cores"], "cores_allowed": cpu["cores_allowed"],
+            "threads": nt, "runs": len(runs), "median_pass_s": round(dt, 4),
+            "sample": f"CPU oracle restatement (not ggml-cpu, which is absent here): layer 0 of the "
+                      f"workload, {S} tokens of the last 512-token micro-batch (n_kv 2048): the 7 Q4_K "
+                      f"projections as fp64 GEMM + double attention, OpenMP on {nt} threads; warm "
+                      f"median of {len(runs)} passes, scaled x{L_LAYERS} layers"}
 
 
 def time_ops(pf, reps=32):
@@ -297,7 +371,8 @@ def time_ops(pf, reps=32):
          lambda i: pf._gemm(FFN, [(lw(i)["down"], D_MODEL, pf.do)], 0.0)),
     ]
     for u in range(TOKENS // UBATCH):
-        ops.append(("fa", 4.0 * NH * UBATCH * UBATCH * (u + 1) * HD, L_LAYERS, (lambda i, uu=u: pf._fa(uu))))
+        kind = "fa" if UBATCH * (u + 1) >= pf.fa_min_kv else "fa-declined"
+        ops.append((kind, 4.0 * NH * UBATCH * UBATCH * (u + 1) * HD, L_LAYERS, (lambda i, uu=u: pf._fa(uu))))
     pf.reset_counters(False)
     out = []
     for kind, flops, per_step, fn in ops:
@@ -371,7 +446,6 @@ def host_path(args):
     weight resident. Prints one JSON line with the PCIe-inclusive rate."""
     import ctypes
     import numpy as np
-    os.environ.setdefault("MI355X_FLASH_ATTN_MIN_KV", str(UBATCH))   # claim every micro-batch's FA
     import ggml_mi355x as mx
     be = mx.Backend()
     be.set_quant_resident(1)
@@ -409,6 +483,7 @@ def host_path(args):
         masks.append(g._new(mx.F16, [n_kv, T], data=m.reshape(-1)))
     bufs = {n: f32(N, T) for n, (N, _) in shapes.items()}
     bufs["attn"] = f32(HD, NH, T)
+    attn_cpu = g._new(mx.F32, [D_MODEL, T], data=rng.standard_normal(D_MODEL * T).astype(np.float32))
 
     def groups(li, u):
         """The graph_compute calls of layer li, micro-batch u."""
@@ -423,8 +498,10 @@ def host_path(args):
         fa = g._new(mx.F32, [HD, NH, T], op=mx.OP_FLASH_ATTN_EXT, srcs=(qv, kv, vv, masks[u]), data=bufs["attn"])
         ctypes.memmove(ctypes.addressof(fa.op_params), (ctypes.c_float * 3)(1.0 / math.sqrt(HD), 0.0, 0.0), 12)
         fa2d = g.permute_view(fa, [D_MODEL, T, 1, 1], [4, D_MODEL * 4, D_MODEL * 4 * T, D_MODEL * 4 * T])
-        o = mm("o", fa2d)
-        return [[q, k, v], [fa, fa2d, o], [mm("gate", x), mm("up", x)], [mm("down", act)]]
+        # the attention is the backend's where it is claimed (n_kv >= FLASH_ATTN_MIN_KV); the
+        # declined one is the host CPU's, and O then reads its result from host memory
+        attn = [fa, fa2d, mm("o", fa2d)] if n_kv >= args.fa_min_kv else [mm("o", attn_cpu)]
+        return [[q, k, v], attn, [mm("gate", x), mm("up", x)], [mm("down", act)]]
 
     calls = [grp for u in range(TOKENS // T) for li in range(L) for grp in groups(li, u)]
 
@@ -441,6 +518,8 @@ def host_path(args):
     run()
     sec = time.time() - t0
     fb = be.cpu_fallbacks()
+    routes = {r: be.route_ops(r) for r in ("prepacked-q", "fused-resident", "fa", "mt", "fused")}
+    be.free()
     out = {"metric": "prefill tok/s through graph_compute (host buffers, PCIe-inclusive)",
            "value": round(TOKENS / sec, 1), "unit": "tok/s", "n_gpus": 1, "ms_per_prefill": round(sec * 1e3, 1),
            "higher_is_better": True, "dtype": "f16", "data": "synthetic host tensors",
@@ -448,8 +527,10 @@ def host_path(args):
                                   f"of {T}: {len(calls) // (TOKENS // T)} graph_compute calls per micro-batch",
                       "layers": L, "route": "prepacked-q (QUANT_RESIDENT)"},
            "first_pass_s": round(first_s, 2), "host_setup_s": round(setup_s, 1), "cpu_fallbacks": fb,
-           "routes": {r: be.route_ops(r) for r in ("prepacked-q", "fused-resident", "fa")}}
-    print(json.dumps(out), flush=True)
+           "routes": routes,
+           "scope": "the backend's ops only: FLASH_ATTN_EXT at n_kv < FLASH_ATTN_MIN_KV and every op "
+                    "the backend does not claim run on the host CPU and are not timed"}
+    return out
 
 
 def graph_time_us(fn_of_i, n_calls, reps=3):
@@ -496,7 +577,7 @@ def synth_blocks(wtype, N, K, seed):
     return blk.reshape(-1)
 
 
-def configs_bench(args):
+def configs_bench(args, subset=False):
     """The single-op configurations, each through the C ABI entry the backend uses for it and
     against the roofline that bounds it (arithmetic intensity against the 2.5 PFLOP/s / 8 TB/s
     ridge of ~312 FLOP/byte). MUL_MAT: mi355x_mul_mat (activation pack + GEMM) on an HBM-resident
@@ -540,9 +621,12 @@ def configs_bench(args):
     W = (np.random.default_rng(0x5EED0000 + 16).standard_normal((8192, 2048), dtype=np.float32) * 0.02)
     mul_mat_case("MUL_MAT F16 N=8192 K=2048", mx.F16, mx.F16_T, W.astype(np.float16).view(np.uint16),
                  8192, 2048, [512])
-    # quantized sweep, decoded inside the GEMM (the per-call route)
+    # quantized sweep, decoded inside the GEMM (the per-call route); the default bench line
+    # carries one shape of it (Q4_K, K 3072, N 8192)
     for ti, (wt, tn) in enumerate(((mx.Q8_0, "Q8_0"), (mx.Q4_K, "Q4_K"), (mx.Q6_K, "Q6_K"))):
         for si, (K, N) in enumerate(((3072, 3072), (3072, 8192), (8192, 3072))):
+            if subset and (wt, K, N) != (mx.Q4_K, 3072, 8192):
+                continue
             P = synth_blocks(wt, N, K, 0x5EED0000 + 32 + 4 * ti + si)
             mul_mat_case(f"MUL_MAT {tn} N={N} K={K}", wt, wt, P, N, K, [32, 128, 512, 2048])
     # FLASH_ATTN_EXT prefill: 32 query / 8 KV heads, d 128, 512 queries, causal
@@ -562,6 +646,10 @@ def configs_bench(args):
         record(f"FLASH_ATTN_EXT n_kv={n_kv}", us, 4.0 * H * T * n_kv * D,
                T * H * D * 4 + 2 * HK * n_kv * D * 2 + T * n_kv * 2 + T * H * D * 4,
                {"tflops_causal_visible": round(visible / us / 1e6, 1)})
+        del q, kc, vc, m, out, wsp
+    torch.cuda.empty_cache()
+    if subset:
+        return cases
     print(json.dumps({
         "metric": "single-op configurations vs their rooflines (MI355X peaks: 2.5 PFLOP/s fp16, 8 TB/s)",
         "n_gpus": 1, "dtype": "f16", "data": "synthetic (N(0,0.02) / random-code weights, N(0,1) activations)",
@@ -631,7 +719,7 @@ def moe_bench(args):
         del copies, X, out, ws, g
         torch.cuda.empty_cache()
     gbs = tot_bytes / tot_us / 1e3
-    print(json.dumps({
+    return {
         "metric": "MUL_MAT_ID expert GEMM GB/s (128 experts, top-8, 512 tok, d 2048, FFN 768, Q4_K)",
         "value": round(gbs, 1), "unit": "GB/s", "n_gpus": 1, "higher_is_better": True,
         "dtype": "f16", "data": "synthetic (Q4_K experts from N(0,0.02), N(0,1) activations and router logits)",
@@ -640,7 +728,7 @@ def moe_bench(args):
         "ops": ops,
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                      "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": None},
-    }))
+    }
 
 
 def main():
@@ -655,15 +743,15 @@ def main():
         pmc_probe(Prefill(args.route, 1))
         return
     if args.moe:
-        moe_bench(args)
+        print(json.dumps(moe_bench(args)), flush=True)
         return
     if args.configs:
         configs_bench(args)
         return
     if args.host_path:
-        host_path(args)
+        print(json.dumps(host_path(args)), flush=True)
         return
-    pf = Prefill(args.route, args.layers)
+    pf = Prefill(args.route, args.layers, args.fa_min_kv)
 
     pf.reset_counters(False)
     for _ in range(args.warmup):
@@ -711,6 +799,11 @@ def main():
         d["sec"] += sec * per_step
         d["launches"] += per_step
     gemm, fa = per["gemm"], per["fa"]
+    declined = per.get("fa-declined")
+    traffic, traffic_src = gemm_traffic(args.route)
+    # causal-visible share of the claimed attention (keys a query may see), besides the rectangle
+    fa_visible = sum(4.0 * NH * HD * sum(UBATCH * u + t + 1 for t in range(UBATCH)) * L_LAYERS
+                     for u in range(TOKENS // UBATCH) if UBATCH * (u + 1) >= args.fa_min_kv)
     gemm_tf = gemm["flops"] / gemm["sec"] / 1e12
     fa_tf = fa["flops"] / fa["sec"] / 1e12
     wbytes = gemm_weight_bytes(args.route) * L_LAYERS * (TOKENS // UBATCH)
@@ -729,14 +822,15 @@ def main():
         "dtype": "f16",
         "data": "synthetic (random-init Q4_K weights from N(0,0.02), N(0,1) activations and KV)",
         "config": {"workload": "llama3-8b-shape Q4_K prefill, 2048 tokens in 4 micro-batches of 512: "
-                               "the backend-claimed ops (fused QKV, FLASH_ATTN_EXT, O, fused gate/up, "
-                               "down) x 32 layers",
+                               "the backend-claimed ops (fused QKV, FLASH_ATTN_EXT at n_kv >= "
+                               f"{args.fa_min_kv}, O, fused gate/up, down) x 32 layers, inputs resident "
+                               "in HBM; not an end-to-end prefill (see host_path)",
                    "layers": args.layers, "route": args.route, "global_batch": TOKENS,
                    "ubatch": UBATCH, "parallelism": "none (1 GPU)",
                    "replay": "hip graph" if graph is not None else "eager"},
         "roofline": {"bound": "mfma", "achieved": round(gemm_tf, 1), "peak": PEAK_F16_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(gemm_tf / PEAK_F16_TFLOPS, 4),
-                     "traffic": GEMM_TRAFFIC_BYTES[args.route],
+                     "traffic": traffic, "traffic_source": traffic_src,
                      "kernel": ("gemm_f16_kernel / gemm_f16_cols_kernel (LDS-DMA, fp16 MFMA 32x32x16)" if args.route == "prepacked-q"
                                 else "gemm_kernel<Q4_K> (register-staged, Q4_K decoded into LDS, fp16 MFMA 32x32x16)"),
                      "avg_launch_us": round(gemm["sec"] / gemm["launches"] * 1e6, 2),
@@ -747,15 +841,33 @@ def main():
                      "weight_GBps": round(wbytes / gemm["sec"] / 1e9, 1)},
             "flash_attn": {"tflops": round(fa_tf, 1), "frac_peak": round(fa_tf / PEAK_F16_TFLOPS, 4),
                            "ms_per_step": round(fa["sec"] * 1e3, 3), "launches_per_step": fa["launches"],
-                           "flop_count": "dense rectangle 4*H*T*n_kv*d"},
+                           "flop_count": "dense rectangle 4*H*T*n_kv*d",
+                           "tflops_causal_visible": round(fa_visible / fa["sec"] / 1e12, 1),
+                           "declined_n_kv_512_us": (round(declined["sec"] / declined["launches"] * 1e6, 2)
+                                                    if declined else None)},
             "pack_act": {"ms_per_step": round(per["pack"]["sec"] * 1e3, 3)},
             "kernel_sum_ms_per_step": round(kern_ms, 3),
             "per_op_us": {f"{k}:{i}": round(sec * 1e6, 2) for i, (k, _, _, sec) in enumerate(ops)},
         },
         "setup_s": round(pf.setup_s, 1),
     }
-    if not args.no_cpu_baseline:
+    if not (args.no_cpu_baseline or args.quick):
         res["cpu_baseline"] = cpu_baseline(pf, args.cpu_threads)
+    if not args.quick:
+        # the single-op configurations and the plugin-boundary rate, as further keys of the line
+        host_q4 = pf.host_q4
+        del pf
+        torch.cuda.empty_cache()
+        t0 = time.time()
+        res["configs"] = configs_bench(args, subset=True)
+        moe = moe_bench(args)
+        res["configs"]["MUL_MAT_ID 128e top-8 Q4_K"] = {
+            "GBps": moe["value"], "frac": moe["roofline"]["frac"], "bound": "hbm", "ops": moe["ops"]}
+        res["configs_s"] = round(time.time() - t0, 1)
+        t0 = time.time()
+        res["host_path"] = host_path(args)
+        res["host_path"]["wall_s"] = round(time.time() - t0, 1)
+        del host_q4
     print(json.dumps(res), flush=True)
 
 
