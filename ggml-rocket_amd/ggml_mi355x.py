@@ -18,6 +18,7 @@ LIB_PATH = os.path.join(_HERE, "lib", "libggml-mi355x.so")
 
 F32, F16, Q8_0, Q4_K, Q6_K, I32, BF16, MXFP4 = 0, 1, 8, 12, 14, 26, 30, 39
 F16_T = 0x101   # the library's tiled fp16 layout (16 x 32 tiles of 1 KB); not a ggml type
+OK, E_ARG, E_DEVICE, E_UNSUPPORTED, E_NOMEM, E_IDS = 0, -1, -2, -3, -4, -5   # mi355x_status
 BLOCK = {F16: 1, F32: 1, BF16: 1, Q8_0: 32, Q4_K: 256, Q6_K: 256, MXFP4: 32}
 TYPE_SIZE = {F16: 2, F32: 4, BF16: 2, Q8_0: 34, Q4_K: 144, Q6_K: 210, MXFP4: 17}
 
@@ -103,6 +104,8 @@ def _bind_optional(L):
         L.mi355x_flash_attn_workspace.restype = sz
         L.mi355x_flash_attn_workspace.argtypes = [pa, i32]
         L.mi355x_flash_attn.argtypes = [pa, i32, vp, sz, vp]
+    if hasattr(L, "mi355x_mul_mat_noalloc"):
+        L.mi355x_mul_mat_noalloc.argtypes = [i32, vp, i64, i64, vp, i64, i64, vp, i64, vp]
     if hasattr(L, "mi355x_mul_mat_id"):
         pm = ctypes.POINTER(MoeArgs)
         L.mi355x_mul_mat_id_workspace.restype = sz
@@ -218,6 +221,14 @@ def mul_mat(wtype: int, w_dev, N: int, K: int, x, out=None, workspace=None):
     check(lib().mi355x_mul_mat(wtype, _ptr(w_dev), N, K, _ptr(x), x.stride(0), M, _ptr(out), out.stride(0),
                                _ptr(workspace), workspace.numel(), stream_handle()), "mul_mat")
     return out
+
+
+def mul_mat_noalloc(wtype: int, w_dev, N: int, K: int, x, out):
+    """mul_mat through mi355x_mul_mat_noalloc: the workspace is the library's static device
+    scratch; `out` [M, >= N] is the caller's. Returns the status (no exception), so callers can
+    check the size limit."""
+    return lib().mi355x_mul_mat_noalloc(wtype, _ptr(w_dev), N, K, _ptr(x), x.stride(0), x.shape[0], _ptr(out),
+                                        out.stride(0), stream_handle())
 
 
 def flash_attn(q, k, v, mask, scale: float, softcap: float = 0.0, nsplit: int = 0, out=None,

@@ -139,6 +139,23 @@ MI355X_API int mi355x_mul_mat(int wtype, const void * w_dev, int64_t N, int64_t 
                               float * dst_dev, int64_t ldd,
                               void * workspace_dev, size_t workspace_bytes, void * stream);
 
+/* Bytes of the static device scratch of mi355x_mul_mat_noalloc (64 MiB per GPU). */
+#define MI355X_NOALLOC_SCRATCH_BYTES ((size_t)64 << 20)
+
+/* mi355x_mul_mat without a workspace argument: no counterpart in the reference. For callers
+ * that cannot allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc). The activation pack lives in a file-scope device array of
+ * MI355X_NOALLOC_SCRATCH_BYTES per GPU, held until the process ends; the call allocates nothing
+ * and frees nothing. Limit: mi355x_mul_mat_workspace(M, K) <= MI355X_NOALLOC_SCRATCH_BYTES
+ * (e.g. M 2048 at K 14336), else MI355X_E_NOMEM with a message. Every call on one GPU shares
+ * that GPU's array: calls that overlap on one GPU (two streams, two threads) race and must be
+ * serialized by the caller. The first call on a device resolves the array's address there
+ * (make it outside a stream capture); later calls may be captured. Same results as
+ * mi355x_mul_mat. */
+MI355X_API int mi355x_mul_mat_noalloc(int wtype, const void * w_dev, int64_t N, int64_t K,
+                                      const float * x_dev, int64_t ldx, int64_t M,
+                                      float * dst_dev, int64_t ldd, void * stream);
+
 /* ---- FLASH_ATTN_EXT ---------------------------------------------------------------------- */
 
 /* One attention op. Strides are in ELEMENTS, so strided ggml views (a KV-cache slice, a
