@@ -437,7 +437,7 @@ def pmc_probe(pf):
 
 def host_path(args):
     """The same prefill through the plugin boundary: every op of the step handed to
-    ggml_backend_mi355x_graph_compute as host tensors, which uploads the inputs, runs the kernels
+    mi355x_backend_graph_compute as host tensors, which uploads the inputs, runs the kernels
     and downloads dst before returning (the contract of the reference backend: no device-resident
     activations, no async slots). One graph_compute per group the ggml scheduler would form:
     {Q, K, V} (fused), {FLASH_ATTN_EXT, O}, {gate, up} (fused), {down}. Weights are per-layer Q4_K

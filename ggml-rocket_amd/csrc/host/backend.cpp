@@ -250,7 +250,7 @@ const uint64_t GUID[2] = {0x4d49333535584d49ULL, 0x2d70726566696c6cULL};
 
 }  // namespace
 
-struct ggml_backend_mi355x {
+struct mi355x_backend {
     uint64_t guid[2] = {GUID[0], GUID[1]};
     int n_threads = 5;
     bool started = false;
@@ -280,7 +280,7 @@ struct ggml_backend_mi355x {
 
 namespace {
 
-using Ctx = ggml_backend_mi355x;
+using Ctx = mi355x_backend;
 
 bool ensure_device(Ctx * c) {
     if (c->dev_checked) return c->dev_ok;
@@ -686,9 +686,9 @@ bool fusable(const mi355x_tensor * n) {
 
 extern "C" {
 
-MI355X_API const char * ggml_backend_mi355x_name(void) { return "MI355X"; }
+MI355X_API const char * mi355x_backend_name(void) { return "MI355X"; }
 
-MI355X_API const char * ggml_backend_mi355x_description(void) {
+MI355X_API const char * mi355x_backend_description(void) {
     static char desc[160];
     static std::once_flag once;
     std::call_once(once, [] {
@@ -706,7 +706,7 @@ MI355X_API const char * ggml_backend_mi355x_description(void) {
     return desc;
 }
 
-MI355X_API void ggml_backend_mi355x_get_memory(size_t * fr, size_t * tot) {
+MI355X_API void mi355x_backend_get_memory(size_t * fr, size_t * tot) {
     size_t f = 0, t = 0;
     int n = 0;
     if (!(hipGetDeviceCount(&n) == hipSuccess && n > 0 && hipMemGetInfo(&f, &t) == hipSuccess)) {
@@ -717,7 +717,7 @@ MI355X_API void ggml_backend_mi355x_get_memory(size_t * fr, size_t * tot) {
     if (tot) *tot = t;
 }
 
-MI355X_API ggml_backend_mi355x_t ggml_backend_mi355x_init(void) {
+MI355X_API mi355x_backend_t mi355x_backend_init(void) {
     Ctx * c = new Ctx();
     int nt = knob_int("N_THREADS", 5);
     c->n_threads = nt < 1 ? 1 : (nt > 8 ? 8 : nt);
@@ -725,11 +725,11 @@ MI355X_API ggml_backend_mi355x_t ggml_backend_mi355x_init(void) {
     return c;
 }
 
-MI355X_API bool ggml_backend_is_mi355x(ggml_backend_mi355x_t c) {
+MI355X_API bool mi355x_backend_is(mi355x_backend_t c) {
     return c && c->guid[0] == GUID[0] && c->guid[1] == GUID[1];
 }
 
-MI355X_API void ggml_backend_mi355x_free(ggml_backend_mi355x_t c) {
+MI355X_API void mi355x_backend_free(mi355x_backend_t c) {
     if (!c) return;
     if (c->stream) (void)hipStreamSynchronize(c->stream);
     c->stage.release();
@@ -749,8 +749,8 @@ MI355X_API void ggml_backend_mi355x_free(ggml_backend_mi355x_t c) {
     delete c;
 }
 
-MI355X_API void ggml_backend_mi355x_set_n_threads(ggml_backend_mi355x_t c, int n) {
-    if (!ggml_backend_is_mi355x(c)) return;
+MI355X_API void mi355x_backend_set_n_threads(mi355x_backend_t c, int n) {
+    if (!mi355x_backend_is(c)) return;
     if (c->started) {
         logw("set_n_threads(%d) after the first compute changes nothing\n", n);
         return;
@@ -759,16 +759,16 @@ MI355X_API void ggml_backend_mi355x_set_n_threads(ggml_backend_mi355x_t c, int n
     c->n_threads = n < 1 ? 1 : (n > 8 ? 8 : n);
 }
 
-MI355X_API void ggml_backend_mi355x_set_quant_resident(ggml_backend_mi355x_t c, int mode) {
-    if (ggml_backend_is_mi355x(c)) c->quant_resident = mode < 0 ? -1 : (mode > 0 ? 1 : 0);
+MI355X_API void mi355x_backend_set_quant_resident(mi355x_backend_t c, int mode) {
+    if (mi355x_backend_is(c)) c->quant_resident = mode < 0 ? -1 : (mode > 0 ? 1 : 0);
 }
 
-MI355X_API int ggml_backend_mi355x_get_n_threads(ggml_backend_mi355x_t c) {
-    return ggml_backend_is_mi355x(c) ? c->n_threads : 0;
+MI355X_API int mi355x_backend_get_n_threads(mi355x_backend_t c) {
+    return mi355x_backend_is(c) ? c->n_threads : 0;
 }
 
-MI355X_API long ggml_backend_mi355x_route_ops(ggml_backend_mi355x_t c, const char * route) {
-    if (!ggml_backend_is_mi355x(c)) return 0;
+MI355X_API long mi355x_backend_route_ops(mi355x_backend_t c, const char * route) {
+    if (!mi355x_backend_is(c)) return 0;
     if (!route) {
         long s = 0;
         for (const auto & kv : c->routes) s += kv.second;
@@ -778,24 +778,24 @@ MI355X_API long ggml_backend_mi355x_route_ops(ggml_backend_mi355x_t c, const cha
     return it == c->routes.end() ? 0 : it->second;
 }
 
-MI355X_API long ggml_backend_mi355x_cpu_fallbacks(ggml_backend_mi355x_t c) {
-    return ggml_backend_is_mi355x(c) ? c->n_cpu_fallbacks : 0;
+MI355X_API long mi355x_backend_cpu_fallbacks(mi355x_backend_t c) {
+    return mi355x_backend_is(c) ? c->n_cpu_fallbacks : 0;
 }
 
-MI355X_API void ggml_backend_mi355x_moe_stats(ggml_backend_mi355x_t c, long * n_resident, long * n_streamed) {
-    if (n_resident) *n_resident = ggml_backend_is_mi355x(c) ? c->moe_resident : 0;
-    if (n_streamed) *n_streamed = ggml_backend_is_mi355x(c) ? c->moe_streamed : 0;
+MI355X_API void mi355x_backend_moe_stats(mi355x_backend_t c, long * n_resident, long * n_streamed) {
+    if (n_resident) *n_resident = mi355x_backend_is(c) ? c->moe_resident : 0;
+    if (n_streamed) *n_streamed = mi355x_backend_is(c) ? c->moe_streamed : 0;
 }
 
-static RouteHealth * breaker_of(ggml_backend_mi355x_t c, const char * g) {
-    if (!ggml_backend_is_mi355x(c) || !g) return nullptr;
+static RouteHealth * breaker_of(mi355x_backend_t c, const char * g) {
+    if (!mi355x_backend_is(c) || !g) return nullptr;
     if (!strcmp(g, "gemm")) return &c->brk_gemm;
     if (!strcmp(g, "fa")) return &c->brk_fa;
     if (!strcmp(g, "moe")) return &c->brk_moe;
     return nullptr;
 }
 
-MI355X_API void ggml_backend_mi355x_route_stats(ggml_backend_mi355x_t c, const char * g, long * attempts,
+MI355X_API void mi355x_backend_route_stats(mi355x_backend_t c, const char * g, long * attempts,
                                                 long * failures, long * bypassed) {
     RouteHealth * b = breaker_of(c, g);
     if (attempts) *attempts = b ? b->attempts : 0;
@@ -803,20 +803,20 @@ MI355X_API void ggml_backend_mi355x_route_stats(ggml_backend_mi355x_t c, const c
     if (bypassed) *bypassed = b ? b->bypassed : 0;
 }
 
-MI355X_API void ggml_backend_mi355x_inject_faults(ggml_backend_mi355x_t c, const char * g, int n) {
+MI355X_API void mi355x_backend_inject_faults(mi355x_backend_t c, const char * g, int n) {
     RouteHealth * b = breaker_of(c, g);
     if (b) b->inject = n < 0 ? 0 : n;
 }
 
-static int graph_compute_nodes(ggml_backend_mi355x_t c, mi355x_tensor * const * nodes, int n_nodes);
+static int graph_compute_nodes(mi355x_backend_t c, mi355x_tensor * const * nodes, int n_nodes);
 
 // Repacked weights with registered original bytes (ggml-rocket.cpp:7005-7047): for this call,
 // each such source descriptor reads the registered bytes (a view at its offset). Only the
 // descriptors change, never the host's tensors, so a CPU split running meanwhile still reads its
 // repacked copy. A source that needs bytes and has none fails the call before any route reads
 // it; a view node reads nothing and does not count as a check of its source.
-MI355X_API int ggml_backend_mi355x_graph_compute(ggml_backend_mi355x_t c, mi355x_tensor * const * nodes, int n_nodes) {
-    if (!ggml_backend_is_mi355x(c) || (n_nodes > 0 && !nodes)) return MI355X_STATUS_FAILED;
+MI355X_API int mi355x_backend_graph_compute(mi355x_backend_t c, mi355x_tensor * const * nodes, int n_nodes) {
+    if (!mi355x_backend_is(c) || (n_nodes > 0 && !nodes)) return MI355X_STATUS_FAILED;
     if (registered_sources() == 0) return graph_compute_nodes(c, nodes, n_nodes);
     struct Saved {
         mi355x_tensor * t;
@@ -854,7 +854,7 @@ MI355X_API int ggml_backend_mi355x_graph_compute(ggml_backend_mi355x_t c, mi355x
     return st;
 }
 
-static int graph_compute_nodes(ggml_backend_mi355x_t c, mi355x_tensor * const * nodes, int n_nodes) {
+static int graph_compute_nodes(mi355x_backend_t c, mi355x_tensor * const * nodes, int n_nodes) {
     c->started = true;
     std::vector<bool> done((size_t)(n_nodes > 0 ? n_nodes : 0), false);
     for (int i = 0; i < n_nodes; i++) {

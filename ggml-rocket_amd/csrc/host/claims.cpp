@@ -453,7 +453,7 @@ using namespace mxh;
 
 extern "C" {
 
-MI355X_API bool ggml_backend_mi355x_supports_op(const mi355x_tensor * op) {
+MI355X_API bool mi355x_backend_supports_op(const mi355x_tensor * op) {
     if (!op) return false;
     // a source in a buffer this backend cannot read as ggml blocks (CPU_REPACK, another device)
     // stays on the CPU unless its original bytes are registered (ggml-rocket.cpp:7036-7043)
@@ -473,20 +473,20 @@ MI355X_API bool ggml_backend_mi355x_supports_op(const mi355x_tensor * op) {
     }
 }
 
-MI355X_API bool ggml_backend_mi355x_offload_op(const mi355x_tensor * op) {
+MI355X_API bool mi355x_backend_offload_op(const mi355x_tensor * op) {
     return op && (op->op == MI355X_OP_MUL_MAT || op->op == MI355X_OP_MUL_MAT_ID) &&
-           ggml_backend_mi355x_supports_op(op);
+           mi355x_backend_supports_op(op);
 }
 
-MI355X_API bool ggml_backend_mi355x_supports_buft(int buffer_kind) {
+MI355X_API bool mi355x_backend_supports_buft(int buffer_kind) {
     return buffer_kind == MI355X_BUF_HOST || buffer_kind == MI355X_BUF_REPACK;
 }
 
-MI355X_API void ggml_backend_mi355x_register_weight_source(const mi355x_tensor * t, const void * data, size_t nbytes) {
+MI355X_API void mi355x_backend_register_weight_source(const mi355x_tensor * t, const void * data, size_t nbytes) {
     if (t && t->data) sources().put(t, data, nbytes);
 }
 
-MI355X_API int ggml_backend_mi355x_weight_key(const mi355x_tensor * t, char * out, int cap) {
+MI355X_API int mi355x_backend_weight_key(const mi355x_tensor * t, char * out, int cap) {
     const std::string k = weight_key(t);
     if (out && cap > 0) {
         const size_t n = k.size() < (size_t)(cap - 1) ? k.size() : (size_t)(cap - 1);
@@ -496,7 +496,9 @@ MI355X_API int ggml_backend_mi355x_weight_key(const mi355x_tensor * t, char * ou
     return (int)k.size();
 }
 
-MI355X_API bool ggml_backend_mi355x_parse_mb(const char * text, size_t * bytes) {
+MI355X_API void mi355x_backend_set_log_callback(mi355x_log_fn fn, void * user) { set_log_sink(fn, user); }
+
+MI355X_API bool mi355x_backend_parse_mb(const char * text, size_t * bytes) {
     return parse_mb(text, bytes);
 }
 

@@ -8,7 +8,7 @@
 
 #include <string>
 
-#include "../../../include/ggml-mi355x.h"
+#include "../../../include/mi355x_backend.h"
 
 namespace mxh {
 
@@ -73,6 +73,7 @@ bool cpu_mul_mat_id(const mi355x_tensor * dst);   // false on an out-of-range id
 bool decode_row_f32(int type, const void * src, float * out, int64_t n);
 
 // ---- logging -------------------------------------------------------------------------------
+void set_log_sink(mi355x_log_fn fn, void * user);
 void logw(const char * fmt, ...) __attribute__((format(printf, 1, 2)));
 void logi(const char * fmt, ...) __attribute__((format(printf, 1, 2)));
 

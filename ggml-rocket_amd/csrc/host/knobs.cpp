@@ -13,15 +13,37 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include <atomic>
+
 #include "host.h"
 
 namespace mxh {
 
+// Log lines go to stderr unless a host installed a sink (the ggml adapter routes them to
+// ggml's logger, which llama.cpp and whisper.cpp redirect or silence).
+namespace {
+std::atomic<mi355x_log_fn> g_log_fn{nullptr};
+std::atomic<void *> g_log_user{nullptr};
+
+void emit(int level, const char * prefix, const char * fmt, va_list ap) {
+    char line[1024];
+    const int n = snprintf(line, sizeof line, "[mi355x] %s", prefix);
+    vsnprintf(line + n, sizeof line - (size_t)n, fmt, ap);
+    const mi355x_log_fn fn = g_log_fn.load(std::memory_order_acquire);
+    if (fn) fn(level, line, g_log_user.load(std::memory_order_acquire));
+    else fputs(line, stderr);
+}
+}  // namespace
+
+void set_log_sink(mi355x_log_fn fn, void * user) {
+    g_log_user.store(user, std::memory_order_release);
+    g_log_fn.store(fn, std::memory_order_release);
+}
+
 void logw(const char * fmt, ...) {
     va_list ap;
     va_start(ap, fmt);
-    fprintf(stderr, "[mi355x] warning: ");
-    vfprintf(stderr, fmt, ap);
+    emit(MI355X_LOG_WARN, "warning: ", fmt, ap);
     va_end(ap);
 }
 
@@ -30,8 +52,7 @@ void logi(const char * fmt, ...) {
     if (quiet) return;
     va_list ap;
     va_start(ap, fmt);
-    fprintf(stderr, "[mi355x] ");
-    vfprintf(stderr, fmt, ap);
+    emit(MI355X_LOG_INFO, "", fmt, ap);
     va_end(ap);
 }
 

@@ -1,9 +1,9 @@
-"""Python binding of libggml-mi355x.so (the gfx950 prefill backend).
+"""Python binding of libmi355x.so (the gfx950 prefill backend).
 
 Two layers, both plain ctypes over the C ABI in include/:
   * the kernel entry points of mi355x_kernels.h (device pointers, sizes, a HIP stream), with
     torch-tensor helpers: torch only allocates device memory and names the stream;
-  * the backend's host layer of ggml-mi355x.h (claim rules, graph compute, counters), which
+  * the backend's host layer of mi355x_backend.h (claim rules, graph compute, counters), which
     mirrors ggml-rocket.h.
 
 There is no fallback: if the shared library is missing, `lib()` raises.
@@ -14,7 +14,7 @@ import ctypes
 import os
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(_HERE, "lib", "libggml-mi355x.so")
+LIB_PATH = os.path.join(_HERE, "lib", "libmi355x.so")
 
 F32, F16, Q8_0, Q4_K, Q6_K, I32, BF16, MXFP4 = 0, 1, 8, 12, 14, 26, 30, 39
 F16_T = 0x101   # the library's tiled fp16 layout (16 x 32 tiles of 1 KB); not a ggml type
@@ -274,7 +274,7 @@ def mul_mat_id(wtype: int, as_dev, n_expert: int, N: int, K: int, b, ids, out=No
     return out
 
 
-# ==== the backend host layer (include/ggml-mi355x.h) =========================================
+# ==== the backend host layer (include/mi355x_backend.h) =========================================
 # A numpy-backed stand-in for the few ggml graph constructors the reference's tests use
 # (ggml_new_tensor_*, ggml_mul_mat, ggml_mul_mat_id, ggml_flash_attn_ext, permute / view), with
 # ggml's ne / nb conventions, so the host-layer tests read like the reference's.
@@ -304,35 +304,35 @@ def _bind_host(L):
         return L
     vp, i32, lng, sz = ctypes.c_void_p, ctypes.c_int, ctypes.c_long, ctypes.c_size_t
     pt = ctypes.POINTER(Tensor)
-    L.ggml_backend_mi355x_name.restype = ctypes.c_char_p
-    L.ggml_backend_mi355x_description.restype = ctypes.c_char_p
-    L.ggml_backend_mi355x_get_memory.argtypes = [ctypes.POINTER(sz), ctypes.POINTER(sz)]
-    L.ggml_backend_mi355x_supports_op.restype = ctypes.c_bool
-    L.ggml_backend_mi355x_supports_op.argtypes = [pt]
-    L.ggml_backend_mi355x_offload_op.restype = ctypes.c_bool
-    L.ggml_backend_mi355x_offload_op.argtypes = [pt]
-    L.ggml_backend_mi355x_supports_buft.restype = ctypes.c_bool
-    L.ggml_backend_mi355x_supports_buft.argtypes = [i32]
-    L.ggml_backend_mi355x_init.restype = vp
-    L.ggml_backend_mi355x_free.argtypes = [vp]
-    L.ggml_backend_is_mi355x.restype = ctypes.c_bool
-    L.ggml_backend_is_mi355x.argtypes = [vp]
-    L.ggml_backend_mi355x_set_n_threads.argtypes = [vp, i32]
-    L.ggml_backend_mi355x_get_n_threads.argtypes = [vp]
-    L.ggml_backend_mi355x_set_quant_resident.argtypes = [vp, i32]
-    L.ggml_backend_mi355x_graph_compute.argtypes = [vp, ctypes.POINTER(pt), i32]
-    L.ggml_backend_mi355x_route_ops.restype = lng
-    L.ggml_backend_mi355x_route_ops.argtypes = [vp, ctypes.c_char_p]
-    L.ggml_backend_mi355x_cpu_fallbacks.restype = lng
-    L.ggml_backend_mi355x_cpu_fallbacks.argtypes = [vp]
-    L.ggml_backend_mi355x_moe_stats.argtypes = [vp, ctypes.POINTER(lng), ctypes.POINTER(lng)]
-    L.ggml_backend_mi355x_route_stats.argtypes = [vp, ctypes.c_char_p, ctypes.POINTER(lng), ctypes.POINTER(lng),
+    L.mi355x_backend_name.restype = ctypes.c_char_p
+    L.mi355x_backend_description.restype = ctypes.c_char_p
+    L.mi355x_backend_get_memory.argtypes = [ctypes.POINTER(sz), ctypes.POINTER(sz)]
+    L.mi355x_backend_supports_op.restype = ctypes.c_bool
+    L.mi355x_backend_supports_op.argtypes = [pt]
+    L.mi355x_backend_offload_op.restype = ctypes.c_bool
+    L.mi355x_backend_offload_op.argtypes = [pt]
+    L.mi355x_backend_supports_buft.restype = ctypes.c_bool
+    L.mi355x_backend_supports_buft.argtypes = [i32]
+    L.mi355x_backend_init.restype = vp
+    L.mi355x_backend_free.argtypes = [vp]
+    L.mi355x_backend_is.restype = ctypes.c_bool
+    L.mi355x_backend_is.argtypes = [vp]
+    L.mi355x_backend_set_n_threads.argtypes = [vp, i32]
+    L.mi355x_backend_get_n_threads.argtypes = [vp]
+    L.mi355x_backend_set_quant_resident.argtypes = [vp, i32]
+    L.mi355x_backend_graph_compute.argtypes = [vp, ctypes.POINTER(pt), i32]
+    L.mi355x_backend_route_ops.restype = lng
+    L.mi355x_backend_route_ops.argtypes = [vp, ctypes.c_char_p]
+    L.mi355x_backend_cpu_fallbacks.restype = lng
+    L.mi355x_backend_cpu_fallbacks.argtypes = [vp]
+    L.mi355x_backend_moe_stats.argtypes = [vp, ctypes.POINTER(lng), ctypes.POINTER(lng)]
+    L.mi355x_backend_route_stats.argtypes = [vp, ctypes.c_char_p, ctypes.POINTER(lng), ctypes.POINTER(lng),
                                                   ctypes.POINTER(lng)]
-    L.ggml_backend_mi355x_inject_faults.argtypes = [vp, ctypes.c_char_p, i32]
-    L.ggml_backend_mi355x_weight_key.argtypes = [pt, ctypes.c_char_p, i32]
-    L.ggml_backend_mi355x_register_weight_source.argtypes = [pt, vp, sz]
-    L.ggml_backend_mi355x_parse_mb.restype = ctypes.c_bool
-    L.ggml_backend_mi355x_parse_mb.argtypes = [ctypes.c_char_p, ctypes.POINTER(sz)]
+    L.mi355x_backend_inject_faults.argtypes = [vp, ctypes.c_char_p, i32]
+    L.mi355x_backend_weight_key.argtypes = [pt, ctypes.c_char_p, i32]
+    L.mi355x_backend_register_weight_source.argtypes = [pt, vp, sz]
+    L.mi355x_backend_parse_mb.restype = ctypes.c_bool
+    L.mi355x_backend_parse_mb.argtypes = [ctypes.c_char_p, ctypes.POINTER(sz)]
     L._host_bound = True
     return L
 
@@ -432,17 +432,17 @@ class Graph:
 
 
 class Backend:
-    """One backend instance (ggml_backend_mi355x_init .. free)."""
+    """One backend instance (mi355x_backend_init .. free)."""
 
     def __init__(self):
         self.L = host()
-        self.h = self.L.ggml_backend_mi355x_init()
+        self.h = self.L.mi355x_backend_init()
         if not self.h:
             raise MI355XError("init failed")
 
     def free(self):
         if self.h:
-            self.L.ggml_backend_mi355x_free(self.h)
+            self.L.mi355x_backend_free(self.h)
             self.h = None
 
     def __del__(self):
@@ -453,29 +453,29 @@ class Backend:
 
     def compute(self, nodes):
         arr = (ctypes.POINTER(Tensor) * len(nodes))(*[ctypes.pointer(n) for n in nodes])
-        return self.L.ggml_backend_mi355x_graph_compute(self.h, arr, len(nodes))
+        return self.L.mi355x_backend_graph_compute(self.h, arr, len(nodes))
 
     def route_ops(self, route=None):
-        return self.L.ggml_backend_mi355x_route_ops(self.h, route.encode() if route else None)
+        return self.L.mi355x_backend_route_ops(self.h, route.encode() if route else None)
 
     def cpu_fallbacks(self):
-        return self.L.ggml_backend_mi355x_cpu_fallbacks(self.h)
+        return self.L.mi355x_backend_cpu_fallbacks(self.h)
 
     def moe_stats(self):
         a, b = ctypes.c_long(), ctypes.c_long()
-        self.L.ggml_backend_mi355x_moe_stats(self.h, ctypes.byref(a), ctypes.byref(b))
+        self.L.mi355x_backend_moe_stats(self.h, ctypes.byref(a), ctypes.byref(b))
         return a.value, b.value
 
     def route_stats(self, group):
         a, b, c = ctypes.c_long(), ctypes.c_long(), ctypes.c_long()
-        self.L.ggml_backend_mi355x_route_stats(self.h, group.encode(), ctypes.byref(a), ctypes.byref(b), ctypes.byref(c))
+        self.L.mi355x_backend_route_stats(self.h, group.encode(), ctypes.byref(a), ctypes.byref(b), ctypes.byref(c))
         return a.value, b.value, c.value
 
     def set_quant_resident(self, mode):
-        self.L.ggml_backend_mi355x_set_quant_resident(self.h, mode)
+        self.L.mi355x_backend_set_quant_resident(self.h, mode)
 
     def inject_faults(self, group, n):
-        self.L.ggml_backend_mi355x_inject_faults(self.h, group.encode(), n)
+        self.L.mi355x_backend_inject_faults(self.h, group.encode(), n)
 
 
 _registered = {}
@@ -487,29 +487,29 @@ def register_weight_source(t, src):
     import numpy as np
     key = ctypes.addressof(t)
     if src is None:
-        host().ggml_backend_mi355x_register_weight_source(ctypes.byref(t), None, 0)
+        host().mi355x_backend_register_weight_source(ctypes.byref(t), None, 0)
         _registered.pop(key, None)
         return
     a = np.ascontiguousarray(src).view(np.uint8).reshape(-1)
     _registered[key] = a
-    host().ggml_backend_mi355x_register_weight_source(ctypes.byref(t), ctypes.c_void_p(a.ctypes.data), a.nbytes)
+    host().mi355x_backend_register_weight_source(ctypes.byref(t), ctypes.c_void_p(a.ctypes.data), a.nbytes)
 
 
 def supports_op(t):
-    return bool(host().ggml_backend_mi355x_supports_op(ctypes.byref(t)))
+    return bool(host().mi355x_backend_supports_op(ctypes.byref(t)))
 
 
 def offload_op(t):
-    return bool(host().ggml_backend_mi355x_offload_op(ctypes.byref(t)))
+    return bool(host().mi355x_backend_offload_op(ctypes.byref(t)))
 
 
 def weight_key(t):
     buf = ctypes.create_string_buffer(256)
-    host().ggml_backend_mi355x_weight_key(ctypes.byref(t), buf, 256)
+    host().mi355x_backend_weight_key(ctypes.byref(t), buf, 256)
     return buf.value.decode()
 
 
 def parse_mb(text):
     v = ctypes.c_size_t(12345)
-    ok = host().ggml_backend_mi355x_parse_mb(text.encode(), ctypes.byref(v))
+    ok = host().mi355x_backend_parse_mb(text.encode(), ctypes.byref(v))
     return ok, v.value

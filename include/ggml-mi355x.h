@@ -1,169 +1,59 @@
 /* SPDX-License-Identifier: MIT
  *
- * ggml-mi355x.h -- the backend's plugin-facing C API.
+ * ggml-mi355x.h -- the ggml backend for one AMD Instinct MI355X (gfx950), the drop-in for
+ * ggml-rocket's public header (ggml-rocket.h:23-91) with "rocket" read as "mi355x".
  *
- * It mirrors the reference's public header (ggml-rocket.h:23-91) and the device/registry hooks
- * of its plugin vtables (ggml-rocket.cpp:7201-7882): the same claim rules, route counters,
- * fallback counter and lifecycle, under this backend's name. The reference compiles against a
- * host's private ggml headers; this API takes a plain C descriptor of the ggml_tensor fields
- * the backend reads (mi355x_tensor), and a ~150-line adapter maps ggml_tensor / ggml_op onto it
- * inside the ggml_backend_*_i vtables (see the integration notes). ggml types keep their ggml
- * ids; ops are named by this enum because ggml's op ordinals move between versions
- * (API.md:335-349), so the adapter maps them by ggml_op_name().
+ * The backend claims GGML_OP_MUL_MAT, GGML_OP_FLASH_ATTN_EXT and GGML_OP_MUL_MAT_ID under the
+ * reference's claim rules and computes them on the GPU; the CPU backend computes every op it
+ * declines. Weights stay in the host's buffers and are cached in HBM on first use. A host loads
+ * it as libggml-mi355x.so through GGML_BACKEND_PATH / ggml_backend_load (the ggml_backend_init
+ * entry of GGML_BACKEND_DL), or links it and calls ggml_backend_mi355x_reg().
+ *
+ * Implemented by ggml-rocket_amd/ggml/ggml-mi355x.cpp over libmi355x's host layer
+ * (include/mi355x_backend.h); built against the host's ggml (make -C ggml-rocket_amd ggml
+ * HOST_GGML_DIR=<llama.cpp or whisper.cpp checkout>).
  */
 #ifndef GGML_MI355X_H
 #define GGML_MI355X_H
 
-#include <stdbool.h>
-#include <stddef.h>
-#include <stdint.h>
+#include "ggml.h"
+#include "ggml-backend.h"
 
 #ifdef __cplusplus
 extern "C" {
 #endif
 
-#ifndef MI355X_API
-#define MI355X_API __attribute__((visibility("default")))
-#endif
+/* Replaces ggml_backend_rocket_init (ggml-rocket.h:23-24): creates a backend instance. It hands
+ * out the host's CPU buffer type, so weights stay in host buffers; nothing touches the GPU
+ * before the first graph_compute. */
+GGML_BACKEND_API ggml_backend_t ggml_backend_mi355x_init(void);
 
-#define MI355X_MAX_DIMS 4
-#define MI355X_MAX_SRC 10
-#define MI355X_MAX_OP_PARAMS 16   /* int32 slots (ggml: GGML_MAX_OP_PARAMS bytes / 4) */
-#define MI355X_MAX_NAME 64
+/* Replaces ggml_backend_is_rocket (ggml-rocket.h:26-27): true if `backend` is an instance of
+ * this backend (GUID match). */
+GGML_BACKEND_API bool ggml_backend_is_mi355x(ggml_backend_t backend);
 
-/* ggml type ids (ggml.h enum ggml_type) */
-enum mi355x_ggml_type {
-    MI355X_TYPE_F32 = 0, MI355X_TYPE_F16 = 1, MI355X_TYPE_Q4_0 = 2, MI355X_TYPE_Q4_1 = 3,
-    MI355X_TYPE_Q5_0 = 6, MI355X_TYPE_Q5_1 = 7, MI355X_TYPE_Q8_0 = 8, MI355X_TYPE_Q8_1 = 9,
-    MI355X_TYPE_Q2_K = 10, MI355X_TYPE_Q3_K = 11, MI355X_TYPE_Q4_K = 12, MI355X_TYPE_Q5_K = 13,
-    MI355X_TYPE_Q6_K = 14, MI355X_TYPE_Q8_K = 15, MI355X_TYPE_IQ2_XXS = 16, MI355X_TYPE_IQ2_XS = 17,
-    MI355X_TYPE_IQ3_XXS = 18, MI355X_TYPE_IQ1_S = 19, MI355X_TYPE_IQ4_NL = 20, MI355X_TYPE_IQ3_S = 21,
-    MI355X_TYPE_IQ2_S = 22, MI355X_TYPE_IQ4_XS = 23, MI355X_TYPE_I8 = 24, MI355X_TYPE_I16 = 25,
-    MI355X_TYPE_I32 = 26, MI355X_TYPE_I64 = 27, MI355X_TYPE_F64 = 28, MI355X_TYPE_IQ1_M = 29,
-    MI355X_TYPE_BF16 = 30, MI355X_TYPE_TQ1_0 = 34, MI355X_TYPE_TQ2_0 = 35, MI355X_TYPE_MXFP4 = 39,
-};
+/* Replaces ggml_backend_rocket_set_n_threads (ggml-rocket.h:29-37): the host threads (1-8,
+ * clamped with a warning) that fill and drain the pinned staging of the host <-> device copies.
+ * Call before the first graph_compute; a later call warns and changes nothing. */
+GGML_BACKEND_API void ggml_backend_mi355x_set_n_threads(ggml_backend_t backend, int n_threads);
 
-/* the ops the backend distinguishes; everything else is MI355X_OP_OTHER */
-enum mi355x_op {
-    MI355X_OP_NONE = 0, MI355X_OP_MUL_MAT, MI355X_OP_MUL_MAT_ID, MI355X_OP_FLASH_ATTN_EXT,
-    MI355X_OP_RESHAPE, MI355X_OP_VIEW, MI355X_OP_PERMUTE, MI355X_OP_TRANSPOSE,
-    MI355X_OP_ADD, MI355X_OP_SCALE, MI355X_OP_OTHER,
-};
+/* Replaces ggml_backend_rocket_moe_stats (ggml-rocket.h:39-57): distinct MoE experts held in the
+ * HBM expert cache, and distinct experts run from a per-call upload, over the backend's life.
+ * Either pointer may be NULL. */
+GGML_BACKEND_API void ggml_backend_mi355x_moe_stats(ggml_backend_t backend, long * n_resident,
+                                                    long * n_streamed);
 
-/* where a tensor's bytes live (ggml_backend_buffer_is_host / the CPU_REPACK buffer type) */
-enum mi355x_buffer_kind {
-    MI355X_BUF_NONE = 0,      /* no buffer yet (a no_alloc graph asking supports_op) */
-    MI355X_BUF_HOST = 1,      /* host memory: CPU, CPU_Mapped, this backend's own */
-    MI355X_BUF_REPACK = 2,    /* ggml-cpu's repacked layout: not readable as ggml blocks */
-    MI355X_BUF_OTHER = 3,     /* device memory of another backend */
-};
+/* Replace ggml_backend_rocket_route_ops / _cpu_fallbacks (ggml-rocket.h:59-88): ops completed
+ * per route ("mt", "prepacked", "prepacked-q", "fused", "fused-resident", "moe", "fa"; NULL =
+ * all), and ops recomputed on the CPU after a device failure. Cumulative. */
+GGML_BACKEND_API long ggml_backend_mi355x_route_ops(ggml_backend_t backend, const char * route);
+GGML_BACKEND_API long ggml_backend_mi355x_cpu_fallbacks(ggml_backend_t backend);
 
-/* The fields of ggml_tensor the backend reads. nb[] are byte strides as in ggml. */
-typedef struct mi355x_tensor {
-    int32_t type;                                   /* enum mi355x_ggml_type */
-    int32_t op;                                     /* enum mi355x_op */
-    int64_t ne[MI355X_MAX_DIMS];
-    size_t  nb[MI355X_MAX_DIMS];
-    int32_t op_params[MI355X_MAX_OP_PARAMS];
-    struct mi355x_tensor * src[MI355X_MAX_SRC];
-    void * data;
-    char name[MI355X_MAX_NAME];
-    int32_t buffer_kind;                            /* enum mi355x_buffer_kind */
-    const void * buffer_id;                         /* identity of the tensor's buffer, or NULL */
-    size_t buffer_size;                             /* that buffer's size in bytes, 0 if none */
-} mi355x_tensor;
-
-/* ggml_status values returned by graph_compute */
-enum mi355x_ggml_status { MI355X_STATUS_FAILED = -1, MI355X_STATUS_SUCCESS = 0 };
-
-typedef struct ggml_backend_mi355x * ggml_backend_mi355x_t;
-
-/* ---- registry / device (ggml-rocket.cpp:7829-7881) ---------------------------------------- */
-
-/* "MI355X": the registry, device and backend name. */
-MI355X_API const char * ggml_backend_mi355x_name(void);
-/* "<gfx arch> (<CUs> CUs, HIP <version>)", or a "no device" text. */
-MI355X_API const char * ggml_backend_mi355x_description(void);
-/* HBM free / total of the current device (0 / 0 without one). */
-MI355X_API void ggml_backend_mi355x_get_memory(size_t * free, size_t * total);
-
-/* Placement hooks. Pure functions of the op's metadata; no backend instance is needed.
- * supports_op: the claim rules of ggml-rocket.cpp:7415-7772 (MUL_MAT 7424-7496, precision
- * declarations 7334-7404, MUL_MAT_ID 7497-7653 with the MoE residency pre-flight 6198-6289,
- * FLASH_ATTN_EXT 7654-7768). offload_op: (MUL_MAT or MUL_MAT_ID) and supports_op (7820-7827).
- * supports_buft: host buffers and CPU_REPACK (7795-7797). */
-MI355X_API bool ggml_backend_mi355x_supports_op(const mi355x_tensor * op);
-MI355X_API bool ggml_backend_mi355x_offload_op(const mi355x_tensor * op);
-MI355X_API bool ggml_backend_mi355x_supports_buft(int buffer_kind);
-
-/* ggml_backend_rocket_register_weight_source (ggml-rocket.cpp:6993-7003, the registry's
- * "…register_weight_source" proc address, API.md:280-314): registers the original (GGUF) bytes
- * of a weight whose tensor lives in CPU_REPACK; data == NULL unregisters it. `t` describes the
- * tensor as placement sees it (its data = its place in the repack buffer, its name, its ne/nb).
- * While registered with a matching name and byte size, supports_buft / supports_op claim ops
- * on it and graph_compute reads the registered bytes (through a view too, at its offset). The
- * host keeps the bytes mapped while the tensor lives and unregisters before freeing it. */
-MI355X_API void ggml_backend_mi355x_register_weight_source(const mi355x_tensor * t, const void * data, size_t nbytes);
-
-/* ---- backend instance (ggml-rocket.h:25-91) ------------------------------------------------ */
-
-/* Creates an instance. Nothing touches the GPU until the first graph_compute (ggml-rocket.cpp:
- * 8024-8155). */
-MI355X_API ggml_backend_mi355x_t ggml_backend_mi355x_init(void);
-/* Frees the instance: device buffers, the HBM weight cache, its MoE residency claims. */
-MI355X_API void ggml_backend_mi355x_free(ggml_backend_mi355x_t backend);
-/* True if `backend` is an instance of this backend (GUID check, 7241-7246). */
-MI355X_API bool ggml_backend_is_mi355x(ggml_backend_mi355x_t backend);
-/* ggml_backend_rocket_set_n_threads (ggml-rocket.cpp:8185-8217): the number of host threads
- * (clamped to 1-8, with a warning) that fill and drain the pinned staging of host <-> device
- * copies, as the reference's value sizes its host worker pool. A call after the first compute
- * warns and changes nothing, as the reference's does. */
-MI355X_API void ggml_backend_mi355x_set_n_threads(ggml_backend_mi355x_t backend, int n_threads);
-MI355X_API int  ggml_backend_mi355x_get_n_threads(ggml_backend_mi355x_t backend);
-
-/* This instance's QUANT_RESIDENT setting (no counterpart in the reference, whose knob is
- * process-wide): 1 holds each quantized weight resident as fp16 ("prepacked-q"), 0 keeps the
- * quantized bytes resident and dequantizes them in LDS per call ("mt"), -1 follows the knob. */
-MI355X_API void ggml_backend_mi355x_set_quant_resident(ggml_backend_mi355x_t backend, int mode);
-
-/* Computes one split: the nodes in order. MUL_MAT (with shared-src1 fusion), MUL_MAT_ID and
- * FLASH_ATTN_EXT run on the GPU; view ops are no-ops; any other op returns FAILED, as does a
- * MUL_MAT_ID whose ids fall outside [0, n_expert). Tensor data are host pointers; every dst is
- * fully written when this returns. A failed device job degrades that op to the CPU (counted in
- * cpu_fallbacks), it never fails the graph (ggml-rocket.cpp:7050-7200). */
-MI355X_API int ggml_backend_mi355x_graph_compute(ggml_backend_mi355x_t backend,
-                                                 mi355x_tensor * const * nodes, int n_nodes);
-
-/* Route counters (ggml-rocket.h:60-88). Routes: "mt" (per-call fused-dequant GEMM),
- * "prepacked" (resident fp16 weight), "prepacked-q" (quantized weight held resident as fp16),
- * "fused" / "fused-resident" (a shared-src1 group), "moe" (MUL_MAT_ID), "fa" (FLASH_ATTN_EXT).
- * NULL returns the total. cpu_fallbacks counts ops computed on the CPU after a device failure;
- * such an op still counts once on its route. Both are cumulative over the backend's life. */
-MI355X_API long ggml_backend_mi355x_route_ops(ggml_backend_mi355x_t backend, const char * route);
-MI355X_API long ggml_backend_mi355x_cpu_fallbacks(ggml_backend_mi355x_t backend);
-
-/* MoE residency (ggml-rocket.h:39-57): experts whose stack was ingested into the HBM expert
- * cache, and experts run from a per-call upload (an unnamed stack, or one over budget). */
-MI355X_API void ggml_backend_mi355x_moe_stats(ggml_backend_mi355x_t backend, long * n_resident,
-                                              long * n_streamed);
-
-/* Device attempts / device failures / breaker bypasses of a route group ("gemm", "fa", "moe"). */
-MI355X_API void ggml_backend_mi355x_route_stats(ggml_backend_mi355x_t backend, const char * group,
-                                                long * attempts, long * failures, long * bypassed);
-
-/* Host-side fault injection for tests: the next `n` device attempts of route group `group`
- * ("gemm", "fa", "moe") report a device failure without launching anything. */
-MI355X_API void ggml_backend_mi355x_inject_faults(ggml_backend_mi355x_t backend, const char * group, int n);
-
-/* The weight-cache key of a weight tensor (ggml-rocket.cpp:4154-4222): its name without this
- * backend's "MI355X#...#<idx>" copy grammar, plus "@" and a 64-bit fingerprint of sixteen
- * 64-byte windows of its bytes, size and type when it has data. Empty for an unnamed tensor or
- * a ggml auto-name ("leaf_<n>", "node_<n>"). Writes at most `cap` bytes; returns the length. */
-MI355X_API int ggml_backend_mi355x_weight_key(const mi355x_tensor * t, char * out, int cap);
-
-/* A byte-size knob in MB, parsed strictly (ggml-rocket.cpp:7932-7964): digits only, no sign, no
- * suffix, no overflow. Returns true and sets *bytes on success; "0" means unlimited. */
-MI355X_API bool ggml_backend_mi355x_parse_mb(const char * text, size_t * bytes);
+/* Replaces ggml_backend_rocket_reg (ggml-rocket.h:90-91): the registry entry ggml's loader and
+ * device enumeration use. Its get_proc_address also answers
+ * "ggml_backend_rocket_register_weight_source" and "ggml_backend_mi355x_register_weight_source"
+ * with void (*)(const struct ggml_tensor *, const void * data, size_t nbytes) (API.md:280-314). */
+GGML_BACKEND_API ggml_backend_reg_t ggml_backend_mi355x_reg(void);
 
 #ifdef __cplusplus
 }

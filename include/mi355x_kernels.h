@@ -1,6 +1,6 @@
 /* SPDX-License-Identifier: MIT
  *
- * mi355x_kernels.h -- the C ABI of the gfx950 prefill kernels (libggml-mi355x.so).
+ * mi355x_kernels.h -- the C ABI of the gfx950 prefill kernels (libmi355x.so).
  *
  * This is the device library of the backend: what librocketnpu is to the reference (its call
  * sites in ggml-rocket.cpp are cited per entry). Plain pointers, sizes and an opaque stream;

@@ -3,7 +3,7 @@
  *
  * This file is test infrastructure. Only tests/, __graft_entry__.smoke() and the cpu_baseline
  * leg of bench.py load it, and only to check or time the HIP path. The product library
- * (libggml-mi355x.so) never links, loads or calls it.
+ * (libmi355x.so) never links, loads or calls it.
  *
  * What it restates, each from the reference file:line it follows:
  *   - fp16 <-> fp32 conversion, round-to-nearest-even (the semantics of ggml_fp32_to_fp16 that

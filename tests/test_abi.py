@@ -9,15 +9,22 @@ import ggml_mi355x as mx
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 
 
-def declared_functions():
+# include/ggml-mi355x.h is the ggml-typed public API: it is implemented by the ggml adapter
+# (ggml-rocket_amd/ggml/ggml-mi355x.cpp), which builds only against a host's ggml headers, so it
+# is checked against that source here rather than against libmi355x.so
+GGML_FACING = "ggml-mi355x.h"
+ADAPTER = os.path.join(ROOT, "ggml-rocket_amd", "ggml", "ggml-mi355x.cpp")
+
+
+def declared_functions(headers=None):
     names = []
     for h in sorted(os.listdir(os.path.join(ROOT, "include"))):
-        if not h.endswith(".h"):
+        if not h.endswith(".h") or (headers is None and h == GGML_FACING) or (headers and h not in headers):
             continue
         text = open(os.path.join(ROOT, "include", h)).read()
         text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
         text = "\n".join(l for l in text.splitlines() if not l.lstrip().startswith("#"))
-        for m in re.finditer(r"MI355X_API\s+[^;{(]*?\b(\w+)\s*\(", text):
+        for m in re.finditer(r"(?:MI355X_API|GGML_BACKEND_API)\s+[^;{(]*?\b(\w+)\s*\(", text):
             names.append(m.group(1))
     return names
 
@@ -25,7 +32,7 @@ def declared_functions():
 def test_headers_declare_entry_points():
     names = declared_functions()
     assert len(names) >= 30, names
-    assert "mi355x_gemm" in names and "ggml_backend_mi355x_graph_compute" in names
+    assert "mi355x_gemm" in names and "mi355x_backend_graph_compute" in names
 
 
 def test_library_exports_every_declared_symbol():
@@ -37,3 +44,20 @@ def test_library_exports_every_declared_symbol():
 def test_library_path_is_in_tree():
     assert os.path.dirname(os.path.abspath(mx.LIB_PATH)).startswith(ROOT)
     assert isinstance(mx.lib(), ctypes.CDLL)
+
+
+def test_ggml_adapter_defines_the_public_api():
+    """Every function of the ggml-facing header (the reference's ggml-rocket.h:23-91 under this
+    backend's name) is defined in the adapter, which also carries the loader entry."""
+    names = declared_functions([GGML_FACING])
+    assert set(names) == {"ggml_backend_mi355x_init", "ggml_backend_is_mi355x", "ggml_backend_mi355x_set_n_threads",
+                          "ggml_backend_mi355x_moe_stats", "ggml_backend_mi355x_route_ops",
+                          "ggml_backend_mi355x_cpu_fallbacks", "ggml_backend_mi355x_reg"}, names
+    src = open(ADAPTER).read()
+    for n in names:
+        assert re.search(r"^\S.*\b" + n + r"\s*\([^;]*\)\s*\{", src, flags=re.M), n
+    assert "GGML_BACKEND_DL_IMPL(" in src
+    # every host-layer call the adapter makes is exported by the core library
+    L = mx.lib()
+    used = set(re.findall(r"\b(mi355x_backend_\w+)\s*\(", src))
+    assert used and all(hasattr(L, n) for n in used), sorted(n for n in used if not hasattr(L, n))

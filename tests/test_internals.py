@@ -98,14 +98,14 @@ def test_breaker_transitions():
 def test_instance_lifecycle():
     L = mx.host()
     a, b = mx.Backend(), mx.Backend()
-    assert L.ggml_backend_is_mi355x(a.h) and L.ggml_backend_is_mi355x(b.h)
-    assert L.ggml_backend_mi355x_get_n_threads(a.h) == 5
-    L.ggml_backend_mi355x_set_n_threads(a.h, 12)
-    assert L.ggml_backend_mi355x_get_n_threads(a.h) == 8        # clamped
-    L.ggml_backend_mi355x_set_n_threads(a.h, 3)
-    assert L.ggml_backend_mi355x_get_n_threads(a.h) == 3
+    assert L.mi355x_backend_is(a.h) and L.mi355x_backend_is(b.h)
+    assert L.mi355x_backend_get_n_threads(a.h) == 5
+    L.mi355x_backend_set_n_threads(a.h, 12)
+    assert L.mi355x_backend_get_n_threads(a.h) == 8        # clamped
+    L.mi355x_backend_set_n_threads(a.h, 3)
+    assert L.mi355x_backend_get_n_threads(a.h) == 3
     assert a.route_ops() == 0 and a.cpu_fallbacks() == 0 and a.moe_stats() == (0, 0)
-    assert L.ggml_backend_mi355x_name() == b"MI355X"
+    assert L.mi355x_backend_name() == b"MI355X"
     a.free()
     b.free()
 

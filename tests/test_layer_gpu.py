@@ -2,7 +2,7 @@
 
 The headline workload's exact integrated path: named Q4_K host weights (quantized by the oracle
 from N(0, 0.02)), M = 512 tokens, d 4096, FFN 14336, 32 query / 8 KV heads of 128, handed to
-ggml_backend_mi355x_graph_compute in the splits the ggml scheduler forms for one layer:
+mi355x_backend_graph_compute in the splits the ggml scheduler forms for one layer:
 {Q, K, V} (a fused group), {FLASH_ATTN_EXT causal at n_kv 2048, O} (O reads the attention's dst
 through a view), {gate, up} (a fused group) and {down} (K = 14336). It runs under both
 QUANT_RESIDENT routes (1: weights decoded once to resident fp16, "fused-resident" /

@@ -90,9 +90,9 @@ def test_placement(label, want, fn):
 def test_supports_buft():
     """ggml-rocket.cpp:7795-7797: host buffers and CPU_REPACK (whose weights are claimed only
     through registered original bytes)."""
-    assert mx.host().ggml_backend_mi355x_supports_buft(mx.BUF_HOST)
-    assert mx.host().ggml_backend_mi355x_supports_buft(mx.BUF_REPACK)
-    assert not mx.host().ggml_backend_mi355x_supports_buft(mx.BUF_OTHER)
+    assert mx.host().mi355x_backend_supports_buft(mx.BUF_HOST)
+    assert mx.host().mi355x_backend_supports_buft(mx.BUF_REPACK)
+    assert not mx.host().mi355x_backend_supports_buft(mx.BUF_OTHER)
 
 
 def _repacked_q4k(g, name="blk.0.ffn_down.weight"):
