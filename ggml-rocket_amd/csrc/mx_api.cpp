@@ -217,7 +217,7 @@ MI355X_API int mi355x_mul_mat(int wtype, const void * w_dev, int64_t N, int64_t 
 
 static int fa_check(const mi355x_fa_args * a) {
     if (!a || !a->q_dev || !a->k_dev || !a->v_dev || !a->dst_dev) return MI355X_E_ARG;
-    if (!mx::fa_dims_supported(a->D, a->DV)) return MI355X_E_UNSUPPORTED;   // D <= 192, DV <= 128, % 8
+    if (!mx::fa_dims_supported(a->D, a->DV)) return MI355X_E_UNSUPPORTED;   // dk, dv <= 256, multiples of 8
     if (a->max_bias != 0.0f) return MI355X_E_UNSUPPORTED;
     if (a->T < 0 || a->H <= 0 || a->HK <= 0 || a->KV < 0 || a->H % a->HK) return MI355X_E_ARG;
     if (a->q_nb1 % 4 || a->q_nb2 % 4 || !aligned(a->q_dev, 16)) return MI355X_E_ARG;
@@ -279,7 +279,7 @@ MI355X_API int mi355x_flash_attn_auto_split(const mi355x_fa_args * a) {
                p.multiProcessorCount > 0) ? p.multiProcessorCount : 256;
     }
     // one block per CU (their LDS rings take 128 KB); fill the chip, but keep at least 12 key
-    // tiles a split: a split costs a partial-output round trip and a combine launch
+    // tiles a split: a split costs a partial-output round trip and the combine launch
     int ns = nb > 0 ? (cus + nb - 1) / nb : 1;
     const int max_by_len = ntiles / 12 > 0 ? ntiles / 12 : 1;
     if (ns > max_by_len) ns = max_by_len;

@@ -110,11 +110,12 @@ __device__ __forceinline__ float wave_sum(float v) {
 }
 
 // Blocks are handed to the 8 XCDs round-robin by linear id. Renumber so that each XCD gets a
-// contiguous run of tile ids: tiles that share a weight panel then share one L2.
+// contiguous run of logical ids (XCD x takes ids [x q + min(x, r), ...) of its q or q + 1
+// blocks, q = n / 8, r = n % 8; a bijection for any n): work items that share an operand panel
+// then share one XCD's L2.
 __device__ __forceinline__ int xcd_tile(int bid, int nblocks) {
-    const int per = nblocks / 8;
-    if (per == 0 || (nblocks % 8)) return bid;
-    return (bid % 8) * per + bid / 8;
+    const int q = nblocks / 8, r = nblocks % 8, x = bid % 8;
+    return x * q + min(x, r) + bid / 8;
 }
 
 // Multiplies a wave's MI x NJ accumulator tiles (32x32 MFMA output layout: element e of tile

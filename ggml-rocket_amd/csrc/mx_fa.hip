@@ -44,6 +44,7 @@ constexpr int FA_QW = 32;       // query rows per wave task
 constexpr int FA_TASKS = 4;     // wave tasks (head, 32-query tile) per block
 constexpr int FA_LDS_MAX = 160 * 1024;
 constexpr int FA_CLS_RESERVE = 2048;   // LDS kept beside the ring for the class rows (KV <= 32768)
+constexpr float FA_LAZY = 8.0f / 1.4426950408889634f;   // ln(2^8): how far a score may pass the running max
 
 // DK: the Q.K contraction (Q and K head dim), DV: the V and output head dim (DK > DV for the
 // non-absorbed MLA of DeepSeek-style models, 192 / 128).
@@ -227,12 +228,14 @@ fa_kernel(FaArgs a) {
     const int wave_s = __builtin_amdgcn_readfirstlane(wave);
     const int slot_task = wave % FA_TASKS, par = wave / FA_TASKS;
 
-    // block -> (kv head, group of 4 wave tasks, kv split); two waves per task
+    // block -> (kv head, group of 4 wave tasks, kv split); two waves per task. Logical ids are
+    // kv-head major and spread so that each XCD takes a contiguous run of them: the blocks of a
+    // kv head read its K and V through one L2.
     const int g = a.H / a.HK;
     const int n_ttiles = (a.T + FA_QW - 1) / FA_QW;
     const int tasks = g * n_ttiles;
     const int bph = (tasks + FA_TASKS - 1) / FA_TASKS;   // blocks per kv head
-    int b = blockIdx.x;
+    int b = xcd_tile(blockIdx.x, gridDim.x);
     const int split = b % a.nsplit;
     b /= a.nsplit;
     const int hk = b / bph;
@@ -244,6 +247,26 @@ fa_kernel(FaArgs a) {
     const int tq = qt * FA_QW + lq;                      // this lane's query token
     const bool qok = active && tq < a.T;
     const int nkt = a.kvp / FA_BKV;
+
+    // Q rows are loaded first: their latency then overlaps the range scan and the first DMA
+    float4v qraw[KSTEPS][2];
+    {
+        const float * q = a.q + (int64_t)h * a.q_nb2 + (int64_t)(qok ? tq : 0) * a.q_nb1;
+#pragma unroll
+        for (int s = 0; s < KSTEPS; s++) {
+            const int d = 16 * s + 8 * lg;   // < DK
+            qraw[s][0] = float4v{0, 0, 0, 0};
+            qraw[s][1] = float4v{0, 0, 0, 0};
+            if (qok && d < a.dk) {
+                qraw[s][0] = *(const float4v *)(q + d);
+                qraw[s][1] = *(const float4v *)(q + d + 4);
+            }
+        }
+    }
+    // Parity-0 waves issue first on their SIMD: both waves of a SIMD reach each step's score
+    // MFMAs together, and the priority lets one run them while the other waits, so afterwards
+    // one wave's softmax overlaps the other's MFMAs instead of both competing for each unit.
+    if (par == 0) __builtin_amdgcn_s_setprio(1);
 
     // the block's key tiles: the union of its tasks' non-skipped ranges (a cooperative scan of
     // the class rows, 16 entries per load), then this split's share
@@ -335,22 +358,15 @@ fa_kernel(FaArgs a) {
 #pragma unroll
         for (int p = 0; p < FA_NS; p++) issue(p);
     }
-    // the Q load runs while the first tiles land
     // ---- Q: scaled, range-guarded, converted to fp16 in the B-operand layout ----
     half8 qf[KSTEPS];
     float qfac = 1.0f;
     {
-        const float * q = a.q + (int64_t)h * a.q_nb2 + (int64_t)(qok ? tq : 0) * a.q_nb1;
         float amax = 0.0f;
         float qv[KSTEPS][8];
 #pragma unroll
         for (int s = 0; s < KSTEPS; s++) {
-            const int d = 16 * s + 8 * lg;   // < DK
-            float4v x0 = {0, 0, 0, 0}, x1 = {0, 0, 0, 0};
-            if (qok && d < a.dk) {
-                x0 = *(const float4v *)(q + d);
-                x1 = *(const float4v *)(q + d + 4);
-            }
+            const float4v x0 = qraw[s][0], x1 = qraw[s][1];
 #pragma unroll
             for (int e = 0; e < 4; e++) {
                 qv[s][e] = x0[e] * a.scale;
@@ -387,17 +403,56 @@ fa_kernel(FaArgs a) {
                 (active && i < ntl) ? (uint32_t)cls_w[tile] : (uint32_t)FA_TILE_SKIP);
             if (cls != FA_TILE_SKIP) {
                 // ---- S^T = K . Q^T for 64 keys: two 32-key blocks ----
+                // Every K fragment read of the tile is issued before the first MFMA, so the LDS
+                // latency is paid once per tile rather than once per MFMA; the scheduling barriers
+                // keep the compiler from interleaving each read with the MFMA that consumes it.
+                // (DK <= 128; the wider heads, whose fragments do not fit the register budget
+                // twice over, read and multiply one 32-key block at a time.)
                 float16v sacc[2];
+                auto kfrag = [&](int kb, int s2) {
+                    return *(const half8 *)(ks + (kb * 32 + lq) * (DK * 2) + (C::kchunk(kb * 32 + lq, 2 * s2 + lg) << 4));
+                };
+                if constexpr (DK <= 128) {
+                    half8 kf[2][KSTEPS];
 #pragma unroll
-                for (int kb = 0; kb < 2; kb++) {
-                    half8 kf[KSTEPS];
+                    for (int kb = 0; kb < 2; kb++)
 #pragma unroll
-                    for (int s2 = 0; s2 < KSTEPS; s2++)
-                        kf[s2] = *(const half8 *)(ks + (kb * 32 + lq) * (DK * 2) + (C::kchunk(kb * 32 + lq, 2 * s2 + lg) << 4));
+                        for (int s2 = 0; s2 < KSTEPS; s2++) kf[kb][s2] = kfrag(kb, s2);
+                    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-                    for (int e = 0; e < 16; e++) sacc[kb][e] = 0.0f;
+                    for (int kb = 0; kb < 2; kb++) {
 #pragma unroll
-                    for (int s2 = 0; s2 < KSTEPS; s2++) sacc[kb] = mfma32(kf[s2], qf[s2], sacc[kb]);
+                        for (int e = 0; e < 16; e++) sacc[kb][e] = 0.0f;
+#pragma unroll
+                        for (int s2 = 0; s2 < KSTEPS; s2++) sacc[kb] = mfma32(kf[kb][s2], qf[s2], sacc[kb]);
+                    }
+                    __builtin_amdgcn_sched_barrier(0);
+                } else {
+#pragma unroll
+                    for (int kb = 0; kb < 2; kb++) {
+                        half8 kf[KSTEPS];
+#pragma unroll
+                        for (int s2 = 0; s2 < KSTEPS; s2++) kf[s2] = kfrag(kb, s2);
+#pragma unroll
+                        for (int e = 0; e < 16; e++) sacc[kb][e] = 0.0f;
+#pragma unroll
+                        for (int s2 = 0; s2 < KSTEPS; s2++) sacc[kb] = mfma32(kf[s2], qf[s2], sacc[kb]);
+                    }
+                }
+                // the V^T fragments of the first two P.V steps do not depend on the softmax: issue
+                // their reads now, so they land while the scores are computed (DK, DV <= 128; the
+                // wider builds have no registers to spare for them)
+                constexpr bool EARLY_V = DK <= 128 && DV <= 128;
+                auto vfrag = [&](int s2, int db) {
+                    return *(const half8 *)(vt + (db * 32 + lq) * 128 + (((2 * s2 + lg) ^ xv) << 4));
+                };
+                half8 vfa[EARLY_V ? 2 : 1][DBLK];
+                if constexpr (EARLY_V) {
+#pragma unroll
+                    for (int s2 = 0; s2 < 2; s2++)
+#pragma unroll
+                        for (int db = 0; db < DBLK; db++) vfa[s2][db] = vfrag(s2, db);
+                    __builtin_amdgcn_sched_barrier(0);
                 }
                 // ---- scores: scale back, cap, mask, key bound (each a wave-uniform case) ----
                 if (q_scaled) {
@@ -448,43 +503,80 @@ fa_kernel(FaArgs a) {
 #pragma unroll
                     for (int ii = 0; ii < 16; ii++) mt = fmaxf(mt, sacc[kb][ii]);
                 mt = fmaxf(mt, __shfl_xor(mt, 32, WAVE));
-                const float m_new = fmaxf(m_run, mt);
-                // No lane-divergent branch here: the P.V MFMA reads every lane's operands, so a
-                // lane whose keys are all masked so far must still supply finite P (zeros).
-                const float m_use = (m_new == -INFINITY) ? 0.0f : m_new;
-                const float alpha = (m_run == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f((m_run - m_use) * LOG2E);
-                const float mb = m_use * LOG2E;
-                float psum = 0.0f;
-#pragma unroll
-                for (int kb = 0; kb < 2; kb++)
-#pragma unroll
-                    for (int ii = 0; ii < 16; ii++) {
-                        // v_exp_f32: exp2(-inf) = 0; results below the fp32 normal range flush to 0
-                        const float p = __builtin_amdgcn_exp2f(fmaf(sacc[kb][ii], LOG2E, -mb));
-                        sacc[kb][ii] = p;
-                        psum += p;
-                    }
-                l_run = l_run * alpha + psum;
-                m_run = m_new;
-                if (__any(alpha != 1.0f)) {   // once the running max settles, most tiles skip this
+                // The running max moves only when a score passes it by more than FA_LAZY (2^8 in
+                // P): P then stays below 256, well inside fp16 and the fp32 sums, and most tiles
+                // skip the rescale of O. When it moves, every row of the wave takes its exact max.
+                // No lane-divergent branch: the P.V MFMA reads every lane's operands, so a lane
+                // whose keys are all masked so far must still supply finite P (zeros).
+                if (__any(mt > m_run + FA_LAZY)) {   // false for a row with every key masked
+                    const float m_new = fmaxf(m_run, mt);
+                    const float alpha = (m_run == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f((m_run - m_new) * LOG2E);
+                    m_run = m_new;
+                    l_run *= alpha;
 #pragma unroll
                     for (int db = 0; db < DBLK; db++)
 #pragma unroll
                         for (int e = 0; e < 16; e++) o[db][e] *= alpha;
                 }
+                const float mb = (m_run == -INFINITY) ? 0.0f : m_run * LOG2E;
+#pragma unroll
+                for (int kb = 0; kb < 2; kb++)
+#pragma unroll
+                    for (int ii = 0; ii < 16; ii++)
+                        // v_exp_f32: exp2(-inf) = 0; results below the fp32 normal range flush to 0
+                        sacc[kb][ii] = __builtin_amdgcn_exp2f(fmaf(sacc[kb][ii], LOG2E, -mb));
                 // ---- O^T += V^T . P^T, 4 steps of 16 keys; V^T's key slots follow vt_pos ----
+                if constexpr (EARLY_V) {
+                    half8 pf[4];
 #pragma unroll
-                for (int s2 = 0; s2 < 4; s2++) {
-                    const int kb = s2 / 2, hs = s2 % 2;
-                    half8 pf;
+                    for (int s2 = 0; s2 < 4; s2++)
 #pragma unroll
-                    for (int e = 0; e < 8; e++) pf[e] = (_Float16)sacc[kb][8 * hs + e];
-                    half8 vf[DBLK];
+                        for (int e = 0; e < 8; e++) pf[s2][e] = (_Float16)sacc[s2 / 2][8 * (s2 % 2) + e];
+                    // the row sum of the P that the MFMA multiplies (its fp16 values), two per
+                    // v_dot2_f32_f16 with fp32 accumulation
+                    float psum = 0.0f;
+                    const half2v one2 = {(_Float16)1.0f, (_Float16)1.0f};
 #pragma unroll
-                    for (int db = 0; db < DBLK; db++)
-                        vf[db] = *(const half8 *)(vt + (db * 32 + lq) * 128 + (((2 * s2 + lg) ^ xv) << 4));
+                    for (int s2 = 0; s2 < 4; s2++)
 #pragma unroll
-                    for (int db = 0; db < DBLK; db++) o[db] = mfma32(vf[db], pf, o[db]);
+                        for (int e = 0; e < 4; e++)
+                            psum = __builtin_amdgcn_fdot2(half2v{pf[s2][2 * e], pf[s2][2 * e + 1]}, one2, psum, false);
+                    l_run += psum;
+                    // the last two steps' fragments are read while the first two steps multiply
+                    half8 vfb[2][DBLK];
+#pragma unroll
+                    for (int s2 = 0; s2 < 2; s2++)
+#pragma unroll
+                        for (int db = 0; db < DBLK; db++) vfb[s2][db] = vfrag(2 + s2, db);
+                    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                    for (int s2 = 0; s2 < 2; s2++)
+#pragma unroll
+                        for (int db = 0; db < DBLK; db++) o[db] = mfma32(vfa[s2][db], pf[s2], o[db]);
+#pragma unroll
+                    for (int s2 = 0; s2 < 2; s2++)
+#pragma unroll
+                        for (int db = 0; db < DBLK; db++) o[db] = mfma32(vfb[s2][db], pf[2 + s2], o[db]);
+                    __builtin_amdgcn_sched_barrier(0);
+                } else {
+                    float psum = 0.0f;
+#pragma unroll
+                    for (int kb = 0; kb < 2; kb++)
+#pragma unroll
+                        for (int ii = 0; ii < 16; ii++) psum += sacc[kb][ii];
+                    l_run += psum;
+#pragma unroll
+                    for (int s2 = 0; s2 < 4; s2++) {
+                        const int kb = s2 / 2, hs = s2 % 2;
+                        half8 pf;
+#pragma unroll
+                        for (int e = 0; e < 8; e++) pf[e] = (_Float16)sacc[kb][8 * hs + e];
+                        half8 vf[DBLK];
+#pragma unroll
+                        for (int db = 0; db < DBLK; db++) vf[db] = vfrag(s2, db);
+#pragma unroll
+                        for (int db = 0; db < DBLK; db++) o[db] = mfma32(vf[db], pf, o[db]);
+                    }
                 }
             }
         }
@@ -515,8 +607,7 @@ fa_kernel(FaArgs a) {
             ob[(DBLK * 16 + 1) * WAVE + lane] = l_run;
         }
         __syncthreads();
-        if (par == 1) return;
-        {
+        if (par == 0) {
             const float m1 = ob[(DBLK * 16) * WAVE + lane], l1 = ob[(DBLK * 16 + 1) * WAVE + lane];
             const float M = fmaxf(m_run, m1);
             const float a0 = (m_run == -INFINITY) ? 0.0f : __expf(m_run - M);
@@ -531,6 +622,8 @@ fa_kernel(FaArgs a) {
     }
 
     const float l_tot = l_run + __shfl_xor(l_run, 32, WAVE);
+    const bool holder = C::PAR == 1 || par == 0;   // the wave holding its task's merged result
+    if (!holder) return;
     if (a.nsplit == 1) {
         if (!qok) return;
         const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;

@@ -77,7 +77,7 @@ hipError_t launch_moe(int wt, const MoeArgs & a, hipStream_t st);
 
 int fa_blocks_per_split(const FaArgs & a);
 int fa_prep_blocks(const FaArgs & a);
-bool fa_dims_supported(int dk, int dv);   // fa_pad_dims: dk <= 192, dv <= 128, multiples of 8
+bool fa_dims_supported(int dk, int dv);   // fa_pad_dims: dk, dv <= 256, multiples of 8
 size_t fa_max_kv(int dk, int dv);          // the longest KV range one launch takes
 hipError_t launch_fa(const FaArgs & a, hipStream_t st);
 
