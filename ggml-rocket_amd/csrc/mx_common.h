@@ -78,7 +78,7 @@ __device__ __forceinline__ float mul_rn(float a, float b) {
 #pragma clang fp contract(off)
         p = a * b;
     }
-    asm volatile("" : "+v"(p));
+    asm("" : "+v"(p));
     return p;
 }
 __device__ __forceinline__ float sub_rn(float a, float b) {
@@ -87,14 +87,14 @@ __device__ __forceinline__ float sub_rn(float a, float b) {
 #pragma clang fp contract(off)
         d = a - b;
     }
-    asm volatile("" : "+v"(d));
+    asm("" : "+v"(d));
     return d;
 }
 // a * b + c rounded once to f32, pinned there like mul_rn (no fold into an f16 conversion). Only
 // for operands whose product is exact in f32, where it equals sub_rn(mul_rn(a, b), -c).
 __device__ __forceinline__ float fma_rn(float a, float b, float c) {
     float r = __builtin_fmaf(a, b, c);
-    asm volatile("" : "+v"(r));
+    asm("" : "+v"(r));
     return r;
 }
 
@@ -143,7 +143,7 @@ __device__ __forceinline__ void scale_rows(Acc (&acc)[MI][NJ], const float * sca
 #pragma unroll
     for (int i = 0; i < MI; i++)
 #pragma unroll
-        for (int j = 0; j < NJ; j++) asm volatile("" : "+v"(acc[i][j]));
+        for (int j = 0; j < NJ; j++) asm("" : "+v"(acc[i][j]));
     __builtin_amdgcn_sched_barrier(0);
 }
 

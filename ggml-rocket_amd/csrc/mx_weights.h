@@ -47,24 +47,22 @@ __host__ __device__ inline int64_t packed_weight_bytes(int wt, int64_t rows, int
 // The 6-bit (scale, min) pair j of a Q4_K block, from its 12 packed bytes held as three
 // little-endian words s0 (bytes 0-3), s1 (4-7), s2 (8-11).
 __device__ __forceinline__ void q4k_sm(int j, uint32_t s0, uint32_t s1, uint32_t s2, int & sc, int & mn) {
-    auto byte = [&](int i) -> uint32_t {
-        const uint32_t w = i < 4 ? s0 : (i < 8 ? s1 : s2);
-        return (w >> (8 * (i & 3))) & 0xFFu;
-    };
-    if (j < 4) {
-        sc = (int)(byte(j) & 63u);
-        mn = (int)(byte(j + 4) & 63u);
-    } else {
-        sc = (int)((byte(j + 4) & 0x0Fu) | ((byte(j - 4) >> 6) << 4));
-        mn = (int)((byte(j + 4) >> 4) | ((byte(j) >> 6) << 4));
-    }
+    // pairs 0-3: 6-bit fields in bytes j (scale) and j+4 (min); pairs 4-7: the low / high nibble
+    // of byte j+4 under the top two bits of bytes j-4 (scale) and j (min). With r = j % 4 the
+    // three bytes are byte r of each word, whichever half j is in. Selects, not branches: j is
+    // uniform, and a branch here would split the caller's scheduling region.
+    const int sh = 8 * (j & 3);
+    const uint32_t lo = (s0 >> sh) & 0xFFu, mid = (s1 >> sh) & 0xFFu, hi = (s2 >> sh) & 0xFFu;
+    const uint32_t first = 0u - (uint32_t)(j < 4);   // all ones for pairs 0-3
+    sc = (int)(((lo & 63u) & first) | (((hi & 0x0Fu) | ((lo >> 6) << 4)) & ~first));
+    mn = (int)(((mid & 63u) & first) | (((hi >> 4) | ((mid >> 6) << 4)) & ~first));
 }
 
 __device__ __forceinline__ void zero_out(bool ok, u32x4 out[4]) {
-    if (!ok) {
 #pragma unroll
-        for (int i = 0; i < 4; i++) out[i] = u32x4{0, 0, 0, 0};
-    }
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int e = 0; e < 4; e++) out[i][e] = ok ? out[i][e] : 0u;
 }
 
 // The E2M1 value of an MXFP4 code, doubled (kvalues_mxfp4 of ggml-common.h): bit 3 is the sign,
@@ -207,7 +205,7 @@ template <> struct WLoad<T_Q4_K> {
             uint32_t l4 = qs[w] & 0x0F0F0F0Fu, h4 = (qs[w] >> 4) & 0x0F0F0F0Fu;   // nibbles as bytes
             // opaque to the compiler, so each byte converts with one v_cvt_f32_ubyteN instead of
             // a 4-bit extract folded from the mask plus a conversion
-            asm volatile("" : "+v"(l4), "+v"(h4));
+            asm("" : "+v"(l4), "+v"(h4));
             float fl[4], fh[4];
 #pragma unroll
             for (int i = 0; i < 4; i++) {

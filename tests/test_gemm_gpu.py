@@ -227,20 +227,25 @@ def test_pack_act_tiled_bitexact(mx):
 
 # Every tile configuration of mi355x_gemm, forced through MI355X_GEMM_CFG, on a ragged fused
 # launch (M and both N not multiples of any tile). Configurations 4-15 are the LDS-DMA kernels,
-# which take fp16 weights only, row-major (F16) or tiled (F16_T).
-N_GEMM_CFGS = 16
+# which take fp16 weights only, row-major (F16) or tiled (F16_T); 16-19 the Q4_K kernel with
+# every operand by DMA (K % 256 == 0, Q4_K only).
+N_GEMM_CFGS = 20
 FIRST_DMA_CFG = 4
+FIRST_QDMA_CFG = 16
 F16_T = 0x101
+QUANT = (O.Q4_K, O.MXFP4, O.Q8_0, O.Q6_K)
 
 
 @pytest.mark.parametrize("cfg", list(range(N_GEMM_CFGS)))
-@pytest.mark.parametrize("wtype", [O.F16, O.Q4_K, F16_T, O.MXFP4])
+@pytest.mark.parametrize("wtype", [O.F16, O.Q4_K, F16_T, O.MXFP4, O.Q8_0, O.Q6_K])
 def test_gemm_every_tile_config(mx, monkeypatch, cfg, wtype):
     import torch
-    if cfg >= FIRST_DMA_CFG and wtype in (O.Q4_K, O.MXFP4):
+    if FIRST_DMA_CFG <= cfg < FIRST_QDMA_CFG and wtype in QUANT:
         pytest.skip("the LDS-DMA configurations take fp16 weights only")
     if cfg < FIRST_DMA_CFG and wtype == F16_T:
         pytest.skip("the register-staged configurations do not read the tiled layout")
+    if cfg >= FIRST_QDMA_CFG and wtype != O.Q4_K:
+        pytest.skip("the all-DMA configurations take Q4_K weights only")
     monkeypatch.setenv("MI355X_GEMM_CFG", str(cfg))
     K, M, Ns = 1280, 300, (528, 144)
     Xf = O.fill_normal((M, K), 900 + cfg)
@@ -248,8 +253,8 @@ def test_gemm_every_tile_config(mx, monkeypatch, cfg, wtype):
     outs, refs = [], []
     for g, N in enumerate(Ns):
         W = O.fill_normal((N, K), 910 + g, 0.0, 0.02)
-        payload = O.quantize(wtype, W) if wtype in (O.Q4_K, O.MXFP4) else O.f32_to_f16_bits(W)
-        refs.append(O.mul_mat(wtype if wtype in (O.Q4_K, O.MXFP4) else O.F16, payload, Xf, N, K))
+        payload = O.quantize(wtype, W) if wtype in QUANT else O.f32_to_f16_bits(W)
+        refs.append(O.mul_mat(wtype if wtype in QUANT else O.F16, payload, Xf, N, K))
         if wtype == F16_T:
             w = mx.tile_f16(O.F16, mx.upload_weight(O.F16, payload, N, K), N, K)
         else:
