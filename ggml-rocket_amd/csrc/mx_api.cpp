@@ -247,18 +247,17 @@ static mx::FaArgs fa_lower(const mi355x_fa_args * a, int nsplit) {
 
 static size_t align256(size_t n) { return (n + 255) & ~(size_t)255; }
 
-// Workspace: V^T [HK][DV][KVp] fp16 | mask classes [T/32][cls_stride] | 256 bytes, the first 16
-// zeroed by the prep kernel | partial O [nsplit][T][H][DV] f32 and (max, sum) [nsplit][T][H][2]
-// f32 when nsplit > 1 (DV as the kernel is built).
+// Workspace: mask classes [T/32][cls_stride] | 256 bytes, the first 16 zeroed by the prep kernel |
+// partial O [nsplit][T][H][DV] f32 and (max, sum) [nsplit][T][H][2] f32 when nsplit > 1 (DV as
+// the kernel is built).
 struct FaLayout {
-    size_t vt, cls, zero, po, pml, total;
+    size_t cls, zero, po, pml, total;
 };
 static FaLayout fa_layout(const mx::FaArgs & f) {
     FaLayout L;
     const size_t nqt = (size_t)(f.T + 31) / 32;
     const size_t rows = (size_t)f.T * f.H * f.nsplit;
-    L.vt = 0;
-    L.cls = L.vt + align256((size_t)f.HK * f.DV * f.kvp * 2);
+    L.cls = 0;
     L.zero = L.cls + align256(nqt * (size_t)f.cls_stride);
     L.po = L.zero + 256;
     L.pml = L.po + (f.nsplit > 1 ? align256(rows * f.DV * 4) : 0);
@@ -305,7 +304,6 @@ MI355X_API int mi355x_flash_attn(const mi355x_fa_args * a, int nsplit,
     const FaLayout L = fa_layout(f);
     if (!workspace_dev || workspace_bytes < L.total || !aligned(workspace_dev, 256)) return MI355X_E_NOMEM;
     char * ws = (char *)workspace_dev;
-    f.vt = (uint16_t *)(ws + L.vt);
     f.cls = (uint8_t *)(ws + L.cls);
     f.kzero = (uint16_t *)(ws + L.zero);
     if (nsplit > 1) {

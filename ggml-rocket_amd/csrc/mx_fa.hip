@@ -1,6 +1,6 @@
 // SPDX-License-Identifier: MIT
-// FLASH_ATTN_EXT prefill for gfx950: online softmax in fp32 registers, K and V^T streamed into
-// LDS by DMA.
+// FLASH_ATTN_EXT prefill for gfx950: online softmax in fp32 registers, K and V streamed into LDS
+// by DMA, V^T read from the row-major V tile by gfx950's transposing LDS load.
 //
 // Semantics (ggml-rocket.cpp:5444-5691 and its reference rocket_fa_ref_f32, 5392-5442):
 //   O[t,h,:] = softmax_j( cap(scale * q[h,t].k[hk,j]) + mask[t,j] ) . v[hk,j,:],  hk = h / (H/HK)
@@ -12,21 +12,20 @@
 // for the P.V MFMA, both contractions accumulate in fp32.
 //
 // One op is two launches:
-//   fa_prep   V -> V^T [HK][DV][KVp] (keys padded to a multiple of 64 with zeros, and permuted
-//             within each 16-key group so that each lane's P^T operand keys are one 16-byte
-//             chunk, see vt_pos); the mask tile classes (per 32-query x 64-key tile: every key
-//             masked / no key masked / mixed).
+//   fa_prep   the mask tile classes (per 32-query x 64-key tile: every key masked / no key
+//             masked / mixed), and 16 zero bytes (the K and V source of padded head dims).
 //   fa        a block is 4 tasks, each 32 query rows of one head, all 4 on one KV head (GQA
 //             reuse of the LDS tiles); two waves per task take alternate key tiles and merge at
 //             the end (one wave per task, alone on its SIMD, for DV 256, whose O tile takes 128
-//             accumulators). Per 64-key tile: K [64][DK] and V^T [DV][64] arrive
-//             in LDS by global_load_lds (a 4-deep ring, two tiles landing while two are used;
-//             2-deep when four stages do not fit, for DK 192 and 256);
+//             accumulators). Per 64-key tile: K [64][DK] and V [64][DV], both row-major as in
+//             the cache, arrive in LDS by global_load_lds (a 4-deep ring, two tiles landing while
+//             two are used; 2-deep when four stages do not fit, for DK 192 and 256);
 //             tiles whose mask is -inf for all the block's queries are skipped, tiles with
 //             no mask entry read no mask. Scores are computed transposed, S^T = K . Q^T, so each
 //             lane owns one query: the row max and sum need one exchange with the partner lane
 //             (l ^ 32), and O^T = V^T . P^T keeps the same ownership, so the rescale by
-//             exp(m_old - m_new) is lane-local.
+//             exp(m_old - m_new) is lane-local. The V^T operand of that product is read from the
+//             V tile by ds_read_b64_tr_b16, which transposes 4 x 16 blocks of fp16 across lanes.
 // Head dims between the built ones (mx_fa_dims.h) run on the next larger build: K chunks past dk
 // are fetched from 16 zero bytes of the workspace (row stride 0), Q columns past dk and V columns
 // past dv are read as zero, output columns past dv are not stored.
@@ -56,7 +55,9 @@ struct FaCfg {
     static constexpr bool KXOR = (KCH & (KCH - 1)) == 0;
     static constexpr int KRPW = KCH >= 16 ? 1 : 16 / KCH;    // K rows per 256-byte bank window
     static constexpr int K_BYTES = FA_BKV * DK * 2;          // [64 keys][DK]
-    static constexpr int V_BYTES = DV * FA_BKV * 2;          // [DV][64 key slots], 128-byte rows
+    static constexpr int VCH = DV / 8;                       // 16-byte chunks per V row
+    static constexpr int VRB = DV * 2;                       // bytes per V row
+    static constexpr int V_BYTES = FA_BKV * DV * 2;          // [64 keys][DV]
     static constexpr int STAGE = K_BYTES + V_BYTES;
     // ring depth: two tiles land while two are used, when four stages fit; else two stages and
     // the next pair is fetched between the steps
@@ -83,6 +84,13 @@ struct FaCfg {
         if constexpr (KXOR) return p ^ ((r / KRPW) & (KCH - 1));
         else return (p + KCH - r % KCH) % KCH;
     }
+    // V rows swizzle their chunks by XOR with vswz(r), a multiple of 4 chunks (64 bytes): the
+    // transposing reads take 64 bytes (32 dims) from each of 4 consecutive keys per 32 lanes, and
+    // the swizzle puts those four segments in different quarters of the 256-byte bank window
+    // (V rows of 128 bytes share a window two at a time, hence r / 2 there)
+    __device__ static __forceinline__ int vswz(int r) {
+        return (4 * (VRB >= 256 ? r : r / 2)) & (VCH - 1) & ~3;
+    }
 };
 
 typedef const void __attribute__((address_space(1))) * fa_gptr_t;
@@ -99,71 +107,19 @@ __device__ __forceinline__ void fa_wait_vm_lgkm0() {
     __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (0 << 8) | ((N >> 4) << 14));
 }
 
-// Position of key r (0..15) of a 16-key group in V^T. The S^T accumulator gives lane group lg
-// the keys {4lg..4lg+3, 8+4lg..8+4lg+3} of each 16 (the MFMA D layout), so the groups are stored
-// as [0-3 | 8-11 | 4-7 | 12-15]: each lane's 8 keys of a K step are then one 16-byte chunk.
-__device__ __forceinline__ int vt_pos(int r) {
-    const int q = r / 4;
-    return 4 * ((q == 1) ? 2 : (q == 2) ? 1 : q) + (r % 4);
-}
-
 // ---------------------------------------------------------------------------------------------
-// prep: V^T and the mask classes
+// prep: the mask classes
 // ---------------------------------------------------------------------------------------------
 enum : uint8_t { FA_TILE_SKIP = 0, FA_TILE_FULL = 1, FA_TILE_MIXED = 2 };
 
-template <int D>   // D = DV, the V head dim
 __global__ void __launch_bounds__(256) fa_prep_kernel(FaArgs a) {
-    __shared__ uint16_t tile[FA_BKV][D + 2];   // +2: row stride 4 bytes off the bank period
     const int t = threadIdx.x;
     const int nkt = a.kvp / FA_BKV;
-    const int nvt = a.HK * nkt;
     const int b = blockIdx.x;
-    if (b == 0 && t < 8) a.kzero[t] = 0;   // the K source of the padded columns
-    if (b < nvt) {
-        // V^T for (hk, key tile)
-        const int hk = b / nkt, j0 = (b % nkt) * FA_BKV;
-        const uint16_t * V = a.v + (int64_t)hk * a.v_nb2;
-        constexpr int CH = D / 8;
-#pragma unroll
-        for (int i = 0; i < FA_BKV * CH / 256; i++) {
-            const int c = t + i * 256, r = c / CH, ch = c % CH;
-            const int j = j0 + r;
-            u32x4 v = {0, 0, 0, 0};
-            if (j < a.KV && 8 * ch < a.dv) v = *(const u32x4 *)(V + (int64_t)j * a.v_nb1 + 8 * ch);
-#pragma unroll
-            for (int e = 0; e < 4; e++) {
-                tile[r][8 * ch + 2 * e] = (uint16_t)(v[e] & 0xFFFFu);
-                tile[r][8 * ch + 2 * e + 1] = (uint16_t)(v[e] >> 16);
-            }
-        }
-        __syncthreads();
-        // output: row d, 8 chunks of 8 key slots; slot p holds the key r with vt_pos(r) = p
-        uint16_t * out = a.vt + ((int64_t)hk * D) * a.kvp + j0;
-#pragma unroll
-        for (int i = 0; i < D * 8 / 256; i++) {
-            const int c = t + i * 256, d = c / 8, ch = c % 8;
-            uint32_t w[4];
-#pragma unroll
-            for (int e = 0; e < 4; e++) {
-                uint32_t pair = 0;
-#pragma unroll
-                for (int h = 0; h < 2; h++) {
-                    const int p = 8 * ch + 2 * e + h;          // slot
-                    const int g16 = p / 16, s16 = p % 16;
-                    const int q = s16 / 4;                     // inverse of vt_pos within 16
-                    const int r = 16 * g16 + 4 * ((q == 1) ? 2 : (q == 2) ? 1 : q) + s16 % 4;
-                    pair |= (uint32_t)tile[r][d] << (16 * h);
-                }
-                w[e] = pair;
-            }
-            *(u32x4 *)(out + (int64_t)d * a.kvp + 8 * ch) = u32x4{w[0], w[1], w[2], w[3]};
-        }
-        return;
-    }
+    if (b == 0 && t < 8) a.kzero[t] = 0;   // the K and V source of the padded columns
     const int nqt = (a.T + FA_QW - 1) / FA_QW;
     const int nct = nqt * a.cls_stride;   // rows padded to cls_stride entries (padding: skip)
-    const int cb = b - nvt;
+    const int cb = b;
     if (cb * 4 < nct) {
         // one wave per (query tile, key tile): lane l scans row l/2, keys 32*(l%2) .. +31
         const int wave = t / WAVE, lane = t % WAVE;
@@ -248,7 +204,21 @@ fa_kernel(FaArgs a) {
     const bool qok = active && tq < a.T;
     const int nkt = a.kvp / FA_BKV;
 
-    // Q rows are loaded first: their latency then overlaps the range scan and the first DMA
+    // Q is converted once per task: the parity-0 wave loads it and, where the ring has room
+    // (four stages), hands the fp16 form to the parity-1 wave through LDS
+    constexpr bool QSHARE = C::PAR == 2 && FA_NS == 4;
+    const bool qload = !QSHARE || par == 0;
+
+    // the block's key tiles: the union of its tasks' non-skipped ranges (a cooperative scan of
+    // the class rows, 16 entries per load; at most one load per thread for KV within
+    // fa_max_kv), then this split's share. The class loads are issued before Q's, so the scan
+    // waits for them alone.
+    const int qt_first = task0 / g, qt_last = min(tasks - 1, task0 + FA_TASKS - 1) / g;
+    const int nchunk = a.cls_stride / 16;
+    const int items = (qt_last - qt_first + 1) * nchunk;
+    u32x4 cw = {0, 0, 0, 0};
+    if (t < items) cw = *(const u32x4 *)(a.cls + (int64_t)(qt_first + t / nchunk) * a.cls_stride + 16 * (t % nchunk));
+
     float4v qraw[KSTEPS][2];
     {
         const float * q = a.q + (int64_t)h * a.q_nb2 + (int64_t)(qok ? tq : 0) * a.q_nb1;
@@ -257,7 +227,7 @@ fa_kernel(FaArgs a) {
             const int d = 16 * s + 8 * lg;   // < DK
             qraw[s][0] = float4v{0, 0, 0, 0};
             qraw[s][1] = float4v{0, 0, 0, 0};
-            if (qok && d < a.dk) {
+            if (qload && qok && d < a.dk) {
                 qraw[s][0] = *(const float4v *)(q + d);
                 qraw[s][1] = *(const float4v *)(q + d + 4);
             }
@@ -268,19 +238,16 @@ fa_kernel(FaArgs a) {
     // one wave's softmax overlaps the other's MFMAs instead of both competing for each unit.
     if (par == 0) __builtin_amdgcn_s_setprio(1);
 
-    // the block's key tiles: the union of its tasks' non-skipped ranges (a cooperative scan of
-    // the class rows, 16 entries per load), then this split's share
-    const int qt_first = task0 / g, qt_last = min(tasks - 1, task0 + FA_TASKS - 1) / g;
+    // Block barriers below wait for LDS work only (lgkmcnt), never for the Q loads in flight.
     __shared__ int range_lo, range_hi;
     if (t == 0) { range_lo = nkt; range_hi = 0; }
-    __syncthreads();
+    __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0)
+    __builtin_amdgcn_s_barrier();
     {
-        const int nchunk = a.cls_stride / 16;
-        const int items = (qt_last - qt_first + 1) * nchunk;
         int mylo = nkt, myhi = 0;
         for (int it = t; it < items; it += C::THREADS) {
             const int q = qt_first + it / nchunk, c = it % nchunk;
-            const u32x4 w = *(const u32x4 *)(a.cls + (int64_t)q * a.cls_stride + 16 * c);
+            const u32x4 w = it == t ? cw : *(const u32x4 *)(a.cls + (int64_t)q * a.cls_stride + 16 * c);
             *(u32x4 *)(smem + C::LDS + (q - qt_first) * a.cls_stride + 16 * c) = w;   // kept for the loop
 #pragma unroll
             for (int e = 0; e < 16; e++)
@@ -292,7 +259,8 @@ fa_kernel(FaArgs a) {
         if (mylo < nkt) atomicMin(&range_lo, mylo);
         if (myhi > 0) atomicMax(&range_hi, myhi);
     }
-    __syncthreads();
+    __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0)
+    __builtin_amdgcn_s_barrier();
     const int lo = range_lo, hi = range_hi;
     const int span = max(0, hi - lo);
     const int per = (span + a.nsplit - 1) / a.nsplit;
@@ -312,24 +280,26 @@ fa_kernel(FaArgs a) {
     // this task's class row, copied into LDS behind the ring by the range scan above
     const uint8_t * cls_w = smem + C::LDS + (qt - qt_first) * a.cls_stride;
 
-    // DMA sources: K rows (keys, clamped to the last key) and V^T rows (dims)
-    // (chunks past dk, padding, read the zero bytes for every key: row stride 0)
+    // DMA sources: K and V rows (keys, clamped to the last key); chunks past dk / dv, padding,
+    // read the zero bytes for every key (row stride 0)
     const uint16_t * ksrc[C::PK];
-    int64_t kstr[C::PK];
+    uint32_t kreal = 0, vreal = 0;   // bit q: source q is a real column (else the zero bytes)
     const uint16_t * vsrc[C::PV];
 #pragma unroll
     for (int q = 0; q < C::PK; q++) {
         const int slot = (q * C::WAVES + wave) * WAVE + lane;
         const int r = slot / C::KCH, c = C::kchunk_inv(r, slot % C::KCH);
         const bool real = 8 * c < a.dk;
-        kstr[q] = real ? a.k_nb1 : 0;
-        ksrc[q] = real ? a.k + (int64_t)hk * a.k_nb2 + 8 * c + (int64_t)r * a.k_nb1 : a.kzero;   // + j0 * kstr per tile
+        kreal |= (uint32_t)real << q;
+        ksrc[q] = real ? a.k + (int64_t)hk * a.k_nb2 + 8 * c + (int64_t)r * a.k_nb1 : a.kzero;   // + key offset per tile
     }
 #pragma unroll
     for (int q = 0; q < C::PV; q++) {
         const int slot = (q * C::WAVES + wave) * WAVE + lane;
-        const int r = slot / 8, c = (slot % 8) ^ ((r / 2) & 7);
-        vsrc[q] = a.vt + ((int64_t)hk * DV + r) * a.kvp + 8 * c;                 // + j0 per tile
+        const int r = slot / C::VCH, c = (slot % C::VCH) ^ C::vswz(r);
+        const bool real = 8 * c < a.dv;
+        vreal |= (uint32_t)real << q;
+        vsrc[q] = real ? a.v + (int64_t)hk * a.v_nb2 + 8 * c + (int64_t)r * a.v_nb1 : a.kzero;   // + key offset per tile
     }
     const int kv_last = max(a.KV - 1, 0);
     // tile i into ring buffer i % FA_NS; past the last tile the last one is fetched again into
@@ -343,25 +313,46 @@ fa_kernel(FaArgs a) {
             const int slot = (q * C::WAVES + wave) * WAVE + lane;
             const int r = slot / C::KCH;
             const int64_t jr = (int64_t)min(j0 + r, kv_last) - r;
-            fa_dma16(ksrc[q] + jr * kstr[q], st + (q * C::WAVES + wave_s) * 1024);
+            fa_dma16(ksrc[q] + ((kreal >> q) & 1u ? jr * a.k_nb1 : 0), st + (q * C::WAVES + wave_s) * 1024);
         }
 #pragma unroll
-        for (int q = 0; q < C::PV; q++) fa_dma16(vsrc[q] + j0, st + C::K_BYTES + (q * C::WAVES + wave_s) * 1024);
+        for (int q = 0; q < C::PV; q++) {
+            const int slot = (q * C::WAVES + wave) * WAVE + lane;
+            const int r = slot / C::VCH;
+            const int64_t jr = (int64_t)min(j0 + r, kv_last) - r;
+            fa_dma16(vsrc[q] + ((vreal >> q) & 1u ? jr * a.v_nb1 : 0), st + C::K_BYTES + (q * C::WAVES + wave_s) * 1024);
+        }
     };
 
-    const int xv = (lq / 2) & 7;                    // V^T row swizzle: rows db*32 + lq
+    // V^T fragments by ds_read_b64_tr_b16, which gives lane i of each 16-lane group element e =
+    // element i % 4 of the group's source lane 4e + i / 4. Source lane s of group gq points at
+    // 4 dims (32 db + 16 (gq % 2) + 4 (s % 4) ..) of key 16 s2 + 8 h + 4 lg + s / 4, so lane i
+    // receives dim 32 db + 16 (gq % 2) + i (its row of the MFMA operand) of keys
+    // 16 s2 + 8 h + 4 lg + 0..3: elements 4h..4h+3 of the fragment, the keys the P^T operand
+    // holds there (the S^T accumulator layout). The lane's byte offset for db is
+    // vbase + ((64 db) ^ vsw): the swizzle (a multiple of 4 chunks) only flips bits of db.
+    int vbase, vsw;
+    {
+        const int sl = lane % 16, gq = lane / 16, y = sl / 4;
+        const int x = 2 * (gq % 2) + (sl % 4) / 2;   // logical chunk within the 32 dims of db
+        vsw = 16 * C::vswz(4 * lg + y);               // equals vswz of every key row it reads
+        vbase = (4 * lg + y) * C::VRB + 16 * x + 8 * (sl % 2);
+    }
 
     // Each step consumes two tiles: parity-0 waves take the even one, parity-1 waves the odd one
     // (the same query rows), and both land in the ring during the step before.
     const int nsteps = (ntl + 1) / 2;
     if (ntl > 0) {
+        issue(0);
+        issue(1);
+        if constexpr (!QSHARE)
 #pragma unroll
-        for (int p = 0; p < FA_NS; p++) issue(p);
+            for (int p = 2; p < FA_NS; p++) issue(p);
     }
     // ---- Q: scaled, range-guarded, converted to fp16 in the B-operand layout ----
     half8 qf[KSTEPS];
     float qfac = 1.0f;
-    {
+    if (qload) {
         float amax = 0.0f;
         float qv[KSTEPS][8];
 #pragma unroll
@@ -384,6 +375,30 @@ fa_kernel(FaArgs a) {
             for (int e = 0; e < 8; e++) qf[s][e] = (_Float16)(qfac == 1.0f ? qv[s][e] : qv[s][e] * inv);
     }
 
+    if constexpr (QSHARE) {
+        // through ring stages 2 and 3, whose tiles are requested once the hand-over is done:
+        // per task [KSTEPS][64 lanes] half8, then the 64 lanes' range factors
+        uint8_t * qx = smem + 2 * C::STAGE + slot_task * (KSTEPS * 1024 + 256);
+        if (par == 0) {
+#pragma unroll
+            for (int s = 0; s < KSTEPS; s++) *(half8 *)(qx + s * 1024 + lane * 16) = qf[s];
+            *(float *)(qx + KSTEPS * 1024 + lane * 4) = qfac;
+        }
+        __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0)
+        __builtin_amdgcn_s_barrier();
+        if (par == 1) {
+#pragma unroll
+            for (int s = 0; s < KSTEPS; s++) qf[s] = *(const half8 *)(qx + s * 1024 + lane * 16);
+            qfac = *(const float *)(qx + KSTEPS * 1024 + lane * 4);
+        }
+        __builtin_amdgcn_s_waitcnt(0xC07F);
+        __builtin_amdgcn_s_barrier();
+        if (ntl > 0) {
+            issue(2);
+            issue(3);
+        }
+    }
+    static_assert(!QSHARE || FA_TASKS * (KSTEPS * 1024 + 256) <= 2 * C::STAGE, "Q hand-over space");
     const bool q_scaled = __any(qfac != 1.0f);   // a row of this wave needed the Q range factor
     if (ntl > 0) {
         fa_wait_vm_lgkm0<(FA_NS - 2) * C::PER>();
@@ -396,7 +411,7 @@ fa_kernel(FaArgs a) {
             const int tile = tile0 + i;
             const int j0 = tile * FA_BKV;
             const uint8_t * ks = smem + (i % FA_NS) * C::STAGE;
-            const uint8_t * vt = ks + C::K_BYTES;
+            const uint8_t * vt = ks + C::K_BYTES;   // V [64 keys][DV], rows swizzled by vswz
             // the class is the same in every lane of the wave: read it into an SGPR, so the branch
             // below is a scalar one
             const uint32_t cls = __builtin_amdgcn_readfirstlane(
@@ -444,7 +459,14 @@ fa_kernel(FaArgs a) {
                 // wider builds have no registers to spare for them)
                 constexpr bool EARLY_V = DK <= 128 && DV <= 128;
                 auto vfrag = [&](int s2, int db) {
-                    return *(const half8 *)(vt + (db * 32 + lq) * 128 + (((2 * s2 + lg) ^ xv) << 4));
+                    typedef short v4s __attribute__((ext_vector_type(4)));
+                    typedef __attribute__((address_space(3))) v4s * lds_v4s;
+                    const uint8_t * p = vt + vbase + ((64 * db) ^ vsw) + 16 * s2 * C::VRB;
+                    const v4s lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s)(p));
+                    const v4s hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s)(p + 8 * C::VRB));
+                    typedef short v8s __attribute__((ext_vector_type(8)));
+                    const v8s w = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+                    return __builtin_bit_cast(half8, w);
                 };
                 half8 vfa[EARLY_V ? 2 : 1][DBLK];
                 if constexpr (EARLY_V) {
@@ -525,7 +547,7 @@ fa_kernel(FaArgs a) {
                     for (int ii = 0; ii < 16; ii++)
                         // v_exp_f32: exp2(-inf) = 0; results below the fp32 normal range flush to 0
                         sacc[kb][ii] = __builtin_amdgcn_exp2f(fmaf(sacc[kb][ii], LOG2E, -mb));
-                // ---- O^T += V^T . P^T, 4 steps of 16 keys; V^T's key slots follow vt_pos ----
+                // ---- O^T += V^T . P^T, 4 steps of 16 keys ----
                 if constexpr (EARLY_V) {
                     half8 pf[4];
 #pragma unroll
@@ -703,9 +725,8 @@ int fa_blocks_per_split(const FaArgs & a) {
 }
 
 int fa_prep_blocks(const FaArgs & a) {
-    const int nkt = a.kvp / FA_BKV;
     const int nqt = (a.T + FA_QW - 1) / FA_QW;
-    return a.HK * nkt + (nqt * a.cls_stride + 3) / 4;
+    return max(1, (nqt * a.cls_stride + 3) / 4);
 }
 
 // the ring plus the class rows of up to FA_TASKS query tiles
@@ -747,7 +768,7 @@ static hipError_t fa_launch_main(const FaArgs & a, int nb, hipStream_t st) {
 
 template <int DK, int DV>
 static hipError_t fa_launch_all(const FaArgs & a, int nb, hipStream_t st) {
-    hipLaunchKernelGGL(fa_prep_kernel<DV>, dim3(fa_prep_blocks(a)), dim3(256), 0, st, a);
+    hipLaunchKernelGGL(fa_prep_kernel, dim3(fa_prep_blocks(a)), dim3(256), 0, st, a);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     e = a.softcap != 0.0f ? fa_launch_main<DK, DV, true>(a, nb, st) : fa_launch_main<DK, DV, false>(a, nb, st);

@@ -41,11 +41,10 @@ struct FaArgs {
     float * dst;               // [T][H][D] via dst_nb2 (token), dst_nb1 (head)
     float * part_o;            // [nsplit][T][H][D] when nsplit > 1
     float * part_ml;           // [nsplit][T][H][2]
-    uint16_t * vt;             // workspace: V^T [HK][D][kvp], written by the prep kernel
     uint8_t * cls;             // workspace: mask class per (32-query tile, 64-key tile), rows of cls_stride
     int64_t q_nb1, q_nb2, k_nb1, k_nb2, v_nb1, v_nb2, mask_nb1, dst_nb1, dst_nb2;
-    uint16_t * kzero;          // workspace: 16 zero bytes (written by the prep kernel), the K
-                               // source of the padded columns
+    uint16_t * kzero;          // workspace: 16 zero bytes (written by the prep kernel), the K and
+                               // V source of the padded columns
     int D, DV, T, H, HK, KV, kvp, cls_stride, nsplit;   // D: Q / K head dim, DV: V / output, as
                                                         // the kernel is built (fa_pad_dims)
     int dk, dv;                // the op's head dims (<= D, DV): columns past them are padding
