@@ -45,6 +45,7 @@ constexpr int FA_LDS_MAX = 160 * 1024;
 constexpr int FA_CLS_RESERVE = 2048;   // LDS kept beside the ring for the class rows (KV <= 32768)
 constexpr float FA_LAZY = 8.0f / 1.4426950408889634f;   // ln(2^8): how far a score may pass the running max
 
+
 // DK: the Q.K contraction (Q and K head dim), DV: the V and output head dim (DK > DV for the
 // non-absorbed MLA of DeepSeek-style models, 192 / 128).
 template <int DK, int DV>
@@ -105,6 +106,98 @@ template <int N>
 __device__ __forceinline__ void fa_wait_vm_lgkm0() {
     static_assert(N >= 0 && N <= 63, "vmcnt");
     __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (0 << 8) | ((N >> 4) << 14));
+}
+
+// V^T fragments by transposing LDS reads: NF fragments of two ds_read_b64_tr_b16 each (keys
+// k..k+3 at the address, k+8..k+11 at 8 rows of VRB bytes further) and a wait for them, in one
+// statement. The intrinsic form makes the compiler wait for every K/V DMA in flight first (it
+// cannot tell these reads from the DMA's LDS writes), which would serialize each tile behind
+// the prefetch of the next; here the results are complete when the statement ends, so no
+// instruction can see the registers before their data.
+typedef int v2i __attribute__((ext_vector_type(2)));
+template <int NF, int VRB>
+__device__ __forceinline__ void fa_tr_read(const uint32_t (&a)[NF], v2i (&r)[2 * NF]);
+template <> __device__ __forceinline__ void fa_tr_read<2, 128>(const uint32_t (&a)[2], v2i (&r)[4]) {
+    asm volatile(
+        "ds_read_b64_tr_b16 %0, %4\n"
+        "ds_read_b64_tr_b16 %1, %4 offset:1024\n"
+        "ds_read_b64_tr_b16 %2, %5\n"
+        "ds_read_b64_tr_b16 %3, %5 offset:1024\n"
+        "s_waitcnt lgkmcnt(0)"
+        : "=&v"(r[0]), "=&v"(r[1]), "=&v"(r[2]), "=&v"(r[3])
+        : "v"(a[0]), "v"(a[1]));
+}
+template <> __device__ __forceinline__ void fa_tr_read<4, 128>(const uint32_t (&a)[4], v2i (&r)[8]) {
+    asm volatile(
+        "ds_read_b64_tr_b16 %0, %8\n"
+        "ds_read_b64_tr_b16 %1, %8 offset:1024\n"
+        "ds_read_b64_tr_b16 %2, %9\n"
+        "ds_read_b64_tr_b16 %3, %9 offset:1024\n"
+        "ds_read_b64_tr_b16 %4, %10\n"
+        "ds_read_b64_tr_b16 %5, %10 offset:1024\n"
+        "ds_read_b64_tr_b16 %6, %11\n"
+        "ds_read_b64_tr_b16 %7, %11 offset:1024\n"
+        "s_waitcnt lgkmcnt(0)"
+        : "=&v"(r[0]), "=&v"(r[1]), "=&v"(r[2]), "=&v"(r[3]), "=&v"(r[4]), "=&v"(r[5]), "=&v"(r[6]), "=&v"(r[7])
+        : "v"(a[0]), "v"(a[1]), "v"(a[2]), "v"(a[3]));
+}
+template <> __device__ __forceinline__ void fa_tr_read<4, 256>(const uint32_t (&a)[4], v2i (&r)[8]) {
+    asm volatile(
+        "ds_read_b64_tr_b16 %0, %8\n"
+        "ds_read_b64_tr_b16 %1, %8 offset:2048\n"
+        "ds_read_b64_tr_b16 %2, %9\n"
+        "ds_read_b64_tr_b16 %3, %9 offset:2048\n"
+        "ds_read_b64_tr_b16 %4, %10\n"
+        "ds_read_b64_tr_b16 %5, %10 offset:2048\n"
+        "ds_read_b64_tr_b16 %6, %11\n"
+        "ds_read_b64_tr_b16 %7, %11 offset:2048\n"
+        "s_waitcnt lgkmcnt(0)"
+        : "=&v"(r[0]), "=&v"(r[1]), "=&v"(r[2]), "=&v"(r[3]), "=&v"(r[4]), "=&v"(r[5]), "=&v"(r[6]), "=&v"(r[7])
+        : "v"(a[0]), "v"(a[1]), "v"(a[2]), "v"(a[3]));
+}
+template <> __device__ __forceinline__ void fa_tr_read<8, 256>(const uint32_t (&a)[8], v2i (&r)[16]) {
+    asm volatile(
+        "ds_read_b64_tr_b16 %0, %16\n"
+        "ds_read_b64_tr_b16 %1, %16 offset:2048\n"
+        "ds_read_b64_tr_b16 %2, %17\n"
+        "ds_read_b64_tr_b16 %3, %17 offset:2048\n"
+        "ds_read_b64_tr_b16 %4, %18\n"
+        "ds_read_b64_tr_b16 %5, %18 offset:2048\n"
+        "ds_read_b64_tr_b16 %6, %19\n"
+        "ds_read_b64_tr_b16 %7, %19 offset:2048\n"
+        "ds_read_b64_tr_b16 %8, %20\n"
+        "ds_read_b64_tr_b16 %9, %20 offset:2048\n"
+        "ds_read_b64_tr_b16 %10, %21\n"
+        "ds_read_b64_tr_b16 %11, %21 offset:2048\n"
+        "ds_read_b64_tr_b16 %12, %22\n"
+        "ds_read_b64_tr_b16 %13, %22 offset:2048\n"
+        "ds_read_b64_tr_b16 %14, %23\n"
+        "ds_read_b64_tr_b16 %15, %23 offset:2048\n"
+        "s_waitcnt lgkmcnt(0)"
+        : "=&v"(r[0]), "=&v"(r[1]), "=&v"(r[2]), "=&v"(r[3]), "=&v"(r[4]), "=&v"(r[5]), "=&v"(r[6]), "=&v"(r[7]), "=&v"(r[8]), "=&v"(r[9]), "=&v"(r[10]), "=&v"(r[11]), "=&v"(r[12]), "=&v"(r[13]), "=&v"(r[14]), "=&v"(r[15])
+        : "v"(a[0]), "v"(a[1]), "v"(a[2]), "v"(a[3]), "v"(a[4]), "v"(a[5]), "v"(a[6]), "v"(a[7]));
+}
+template <> __device__ __forceinline__ void fa_tr_read<8, 512>(const uint32_t (&a)[8], v2i (&r)[16]) {
+    asm volatile(
+        "ds_read_b64_tr_b16 %0, %16\n"
+        "ds_read_b64_tr_b16 %1, %16 offset:4096\n"
+        "ds_read_b64_tr_b16 %2, %17\n"
+        "ds_read_b64_tr_b16 %3, %17 offset:4096\n"
+        "ds_read_b64_tr_b16 %4, %18\n"
+        "ds_read_b64_tr_b16 %5, %18 offset:4096\n"
+        "ds_read_b64_tr_b16 %6, %19\n"
+        "ds_read_b64_tr_b16 %7, %19 offset:4096\n"
+        "ds_read_b64_tr_b16 %8, %20\n"
+        "ds_read_b64_tr_b16 %9, %20 offset:4096\n"
+        "ds_read_b64_tr_b16 %10, %21\n"
+        "ds_read_b64_tr_b16 %11, %21 offset:4096\n"
+        "ds_read_b64_tr_b16 %12, %22\n"
+        "ds_read_b64_tr_b16 %13, %22 offset:4096\n"
+        "ds_read_b64_tr_b16 %14, %23\n"
+        "ds_read_b64_tr_b16 %15, %23 offset:4096\n"
+        "s_waitcnt lgkmcnt(0)"
+        : "=&v"(r[0]), "=&v"(r[1]), "=&v"(r[2]), "=&v"(r[3]), "=&v"(r[4]), "=&v"(r[5]), "=&v"(r[6]), "=&v"(r[7]), "=&v"(r[8]), "=&v"(r[9]), "=&v"(r[10]), "=&v"(r[11]), "=&v"(r[12]), "=&v"(r[13]), "=&v"(r[14]), "=&v"(r[15])
+        : "v"(a[0]), "v"(a[1]), "v"(a[2]), "v"(a[3]), "v"(a[4]), "v"(a[5]), "v"(a[6]), "v"(a[7]));
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -458,22 +551,30 @@ fa_kernel(FaArgs a) {
                 // their reads now, so they land while the scores are computed (DK, DV <= 128; the
                 // wider builds have no registers to spare for them)
                 constexpr bool EARLY_V = DK <= 128 && DV <= 128;
-                auto vfrag = [&](int s2, int db) {
-                    typedef short v4s __attribute__((ext_vector_type(4)));
-                    typedef __attribute__((address_space(3))) v4s * lds_v4s;
-                    const uint8_t * p = vt + vbase + ((64 * db) ^ vsw) + 16 * s2 * C::VRB;
-                    const v4s lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s)(p));
-                    const v4s hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s)(p + 8 * C::VRB));
-                    typedef short v8s __attribute__((ext_vector_type(8)));
-                    const v8s w = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-                    return __builtin_bit_cast(half8, w);
+                // the fragments of NS2 consecutive 16-key steps from s2 on, for every db
+                const uint32_t vt_lds = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const uint8_t *)vt;
+                auto vfrags = [&](int s2, auto & f) {
+                    constexpr int NS2 = sizeof(f) / sizeof(f[0]);
+                    uint32_t ad[NS2 * DBLK];
+#pragma unroll
+                    for (int i = 0; i < NS2; i++)
+#pragma unroll
+                        for (int db = 0; db < DBLK; db++)
+                            ad[i * DBLK + db] = vt_lds + vbase + ((64 * db) ^ vsw) + 16 * (s2 + i) * C::VRB;
+                    v2i r[2 * NS2 * DBLK];
+                    fa_tr_read<NS2 * DBLK, C::VRB>(ad, r);
+#pragma unroll
+                    for (int i = 0; i < NS2; i++)
+#pragma unroll
+                        for (int db = 0; db < DBLK; db++) {
+                            const v2i lo = r[2 * (i * DBLK + db)], hi = r[2 * (i * DBLK + db) + 1];
+                            typedef int v4i __attribute__((ext_vector_type(4)));
+                            f[i][db] = __builtin_bit_cast(half8, v4i{lo[0], lo[1], hi[0], hi[1]});
+                        }
                 };
                 half8 vfa[EARLY_V ? 2 : 1][DBLK];
                 if constexpr (EARLY_V) {
-#pragma unroll
-                    for (int s2 = 0; s2 < 2; s2++)
-#pragma unroll
-                        for (int db = 0; db < DBLK; db++) vfa[s2][db] = vfrag(s2, db);
+                    vfrags(0, vfa);   // their wait overlaps the score MFMAs in flight
                     __builtin_amdgcn_sched_barrier(0);
                 }
                 // ---- scores: scale back, cap, mask, key bound (each a wave-uniform case) ----
@@ -564,17 +665,15 @@ fa_kernel(FaArgs a) {
                         for (int e = 0; e < 4; e++)
                             psum = __builtin_amdgcn_fdot2(half2v{pf[s2][2 * e], pf[s2][2 * e + 1]}, one2, psum, false);
                     l_run += psum;
-                    // the last two steps' fragments are read while the first two steps multiply
-                    half8 vfb[2][DBLK];
-#pragma unroll
-                    for (int s2 = 0; s2 < 2; s2++)
-#pragma unroll
-                        for (int db = 0; db < DBLK; db++) vfb[s2][db] = vfrag(2 + s2, db);
-                    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
                     for (int s2 = 0; s2 < 2; s2++)
 #pragma unroll
                         for (int db = 0; db < DBLK; db++) o[db] = mfma32(vfa[s2][db], pf[s2], o[db]);
+                    __builtin_amdgcn_sched_barrier(0);
+                    // the last two steps' fragments are read while the first two steps multiply
+                    half8 vfb[2][DBLK];
+                    vfrags(2, vfb);
+                    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
                     for (int s2 = 0; s2 < 2; s2++)
 #pragma unroll
@@ -593,11 +692,10 @@ fa_kernel(FaArgs a) {
                         half8 pf;
 #pragma unroll
                         for (int e = 0; e < 8; e++) pf[e] = (_Float16)sacc[kb][8 * hs + e];
-                        half8 vf[DBLK];
+                        half8 vf[1][DBLK];
+                        vfrags(s2, vf);
 #pragma unroll
-                        for (int db = 0; db < DBLK; db++) vf[db] = vfrag(s2, db);
-#pragma unroll
-                        for (int db = 0; db < DBLK; db++) o[db] = mfma32(vf[db], pf, o[db]);
+                        for (int db = 0; db < DBLK; db++) o[db] = mfma32(vf[0][db], pf, o[db]);
                     }
                 }
             }
