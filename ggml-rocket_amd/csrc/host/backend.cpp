@@ -246,6 +246,19 @@ struct WEntry {
     int64_t rows = 0, K = 0;
 };
 
+// What the weight cache did with the weights offered to it, per use: the fp16 image of a MUL_MAT
+// weight (F16 / F32 / BF16 weights, and quantized ones under QUANT_RESIDENT), its quantized HBM
+// layout (decoded in the GEMM on every call), and MUL_MAT_ID expert stacks. Reported at free():
+// a run whose cache filled up early reads exactly like one that held everything, except here.
+enum WeightUse { USE_F16 = 0, USE_QUANT = 1, USE_MOE = 2, N_USES = 3 };
+struct CacheOutcome {
+    long hits = 0, fills = 0, per_call = 0, nokey_calls = 0;
+    size_t bytes = 0;                             // resident bytes of this use
+    std::unordered_set<std::string> streamed;     // keys that ran from per-call scratch
+    std::string first_decline;                    // why the first weight was turned away
+    size_t used_at_decline = 0;                   // cache bytes at that moment
+};
+
 const uint64_t GUID[2] = {0x4d49333535584d49ULL, 0x2d70726566696c6cULL};
 
 }  // namespace
@@ -264,6 +277,7 @@ struct mi355x_backend {
 
     std::unordered_map<std::string, WEntry> wcache;
     size_t cache_used = 0, cache_budget = 0;
+    CacheOutcome outcome[N_USES];
 
     std::map<std::string, long> routes;
     long n_cpu_fallbacks = 0;
@@ -433,23 +447,40 @@ int build_weight(Ctx * c, int t, const void * src, int64_t rows, int64_t K, int 
 
 // A weight in device form: from the cache, or built into it, or (no key / over budget) built
 // into per-call scratch. `resident` tells which.
-int get_weight(Ctx * c, const mi355x_tensor * a, int64_t rows, int64_t K, bool want_f16, bool tiled_ok,
+int get_weight(Ctx * c, const mi355x_tensor * a, int64_t rows, int64_t K, bool want_f16, bool tiled_ok, bool moe,
                DevBuf & scratch, WEntry & out, bool & resident) {
     const int lay = dev_layout(a->type, want_f16, tiled_ok, K);
     const int64_t dbytes = mi355x_weight_bytes(lay, rows, K);
     if (dbytes < 0) return MI355X_E_ARG;
+    CacheOutcome & oc = c->outcome[moe ? USE_MOE : (lay == MI355X_F16 || lay == MI355X_F16_T) ? USE_F16 : USE_QUANT];
     std::string key = weight_key(a);
+    if (key.empty()) oc.nokey_calls++;
     if (!key.empty()) {
         key += "|L" + std::to_string(lay);
         auto it = c->wcache.find(key);
         if (it != c->wcache.end() && it->second.rows == rows && it->second.K == K && it->second.dev_type == lay) {
             out = it->second;
             resident = true;
+            oc.hits++;
             return MI355X_OK;
         }
-        if (c->cache_used + (size_t)dbytes <= c->cache_budget) {
+        const bool fits = c->cache_used + (size_t)dbytes <= c->cache_budget;
+        if (!fits && oc.first_decline.empty()) {
+            char why[160];
+            snprintf(why, sizeof why, "%.1f MB more would pass the %.0f MB budget", (double)dbytes / (1 << 20),
+                     (double)c->cache_budget / (1 << 20));
+            oc.first_decline = why;
+            oc.used_at_decline = c->cache_used;
+        }
+        if (fits) {
             void * p = nullptr;
-            if (hipMalloc(&p, (size_t)dbytes) == hipSuccess) {
+            if (hipMalloc(&p, (size_t)dbytes) != hipSuccess && oc.first_decline.empty()) {
+                char why[160];
+                snprintf(why, sizeof why, "the device allocation of %.1f MB failed", (double)dbytes / (1 << 20));
+                oc.first_decline = why;
+                oc.used_at_decline = c->cache_used;
+            }
+            if (p) {
                 const int rc = build_weight(c, a->type, a->data, rows, K, lay, p);
                 if (rc != MI355X_OK) {
                     (void)hipFree(p);
@@ -463,13 +494,17 @@ int get_weight(Ctx * c, const mi355x_tensor * a, int64_t rows, int64_t K, bool w
                 e.K = K;
                 c->wcache[key] = e;
                 c->cache_used += e.bytes;
+                oc.fills++;
+                oc.bytes += e.bytes;
                 out = e;
                 resident = true;
                 return MI355X_OK;
             }
             (void)hipGetLastError();
         }
+        oc.streamed.insert(key);
     }
+    oc.per_call++;
     TRY(scratch.ensure((size_t)dbytes));
     TRY(build_weight(c, a->type, a->data, rows, K, lay, scratch.p));
     out.dev = scratch.p;
@@ -499,7 +534,7 @@ int mul_mat_device(Ctx * c, const std::vector<mi355x_tensor *> & grp, bool want_
     for (size_t i = 0; i < grp.size(); i++) {
         const mi355x_tensor * a = grp[i]->src[0];
         bool res = false;
-        TRY(get_weight(c, a, a->ne[1], K, want_f16, true, c->wscratch[i], ws[i], res));
+        TRY(get_weight(c, a, a->ne[1], K, want_f16, true, false, c->wscratch[i], ws[i], res));
         all_resident = all_resident && res;
         outs[i].w_dev = ws[i].dev;
         outs[i].rows_total = a->ne[1];
@@ -615,7 +650,7 @@ int mul_mat_id_device(Ctx * c, mi355x_tensor * dst, bool & resident) {
     panel.ne[1] = N * E;
     panel.ne[2] = 1;
     WEntry w;
-    TRY(get_weight(c, &panel, N * E, K, false, false, c->moe_wscratch, w, resident));
+    TRY(get_weight(c, &panel, N * E, K, false, false, true, c->moe_wscratch, w, resident));
     const size_t bb = (size_t)T * ne11 * K * 4, ib = (size_t)T * U * 4, ob = (size_t)T * U * N * 4;
     TRY(c->moe_b.ensure(bb));
     TRY(c->moe_ids.ensure(ib));
@@ -729,14 +764,43 @@ MI355X_API bool mi355x_backend_is(mi355x_backend_t c) {
     return c && c->guid[0] == GUID[0] && c->guid[1] == GUID[1];
 }
 
+namespace {
+
+// The teardown report of the weight cache, one block per use that saw any weight (same tags as
+// the reference's outcome lines, ggml-rocket.cpp:5185-5303; counts and wording of this cache).
+// Weights, not calls, except where a weight has no stable name to count it by.
+void report_residency(const Ctx * c) {
+    static const char * tag[N_USES] = {"[f16-resident]", "[dq-cache]", "[moe]"};
+    static const char * form[N_USES] = {"the fp16 image", "the quantized layout", "the expert stack"};
+    for (int u = 0; u < N_USES; u++) {
+        const CacheOutcome & o = c->outcome[u];
+        const long resident = o.fills, streamed = (long)o.streamed.size();
+        if (resident + streamed + o.nokey_calls == 0) continue;
+        const double pct = resident + streamed ? 100.0 * resident / (double)(resident + streamed) : 0.0;
+        logi("%s %ld weights resident in HBM as %s (%.1f MB), %ld run from per-call uploads: %.0f%% resident; "
+             "%ld cached calls, %ld per-call builds\n",
+             tag[u], resident, form[u], (double)o.bytes / (1 << 20), streamed, pct, o.hits, o.per_call);
+        if (!o.first_decline.empty())
+            logi("%s first weight turned away at %.1f MB cached: %s\n", tag[u], (double)o.used_at_decline / (1 << 20),
+                 o.first_decline.c_str());
+        if (streamed && pct < 80.0)
+            logw("%s only %.0f%% resident: every call of a weight outside the cache uploads and converts it again, "
+                 "so this run measures the per-call path; raise MI355X_CACHE_MB if HBM allows\n", tag[u], pct);
+        if (o.nokey_calls)
+            logi("%s %ld calls had a weight with no stable name, which no cache budget can hold\n", tag[u],
+                 o.nokey_calls);
+    }
+}
+
+}  // namespace
+
 MI355X_API void mi355x_backend_free(mi355x_backend_t c) {
     if (!c) return;
     if (c->stream) (void)hipStreamSynchronize(c->stream);
     c->stage.release();
     c->pool.reset();
     for (auto & kv : c->wcache) (void)hipFree(kv.second.dev);
-    if (!c->wcache.empty())
-        logi("[weights] %zu weights resident, %.1f MB of HBM\n", c->wcache.size(), (double)c->cache_used / (1 << 20));
+    report_residency(c);
     c->wcache.clear();
     for (DevBuf * b : {&c->act, &c->a16, &c->scales, &c->out, &c->wstage, &c->wconv, &c->fa_q, &c->fa_k, &c->fa_v,
                        &c->fa_m, &c->fa_o, &c->fa_ws, &c->moe_b, &c->moe_ids, &c->moe_o, &c->moe_ws,

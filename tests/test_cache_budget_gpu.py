@@ -2,8 +2,8 @@
 the cache budget streams per call): with CACHE_MB=1 no weight fits, so every MUL_MAT decodes its
 weight into per-call scratch on route "mt" (QUANT_RESIDENT=1 included) and still matches the
 oracle; a named expert stack past the budget is streamed, and moe_stats counts each routed
-expert once over the backend's life (ggml-rocket.h:39-57). Knobs are read once per process, so
-this runs in a child process."""
+expert once over the backend's life (ggml-rocket.h:39-57); the teardown report names the outcome.
+Knobs are read once per process, so this runs in a child process."""
 import json
 import os
 import subprocess
@@ -34,3 +34,9 @@ def test_weight_cache_over_budget_streams(torch_cuda):
     # the same ids again count nothing new; new ids add only the experts not seen before
     assert out["moe_1"]["stats"] == out["moe_0"]["stats"]
     assert out["moe_2"]["distinct"] > out["moe_0"]["distinct"]
+    # the teardown report says the cache held nothing and why (ggml-rocket.cpp:5185-5303)
+    report = [ln for ln in r.stderr.splitlines() if "[mi355x]" in ln]
+    assert any("[f16-resident] 0 weights resident" in ln and "0% resident" in ln for ln in report), report
+    assert any("[f16-resident] first weight turned away at 0.0 MB cached" in ln and "1 MB budget" in ln
+               for ln in report), report
+    assert any("[moe] 0 weights resident" in ln and "1 run from per-call uploads" in ln for ln in report), report
