@@ -409,13 +409,13 @@ int d2h(Ctx * c, void * dst, const void * src, size_t n) {
 
 #define TRY(x) do { const int _rc = (x); if (_rc != MI355X_OK) return _rc; } while (0)
 
-// The device layout a weight of ggml type `t` is read in: fp16 for F16 / F32 / BF16 weights and
-// for quantized ones when the resident-fp16 form is asked for, the quantized HBM layout
-// otherwise. The fp16 form is the tiled one (MI355X_F16_T, the GEMM's fastest input) when the
+// The device layout a weight of ggml type `t` is read in: fp16 for F16 / F32 / BF16 weights, for
+// quantized ones when the resident-fp16 form is asked for, and for the types only a registered
+// host decoder reads; the quantized HBM layout otherwise. The fp16 form is the tiled one (MI355X_F16_T, the GEMM's fastest input) when the
 // caller reads it through mi355x_gemm (`tiled_ok`) and K % 64 == 0; row-major otherwise (the
 // expert kernel of MUL_MAT_ID reads rows).
 int dev_layout(int t, bool want_f16, bool tiled_ok, int64_t K) {
-    if (want_f16 || t == MI355X_TYPE_F16 || t == MI355X_TYPE_F32 || t == MI355X_TYPE_BF16)
+    if (want_f16 || !device_weight_type(t) || t == MI355X_TYPE_F16 || t == MI355X_TYPE_F32 || t == MI355X_TYPE_BF16)
         return (tiled_ok && K % 64 == 0) ? MI355X_F16_T : MI355X_F16;
     return t;   // Q8_0, Q4_K, Q6_K, MXFP4
 }
@@ -423,6 +423,23 @@ int dev_layout(int t, bool want_f16, bool tiled_ok, int64_t K) {
 // Builds the device form `lay` of `rows` rows of K values of ggml type `t` (host bytes `src`) at
 // `dst`. Uses wstage / wconv as staging.
 int build_weight(Ctx * c, int t, const void * src, int64_t rows, int64_t K, int lay, void * dst) {
+    if (!device_weight_type(t)) {
+        // a type only ggml's registered decoder reads: rows to f32 on the host (the copy workers'
+        // threads), then the f32 weight's path to fp16
+        const mi355x_to_float_fn fn = host_to_float(t);
+        const int64_t rb = row_bytes(t, K);
+        if (!fn || rb < 0) return MI355X_E_UNSUPPORTED;
+        std::vector<float> f((size_t)rows * (size_t)K);
+        const int nt = (int)std::max<int64_t>(1, std::min<int64_t>(c->n_threads, rows / 16));
+        std::vector<std::thread> th;
+        for (int i = 0; i < nt; i++)
+            th.emplace_back([&, i] {
+                for (int64_t r = i; r < rows; r += nt)
+                    fn((const uint8_t *)src + r * rb, f.data() + (size_t)r * (size_t)K, K);
+            });
+        for (auto & x : th) x.join();
+        return build_weight(c, MI355X_TYPE_F32, f.data(), rows, K, lay, dst);
+    }
     const size_t raw = (size_t)row_bytes(t, K) * (size_t)rows;
     if ((t == MI355X_TYPE_F16 || t == MI355X_TYPE_Q4_K) && lay == t) return h2d(c, dst, src, raw);
     TRY(c->wstage.ensure(raw));
@@ -942,7 +959,8 @@ static int graph_compute_nodes(mi355x_backend_t c, mi355x_tensor * const * nodes
                 }
                 const bool quant = type_is_quantized(node->src[0]->type);
                 const bool qres = c->quant_resident < 0 ? quant_resident_on() : c->quant_resident > 0;
-                const bool want_f16 = quant && qres;
+                // a type only the host decodes is always an fp16 image
+                const bool want_f16 = quant && (qres || !device_weight_type(node->src[0]->type));
                 bool resident = false;
                 guarded(c, c->brk_gemm, "MUL_MAT",
                         [&] { return mul_mat_device(c, grp, want_f16, resident); },

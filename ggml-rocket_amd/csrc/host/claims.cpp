@@ -359,7 +359,7 @@ static bool claim_mul_mat(const mi355x_tensor * op) {
     const bool a_quant = type_is_quantized(a->type);
     if (prec_declines(op)) return false;
     return a->op == MI355X_OP_NONE                      // a static leaf weight (7434-7440)
-        && device_weight_type(a->type)
+        && weight_type_ok(a->type)
         && b->type == MI355X_TYPE_F32
         && op->type == MI355X_TYPE_F32
         && is_contiguous(a) && is_contiguous(b) && is_contiguous(op)
@@ -382,7 +382,7 @@ static bool claim_mul_mat_id(const mi355x_tensor * op) {
     const int64_t K = a->ne[0], N = a->ne[1], n_tokens = id->ne[1];
     const bool a_quant = type_is_quantized(a->type);
     const bool computable = a->op == MI355X_OP_NONE
-        && device_weight_type(a->type)
+        && weight_type_ok(a->type)
         && b->type == MI355X_TYPE_F32
         && id->type == MI355X_TYPE_I32
         && op->type == MI355X_TYPE_F32
@@ -408,7 +408,9 @@ static bool claim_mul_mat_id(const mi355x_tensor * op) {
     const std::string key = weight_key(a);
     bool admitted = false;
     if (moe_preflight_decided(key, &admitted)) return admitted;
-    const size_t stack_bytes = (size_t)row_bytes(a->type, K) * (size_t)N * (size_t)n_expert;
+    // a host-decoded type is held as its fp16 image
+    const size_t rb = device_weight_type(a->type) ? (size_t)row_bytes(a->type, K) : (size_t)K * 2;
+    const size_t stack_bytes = rb * (size_t)N * (size_t)n_expert;
     return moe_preflight_admit(key, stack_bytes, a->buffer_id, a->buffer_size);
 }
 

@@ -94,7 +94,12 @@ bool decode_row_f32(int type, const void * src, float * y, int64_t n) {
                 y += 32;
             }
             return true;
-        default: return false;
+        default:
+            if (const mi355x_to_float_fn fn = host_to_float(type)) {   // ggml's own decoder
+                fn(src, y, n);
+                return true;
+            }
+            return false;
     }
 }
 

@@ -28,6 +28,12 @@ size_t registered_sources();
 // The weight types the device path decodes (HBM layouts of mx_weights.h, after a conversion to
 // fp16 for F32 and BF16).
 bool device_weight_type(int type);
+// ggml's decoder of a quantized type registered by the plugin (mi355x_backend_set_to_float), or
+// nullptr; such weights are decoded on the host into an fp16 image
+mi355x_to_float_fn host_to_float(int type);
+int register_to_float(int type, int64_t block, int64_t bytes, mi355x_to_float_fn fn);
+// a weight type some route takes: decoded on the device, or on the host by a registered decoder
+bool weight_type_ok(int type);
 
 // ---- knobs (read once; MI355X_<name> first, then the reference's ROCKET_<name>) -----------
 const char * knob_env(const char * name);   // set-but-empty counts as unset

@@ -16,6 +16,7 @@
 #include <atomic>
 
 #include "host.h"
+#include "../../../include/mi355x_kernels.h"
 
 namespace mxh {
 
@@ -57,6 +58,31 @@ void logi(const char * fmt, ...) {
 }
 
 // ---- ggml type facts: block size and block bytes (ggml's published formats) ----------------
+// Decoders registered for quantized types the kernels do not decode, with ggml's block facts.
+namespace {
+constexpr int N_TYPE_IDS = 64;
+struct HostDecoder {
+    std::atomic<mi355x_to_float_fn> fn{nullptr};
+    std::atomic<int64_t> block{0}, bytes{0};
+};
+HostDecoder g_decoders[N_TYPE_IDS];
+}  // namespace
+
+mi355x_to_float_fn host_to_float(int t) {
+    return (t >= 0 && t < N_TYPE_IDS) ? g_decoders[t].fn.load(std::memory_order_acquire) : nullptr;
+}
+
+int register_to_float(int t, int64_t block, int64_t bytes, mi355x_to_float_fn fn) {
+    if (t < 0 || t >= N_TYPE_IDS || !fn || block <= 1 || bytes <= 0) return MI355X_E_ARG;
+    if (device_weight_type(t)) return MI355X_OK;   // decoded on the device; nothing to add
+    const int64_t b = type_block(t), s = type_bytes(t);
+    if ((b > 0 && b != block) || (s > 0 && s != bytes)) return MI355X_E_ARG;
+    g_decoders[t].block.store(block, std::memory_order_release);
+    g_decoders[t].bytes.store(bytes, std::memory_order_release);
+    g_decoders[t].fn.store(fn, std::memory_order_release);
+    return MI355X_OK;
+}
+
 int64_t type_block(int t) {
     switch (t) {
         case MI355X_TYPE_F32: case MI355X_TYPE_F16: case MI355X_TYPE_BF16: case MI355X_TYPE_I8:
@@ -70,7 +96,7 @@ int64_t type_block(int t) {
         case MI355X_TYPE_IQ3_XXS: case MI355X_TYPE_IQ1_S: case MI355X_TYPE_IQ3_S: case MI355X_TYPE_IQ2_S:
         case MI355X_TYPE_IQ4_XS: case MI355X_TYPE_IQ1_M: case MI355X_TYPE_TQ1_0: case MI355X_TYPE_TQ2_0:
             return 256;
-        default: return 0;
+        default: return (t >= 0 && t < N_TYPE_IDS) ? g_decoders[t].block.load(std::memory_order_acquire) : 0;
     }
 }
 
@@ -94,7 +120,7 @@ int64_t type_bytes(int t) {
         case MI355X_TYPE_Q8_K: return 292;
         case MI355X_TYPE_IQ4_NL: return 18;
         case MI355X_TYPE_MXFP4: return 17;
-        default: return 0;
+        default: return (t >= 0 && t < N_TYPE_IDS) ? g_decoders[t].bytes.load(std::memory_order_acquire) : 0;
     }
 }
 
@@ -138,6 +164,10 @@ bool is_contiguous(const mi355x_tensor * t) {
 bool device_weight_type(int t) {
     return t == MI355X_TYPE_F16 || t == MI355X_TYPE_F32 || t == MI355X_TYPE_BF16 ||
            t == MI355X_TYPE_Q8_0 || t == MI355X_TYPE_Q4_K || t == MI355X_TYPE_Q6_K || t == MI355X_TYPE_MXFP4;
+}
+
+bool weight_type_ok(int t) {
+    return device_weight_type(t) || (type_is_quantized(t) && host_to_float(t) != nullptr);
 }
 
 // ---- knobs -----------------------------------------------------------------------------------
@@ -259,3 +289,7 @@ bool fusion_on() {
 }
 
 }  // namespace mxh
+
+MI355X_API int mi355x_backend_set_to_float(int type, int64_t block_size, int64_t type_size, mi355x_to_float_fn fn) {
+    return mxh::register_to_float(type, block_size, type_size, fn);
+}

@@ -17,6 +17,7 @@ _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "lib", "libmi355x.so")
 
 F32, F16, Q8_0, Q4_K, Q6_K, I32, BF16, MXFP4 = 0, 1, 8, 12, 14, 26, 30, 39
+Q4_0, Q4_1, Q5_0, Q5_K = 2, 3, 6, 13
 F16_T = 0x101   # the library's tiled fp16 layout (16 x 32 tiles of 1 KB); not a ggml type
 OK, E_ARG, E_DEVICE, E_UNSUPPORTED, E_NOMEM, E_IDS = 0, -1, -2, -3, -4, -5   # mi355x_status
 BLOCK = {F16: 1, F32: 1, BF16: 1, Q8_0: 32, Q4_K: 256, Q6_K: 256, MXFP4: 32}
@@ -283,8 +284,10 @@ OP_NONE, OP_MUL_MAT, OP_MUL_MAT_ID, OP_FLASH_ATTN_EXT, OP_RESHAPE, OP_VIEW, OP_P
     OP_TRANSPOSE, OP_ADD, OP_SCALE, OP_OTHER = range(11)
 BUF_NONE, BUF_HOST, BUF_REPACK, BUF_OTHER = range(4)
 STATUS_SUCCESS, STATUS_FAILED = 0, -1
-_TYPE_SIZE_ALL = {0: (1, 4), 1: (1, 2), 8: (32, 34), 12: (256, 144), 14: (256, 210), 26: (1, 4),
-                  30: (1, 2), 2: (32, 18), 13: (256, 176), 39: (32, 17)}
+# ggml's published (block values, block bytes) of the types the descriptors here may carry
+_TYPE_SIZE_ALL = {0: (1, 4), 1: (1, 2), 2: (32, 18), 3: (32, 20), 6: (32, 22), 7: (32, 24), 8: (32, 34),
+                  10: (256, 84), 11: (256, 110), 12: (256, 144), 13: (256, 176), 14: (256, 210), 26: (1, 4),
+                  30: (1, 2), 39: (32, 17)}
 
 
 class Tensor(ctypes.Structure):
@@ -297,6 +300,22 @@ Tensor._fields_ = [("type", ctypes.c_int32), ("op", ctypes.c_int32),
                    ("data", ctypes.c_void_p), ("name", ctypes.c_char * 64),
                    ("buffer_kind", ctypes.c_int32), ("buffer_id", ctypes.c_void_p),
                    ("buffer_size", ctypes.c_size_t)]
+
+
+# ggml_to_float_t: (const void * src, float * dst, int64_t n)
+TO_FLOAT_FN = ctypes.CFUNCTYPE(None, ctypes.c_void_p, ctypes.POINTER(ctypes.c_float), ctypes.c_int64)
+_decoders = {}
+
+
+def set_to_float(ttype, block, type_size, fn):
+    """Registers a row decoder for a quantized type the kernels do not decode (the plugin passes
+    ggml's to_float). `fn(src_addr, dst_float_ptr, n)`; kept alive for the process. Returns the
+    status (0 or -1)."""
+    cb = TO_FLOAT_FN(fn)
+    st = host().mi355x_backend_set_to_float(ttype, block, type_size, cb)
+    if st == 0:
+        _decoders[ttype] = cb
+    return st
 
 
 def _bind_host(L):
@@ -333,6 +352,8 @@ def _bind_host(L):
     L.mi355x_backend_register_weight_source.argtypes = [pt, vp, sz]
     L.mi355x_backend_parse_mb.restype = ctypes.c_bool
     L.mi355x_backend_parse_mb.argtypes = [ctypes.c_char_p, ctypes.POINTER(sz)]
+    L.mi355x_backend_set_to_float.restype = i32
+    L.mi355x_backend_set_to_float.argtypes = [i32, ctypes.c_int64, ctypes.c_int64, TO_FLOAT_FN]
     L._host_bound = True
     return L
 

@@ -170,6 +170,21 @@ enum mi355x_log_level { MI355X_LOG_INFO = 1, MI355X_LOG_WARN = 2 };
 typedef void (*mi355x_log_fn)(int level, const char * text, void * user);
 MI355X_API void mi355x_backend_set_log_callback(mi355x_log_fn fn, void * user);
 
+/* ggml's row decoder of a weight type (ggml_to_float_t): n values of `src` to f32 in `dst`. */
+typedef void (*mi355x_to_float_fn)(const void * src, float * dst, int64_t n);
+
+/* Lets the backend take MUL_MAT / MUL_MAT_ID weights of a quantized ggml type its kernels do not
+ * decode (they decode Q8_0, Q4_K, Q6_K and MXFP4): `fn` is ggml's dequantizer for the type,
+ * ggml_get_type_traits(type)->to_float, with its blck_size and type_size. Such a weight is
+ * decoded on the host through `fn` (row by row, then rounded to fp16: the reference's path for
+ * every quant type, rocket_weight_to_fp16, ggml-rocket.cpp:3894-3909) and kept as an fp16 image
+ * in the HBM cache; the CPU fallback decodes it through `fn` too. Process-wide; register before
+ * the first graph that uses the type. Returns 0 (also for a type the kernels decode natively,
+ * whose device decoder stays in use), or -1 (MI355X_E_ARG) for a type id outside 0..63, a plain
+ * type, sizes that disagree with ggml's published ones, or fn == NULL. No counterpart in the
+ * reference's header: there the plugin calls ggml's traits directly. */
+MI355X_API int mi355x_backend_set_to_float(int type, int64_t block_size, int64_t type_size, mi355x_to_float_fn fn);
+
 /* A byte-size knob in MB, parsed strictly (ggml-rocket.cpp:7932-7964): digits only, no sign, no
  * suffix, no overflow. Returns true and sets *bytes on success; "0" means unlimited. */
 MI355X_API bool mi355x_backend_parse_mb(const char * text, size_t * bytes);

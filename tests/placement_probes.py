@@ -157,10 +157,37 @@ def prec_quant_rows():
     ]
 
 
+def host_decoder_rows():
+    """A quantized type the kernels do not decode is claimed once the plugin registers ggml's
+    decoder for it (mi355x_backend_set_to_float), with ggml's block facts; bad registrations are
+    refused and a natively decoded type keeps its device decoder."""
+    def nop(src, dst, n):
+        pass
+    rows = [("Q4_1 leaf before registration -> CPU", False, mm_supported(256, 128, 512, mx.Q4_1))]
+    st_bad_size = mx.set_to_float(mx.Q4_1, 32, 18, nop)        # Q4_1 blocks are 20 bytes
+    st_bad_type = mx.set_to_float(70, 32, 18, nop)
+    st_plain = mx.set_to_float(mx.F16, 1, 2, nop)
+    st_native = mx.set_to_float(mx.Q4_K, 256, 144, nop)
+    st_ok = mx.set_to_float(mx.Q4_1, 32, 20, nop)
+    rows += [
+        ("registration with wrong block bytes refused", True, st_bad_size == -1),
+        ("registration of a type id past 63 refused", True, st_bad_type == -1),
+        ("registration of a plain type refused", True, st_plain == -1),
+        ("registration of a natively decoded type accepted and ignored", True, st_native == 0),
+        ("registration of Q4_1 accepted", True, st_ok == 0),
+        ("Q4_1 leaf, M >= quant floor -> offload", True, mm_supported(256, 128, 512, mx.Q4_1)),
+        ("Q4_1 leaf, M(256) < quant floor -> CPU", False, mm_supported(256, 128, 256, mx.Q4_1)),
+        ("Q4_1 leaf, K % 32 != 0 -> CPU", False, mm_supported(272, 128, 512, mx.Q4_1)),
+        ("Q5_K leaf (not registered) -> CPU", False, mm_supported(256, 128, 512, mx.Q5_K)),
+        ("Q4_1 expert stack (FORCED) -> offload", True, moe_supported(256, 128, 8, 512, mx.Q4_1, "blk.0.ffn_up_exps.weight")),
+    ]
+    return rows
+
+
 if __name__ == "__main__":
     mode = sys.argv[1]
     fn = {"auto": moe_auto_rows, "budget": moe_budget_rows, "off": moe_off_rows, "forced": moe_forced_rows,
-          "prec_quant": prec_quant_rows}.get(mode)
+          "prec_quant": prec_quant_rows, "host_decoder": host_decoder_rows}.get(mode)
     if mode == "src_admitted":
         print(json.dumps(moe_src_admitted()))
     else:

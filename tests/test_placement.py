@@ -77,8 +77,10 @@ CASES = [
     ("FA: head_dim 288 -> CPU (> 256)", False, lambda: fa_supported(288, 256, 8, 1024, 2, mx.F16, 0.0)),
     # Narrower: a quantized type without a device decoder is declined (the reference takes any
     # type with a ggml to_float, 7452-7455).
-    ("Q4_0 leaf -> CPU (no device decoder)", False, lambda: mm_supported(K, N, MQ, 2)),
-    ("Q5_K leaf -> CPU (no device decoder)", False, lambda: mm_supported(K, N, MQ, 13)),
+    # a type with neither a device decoder nor a registered host one (the plugin registers
+    # ggml's to_float for every quantized type; this process registers none)
+    ("Q4_1 leaf -> CPU (no decoder)", False, lambda: mm_supported(K, N, MQ, 3)),
+    ("Q2_K leaf -> CPU (no decoder)", False, lambda: mm_supported(K, N, MQ, 10)),
 ]
 
 
@@ -152,7 +154,8 @@ def _child(mode, env):
 
 @pytest.mark.parametrize("mode,env", [("auto", {}), ("budget", {"MI355X_MOE_CACHE_MB": "1"}),
                                       ("off", {"MI355X_MOE": "0"}), ("forced", {"MI355X_MOE": "1"}),
-                                      ("prec_quant", {"ROCKET_INT8": "1", "ROCKET_INT4": "1"})])
+                                      ("prec_quant", {"ROCKET_INT8": "1", "ROCKET_INT4": "1"}),
+                                      ("host_decoder", {"MI355X_MOE": "1"})])
 def test_moe_and_knob_modes(mode, env):
     bad = [row for row in _child(mode, env) if row[1] != row[2]]
     assert not bad, bad
