@@ -10,7 +10,7 @@
 // graph_compute returns. Large copies go through pinned staging slots, filled and drained by
 // n_threads copy workers while the DMA engine moves the neighbouring chunk. Weights are uploaded once into the HBM weight cache, keyed by
 // weight_key (name + content fingerprint), in the layout the kernels read:
-//   F16 / Q4_K   the ggml payload as-is;   Q8_0 / Q6_K / MXFP4   split into aligned planes;
+//   F16 / Q4_K / Q5_K   the ggml payload as-is;   Q4_0 / Q8_0 / Q6_K / MXFP4   split into aligned planes;
 //   F32 / BF16   converted to fp16;        QUANT_RESIDENT=1   quant weights decoded to fp16.
 
 #include <stdarg.h>
@@ -242,7 +242,7 @@ struct Stager {
 struct WEntry {
     void * dev = nullptr;
     size_t bytes = 0;
-    int dev_type = 0;   // layout the kernels read: F16, F16_T, Q8_0, Q4_K, Q6_K or MXFP4
+    int dev_type = 0;   // layout the kernels read: F16, F16_T, Q4_0, Q8_0, Q4_K, Q5_K, Q6_K or MXFP4
     int64_t rows = 0, K = 0;
 };
 
@@ -417,7 +417,7 @@ int d2h(Ctx * c, void * dst, const void * src, size_t n) {
 int dev_layout(int t, bool want_f16, bool tiled_ok, int64_t K) {
     if (want_f16 || !device_weight_type(t) || t == MI355X_TYPE_F16 || t == MI355X_TYPE_F32 || t == MI355X_TYPE_BF16)
         return (tiled_ok && K % 64 == 0) ? MI355X_F16_T : MI355X_F16;
-    return t;   // Q8_0, Q4_K, Q6_K, MXFP4
+    return t;   // Q4_0, Q8_0, Q4_K, Q5_K, Q6_K, MXFP4
 }
 
 // Builds the device form `lay` of `rows` rows of K values of ggml type `t` (host bytes `src`) at
@@ -441,7 +441,7 @@ int build_weight(Ctx * c, int t, const void * src, int64_t rows, int64_t K, int 
         return build_weight(c, MI355X_TYPE_F32, f.data(), rows, K, lay, dst);
     }
     const size_t raw = (size_t)row_bytes(t, K) * (size_t)rows;
-    if ((t == MI355X_TYPE_F16 || t == MI355X_TYPE_Q4_K) && lay == t) return h2d(c, dst, src, raw);
+    if ((t == MI355X_TYPE_F16 || t == MI355X_TYPE_Q4_K || t == MI355X_TYPE_Q5_K) && lay == t) return h2d(c, dst, src, raw);
     TRY(c->wstage.ensure(raw));
     TRY(h2d(c, c->wstage.p, src, raw));
     if (t == MI355X_TYPE_F32 || t == MI355X_TYPE_BF16) {
@@ -453,7 +453,7 @@ int build_weight(Ctx * c, int t, const void * src, int64_t rows, int64_t K, int 
     if (lay != MI355X_F16 && lay != MI355X_F16_T) return mi355x_weight_pack(t, c->wstage.p, rows, K, dst, c->stream);
     // -> fp16: from the HBM layout, built first when that differs from the ggml one
     const void * q = c->wstage.p;
-    if (t == MI355X_TYPE_Q8_0 || t == MI355X_TYPE_Q6_K || t == MI355X_TYPE_MXFP4) {
+    if (t == MI355X_TYPE_Q4_0 || t == MI355X_TYPE_Q8_0 || t == MI355X_TYPE_Q6_K || t == MI355X_TYPE_MXFP4) {
         TRY(c->wconv.ensure(raw));
         TRY(mi355x_weight_pack(t, c->wstage.p, rows, K, c->wconv.p, c->stream));
         q = c->wconv.p;

@@ -6,7 +6,7 @@
 // MI355X-specific differences, each stated where it is applied:
 //   * the accumulator declaration: this device accumulates in fp32 and writes F32, so an F32 or
 //     BF16 accumulator declaration is met (the NPU route could not, 7372-7380);
-//   * the weight types: the device decodes F16, F32, BF16, Q8_0, Q4_K, Q6_K and MXFP4; other ggml quant
+//   * the weight types: the device decodes F16, F32, BF16, Q4_0, Q8_0, Q4_K, Q5_K, Q6_K and MXFP4; other ggml quant
 //     types are declined rather than claimed and then computed on the host;
 //   * FLASH_ATTN_EXT: head dims up to 256, and the strides the kernel reads.
 

@@ -54,6 +54,32 @@ bool decode_row_f32(int type, const void * src, float * y, int64_t n) {
                 for (int l = 0; l < 32; l++) *y++ = d * (float)(int8_t)x[2 + l];
             }
             return true;
+        case MI355X_TYPE_Q4_0:   // dequantize_row_q4_0: d * (q - 8), low nibbles first
+            for (int64_t b = 0; b < n / 32; b++, x += 18) {
+                const float d = h2f(rd16(x));
+                for (int l = 0; l < 16; l++) y[l] = (float)((x[2 + l] & 15) - 8) * d;
+                for (int l = 0; l < 16; l++) y[16 + l] = (float)((x[2 + l] >> 4) - 8) * d;
+                y += 32;
+            }
+            return true;
+        case MI355X_TYPE_Q5_K:   // dequantize_row_q5_K: Q4_K's scales, a fifth bit from qh
+            for (int64_t b = 0; b < n / 256; b++, x += 176) {
+                const float d = h2f(rd16(x)), dmin = h2f(rd16(x + 2));
+                const uint8_t * s = x + 4;
+                const uint8_t * qh = x + 16;
+                const uint8_t * q = x + 48;
+                for (int j = 0; j < 8; j++) {
+                    int sc, mn;
+                    if (j < 4) { sc = s[j] & 63; mn = s[j + 4] & 63; }
+                    else { sc = (s[j + 4] & 15) | ((s[j - 4] >> 6) << 4); mn = (s[j + 4] >> 4) | ((s[j] >> 6) << 4); }
+                    const float dd = d * (float)sc, mm = dmin * (float)mn;
+                    const uint8_t * qq = q + 32 * (j / 2);
+                    const int sh = (j % 2) * 4;
+                    for (int l = 0; l < 32; l++)
+                        *y++ = dd * (float)(((qq[l] >> sh) & 15) | (((qh[l] >> j) & 1) << 4)) - mm;
+                }
+            }
+            return true;
         case MI355X_TYPE_Q4_K:
             for (int64_t b = 0; b < n / 256; b++, x += 144) {
                 const float d = h2f(rd16(x)), dmin = h2f(rd16(x + 2));

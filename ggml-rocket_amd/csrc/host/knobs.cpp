@@ -163,7 +163,8 @@ bool is_contiguous(const mi355x_tensor * t) {
 
 bool device_weight_type(int t) {
     return t == MI355X_TYPE_F16 || t == MI355X_TYPE_F32 || t == MI355X_TYPE_BF16 ||
-           t == MI355X_TYPE_Q8_0 || t == MI355X_TYPE_Q4_K || t == MI355X_TYPE_Q6_K || t == MI355X_TYPE_MXFP4;
+           t == MI355X_TYPE_Q8_0 || t == MI355X_TYPE_Q4_0 || t == MI355X_TYPE_Q4_K || t == MI355X_TYPE_Q5_K ||
+           t == MI355X_TYPE_Q6_K || t == MI355X_TYPE_MXFP4;
 }
 
 bool weight_type_ok(int t) {

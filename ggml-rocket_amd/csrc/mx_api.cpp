@@ -23,11 +23,13 @@ inline int hip_status(hipError_t e) {
 }
 
 inline bool known_wtype(int wt) {
-    return wt == mx::T_F16 || wt == mx::T_Q8_0 || wt == mx::T_Q4_K || wt == mx::T_Q6_K || wt == mx::T_MXFP4;
+    return wt == mx::T_F16 || wt == mx::T_Q8_0 || wt == mx::T_Q4_0 || wt == mx::T_Q4_K || wt == mx::T_Q5_K ||
+           wt == mx::T_Q6_K || wt == mx::T_MXFP4;
 }
 
 inline int64_t blck(int wt) {
-    return (wt == mx::T_Q4_K || wt == mx::T_Q6_K) ? 256 : ((wt == mx::T_Q8_0 || wt == mx::T_MXFP4) ? 32 : 1);
+    if (wt == mx::T_Q4_K || wt == mx::T_Q5_K || wt == mx::T_Q6_K) return 256;
+    return (wt == mx::T_Q8_0 || wt == mx::T_Q4_0 || wt == mx::T_MXFP4) ? 32 : 1;
 }
 
 inline bool aligned(const void * p, size_t a) { return ((uintptr_t)p % a) == 0; }
@@ -80,7 +82,8 @@ MI355X_API int mi355x_weight_pack(int wtype, const void * src_dev, int64_t rows,
     if (!known_wtype(wtype) || rows < 0 || K <= 0 || K % blck(wtype) || K % 32) return MI355X_E_ARG;
     if (rows == 0) return MI355X_OK;
     if (!src_dev || !dst_dev) return MI355X_E_ARG;
-    if ((wtype == mx::T_Q8_0 || wtype == mx::T_Q6_K || wtype == mx::T_MXFP4) && src_dev == dst_dev) return MI355X_E_ARG;
+    if ((wtype == mx::T_Q8_0 || wtype == mx::T_Q4_0 || wtype == mx::T_Q6_K || wtype == mx::T_MXFP4) && src_dev == dst_dev)
+        return MI355X_E_ARG;
     return hip_status(mx::launch_pack_weight(wtype, src_dev, rows, K, dst_dev, S(stream)));
 }
 

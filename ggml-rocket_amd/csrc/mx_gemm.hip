@@ -330,7 +330,7 @@ constexpr int SK_NW = 4;
 // file without spilling, one otherwise.
 template <int WT, int MT>
 constexpr int skinny_occupancy() {
-    return (WT == T_Q4_K || WT == T_MXFP4 || MT == 1) ? 2 : 1;
+    return (WT == T_Q4_K || WT == T_MXFP4 || WT == T_Q4_0 || MT == 1) ? 2 : 1;
 }
 
 template <int WT, int MT, int CH>
@@ -1209,6 +1209,21 @@ __global__ void pack_mxfp4_kernel(const uint8_t * __restrict__ src, int64_t rows
     dst[rows * (K / 2) + row * nb + b] = s[0];
 }
 
+// ggml Q4_0 -> split planes. One thread per block.
+__global__ void pack_q4_0_kernel(const uint8_t * __restrict__ src, int64_t rows, int64_t K,
+                                 uint8_t * __restrict__ dst) {
+    const int64_t nb = K / 32;
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= rows * nb) return;
+    const int64_t row = i / nb, b = i % nb;
+    const uint8_t * s = src + i * 18;
+    uint8_t * qs = dst + row * (K / 2) + b * 16;
+    for (int l = 0; l < 16; l++) qs[l] = s[2 + l];
+    uint8_t * d = dst + rows * (K / 2) + (row * nb + b) * 2;
+    d[0] = s[0];
+    d[1] = s[1];
+}
+
 // ggml Q6_K -> split planes. One thread per block.
 __global__ void pack_q6_k_kernel(const uint8_t * __restrict__ src, int64_t rows, int64_t K,
                                  uint8_t * __restrict__ dst) {
@@ -1612,7 +1627,9 @@ hipError_t launch_gemm(int wt, const GemmArgs & a_in, int /*unused*/, hipStream_
         switch (wt) {
             case T_F16: return launch_skinny<T_F16>(a, nblocks, st);
             case T_Q8_0: return launch_skinny<T_Q8_0>(a, nblocks, st);
+            case T_Q4_0: return launch_skinny<T_Q4_0>(a, nblocks, st);
             case T_Q4_K: return launch_skinny<T_Q4_K>(a, nblocks, st);
+            case T_Q5_K: return launch_skinny<T_Q5_K>(a, nblocks, st);
             case T_Q6_K: return launch_skinny<T_Q6_K>(a, nblocks, st);
             case T_MXFP4: return launch_skinny<T_MXFP4>(a, nblocks, st);
             default: return hipErrorInvalidValue;
@@ -1638,7 +1655,9 @@ hipError_t launch_gemm(int wt, const GemmArgs & a_in, int /*unused*/, hipStream_
         case T_F16: return launch_cfg<T_F16>(cfg, a, nblocks, st);
         case T_F16T: return launch_cfg<T_F16T>(cfg, a, nblocks, st);
         case T_Q8_0: return launch_cfg<T_Q8_0>(cfg, a, nblocks, st);
+        case T_Q4_0: return launch_cfg<T_Q4_0>(cfg, a, nblocks, st);
         case T_Q4_K: return launch_cfg<T_Q4_K>(cfg, a, nblocks, st);
+        case T_Q5_K: return launch_cfg<T_Q5_K>(cfg, a, nblocks, st);
         case T_Q6_K: return launch_cfg<T_Q6_K>(cfg, a, nblocks, st);
         case T_MXFP4: return launch_cfg<T_MXFP4>(cfg, a, nblocks, st);
         default: return hipErrorInvalidValue;
@@ -1654,7 +1673,9 @@ static hipError_t launch_dequant(int wt, const void * W, int64_t rows, int64_t K
     switch (wt) {
         case T_F16: hipLaunchKernelGGL((dequant_f16_kernel<T_F16, TL>), grid, dim3(256), 0, st, w, rows, K, out); break;
         case T_Q8_0: hipLaunchKernelGGL((dequant_f16_kernel<T_Q8_0, TL>), grid, dim3(256), 0, st, w, rows, K, out); break;
+        case T_Q4_0: hipLaunchKernelGGL((dequant_f16_kernel<T_Q4_0, TL>), grid, dim3(256), 0, st, w, rows, K, out); break;
         case T_Q4_K: hipLaunchKernelGGL((dequant_f16_kernel<T_Q4_K, TL>), grid, dim3(256), 0, st, w, rows, K, out); break;
+        case T_Q5_K: hipLaunchKernelGGL((dequant_f16_kernel<T_Q5_K, TL>), grid, dim3(256), 0, st, w, rows, K, out); break;
         case T_Q6_K: hipLaunchKernelGGL((dequant_f16_kernel<T_Q6_K, TL>), grid, dim3(256), 0, st, w, rows, K, out); break;
         case T_MXFP4: hipLaunchKernelGGL((dequant_f16_kernel<T_MXFP4, TL>), grid, dim3(256), 0, st, w, rows, K, out); break;
         default: return hipErrorInvalidValue;
@@ -1681,7 +1702,8 @@ hipError_t launch_pack_weight(int wt, const void * src, int64_t rows, int64_t K,
     uint8_t * d = (uint8_t *)dst;
     switch (wt) {
         case T_F16:
-        case T_Q4_K: {
+        case T_Q4_K:
+        case T_Q5_K: {
             const int64_t bytes = packed_weight_bytes(wt, rows, K);
             if (s != d) return hipMemcpyAsync(d, s, (size_t)bytes, hipMemcpyDeviceToDevice, st);
             return hipSuccess;
@@ -1696,6 +1718,12 @@ hipError_t launch_pack_weight(int wt, const void * src, int64_t rows, int64_t K,
             const int64_t n = rows * (K / 256);
             if (n <= 0) return hipSuccess;
             hipLaunchKernelGGL(pack_q6_k_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, s, rows, K, d);
+            return hipGetLastError();
+        }
+        case T_Q4_0: {
+            const int64_t n = rows * (K / 32);
+            if (n <= 0) return hipSuccess;
+            hipLaunchKernelGGL(pack_q4_0_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, s, rows, K, d);
             return hipGetLastError();
         }
         case T_MXFP4: {

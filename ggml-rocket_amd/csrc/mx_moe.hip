@@ -307,6 +307,8 @@ hipError_t launch_moe(int wt, const MoeArgs & a, hipStream_t st) {
     switch (wt) {
         case T_F16: hipLaunchKernelGGL(moe_gemm_kernel<T_F16>, dim3((unsigned)nb), dim3(MOE_THREADS), lds, st, a); break;
         case T_Q8_0: hipLaunchKernelGGL(moe_gemm_kernel<T_Q8_0>, dim3((unsigned)nb), dim3(MOE_THREADS), lds, st, a); break;
+        case T_Q4_0: hipLaunchKernelGGL(moe_gemm_kernel<T_Q4_0>, dim3((unsigned)nb), dim3(MOE_THREADS), lds, st, a); break;
+        case T_Q5_K: hipLaunchKernelGGL(moe_gemm_kernel<T_Q5_K>, dim3((unsigned)nb), dim3(MOE_THREADS), lds, st, a); break;
         case T_Q4_K: hipLaunchKernelGGL(moe_gemm_kernel<T_Q4_K>, dim3((unsigned)nb), dim3(MOE_THREADS), lds, st, a); break;
         case T_Q6_K: hipLaunchKernelGGL(moe_gemm_kernel<T_Q6_K>, dim3((unsigned)nb), dim3(MOE_THREADS), lds, st, a); break;
         case T_MXFP4: hipLaunchKernelGGL(moe_gemm_kernel<T_MXFP4>, dim3((unsigned)nb), dim3(MOE_THREADS), lds, st, a); break;

@@ -14,11 +14,15 @@
 //         d fp16 [rows][K/256] at rows*K*13/16.
 //   MXFP4 split into two planes (a ggml block is 17 B: { u8 e; u8 qs[16]; } per 32 values):
 //         qs [rows][K/2] at 0 (16 bytes per block), then e [rows][K/32] at rows*K/2.
+//   Q4_0  split into two planes (a ggml block is 18 B: { fp16 d; u8 qs[16]; } per 32 values):
+//         qs [rows][K/2] at 0, then d fp16 [rows][K/32] at rows*K/2.
+//   Q5_K  [rows][K/256] blocks of 176 B, the ggml payload unchanged: { fp16 d, fp16 dmin,
+//         u8 scales[12], u8 qh[32], u8 qs[128] }. Every block starts on a 16-byte boundary.
 // The split layouts hold exactly the ggml bytes, re-ordered; their size equals the ggml size.
 //
 // Decoding follows ggml's dequantizers value for value (the to_float contract the reference
-// uses at ggml-rocket.cpp:3894-3906): Q8_0 y = d*q; Q4_K y = (d*sc)*q - dmin*m; Q6_K
-// y = (d*sc)*(q-32); MXFP4 y = kvalues_mxfp4[code] * 2^(e-128) (E2M1 codes doubled to integers,
+// uses at ggml-rocket.cpp:3894-3906): Q8_0 y = d*q; Q4_0 y = d*(q-8); Q4_K and Q5_K
+// y = (d*sc)*q - dmin*m (Q5_K's q has a fifth bit); Q6_K y = (d*sc)*(q-32); MXFP4 y = kvalues_mxfp4[code] * 2^(e-128) (E2M1 codes doubled to integers,
 // the E8M0 scale halved: GGML_E8M0_TO_FP32_HALF), exact in f32. Each product and difference is
 // rounded on its own, then the f32 result is rounded once to fp16 (ggml_fp32_to_fp16_row, 3907).
 //
@@ -40,6 +44,8 @@ __host__ __device__ inline int64_t packed_weight_bytes(int wt, int64_t rows, int
         case T_Q4_K: return rows * (K / 256) * 144;
         case T_Q6_K: return rows * (K / 256) * 210;
         case T_MXFP4: return rows * (K / 32) * 17;
+        case T_Q4_0: return rows * (K / 32) * 18;
+        case T_Q5_K: return rows * (K / 256) * 176;
         default: return -1;
     }
 }
@@ -169,6 +175,104 @@ template <> struct WLoad<T_MXFP4> {
         zero_out(ok, out);
         run0 = 32 * u;
         run1 = 32 * u + 16;
+    }
+};
+
+// Q4_0: one 32-value block per item, as MXFP4.
+template <> struct WLoad<T_Q4_0> {
+    u32x4 qs;    // weight j in the low nibble of byte j, weight j + 16 in the high one
+    uint16_t d;
+    bool ok;
+    __device__ __forceinline__ void load(const uint8_t * W, int64_t rows, int64_t K, int64_t row,
+                                         int64_t k0, int u, bool ok_row) {
+        int64_t k = k0 + 32 * u;
+        ok = ok_row && k < K;
+        k = k < K ? k : 0;
+        qs = *(const u32x4 *)(W + row * (K / 2) + k / 2);
+        d = *((const uint16_t *)(W + rows * (K / 2)) + row * (K / 32) + k / 32);
+    }
+    __device__ __forceinline__ void decode(int u, u32x4 out[4], int & run0, int & run1) const {
+        const float df = h2f_bits(d);
+        uint32_t o[16];
+#pragma unroll
+        for (int w = 0; w < 4; w++) {
+            const uint32_t word = qs[w];
+            float lo[4], hi[4];
+#pragma unroll
+            for (int b = 0; b < 4; b++) {
+                // (q - 8) * d: a 4-bit integer times an fp16 value, exact in f32
+                lo[b] = mul_rn(df, (float)((int)((word >> (8 * b)) & 15u) - 8));
+                hi[b] = mul_rn(df, (float)((int)((word >> (8 * b + 4)) & 15u) - 8));
+            }
+            o[2 * w] = pack2h(lo[0], lo[1]);
+            o[2 * w + 1] = pack2h(lo[2], lo[3]);
+            o[8 + 2 * w] = pack2h(hi[0], hi[1]);
+            o[8 + 2 * w + 1] = pack2h(hi[2], hi[3]);
+        }
+#pragma unroll
+        for (int i = 0; i < 4; i++) out[i] = u32x4{o[4 * i], o[4 * i + 1], o[4 * i + 2], o[4 * i + 3]};
+        zero_out(ok, out);
+        run0 = 32 * u;
+        run1 = 32 * u + 16;
+    }
+};
+
+// Q5_K: as Q4_K, plus 16 bytes of fifth bits per item (qh[16u .. 16u+15], bits 2j and 2j+1).
+template <> struct WLoad<T_Q5_K> {
+    u32x4 hdr;   // d, dmin, scales[12]
+    u32x4 qh;    // fifth bits of weights l = 16u .. 16u+15 of every sub-block
+    u32x4 qs;    // 16 bytes of nibbles
+    int j;       // quarter of the block (0..3)
+    bool ok;
+    __device__ __forceinline__ void load(const uint8_t * W, int64_t rows, int64_t K, int64_t row,
+                                         int64_t k0, int u, bool ok_row) {
+        const int64_t blk = k0 / 256;
+        j = (int)((k0 % 256) / 64);
+        ok = ok_row;
+        const uint8_t * b = W + (row * (K / 256) + blk) * 176;
+        hdr = *(const u32x4 *)b;
+        qh = *(const u32x4 *)(b + 16 + 16 * u);
+        qs = *(const u32x4 *)(b + 48 + 32 * j + 16 * u);
+    }
+    // Byte b of qs is q[32j + 16u + b]: its low nibble is weight 64j + 16u + b (sub-block 2j)
+    // with fifth bit 2j of qh byte b, its high nibble weight 64j + 32 + 16u + b (sub-block
+    // 2j+1) with bit 2j+1.
+    __device__ __forceinline__ void decode(int u, u32x4 out[4], int & run0, int & run1) const {
+        const float d = h2f_bits((uint16_t)(hdr[0] & 0xFFFFu));
+        const float dmin = h2f_bits((uint16_t)(hdr[0] >> 16));
+        int s0, m0, s1, m1;
+        q4k_sm(2 * j, hdr[1], hdr[2], hdr[3], s0, m0);
+        q4k_sm(2 * j + 1, hdr[1], hdr[2], hdr[3], s1, m1);
+        // d * sc has at most 17 significant bits and d * sc * q at most 22: exact in f32, so one
+        // fma rounds d*sc*q - dmin*m as the CPU's rounded product followed by the difference
+        const float d0 = d * (float)s0, mm0 = dmin * (float)m0;
+        const float d1 = d * (float)s1, mm1 = dmin * (float)m1;
+        uint32_t lo[8], hi[8];
+#pragma unroll
+        for (int w = 0; w < 4; w++) {
+            // the fifth bits as 0x10 per byte, for the low and the high nibbles
+            const uint32_t b0 = ((qh[w] >> (2 * j)) & 0x01010101u) << 4;
+            const uint32_t b1 = ((qh[w] >> (2 * j + 1)) & 0x01010101u) << 4;
+            uint32_t l5 = (qs[w] & 0x0F0F0F0Fu) | b0, h5 = ((qs[w] >> 4) & 0x0F0F0F0Fu) | b1;
+            asm("" : "+v"(l5), "+v"(h5));
+            float fl[4], fh[4];
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                fl[i] = fma_rn(d0, (float)((l5 >> (8 * i)) & 0xFFu), -mm0);
+                fh[i] = fma_rn(d1, (float)((h5 >> (8 * i)) & 0xFFu), -mm1);
+            }
+            lo[2 * w] = pack2h(fl[0], fl[1]);
+            lo[2 * w + 1] = pack2h(fl[2], fl[3]);
+            hi[2 * w] = pack2h(fh[0], fh[1]);
+            hi[2 * w + 1] = pack2h(fh[2], fh[3]);
+        }
+        out[0] = u32x4{lo[0], lo[1], lo[2], lo[3]};
+        out[1] = u32x4{lo[4], lo[5], lo[6], lo[7]};
+        out[2] = u32x4{hi[0], hi[1], hi[2], hi[3]};
+        out[3] = u32x4{hi[4], hi[5], hi[6], hi[7]};
+        zero_out(ok, out);
+        run0 = 16 * u;
+        run1 = 32 + 16 * u;
     }
 };
 

@@ -315,8 +315,8 @@ ggml_backend_reg_t ggml_backend_mi355x_reg(void) {
     static std::once_flag routed;
     std::call_once(routed, [] {
         mi355x_backend_set_log_callback(to_ggml_log, nullptr);
-        // every quantized type ggml can decode: the kernels keep theirs (Q8_0, Q4_K, Q6_K,
-        // MXFP4), the rest are decoded on the host by ggml's own to_float into fp16 images, as the
+        // every quantized type ggml can decode: the kernels keep theirs (Q4_0, Q8_0, Q4_K, Q5_K,
+        // Q6_K, MXFP4), the rest are decoded on the host by ggml's own to_float into fp16 images, as the
         // reference decodes every quant type (ggml-rocket.cpp:3894-3909)
         for (int t = 0; t < GGML_TYPE_COUNT; t++) {
             const ggml_type_traits * tr = ggml_get_type_traits((ggml_type)t);

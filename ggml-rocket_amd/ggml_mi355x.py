@@ -17,11 +17,11 @@ _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "lib", "libmi355x.so")
 
 F32, F16, Q8_0, Q4_K, Q6_K, I32, BF16, MXFP4 = 0, 1, 8, 12, 14, 26, 30, 39
-Q4_0, Q4_1, Q5_0, Q5_K = 2, 3, 6, 13
+Q4_0, Q4_1, Q5_0, Q2_K, Q5_K = 2, 3, 6, 10, 13
 F16_T = 0x101   # the library's tiled fp16 layout (16 x 32 tiles of 1 KB); not a ggml type
 OK, E_ARG, E_DEVICE, E_UNSUPPORTED, E_NOMEM, E_IDS = 0, -1, -2, -3, -4, -5   # mi355x_status
-BLOCK = {F16: 1, F32: 1, BF16: 1, Q8_0: 32, Q4_K: 256, Q6_K: 256, MXFP4: 32}
-TYPE_SIZE = {F16: 2, F32: 4, BF16: 2, Q8_0: 34, Q4_K: 144, Q6_K: 210, MXFP4: 17}
+BLOCK = {F16: 1, F32: 1, BF16: 1, Q8_0: 32, Q4_0: 32, Q4_K: 256, Q5_K: 256, Q6_K: 256, MXFP4: 32}
+TYPE_SIZE = {F16: 2, F32: 4, BF16: 2, Q8_0: 34, Q4_0: 18, Q4_K: 144, Q5_K: 176, Q6_K: 210, MXFP4: 17}
 
 _lib = None
 
@@ -164,7 +164,7 @@ def upload_weight(wtype: int, payload, rows: int, K: int, device="cuda"):
     nbytes = weight_bytes(wtype, rows, K)
     if nbytes < 0 or raw.numel() != nbytes:
         raise MI355XError(f"payload of {raw.numel()} bytes is not {rows} rows of K={K} of type {wtype}")
-    if wtype in (F16, Q4_K):
+    if wtype in (F16, Q4_K, Q5_K):
         return raw
     out = torch.empty(nbytes, dtype=torch.uint8, device=device)
     check(lib().mi355x_weight_pack(wtype, _ptr(raw), rows, K, _ptr(out), stream_handle()), "weight_pack")

@@ -15,10 +15,10 @@
  *                mask [T'][KV'] fp16 (T' >= T, KV' >= KV), dst [T][H][DV] F32.
  *   MUL_MAT_ID   as [E][N][K], b [T][ne11][K] F32, ids [T][n_used] I32, dst [T][n_used][N] F32.
  *
- * Weight types are ggml type ids: F16 = 1, Q8_0 = 8, Q4_K = 12, Q6_K = 14, MXFP4 = 39. A weight
- * reaches a GEMM in its HBM layout: F16 and Q4_K are the ggml payload unchanged; Q8_0, Q6_K and
- * MXFP4 are re-laid out once by mi355x_weight_pack (same bytes, split into 16-byte-aligned
- * planes).
+ * Weight types are ggml type ids: F16 = 1, Q4_0 = 2, Q8_0 = 8, Q4_K = 12, Q5_K = 13, Q6_K = 14,
+ * MXFP4 = 39. A weight reaches a GEMM in its HBM layout: F16, Q4_K and Q5_K are the ggml payload
+ * unchanged; Q4_0, Q8_0, Q6_K and MXFP4 are re-laid out once by mi355x_weight_pack (same bytes,
+ * split into 16-byte-aligned planes).
  */
 #ifndef MI355X_KERNELS_H
 #define MI355X_KERNELS_H
@@ -41,7 +41,8 @@ enum mi355x_status {
     MI355X_E_IDS = -5,          /* MUL_MAT_ID: an expert id outside [0, n_expert) */
 };
 
-enum mi355x_wtype { MI355X_F16 = 1, MI355X_Q8_0 = 8, MI355X_Q4_K = 12, MI355X_Q6_K = 14, MI355X_MXFP4 = 39,
+enum mi355x_wtype { MI355X_F16 = 1, MI355X_Q4_0 = 2, MI355X_Q8_0 = 8, MI355X_Q4_K = 12, MI355X_Q5_K = 13,
+                    MI355X_Q6_K = 14, MI355X_MXFP4 = 39,
                     /* not a ggml type: fp16 [rows][K] in 16 x 32 tiles of 1 KB, row-major inside,
                      * tile (r/16, k/32) at element ((r/16)*(K/32) + k/32)*512; rows padded to a
                      * multiple of 16 (padding never read). The resident fp16 form the GEMM streams
@@ -70,8 +71,8 @@ MI355X_API const char * mi355x_status_str(int status);
  * or -1 if K is not a whole number of the type's blocks. */
 MI355X_API int64_t mi355x_weight_bytes(int wtype, int64_t rows, int64_t K);
 
-/* ggml payload (device) -> HBM layout (device). For F16 and Q4_K this is a copy (or nothing,
- * when src_dev == dst_dev). Replaces the resident pack rocket_weights_pack (ggml-rocket.cpp:
+/* ggml payload (device) -> HBM layout (device). For F16, Q4_K and Q5_K this is a copy (or
+ * nothing, when src_dev == dst_dev); the split layouts need dst_dev != src_dev. Replaces the resident pack rocket_weights_pack (ggml-rocket.cpp:
  * 4362) and its segment form rocket_weights_pack_seg (5121). */
 MI355X_API int mi355x_weight_pack(int wtype, const void * src_dev, int64_t rows, int64_t K,
                                   void * dst_dev, void * stream);
@@ -82,7 +83,7 @@ MI355X_API int mi355x_weight_pack(int wtype, const void * src_dev, int64_t rows,
 MI355X_API int mi355x_weight_dequant_f16(int wtype, const void * w_dev, int64_t rows, int64_t K,
                                          uint16_t * out_dev, void * stream);
 
-/* A weight in HBM layout (F16, Q8_0, Q4_K, Q6_K) -> MI355X_F16_T, decoded exactly as
+/* A weight in HBM layout (any weight type above) -> MI355X_F16_T, decoded exactly as
  * mi355x_weight_dequant_f16 decodes it (the same fp16 values, tiled). K % 64 == 0; out_dev holds
  * mi355x_weight_bytes(MI355X_F16_T, rows, K) bytes and does not alias w_dev. The tiled resident
  * form of rocket_weight_to_fp16 + the resident pack (ggml-rocket.cpp:3843-3931, 4362). */

@@ -35,7 +35,8 @@
 #define ORC_API __attribute__((visibility("default")))
 
 /* ggml type ids (ggml.h enum ggml_type); the formats this path carries. */
-enum { T_F32 = 0, T_F16 = 1, T_Q8_0 = 8, T_Q4_K = 12, T_Q6_K = 14, T_BF16 = 30, T_MXFP4 = 39 };
+enum { T_F32 = 0, T_F16 = 1, T_Q4_0 = 2, T_Q8_0 = 8, T_Q4_K = 12, T_Q5_K = 13, T_Q6_K = 14, T_BF16 = 30,
+       T_MXFP4 = 39 };
 
 /* ------------------------------------------------------------------------------------------ */
 /* fp16                                                                                        */
@@ -129,8 +130,13 @@ ORC_API void orc_fill_normal(float * v, int64_t n, uint64_t seed, float mean, fl
 
 /* ------------------------------------------------------------------------------------------ */
 /* block formats (ggml's published layouts)                                                    */
+/*   Q4_0: { fp16 d; u8 qs[16]; }                                          18 B / 32 weights     */
+/*     (qs[j] low nibble = weight j, high nibble = weight j + 16; y = d * (q - 8))              */
 /*   Q8_0: { fp16 d; int8 qs[32]; }                                       34 B / 32 weights     */
 /*   Q4_K: { fp16 d; fp16 dmin; u8 scales[12]; u8 qs[128]; }             144 B / 256 weights    */
+/*   Q5_K: { fp16 d; fp16 dmin; u8 scales[12]; u8 qh[32]; u8 qs[128]; } 176 B / 256 weights    */
+/*     (Q4_K's scales and nibbles plus a fifth bit: weight 32 i + l of sub-block i takes bit i  */
+/*     of qh[l], i.e. +16 before the scale)                                                    */
 /*   Q6_K: { u8 ql[128]; u8 qh[64]; int8 scales[16]; fp16 d; }           210 B / 256 weights    */
 /*   MXFP4: { u8 e; u8 qs[16]; }                                           17 B / 32 weights     */
 /*     (the OCP microscaling FP4 block ggml stores for gpt-oss: an E8M0 power-of-two scale and  */
@@ -140,8 +146,8 @@ ORC_API void orc_fill_normal(float * v, int64_t n, uint64_t seed, float mean, fl
 ORC_API int64_t orc_block_size(int type) {
     switch (type) {
         case T_F32: case T_F16: case T_BF16: return 1;
-        case T_Q8_0: case T_MXFP4: return 32;
-        case T_Q4_K: case T_Q6_K: return 256;
+        case T_Q4_0: case T_Q8_0: case T_MXFP4: return 32;
+        case T_Q4_K: case T_Q5_K: case T_Q6_K: return 256;
         default: return 0;
     }
 }
@@ -149,8 +155,10 @@ ORC_API int64_t orc_type_size(int type) {
     switch (type) {
         case T_F32: return 4;
         case T_F16: case T_BF16: return 2;
+        case T_Q4_0: return 18;
         case T_Q8_0: return 34;
         case T_Q4_K: return 144;
+        case T_Q5_K: return 176;
         case T_Q6_K: return 210;
         case T_MXFP4: return 17;
         default: return 0;
@@ -181,6 +189,39 @@ static void dequant_q8_0(const uint8_t * x, float * y, int64_t K) {
         const float d = orc_f16_to_f32(rd16(x));
         const int8_t * qs = (const int8_t *)(x + 2);
         for (int l = 0; l < 32; l++) y[l] = d * (float)qs[l];
+    }
+}
+
+static void dequant_q4_0(const uint8_t * x, float * y, int64_t K) {
+    for (int64_t b = 0; b < K / 32; b++, x += 18, y += 32) {
+        const float d = orc_f16_to_f32(rd16(x));
+        for (int j = 0; j < 16; j++) {
+            y[j] = (float)((int)(x[2 + j] & 0x0F) - 8) * d;
+            y[j + 16] = (float)((int)(x[2 + j] >> 4) - 8) * d;
+        }
+    }
+}
+
+/* Q5_K: per 64 weights j (sub-blocks 2j, 2j+1) the nibbles of qs[32j..32j+31], the fifth bits
+ * 2j and 2j+1 of qh[0..31]; y = (d * sc) * q - dmin * m, the products rounded on their own. */
+static void dequant_q5_k(const uint8_t * x, float * y, int64_t K) {
+    for (int64_t b = 0; b < K / 256; b++, x += 176) {
+        const float d = orc_f16_to_f32(rd16(x));
+        const float dmin = orc_f16_to_f32(rd16(x + 2));
+        const uint8_t * sc = x + 4;
+        const uint8_t * qh = x + 16;
+        const uint8_t * qs = x + 48;
+        for (int j = 0; j < 4; j++) {
+            int s0, m0, s1, m1;
+            q4k_scale_min(2 * j, sc, &s0, &m0);
+            q4k_scale_min(2 * j + 1, sc, &s1, &m1);
+            const float d0 = d * (float)s0, mm0 = dmin * (float)m0;
+            const float d1 = d * (float)s1, mm1 = dmin * (float)m1;
+            for (int l = 0; l < 32; l++)
+                *y++ = d0 * (float)((qs[32 * j + l] & 0x0F) + (((qh[l] >> (2 * j)) & 1) << 4)) - mm0;
+            for (int l = 0; l < 32; l++)
+                *y++ = d1 * (float)((qs[32 * j + l] >> 4) + (((qh[l] >> (2 * j + 1)) & 1) << 4)) - mm1;
+        }
     }
 }
 
@@ -255,8 +296,10 @@ ORC_API int orc_dequant_row(int type, const void * src, float * dst, int64_t K) 
         case T_F32: memcpy(dst, src, (size_t)K * 4); return 0;
         case T_F16: for (int64_t i = 0; i < K; i++) dst[i] = orc_f16_to_f32(rd16(x + 2 * i)); return 0;
         case T_BF16: for (int64_t i = 0; i < K; i++) dst[i] = bf16_to_f32(rd16(x + 2 * i)); return 0;
+        case T_Q4_0: if (K % 32) return -1; dequant_q4_0(x, dst, K); return 0;
         case T_Q8_0: if (K % 32) return -1; dequant_q8_0(x, dst, K); return 0;
         case T_Q4_K: if (K % 256) return -1; dequant_q4_k(x, dst, K); return 0;
+        case T_Q5_K: if (K % 256) return -1; dequant_q5_k(x, dst, K); return 0;
         case T_Q6_K: if (K % 256) return -1; dequant_q6_k(x, dst, K); return 0;
         case T_MXFP4: if (K % 32) return -1; dequant_mxfp4(x, dst, K); return 0;
         default: return -1;
@@ -310,6 +353,19 @@ static void quant_q8_0(const float * x, uint8_t * y, int64_t K) {
 
 static inline int clampi(int v, int lo, int hi) { return v < lo ? lo : (v > hi ? hi : v); }
 
+static void quant_q4_0(const float * x, uint8_t * y, int64_t K) {
+    for (int64_t b = 0; b < K / 32; b++, x += 32, y += 18) {
+        float amax = 0.0f;
+        for (int l = 0; l < 32; l++) amax = fmaxf(amax, fabsf(x[l]));
+        const uint16_t dh = orc_f32_to_f16(amax / 7.0f);
+        const float dq = orc_f16_to_f32(dh);
+        wr16(y, dh);
+        int q[32];
+        for (int l = 0; l < 32; l++) q[l] = dq > 0.0f ? clampi((int)lrintf(x[l] / dq), -8, 7) + 8 : 8;
+        for (int j = 0; j < 16; j++) y[2 + j] = (uint8_t)(q[j] | (q[j + 16] << 4));
+    }
+}
+
 static void quant_q4_k(const float * x, uint8_t * y, int64_t K) {
     for (int64_t b = 0; b < K / 256; b++, x += 256, y += 144) {
         float scale[8], minv[8];
@@ -348,6 +404,51 @@ static void quant_q4_k(const float * x, uint8_t * y, int64_t K) {
         for (int j = 0; j < 4; j++)
             for (int l = 0; l < 32; l++)
                 qs[32 * j + l] = (uint8_t)(q[64 * j + l] | (q[64 * j + 32 + l] << 4));
+    }
+}
+
+static void quant_q5_k(const float * x, uint8_t * y, int64_t K) {
+    for (int64_t b = 0; b < K / 256; b++, x += 256, y += 176) {
+        float scale[8], minv[8];
+        float max_scale = 0.0f, max_min = 0.0f;
+        for (int j = 0; j < 8; j++) {
+            float lo = 0.0f, hi = 0.0f;
+            for (int l = 0; l < 32; l++) { lo = fminf(lo, x[32 * j + l]); hi = fmaxf(hi, x[32 * j + l]); }
+            scale[j] = (hi - lo) / 31.0f;
+            minv[j] = -lo;
+            max_scale = fmaxf(max_scale, scale[j]);
+            max_min = fmaxf(max_min, minv[j]);
+        }
+        const uint16_t dh = orc_f32_to_f16(max_scale / 63.0f), dmh = orc_f32_to_f16(max_min / 63.0f);
+        const float dq = orc_f16_to_f32(dh), dmq = orc_f16_to_f32(dmh);
+        int sc[8], mn[8];
+        for (int j = 0; j < 8; j++) {
+            sc[j] = dq > 0.0f ? clampi((int)lrintf(scale[j] / dq), 0, 63) : 0;
+            mn[j] = dmq > 0.0f ? clampi((int)lrintf(minv[j] / dmq), 0, 63) : 0;
+        }
+        wr16(y, dh);
+        wr16(y + 2, dmh);
+        uint8_t * s = y + 4;
+        for (int j = 0; j < 4; j++) {
+            s[j]     = (uint8_t)((sc[j] & 63) | ((sc[j + 4] >> 4) << 6));
+            s[j + 4] = (uint8_t)((mn[j] & 63) | ((mn[j + 4] >> 4) << 6));
+            s[j + 8] = (uint8_t)((sc[j + 4] & 15) | ((mn[j + 4] & 15) << 4));
+        }
+        uint8_t q[256];
+        for (int j = 0; j < 8; j++) {
+            const float dd = dq * (float)sc[j], mm = dmq * (float)mn[j];
+            for (int l = 0; l < 32; l++)
+                q[32 * j + l] = (uint8_t)(dd > 0.0f ? clampi((int)lrintf((x[32 * j + l] + mm) / dd), 0, 31) : 0);
+        }
+        uint8_t * qh = y + 16;
+        uint8_t * qs = y + 48;
+        memset(qh, 0, 32);
+        for (int j = 0; j < 4; j++)
+            for (int l = 0; l < 32; l++) {
+                const uint8_t a = q[64 * j + l], c = q[64 * j + 32 + l];
+                qs[32 * j + l] = (uint8_t)((a & 15) | ((c & 15) << 4));
+                qh[l] |= (uint8_t)(((a >> 4) << (2 * j)) | ((c >> 4) << (2 * j + 1)));
+            }
     }
 }
 
@@ -421,8 +522,10 @@ ORC_API int orc_quantize_rows(int type, const float * src, void * dst, int64_t n
         switch (type) {
             case T_F32: memcpy(y, x, (size_t)K * 4); break;
             case T_F16: for (int64_t i = 0; i < K; i++) wr16(y + 2 * i, orc_f32_to_f16(x[i])); break;
+            case T_Q4_0: quant_q4_0(x, y, K); break;
             case T_Q8_0: quant_q8_0(x, y, K); break;
             case T_Q4_K: quant_q4_k(x, y, K); break;
+            case T_Q5_K: quant_q5_k(x, y, K); break;
             case T_Q6_K: quant_q6_k(x, y, K); break;
             case T_MXFP4: quant_mxfp4(x, y, K); break;
             default: break;

@@ -178,7 +178,7 @@ def host_decoder_rows():
         ("Q4_1 leaf, M >= quant floor -> offload", True, mm_supported(256, 128, 512, mx.Q4_1)),
         ("Q4_1 leaf, M(256) < quant floor -> CPU", False, mm_supported(256, 128, 256, mx.Q4_1)),
         ("Q4_1 leaf, K % 32 != 0 -> CPU", False, mm_supported(272, 128, 512, mx.Q4_1)),
-        ("Q5_K leaf (not registered) -> CPU", False, mm_supported(256, 128, 512, mx.Q5_K)),
+        ("Q2_K leaf (not registered) -> CPU", False, mm_supported(256, 128, 512, mx.Q2_K)),
         ("Q4_1 expert stack (FORCED) -> offload", True, moe_supported(256, 128, 8, 512, mx.Q4_1, "blk.0.ffn_up_exps.weight")),
     ]
     return rows

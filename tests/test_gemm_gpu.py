@@ -2,7 +2,8 @@
 
 Cases follow test-rocket-matmul.cpp: its F16 shapes (incl. M not a multiple of 4), the
 outlier-row case, the fused shared-src1 groups, its quantized shapes, plus the single-op shapes:
-the F16 [8192 x 2048] x [512 x 2048] case and the Q8_0 / Q4_K / Q6_K sweep. Bars (tests/bars.py):
+the F16 [8192 x 2048] x [512 x 2048] case and the Q8_0 / Q4_K / Q6_K sweep, and the Q4_0 / Q5_K
+decoders on the same shapes. Bars (tests/bars.py):
 the element bar, worst-column cosine >= 0.999, and max|d|/max|ref| <= 1e-2.
 """
 import numpy as np
@@ -57,7 +58,7 @@ def test_pack_act_bitexact(mx):
     assert np.array_equal(got_a, want_a)
 
 
-@pytest.mark.parametrize("wtype", [O.F16, O.Q8_0, O.Q4_K, O.Q6_K, O.MXFP4])
+@pytest.mark.parametrize("wtype", [O.F16, O.Q8_0, O.Q4_0, O.Q4_K, O.Q5_K, O.Q6_K, O.MXFP4])
 def test_dequant_f16_bitexact(mx, wtype):
     N, K = 96, 1024
     W = O.fill_normal((N, K), 11 + wtype, 0.0, 0.02)
@@ -117,7 +118,8 @@ def test_cfg_f16_8192x2048_m512(mx):
 
 
 QSHAPES = [(256, 128, 64, O.Q8_0), (3840, 256, 128, O.Q8_0), (256, 128, 64, O.Q4_K),
-           (3840, 256, 128, O.Q4_K), (512, 256, 128, O.Q6_K), (2880, 256, 128, O.MXFP4)]
+           (3840, 256, 128, O.Q4_K), (512, 256, 128, O.Q6_K), (2880, 256, 128, O.MXFP4),
+           (256, 128, 64, O.Q4_0), (2880, 256, 128, O.Q4_0), (256, 128, 64, O.Q5_K), (3840, 256, 128, O.Q5_K)]
 
 
 @pytest.mark.parametrize("K,N,M,wtype", QSHAPES)
@@ -176,7 +178,7 @@ def test_gemm_rows_of_a_panel(mx):
     import torch
     K, N, E, M = 512, 128, 3, 40
     W = O.fill_normal((E * N, K), 77, 0.0, 0.02)
-    for wtype in (O.Q8_0, O.Q6_K, O.Q4_K):
+    for wtype in (O.Q8_0, O.Q6_K, O.Q4_K, O.Q4_0, O.Q5_K):
         Q = O.quantize(wtype, W)
         w = mx.upload_weight(wtype, Q, E * N, K)
         Xf = O.fill_normal((M, K), 78)
@@ -196,7 +198,7 @@ def _untile(buf, rows, K):
     return t.transpose(0, 2, 1, 3).reshape(rp, K)[:rows]
 
 
-@pytest.mark.parametrize("wtype", [O.F16, O.Q8_0, O.Q4_K, O.Q6_K, O.MXFP4])
+@pytest.mark.parametrize("wtype", [O.F16, O.Q8_0, O.Q4_0, O.Q4_K, O.Q5_K, O.Q6_K, O.MXFP4])
 def test_f16_tiled_bitexact(mx, wtype):
     """The tiled resident form holds exactly the fp16 values of the row-major one (rows not a
     multiple of 16: padded, the padding never read)."""
@@ -233,11 +235,11 @@ N_GEMM_CFGS = 20
 FIRST_DMA_CFG = 4
 FIRST_QDMA_CFG = 16
 F16_T = 0x101
-QUANT = (O.Q4_K, O.MXFP4, O.Q8_0, O.Q6_K)
+QUANT = (O.Q4_K, O.MXFP4, O.Q8_0, O.Q6_K, O.Q4_0, O.Q5_K)
 
 
 @pytest.mark.parametrize("cfg", list(range(N_GEMM_CFGS)))
-@pytest.mark.parametrize("wtype", [O.F16, O.Q4_K, F16_T, O.MXFP4, O.Q8_0, O.Q6_K])
+@pytest.mark.parametrize("wtype", [O.F16, O.Q4_K, F16_T, O.MXFP4, O.Q8_0, O.Q6_K, O.Q4_0, O.Q5_K])
 def test_gemm_every_tile_config(mx, monkeypatch, cfg, wtype):
     import torch
     if FIRST_DMA_CFG <= cfg < FIRST_QDMA_CFG and wtype in QUANT:
@@ -312,13 +314,14 @@ def test_gemm_tiled_rows_of_a_panel(mx):
 # N (not a multiple of the 128-row block), a K with a 32-value tail where the format allows one,
 # K splits added atomically into an output cleared by the pack (mi355x_mul_mat) or by the GEMM
 # launch itself (mi355x_gemm on NaN-filled outputs, two fused weights).
-SKINNY_TYPES = [O.F16, O.Q8_0, O.Q4_K, O.Q6_K, O.MXFP4]
+SKINNY_TYPES = [O.F16, O.Q8_0, O.Q4_K, O.Q6_K, O.MXFP4, O.Q4_0, O.Q5_K]
+SUPER_BLOCK = (O.Q4_K, O.Q5_K, O.Q6_K)   # 256-value blocks: no 32-value K tail
 
 
 @pytest.mark.parametrize("M", [1, 33, 96, 128])
 @pytest.mark.parametrize("wtype", SKINNY_TYPES)
 def test_skinny_mul_mat(mx, wtype, M):
-    K = 2560 if wtype in (O.Q4_K, O.Q6_K) else 1312
+    K = 2560 if wtype in SUPER_BLOCK else 1312
     N = 400
     W = O.fill_normal((N, K), 960 + wtype, 0.0, 0.02)
     Xf = O.fill_normal((M, K), 961 + M)
@@ -338,7 +341,7 @@ def test_skinny_mul_mat(mx, wtype, M):
 @pytest.mark.parametrize("wtype", SKINNY_TYPES)
 def test_skinny_gemm_fused_nan_outputs(mx, wtype):
     import torch
-    K = 1536 if wtype in (O.Q4_K, O.Q6_K) else 1248
+    K = 1536 if wtype in SUPER_BLOCK else 1248
     M, Ns = 70, (144, 272)
     Xf = O.fill_normal((M, K), 970)
     a16, sc = mx.pack_act(_dev(Xf))

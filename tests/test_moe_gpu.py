@@ -93,6 +93,8 @@ CASES = [
     (1024, 128, 8, 1, 2, 64, O.Q4_K, 0.9990, False),
     (1152, 128, 8, 2, 2, 64, O.Q8_0, 0.9990, False),
     (512, 256, 8, 2, 4, 80, O.Q6_K, 0.9990, False),
+    (1152, 128, 8, 2, 2, 64, O.Q4_0, 0.9985, False),
+    (1024, 128, 8, 1, 2, 66, O.Q5_K, 0.9990, False),
 ]
 
 

@@ -136,17 +136,67 @@ def test_q6_k_known_answer():
     assert np.array_equal(y2[other], y[other])
 
 
-@pytest.mark.parametrize("wtype", [O.Q8_0, O.Q4_K, O.Q6_K])
+def test_q4_0_known_block():
+    # ggml's block_q4_0: qs[j] low nibble = weight j, high nibble = weight j + 16; y = d * (q - 8)
+    blk = np.zeros(18, dtype=np.uint8)
+    blk[0:2] = np.frombuffer(np.uint16(_h(0.25)).tobytes(), np.uint8)
+    lo = np.arange(16, dtype=np.uint8)              # weights 0..15: codes 0..15
+    hi = (15 - np.arange(16)).astype(np.uint8)      # weights 16..31: codes 15..0
+    blk[2:] = lo | (hi << 4)
+    y = O.dequantize(O.Q4_0, blk, 32)
+    want = np.float32(0.25) * np.concatenate([lo, hi]).astype(np.float32) - np.float32(2.0)
+    assert np.array_equal(y, want)
+    assert y[8] == 0.0 and y[0] == -2.0 and y[16] == 1.75
+
+
+def _q5k_block(d, dmin, scale_bytes, qh, qs):
+    b = np.zeros(176, dtype=np.uint8)
+    b[0:2] = np.frombuffer(np.uint16(_h(d)).tobytes(), np.uint8)
+    b[2:4] = np.frombuffer(np.uint16(_h(dmin)).tobytes(), np.uint8)
+    b[4:16] = scale_bytes
+    b[16:48] = qh
+    b[48:] = qs
+    return b
+
+
+def test_q5_k_known_answer():
+    # the scales and mins of Q4_K (same 12-byte packing, pinned above); the fifth bit of weight
+    # 32 i + l (sub-block i) is bit i of qh[l] and adds 16 to its code before the scale
+    sb = np.array([0xC1, 0x02, 0x43, 0x84, 0x05, 0xC6, 0x07, 0x48, 0x21, 0x43, 0x65, 0x87], np.uint8)
+    sc = np.array([1, 2, 3, 4, 49, 3, 5 | (1 << 4), 7 | (2 << 4)], np.float32)
+    mn = np.array([5, 6, 7, 8, 2, 4 | (3 << 4), 6, 8 | (1 << 4)], np.float32)
+    # all codes 0: y = -dmin * m
+    y0 = O.dequantize(O.Q5_K, _q5k_block(1.0, 0.5, sb, np.zeros(32, np.uint8), np.zeros(128, np.uint8)), 256)
+    assert np.array_equal(y0, np.repeat(np.float32(-0.5) * mn, 32))
+    # every fifth bit set, nibbles 0: code 16 in every weight
+    y1 = O.dequantize(O.Q5_K, _q5k_block(2.0, 0.5, sb, np.full(32, 0xFF, np.uint8), np.zeros(128, np.uint8)), 256)
+    assert np.array_equal(y1, np.repeat(np.float32(2.0) * sc * np.float32(16.0) - np.float32(0.5) * mn, 32))
+    # one weight per sub-block: weight 32 i + 7 gets code 16 * (i % 2 == 0) + i via qh bit i / nibble
+    qh = np.zeros(32, np.uint8)
+    qs = np.zeros(128, np.uint8)
+    for i in range(8):
+        if i % 2 == 0:
+            qh[7] |= 1 << i
+        qs[32 * (i // 2) + 7] |= i << (4 * (i % 2))
+    y2 = O.dequantize(O.Q5_K, _q5k_block(1.0, 0.0, np.array([1] * 4 + [0] * 4 + [0x01] * 4, np.uint8), qh, qs), 256)
+    want = np.zeros(256, np.float32)
+    for i in range(8):
+        want[32 * i + 7] = (16 if i % 2 == 0 else 0) + i
+    assert np.array_equal(y2, want)
+
+
+@pytest.mark.parametrize("wtype", [O.Q8_0, O.Q4_K, O.Q6_K, O.Q4_0, O.Q5_K])
 def test_quant_roundtrip(wtype):
-    """Within about half a quantization step of each sub-block: symmetric amax/127 (Q8_0) and
-    amax/31 (Q6_K) steps, the asymmetric (max-min)/15 step of Q4_K; slack for the fp16 / 6-bit /
-    8-bit rounding of the scales."""
+    """Within about half a quantization step of each sub-block: symmetric amax/127 (Q8_0),
+    amax/31 (Q6_K) and amax/7 (Q4_0) steps, the asymmetric (max-min)/15 step of Q4_K and
+    (max-min)/31 of Q5_K; slack for the fp16 / 6-bit / 8-bit rounding of the scales."""
     W = O.fill_normal((64, 1024), 5, 0.0, 0.02)
     d = O.dequantize(wtype, O.quantize(wtype, W), 1024)
-    blk = {O.Q8_0: 32, O.Q4_K: 32, O.Q6_K: 16}[wtype]
+    blk = {O.Q8_0: 32, O.Q4_K: 32, O.Q6_K: 16, O.Q4_0: 32, O.Q5_K: 32}[wtype]
     Wb = W.reshape(64, -1, blk)
     amax = np.abs(Wb).max(-1)
-    step = {O.Q8_0: amax / 127, O.Q6_K: amax / 31, O.Q4_K: (Wb.max(-1) - Wb.min(-1)) / 15}[wtype]
+    step = {O.Q8_0: amax / 127, O.Q6_K: amax / 31, O.Q4_K: (Wb.max(-1) - Wb.min(-1)) / 15,
+            O.Q4_0: amax / 7, O.Q5_K: (Wb.max(-1) - Wb.min(-1)) / 31}[wtype]
     err = np.abs(d - W).reshape(64, -1, blk).max(-1)
     assert np.all(err <= 0.75 * step + 1e-6)
 
@@ -155,6 +205,7 @@ def test_row_size():
     assert O.row_size(O.Q8_0, 64) == 68 and O.row_size(O.Q4_K, 512) == 288
     assert O.row_size(O.Q6_K, 256) == 210 and O.row_size(O.Q4_K, 100) == -1
     assert O.row_size(O.MXFP4, 64) == 34 and O.row_size(O.MXFP4, 48) == -1
+    assert O.row_size(O.Q4_0, 64) == 36 and O.row_size(O.Q5_K, 512) == 352 and O.row_size(O.Q5_K, 128) == -1
 
 
 # The OCP microscaling FP4 definition the MXFP4 decoder restates: an E2M1 code is

@@ -26,6 +26,8 @@ CASES = [
     ("Q8_0 leaf, M >= quant floor -> offload", True, lambda: mm_supported(K, N, MQ, mx.Q8_0)),
     ("Q4_K leaf, M >= quant floor -> offload", True, lambda: mm_supported(K, N, MQ, mx.Q4_K)),
     ("Q6_K leaf, M >= quant floor -> offload", True, lambda: mm_supported(K, N, MQ, mx.Q6_K)),
+    ("Q4_0 leaf, M >= quant floor -> offload", True, lambda: mm_supported(K, N, MQ, mx.Q4_0)),
+    ("Q5_K leaf, M >= quant floor -> offload", True, lambda: mm_supported(K, N, MQ, mx.Q5_K)),
     # MXFP4 (gpt-oss): the reference claims it for its MoE route; decoded exactly to fp16 here,
     # so MUL_MAT takes it as it takes the other quant types
     ("MXFP4 leaf, M >= quant floor -> offload", True, lambda: mm_supported(K, N, MQ, mx.MXFP4)),
