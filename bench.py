@@ -201,6 +201,16 @@ class Prefill:
             m[j > UBATCH * u + t] = float("-inf")
             self.masks.append(m.half())
         self.fa_ws = torch.empty(64 << 20, dtype=torch.uint8, device=dev)
+        # K-split partials of the widest split among the layer's launches (summed in split order)
+        launches = [[shapes["q"], shapes["k"], shapes["v"]], [shapes["o"]], [shapes["gate"], shapes["up"]],
+                    [shapes["down"]]]
+        need = 0
+        for outs in launches:
+            arr = (mx.GemmOut * len(outs))()
+            for i, (N, K) in enumerate(outs):
+                arr[i] = mx.GemmOut(None, N, 0, N, None, N)
+            need = max(need, int(mx.lib().mi355x_gemm_workspace(self.wt, UBATCH, outs[0][1], arr, len(outs))))
+        self.part = torch.empty(max(need, 256), dtype=torch.uint8, device=dev)
         self.timing = None
 
     # ---- op launchers (optionally bracketed by events on the launch stream) ----
@@ -226,9 +236,9 @@ class Prefill:
         arr = (mx.GemmOut * len(outs))()
         for i, (w, N, c) in enumerate(outs):
             arr[i] = mx.GemmOut(w.data_ptr(), N, 0, N, c.data_ptr(), c.stride(0))
-        self._ev("gemm", lambda: mx.check(mx.lib().mi355x_gemm(
+        self._ev("gemm", lambda: mx.check(mx.lib().mi355x_gemm_ws(
             self.wt, mx._ptr(self.a16), mx._ptr(self.scales), UBATCH, K, arr, len(outs),
-            mx.stream_handle()), "gemm"))
+            mx._ptr(self.part), self.part.numel(), mx.stream_handle()), "gemm"))
         self.flops["gemm"] += flops
 
     def _fa(self, u):
@@ -610,8 +620,8 @@ def configs_bench(args, subset=False):
         for M in Ms:
             x = torch.randn(M, K, device="cuda")
             out = torch.empty(M, N, device="cuda")
-            wsp = torch.empty(max(1, int(mx.lib().mi355x_mul_mat_workspace(M, K))), dtype=torch.uint8,
-                              device="cuda")
+            wsp = torch.empty(max(1, int(mx.lib().mi355x_mul_mat_workspace_for(dev_type, N, K, M))),
+                              dtype=torch.uint8, device="cuda")
             us = graph_time_us(lambda i: mx.mul_mat(dev_type, ws[i % ncopy], N, K, x, out, wsp), ncopy)
             record(f"{name} M={M}", us, 2.0 * M * N * K, payload.nbytes + M * K * 4 + M * N * 4)
         del ws

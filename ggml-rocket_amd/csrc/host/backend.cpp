@@ -272,7 +272,7 @@ struct mi355x_backend {
     bool dev_checked = false, dev_ok = false;
     hipStream_t stream = nullptr;
 
-    DevBuf act, a16, scales, out, wstage, wconv, fa_q, fa_k, fa_v, fa_m, fa_o, fa_ws, moe_b, moe_ids, moe_o, moe_ws;
+    DevBuf act, a16, scales, out, part, wstage, wconv, fa_q, fa_k, fa_v, fa_m, fa_o, fa_ws, moe_b, moe_ids, moe_o, moe_ws;
     DevBuf wscratch[4], moe_wscratch;   // per-call weights: unnamed, or over the cache budget
 
     std::unordered_map<std::string, WEntry> wcache;
@@ -567,8 +567,11 @@ int mul_mat_device(Ctx * c, const std::vector<mi355x_tensor *> & grp, bool want_
                                   c->stream));
     else
         TRY(mi355x_pack_act((const float *)c->act.p, K, M, K, (uint16_t *)c->a16.p, (float *)c->scales.p, c->stream));
-    TRY(mi355x_gemm(ws[0].dev_type, (const uint16_t *)c->a16.p, (const float *)c->scales.p, M, K, outs, (int)grp.size(),
-                    c->stream));
+    // K-split partials, summed in a fixed order (reproducible results)
+    const size_t pbytes = mi355x_gemm_workspace(ws[0].dev_type, M, K, outs, (int)grp.size());
+    if (pbytes) TRY(c->part.ensure(pbytes));
+    TRY(mi355x_gemm_ws(ws[0].dev_type, (const uint16_t *)c->a16.p, (const float *)c->scales.p, M, K, outs,
+                       (int)grp.size(), pbytes ? c->part.p : nullptr, pbytes, c->stream));
     // dst[i] is [N_i, M] contiguous: one member takes the output as is; a group's outputs come
     // back as whole rows of the concatenated [M][ntot] and are split into the members' column
     // blocks on the host
@@ -819,7 +822,7 @@ MI355X_API void mi355x_backend_free(mi355x_backend_t c) {
     for (auto & kv : c->wcache) (void)hipFree(kv.second.dev);
     report_residency(c);
     c->wcache.clear();
-    for (DevBuf * b : {&c->act, &c->a16, &c->scales, &c->out, &c->wstage, &c->wconv, &c->fa_q, &c->fa_k, &c->fa_v,
+    for (DevBuf * b : {&c->act, &c->a16, &c->scales, &c->out, &c->part, &c->wstage, &c->wconv, &c->fa_q, &c->fa_k, &c->fa_v,
                        &c->fa_m, &c->fa_o, &c->fa_ws, &c->moe_b, &c->moe_ids, &c->moe_o, &c->moe_ws,
                        &c->wscratch[0], &c->wscratch[1], &c->wscratch[2], &c->wscratch[3], &c->moe_wscratch})
         b->release();

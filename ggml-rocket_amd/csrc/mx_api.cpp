@@ -135,17 +135,15 @@ MI355X_API int mi355x_pack_act_tiled(const float * x_dev, int64_t ldx, int64_t M
     return pack_impl(true, x_dev, ldx, M, K, a16_dev, scales_dev, stream, nullptr, 0, 0);
 }
 
-// c_zeroed: the outputs were cleared by the activation pack (mi355x_mul_mat)
-static int gemm_impl(int wtype, const uint16_t * a16_dev, const float * scales_dev, int64_t M, int64_t K,
-                     const mi355x_gemm_out * outs, int n_out, void * stream, bool c_zeroed) {
+// The launch arguments of a GEMM, checked; `with_ptrs` also checks the operand pointers.
+static int gemm_lower(int wtype, const uint16_t * a16_dev, const float * scales_dev, int64_t M, int64_t K,
+                      const mi355x_gemm_out * outs, int n_out, bool with_ptrs, mx::GemmArgs & a) {
     const bool tiled = wtype == mx::T_F16T;
     if ((!known_wtype(wtype) && !tiled) || M < 0 || K <= 0 || K % 32 || K % blck(wtype) || M > INT32_MAX ||
         K > INT32_MAX)
         return MI355X_E_ARG;
     if (n_out < 1 || n_out > mx::GEMM_MAX_GROUPS || !outs) return MI355X_E_ARG;
-    if (M == 0) return MI355X_OK;
-    if (!a16_dev || !scales_dev || !aligned(a16_dev, 16)) return MI355X_E_ARG;
-    mx::GemmArgs a;
+    if (with_ptrs && M > 0 && (!a16_dev || !scales_dev || !aligned(a16_dev, 16))) return MI355X_E_ARG;
     memset(&a, 0, sizeof(a));
     a.A = a16_dev;
     a.scales = scales_dev;
@@ -157,9 +155,9 @@ static int gemm_impl(int wtype, const uint16_t * a16_dev, const float * scales_d
     int nt = 0;
     for (int i = 0; i < n_out; i++) {
         const mi355x_gemm_out & o = outs[i];
-        if (!o.w_dev || !o.c_dev || o.N <= 0 || o.N % 16 || o.N > INT32_MAX || o.ldc < o.N || o.row0 < 0 ||
-            o.rows_total < o.row0 + o.N || !aligned(o.w_dev, 16))
+        if (o.N <= 0 || o.N % 16 || o.N > INT32_MAX || o.ldc < o.N || o.row0 < 0 || o.rows_total < o.row0 + o.N)
             return MI355X_E_ARG;
+        if (with_ptrs && (!o.w_dev || !o.c_dev || !aligned(o.w_dev, 16))) return MI355X_E_ARG;
         a.g[i].W = o.w_dev;
         a.g[i].rows_total = o.rows_total;
         a.g[i].row0 = o.row0;
@@ -169,13 +167,37 @@ static int gemm_impl(int wtype, const uint16_t * a16_dev, const float * scales_d
         a.g[i].ntile_begin = nt;
         nt += (int)((o.N + 127) / 128);
     }
-    return hip_status(mx::launch_gemm(wtype, a, nt, S(stream), c_zeroed));
+    return MI355X_OK;
+}
+
+// c_zeroed: the outputs were cleared by the activation pack (mi355x_mul_mat); part / part_bytes:
+// workspace for the partial sums of a K split past two ways
+static int gemm_impl(int wtype, const uint16_t * a16_dev, const float * scales_dev, int64_t M, int64_t K,
+                     const mi355x_gemm_out * outs, int n_out, void * stream, bool c_zeroed, void * part,
+                     size_t part_bytes) {
+    mx::GemmArgs a;
+    const int st = gemm_lower(wtype, a16_dev, scales_dev, M, K, outs, n_out, true, a);
+    if (st != MI355X_OK || M == 0) return st;
+    if (part && !aligned(part, 16)) return MI355X_E_ARG;
+    return hip_status(mx::launch_gemm(wtype, a, 0, S(stream), c_zeroed, (float *)part, part ? part_bytes : 0));
 }
 
 MI355X_API int mi355x_gemm(int wtype, const uint16_t * a16_dev, const float * scales_dev,
                            int64_t M, int64_t K, const mi355x_gemm_out * outs, int n_out,
                            void * stream) {
-    return gemm_impl(wtype, a16_dev, scales_dev, M, K, outs, n_out, stream, false);
+    return gemm_impl(wtype, a16_dev, scales_dev, M, K, outs, n_out, stream, false, nullptr, 0);
+}
+
+MI355X_API size_t mi355x_gemm_workspace(int wtype, int64_t M, int64_t K, const mi355x_gemm_out * outs, int n_out) {
+    mx::GemmArgs a;
+    if (M <= 0 || gemm_lower(wtype, nullptr, nullptr, M, K, outs, n_out, false, a) != MI355X_OK) return 0;
+    return mx::gemm_split_bytes(wtype, a);
+}
+
+MI355X_API int mi355x_gemm_ws(int wtype, const uint16_t * a16_dev, const float * scales_dev,
+                              int64_t M, int64_t K, const mi355x_gemm_out * outs, int n_out,
+                              void * workspace_dev, size_t workspace_bytes, void * stream) {
+    return gemm_impl(wtype, a16_dev, scales_dev, M, K, outs, n_out, stream, false, workspace_dev, workspace_bytes);
 }
 
 // M rows rounded up to 16: the tiled layout's padding (the row-major pack uses M rows of it).
@@ -188,6 +210,19 @@ MI355X_API size_t mi355x_mul_mat_workspace(int64_t M, int64_t K) {
     return mul_mat_a16_bytes(M, K) + (size_t)M * 4;
 }
 
+// The K-split partials of mi355x_mul_mat start at this offset of its workspace.
+static size_t mul_mat_part_offset(int64_t M, int64_t K) {
+    return (mi355x_mul_mat_workspace(M, K) + 255) & ~(size_t)255;
+}
+
+MI355X_API size_t mi355x_mul_mat_workspace_for(int wtype, int64_t N, int64_t K, int64_t M) {
+    const size_t need = mi355x_mul_mat_workspace(M, K);
+    if (need == 0) return 0;
+    const mi355x_gemm_out o = {nullptr, N, 0, N, nullptr, N};
+    const size_t part = mi355x_gemm_workspace(wtype, M, K, &o, 1);
+    return part ? mul_mat_part_offset(M, K) + part : need;
+}
+
 MI355X_API int mi355x_mul_mat(int wtype, const void * w_dev, int64_t N, int64_t K,
                               const float * x_dev, int64_t ldx, int64_t M,
                               float * dst_dev, int64_t ldd,
@@ -198,7 +233,11 @@ MI355X_API int mi355x_mul_mat(int wtype, const void * w_dev, int64_t N, int64_t 
     if (!workspace_dev || workspace_bytes < need) return MI355X_E_NOMEM;
     uint16_t * a16 = (uint16_t *)workspace_dev;
     float * scales = (float *)((char *)workspace_dev + mul_mat_a16_bytes(M, K));
-    // a GEMM that adds its K splits into dst has it cleared by the pack, in the same launch
+    // the room past the pack holds K-split partials
+    const size_t poff = mul_mat_part_offset(M, K);
+    void * part = workspace_bytes > poff ? (char *)workspace_dev + poff : nullptr;
+    const size_t part_bytes = part ? workspace_bytes - poff : 0;
+    // a GEMM that adds a two-way K split into dst has it cleared by the pack, in the same launch
     bool zero = false;
     if ((known_wtype(wtype) || wtype == mx::T_F16T) && K > 0 && K <= INT32_MAX && M <= INT32_MAX && N > 0 &&
         N <= INT32_MAX && dst_dev && ldd >= N) {
@@ -208,12 +247,12 @@ MI355X_API int mi355x_mul_mat(int wtype, const void * w_dev, int64_t N, int64_t 
         probe.K = (int)K;
         probe.ng = 1;
         probe.g[0].N = (int)N;
-        zero = mx::gemm_accumulates(wtype, probe);
+        zero = mx::gemm_accumulates(wtype, probe, part_bytes);
     }
     int st = pack_impl(wtype == mx::T_F16T, x_dev, ldx, M, K, a16, scales, stream, zero ? dst_dev : nullptr, ldd, N);
     if (st != MI355X_OK) return st;
     mi355x_gemm_out o = {w_dev, N, 0, N, dst_dev, ldd};
-    return gemm_impl(wtype, a16, scales, M, K, &o, 1, stream, zero);
+    return gemm_impl(wtype, a16, scales, M, K, &o, 1, stream, zero, part, part_bytes);
 }
 
 // ---- FLASH_ATTN_EXT ---------------------------------------------------------------------------

@@ -206,6 +206,19 @@ __device__ __forceinline__ void mma_slab(const uint8_t * st, int wm, int wn, int
     }
 }
 
+// Where a K-split block writes: with partials (a split past two ways) its split's slab of them,
+// row stride ldp, group g's columns from pcol; otherwise the group's own output, which it adds
+// into when the split is two ways.
+__device__ __forceinline__ void split_target(const GemmArgs & a, int g, int split, float *& Cp, int64_t & ldc) {
+    if (!a.part) return;
+    int64_t pcol = a.g[0].pcol;
+#pragma unroll
+    for (int i = 1; i < GEMM_MAX_GROUPS; i++)
+        if (i == g) pcol = a.g[i].pcol;
+    Cp = a.part + (int64_t)split * a.M * a.ldp + pcol;
+    ldc = a.ldp;
+}
+
 template <int WT, int BM, int BN, int WM, int WN, int R, int KSPLIT>
 __global__ void __launch_bounds__(GEMM_THREADS)
 __attribute__((amdgpu_waves_per_eu((BM == 128 && BN == 128) ? 2 : 1, (BM == 128 && BN == 128) ? 2 : 1)))
@@ -240,6 +253,7 @@ gemm_kernel(GemmArgs args) {
             G.W = args.g[i].W; G.rows_total = args.g[i].rows_total; G.row0 = args.g[i].row0; G.N = args.g[i].N;
             G.C = args.g[i].C; G.ldc = args.g[i].ldc; G.ntile_begin = args.g[i].ntile_begin;
         }
+    split_target(args, g, split, G.C, G.ldc);
     const int n0 = (nt - G.ntile_begin) * BN;
     const int m0 = mt * BM;
 
@@ -299,7 +313,7 @@ gemm_kernel(GemmArgs args) {
             for (int j = 0; j < C::NJ; j++) {
                 const int n = n0 + wn * C::TN + j * 32 + lr;
                 if (n < G.N) {
-                    if (ks == 1) crow[n] = acc[i][j][e];
+                    if (ks == 1 || args.part) crow[n] = acc[i][j][e];
                     else unsafeAtomicAdd(crow + n, acc[i][j][e]);
                 }
             }
@@ -319,9 +333,14 @@ gemm_kernel(GemmArgs args) {
 // weight of the next group is in flight in a second register set while this one is multiplied.
 // Issue order matters: one vmcnt counter covers every load in issue order, so each step issues
 // the next group's activation loads before its weight loads (their LDS store then waits for them
-// alone, not for the weight). Past the block's last group the loads re-fetch it (decoded as
-// zero), so the loop body has no branch between a load and its use. Blocks split K and add their
-// partial sums atomically into a zeroed output.
+// alone, not for the weight), and nothing consumes a loaded value before the step's compute: the
+// activation's row / K mask is applied at its LDS store, since a select right after a load would
+// make the compiler wait for that load before issuing the next. Past the block's last group the
+// loads re-fetch it and are never multiplied, so the loop body has no branch between a load and
+// its use. The weights are decoded by the packed-fp16 decoders (decode_fast: a quarter to a half
+// of the VALU instructions of the exact decode, which bounded this kernel). Blocks split K: past
+// two ways each writes its slab of the partials, summed in split order by reduce_splits_kernel;
+// two ways add into a zeroed output.
 // ---------------------------------------------------------------------------------------------
 constexpr int SK_MAX_M = 128;
 constexpr int SK_NW = 4;
@@ -363,6 +382,7 @@ gemm_skinny_kernel(GemmArgs args, int groups_per_block) {
             G.W = args.g[i].W; G.rows_total = args.g[i].rows_total; G.row0 = args.g[i].row0; G.N = args.g[i].N;
             G.C = args.g[i].C; G.ldc = args.g[i].ldc; G.ntile_begin = args.g[i].ntile_begin;
         }
+    split_target(args, g, split, G.C, G.ldc);
     const int n = (nt - G.ntile_begin) * (32 * NW) + 32 * wave + lr;   // this lane's weight row
     const bool okn = n < G.N;
     const int64_t row = G.row0 + (okn ? n : G.N - 1);
@@ -372,22 +392,28 @@ gemm_skinny_kernel(GemmArgs args, int groups_per_block) {
     const int gn = max(0, min(ngroups, gb + groups_per_block) - gb);    // groups of the block
     const int glast = gb + max(gn, 1) - 1;
 
-    auto load_a = [&](u32x4 (&av)[APT], int grp) {   // rows past M and k past K read as zero
+    // rows past M and k past K read as zero: the load takes a valid address and the mask is
+    // applied when the value is stored to LDS (where the load is waited for anyway), so no
+    // wait sits between one load and the next
+    auto load_a = [&](u32x4 (&av)[APT], uint32_t & amask, int grp) {
         const int64_t kb = (int64_t)min(grp, glast) * CH * 64;
+        amask = 0;
 #pragma unroll
         for (int i = 0; i < APT; i++) {
             const int q = t + i * NW * WAVE, r = q / CPR, c = q % CPR;
             const int64_t k = kb + 8 * c;
             const bool ok = r < args.M && k < args.K;
             av[i] = *(const u32x4 *)(args.A + (ok ? (int64_t)r * args.lda + k : 0));
-            if (!ok) av[i] = u32x4{0, 0, 0, 0};
+            amask |= ok ? (1u << i) : 0u;
         }
     };
-    auto store_a = [&](const u32x4 (&av)[APT], int buf) {
+    auto store_a = [&](const u32x4 (&av)[APT], uint32_t amask, int buf) {
 #pragma unroll
         for (int i = 0; i < APT; i++) {
             const int q = t + i * NW * WAVE, r = q / CPR, c = q % CPR;
-            *(u32x4 *)(sa + buf * SLICE + (r * CPR + (c ^ (r & 7))) * 16) = av[i];
+            const bool ok = (amask >> i) & 1u;
+            const u32x4 v = {ok ? av[i][0] : 0u, ok ? av[i][1] : 0u, ok ? av[i][2] : 0u, ok ? av[i][3] : 0u};
+            *(u32x4 *)(sa + buf * SLICE + (r * CPR + (c ^ (r & 7))) * 16) = v;
         }
     };
     auto load_w = [&](WLoad<WT> (&w)[CH], int grp) {
@@ -410,7 +436,7 @@ gemm_skinny_kernel(GemmArgs args, int groups_per_block) {
         for (int c = 0; c < CH; c++) {
             u32x4 b[4];
             int run0, run1;
-            w[c].decode(lg, b, run0, run1);
+            w[c].decode_fast(lg, b, run0, run1);
 #pragma unroll
             for (int s = 0; s < 4; s++) {
                 const int ch = 8 * c + (s < 2 ? run0 + 8 * s : run1 + 8 * (s - 2)) / 8;   // slice chunk
@@ -427,21 +453,22 @@ gemm_skinny_kernel(GemmArgs args, int groups_per_block) {
 
     WLoad<WT> w0[CH], w1[CH];
     u32x4 av[APT];
-    load_a(av, gb);
+    uint32_t amask;
+    load_a(av, amask, gb);
     load_w(w0, gb);
-    store_a(av, 0);
+    store_a(av, amask, 0);
     __syncthreads();
     int q = 0;
     for (; q + 2 <= gn; q += 2) {
-        load_a(av, gb + q + 1);
+        load_a(av, amask, gb + q + 1);
         load_w(w1, gb + q + 1);
         compute(w0, 0);
-        store_a(av, 1);
+        store_a(av, amask, 1);
         __syncthreads();
-        load_a(av, gb + q + 2);
+        load_a(av, amask, gb + q + 2);
         load_w(w0, gb + q + 2);
         compute(w1, 1);
-        store_a(av, 0);
+        store_a(av, amask, 0);
         __syncthreads();
     }
     if (q < gn) compute(w0, 0);
@@ -455,7 +482,7 @@ gemm_skinny_kernel(GemmArgs args, int groups_per_block) {
             const int r = i * 32 + 8 * (e / 4) + 4 * lg + (e % 4);
             if (r >= args.M) continue;
             float * p = G.C + (int64_t)r * G.ldc + n;
-            if (ks == 1) *p = acc[i][0][e];
+            if (ks == 1 || args.part) *p = acc[i][0][e];
             else unsafeAtomicAdd(p, acc[i][0][e]);
         }
     }
@@ -955,6 +982,7 @@ gemm_q4k_kernel(GemmArgs args) {
             W = (const uint8_t *)args.g[i].W; row0 = args.g[i].row0; N = args.g[i].N;
             ntb = args.g[i].ntile_begin; Cp = args.g[i].C; ldc = args.g[i].ldc;
         }
+    split_target(args, g, split, Cp, ldc);
     const int n0 = (nt - ntb) * C::BN, m0 = mt * BM;
     const int M = args.M, K = args.K;
     const int nsb = K / 256;                                   // Q4_K blocks a row
@@ -1116,11 +1144,50 @@ gemm_q4k_kernel(GemmArgs args) {
             for (int j = 0; j < C::NJ; j++) {
                 const int n = n0 + wn * C::TN + j * 32 + lr;
                 if (n < N) {
-                    if (ks == 1) crow[n] = acc[i][j][e];
+                    if (ks == 1 || args.part) crow[n] = acc[i][j][e];
                     else unsafeAtomicAdd(crow + n, acc[i][j][e]);
                 }
             }
         }
+    }
+}
+
+// The K-split partials summed in split order, C_g[r][n] = P[0][r][pcol_g + n] + P[1][..] + ...:
+// one thread per 4 columns of a partial row (every group's N and pcol are multiples of 16).
+__global__ void __launch_bounds__(256) reduce_splits_kernel(GemmArgs a, int ks) {
+    const int64_t q = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    const int64_t per_row = a.ldp / 4;
+    if (q >= (int64_t)a.M * per_row) return;
+    const int64_t r = q / per_row, c = 4 * (q % per_row);
+    int g = 0;
+#pragma unroll
+    for (int i = 1; i < GEMM_MAX_GROUPS; i++)
+        if (i < a.ng && c >= a.g[i].pcol) g = i;
+    float * C = a.g[0].C;
+    int64_t ldc = a.g[0].ldc, pcol = a.g[0].pcol;
+#pragma unroll
+    for (int i = 1; i < GEMM_MAX_GROUPS; i++)
+        if (i == g) { C = a.g[i].C; ldc = a.g[i].ldc; pcol = a.g[i].pcol; }
+    const int64_t slab = (int64_t)a.M * a.ldp;
+    const float * p = a.part + r * a.ldp + c;
+    float4v s = *(const float4v *)p;
+    // loads in batches of 8 (all in flight at once), added in split order
+    for (int k0 = 1; k0 < ks; k0 += 8) {
+        float4v v[8];
+#pragma unroll
+        for (int j = 0; j < 8; j++) v[j] = k0 + j < ks ? *(const float4v *)(p + (k0 + j) * slab) : float4v{0, 0, 0, 0};
+#pragma unroll
+        for (int j = 0; j < 8; j++)
+            if (k0 + j < ks)
+#pragma unroll
+                for (int e = 0; e < 4; e++) s[e] += v[j][e];
+    }
+    float * o = C + r * ldc + (c - pcol);
+    if ((reinterpret_cast<uintptr_t>(o) & 15) == 0) {
+        *(float4v *)o = s;
+    } else {
+#pragma unroll
+        for (int e = 0; e < 4; e++) o[e] = s[e];
     }
 }
 
@@ -1445,28 +1512,28 @@ static int64_t tiles_n_cols(const GemmArgs & a) {
 static double reg_split_est(const GemmArgs & a) {
     return 6.65 * std::pow((double)a.K, 0.75) / std::sqrt((double)a.M * (double)tiles_n_cols(a));
 }
-static int reg_split(const GemmArgs & a) {
+static int reg_split(const GemmArgs & a, int cap) {
     const int nk = (a.K + BK - 1) / BK;
     if (const char * e = getenv("MI355X_GEMM_KSPLIT")) {
         const int v = atoi(e);
-        if (v >= 2 && v <= nk) return v;
+        if (v >= 2 && v <= nk) return std::min(v, cap);
     }
     int ks = (int)std::lround(reg_split_est(a));
-    const int cap = nk / 4 < 16 ? nk / 4 : 16;
-    if (ks > cap) ks = cap;
+    const int most = std::min(nk / 4 < 16 ? nk / 4 : 16, cap);
+    if (ks > most) ks = most;
     return ks < 2 ? 2 : ks;
 }
 
 // The K split of the Q4_K DMA split configurations (18, 19): about one block per CU, in whole
 // Q4_K blocks of K, at least 2 ways and at least 2 blocks (8 stages) a split.
 // MI355X_GEMM_KSPLIT=<n> forces n (for tuning).
-static int q4k_split(const GemmArgs & a, int bm, int bn) {
+static int q4k_split(const GemmArgs & a, int bm, int bn, int cap) {
     const int nsb = a.K / 256;
-    const int cap = std::max(2, nsb / 2);
+    const int most = std::min(std::max(2, nsb / 2), cap);
     int ks = 0;
     if (const char * e = getenv("MI355X_GEMM_KSPLIT")) ks = atoi(e);
     if (ks < 2) ks = (int)std::lround((double)cu_count() / tiles_of(a, bm, bn));
-    ks = std::min(std::max(ks, 2), cap);
+    ks = std::min(std::max(ks, 2), most);
     // equal splits of whole blocks: the count that leaves no split empty
     const int per = (nsb + ks - 1) / ks;
     return (nsb + per - 1) / per;
@@ -1573,8 +1640,8 @@ static int skinny_ntiles(const GemmArgs & a) {
     return nt;
 }
 
-// K groups per block; the split count is ceil(groups / that)
-static int skinny_gpb(const GemmArgs & a) {
+// K groups per block (the split count is ceil(groups / that)), at most `cap` splits
+static int skinny_gpb(const GemmArgs & a, int cap) {
     const int ngroups = ((a.K + 63) / 64 + skinny_ch(a.M) - 1) / skinny_ch(a.M);
     double blocks = 240.0;
     if (const char * e = getenv("MI355X_SKINNY_BLOCKS")) {   // tuning override
@@ -1582,86 +1649,119 @@ static int skinny_gpb(const GemmArgs & a) {
         if (v > 0) blocks = v;
     }
     const double target = blocks / skinny_ntiles(a);
-    const int ks = std::max(1, (int)std::lround(target));
+    const int ks = std::min(std::max(1, (int)std::lround(target)), cap);
     return (ngroups + ks - 1) / ks;
 }
 
-static int skinny_split(const GemmArgs & a) {
-    const int ngroups = ((a.K + 63) / 64 + skinny_ch(a.M) - 1) / skinny_ch(a.M);
-    const int gpb = skinny_gpb(a);
-    return (ngroups + gpb - 1) / gpb;
-}
-
 template <int WT>
-static hipError_t launch_skinny(const GemmArgs & a, int nblocks, hipStream_t st) {
-    const int mt = (a.M + 31) / 32, gpb = skinny_gpb(a);
+static hipError_t launch_skinny(const GemmArgs & a, int nblocks, int gpb, hipStream_t st) {
+    const int mt = (a.M + 31) / 32;
     if (mt == 1) hipLaunchKernelGGL((gemm_skinny_kernel<WT, 1, 4>), dim3(nblocks), dim3(SK_NW * WAVE), 0, st, a, gpb);
     else if (mt == 2) hipLaunchKernelGGL((gemm_skinny_kernel<WT, 2, 4>), dim3(nblocks), dim3(SK_NW * WAVE), 0, st, a, gpb);
     else hipLaunchKernelGGL((gemm_skinny_kernel<WT, 4, 2>), dim3(nblocks), dim3(SK_NW * WAVE), 0, st, a, gpb);
     return hipGetLastError();
 }
 
-bool gemm_accumulates(int wt, const GemmArgs & a) {
-    if (use_skinny(wt, a)) return skinny_split(a) > 1;
-    return kCfgs[choose_cfg(wt, a)].ksplit > 1;
+// A launch's configuration and K split. The split is at most `cap` ways: the number of partial
+// slabs [M][sum of N] the caller's workspace holds, and at least 2.
+struct GemmPlan {
+    bool skinny;
+    int cfg;    // kCfgs index (unused for the skinny kernel)
+    int ks;     // K split
+    int gpb;    // skinny kernel: K groups per block
+};
+
+static int64_t total_cols(const GemmArgs & a) {
+    int64_t n = 0;
+    for (int i = 0; i < a.ng; i++) n += a.g[i].N;
+    return n;
 }
 
-hipError_t launch_gemm(int wt, const GemmArgs & a_in, int /*unused*/, hipStream_t st, bool c_zeroed) {
-    GemmArgs a = a_in;
+static int split_cap(const GemmArgs & a, size_t part_bytes) {
+    const size_t slab = (size_t)a.M * (size_t)total_cols(a) * sizeof(float);
+    const size_t n = slab ? part_bytes / slab : 0;
+    return (int)std::max<size_t>(2, std::min<size_t>(n, 64));
+}
+
+static GemmPlan plan_gemm(int wt, const GemmArgs & a, int cap) {
+    GemmPlan p{};
     if (use_skinny(wt, a)) {
-        const int bn = 32 * SK_NW;
-        int nt = 0;
-        for (int i = 0; i < a.ng; i++) {
-            a.g[i].ntile_begin = nt;
-            nt += (a.g[i].N + bn - 1) / bn;
-        }
-        a.m_tiles = 1;
-        a.ksplit = skinny_split(a);
-        const int nblocks = nt * a.ksplit;
-        if (nblocks <= 0) return hipSuccess;
-        if (a.ksplit > 1 && !c_zeroed) {
-            hipLaunchKernelGGL(zero_rows_kernel, dim3(a.M, a.ng), dim3(256), 0, st, a);
-            hipError_t e = hipGetLastError();
-            if (e != hipSuccess) return e;
-        }
-        switch (wt) {
-            case T_F16: return launch_skinny<T_F16>(a, nblocks, st);
-            case T_Q8_0: return launch_skinny<T_Q8_0>(a, nblocks, st);
-            case T_Q4_0: return launch_skinny<T_Q4_0>(a, nblocks, st);
-            case T_Q4_K: return launch_skinny<T_Q4_K>(a, nblocks, st);
-            case T_Q5_K: return launch_skinny<T_Q5_K>(a, nblocks, st);
-            case T_Q6_K: return launch_skinny<T_Q6_K>(a, nblocks, st);
-            case T_MXFP4: return launch_skinny<T_MXFP4>(a, nblocks, st);
-            default: return hipErrorInvalidValue;
-        }
+        p.skinny = true;
+        p.cfg = SKINNY_CFG;
+        p.gpb = skinny_gpb(a, cap);
+        const int ngroups = ((a.K + 63) / 64 + skinny_ch(a.M) - 1) / skinny_ch(a.M);
+        p.ks = (ngroups + p.gpb - 1) / p.gpb;
+        return p;
     }
-    const int cfg = choose_cfg(wt, a);
-    const CfgDesc & d = kCfgs[cfg];
-    a.m_tiles = (a.M + d.bm - 1) / d.bm;
+    p.cfg = choose_cfg(wt, a);
+    const CfgDesc & d = kCfgs[p.cfg];
+    p.ks = p.cfg == 1 ? reg_split(a, cap)
+         : (d.kind == Q4KDMA && d.ksplit > 1) ? q4k_split(a, d.bm, d.bn, cap) : d.ksplit;
+    return p;
+}
+
+size_t gemm_split_bytes(int wt, const GemmArgs & a) {
+    const GemmPlan p = plan_gemm(wt, a, 64);
+    return p.ks > 2 ? (size_t)p.ks * (size_t)a.M * (size_t)total_cols(a) * sizeof(float) : 0;
+}
+
+bool gemm_accumulates(int wt, const GemmArgs & a, size_t part_bytes) {
+    return plan_gemm(wt, a, split_cap(a, part_bytes)).ks == 2;
+}
+
+hipError_t launch_gemm(int wt, const GemmArgs & a_in, int /*unused*/, hipStream_t st, bool c_zeroed, float * part,
+                       size_t part_bytes) {
+    GemmArgs a = a_in;
+    const GemmPlan p = plan_gemm(wt, a, part ? split_cap(a, part_bytes) : 2);
+    const int bn = p.skinny ? 32 * SK_NW : kCfgs[p.cfg].bn;
     int nt = 0;
+    int64_t pcol = 0;
     for (int i = 0; i < a.ng; i++) {
         a.g[i].ntile_begin = nt;
-        nt += (a.g[i].N + d.bn - 1) / d.bn;
+        nt += (a.g[i].N + bn - 1) / bn;
+        a.g[i].pcol = pcol;
+        pcol += a.g[i].N;
     }
-    a.ksplit = cfg == 1 ? reg_split(a) : (d.kind == Q4KDMA && d.ksplit > 1) ? q4k_split(a, d.bm, d.bn) : d.ksplit;
+    a.m_tiles = p.skinny ? 1 : (a.M + kCfgs[p.cfg].bm - 1) / kCfgs[p.cfg].bm;
+    a.ksplit = p.ks;
+    a.part = p.ks > 2 ? part : nullptr;
+    a.ldp = pcol;
     const int nblocks = nt * a.m_tiles * a.ksplit;
     if (nblocks <= 0) return hipSuccess;
-    if (d.ksplit > 1 && !c_zeroed) {
+    if (p.ks == 2 && !c_zeroed) {
         hipLaunchKernelGGL(zero_rows_kernel, dim3(a.M, a.ng), dim3(256), 0, st, a);
         hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
     }
-    switch (wt) {
-        case T_F16: return launch_cfg<T_F16>(cfg, a, nblocks, st);
-        case T_F16T: return launch_cfg<T_F16T>(cfg, a, nblocks, st);
-        case T_Q8_0: return launch_cfg<T_Q8_0>(cfg, a, nblocks, st);
-        case T_Q4_0: return launch_cfg<T_Q4_0>(cfg, a, nblocks, st);
-        case T_Q4_K: return launch_cfg<T_Q4_K>(cfg, a, nblocks, st);
-        case T_Q5_K: return launch_cfg<T_Q5_K>(cfg, a, nblocks, st);
-        case T_Q6_K: return launch_cfg<T_Q6_K>(cfg, a, nblocks, st);
-        case T_MXFP4: return launch_cfg<T_MXFP4>(cfg, a, nblocks, st);
-        default: return hipErrorInvalidValue;
+    hipError_t e = hipErrorInvalidValue;
+    if (p.skinny) {
+        switch (wt) {
+            case T_F16: e = launch_skinny<T_F16>(a, nblocks, p.gpb, st); break;
+            case T_Q8_0: e = launch_skinny<T_Q8_0>(a, nblocks, p.gpb, st); break;
+            case T_Q4_0: e = launch_skinny<T_Q4_0>(a, nblocks, p.gpb, st); break;
+            case T_Q4_K: e = launch_skinny<T_Q4_K>(a, nblocks, p.gpb, st); break;
+            case T_Q5_K: e = launch_skinny<T_Q5_K>(a, nblocks, p.gpb, st); break;
+            case T_Q6_K: e = launch_skinny<T_Q6_K>(a, nblocks, p.gpb, st); break;
+            case T_MXFP4: e = launch_skinny<T_MXFP4>(a, nblocks, p.gpb, st); break;
+            default: break;
+        }
+    } else {
+        switch (wt) {
+            case T_F16: e = launch_cfg<T_F16>(p.cfg, a, nblocks, st); break;
+            case T_F16T: e = launch_cfg<T_F16T>(p.cfg, a, nblocks, st); break;
+            case T_Q8_0: e = launch_cfg<T_Q8_0>(p.cfg, a, nblocks, st); break;
+            case T_Q4_0: e = launch_cfg<T_Q4_0>(p.cfg, a, nblocks, st); break;
+            case T_Q4_K: e = launch_cfg<T_Q4_K>(p.cfg, a, nblocks, st); break;
+            case T_Q5_K: e = launch_cfg<T_Q5_K>(p.cfg, a, nblocks, st); break;
+            case T_Q6_K: e = launch_cfg<T_Q6_K>(p.cfg, a, nblocks, st); break;
+            case T_MXFP4: e = launch_cfg<T_MXFP4>(p.cfg, a, nblocks, st); break;
+            default: break;
+        }
     }
+    if (e != hipSuccess || !a.part) return e;
+    const int64_t threads = (int64_t)a.M * (a.ldp / 4);
+    hipLaunchKernelGGL(reduce_splits_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, st, a, a.ksplit);
+    return hipGetLastError();
 }
 
 template <bool TL>

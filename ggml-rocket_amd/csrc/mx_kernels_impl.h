@@ -19,6 +19,7 @@ struct GemmGroup {
     float * C;             // output [M][ldc]
     int64_t ldc;
     int ntile_begin;       // first global N tile of this group
+    int64_t pcol;          // first column of this group in a row of the K-split partials
 };
 
 struct GemmArgs {
@@ -29,6 +30,9 @@ struct GemmArgs {
     int m_tiles;
     int ng;
     int ksplit;            // K split of a register-staged split configuration (set by the launcher)
+    float * part;          // K splits past two: [ksplit][M][ldp] partial sums, one slab per split,
+                           // summed in split order by a second launch (null: no such split)
+    int64_t ldp;           // row length of the partials: the groups' N, concatenated
     GemmGroup g[GEMM_MAX_GROUPS];
 };
 
@@ -86,10 +90,17 @@ hipError_t launch_pack_act(const float * X, int64_t ldx, int M, int K, uint16_t 
 hipError_t launch_pack_act_tiled(const float * X, int64_t ldx, int M, int K, uint16_t * A16, float * scales,
                                  hipStream_t st, float * zc = nullptr, int64_t ldzc = 0, int zn = 0);
 // c_zeroed: the outputs are already zero (the pack cleared them), so a launch that adds its K
-// splits into them needs no fill of its own
-hipError_t launch_gemm(int wt, const GemmArgs & a, int n_tiles_total, hipStream_t st, bool c_zeroed = false);
-// whether launch_gemm would add into its outputs (a K split) rather than write them
-bool gemm_accumulates(int wt, const GemmArgs & a);
+// splits into them needs no fill of its own. part / part_bytes: workspace for the partial sums
+// of a K split past two ways; a split that does not fit is narrowed, down to two ways (added
+// into the zeroed output: with two addends on zero the order cannot change the sum). Every
+// split is therefore reduced in a fixed order, and equal inputs give equal bits.
+hipError_t launch_gemm(int wt, const GemmArgs & a, int n_tiles_total, hipStream_t st, bool c_zeroed = false,
+                       float * part = nullptr, size_t part_bytes = 0);
+// whether launch_gemm, with part_bytes of partial workspace, would add into its outputs (a
+// two-way K split) rather than write them
+bool gemm_accumulates(int wt, const GemmArgs & a, size_t part_bytes);
+// partial workspace bytes of the launch's fastest K split (0 if it splits two ways or less)
+size_t gemm_split_bytes(int wt, const GemmArgs & a);
 hipError_t launch_dequant_f16(int wt, const void * W, int64_t rows, int64_t K, uint16_t * out, hipStream_t st);
 hipError_t launch_f16_tiled(int wt, const void * W, int64_t rows, int64_t K, uint16_t * out, hipStream_t st);
 hipError_t launch_pack_weight(int wt, const void * src, int64_t rows, int64_t K, void * dst, hipStream_t st);

@@ -78,6 +78,24 @@ __device__ __forceinline__ int mxfp4_code(uint32_t c) {
     return (c & 8u) ? -mag : mag;
 }
 
+// Packed-fp16 decoding, for kernels whose decode VALU is the bound (the skinny GEMM): a small
+// integer code c (0 <= c < 256) is placed under the fp16 exponent of 1024, whose mantissa step is
+// 1, by one byte permute per pair (v_perm_b32: bytes {c0, 0x64, c1, 0x64} = {1024 + c0, 1024 +
+// c1}); subtracting the offset is exact, and one packed FMA applies scale and bias. The scale
+// and bias are rounded to fp16 before the product, so a value can differ from the exact decode
+// by a few fp16 ulp; the dequant kernels keep the exact form.
+__device__ __forceinline__ half2v h2_of(uint32_t u) { return __builtin_bit_cast(half2v, u); }
+__device__ __forceinline__ uint32_t u_of(half2v h) { return __builtin_bit_cast(uint32_t, h); }
+// bytes 0,1 (sel01) or 2,3 (sel23) of x, each < 256, as {1024 + x.b0, 1024 + x.b1} etc.
+constexpr uint32_t PERM_B01 = 0x04010400u, PERM_B23 = 0x04030402u;
+__device__ __forceinline__ half2v magic_pair(uint32_t x, uint32_t sel) {
+    return h2_of(__builtin_amdgcn_perm(0x64646464u, x, sel));
+}
+__device__ __forceinline__ half2v splat_h(float v) {
+    const _Float16 h = (_Float16)v;
+    return half2v{h, h};
+}
+
 // Global-load stage of one thread's share of a BK=64 weight tile: 32 consecutive-in-format
 // values of one row. `u` (0/1) selects which half of the row's 64 values the thread takes.
 // decode() produces them as fp16 in two runs of 16, at K offsets run0 and run1 of the slab.
@@ -93,6 +111,9 @@ template <> struct WLoad<T_F16> {
         const u32x4 * p = (const u32x4 *)(W + (row * K + (k < K ? k : 0)) * 2);
 #pragma unroll
         for (int i = 0; i < 4; i++) v[i] = p[i];
+    }
+    __device__ __forceinline__ void decode_fast(int u, u32x4 out[4], int & run0, int & run1) const {
+        decode(u, out, run0, run1);
     }
     __device__ __forceinline__ void decode(int u, u32x4 out[4], int & run0, int & run1) const {
 #pragma unroll
@@ -136,6 +157,23 @@ template <> struct WLoad<T_Q8_0> {
         run0 = 32 * u;
         run1 = 32 * u + 16;
     }
+    // packed: a signed byte b as 1024 + (b ^ 0x80) = 1152 + b, less 1152, times d (a zero scale
+    // where the item is masked: a finite code times zero is zero, one select per item)
+    __device__ __forceinline__ void decode_fast(int u, u32x4 out[4], int & run0, int & run1) const {
+        const half2v D = h2_of(ok ? (uint32_t)d * 0x10001u : 0u);
+        const half2v OFF = {(_Float16)-1152.0f, (_Float16)-1152.0f};
+        uint32_t o[16];
+#pragma unroll
+        for (int w = 0; w < 8; w++) {
+            const uint32_t x = q[w / 4][w % 4] ^ 0x80808080u;
+            o[2 * w] = u_of((magic_pair(x, PERM_B01) + OFF) * D);
+            o[2 * w + 1] = u_of((magic_pair(x, PERM_B23) + OFF) * D);
+        }
+#pragma unroll
+        for (int i = 0; i < 4; i++) out[i] = u32x4{o[4 * i], o[4 * i + 1], o[4 * i + 2], o[4 * i + 3]};
+        run0 = 32 * u;
+        run1 = 32 * u + 16;
+    }
 };
 
 // MXFP4: one 32-value block per item (the same slab halves as Q8_0).
@@ -150,6 +188,9 @@ template <> struct WLoad<T_MXFP4> {
         k = k < K ? k : 0;
         qs = *(const u32x4 *)(W + row * (K / 2) + k / 2);
         e = W[rows * (K / 2) + row * (K / 32) + k / 32];
+    }
+    __device__ __forceinline__ void decode_fast(int u, u32x4 out[4], int & run0, int & run1) const {
+        decode(u, out, run0, run1);
     }
     __device__ __forceinline__ void decode(int u, u32x4 out[4], int & run0, int & run1) const {
         // 2^(e-128) from its bits: a subnormal for e < 2
@@ -190,6 +231,9 @@ template <> struct WLoad<T_Q4_0> {
         k = k < K ? k : 0;
         qs = *(const u32x4 *)(W + row * (K / 2) + k / 2);
         d = *((const uint16_t *)(W + rows * (K / 2)) + row * (K / 32) + k / 32);
+    }
+    __device__ __forceinline__ void decode_fast(int u, u32x4 out[4], int & run0, int & run1) const {
+        decode(u, out, run0, run1);
     }
     __device__ __forceinline__ void decode(int u, u32x4 out[4], int & run0, int & run1) const {
         const float df = h2f_bits(d);
@@ -237,6 +281,9 @@ template <> struct WLoad<T_Q5_K> {
     // Byte b of qs is q[32j + 16u + b]: its low nibble is weight 64j + 16u + b (sub-block 2j)
     // with fifth bit 2j of qh byte b, its high nibble weight 64j + 32 + 16u + b (sub-block
     // 2j+1) with bit 2j+1.
+    __device__ __forceinline__ void decode_fast(int u, u32x4 out[4], int & run0, int & run1) const {
+        decode(u, out, run0, run1);
+    }
     __device__ __forceinline__ void decode(int u, u32x4 out[4], int & run0, int & run1) const {
         const float d = h2f_bits((uint16_t)(hdr[0] & 0xFFFFu));
         const float dmin = h2f_bits((uint16_t)(hdr[0] >> 16));
@@ -329,6 +376,34 @@ template <> struct WLoad<T_Q4_K> {
         run0 = 16 * u;
         run1 = 32 + 16 * u;
     }
+    // packed: (1024 + q - 1024) * fp16(d*sc) + fp16(-dmin*m)
+    __device__ __forceinline__ void decode_fast(int u, u32x4 out[4], int & run0, int & run1) const {
+        const float d = h2f_bits((uint16_t)(hdr[0] & 0xFFFFu));
+        const float dmin = h2f_bits((uint16_t)(hdr[0] >> 16));
+        int s0, m0, s1, m1;
+        q4k_sm(2 * j, hdr[1], hdr[2], hdr[3], s0, m0);
+        q4k_sm(2 * j + 1, hdr[1], hdr[2], hdr[3], s1, m1);
+        // a masked item decodes to zero through zero scales
+        const float z = ok ? 1.0f : 0.0f;
+        const half2v S0 = splat_h(z * (d * (float)s0)), B0 = splat_h(z * -(dmin * (float)m0));
+        const half2v S1 = splat_h(z * (d * (float)s1)), B1 = splat_h(z * -(dmin * (float)m1));
+        const half2v OFF = {(_Float16)-1024.0f, (_Float16)-1024.0f};
+        uint32_t lo[8], hi[8];
+#pragma unroll
+        for (int w = 0; w < 4; w++) {
+            const uint32_t l4 = qs[w] & 0x0F0F0F0Fu, h4 = (qs[w] >> 4) & 0x0F0F0F0Fu;
+            lo[2 * w] = u_of((magic_pair(l4, PERM_B01) + OFF) * S0 + B0);
+            lo[2 * w + 1] = u_of((magic_pair(l4, PERM_B23) + OFF) * S0 + B0);
+            hi[2 * w] = u_of((magic_pair(h4, PERM_B01) + OFF) * S1 + B1);
+            hi[2 * w + 1] = u_of((magic_pair(h4, PERM_B23) + OFF) * S1 + B1);
+        }
+        out[0] = u32x4{lo[0], lo[1], lo[2], lo[3]};
+        out[1] = u32x4{lo[4], lo[5], lo[6], lo[7]};
+        out[2] = u32x4{hi[0], hi[1], hi[2], hi[3]};
+        out[3] = u32x4{hi[4], hi[5], hi[6], hi[7]};
+        run0 = 16 * u;
+        run1 = 32 + 16 * u;
+    }
 };
 
 template <> struct WLoad<T_Q6_K> {
@@ -356,6 +431,9 @@ template <> struct WLoad<T_Q6_K> {
         const int i0 = u + 4 * hi;
         sc = (uint32_t)(uint8_t)scp[i0] | ((uint32_t)(uint8_t)scp[i0 + 2] << 8);
         d = *dp;
+    }
+    __device__ __forceinline__ void decode_fast(int u, u32x4 out[4], int & run0, int & run1) const {
+        decode(u, out, run0, run1);
     }
     __device__ __forceinline__ void decode(int u, u32x4 out[4], int & run0, int & run1) const {
         const float df = h2f_bits(d);

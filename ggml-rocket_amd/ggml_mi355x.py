@@ -87,8 +87,13 @@ def lib():
     L.mi355x_pack_act.argtypes = [vp, i64, i64, i64, vp, vp, vp]
     L.mi355x_pack_act_tiled.argtypes = [vp, i64, i64, i64, vp, vp, vp]
     L.mi355x_gemm.argtypes = [i32, vp, vp, i64, i64, ctypes.POINTER(GemmOut), i32, vp]
+    L.mi355x_gemm_workspace.restype = sz
+    L.mi355x_gemm_workspace.argtypes = [i32, i64, i64, ctypes.POINTER(GemmOut), i32]
+    L.mi355x_gemm_ws.argtypes = [i32, vp, vp, i64, i64, ctypes.POINTER(GemmOut), i32, vp, sz, vp]
     L.mi355x_mul_mat_workspace.restype = sz
     L.mi355x_mul_mat_workspace.argtypes = [i64, i64]
+    L.mi355x_mul_mat_workspace_for.restype = sz
+    L.mi355x_mul_mat_workspace_for.argtypes = [i32, i64, i64, i64]
     L.mi355x_mul_mat.argtypes = [i32, vp, i64, i64, vp, i64, i64, vp, i64, vp, sz, vp]
     _bind_optional(L)
     _lib = L
@@ -201,13 +206,21 @@ def pack_act(x, tiled: bool = False):
     return a16, sc
 
 
-def gemm(wtype: int, a16, scales, K: int, outs):
-    """outs: list of (w_dev, rows_total, row0, N, c_tensor). M = len(scales)."""
+def gemm(wtype: int, a16, scales, K: int, outs, split_workspace: bool = True):
+    """outs: list of (w_dev, rows_total, row0, N, c_tensor). M = len(scales). With
+    split_workspace, mi355x_gemm_ws with the workspace its fastest K split asks for; without,
+    mi355x_gemm (K split at most two ways)."""
     arr = (GemmOut * len(outs))()
     for i, (w, rows_total, row0, N, c) in enumerate(outs):
         arr[i] = GemmOut(w.data_ptr(), rows_total, row0, N, c.data_ptr(), c.stride(0))
     M = scales.shape[0]
-    check(lib().mi355x_gemm(wtype, _ptr(a16), _ptr(scales), M, K, arr, len(outs), stream_handle()), "gemm")
+    if not split_workspace:
+        check(lib().mi355x_gemm(wtype, _ptr(a16), _ptr(scales), M, K, arr, len(outs), stream_handle()), "gemm")
+        return
+    need = int(lib().mi355x_gemm_workspace(wtype, M, K, arr, len(outs)))
+    ws = _torch().empty(max(need, 1), dtype=_torch().uint8, device=a16.device)
+    check(lib().mi355x_gemm_ws(wtype, _ptr(a16), _ptr(scales), M, K, arr, len(outs), _ptr(ws), need,
+                               stream_handle()), "gemm_ws")
 
 
 def mul_mat(wtype: int, w_dev, N: int, K: int, x, out=None, workspace=None):
@@ -216,7 +229,7 @@ def mul_mat(wtype: int, w_dev, N: int, K: int, x, out=None, workspace=None):
     M = x.shape[0]
     if out is None:
         out = torch.empty((M, N), dtype=torch.float32, device=x.device)
-    need = int(lib().mi355x_mul_mat_workspace(M, K))
+    need = int(lib().mi355x_mul_mat_workspace_for(wtype, N, K, M))
     if workspace is None or workspace.numel() < need:
         workspace = torch.empty(max(need, 1), dtype=torch.uint8, device=x.device)
     check(lib().mi355x_mul_mat(wtype, _ptr(w_dev), N, K, _ptr(x), x.stride(0), M, _ptr(out), out.stride(0),

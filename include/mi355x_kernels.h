@@ -125,16 +125,42 @@ typedef struct mi355x_gemm_out {
  * MI355X_F16_T weights a16 is tiled too (mi355x_pack_act_tiled).
  * Replaces rocket_matmul_fp16_prepacked (ggml-rocket.cpp:4449, 5144),
  * rocket_matmul_fp16_stream (4834), rocket_matmul_fp16_mt (4844) and the fused
- * rocket_matmul_fp16_stream_fused (5004). */
+ * rocket_matmul_fp16_stream_fused (5004).
+ * Results are reproducible: equal inputs give equal bits on every call. A launch may split K
+ * over blocks; this entry has no workspace, so it splits at most two ways, adding both parts
+ * into the zeroed output (two addends on zero sum the same in either order). Wider splits, the
+ * fast form for M <= 128 and for deep K, need mi355x_gemm_ws. */
 MI355X_API int mi355x_gemm(int wtype, const uint16_t * a16_dev, const float * scales_dev,
                            int64_t M, int64_t K, const mi355x_gemm_out * outs, int n_out,
                            void * stream);
 
-/* Workspace bytes mi355x_mul_mat needs for M rows of K. */
+/* Bytes of device workspace with which mi355x_gemm_ws runs this launch's fastest K split: one
+ * F32 slab [M][sum of the outputs' N] per split when it splits more than two ways, else 0 (0 also
+ * for invalid arguments; the pointers in `outs` are not read). */
+MI355X_API size_t mi355x_gemm_workspace(int wtype, int64_t M, int64_t K, const mi355x_gemm_out * outs, int n_out);
+
+/* mi355x_gemm with a workspace (16-byte aligned) for the partial sums of a K split past two ways.
+ * Each split writes its slab; a second launch sums the slabs in split order into the outputs,
+ * so the result does not depend on the order in which blocks finish (reproducible, as the CPU
+ * backend's MUL_MAT is). With fewer bytes than mi355x_gemm_workspace asks, the split narrows to
+ * what fits (down to two ways). The same bytes give the same bits on every call; a different
+ * workspace size may pick a different split and round differently. */
+MI355X_API int mi355x_gemm_ws(int wtype, const uint16_t * a16_dev, const float * scales_dev,
+                              int64_t M, int64_t K, const mi355x_gemm_out * outs, int n_out,
+                              void * workspace_dev, size_t workspace_bytes, void * stream);
+
+/* Workspace bytes mi355x_mul_mat needs for M rows of K: the activation pack. */
 MI355X_API size_t mi355x_mul_mat_workspace(int64_t M, int64_t K);
 
+/* Workspace bytes with which mi355x_mul_mat runs its fastest K split for this shape: the pack,
+ * then (from the next 256-byte boundary) the split partials mi355x_gemm_workspace names. */
+MI355X_API size_t mi355x_mul_mat_workspace_for(int wtype, int64_t N, int64_t K, int64_t M);
+
 /* dst[M][ldd] = x[M][ldx] . w[N][K]^T: mi355x_pack_act (mi355x_pack_act_tiled for MI355X_F16_T)
- * then mi355x_gemm, the activation pack in `workspace_dev`. The whole MUL_MAT of ggml-rocket.cpp:4548-4871 on device. */
+ * then mi355x_gemm_ws, the activation pack at the start of `workspace_dev` and the K-split
+ * partials in the bytes past it (mi355x_mul_mat_workspace_for sizes both; with only
+ * mi355x_mul_mat_workspace bytes the split is at most two ways). Reproducible as mi355x_gemm_ws.
+ * The whole MUL_MAT of ggml-rocket.cpp:4548-4871 on device. */
 MI355X_API int mi355x_mul_mat(int wtype, const void * w_dev, int64_t N, int64_t K,
                               const float * x_dev, int64_t ldx, int64_t M,
                               float * dst_dev, int64_t ldd,
@@ -152,7 +178,8 @@ MI355X_API int mi355x_mul_mat(int wtype, const void * w_dev, int64_t N, int64_t 
  * that GPU's array: calls that overlap on one GPU (two streams, two threads) race and must be
  * serialized by the caller. The first call on a device resolves the array's address there
  * (make it outside a stream capture); later calls may be captured. Same results as
- * mi355x_mul_mat. */
+ * mi355x_mul_mat given MI355X_NOALLOC_SCRATCH_BYTES of workspace (K-split partials use the
+ * scratch past the pack). */
 MI355X_API int mi355x_mul_mat_noalloc(int wtype, const void * w_dev, int64_t N, int64_t K,
                                       const float * x_dev, int64_t ldx, int64_t M,
                                       float * dst_dev, int64_t ldd, void * stream);

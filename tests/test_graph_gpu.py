@@ -42,7 +42,7 @@ def test_graph_skinny_mul_mat_k_split(mx):
     w = mx.upload_weight(O.Q4_K, O.quantize(O.Q4_K, W), N, K)
     x = torch.empty((M, K), dtype=torch.float32, device="cuda")
     out = torch.empty((M, N), dtype=torch.float32, device="cuda")
-    ws = torch.empty(int(mx.lib().mi355x_mul_mat_workspace(M, K)), dtype=torch.uint8, device="cuda")
+    ws = torch.empty(int(mx.lib().mi355x_mul_mat_workspace_for(O.Q4_K, N, K, M)), dtype=torch.uint8, device="cuda")
     inputs = [torch.from_numpy(O.fill_normal((M, K), 1201 + i)).cuda() for i in range(3)]
     refs = []
     for X in inputs:
@@ -60,8 +60,8 @@ def test_graph_skinny_mul_mat_k_split(mx):
             got = out.cpu().numpy()
             want = ref.cpu().numpy()
             assert np.isfinite(got).all(), (rep, i)
-            # the K split adds atomically: the order of the addends may differ between runs
-            np.testing.assert_allclose(got, want, rtol=1e-5, atol=1e-5 * np.abs(want).max())
+            # the K-split partials are summed in split order: every replay gives the eager bits
+            assert np.array_equal(got, want), (rep, i)
 
 
 def test_graph_flash_attn_kv_split(mx):
