@@ -128,7 +128,9 @@ __global__ void __launch_bounds__(MOE_SORT_THREADS) moe_sort_kernel(MoeArgs a) {
 // are one even round over 256 CUs, where 256-column blocks left half the CUs with double work.
 // Two register stages for every type: one block per CU (one wave per SIMD) with 4 stages of
 // Q4_K lookahead ran at the same speed as with 2, so the slabs are not waiting on memory.
-template <int WT> constexpr int moe_stages() { return 2; }
+// Register stages of slab lookahead: four where they fit in the three-wave register budget
+// without spilling, three for the formats whose stage is wider (F16, Q6_K).
+template <int WT> constexpr int moe_stages() { return (WT == T_F16 || WT == T_Q6_K) ? 3 : 4; }
 
 template <int WT>
 __global__ void __launch_bounds__(MOE_THREADS) __attribute__((amdgpu_waves_per_eu(3, 3)))
@@ -188,27 +190,32 @@ moe_gemm_kernel(MoeArgs a) {
 
     struct Stage {
         u32x4 a0, a1;
+        bool ok0, ok1;   // activation chunk real (else stored as zero)
         WLoad<WT> w;
     };
-    auto load_a = [&](int arow, int64_t k0) -> u32x4 {
+    // Pad rows and k past K load from a valid address and are zeroed at the LDS store: a branch
+    // around the load, or a select right after it, would make the compiler wait for the newest
+    // loads at the join and cut the register stages' lookahead to one.
+    auto load_a = [&](int arow, int64_t k0, bool & ok) -> u32x4 {
         const int64_t k = k0 + 8 * ac;
-        if (arow < 0 || k >= K) return u32x4{0, 0, 0, 0};
-        return *(const u32x4 *)(a.a16 + (int64_t)arow * K + k);
+        ok = arow >= 0 && k < K;
+        return *(const u32x4 *)(a.a16 + (ok ? (int64_t)arow * K + k : 0));
     };
     const int nk = (K + MOE_BK - 1) / MOE_BK;
     auto load = [&](Stage & g, int kt) {
         const int64_t k0 = (int64_t)min(kt, nk - 1) * MOE_BK;   // past the end: a repeat nobody uses
-        g.a0 = load_a(arow0, k0);
-        g.a1 = load_a(arow1, k0);
+        g.a0 = load_a(arow0, k0, g.ok0);
+        g.a1 = load_a(arow1, k0, g.ok1);
         g.w.load(W, rows_total, K, wrow, k0, wu, wok);
     };
     auto store = [&](uint8_t * st, const Stage & g) {
-        *(u32x4 *)(st + swz<8>(ar, ac)) = g.a0;
-        *(u32x4 *)(st + swz<8>(ar + 32, ac)) = g.a1;
+        const u32x4 z = {0, 0, 0, 0};
+        *(u32x4 *)(st + swz<8>(ar, ac)) = g.ok0 ? g.a0 : z;
+        *(u32x4 *)(st + swz<8>(ar + 32, ac)) = g.ok1 ? g.a1 : z;
         uint8_t * bs = st + MOE_A_BYTES;
         u32x4 o[4];
         int r0, r1;
-        g.w.decode(wu, o, r0, r1);
+        g.w.decode_fast(wu, o, r0, r1);
         *(u32x4 *)(bs + swz<8>(wr, r0 / 8)) = o[0];
         *(u32x4 *)(bs + swz<8>(wr, r0 / 8 + 1)) = o[1];
         *(u32x4 *)(bs + swz<8>(wr, r1 / 8)) = o[2];
