@@ -121,7 +121,7 @@ struct DevBuf {
 // as long as starting a thread.
 class CopyPool {
 public:
-    explicit CopyPool(int n) {
+    explicit CopyPool(int n, size_t min_part) : min_part_(min_part) {
         for (int i = 1; i < n; i++) th_.emplace_back([this] { work(); });
     }
     ~CopyPool() {
@@ -154,8 +154,7 @@ public:
         job_ = nullptr;
     }
     void copy(void * dst, const void * src, size_t n) {
-        const size_t MIN_PART = (size_t)1 << 20;
-        const int parts = (int)std::min<size_t>((size_t)threads(), (n + MIN_PART - 1) / MIN_PART);
+        const int parts = (int)std::min<size_t>((size_t)threads(), (n + min_part_ - 1) / min_part_);
         const size_t per = ((n + parts - 1) / parts + 63) & ~(size_t)63;
         run(parts, [&](int i) {
             const size_t o = (size_t)i * per;
@@ -185,6 +184,7 @@ private:
             drain();
         }
     }
+    const size_t min_part_;   // smallest part one worker copies
     std::vector<std::thread> th_;
     std::mutex mu_;
     std::condition_variable cv_, done_;
@@ -199,16 +199,29 @@ private:
 // (ggml's CPU buffers), and a copy from pageable memory crawls through the runtime's own small
 // bounce buffer. A large copy is cut into CHUNK-sized pieces that cycle through NSLOT pinned
 // slots: the copy workers fill (or drain) one slot while the DMA engine moves another. Slots are
-// reused only after the event of their last DMA has completed.
+// reused only after the event of their last DMA has completed, and the ring continues from one
+// copy to the next. Measured on the 8B-shape layer's transfers (8-60 MB operands): chunks of 2 to
+// 16 MB and 4 to 8 slots perform alike (within 5%); below 2 MB, or with copy parts under 512 KB,
+// the per-chunk wake-ups of the copy workers and event waits cost more than the overlap gains.
 struct Stager {
-    static constexpr size_t CHUNK = (size_t)8 << 20;
-    static constexpr int NSLOT = 3;
-    void * slot[NSLOT] = {};
-    hipEvent_t ev[NSLOT] = {};
-    bool pending[NSLOT] = {};
+    static constexpr int MAX_SLOT = 16;
+    size_t CHUNK = (size_t)8 << 20;   // MI355X_STAGE_CHUNK_KB overrides (tuning)
+    int NSLOT = 4;                    // MI355X_STAGE_SLOTS overrides (tuning), <= MAX_SLOT
+    void * slot[MAX_SLOT] = {};
+    hipEvent_t ev[MAX_SLOT] = {};
+    bool pending[MAX_SLOT] = {};
+    int next = 0;    // the slot the next chunk of an upload takes
     bool ready = false;
     int init() {
         if (ready) return MI355X_OK;
+        if (const char * e = getenv("MI355X_STAGE_CHUNK_KB")) {
+            const long v = atol(e);
+            if (v >= 64 && v <= (64 << 10)) CHUNK = (size_t)v << 10;
+        }
+        if (const char * e = getenv("MI355X_STAGE_SLOTS")) {
+            const int v = atoi(e);
+            if (v >= 2 && v <= MAX_SLOT) NSLOT = v;
+        }
         for (int i = 0; i < NSLOT; i++) {
             if (hipHostMalloc(&slot[i], CHUNK, hipHostMallocDefault) != hipSuccess ||
                 hipEventCreateWithFlags(&ev[i], hipEventDisableTiming) != hipSuccess) {
@@ -227,7 +240,7 @@ struct Stager {
         return hipEventSynchronize(ev[i]) == hipSuccess ? MI355X_OK : MI355X_E_DEVICE;
     }
     void release() {
-        for (int i = 0; i < NSLOT; i++) {
+        for (int i = 0; i < MAX_SLOT; i++) {
             if (pending[i] && ev[i]) (void)hipEventSynchronize(ev[i]);
             if (ev[i]) (void)hipEventDestroy(ev[i]);
             if (slot[i]) (void)hipHostFree(slot[i]);
@@ -267,6 +280,17 @@ struct mi355x_backend {
     uint64_t guid[2] = {GUID[0], GUID[1]};
     int n_threads = 5;
     bool started = false;
+    // The device copy of a FLASH_ATTN_EXT dst written back in this graph_compute call (the fa_o
+    // buffer): a MUL_MAT later in the call whose src1 is exactly those host bytes (O reading the
+    // attention through a view) reads them from here instead of uploading them again. Cleared
+    // at the start of each call and at each FLASH_ATTN_EXT; not used in a call where another
+    // node's dst overlaps an attention's dst (mirror_ok).
+    bool mirror_ok = false;
+    struct {
+        const void * host = nullptr;
+        size_t bytes = 0;
+        const void * dev = nullptr;
+    } fa_mirror;
     int quant_resident = -1;   // -1: the QUANT_RESIDENT knob; 0 / 1: this instance's choice
 
     bool dev_checked = false, dev_ok = false;
@@ -331,7 +355,14 @@ int sync(Ctx * c) {
 constexpr size_t STAGE_MIN = (size_t)1 << 20;
 
 bool staging_on(Ctx * c) {
-    if (!c->pool) c->pool.reset(new CopyPool(c->n_threads));
+    if (!c->pool) {
+        size_t part = (size_t)1 << 20;   // MI355X_COPY_PART_KB overrides (tuning)
+        if (const char * e = getenv("MI355X_COPY_PART_KB")) {
+            const long v = atol(e);
+            if (v >= 16 && v <= (64 << 10)) part = (size_t)v << 10;
+        }
+        c->pool.reset(new CopyPool(c->n_threads, part));
+    }
     return c->stage.init() == MI355X_OK;
 }
 
@@ -342,9 +373,10 @@ int h2d(Ctx * c, void * dst, const void * src, size_t n) {
         return hipMemcpyAsync(dst, src, n, hipMemcpyHostToDevice, c->stream) == hipSuccess ? MI355X_OK
                                                                                           : MI355X_E_DEVICE;
     Stager & S = c->stage;
-    for (size_t o = 0, i = 0; o < n; o += Stager::CHUNK, i++) {
-        const int k = (int)(i % Stager::NSLOT);
-        const size_t len = std::min(Stager::CHUNK, n - o);
+    for (size_t o = 0; o < n; o += S.CHUNK) {
+        const int k = S.next;
+        S.next = (S.next + 1) % S.NSLOT;
+        const size_t len = std::min(S.CHUNK, n - o);
         TRY_RC(S.settle(k));
         c->pool->copy(S.slot[k], (const char *)src + o, len);
         if (hipMemcpyAsync((char *)dst + o, S.slot[k], len, hipMemcpyHostToDevice, c->stream) != hipSuccess ||
@@ -361,10 +393,10 @@ int h2d(Ctx * c, void * dst, const void * src, size_t n) {
 int d2h_rows(Ctx * c, const void * src, size_t pitch, size_t width, int64_t rows,
              const std::function<void(int64_t, int64_t, const char *)> & take) {
     Stager & S = c->stage;
-    const int64_t per = std::max<int64_t>(1, (int64_t)(Stager::CHUNK / width));
+    const int64_t per = std::max<int64_t>(1, (int64_t)(S.CHUNK / width));
     const int64_t nchunk = (rows + per - 1) / per;
     auto launch = [&](int64_t i) -> int {
-        const int k = (int)(i % Stager::NSLOT);
+        const int k = (int)(i % S.NSLOT);
         const int64_t r0 = i * per, r1 = std::min(rows, r0 + per);
         const hipError_t e = pitch == width
             ? hipMemcpyAsync(S.slot[k], (const char *)src + r0 * pitch, (size_t)(r1 - r0) * width,
@@ -375,13 +407,13 @@ int d2h_rows(Ctx * c, const void * src, size_t pitch, size_t width, int64_t rows
         S.pending[k] = true;
         return MI355X_OK;
     };
-    for (int64_t i = 0; i < std::min<int64_t>(nchunk, Stager::NSLOT); i++) TRY_RC(launch(i));
+    for (int64_t i = 0; i < std::min<int64_t>(nchunk, S.NSLOT); i++) TRY_RC(launch(i));
     for (int64_t i = 0; i < nchunk; i++) {
-        const int k = (int)(i % Stager::NSLOT);
+        const int k = (int)(i % S.NSLOT);
         TRY_RC(S.settle(k));
         const int64_t r0 = i * per, r1 = std::min(rows, r0 + per);
         take(r0, r1, (const char *)S.slot[k]);
-        if (i + Stager::NSLOT < nchunk) TRY_RC(launch(i + Stager::NSLOT));
+        if (i + S.NSLOT < nchunk) TRY_RC(launch(i + S.NSLOT));
     }
     return MI355X_OK;
 }
@@ -561,12 +593,19 @@ int mul_mat_device(Ctx * c, const std::vector<mi355x_tensor *> & grp, bool want_
         outs[i].ldc = ntot;
         col += a->ne[1];
     }
-    TRY(h2d(c, c->act.p, b->data, (size_t)M * K * 4));
-    if (ws[0].dev_type == MI355X_F16_T)
-        TRY(mi355x_pack_act_tiled((const float *)c->act.p, K, M, K, (uint16_t *)c->a16.p, (float *)c->scales.p,
-                                  c->stream));
+    // src1 from the attention this call just computed (same host bytes, row-major F32): its
+    // device copy; otherwise uploaded
+    const float * act = (const float *)c->act.p;
+    const bool dense = b->type == MI355X_TYPE_F32 && b->nb[0] == 4 && b->nb[1] == (size_t)K * 4 &&
+                       b->nb[2] == b->nb[1] * (size_t)b->ne[1] && b->nb[3] == b->nb[2] * (size_t)b->ne[2];
+    if (dense && c->fa_mirror.dev && b->data == c->fa_mirror.host && (size_t)M * K * 4 <= c->fa_mirror.bytes)
+        act = (const float *)c->fa_mirror.dev;
     else
-        TRY(mi355x_pack_act((const float *)c->act.p, K, M, K, (uint16_t *)c->a16.p, (float *)c->scales.p, c->stream));
+        TRY(h2d(c, c->act.p, b->data, (size_t)M * K * 4));
+    if (ws[0].dev_type == MI355X_F16_T)
+        TRY(mi355x_pack_act_tiled(act, K, M, K, (uint16_t *)c->a16.p, (float *)c->scales.p, c->stream));
+    else
+        TRY(mi355x_pack_act(act, K, M, K, (uint16_t *)c->a16.p, (float *)c->scales.p, c->stream));
     // K-split partials, summed in a fixed order (reproducible results)
     const size_t pbytes = mi355x_gemm_workspace(ws[0].dev_type, M, K, outs, (int)grp.size());
     if (pbytes) TRY(c->part.ensure(pbytes));
@@ -579,7 +618,7 @@ int mul_mat_device(Ctx * c, const std::vector<mi355x_tensor *> & grp, bool want_
         TRY(d2h(c, grp[0]->data, c->out.p, (size_t)M * ntot * 4));
         return sync(c);
     }
-    if ((size_t)M * ntot * 4 < STAGE_MIN || (size_t)ntot * 4 > Stager::CHUNK || !staging_on(c)) {
+    if ((size_t)M * ntot * 4 < STAGE_MIN || !staging_on(c) || (size_t)ntot * 4 > c->stage.CHUNK) {
         col = 0;
         for (auto * d : grp) {
             const int64_t N = d->src[0]->ne[1];
@@ -654,7 +693,13 @@ int flash_attn_device(Ctx * c, mi355x_tensor * dst) {
     if (ws) TRY(c->fa_ws.ensure(ws));
     TRY(mi355x_flash_attn(&a, 0, ws ? c->fa_ws.p : nullptr, ws, c->stream));
     TRY(d2h(c, dst->data, c->fa_o.p, ob));
-    return sync(c);
+    TRY(sync(c));
+    if (c->mirror_ok) {
+        c->fa_mirror.host = dst->data;
+        c->fa_mirror.bytes = ob;
+        c->fa_mirror.dev = c->fa_o.p;
+    }
+    return MI355X_OK;
 }
 
 // ---- MUL_MAT_ID -------------------------------------------------------------------------------
@@ -940,6 +985,25 @@ MI355X_API int mi355x_backend_graph_compute(mi355x_backend_t c, mi355x_tensor * 
 
 static int graph_compute_nodes(mi355x_backend_t c, mi355x_tensor * const * nodes, int n_nodes) {
     c->started = true;
+    c->fa_mirror = {};
+    // the attention's device copy may stand in for its host bytes only if no other node of the
+    // call writes over them
+    c->mirror_ok = true;
+    for (int i = 0; i < n_nodes && c->mirror_ok; i++) {
+        const mi355x_tensor * f = nodes[i];
+        if (!f || f->op != MI355X_OP_FLASH_ATTN_EXT || !f->data) continue;
+        const char * h = (const char *)f->data;
+        const size_t hb = nbytes(f);
+        for (int j = 0; j < n_nodes; j++) {
+            const mi355x_tensor * o = nodes[j];
+            if (!o || j == i || is_view_op(o->op) || o->op == MI355X_OP_NONE || !o->data) continue;
+            const char * d = (const char *)o->data;
+            if (d < h + hb && h < d + nbytes(o)) {
+                c->mirror_ok = false;
+                break;
+            }
+        }
+    }
     std::vector<bool> done((size_t)(n_nodes > 0 ? n_nodes : 0), false);
     for (int i = 0; i < n_nodes; i++) {
         if (done[i]) continue;
@@ -976,6 +1040,7 @@ static int graph_compute_nodes(mi355x_backend_t c, mi355x_tensor * const * nodes
                 break;
             }
             case MI355X_OP_FLASH_ATTN_EXT: {
+                c->fa_mirror = {};
                 guarded(c, c->brk_fa, "FLASH_ATTN_EXT", [&] { return flash_attn_device(c, node); },
                         [&] { cpu_flash_attn(node); });
                 c->routes["fa"]++;
