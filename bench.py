@@ -120,6 +120,9 @@ def parse():
     p.add_argument("--host-path", action="store_true",
                    help="run the prefill through graph_compute with host tensors (the plugin "
                         "boundary, PCIe-inclusive) and print that rate instead")
+    p.add_argument("--gguf", default=None,
+                   help="with --host-path: take the model (dims, tensor names, weight bytes) from this "
+                        "llama GGUF, memory-mapped (e.g. one written by ggml-rocket_amd/llama3_gguf.py)")
     p.add_argument("--configs", action="store_true",
                    help="time the single-op configurations (F16 MUL_MAT 8192x2048 at M 512; Q8_0 / Q4_K / "
                         "Q6_K MUL_MAT at K,N in {3072x3072, 3072x8192, 8192x3072}, M in {32, 128, 512, "
@@ -453,38 +456,68 @@ def host_path(args):
     {Q, K, V} (fused), {FLASH_ATTN_EXT, O}, {gate, up} (fused), {down}. Weights are per-layer Q4_K
     payloads in host memory with their own names, so the first pass builds the HBM weight cache
     (decoded, tiled fp16: the QUANT_RESIDENT route) and the second, timed, pass finds every
-    weight resident. Prints one JSON line with the PCIe-inclusive rate."""
+    weight resident. Prints one JSON line with the PCIe-inclusive rate.
+
+    With --gguf PATH the model comes from a GGUF file instead (llama.cpp's tensor names, e.g. the
+    random-init Llama-3-8B of llama3_gguf.py): its dims from the file's llama.* metadata, its
+    weights passed to the backend as views of the memory-mapped file under their GGUF names, as a
+    host's ggml hands a mapped model's tensors over."""
     import ctypes
     import numpy as np
     import ggml_mi355x as mx
     be = mx.Backend()
     be.set_quant_resident(1)
-    L, T = args.layers, UBATCH
-    shapes = {"q": (D_MODEL, D_MODEL), "k": (NKV * HD, D_MODEL), "v": (NKV * HD, D_MODEL),
-              "o": (D_MODEL, D_MODEL), "gate": (FFN, D_MODEL), "up": (FFN, D_MODEL), "down": (D_MODEL, FFN)}
-    rng = np.random.default_rng(1234)
+    T = UBATCH
     t0 = time.time()
-    base = {}
-    for i, (name, (N, K)) in enumerate(shapes.items()):
-        base[name] = synth_q4k(N, K, 0x5EED0000 + 80 + i)
     wg = mx.Graph()
     wts = []
-    for li in range(L):
-        lw = {}
-        for name, (N, K) in shapes.items():
-            q = base[name].copy()
-            if li > 0:   # fresh nibbles under layer 0's block headers: valid Q4_K, distinct per layer
-                q.reshape(-1, 144)[:, 16:] = rng.integers(0, 256, (q.size // 144, 128), dtype=np.uint8)
-            lw[name] = wg._new(mx.Q4_K, [K, N], name=f"blk.{li}.{name}.weight", data=q)
-        wts.append(lw)
+    gguf = getattr(args, "gguf", None)
+    if gguf:
+        import gguf_io
+        r = gguf_io.Reader(gguf)
+        kv = r.kv
+        if kv.get("general.architecture") != "llama":
+            raise SystemExit(f"{gguf}: architecture {kv.get('general.architecture')!r}, not llama")
+        d_model, ffn = int(kv["llama.embedding_length"]), int(kv["llama.feed_forward_length"])
+        nh, nkv = int(kv["llama.attention.head_count"]), int(kv["llama.attention.head_count_kv"])
+        hd = d_model // nh
+        L = min(args.layers, int(kv["llama.block_count"]))
+        gname = {"q": "attn_q", "k": "attn_k", "v": "attn_v", "o": "attn_output", "gate": "ffn_gate",
+                 "up": "ffn_up", "down": "ffn_down"}
+        shapes = {}
+        for li in range(L):
+            lw = {}
+            for name, g in gname.items():
+                tn = f"blk.{li}.{g}.weight"
+                t, ne, _, _ = r.tensors[tn]
+                shapes[name] = (int(ne[1]), int(ne[0]))
+                lw[name] = wg._new(t, [int(ne[0]), int(ne[1])], name=tn, data=r.data(tn))
+            wts.append(lw)
+    else:
+        d_model, ffn, nh, nkv, hd, L = D_MODEL, FFN, NH, NKV, HD, args.layers
+        shapes = {"q": (d_model, d_model), "k": (nkv * hd, d_model), "v": (nkv * hd, d_model),
+                  "o": (d_model, d_model), "gate": (ffn, d_model), "up": (ffn, d_model), "down": (d_model, ffn)}
+        rng = np.random.default_rng(1234)
+        base = {}
+        for i, (name, (N, K)) in enumerate(shapes.items()):
+            base[name] = synth_q4k(N, K, 0x5EED0000 + 80 + i)
+        for li in range(L):
+            lw = {}
+            for name, (N, K) in shapes.items():
+                q = base[name].copy()
+                if li > 0:   # fresh nibbles under layer 0's block headers: valid Q4_K, distinct per layer
+                    q.reshape(-1, 144)[:, 16:] = rng.integers(0, 256, (q.size // 144, 128), dtype=np.uint8)
+                lw[name] = wg._new(mx.Q4_K, [K, N], name=f"blk.{li}.{name}.weight", data=q)
+            wts.append(lw)
+    rng = np.random.default_rng(1234)
     setup_s = time.time() - t0
 
     g = mx.Graph()
     f32 = lambda *n: np.zeros(int(np.prod(n)), dtype=np.float32)
-    x = g._new(mx.F32, [D_MODEL, T], data=rng.standard_normal(D_MODEL * T).astype(np.float32))
-    act = g._new(mx.F32, [FFN, T], data=rng.standard_normal(FFN * T).astype(np.float32))
-    kc = g._new(mx.F16, [HD, NKV, TOKENS], data=rng.standard_normal(HD * NKV * TOKENS).astype(np.float16))
-    vc = g._new(mx.F16, [HD, NKV, TOKENS], data=rng.standard_normal(HD * NKV * TOKENS).astype(np.float16))
+    x = g._new(mx.F32, [d_model, T], data=rng.standard_normal(d_model * T).astype(np.float32))
+    act = g._new(mx.F32, [ffn, T], data=rng.standard_normal(ffn * T).astype(np.float32))
+    kc = g._new(mx.F16, [hd, nkv, TOKENS], data=rng.standard_normal(hd * nkv * TOKENS).astype(np.float16))
+    vc = g._new(mx.F16, [hd, nkv, TOKENS], data=rng.standard_normal(hd * nkv * TOKENS).astype(np.float16))
     masks = []
     for u in range(TOKENS // T):
         n_kv = T * (u + 1)
@@ -492,8 +525,8 @@ def host_path(args):
         m[np.arange(n_kv)[None, :] > T * u + np.arange(T)[:, None]] = -np.inf
         masks.append(g._new(mx.F16, [n_kv, T], data=m.reshape(-1)))
     bufs = {n: f32(N, T) for n, (N, _) in shapes.items()}
-    bufs["attn"] = f32(HD, NH, T)
-    attn_cpu = g._new(mx.F32, [D_MODEL, T], data=rng.standard_normal(D_MODEL * T).astype(np.float32))
+    bufs["attn"] = f32(hd, nh, T)
+    attn_cpu = g._new(mx.F32, [d_model, T], data=rng.standard_normal(d_model * T).astype(np.float32))
 
     def groups(li, u):
         """The graph_compute calls of layer li, micro-batch u."""
@@ -502,12 +535,12 @@ def host_path(args):
         mm = lambda name, src: g._new(mx.F32, [shapes[name][0], T], op=mx.OP_MUL_MAT, srcs=(w[name], src),
                                       data=bufs[name])
         q, k, v = mm("q", x), mm("k", x), mm("v", x)
-        qv = g.permute_view(q, [HD, T, NH, 1], [4, D_MODEL * 4, HD * 4, D_MODEL * 4 * T])
-        kv = g.permute_view(kc, [HD, n_kv, NKV, 1], [2, NKV * HD * 2, HD * 2, NKV * HD * 2 * n_kv])
-        vv = g.permute_view(vc, [HD, n_kv, NKV, 1], [2, NKV * HD * 2, HD * 2, NKV * HD * 2 * n_kv])
-        fa = g._new(mx.F32, [HD, NH, T], op=mx.OP_FLASH_ATTN_EXT, srcs=(qv, kv, vv, masks[u]), data=bufs["attn"])
-        ctypes.memmove(ctypes.addressof(fa.op_params), (ctypes.c_float * 3)(1.0 / math.sqrt(HD), 0.0, 0.0), 12)
-        fa2d = g.permute_view(fa, [D_MODEL, T, 1, 1], [4, D_MODEL * 4, D_MODEL * 4 * T, D_MODEL * 4 * T])
+        qv = g.permute_view(q, [hd, T, nh, 1], [4, d_model * 4, hd * 4, d_model * 4 * T])
+        kv = g.permute_view(kc, [hd, n_kv, nkv, 1], [2, nkv * hd * 2, hd * 2, nkv * hd * 2 * n_kv])
+        vv = g.permute_view(vc, [hd, n_kv, nkv, 1], [2, nkv * hd * 2, hd * 2, nkv * hd * 2 * n_kv])
+        fa = g._new(mx.F32, [hd, nh, T], op=mx.OP_FLASH_ATTN_EXT, srcs=(qv, kv, vv, masks[u]), data=bufs["attn"])
+        ctypes.memmove(ctypes.addressof(fa.op_params), (ctypes.c_float * 3)(1.0 / math.sqrt(hd), 0.0, 0.0), 12)
+        fa2d = g.permute_view(fa, [d_model, T, 1, 1], [4, d_model * 4, d_model * 4 * T, d_model * 4 * T])
         # the attention is the backend's where it is claimed (n_kv >= FLASH_ATTN_MIN_KV); the
         # declined one is the host CPU's, and O then reads its result from host memory
         attn = [fa, fa2d, mm("o", fa2d)] if n_kv >= args.fa_min_kv else [mm("o", attn_cpu)]
@@ -532,10 +565,13 @@ def host_path(args):
     be.free()
     out = {"metric": "prefill tok/s through graph_compute (host buffers, PCIe-inclusive)",
            "value": round(TOKENS / sec, 1), "unit": "tok/s", "n_gpus": 1, "ms_per_prefill": round(sec * 1e3, 1),
-           "higher_is_better": True, "dtype": "f16", "data": "synthetic host tensors",
+           "higher_is_better": True, "dtype": "f16",
+           "data": (f"weights memory-mapped from {os.path.basename(gguf)}, synthetic activations" if gguf
+                    else "synthetic host tensors"),
            "config": {"workload": f"llama3-8b-shape Q4_K prefill, {TOKENS} tokens in {TOKENS // T} micro-batches "
                                   f"of {T}: {len(calls) // (TOKENS // T)} graph_compute calls per micro-batch",
-                      "layers": L, "route": "prepacked-q (QUANT_RESIDENT)"},
+                      "layers": L, "d_model": d_model, "ffn": ffn, "heads": nh, "kv_heads": nkv,
+                      "route": "prepacked-q (QUANT_RESIDENT)"},
            "first_pass_s": round(first_s, 2), "host_setup_s": round(setup_s, 1), "cpu_fallbacks": fb,
            "routes": routes,
            "scope": "the backend's ops only: FLASH_ATTN_EXT at n_kv < FLASH_ATTN_MIN_KV and every op "

@@ -857,6 +857,21 @@ void report_residency(const Ctx * c) {
     }
 }
 
+// The teardown line of the route counters (ops completed per route, CPU fallbacks), so a run
+// through a host that cannot call the counter API (llama-bench) still shows where ops ran.
+void report_routes(const Ctx * c) {
+    long total = 0;
+    std::string line;
+    for (const auto & kv : c->routes) {
+        if (!kv.second) continue;
+        total += kv.second;
+        line += " " + kv.first + "=" + std::to_string(kv.second);
+    }
+    if (total || c->n_cpu_fallbacks)
+        logi("[routes] %ld ops on the device:%s; %ld recomputed on the CPU after a device failure\n", total,
+             line.c_str(), c->n_cpu_fallbacks);
+}
+
 }  // namespace
 
 MI355X_API void mi355x_backend_free(mi355x_backend_t c) {
@@ -866,6 +881,7 @@ MI355X_API void mi355x_backend_free(mi355x_backend_t c) {
     c->pool.reset();
     for (auto & kv : c->wcache) (void)hipFree(kv.second.dev);
     report_residency(c);
+    report_routes(c);
     c->wcache.clear();
     for (DevBuf * b : {&c->act, &c->a16, &c->scales, &c->out, &c->part, &c->wstage, &c->wconv, &c->fa_q, &c->fa_k, &c->fa_v,
                        &c->fa_m, &c->fa_o, &c->fa_ws, &c->moe_b, &c->moe_ids, &c->moe_o, &c->moe_ws,
