@@ -214,6 +214,7 @@ class Prefill:
                 arr[i] = mx.GemmOut(None, N, 0, N, None, N)
             need = max(need, int(mx.lib().mi355x_gemm_workspace(self.wt, UBATCH, outs[0][1], arr, len(outs))))
         self.part = torch.empty(max(need, 256), dtype=torch.uint8, device=dev)
+        self._acc = {}
         self.timing = None
 
     # ---- op launchers (optionally bracketed by events on the launch stream) ----
@@ -228,21 +229,50 @@ class Prefill:
         e.record()
         self.timing.append((kind, s, e))
 
-    def _pack(self, x, K):
-        fn = self.mx.lib().mi355x_pack_act_tiled if self.wt == self.mx.F16_T else self.mx.lib().mi355x_pack_act
-        self._ev("pack", lambda: self.mx.check(fn(
-            self.mx._ptr(x), x.stride(0), x.shape[0], K, self.mx._ptr(self.a16),
-            self.mx._ptr(self.scales), self.mx.stream_handle()), "pack"))
+    def _pack(self, x, K, clear=None):
+        """The activation pack; `clear` = the next GEMM's output when that GEMM adds a two-way K
+        split into it (cleared by the pack in the same launch, as the backend does)."""
+        mx = self.mx
+        if clear is not None:
+            self._ev("pack", lambda: mx.check(mx.lib().mi355x_pack_act_clear(
+                int(self.wt == mx.F16_T), mx._ptr(x), x.stride(0), x.shape[0], K, mx._ptr(self.a16),
+                mx._ptr(self.scales), mx._ptr(clear), clear.stride(0), clear.shape[1], mx.stream_handle()), "pack"))
+            return
+        fn = mx.lib().mi355x_pack_act_tiled if self.wt == mx.F16_T else mx.lib().mi355x_pack_act
+        self._ev("pack", lambda: mx.check(fn(
+            mx._ptr(x), x.stride(0), x.shape[0], K, mx._ptr(self.a16),
+            mx._ptr(self.scales), mx.stream_handle()), "pack"))
 
-    def _gemm(self, K, outs, flops):
+    def _accumulates(self, K, outs):
+        """Whether this launch adds a two-way K split into its (single) output."""
+        mx = self.mx
+        key = (K, tuple(N for _, N, _ in outs))
+        if key not in self._acc:
+            arr = (mx.GemmOut * len(outs))()
+            for i, (_, N, _) in enumerate(outs):
+                arr[i] = mx.GemmOut(None, N, 0, N, None, N)
+            st = int(mx.lib().mi355x_gemm_accumulates(self.wt, UBATCH, K, arr, len(outs), self.part.numel()))
+            if st < 0:
+                raise RuntimeError(f"mi355x_gemm_accumulates: status {st}")
+            self._acc[key] = st == 1 and len(outs) == 1
+        return self._acc[key]
+
+    def _gemm(self, K, outs, flops, zeroed=False):
         mx = self.mx
         arr = (mx.GemmOut * len(outs))()
         for i, (w, N, c) in enumerate(outs):
             arr[i] = mx.GemmOut(w.data_ptr(), N, 0, N, c.data_ptr(), c.stride(0))
+        flags = 1 if zeroed else 0   # MI355X_GEMM_OUT_ZEROED
         self._ev("gemm", lambda: mx.check(mx.lib().mi355x_gemm_ws(
             self.wt, mx._ptr(self.a16), mx._ptr(self.scales), UBATCH, K, arr, len(outs),
-            mx._ptr(self.part), self.part.numel(), mx.stream_handle()), "gemm"))
+            mx._ptr(self.part), self.part.numel(), flags, mx.stream_handle()), "gemm"))
         self.flops["gemm"] += flops
+
+    def _mm(self, x, K, outs, flops):
+        """pack + GEMM, the pack clearing the output when the GEMM accumulates into it."""
+        acc = self._accumulates(K, outs)
+        self._pack(x, K, clear=outs[0][2] if acc else None)
+        self._gemm(K, outs, flops, zeroed=acc)
 
     def _fa(self, u):
         n_kv = UBATCH * (u + 1)
@@ -260,19 +290,15 @@ class Prefill:
         for u in range(TOKENS // UBATCH):
             for lw in self.layers:
                 M = UBATCH
-                self._pack(self.x, D_MODEL)
-                self._gemm(D_MODEL, [(lw["q"], sh["q"][0], self.qo), (lw["k"], sh["k"][0], self.ko),
-                                     (lw["v"], sh["v"][0], self.vo)],
-                           2.0 * M * D_MODEL * (D_MODEL + 2 * NKV * HD))
+                self._mm(self.x, D_MODEL, [(lw["q"], sh["q"][0], self.qo), (lw["k"], sh["k"][0], self.ko),
+                                           (lw["v"], sh["v"][0], self.vo)],
+                         2.0 * M * D_MODEL * (D_MODEL + 2 * NKV * HD))
                 if UBATCH * (u + 1) >= self.fa_min_kv:
                     self._fa(u)
-                self._pack(self.attn, D_MODEL)
-                self._gemm(D_MODEL, [(lw["o"], D_MODEL, self.oo)], 2.0 * M * D_MODEL * D_MODEL)
-                self._pack(self.x, D_MODEL)
-                self._gemm(D_MODEL, [(lw["gate"], FFN, self.go), (lw["up"], FFN, self.uo)],
-                           2.0 * M * D_MODEL * 2 * FFN)
-                self._pack(self.act, FFN)
-                self._gemm(FFN, [(lw["down"], D_MODEL, self.do)], 2.0 * M * FFN * D_MODEL)
+                self._mm(self.attn, D_MODEL, [(lw["o"], D_MODEL, self.oo)], 2.0 * M * D_MODEL * D_MODEL)
+                self._mm(self.x, D_MODEL, [(lw["gate"], FFN, self.go), (lw["up"], FFN, self.uo)],
+                         2.0 * M * D_MODEL * 2 * FFN)
+                self._mm(self.act, FFN, [(lw["down"], D_MODEL, self.do)], 2.0 * M * FFN * D_MODEL)
 
     def reset_counters(self, timing):
         self.flops = {"gemm": 0.0, "fa": 0.0}
@@ -381,7 +407,8 @@ def time_ops(pf, reps=32):
         ("gemm", 2.0 * M * D_MODEL * 2 * FFN, L_LAYERS * 4,
          lambda i: pf._gemm(D_MODEL, [(lw(i)["gate"], FFN, pf.go), (lw(i)["up"], FFN, pf.uo)], 0.0)),
         ("gemm", 2.0 * M * FFN * D_MODEL, L_LAYERS * 4,
-         lambda i: pf._gemm(FFN, [(lw(i)["down"], D_MODEL, pf.do)], 0.0)),
+         lambda i: pf._gemm(FFN, [(lw(i)["down"], D_MODEL, pf.do)], 0.0,
+                            zeroed=pf._accumulates(FFN, [(None, D_MODEL, pf.do)]))),
     ]
     for u in range(TOKENS // UBATCH):
         kind = "fa" if UBATCH * (u + 1) >= pf.fa_min_kv else "fa-declined"
@@ -421,6 +448,7 @@ def pmc_probe(pf):
     torch = pf.torch
     lw, sh = pf.layers[0], pf.shapes
     pf.reset_counters(False)
+    down_acc = pf._accumulates(FFN, [(None, D_MODEL, pf.do)])   # as in the step: the pack clears
     ops = [
         ("pack x[512,4096]", lambda: pf._pack(pf.x, D_MODEL)),
         ("gemm qkv 512x4096x6144", lambda: pf._gemm(D_MODEL, [(lw["q"], sh["q"][0], pf.qo),
@@ -429,8 +457,8 @@ def pmc_probe(pf):
         ("gemm o 512x4096x4096", lambda: pf._gemm(D_MODEL, [(lw["o"], D_MODEL, pf.oo)], 0.0)),
         ("gemm gate/up 512x4096x28672", lambda: pf._gemm(D_MODEL, [(lw["gate"], FFN, pf.go),
                                                                   (lw["up"], FFN, pf.uo)], 0.0)),
-        ("pack act[512,14336]", lambda: pf._pack(pf.act, FFN)),
-        ("gemm down 512x14336x4096", lambda: pf._gemm(FFN, [(lw["down"], D_MODEL, pf.do)], 0.0)),
+        ("pack act[512,14336]", lambda: pf._pack(pf.act, FFN, clear=pf.do if down_acc else None)),
+        ("gemm down 512x14336x4096", lambda: pf._gemm(FFN, [(lw["down"], D_MODEL, pf.do)], 0.0, zeroed=down_acc)),
         ("fa n_kv 2048", lambda: pf._fa(3)),
     ]
     for _, fn in ops:

@@ -593,6 +593,12 @@ int mul_mat_device(Ctx * c, const std::vector<mi355x_tensor *> & grp, bool want_
         outs[i].ldc = ntot;
         col += a->ne[1];
     }
+    // K-split partials, summed in a fixed order (reproducible results); a two-way split adds
+    // into the outputs, which the activation pack then clears in the same launch
+    const size_t pbytes = mi355x_gemm_workspace(ws[0].dev_type, M, K, outs, (int)grp.size());
+    if (pbytes) TRY(c->part.ensure(pbytes));
+    const int acc = mi355x_gemm_accumulates(ws[0].dev_type, M, K, outs, (int)grp.size(), pbytes);
+    if (acc < 0) return acc;
     // src1 from the attention this call just computed (same host bytes, row-major F32): its
     // device copy; otherwise uploaded
     const float * act = (const float *)c->act.p;
@@ -602,15 +608,17 @@ int mul_mat_device(Ctx * c, const std::vector<mi355x_tensor *> & grp, bool want_
         act = (const float *)c->fa_mirror.dev;
     else
         TRY(h2d(c, c->act.p, b->data, (size_t)M * K * 4));
-    if (ws[0].dev_type == MI355X_F16_T)
+    const int tiled = ws[0].dev_type == MI355X_F16_T;
+    if (acc)   // the outputs are the ntot columns of c->out
+        TRY(mi355x_pack_act_clear(tiled, act, K, M, K, (uint16_t *)c->a16.p, (float *)c->scales.p, (float *)c->out.p,
+                                  ntot, ntot, c->stream));
+    else if (tiled)
         TRY(mi355x_pack_act_tiled(act, K, M, K, (uint16_t *)c->a16.p, (float *)c->scales.p, c->stream));
     else
         TRY(mi355x_pack_act(act, K, M, K, (uint16_t *)c->a16.p, (float *)c->scales.p, c->stream));
-    // K-split partials, summed in a fixed order (reproducible results)
-    const size_t pbytes = mi355x_gemm_workspace(ws[0].dev_type, M, K, outs, (int)grp.size());
-    if (pbytes) TRY(c->part.ensure(pbytes));
     TRY(mi355x_gemm_ws(ws[0].dev_type, (const uint16_t *)c->a16.p, (const float *)c->scales.p, M, K, outs,
-                       (int)grp.size(), pbytes ? c->part.p : nullptr, pbytes, c->stream));
+                       (int)grp.size(), pbytes ? c->part.p : nullptr, pbytes, acc ? MI355X_GEMM_OUT_ZEROED : 0,
+                       c->stream));
     // dst[i] is [N_i, M] contiguous: one member takes the output as is; a group's outputs come
     // back as whole rows of the concatenated [M][ntot] and are split into the members' column
     // blocks on the host

@@ -135,6 +135,13 @@ MI355X_API int mi355x_pack_act_tiled(const float * x_dev, int64_t ldx, int64_t M
     return pack_impl(true, x_dev, ldx, M, K, a16_dev, scales_dev, stream, nullptr, 0, 0);
 }
 
+MI355X_API int mi355x_pack_act_clear(int tiled, const float * x_dev, int64_t ldx, int64_t M, int64_t K,
+                                     uint16_t * a16_dev, float * scales_dev, float * clear_dev, int64_t ld_clear,
+                                     int64_t n_clear, void * stream) {
+    if (!clear_dev || n_clear <= 0 || !aligned(clear_dev, 4)) return MI355X_E_ARG;
+    return pack_impl(tiled != 0, x_dev, ldx, M, K, a16_dev, scales_dev, stream, clear_dev, ld_clear, n_clear);
+}
+
 // The launch arguments of a GEMM, checked; `with_ptrs` also checks the operand pointers.
 static int gemm_lower(int wtype, const uint16_t * a16_dev, const float * scales_dev, int64_t M, int64_t K,
                       const mi355x_gemm_out * outs, int n_out, bool with_ptrs, mx::GemmArgs & a) {
@@ -194,10 +201,19 @@ MI355X_API size_t mi355x_gemm_workspace(int wtype, int64_t M, int64_t K, const m
     return mx::gemm_split_bytes(wtype, a);
 }
 
+MI355X_API int mi355x_gemm_accumulates(int wtype, int64_t M, int64_t K, const mi355x_gemm_out * outs, int n_out,
+                                       size_t workspace_bytes) {
+    mx::GemmArgs a;
+    const int st = gemm_lower(wtype, nullptr, nullptr, M, K, outs, n_out, false, a);
+    if (st != MI355X_OK) return st;
+    return M > 0 && mx::gemm_accumulates(wtype, a, workspace_bytes) ? 1 : 0;
+}
+
 MI355X_API int mi355x_gemm_ws(int wtype, const uint16_t * a16_dev, const float * scales_dev,
                               int64_t M, int64_t K, const mi355x_gemm_out * outs, int n_out,
-                              void * workspace_dev, size_t workspace_bytes, void * stream) {
-    return gemm_impl(wtype, a16_dev, scales_dev, M, K, outs, n_out, stream, false, workspace_dev, workspace_bytes);
+                              void * workspace_dev, size_t workspace_bytes, int flags, void * stream) {
+    return gemm_impl(wtype, a16_dev, scales_dev, M, K, outs, n_out, stream, (flags & MI355X_GEMM_OUT_ZEROED) != 0,
+                     workspace_dev, workspace_bytes);
 }
 
 // M rows rounded up to 16: the tiled layout's padding (the row-major pack uses M rows of it).

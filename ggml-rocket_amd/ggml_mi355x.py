@@ -89,7 +89,9 @@ def lib():
     L.mi355x_gemm.argtypes = [i32, vp, vp, i64, i64, ctypes.POINTER(GemmOut), i32, vp]
     L.mi355x_gemm_workspace.restype = sz
     L.mi355x_gemm_workspace.argtypes = [i32, i64, i64, ctypes.POINTER(GemmOut), i32]
-    L.mi355x_gemm_ws.argtypes = [i32, vp, vp, i64, i64, ctypes.POINTER(GemmOut), i32, vp, sz, vp]
+    L.mi355x_gemm_ws.argtypes = [i32, vp, vp, i64, i64, ctypes.POINTER(GemmOut), i32, vp, sz, i32, vp]
+    L.mi355x_gemm_accumulates.argtypes = [i32, i64, i64, ctypes.POINTER(GemmOut), i32, sz]
+    L.mi355x_pack_act_clear.argtypes = [i32, vp, i64, i64, i64, vp, vp, vp, i64, i64, vp]
     L.mi355x_mul_mat_workspace.restype = sz
     L.mi355x_mul_mat_workspace.argtypes = [i64, i64]
     L.mi355x_mul_mat_workspace_for.restype = sz
@@ -219,7 +221,7 @@ def gemm(wtype: int, a16, scales, K: int, outs, split_workspace: bool = True):
         return
     need = int(lib().mi355x_gemm_workspace(wtype, M, K, arr, len(outs)))
     ws = _torch().empty(max(need, 1), dtype=_torch().uint8, device=a16.device)
-    check(lib().mi355x_gemm_ws(wtype, _ptr(a16), _ptr(scales), M, K, arr, len(outs), _ptr(ws), need,
+    check(lib().mi355x_gemm_ws(wtype, _ptr(a16), _ptr(scales), M, K, arr, len(outs), _ptr(ws), need, 0,
                                stream_handle()), "gemm_ws")
 
 

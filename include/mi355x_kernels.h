@@ -103,6 +103,15 @@ MI355X_API int mi355x_convert_f16(int type, const void * src_dev, int64_t n, uin
 MI355X_API int mi355x_pack_act(const float * x_dev, int64_t ldx, int64_t M, int64_t K,
                                uint16_t * a16_dev, float * scales_dev, void * stream);
 
+/* mi355x_pack_act (tiled != 0: mi355x_pack_act_tiled) that also clears columns [0, n_clear) of
+ * the M rows of an F32 matrix clear_dev (row stride ld_clear elements): the output of a GEMM that
+ * adds a two-way K split into it (mi355x_gemm_accumulates), cleared in the same launch instead
+ * of by a fill of the GEMM's own (pass MI355X_GEMM_OUT_ZEROED to mi355x_gemm_ws). No counterpart
+ * in the reference, whose NPU GEMM writes its output. */
+MI355X_API int mi355x_pack_act_clear(int tiled, const float * x_dev, int64_t ldx, int64_t M, int64_t K,
+                                     uint16_t * a16_dev, float * scales_dev, float * clear_dev, int64_t ld_clear,
+                                     int64_t n_clear, void * stream);
+
 /* mi355x_pack_act with the fp16 output in the MI355X_F16_T layout (ceil(M/16)*16 rows; the
  * padding rows are never read), for a GEMM on MI355X_F16_T weights. K % 32 == 0. Same values and
  * scales as mi355x_pack_act (rocket_pack_activations, ggml-rocket.cpp:1451-1502). */
@@ -147,7 +156,18 @@ MI355X_API size_t mi355x_gemm_workspace(int wtype, int64_t M, int64_t K, const m
  * workspace size may pick a different split and round differently. */
 MI355X_API int mi355x_gemm_ws(int wtype, const uint16_t * a16_dev, const float * scales_dev,
                               int64_t M, int64_t K, const mi355x_gemm_out * outs, int n_out,
-                              void * workspace_dev, size_t workspace_bytes, void * stream);
+                              void * workspace_dev, size_t workspace_bytes, int flags, void * stream);
+
+/* flags of mi355x_gemm_ws: the outputs are already zero (cleared by mi355x_pack_act_clear), so a
+ * launch that adds a two-way split into them launches no fill of its own. */
+#define MI355X_GEMM_OUT_ZEROED 1
+
+/* 1 if mi355x_gemm_ws with `workspace_bytes` of workspace adds a two-way K split into zeroed
+ * outputs for this launch (the outputs must then be zero: cleared by the caller, with
+ * MI355X_GEMM_OUT_ZEROED, or by the launch itself), 0 if it writes them, or a negative status
+ * for arguments mi355x_gemm_ws would refuse (the pointers in `outs` are not read). */
+MI355X_API int mi355x_gemm_accumulates(int wtype, int64_t M, int64_t K, const mi355x_gemm_out * outs, int n_out,
+                                       size_t workspace_bytes);
 
 /* Workspace bytes mi355x_mul_mat needs for M rows of K: the activation pack. */
 MI355X_API size_t mi355x_mul_mat_workspace(int64_t M, int64_t K);

@@ -410,3 +410,38 @@ def test_split_k_reproducible(mx, monkeypatch, wtype, M, N, K, cfg, use_ws):
     # a column cosine over fewer than 8 rows says nothing (one near-zero value can flip its sign)
     _assert_bars(ref, got[0][rows], len(rows), N, f"split {O.TYPE_NAMES[wtype]} M={M} cfg={cfg}",
                  cos_floor=0.999 if len(rows) >= 8 else -1.0)
+
+
+def test_pack_clear_then_accumulating_gemm(mx):
+    """mi355x_pack_act_clear + MI355X_GEMM_OUT_ZEROED (the pack clears the output of a GEMM that
+    adds a two-way K split into it) gives the bits of the launch that clears its output itself."""
+    import torch
+    M, N, K = 512, 4096, 14336
+    W16 = O.f32_to_f16_bits(O.fill_normal((N, K), 1400, 0.0, 0.02))
+    Xf = O.fill_normal((M, K), 1401)
+    w = mx.tile_f16(O.F16, mx.upload_weight(O.F16, W16, N, K), N, K)
+    arr = (mx.GemmOut * 1)()
+    arr[0] = mx.GemmOut(None, N, 0, N, None, N)
+    part = int(mx.lib().mi355x_gemm_workspace(F16_T, M, K, arr, 1))
+    acc = int(mx.lib().mi355x_gemm_accumulates(F16_T, M, K, arr, 1, part))
+    print(f"split workspace {part} bytes, accumulates {acc}")
+    assert acc in (0, 1)
+    x = _dev(Xf)
+    a16, sc = mx.pack_act(x, tiled=True)
+    ws = torch.empty(max(part, 256), dtype=torch.uint8, device="cuda")
+    outs = []
+    for zeroed in (False, True):
+        c = torch.full((M, N + 8), float("nan"), dtype=torch.float32, device="cuda")
+        arr[0] = mx.GemmOut(w.data_ptr(), N, 0, N, c.data_ptr(), c.stride(0))
+        if zeroed:
+            mx.check(mx.lib().mi355x_pack_act_clear(1, mx._ptr(x), x.stride(0), M, K, mx._ptr(a16), mx._ptr(sc),
+                                                    mx._ptr(c), c.stride(0), N, mx.stream_handle()), "pack_clear")
+        mx.check(mx.lib().mi355x_gemm_ws(F16_T, mx._ptr(a16), mx._ptr(sc), M, K, arr, 1, mx._ptr(ws), part,
+                                         1 if (zeroed and acc) else 0, mx.stream_handle()), "gemm_ws")
+        torch.cuda.synchronize()
+        got = c.cpu().numpy()
+        assert np.isnan(got[:, N:]).all(), "wrote past N"
+        outs.append(got[:, :N])
+    assert np.array_equal(outs[0], outs[1])
+    rows = np.arange(0, M, 16)
+    _assert_bars(O.mul_mat(O.F16, W16, Xf[rows], N, K), outs[1][rows], len(rows), N, "pack-clear + zeroed GEMM")
