@@ -205,6 +205,15 @@ template <> __device__ __forceinline__ void fa_tr_read<8, 512>(const uint32_t (&
 // ---------------------------------------------------------------------------------------------
 enum : uint8_t { FA_TILE_SKIP = 0, FA_TILE_FULL = 1, FA_TILE_MIXED = 2 };
 
+// The value of lane i ^ 32 (the lane holding the same query's other 16 scores): gfx950's
+// v_permlane32_swap exchanges lanes 32-63 of its first operand with lanes 0-31 of its second, so
+// with both operands = x, lanes 0-31 find the partner in the second result and lanes 32-63 in the
+// first. A VALU exchange: no LDS round trip and no wait on the LDS reads in flight.
+__device__ __forceinline__ float fa_partner(float x) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float((threadIdx.x & 32) ? r[0] : r[1]);
+}
+
 __global__ void __launch_bounds__(256) fa_prep_kernel(FaArgs a) {
     const int t = threadIdx.x;
     const int nkt = a.kvp / FA_BKV;
@@ -354,7 +363,9 @@ fa_kernel(FaArgs a) {
     }
     __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0)
     __builtin_amdgcn_s_barrier();
-    const int lo = range_lo, hi = range_hi;
+    // block-uniform: read into SGPRs, so the tile indices and the per-tile DMA offsets below are
+    // scalar arithmetic
+    const int lo = __builtin_amdgcn_readfirstlane(range_lo), hi = __builtin_amdgcn_readfirstlane(range_hi);
     const int span = max(0, hi - lo);
     const int per = (span + a.nsplit - 1) / a.nsplit;
     const int tile0 = lo + split * per;
@@ -401,6 +412,18 @@ fa_kernel(FaArgs a) {
         uint8_t * st = smem + (i % FA_NS) * C::STAGE;
         i = min(i, max(ntl - 1, 0));
         const int j0 = (tile0 + i) * FA_BKV;
+        if (j0 + FA_BKV <= a.KV) {
+            // every key of the tile exists: one scalar row offset for the whole wave, added to
+            // the real sources only
+            const int64_t ko = (int64_t)j0 * a.k_nb1, vo = (int64_t)j0 * a.v_nb1;
+#pragma unroll
+            for (int q = 0; q < C::PK; q++)
+                fa_dma16(ksrc[q] + ((kreal >> q) & 1u ? ko : 0), st + (q * C::WAVES + wave_s) * 1024);
+#pragma unroll
+            for (int q = 0; q < C::PV; q++)
+                fa_dma16(vsrc[q] + ((vreal >> q) & 1u ? vo : 0), st + C::K_BYTES + (q * C::WAVES + wave_s) * 1024);
+            return;
+        }
 #pragma unroll
         for (int q = 0; q < C::PK; q++) {
             const int slot = (q * C::WAVES + wave) * WAVE + lane;
@@ -625,7 +648,7 @@ fa_kernel(FaArgs a) {
                 for (int kb = 0; kb < 2; kb++)
 #pragma unroll
                     for (int ii = 0; ii < 16; ii++) mt = fmaxf(mt, sacc[kb][ii]);
-                mt = fmaxf(mt, __shfl_xor(mt, 32, WAVE));
+                mt = fmaxf(mt, fa_partner(mt));
                 // The running max moves only when a score passes it by more than FA_LAZY (2^8 in
                 // P): P then stays below 256, well inside fp16 and the fp32 sums, and most tiles
                 // skip the rescale of O. When it moves, every row of the wave takes its exact max.
@@ -741,7 +764,7 @@ fa_kernel(FaArgs a) {
         }
     }
 
-    const float l_tot = l_run + __shfl_xor(l_run, 32, WAVE);
+    const float l_tot = l_run + fa_partner(l_run);
     const bool holder = C::PAR == 1 || par == 0;   // the wave holding its task's merged result
     if (!holder) return;
     if (a.nsplit == 1) {
