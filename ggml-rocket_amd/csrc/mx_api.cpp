@@ -6,7 +6,10 @@
 
 #include <hip/hip_runtime.h>
 #include <stdio.h>
+#include <stdlib.h>
 #include <string.h>
+
+#include <algorithm>
 
 #include "mx_fa_dims.h"
 #include "mx_kernels_impl.h"
@@ -297,6 +300,7 @@ static mx::FaArgs fa_lower(const mi355x_fa_args * a, int nsplit) {
     f.dk = a->D; f.dv = a->DV;
     mx::fa_pad_dims(a->D, a->DV, f.D, f.DV);   // the kernel's dims (checked by fa_check)
     f.T = a->T; f.H = a->H; f.HK = a->HK; f.KV = a->KV; f.nsplit = nsplit;
+    f.tasks = 4;
     f.kvp = (int)((a->KV + 63) / 64 * 64);
     f.cls_stride = (f.kvp / 64 + 15) / 16 * 16;
     f.scale = a->scale; f.softcap = a->softcap;
@@ -323,11 +327,7 @@ static FaLayout fa_layout(const mx::FaArgs & f) {
     return L;
 }
 
-MI355X_API int mi355x_flash_attn_auto_split(const mi355x_fa_args * a) {
-    if (fa_check(a) != MI355X_OK) return 1;
-    const mx::FaArgs f = fa_lower(a, 1);
-    const int nb = mx::fa_blocks_per_split(f);
-    const int ntiles = (a->KV + 63) / 64;
+static int device_cus() {
     static int cus = 0;   // read once: this may run while a stream is being captured
     if (cus == 0) {
         int dev = 0;
@@ -335,18 +335,60 @@ MI355X_API int mi355x_flash_attn_auto_split(const mi355x_fa_args * a) {
         cus = (hipGetDevice(&dev) == hipSuccess && hipGetDeviceProperties(&p, dev) == hipSuccess &&
                p.multiProcessorCount > 0) ? p.multiProcessorCount : 256;
     }
-    // one block per CU (their LDS rings take 128 KB); fill the chip, but keep at least 12 key
-    // tiles a split: a split costs a partial-output round trip and the combine launch
-    int ns = nb > 0 ? (cus + nb - 1) / nb : 1;
+    return cus;
+}
+
+// The launch of an op: wave tasks per block and KV split (nsplit_req > 0: that split). One block
+// per CU (their LDS rings take 128 KB). A step is two 64-key tiles for every task of a block:
+// measured at head dims 128 / 128 on MI355X, 2.4 us with four tasks a block and 1.55 us with
+// two (half the MFMA work, but the same barrier, DMA and latency chain per step), scaled here by
+// the MFMA work of other head dims. A split writes its unnormalised partials and reads them back
+// in the combine launch (about 3 us plus the partial bytes at 6 TB/s: 8.6 us at 512 queries x 32
+// heads split two ways), and keeps at least 12 key tiles. MI355X_FA_TASKS (2 or 4) pins the
+// task count, for tests.
+struct FaPlan {
+    int tasks, nsplit;
+};
+static FaPlan fa_plan(const mi355x_fa_args * a, int nsplit_req) {
+    mx::FaArgs f = fa_lower(a, 1);
+    const int ntiles = (int)((a->KV + 63) / 64);
+    const int cus = device_cus();
+    int pin = 0;
+    if (const char * e = getenv("MI355X_FA_TASKS"))
+        if (*e) pin = atoi(e);
     const int max_by_len = ntiles / 12 > 0 ? ntiles / 12 : 1;
-    if (ns > max_by_len) ns = max_by_len;
-    if (ns > 16) ns = 16;
-    return ns < 1 ? 1 : ns;
+    FaPlan best{4, nsplit_req > 0 ? nsplit_req : 1};
+    double best_us = 0.0;
+    bool have = false;
+    for (int tasks = 2; tasks <= 4; tasks += 2) {
+        if (!mx::fa_tasks_ok(f.DV, tasks) || (pin && pin != tasks)) continue;
+        f.tasks = tasks;
+        const int nb = mx::fa_blocks_per_split(f);
+        const double step_us = (tasks == 2 ? 1.55 : 2.4) * (f.D + f.DV) / 256.0;
+        const int lo = nsplit_req > 0 ? nsplit_req : 1, hi = nsplit_req > 0 ? nsplit_req : std::min(max_by_len, 16);
+        for (int ns = lo; ns <= hi; ns++) {
+            const double rounds = (double)((int64_t)nb * ns + cus - 1) / cus;
+            const int steps = ((ntiles + ns - 1) / ns + 1) / 2;
+            const double part_mb = (double)ns * a->T * a->H * f.DV * 8.0 / 1e6;
+            const double us = (int64_t)rounds * steps * step_us + (ns > 1 ? 3.0 + part_mb / 6.0 : 0.0);
+            if (!have || us < best_us - 1e-9) {
+                best = {tasks, ns};
+                best_us = us;
+                have = true;
+            }
+        }
+    }
+    return best;
+}
+
+MI355X_API int mi355x_flash_attn_auto_split(const mi355x_fa_args * a) {
+    if (fa_check(a) != MI355X_OK) return 1;
+    return fa_plan(a, 0).nsplit;
 }
 
 MI355X_API size_t mi355x_flash_attn_workspace(const mi355x_fa_args * a, int nsplit) {
     if (fa_check(a) != MI355X_OK) return 0;
-    if (nsplit <= 0) nsplit = mi355x_flash_attn_auto_split(a);
+    if (nsplit <= 0) nsplit = fa_plan(a, 0).nsplit;
     if (nsplit > 64) return 0;
     return fa_layout(fa_lower(a, nsplit)).total;
 }
@@ -356,9 +398,11 @@ MI355X_API int mi355x_flash_attn(const mi355x_fa_args * a, int nsplit,
     const int st = fa_check(a);
     if (st != MI355X_OK) return st;
     if (a->T == 0) return MI355X_OK;
-    if (nsplit <= 0) nsplit = mi355x_flash_attn_auto_split(a);
     if (nsplit > 64) return MI355X_E_ARG;
-    mx::FaArgs f = fa_lower(a, nsplit);
+    const FaPlan plan = fa_plan(a, nsplit);
+    mx::FaArgs f = fa_lower(a, plan.nsplit);
+    f.tasks = plan.tasks;
+    nsplit = plan.nsplit;
     const FaLayout L = fa_layout(f);
     if (!workspace_dev || workspace_bytes < L.total || !aligned(workspace_dev, 256)) return MI355X_E_NOMEM;
     char * ws = (char *)workspace_dev;

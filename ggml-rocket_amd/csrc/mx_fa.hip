@@ -40,7 +40,12 @@ namespace mx {
 
 constexpr int FA_BKV = 64;      // keys per tile
 constexpr int FA_QW = 32;       // query rows per wave task
-constexpr int FA_TASKS = 4;     // wave tasks (head, 32-query tile) per block
+// Wave tasks (head, 32-query tile) per block, FaArgs::tasks (fa_tasks_ok): 4 (two waves a task, taking
+// alternate key tiles; one wave a task for DV 256) or, for DV <= 128, 2 (four waves a task: each
+// of the two tile parities split again into the tile's two 32-key halves). Two tasks make twice
+// the blocks for the same work, so the chip fills without splitting the key range, and their
+// key tiles serve half as many queries; four tasks do twice the MFMA work per step and LDS
+// fill, which pays off once the key range is long enough to split (the launcher's choice).
 constexpr int FA_LDS_MAX = 160 * 1024;
 constexpr int FA_CLS_RESERVE = 2048;   // LDS kept beside the ring for the class rows (KV <= 32768)
 constexpr float FA_LAZY = 8.0f / 1.4426950408889634f;   // ln(2^8): how far a score may pass the running max
@@ -48,7 +53,7 @@ constexpr float FA_LAZY = 8.0f / 1.4426950408889634f;   // ln(2^8): how far a sc
 
 // DK: the Q.K contraction (Q and K head dim), DV: the V and output head dim (DK > DV for the
 // non-absorbed MLA of DeepSeek-style models, 192 / 128).
-template <int DK, int DV>
+template <int DK, int DV, int NTASK = 4>
 struct FaCfg {
     static constexpr int KCH = DK / 8;                       // 16-byte chunks per K row
     // K rows swizzle their chunks by XOR when KCH is a power of two (conflict free), else by a
@@ -67,7 +72,12 @@ struct FaCfg {
     // waves per task: two taking alternate key tiles (merged at the end), or for DV > 128 one
     // wave taking every tile, alone on its SIMD so the 128 accumulators of its O tile fit
     static constexpr int PAR = DV > 128 ? 1 : 2;
-    static constexpr int WAVES = FA_TASKS * PAR;
+    // and, with two tasks a block, two waves per tile, each taking one 32-key half of it
+    static constexpr int TASKS = NTASK;
+    static constexpr int HALF = TASKS == 2 ? 2 : 1;
+    static_assert(fa_tasks_ok(DV, TASKS), "tasks");
+    static constexpr int WAVES = TASKS * PAR * HALF;
+    static_assert(WAVES == 4 || WAVES == 8, "waves");
     static constexpr int THREADS = WAVES * WAVE;
     static constexpr int PK = K_BYTES / (THREADS * 16);   // DMA instructions per wave
     static constexpr int PV = V_BYTES / (THREADS * 16);
@@ -271,11 +281,11 @@ __global__ void __launch_bounds__(256) fa_prep_kernel(FaArgs a) {
 // ---------------------------------------------------------------------------------------------
 // main kernel
 // ---------------------------------------------------------------------------------------------
-template <int DK, int DV, bool SOFTCAP>
-__global__ void __launch_bounds__((FaCfg<DK, DV>::THREADS))
-__attribute__((amdgpu_waves_per_eu(FaCfg<DK, DV>::PAR, FaCfg<DK, DV>::PAR)))
+template <int DK, int DV, int NTASK, bool SOFTCAP>
+__global__ void __launch_bounds__((FaCfg<DK, DV, NTASK>::THREADS))
+__attribute__((amdgpu_waves_per_eu(FaCfg<DK, DV, NTASK>::PAR, FaCfg<DK, DV, NTASK>::PAR)))
 fa_kernel(FaArgs a) {
-    using C = FaCfg<DK, DV>;
+    using C = FaCfg<DK, DV, NTASK>;
     extern __shared__ __align__(16) uint8_t smem[];
     constexpr int FA_NS = C::NS;
     constexpr int KSTEPS = DK / 16;  // QK contraction steps
@@ -284,7 +294,12 @@ fa_kernel(FaArgs a) {
     const int t = threadIdx.x, lane = t % WAVE, wave = t / WAVE;
     const int lq = lane % 32, lg = lane / 32;
     const int wave_s = __builtin_amdgcn_readfirstlane(wave);
-    const int slot_task = wave % FA_TASKS, par = wave / FA_TASKS;
+    constexpr int TASKS = C::TASKS;
+    // wave = task + TASKS (half + HALF par): the two waves of a SIMD (w, w + 4) are one task's
+    // two parities, which take alternate key tiles
+    const int slot_task = wave % TASKS, half = (wave / TASKS) % C::HALF, par = wave / (TASKS * C::HALF);
+    constexpr int KB = 2 / C::HALF;          // 32-key blocks of a tile per wave
+    const int kb0 = C::HALF == 2 ? half : 0;  // the first of them
 
     // block -> (kv head, group of 4 wave tasks, kv split); two waves per task. Logical ids are
     // kv-head major and spread so that each XCD takes a contiguous run of them: the blocks of a
@@ -292,12 +307,12 @@ fa_kernel(FaArgs a) {
     const int g = a.H / a.HK;
     const int n_ttiles = (a.T + FA_QW - 1) / FA_QW;
     const int tasks = g * n_ttiles;
-    const int bph = (tasks + FA_TASKS - 1) / FA_TASKS;   // blocks per kv head
+    const int bph = (tasks + TASKS - 1) / TASKS;   // blocks per kv head
     int b = xcd_tile(blockIdx.x, gridDim.x);
     const int split = b % a.nsplit;
     b /= a.nsplit;
     const int hk = b / bph;
-    const int task0 = (b % bph) * FA_TASKS;
+    const int task0 = (b % bph) * TASKS;
     const int task = task0 + slot_task;
     const bool active = task < tasks;
     const int h = hk * g + (active ? task % g : 0);
@@ -306,16 +321,17 @@ fa_kernel(FaArgs a) {
     const bool qok = active && tq < a.T;
     const int nkt = a.kvp / FA_BKV;
 
-    // Q is converted once per task: the parity-0 wave loads it and, where the ring has room
-    // (four stages), hands the fp16 form to the parity-1 wave through LDS
+    // Q is converted once per task: its first wave loads it and, where the ring has room (four
+    // stages), hands the fp16 form to the task's other waves through LDS
     constexpr bool QSHARE = C::PAR == 2 && FA_NS == 4;
-    const bool qload = !QSHARE || par == 0;
+    const bool lead = par == 0 && half == 0;   // the task's first wave
+    const bool qload = !QSHARE || lead;
 
     // the block's key tiles: the union of its tasks' non-skipped ranges (a cooperative scan of
     // the class rows, 16 entries per load; at most one load per thread for KV within
     // fa_max_kv), then this split's share. The class loads are issued before Q's, so the scan
     // waits for them alone.
-    const int qt_first = task0 / g, qt_last = min(tasks - 1, task0 + FA_TASKS - 1) / g;
+    const int qt_first = task0 / g, qt_last = min(tasks - 1, task0 + TASKS - 1) / g;
     const int nchunk = a.cls_stride / 16;
     const int items = (qt_last - qt_first + 1) * nchunk;
     u32x4 cw = {0, 0, 0, 0};
@@ -495,14 +511,14 @@ fa_kernel(FaArgs a) {
         // through ring stages 2 and 3, whose tiles are requested once the hand-over is done:
         // per task [KSTEPS][64 lanes] half8, then the 64 lanes' range factors
         uint8_t * qx = smem + 2 * C::STAGE + slot_task * (KSTEPS * 1024 + 256);
-        if (par == 0) {
+        if (lead) {
 #pragma unroll
             for (int s = 0; s < KSTEPS; s++) *(half8 *)(qx + s * 1024 + lane * 16) = qf[s];
             *(float *)(qx + KSTEPS * 1024 + lane * 4) = qfac;
         }
         __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0)
         __builtin_amdgcn_s_barrier();
-        if (par == 1) {
+        if (!lead) {
 #pragma unroll
             for (int s = 0; s < KSTEPS; s++) qf[s] = *(const half8 *)(qx + s * 1024 + lane * 16);
             qfac = *(const float *)(qx + KSTEPS * 1024 + lane * 4);
@@ -514,7 +530,7 @@ fa_kernel(FaArgs a) {
             issue(3);
         }
     }
-    static_assert(!QSHARE || FA_TASKS * (KSTEPS * 1024 + 256) <= 2 * C::STAGE, "Q hand-over space");
+    static_assert(!QSHARE || TASKS * (KSTEPS * 1024 + 256) <= 2 * C::STAGE, "Q hand-over space");
     const bool q_scaled = __any(qfac != 1.0f);   // a row of this wave needed the Q range factor
     if (ntl > 0) {
         fa_wait_vm_lgkm0<(FA_NS - 2) * C::PER>();
@@ -533,46 +549,46 @@ fa_kernel(FaArgs a) {
             const uint32_t cls = __builtin_amdgcn_readfirstlane(
                 (active && i < ntl) ? (uint32_t)cls_w[tile] : (uint32_t)FA_TILE_SKIP);
             if (cls != FA_TILE_SKIP) {
-                // ---- S^T = K . Q^T for 64 keys: two 32-key blocks ----
+                // ---- S^T = K . Q^T for this wave's 32-key blocks of the tile (kb0 .. kb0 + KB - 1) ----
                 // Every K fragment read of the tile is issued before the first MFMA, so the LDS
                 // latency is paid once per tile rather than once per MFMA; the scheduling barriers
                 // keep the compiler from interleaving each read with the MFMA that consumes it.
                 // (DK <= 128; the wider heads, whose fragments do not fit the register budget
                 // twice over, read and multiply one 32-key block at a time.)
-                float16v sacc[2];
+                float16v sacc[KB];
                 auto kfrag = [&](int kb, int s2) {
                     return *(const half8 *)(ks + (kb * 32 + lq) * (DK * 2) + (C::kchunk(kb * 32 + lq, 2 * s2 + lg) << 4));
                 };
                 if constexpr (DK <= 128) {
-                    half8 kf[2][KSTEPS];
+                    half8 kf[KB][KSTEPS];
 #pragma unroll
-                    for (int kb = 0; kb < 2; kb++)
+                    for (int kk = 0; kk < KB; kk++)
 #pragma unroll
-                        for (int s2 = 0; s2 < KSTEPS; s2++) kf[kb][s2] = kfrag(kb, s2);
+                        for (int s2 = 0; s2 < KSTEPS; s2++) kf[kk][s2] = kfrag(kb0 + kk, s2);
                     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-                    for (int kb = 0; kb < 2; kb++) {
+                    for (int kk = 0; kk < KB; kk++) {
 #pragma unroll
-                        for (int e = 0; e < 16; e++) sacc[kb][e] = 0.0f;
+                        for (int e = 0; e < 16; e++) sacc[kk][e] = 0.0f;
 #pragma unroll
-                        for (int s2 = 0; s2 < KSTEPS; s2++) sacc[kb] = mfma32(kf[kb][s2], qf[s2], sacc[kb]);
+                        for (int s2 = 0; s2 < KSTEPS; s2++) sacc[kk] = mfma32(kf[kk][s2], qf[s2], sacc[kk]);
                     }
                     __builtin_amdgcn_sched_barrier(0);
                 } else {
 #pragma unroll
-                    for (int kb = 0; kb < 2; kb++) {
+                    for (int kk = 0; kk < KB; kk++) {
                         half8 kf[KSTEPS];
 #pragma unroll
-                        for (int s2 = 0; s2 < KSTEPS; s2++) kf[s2] = kfrag(kb, s2);
+                        for (int s2 = 0; s2 < KSTEPS; s2++) kf[s2] = kfrag(kb0 + kk, s2);
 #pragma unroll
-                        for (int e = 0; e < 16; e++) sacc[kb][e] = 0.0f;
+                        for (int e = 0; e < 16; e++) sacc[kk][e] = 0.0f;
 #pragma unroll
-                        for (int s2 = 0; s2 < KSTEPS; s2++) sacc[kb] = mfma32(kf[s2], qf[s2], sacc[kb]);
+                        for (int s2 = 0; s2 < KSTEPS; s2++) sacc[kk] = mfma32(kf[s2], qf[s2], sacc[kk]);
                     }
                 }
-                // the V^T fragments of the first two P.V steps do not depend on the softmax: issue
-                // their reads now, so they land while the scores are computed (DK, DV <= 128; the
-                // wider builds have no registers to spare for them)
+                // the V^T fragments of the wave's first two 16-key P.V steps do not depend on the
+                // softmax: issue their reads now, so they land while the scores are computed (DK,
+                // DV <= 128; the wider builds have no registers to spare for them)
                 constexpr bool EARLY_V = DK <= 128 && DV <= 128;
                 // the fragments of NS2 consecutive 16-key steps from s2 on, for every db
                 const uint32_t vt_lds = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const uint8_t *)vt;
@@ -597,29 +613,29 @@ fa_kernel(FaArgs a) {
                 };
                 half8 vfa[EARLY_V ? 2 : 1][DBLK];
                 if constexpr (EARLY_V) {
-                    vfrags(0, vfa);   // their wait overlaps the score MFMAs in flight
+                    vfrags(2 * kb0, vfa);   // their wait overlaps the score MFMAs in flight
                     __builtin_amdgcn_sched_barrier(0);
                 }
                 // ---- scores: scale back, cap, mask, key bound (each a wave-uniform case) ----
                 if (q_scaled) {
 #pragma unroll
-                    for (int kb = 0; kb < 2; kb++)
+                    for (int kk = 0; kk < KB; kk++)
 #pragma unroll
-                        for (int ii = 0; ii < 16; ii++) sacc[kb][ii] *= qfac;
+                        for (int ii = 0; ii < 16; ii++) sacc[kk][ii] *= qfac;
                 }
                 if (SOFTCAP) {
 #pragma unroll
-                    for (int kb = 0; kb < 2; kb++)
+                    for (int kk = 0; kk < KB; kk++)
 #pragma unroll
-                        for (int ii = 0; ii < 16; ii++) sacc[kb][ii] = a.softcap * tanhf(sacc[kb][ii] * inv_cap);
+                        for (int ii = 0; ii < 16; ii++) sacc[kk][ii] = a.softcap * tanhf(sacc[kk][ii] * inv_cap);
                 }
                 if (cls == FA_TILE_MIXED) {
                     if (mrow) {
 #pragma unroll
-                        for (int kb = 0; kb < 2; kb++)
+                        for (int kk = 0; kk < KB; kk++)
 #pragma unroll
                             for (int q4 = 0; q4 < 4; q4++) {
-                                const int jb = j0 + kb * 32 + 8 * q4 + 4 * lg;   // first of 4 keys
+                                const int jb = j0 + (kb0 + kk) * 32 + 8 * q4 + 4 * lg;   // first of 4 keys
                                 float mk[4];
                                 if (jb + 3 < a.KV) {
                                     const u32x2 mm = *(const u32x2 *)(mrow + jb);
@@ -632,22 +648,22 @@ fa_kernel(FaArgs a) {
                                     for (int e = 0; e < 4; e++) mk[e] = (jb + e < a.KV) ? h2f_bits(mrow[jb + e]) : 0.0f;
                                 }
 #pragma unroll
-                                for (int e = 0; e < 4; e++) sacc[kb][4 * q4 + e] += mk[e];
+                                for (int e = 0; e < 4; e++) sacc[kk][4 * q4 + e] += mk[e];
                             }
                     }
                 }
                 if (j0 + FA_BKV > a.KV) {
 #pragma unroll
-                    for (int kb = 0; kb < 2; kb++)
+                    for (int kk = 0; kk < KB; kk++)
 #pragma unroll
                         for (int ii = 0; ii < 16; ii++)
-                            if (j0 + kb * 32 + 8 * (ii / 4) + 4 * lg + (ii % 4) >= a.KV) sacc[kb][ii] = -INFINITY;
+                            if (j0 + (kb0 + kk) * 32 + 8 * (ii / 4) + 4 * lg + (ii % 4) >= a.KV) sacc[kk][ii] = -INFINITY;
                 }
                 float mt = -INFINITY;
 #pragma unroll
-                for (int kb = 0; kb < 2; kb++)
+                for (int kk = 0; kk < KB; kk++)
 #pragma unroll
-                    for (int ii = 0; ii < 16; ii++) mt = fmaxf(mt, sacc[kb][ii]);
+                    for (int ii = 0; ii < 16; ii++) mt = fmaxf(mt, sacc[kk][ii]);
                 mt = fmaxf(mt, fa_partner(mt));
                 // The running max moves only when a score passes it by more than FA_LAZY (2^8 in
                 // P): P then stays below 256, well inside fp16 and the fp32 sums, and most tiles
@@ -666,16 +682,16 @@ fa_kernel(FaArgs a) {
                 }
                 const float mb = (m_run == -INFINITY) ? 0.0f : m_run * LOG2E;
 #pragma unroll
-                for (int kb = 0; kb < 2; kb++)
+                for (int kk = 0; kk < KB; kk++)
 #pragma unroll
                     for (int ii = 0; ii < 16; ii++)
                         // v_exp_f32: exp2(-inf) = 0; results below the fp32 normal range flush to 0
-                        sacc[kb][ii] = __builtin_amdgcn_exp2f(fmaf(sacc[kb][ii], LOG2E, -mb));
-                // ---- O^T += V^T . P^T, 4 steps of 16 keys ----
+                        sacc[kk][ii] = __builtin_amdgcn_exp2f(fmaf(sacc[kk][ii], LOG2E, -mb));
+                // ---- O^T += V^T . P^T, one step per 16 keys of the wave ----
                 if constexpr (EARLY_V) {
-                    half8 pf[4];
+                    half8 pf[2 * KB];
 #pragma unroll
-                    for (int s2 = 0; s2 < 4; s2++)
+                    for (int s2 = 0; s2 < 2 * KB; s2++)
 #pragma unroll
                         for (int e = 0; e < 8; e++) pf[s2][e] = (_Float16)sacc[s2 / 2][8 * (s2 % 2) + e];
                     // the row sum of the P that the MFMA multiplies (its fp16 values), two per
@@ -683,7 +699,7 @@ fa_kernel(FaArgs a) {
                     float psum = 0.0f;
                     const half2v one2 = {(_Float16)1.0f, (_Float16)1.0f};
 #pragma unroll
-                    for (int s2 = 0; s2 < 4; s2++)
+                    for (int s2 = 0; s2 < 2 * KB; s2++)
 #pragma unroll
                         for (int e = 0; e < 4; e++)
                             psum = __builtin_amdgcn_fdot2(half2v{pf[s2][2 * e], pf[s2][2 * e + 1]}, one2, psum, false);
@@ -693,30 +709,32 @@ fa_kernel(FaArgs a) {
 #pragma unroll
                         for (int db = 0; db < DBLK; db++) o[db] = mfma32(vfa[s2][db], pf[s2], o[db]);
                     __builtin_amdgcn_sched_barrier(0);
-                    // the last two steps' fragments are read while the first two steps multiply
-                    half8 vfb[2][DBLK];
-                    vfrags(2, vfb);
-                    __builtin_amdgcn_sched_barrier(0);
+                    if constexpr (KB == 2) {
+                        // the last two steps' fragments are read while the first two steps multiply
+                        half8 vfb[2][DBLK];
+                        vfrags(2, vfb);
+                        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-                    for (int s2 = 0; s2 < 2; s2++)
+                        for (int s2 = 0; s2 < 2; s2++)
 #pragma unroll
-                        for (int db = 0; db < DBLK; db++) o[db] = mfma32(vfb[s2][db], pf[2 + s2], o[db]);
-                    __builtin_amdgcn_sched_barrier(0);
+                            for (int db = 0; db < DBLK; db++) o[db] = mfma32(vfb[s2][db], pf[2 + s2], o[db]);
+                        __builtin_amdgcn_sched_barrier(0);
+                    }
                 } else {
                     float psum = 0.0f;
 #pragma unroll
-                    for (int kb = 0; kb < 2; kb++)
+                    for (int kk = 0; kk < KB; kk++)
 #pragma unroll
-                        for (int ii = 0; ii < 16; ii++) psum += sacc[kb][ii];
+                        for (int ii = 0; ii < 16; ii++) psum += sacc[kk][ii];
                     l_run += psum;
 #pragma unroll
-                    for (int s2 = 0; s2 < 4; s2++) {
-                        const int kb = s2 / 2, hs = s2 % 2;
+                    for (int j = 0; j < 2 * KB; j++) {
+                        const int kk = j / 2, hs = j % 2;
                         half8 pf;
 #pragma unroll
-                        for (int e = 0; e < 8; e++) pf[e] = (_Float16)sacc[kb][8 * hs + e];
+                        for (int e = 0; e < 8; e++) pf[e] = (_Float16)sacc[kk][8 * hs + e];
                         half8 vf[1][DBLK];
-                        vfrags(s2, vf);
+                        vfrags(2 * kb0 + j, vf);
 #pragma unroll
                         for (int db = 0; db < DBLK; db++) o[db] = mfma32(vf[0][db], pf, o[db]);
                     }
@@ -738,10 +756,12 @@ fa_kernel(FaArgs a) {
     fa_wait_vm_lgkm0<0>();   // no DMA may still be writing LDS: the merge below reuses the ring
     __syncthreads();
 
-    // ---- merge each task's two waves (same rows, disjoint key tiles) through LDS ----
-    if constexpr (C::PAR == 2) {
-        float * ob = (float *)smem + (size_t)slot_task * (DBLK * 16 + 2) * WAVE;   // [DBLK*16 + 2][64]
-        if (par == 1) {
+    // ---- merge each task's waves (same rows, disjoint keys) through LDS: each parity-1 wave
+    // into its parity-0 partner, then the parity-0 wave of the second key halves into the task's
+    // first wave ----
+    auto merge = [&](bool give, bool take, int slot) {
+        float * ob = (float *)smem + (size_t)slot * (DBLK * 16 + 2) * WAVE;   // [DBLK*16 + 2][64]
+        if (give) {
 #pragma unroll
             for (int db = 0; db < DBLK; db++)
 #pragma unroll
@@ -750,7 +770,7 @@ fa_kernel(FaArgs a) {
             ob[(DBLK * 16 + 1) * WAVE + lane] = l_run;
         }
         __syncthreads();
-        if (par == 0) {
+        if (take) {
             const float m1 = ob[(DBLK * 16) * WAVE + lane], l1 = ob[(DBLK * 16 + 1) * WAVE + lane];
             const float M = fmaxf(m_run, m1);
             const float a0 = (m_run == -INFINITY) ? 0.0f : __expf(m_run - M);
@@ -762,11 +782,16 @@ fa_kernel(FaArgs a) {
             l_run = l_run * a0 + l1 * a1;
             m_run = M;
         }
+    };
+    static_assert(C::PAR == 1 || TASKS * C::HALF * (DBLK * 16 + 2) * WAVE * 4 <= C::LDS, "merge space");
+    if constexpr (C::PAR == 2) merge(par == 1, par == 0, slot_task + TASKS * half);
+    if constexpr (C::HALF == 2) {
+        __syncthreads();   // the first merge's reads are done before its area is written again
+        merge(par == 0 && half == 1, lead, slot_task);
     }
 
     const float l_tot = l_run + fa_partner(l_run);
-    const bool holder = C::PAR == 1 || par == 0;   // the wave holding its task's merged result
-    if (!holder) return;
+    if (!lead) return;   // the task's first wave holds its merged result
     if (a.nsplit == 1) {
         if (!qok) return;
         const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
@@ -842,7 +867,7 @@ __global__ void __launch_bounds__(256) fa_combine_kernel(FaArgs a) {
 int fa_blocks_per_split(const FaArgs & a) {
     const int g = a.H / a.HK;
     const int n_ttiles = (a.T + FA_QW - 1) / FA_QW;
-    return a.HK * ((g * n_ttiles + FA_TASKS - 1) / FA_TASKS);
+    return a.HK * ((g * n_ttiles + a.tasks - 1) / a.tasks);
 }
 
 int fa_prep_blocks(const FaArgs & a) {
@@ -850,7 +875,7 @@ int fa_prep_blocks(const FaArgs & a) {
     return max(1, (nqt * a.cls_stride + 3) / 4);
 }
 
-// the ring plus the class rows of up to FA_TASKS query tiles
+// the ring plus the class rows of up to `tasks` query tiles
 static size_t fa_ring_bytes(int D, int DV) {
     if (D == 64 && DV == 64) return FaCfg<64, 64>::LDS;
     if (D == 128 && DV == 128) return FaCfg<128, 128>::LDS;
@@ -858,7 +883,7 @@ static size_t fa_ring_bytes(int D, int DV) {
     if (D == 256 && DV == 256) return FaCfg<256, 256>::LDS;
     return 0;
 }
-static size_t fa_lds_bytes(const FaArgs & a) { return fa_ring_bytes(a.D, a.DV) + (size_t)FA_TASKS * a.cls_stride; }
+static size_t fa_lds_bytes(const FaArgs & a) { return fa_ring_bytes(a.D, a.DV) + (size_t)a.tasks * a.cls_stride; }
 
 bool fa_dims_supported(int dk, int dv) {
     int D = 0, DV = 0;
@@ -870,20 +895,20 @@ size_t fa_max_kv(int dk, int dv) {
     if (!fa_pad_dims(dk, dv, D, DV)) return 0;
     const size_t ring = fa_ring_bytes(D, DV);
     if (!ring) return 0;
-    // class rows of FA_TASKS query tiles (one byte per 64-key tile, rows of a multiple of 16)
-    return (size_t)(FA_LDS_MAX - ring - 64) / FA_TASKS / 16 * 16 * FA_BKV;
+    // class rows of up to 4 query tiles (one byte per 64-key tile, rows of a multiple of 16)
+    return (size_t)(FA_LDS_MAX - ring - 64) / 4 / 16 * 16 * FA_BKV;
 }
 
-template <int DK, int DV, bool SC>
+template <int DK, int DV, int NT, bool SC>
 static hipError_t fa_launch_main(const FaArgs & a, int nb, hipStream_t st) {
     static bool done = false;
     if (!done) {
-        hipError_t e = hipFuncSetAttribute((const void *)fa_kernel<DK, DV, SC>,
+        hipError_t e = hipFuncSetAttribute((const void *)fa_kernel<DK, DV, NT, SC>,
                                            hipFuncAttributeMaxDynamicSharedMemorySize, FA_LDS_MAX - 64);
         if (e != hipSuccess) return e;
         done = true;
     }
-    hipLaunchKernelGGL((fa_kernel<DK, DV, SC>), dim3(nb), dim3(FaCfg<DK, DV>::THREADS), fa_lds_bytes(a), st, a);
+    hipLaunchKernelGGL((fa_kernel<DK, DV, NT, SC>), dim3(nb), dim3(FaCfg<DK, DV, NT>::THREADS), fa_lds_bytes(a), st, a);
     return hipGetLastError();
 }
 
@@ -892,7 +917,14 @@ static hipError_t fa_launch_all(const FaArgs & a, int nb, hipStream_t st) {
     hipLaunchKernelGGL(fa_prep_kernel, dim3(fa_prep_blocks(a)), dim3(256), 0, st, a);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    e = a.softcap != 0.0f ? fa_launch_main<DK, DV, true>(a, nb, st) : fa_launch_main<DK, DV, false>(a, nb, st);
+    if constexpr (DV <= 128) {
+        if (a.tasks == 2)
+            e = a.softcap != 0.0f ? fa_launch_main<DK, DV, 2, true>(a, nb, st) : fa_launch_main<DK, DV, 2, false>(a, nb, st);
+        else
+            e = a.softcap != 0.0f ? fa_launch_main<DK, DV, 4, true>(a, nb, st) : fa_launch_main<DK, DV, 4, false>(a, nb, st);
+    } else {
+        e = a.softcap != 0.0f ? fa_launch_main<DK, DV, 4, true>(a, nb, st) : fa_launch_main<DK, DV, 4, false>(a, nb, st);
+    }
     if (e != hipSuccess || a.nsplit == 1) return e;
     const int64_t rows = (int64_t)a.T * a.H;
     const int rpb = 256 / (DV / 4);
@@ -901,6 +933,7 @@ static hipError_t fa_launch_all(const FaArgs & a, int nb, hipStream_t st) {
 }
 
 hipError_t launch_fa(const FaArgs & a, hipStream_t st) {
+    if (!fa_tasks_ok(a.DV, a.tasks)) return hipErrorInvalidValue;
     const int nb = fa_blocks_per_split(a) * a.nsplit;
     if (nb <= 0) return hipSuccess;
     if (a.D == 64 && a.DV == 64) return fa_launch_all<64, 64>(a, nb, st);

@@ -51,6 +51,7 @@ struct FaArgs {
                                // V source of the padded columns
     int D, DV, T, H, HK, KV, kvp, cls_stride, nsplit;   // D: Q / K head dim, DV: V / output, as
                                                         // the kernel is built (fa_pad_dims)
+    int tasks;                 // wave tasks per block: 4, or 2 (DV <= 128; four waves a task)
     int dk, dv;                // the op's head dims (<= D, DV): columns past them are padding
     float scale, softcap;
 };
@@ -78,7 +79,9 @@ struct MoeArgs {
 int moe_max_tiles(int T, int U, int E);
 hipError_t launch_moe(int wt, const MoeArgs & a, hipStream_t st);
 
-int fa_blocks_per_split(const FaArgs & a);
+// FaArgs::tasks: 4 for every build, 2 for DV <= 128
+__host__ __device__ constexpr bool fa_tasks_ok(int DV, int tasks) { return tasks == 4 || (tasks == 2 && DV <= 128); }
+int fa_blocks_per_split(const FaArgs & a);   // for a.tasks
 int fa_prep_blocks(const FaArgs & a);
 bool fa_dims_supported(int dk, int dv);   // fa_pad_dims: dk, dv <= 256, multiples of 8
 size_t fa_max_kv(int dk, int dv);          // the longest KV range one launch takes

@@ -6,7 +6,8 @@ The reference sends the last two to its host fallback because its NPU keeps an f
 surface; here scores stay in fp32 registers and a Q row past fp16 range is divided by a per-row
 factor, so all four run on the device, scored against the same oracle and tolerances.
 Plus the prefill attention shapes: 32 query / 8 KV heads, d 128, 512 tokens, n_kv 1024/4096/8192,
-N(0,1) inputs, causal mask, scale 1/sqrt(128); scored on sampled query rows.
+N(0,1) inputs, causal mask, scale 1/sqrt(128); scored on sampled query rows. Every case runs
+under both block layouts (two or four wave tasks per block).
 """
 import numpy as np
 import pytest
@@ -16,6 +17,15 @@ from fa_cases import REFERENCE_CASES, fill_case, causal_mask, TYPICAL, SCALED, Q
 from bars import compare
 
 pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(params=[2, 4], ids=["tasks2", "tasks4"], autouse=True)
+def fa_tasks(request, monkeypatch):
+    """Every case under both block layouts: two wave tasks per block (four waves a task, each
+    taking one 32-key half of alternate tiles) and four (two waves a task). The library picks
+    between them per call; MI355X_FA_TASKS pins the choice (builds with DV 256 have only four)."""
+    monkeypatch.setenv("MI355X_FA_TASKS", str(request.param))
+    return request.param
 
 
 @pytest.fixture(scope="module")
