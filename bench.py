@@ -441,6 +441,49 @@ def time_ops(pf, reps=32):
     return out
 
 
+def vendor_gemm(ops, reps=24):
+    """The four projections at M = 512 through the vendor library, beside this backend's launch:
+    torch.mm on fp16 operands with an fp32 output (hipBLASLt on ROCm; the same arithmetic: fp16
+    products, fp32 accumulation, fp32 result), each weight cycled through enough copies to
+    exceed the 256 MB last-level cache, timed with HIP events over `reps` back-to-back calls.
+    The ours_us figures are time_ops' graph-replayed launches of the same shapes."""
+    import torch
+    names = ["qkv", "o", "gate_up", "down"]
+    shapes = [(D_MODEL + 2 * NKV * HD, D_MODEL), (D_MODEL, D_MODEL), (2 * FFN, D_MODEL), (D_MODEL, FFN)]
+    ours = [sec for kind, _, _, sec in ops if kind == "gemm"]
+    out = {}
+    for name, (N, K), mine in zip(names, shapes, ours):
+        copies = max(2, int(600e6 // (N * K * 2)) + 1)
+        g = torch.Generator(device="cuda")
+        g.manual_seed(N + K)
+        Ws = [torch.randn(N, K, device="cuda", dtype=torch.float16, generator=g) * 0.02 for _ in range(copies)]
+        A = torch.randn(UBATCH, K, device="cuda", dtype=torch.float16, generator=g)
+        try:
+            mm = lambda i: torch.mm(A, Ws[i % copies].t(), out_dtype=torch.float32)
+            mm(0)
+            outdt = "f32"
+        except (TypeError, RuntimeError):
+            mm = lambda i: torch.mm(A, Ws[i % copies].t())
+            outdt = "f16"
+        for i in range(3):
+            mm(i)
+        torch.cuda.synchronize()
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s.record()
+        for i in range(reps):
+            mm(i)
+        e.record()
+        torch.cuda.synchronize()
+        us = s.elapsed_time(e) * 1e3 / reps
+        flop = 2.0 * UBATCH * N * K
+        out[name] = {"N": N, "K": K, "hipblaslt_us": round(us, 2), "hipblaslt_tflops": round(flop / us / 1e6, 1),
+                     "ours_us": round(mine * 1e6, 2), "ours_tflops": round(flop / mine / 1e12, 1),
+                     "speedup_vs_hipblaslt": round(us / (mine * 1e6), 3), "hipblaslt_out": outdt}
+        del Ws, A
+        torch.cuda.empty_cache()
+    return out
+
+
 def pmc_probe(pf):
     """One eager launch of each distinct op of the step (after one warm-up pass), then a plain
     device copy of 1 GiB, whose FETCH_SIZE / WRITE_SIZE read against its known 1 GiB in and out
@@ -925,6 +968,8 @@ def main():
         },
         "setup_s": round(pf.setup_s, 1),
     }
+    if not args.quick:
+        res["kernels"]["gemm_vs_hipblaslt"] = vendor_gemm(ops)
     if not (args.no_cpu_baseline or args.quick):
         res["cpu_baseline"] = cpu_baseline(pf, args.cpu_threads)
     if not args.quick:

@@ -329,8 +329,8 @@ fa_kernel(FaArgs a) {
 
     // the block's key tiles: the union of its tasks' non-skipped ranges (a cooperative scan of
     // the class rows, 16 entries per load; at most one load per thread for KV within
-    // fa_max_kv), then this split's share. The class loads are issued before Q's, so the scan
-    // waits for them alone.
+    // fa_max_kv), then this split's share. The class loads are issued before Q's; Q is converted
+    // right after the scan, which by then has waited for the loads in flight.
     const int qt_first = task0 / g, qt_last = min(tasks - 1, task0 + TASKS - 1) / g;
     const int nchunk = a.cls_stride / 16;
     const int items = (qt_last - qt_first + 1) * nchunk;
@@ -356,7 +356,7 @@ fa_kernel(FaArgs a) {
     // one wave's softmax overlaps the other's MFMAs instead of both competing for each unit.
     if (par == 0) __builtin_amdgcn_s_setprio(1);
 
-    // Block barriers below wait for LDS work only (lgkmcnt), never for the Q loads in flight.
+    // The barriers wait for LDS work only (lgkmcnt), never for global loads in flight.
     __shared__ int range_lo, range_hi;
     if (t == 0) { range_lo = nkt; range_hi = 0; }
     __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0)
@@ -377,6 +377,44 @@ fa_kernel(FaArgs a) {
         if (mylo < nkt) atomicMin(&range_lo, mylo);
         if (myhi > 0) atomicMax(&range_hi, myhi);
     }
+    // ---- Q: scaled, range-guarded, converted to fp16 in the B-operand layout while the scan's
+    // atomics land. Where the ring has room the task's first wave hands the fp16 form to the
+    // task's other waves through ring stages 2 and 3 (no tile is requested yet), published by
+    // the barrier that publishes the range: per task [KSTEPS][64 lanes] half8, then the 64
+    // lanes' range factors ----
+    half8 qf[KSTEPS];
+    float qfac = 1.0f;
+    if (qload) {
+        float amax = 0.0f;
+        float qv[KSTEPS][8];
+#pragma unroll
+        for (int s = 0; s < KSTEPS; s++) {
+            const float4v x0 = qraw[s][0], x1 = qraw[s][1];
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                qv[s][e] = x0[e] * a.scale;
+                qv[s][4 + e] = x1[e] * a.scale;
+                amax = fmaxf(amax, fmaxf(fabsf(qv[s][e]), fabsf(qv[s][4 + e])));
+            }
+        }
+        amax = fmaxf(amax, __shfl_xor(amax, 32, WAVE));
+        // 65504 is the largest finite fp16; a row past it is divided by f = amax / 32768
+        if (amax > 65504.0f) qfac = amax / 32768.0f;
+        const float inv = 1.0f / qfac;
+#pragma unroll
+        for (int s = 0; s < KSTEPS; s++)
+#pragma unroll
+            for (int e = 0; e < 8; e++) qf[s][e] = (_Float16)(qfac == 1.0f ? qv[s][e] : qv[s][e] * inv);
+    }
+    uint8_t * const qx = smem + 2 * C::STAGE + slot_task * (KSTEPS * 1024 + 256);
+    if constexpr (QSHARE) {
+        if (lead) {
+#pragma unroll
+            for (int s = 0; s < KSTEPS; s++) *(half8 *)(qx + s * 1024 + lane * 16) = qf[s];
+            *(float *)(qx + KSTEPS * 1024 + lane * 4) = qfac;
+        }
+    }
+    static_assert(!QSHARE || TASKS * (KSTEPS * 1024 + 256) <= 2 * C::STAGE, "Q hand-over space");
     __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0)
     __builtin_amdgcn_s_barrier();
     // block-uniform: read into SGPRs, so the tile indices and the per-tile DMA offsets below are
@@ -481,56 +519,21 @@ fa_kernel(FaArgs a) {
 #pragma unroll
             for (int p = 2; p < FA_NS; p++) issue(p);
     }
-    // ---- Q: scaled, range-guarded, converted to fp16 in the B-operand layout ----
-    half8 qf[KSTEPS];
-    float qfac = 1.0f;
-    if (qload) {
-        float amax = 0.0f;
-        float qv[KSTEPS][8];
-#pragma unroll
-        for (int s = 0; s < KSTEPS; s++) {
-            const float4v x0 = qraw[s][0], x1 = qraw[s][1];
-#pragma unroll
-            for (int e = 0; e < 4; e++) {
-                qv[s][e] = x0[e] * a.scale;
-                qv[s][4 + e] = x1[e] * a.scale;
-                amax = fmaxf(amax, fmaxf(fabsf(qv[s][e]), fabsf(qv[s][4 + e])));
-            }
-        }
-        amax = fmaxf(amax, __shfl_xor(amax, 32, WAVE));
-        // 65504 is the largest finite fp16; a row past it is divided by f = amax / 32768
-        if (amax > 65504.0f) qfac = amax / 32768.0f;
-        const float inv = 1.0f / qfac;
-#pragma unroll
-        for (int s = 0; s < KSTEPS; s++)
-#pragma unroll
-            for (int e = 0; e < 8; e++) qf[s][e] = (_Float16)(qfac == 1.0f ? qv[s][e] : qv[s][e] * inv);
-    }
-
     if constexpr (QSHARE) {
-        // through ring stages 2 and 3, whose tiles are requested once the hand-over is done:
-        // per task [KSTEPS][64 lanes] half8, then the 64 lanes' range factors
-        uint8_t * qx = smem + 2 * C::STAGE + slot_task * (KSTEPS * 1024 + 256);
-        if (lead) {
-#pragma unroll
-            for (int s = 0; s < KSTEPS; s++) *(half8 *)(qx + s * 1024 + lane * 16) = qf[s];
-            *(float *)(qx + KSTEPS * 1024 + lane * 4) = qfac;
-        }
-        __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0)
-        __builtin_amdgcn_s_barrier();
+        // the other waves take their task's Q; stages 2 and 3 are requested once every wave has
+        // read it
         if (!lead) {
 #pragma unroll
             for (int s = 0; s < KSTEPS; s++) qf[s] = *(const half8 *)(qx + s * 1024 + lane * 16);
             qfac = *(const float *)(qx + KSTEPS * 1024 + lane * 4);
         }
-        __builtin_amdgcn_s_waitcnt(0xC07F);
+        __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0)
         __builtin_amdgcn_s_barrier();
         if (ntl > 0) {
             issue(2);
             issue(3);
         }
     }
-    static_assert(!QSHARE || TASKS * (KSTEPS * 1024 + 256) <= 2 * C::STAGE, "Q hand-over space");
     const bool q_scaled = __any(qfac != 1.0f);   // a row of this wave needed the Q range factor
     if (ntl > 0) {
         fa_wait_vm_lgkm0<(FA_NS - 2) * C::PER>();
