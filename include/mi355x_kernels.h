@@ -218,16 +218,20 @@ typedef struct mi355x_fa_args {
     float scale, max_bias, softcap;
 } mi355x_fa_args;
 
-/* The KV-split count mi355x_flash_attn uses when called with nsplit = 0. */
+/* The KV-split count mi355x_flash_attn uses when called with nsplit = 0. The launch is planned per
+ * call: the block layout (two or four 32-query tasks per block) and the split that together
+ * minimise an estimate from measured per-step costs; MI355X_FA_TASKS=2|4 in the environment pins
+ * the layout (for tests). The result does not depend on the layout beyond fp32 summation order. */
 MI355X_API int mi355x_flash_attn_auto_split(const mi355x_fa_args * a);
 
-/* Workspace bytes for `nsplit` KV splits (0 = auto): V transposed into [HK][DV][KV rounded up to
- * 64], the per-tile mask classes, the split-merge counters and, for nsplit > 1, the partial
- * outputs. Always non-zero for a valid op; the workspace must be 256-byte aligned. */
+/* Workspace bytes for `nsplit` KV splits (0 = auto): the per-tile mask classes, 16 zero bytes
+ * (the source of zero-padded head dims) and, for nsplit > 1, the partial outputs and their
+ * (max, sum). Always non-zero for a valid op; the workspace must be 256-byte aligned. */
 MI355X_API size_t mi355x_flash_attn_workspace(const mi355x_fa_args * a, int nsplit);
 
 /* dst = softmax(cap(scale * q.k) + mask) . v for every (token, head); head h reads KV head
- * h / (H / HK). Two kernels on `stream`: a prep pass over V and the mask, then the attention.
+ * h / (H / HK). On `stream`: a prep pass over the mask, the attention, and for a KV split a
+ * launch that merges the splits.
  * Concurrent calls must not share a workspace. D and DV up to 256, multiples of 8 (the kernels
  * are built for (64, 64), (128, 128), the MLA (192, 128) and (256, 256); other dims run
  * zero-padded on the smallest that holds them); H % HK == 0; max_bias
