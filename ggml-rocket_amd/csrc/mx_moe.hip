@@ -28,8 +28,7 @@ constexpr int MOE_BN = 128;           // output columns per block: 4 waves x 32
 constexpr int MOE_BK = 64;
 constexpr int MOE_THREADS = 256;
 constexpr int MOE_A_BYTES = MOE_BM * MOE_BK * 2;   // 8 KiB
-constexpr int MOE_B_BYTES = MOE_BN * MOE_BK * 2;   // 16 KiB
-constexpr int MOE_STAGE = MOE_A_BYTES + MOE_B_BYTES;   // two stages: 48 KiB, three blocks per CU
+constexpr int MOE_STAGE = MOE_A_BYTES;   // the activation slab only: the weights go to registers
 constexpr int MOE_SORT_THREADS = 1024;
 
 // ---------------------------------------------------------------------------------------------
@@ -117,20 +116,20 @@ __global__ void __launch_bounds__(MOE_SORT_THREADS) moe_sort_kernel(MoeArgs a) {
 // grouped expert GEMM
 // ---------------------------------------------------------------------------------------------
 // Block = (tile of MOE_BM rows of one expert, MOE_BN output columns); wave w owns columns
-// w*32 .. w*32+31 of the block for all MOE_BM rows (2 MFMA tiles of 32x32). Threads 2n and 2n+1
-// stage the two 32-value halves of weight row n0 + n (decoded to fp16 on their way into LDS, as
-// in the dense register-staged GEMM), and every thread two 16-byte chunks of the tile's
-// gathered activation rows; loads run R K slabs ahead of the MFMAs, so an HBM round trip has
-// R - 1 slabs of work to hide behind before its data is decoded. The slab loop is bound by the
-// per-slab chain of load, decode, LDS store, barrier and MFMA (a decode with a third of the
-// VALU instructions ran at the same speed, as did four register stages); 128-column blocks fit
-// three to a CU (48 KiB of LDS each), so 768 of them (128 experts x 6 column blocks of a 768-wide gate/up)
-// are one even round over 256 CUs, where 256-column blocks left half the CUs with double work.
-// Two register stages for every type: one block per CU (one wave per SIMD) with 4 stages of
-// Q4_K lookahead ran at the same speed as with 2, so the slabs are not waiting on memory.
+// w*32 .. w*32+31 of the block for all MOE_BM rows (2 MFMA tiles of 32x32, one where the tile has
+// 32 rows or fewer). Lane l of wave w loads and decodes one 32-value half (l / 32) of weight row
+// n0 + 32 w + l % 32 per 64-deep K slab straight into its MFMA B operand: the decoder yields the
+// half as four runs of 8 consecutive k, and MFMA step i takes run i, so lane l's B slots of step
+// i hold those 8 k and its A slots read the same 8 k of its activation row from LDS (the order in
+// which K enters the MFMAs is free as long as both operands follow it; the two halves together
+// are the slab's 64 k). The weights never pass through LDS; the tile's gathered activation rows
+// do (every thread stages two 16-byte chunks), double-buffered, one barrier per slab. Loads run R
+// K slabs ahead of the MFMAs, so an HBM round trip has R - 1 slabs of work to hide behind before
+// its data is decoded. 128-column blocks: 768 of them (128 experts x 6 column blocks of a
+// 768-wide gate/up) are one round of three blocks per CU over 256 CUs.
 // Register stages of slab lookahead: four where they fit in the three-wave register budget
-// without spilling, three for the formats whose stage is wider (F16, Q6_K).
-template <int WT> constexpr int moe_stages() { return (WT == T_F16 || WT == T_Q6_K) ? 3 : 4; }
+// without spilling, three for the formats whose stage is wider (F16, Q5_K, Q6_K).
+template <int WT> constexpr int moe_stages() { return (WT == T_F16 || WT == T_Q6_K || WT == T_Q5_K) ? 3 : 4; }
 
 template <int WT>
 __global__ void __launch_bounds__(MOE_THREADS) __attribute__((amdgpu_waves_per_eu(3, 3)))
@@ -175,7 +174,8 @@ moe_gemm_kernel(MoeArgs a) {
     const int n0 = nt * MOE_BN;
     const uint8_t * W = (const uint8_t *)a.w;
     const int64_t rows_total = (int64_t)a.E * a.N;
-    const int wr = t / 2, wu = t % 2;   // this thread's weight row in the block, and its half
+    const int lr = lane % 32, lg = lane / 32;
+    const int wr = wave * 32 + lr, wu = lg;   // this lane's weight row (output column) in the block, and its half
     const int64_t wrow = (int64_t)e * a.N + min(n0 + wr, a.N - 1);   // clamped: loads are unconditional
     const bool wok = n0 + wr < a.N;
     // A: thread t stages rows t / 8 and 32 + t / 8, chunk t % 8
@@ -208,32 +208,33 @@ moe_gemm_kernel(MoeArgs a) {
         g.a1 = load_a(arow1, k0, g.ok1);
         g.w.load(W, rows_total, K, wrow, k0, wu, wok);
     };
+    // the lane's B operand of the next slab to multiply (four runs of 8 fp16 weights) and the
+    // slab's 8-k chunk each run holds
+    u32x4 bq[4];
+    int kc[4];
     auto store = [&](uint8_t * st, const Stage & g) {
         const u32x4 z = {0, 0, 0, 0};
         *(u32x4 *)(st + swz<8>(ar, ac)) = g.ok0 ? g.a0 : z;
         *(u32x4 *)(st + swz<8>(ar + 32, ac)) = g.ok1 ? g.a1 : z;
-        uint8_t * bs = st + MOE_A_BYTES;
-        u32x4 o[4];
         int r0, r1;
-        g.w.decode_fast(wu, o, r0, r1);
-        *(u32x4 *)(bs + swz<8>(wr, r0 / 8)) = o[0];
-        *(u32x4 *)(bs + swz<8>(wr, r0 / 8 + 1)) = o[1];
-        *(u32x4 *)(bs + swz<8>(wr, r1 / 8)) = o[2];
-        *(u32x4 *)(bs + swz<8>(wr, r1 / 8 + 1)) = o[3];
+        g.w.decode_fast(wu, bq, r0, r1);
+        kc[0] = r0 / 8;
+        kc[1] = r0 / 8 + 1;
+        kc[2] = r1 / 8;
+        kc[3] = r1 / 8 + 1;
     };
 
-    const int lr = lane % 32, lg = lane / 32;
+    const bool two = rows_here > 32;   // block-uniform: the second 32-row MFMA tile has real rows
     auto mma = [&](const uint8_t * st) {
-        const uint8_t * Bs = st + MOE_A_BYTES;
 #pragma unroll
         for (int ks = 0; ks < MOE_BK / 16; ks++) {
-            const int c = 2 * ks + lg;
-            half8 af[2];
-#pragma unroll
-            for (int i = 0; i < 2; i++) af[i] = *(const half8 *)(st + swz<8>(i * 32 + lr, c));
-            const half8 bf = *(const half8 *)(Bs + swz<8>(wave * 32 + lr, c));
-#pragma unroll
-            for (int i = 0; i < 2; i++) acc[i] = mfma32(af[i], bf, acc[i]);
+            const half8 bf = __builtin_bit_cast(half8, bq[ks]);
+            const half8 a0 = *(const half8 *)(st + swz<8>(lr, kc[ks]));
+            acc[0] = mfma32(a0, bf, acc[0]);
+            if (two) {
+                const half8 a1 = *(const half8 *)(st + swz<8>(32 + lr, kc[ks]));
+                acc[1] = mfma32(a1, bf, acc[1]);
+            }
         }
     };
 
