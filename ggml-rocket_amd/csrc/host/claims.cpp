@@ -8,7 +8,7 @@
 //     BF16 accumulator declaration is met (the NPU route could not, 7372-7380);
 //   * the weight types: the device decodes F16, F32, BF16, Q4_0, Q8_0, Q4_K, Q5_K, Q6_K and MXFP4; other ggml quant
 //     types are declined rather than claimed and then computed on the host;
-//   * FLASH_ATTN_EXT: head dims up to 256, and the strides the kernel reads.
+//   * FLASH_ATTN_EXT: head dims up to 1024 (dk % 32, dv % 8), and the strides the kernels read.
 
 #include <atomic>
 #include <map>
@@ -438,10 +438,13 @@ static bool claim_flash_attn(const mi355x_tensor * op) {
         && n_tokens >= flash_attn_min_t()
         && n_kv >= flash_attn_min_kv();
     if (!ref_rules) return false;
-    // what the kernel reads: head dims it holds zero-padded (dk, dv <= 256; the kernels are
-    // built for 64/64, 128/128, the MLA 192/128 and 256/256); element strides; 16-byte rows
+    // what the kernels read: head dims the fused kernel holds zero-padded (dk, dv <= 256; built
+    // for 64/64, 128/128, the MLA 192/128 and 256/256) or, past those, the two-GEMM path (dk % 32
+    // == 0, dv % 8 == 0, both up to 1024: the absorbed MLA's 576 / 512); element strides;
+    // 16-byte rows
     int dk_pad = 0, dv_pad = 0;
-    const bool dims = head_dim <= 256 && dv <= 256 && mx::fa_pad_dims((int)head_dim, (int)dv, dk_pad, dv_pad);
+    const bool dims = (head_dim <= 256 && dv <= 256 && mx::fa_pad_dims((int)head_dim, (int)dv, dk_pad, dv_pad)) ||
+                      mx::fa_wide_dims((int)head_dim, (int)dv);
     const bool q_ok = q->nb[0] == 4 && q->nb[1] % 16 == 0 && q->nb[2] % 16 == 0;
     const bool kv_ok = k->nb[0] == 2 && v->nb[0] == 2 && k->nb[1] % 16 == 0 && k->nb[2] % 16 == 0 &&
                        v->nb[1] % 16 == 0 && v->nb[2] % 16 == 0;

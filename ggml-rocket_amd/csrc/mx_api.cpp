@@ -276,9 +276,18 @@ MI355X_API int mi355x_mul_mat(int wtype, const void * w_dev, int64_t N, int64_t 
 
 // ---- FLASH_ATTN_EXT ---------------------------------------------------------------------------
 
+// Head dims past the fused kernel's builds (dk or dv > 256): two GEMMs around a softmax pass
+// (mx_fa_wide.hip).
+static bool fa_is_wide(const mi355x_fa_args * a) {
+    return !mx::fa_dims_supported(a->D, a->DV) && mx::fa_wide_dims(a->D, a->DV);
+}
+static constexpr int64_t FA_WIDE_MAX_KV = 1 << 20;
+
 static int fa_check(const mi355x_fa_args * a) {
     if (!a || !a->q_dev || !a->k_dev || !a->v_dev || !a->dst_dev) return MI355X_E_ARG;
-    if (!mx::fa_dims_supported(a->D, a->DV)) return MI355X_E_UNSUPPORTED;   // dk, dv <= 256, multiples of 8
+    const bool wide = fa_is_wide(a);
+    // dk, dv <= 256, multiples of 8 (fused kernel); else dk % 32 == 0, dv % 8 == 0 up to 1024
+    if (!wide && !mx::fa_dims_supported(a->D, a->DV)) return MI355X_E_UNSUPPORTED;
     if (a->max_bias != 0.0f) return MI355X_E_UNSUPPORTED;
     if (a->T < 0 || a->H <= 0 || a->HK <= 0 || a->KV < 0 || a->H % a->HK) return MI355X_E_ARG;
     if (a->q_nb1 % 4 || a->q_nb2 % 4 || !aligned(a->q_dev, 16)) return MI355X_E_ARG;
@@ -286,8 +295,34 @@ static int fa_check(const mi355x_fa_args * a) {
     if (!aligned(a->k_dev, 16) || !aligned(a->v_dev, 16)) return MI355X_E_ARG;
     if (a->dst_nb1 % 4 || a->dst_nb2 % 4 || !aligned(a->dst_dev, 16)) return MI355X_E_ARG;
     if (a->mask_dev && (a->mask_nb1 % 4 || a->mask_nb1 < a->KV || !aligned(a->mask_dev, 8))) return MI355X_E_ARG;
-    if ((size_t)a->KV > mx::fa_max_kv(a->D, a->DV)) return MI355X_E_UNSUPPORTED;
+    if (wide ? (int64_t)a->KV > FA_WIDE_MAX_KV : (size_t)a->KV > mx::fa_max_kv(a->D, a->DV)) return MI355X_E_UNSUPPORTED;
     return MI355X_OK;
+}
+
+// Workspace of the wide path: fp16 queries and their row scales, one KV head's keys and
+// transposed values, and one chunk of query rows' scores, fp16 P, 1 / row sums and output rows.
+struct FaWideLayout {
+    size_t q16, qsc, kc, vt, s, p16, psc, o, total;
+    int kvp, rows_chunk;
+};
+static size_t up256_fa(size_t n) { return (n + 255) & ~(size_t)255; }
+static FaWideLayout fa_wide_layout(const mi355x_fa_args * a) {
+    FaWideLayout L;
+    L.kvp = (int)((a->KV + 63) / 64 * 64);
+    if (L.kvp == 0) L.kvp = 64;
+    L.rows_chunk = mx::fa_wide_rows_chunk(a->T, a->H, a->HK, L.kvp);
+    const size_t rows = (size_t)a->H * a->T, rc = (size_t)L.rows_chunk, kvp = (size_t)L.kvp;
+    size_t o = 0;
+    L.q16 = o;  o += up256_fa(rows * a->D * 2);
+    L.qsc = o;  o += up256_fa(rows * 4);
+    L.kc = o;   o += up256_fa(kvp * a->D * 2);
+    L.vt = o;   o += up256_fa((size_t)a->DV * kvp * 2);
+    L.s = o;    o += up256_fa(rc * kvp * 4);
+    L.p16 = o;  o += up256_fa(rc * kvp * 2);
+    L.psc = o;  o += up256_fa(rc * 4);
+    L.o = o;    o += up256_fa(rc * a->DV * 4);
+    L.total = o;
+    return L;
 }
 
 static mx::FaArgs fa_lower(const mi355x_fa_args * a, int nsplit) {
@@ -382,12 +417,13 @@ static FaPlan fa_plan(const mi355x_fa_args * a, int nsplit_req) {
 }
 
 MI355X_API int mi355x_flash_attn_auto_split(const mi355x_fa_args * a) {
-    if (fa_check(a) != MI355X_OK) return 1;
+    if (fa_check(a) != MI355X_OK || fa_is_wide(a)) return 1;
     return fa_plan(a, 0).nsplit;
 }
 
 MI355X_API size_t mi355x_flash_attn_workspace(const mi355x_fa_args * a, int nsplit) {
     if (fa_check(a) != MI355X_OK) return 0;
+    if (fa_is_wide(a)) return fa_wide_layout(a).total;   // no KV split on this path
     if (nsplit <= 0) nsplit = fa_plan(a, 0).nsplit;
     if (nsplit > 64) return 0;
     return fa_layout(fa_lower(a, nsplit)).total;
@@ -398,6 +434,25 @@ MI355X_API int mi355x_flash_attn(const mi355x_fa_args * a, int nsplit,
     const int st = fa_check(a);
     if (st != MI355X_OK) return st;
     if (a->T == 0) return MI355X_OK;
+    if (fa_is_wide(a)) {
+        const FaWideLayout L = fa_wide_layout(a);
+        if (!workspace_dev || workspace_bytes < L.total || !aligned(workspace_dev, 256)) return MI355X_E_NOMEM;
+        char * ws = (char *)workspace_dev;
+        mx::FaWideArgs w;
+        memset(&w, 0, sizeof(w));
+        w.q = a->q_dev; w.k = a->k_dev; w.v = a->v_dev; w.mask = a->mask_dev; w.dst = a->dst_dev;
+        w.q_nb1 = a->q_nb1; w.q_nb2 = a->q_nb2; w.k_nb1 = a->k_nb1; w.k_nb2 = a->k_nb2;
+        w.v_nb1 = a->v_nb1; w.v_nb2 = a->v_nb2; w.mask_nb1 = a->mask_nb1;
+        w.dst_nb1 = a->dst_nb1; w.dst_nb2 = a->dst_nb2;
+        w.dk = a->D; w.dv = a->DV; w.T = a->T; w.H = a->H; w.HK = a->HK; w.KV = a->KV;
+        w.kvp = L.kvp; w.rows_chunk = L.rows_chunk;
+        w.scale = a->scale; w.softcap = a->softcap;
+        w.q16 = (uint16_t *)(ws + L.q16); w.qsc = (float *)(ws + L.qsc);
+        w.kc = (uint16_t *)(ws + L.kc); w.vt = (uint16_t *)(ws + L.vt);
+        w.s = (float *)(ws + L.s); w.p16 = (uint16_t *)(ws + L.p16);
+        w.psc = (float *)(ws + L.psc); w.o = (float *)(ws + L.o);
+        return hip_status(mx::launch_fa_wide(w, S(stream)));
+    }
     if (nsplit > 64) return MI355X_E_ARG;
     const FaPlan plan = fa_plan(a, nsplit);
     mx::FaArgs f = fa_lower(a, plan.nsplit);

@@ -20,4 +20,10 @@ inline bool fa_pad_dims(int dk, int dv, int & D, int & DV) {
     return false;
 }
 
+// Head dims past those builds (the absorbed MLA's 576 / 512) run as two GEMMs around a softmax
+// pass (mx_fa_wide.hip): dk % 32 == 0 (the Q.K GEMM's depth), dv % 8 == 0, both up to 1024.
+inline bool fa_wide_dims(int dk, int dv) {
+    return dk > 0 && dv > 0 && dk % 32 == 0 && dv % 8 == 0 && dk <= 1024 && dv <= 1024;
+}
+
 }  // namespace mx

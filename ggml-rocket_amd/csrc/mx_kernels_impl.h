@@ -56,6 +56,30 @@ struct FaArgs {
     float scale, softcap;
 };
 
+// FLASH_ATTN_EXT with head dims past 256 (two GEMMs around a softmax pass): strides in
+// elements as in FaArgs; scratch pointers carved from the caller's workspace.
+struct FaWideArgs {
+    const float * q;
+    const uint16_t * k;
+    const uint16_t * v;
+    const uint16_t * mask;
+    float * dst;
+    int64_t q_nb1, q_nb2, k_nb1, k_nb2, v_nb1, v_nb2, mask_nb1, dst_nb1, dst_nb2;
+    int dk, dv, T, H, HK, KV, kvp, rows_chunk;   // kvp: KV rounded up to 64
+    float scale, softcap;
+    uint16_t * q16;            // [HK][H/HK * T][dk] fp16 queries, rows (local head, token)
+    float * qsc;               // their row scales
+    uint16_t * kc;             // [kvp][dk] one KV head's keys, rows past KV zero
+    uint16_t * vt;             // [dv][kvp] its values transposed, columns past KV zero
+    float * s;                 // [rows_chunk][kvp] scores of a chunk of query rows
+    uint16_t * p16;            // [rows_chunk][kvp] fp16 P
+    float * psc;               // [rows_chunk] 1 / row sum of P
+    float * o;                 // [rows_chunk][dv] normalised output rows
+};
+
+int fa_wide_rows_chunk(int T, int H, int HK, int kvp);    // query rows per chunk
+hipError_t launch_fa_wide(const FaWideArgs & a, hipStream_t st);
+
 // MUL_MAT_ID launch: strides in elements; scratch pointers carved from the caller's workspace.
 struct MoeArgs {
     const void * w;            // expert panel, E*N rows of K, HBM layout

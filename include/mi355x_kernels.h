@@ -226,15 +226,19 @@ MI355X_API int mi355x_flash_attn_auto_split(const mi355x_fa_args * a);
 
 /* Workspace bytes for `nsplit` KV splits (0 = auto): the per-tile mask classes, 16 zero bytes
  * (the source of zero-padded head dims) and, for nsplit > 1, the partial outputs and their
- * (max, sum). Always non-zero for a valid op; the workspace must be 256-byte aligned. */
+ * (max, sum); for head dims past 256, the fp16 queries, one KV head's keys and transposed
+ * values, and a chunk of query rows' scores and fp16 P (at most 64 MiB of F32 scores). Always
+ * non-zero for a valid op; the workspace must be 256-byte aligned. */
 MI355X_API size_t mi355x_flash_attn_workspace(const mi355x_fa_args * a, int nsplit);
 
 /* dst = softmax(cap(scale * q.k) + mask) . v for every (token, head); head h reads KV head
  * h / (H / HK). On `stream`: a prep pass over the mask, the attention, and for a KV split a
  * launch that merges the splits.
- * Concurrent calls must not share a workspace. D and DV up to 256, multiples of 8 (the kernels
- * are built for (64, 64), (128, 128), the MLA (192, 128) and (256, 256); other dims run
- * zero-padded on the smallest that holds them); H % HK == 0; max_bias
+ * Concurrent calls must not share a workspace. D and DV up to 256, multiples of 8, run fused (the
+ * kernels are built for (64, 64), (128, 128), the MLA (192, 128) and (256, 256); other dims run
+ * zero-padded on the smallest that holds them); past 256 (the absorbed MLA's 576 / 512: D % 32
+ * == 0, DV % 8 == 0, both up to 1024) as two GEMMs around a softmax pass over a bounded chunk
+ * of query rows at a time, with no KV split; H % HK == 0; max_bias
  * must be 0 (no ALiBi); the mask
  * covers [T][KV] with mask_nb1 % 4 == 0; q rows and dst rows 16-byte aligned; k/v rows 16-byte
  * aligned. Rows whose every key is masked are written as zeros. Replaces

@@ -206,6 +206,33 @@ def test_flash_attn_mla_graph(be):
     assert r["nonfinite"] == 0 and r["max_abs"] <= 2e-2 and r["range_err"] <= 1e-2
 
 
+def test_flash_attn_absorbed_mla_graph(be):
+    """The absorbed MLA's FLASH_ATTN_EXT through graph_compute: keys of 576, values of 512 as a view
+    of the keys' first 512 dims (the latent cache read twice), 16 query heads on one KV head, causal
+    at n_kv 1024; claimed and run on the device (the two-GEMM path), no CPU fallback."""
+    D, DV, T, H, KV, HK = 576, 512, 96, 16, 1024, 1
+    Q = O.fill_normal((H, T, D), 970)
+    K16 = O.f32_to_f16_bits(O.fill_normal((HK, KV, D), 971))
+    V16 = np.ascontiguousarray(K16[:, :, :DV])
+    M16 = O.f32_to_f16_bits(causal_mask(T, KV))
+    scale = float(np.float32(1.0) / np.sqrt(np.float32(D)))
+    want = O.flash_attn(Q, K16, V16, M16, scale)
+    g = mx.Graph()
+    q = g.new_tensor(mx.F32, [D, T, H])
+    k = g.new_tensor(mx.F16, [D, KV, HK])
+    v = g.permute_view(k, [DV, KV, HK, 1], [2, k.nb[1], k.nb[2], k.nb[3]])
+    m = g.new_tensor(mx.F16, [KV, T])
+    g.set(q, Q), g.set(k, K16), g.set(m, M16)
+    o = g.flash_attn_ext(q, k, v, m, scale)
+    mk = Mark(be, "fa")
+    assert be.compute([o]) == mx.STATUS_SUCCESS
+    mk.check("absorbed mla")
+    got = g.get(o, np.float32, (T, H, DV))
+    r = compare(want, got)
+    print(f"absorbed MLA graph: {r}")
+    assert r["nonfinite"] == 0 and r["max_abs"] <= 2e-2 and r["range_err"] <= 1e-2
+
+
 def _moe_graph(g, wt, K, N, E, ne11, U, T, payload, X, ids, name):
     a = g.new_tensor(wt, [K, N, E], name)
     b = g.new_tensor(mx.F32, [K, ne11, T])

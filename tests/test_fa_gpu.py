@@ -224,3 +224,63 @@ def test_fa_padded_head_dims(mx, D, DV, softcap):
         r = compare(want, got)
         print(f"padded D={D} DV={DV} softcap={softcap} nsplit={ns}: {r}")
         assert r["nonfinite"] == 0 and r["max_abs"] <= 2e-2 and r["range_err"] <= 1e-2, (ns, r)
+
+
+@pytest.mark.parametrize("D,DV,H,HK,softcap", [(576, 512, 16, 1, 0.0), (576, 512, 8, 1, 30.0), (320, 264, 8, 2, 0.0),
+                                               (288, 128, 8, 4, 0.0), (128, 512, 4, 1, 0.0)])
+def test_fa_wide_head_dims(mx, D, DV, H, HK, softcap):
+    """Head dims past 256 (the absorbed MLA's 576 / 512, and any dk % 32 == 0, dv % 8 == 0 up to
+    1024) run as two GEMMs around a softmax pass: causal mask with holes and a fully masked row,
+    ragged T and n_kv, output columns past dv untouched (NaN-filled output with a wider row)."""
+    import torch
+    T, KV = 70, 389
+    Q = O.fill_normal((H, T, D), 1990 + D)
+    K16 = O.f32_to_f16_bits(O.fill_normal((HK, KV, D), 1991 + D))
+    V16 = O.f32_to_f16_bits(O.fill_normal((HK, KV, DV), 1992 + DV))
+    M = np.full((T, 392), 7.0, np.float32)
+    M[:, :KV] = causal_mask(T, KV)
+    rnd = O.fill_uniform((T, KV), 1993, 1.0)
+    M[:, :KV][rnd > 0.8] = -np.inf
+    M[5, :] = -np.inf
+    M16 = O.f32_to_f16_bits(M)
+    scale = float(np.float32(1.0) / np.sqrt(np.float32(D)))
+    want = O.flash_attn(Q, K16, V16, M16, scale, softcap=softcap)
+    q = torch.from_numpy(Q).cuda()
+    k = torch.from_numpy(K16.view(np.float16)).cuda()
+    v = torch.from_numpy(V16.view(np.float16)).cuda()
+    m = torch.from_numpy(M16.view(np.float16)).cuda()
+    wide = torch.full((T, H, DV + 16), float("nan"), dtype=torch.float32, device="cuda")
+    out = wide[:, :, :DV]
+    mx.flash_attn(q, k, v, m, scale, softcap=softcap, out=out)
+    torch.cuda.synchronize()
+    w = wide.cpu().numpy()
+    assert np.isnan(w[:, :, DV:]).all(), "wrote past dv"
+    got = w[:, :, :DV]
+    assert np.all(got[5] == 0.0)
+    r = compare(want, got)
+    print(f"wide D={D} DV={DV} H={H} HK={HK} softcap={softcap}: {r}")
+    assert r["nonfinite"] == 0 and r["max_abs"] <= 2e-2 and r["range_err"] <= 1e-2, r
+
+
+def test_fa_wide_mla_prefill_chunked(mx):
+    """The absorbed-MLA shape at prefill size, 16 query heads on one KV head, 512 queries over 4100
+    keys (causal, last 512 positions): the 8192 query rows take three chunks of the scores'
+    workspace slab; sampled tokens against the oracle."""
+    import torch
+    H, HK, T, KV, D, DV = 16, 1, 512, 4100, 576, 512
+    Q = O.fill_normal((H, T, D), 2990)
+    K16 = O.f32_to_f16_bits(O.fill_normal((HK, KV, D), 2991))
+    V16 = O.f32_to_f16_bits(O.fill_normal((HK, KV, DV), 2992))
+    M = causal_mask(T, KV)
+    M16 = O.f32_to_f16_bits(M)
+    scale = float(np.float32(1.0) / np.sqrt(np.float32(D)))
+    q = torch.from_numpy(Q).cuda()
+    k = torch.from_numpy(K16.view(np.float16)).cuda()
+    v = torch.from_numpy(V16.view(np.float16)).cuda()
+    m = torch.from_numpy(M16.view(np.float16)).cuda()
+    got = mx.flash_attn(q, k, v, m, scale).cpu().numpy()
+    idx = np.array([0, 1, 137, 255, 256, 400, 510, 511])
+    want = O.flash_attn(np.ascontiguousarray(Q[:, idx, :]), K16, V16, np.ascontiguousarray(M16[idx, :]), scale)
+    r = compare(want, got[idx])
+    print(f"wide MLA prefill sampled rows: {r}")
+    assert r["nonfinite"] == 0 and r["max_abs"] <= 2e-2 and r["range_err"] <= 1e-2, r

@@ -64,9 +64,9 @@ CASES = [
     ("FA: head_dim%32 != 0 (48) -> CPU", False, lambda: fa_supported(48, 256, 8, 1024, 2, mx.F16, 0.0)),
     ("FA: K/V not F16 -> CPU", False, lambda: fa_supported(64, 256, 8, 1024, 2, mx.F32, 0.0)),
     ("FA: ALiBi (max_bias > 0) -> CPU", False, lambda: fa_supported(64, 256, 8, 1024, 2, mx.F16, 8.0)),
-    # Narrower than the reference: the kernels take dk and dv up to 256 (zero-padded onto the
-    # 64/64, 128/128, 192/128 and 256/256 builds); the reference takes any dk%32 / dv%16
-    # (ggml-rocket.cpp:7740-7760).
+    # The fused kernel takes dk and dv up to 256 (zero-padded onto the 64/64, 128/128, 192/128 and
+    # 256/256 builds), the two-GEMM path dk % 32 / dv % 8 up to 1024; the reference takes any
+    # dk%32 / dv%16 (ggml-rocket.cpp:7740-7760), so only head dims past 1024 are narrower.
     ("FA: head_dim 128 -> offload", True, lambda: fa_supported(128, 512, 32, 4096, 8, mx.F16, 0.0)),
     ("FA: head_dim 96 -> offload (padded to 128)", True, lambda: fa_supported(96, 256, 8, 1024, 2, mx.F16, 0.0)),
     ("FA: head_dim 32 -> offload (padded to 64)", True, lambda: fa_supported(32, 256, 8, 1024, 2, mx.F16, 0.0)),
@@ -75,8 +75,9 @@ CASES = [
     ("FA: dk 128 / dv 64 -> offload (dv padded to 128)", True, lambda: fa_supported(128, 256, 8, 1024, 2, mx.F16, 0.0, 0, 64)),
     ("FA: dk 192 / dv 192 -> offload (padded to 256)", True, lambda: fa_supported(192, 256, 8, 1024, 2, mx.F16, 0.0)),
     ("FA: head_dim 256 (Gemma) -> offload", True, lambda: fa_supported(256, 256, 8, 1024, 2, mx.F16, 0.0)),
-    ("FA: dk 576 / dv 512 (absorbed MLA) -> CPU", False, lambda: fa_supported(576, 256, 8, 1024, 1, mx.F16, 0.0, 0, 512)),
-    ("FA: head_dim 288 -> CPU (> 256)", False, lambda: fa_supported(288, 256, 8, 1024, 2, mx.F16, 0.0)),
+    ("FA: dk 576 / dv 512 (absorbed MLA) -> offload (two-GEMM path)", True, lambda: fa_supported(576, 256, 8, 1024, 1, mx.F16, 0.0, 0, 512)),
+    ("FA: head_dim 288 -> offload (two-GEMM path)", True, lambda: fa_supported(288, 256, 8, 1024, 2, mx.F16, 0.0)),
+    ("FA: head_dim 1056 -> CPU (> 1024)", False, lambda: fa_supported(1056, 256, 8, 1024, 2, mx.F16, 0.0)),
     # Narrower: a quantized type without a device decoder is declined (the reference takes any
     # type with a ggml to_float, 7452-7455).
     # a type with neither a device decoder nor a registered host one (the plugin registers
