@@ -765,6 +765,27 @@ def configs_bench(args, subset=False):
                {"tflops_causal_visible": round(visible / us / 1e6, 1)})
         del q, kc, vc, m, out, wsp
     torch.cuda.empty_cache()
+    # FLASH_ATTN_EXT with the absorbed MLA's head dims (DeepSeek-style: keys of 576, values the
+    # first 512 of them), 16 query heads on one KV head, 512 queries over 4096 keys, causal: the
+    # two-GEMM path for head dims past 256
+    T, H, HK, D, DV, n_kv = 512, 16, 1, 576, 512, 4096
+    q = torch.randn(T, H, D, device="cuda")
+    kc = torch.randn(n_kv, HK, D, device="cuda").half()
+    j = torch.arange(n_kv, device="cuda")[None, :]
+    t = torch.arange(T, device="cuda")[:, None]
+    m = torch.where(j > n_kv - T + t, float("-inf"), 0.0).half()
+    out = torch.empty(T, H, DV, device="cuda")
+    kview = kc.permute(1, 0, 2)
+    wsp = torch.empty(mx.flash_attn_workspace(q.permute(1, 0, 2), kview, kview[:, :, :DV], m, out) + 256,
+                      dtype=torch.uint8, device="cuda")
+    us = graph_time_us(lambda i: mx.flash_attn(q.permute(1, 0, 2), kview, kview[:, :, :DV], m, 1.0 / math.sqrt(D),
+                                               out=out, workspace=wsp), 8)
+    visible = 2.0 * H * (D + DV) * sum(n_kv - T + tt + 1 for tt in range(T))
+    record(f"FLASH_ATTN_EXT absorbed MLA 576/512 n_kv={n_kv}", us, 2.0 * H * T * n_kv * (D + DV),
+           T * H * D * 4 + HK * n_kv * D * 2 + T * n_kv * 2 + T * H * DV * 4,
+           {"tflops_causal_visible": round(visible / us / 1e6, 1)})
+    del q, kc, m, out, wsp
+    torch.cuda.empty_cache()
     if subset:
         return cases
     print(json.dumps({

@@ -247,6 +247,22 @@ def mul_mat_noalloc(wtype: int, w_dev, N: int, K: int, x, out):
                                         out.stride(0), stream_handle())
 
 
+def _fa_args(q, k, v, mask, out, scale, softcap=0.0, max_bias=0.0):
+    H, T, D = q.shape
+    HK, KV, DV = v.shape
+    return FaArgs(q.data_ptr(), q.stride(1), q.stride(0),
+                  k.data_ptr(), k.stride(1), k.stride(0),
+                  v.data_ptr(), v.stride(1), v.stride(0),
+                  mask.data_ptr() if mask is not None else None, mask.stride(0) if mask is not None else 0,
+                  out.data_ptr(), out.stride(1), out.stride(0),
+                  D, DV, T, H, KV, HK, scale, max_bias, softcap)
+
+
+def flash_attn_workspace(q, k, v, mask, out, scale: float = 1.0, softcap: float = 0.0, nsplit: int = 0) -> int:
+    """Workspace bytes mi355x_flash_attn needs for these operands (0 for an unsupported op)."""
+    return int(lib().mi355x_flash_attn_workspace(ctypes.byref(_fa_args(q, k, v, mask, out, scale, softcap)), nsplit))
+
+
 def flash_attn(q, k, v, mask, scale: float, softcap: float = 0.0, nsplit: int = 0, out=None,
                workspace=None, max_bias: float = 0.0):
     """q [H, T, D] f32 (any strides with unit last-dim stride), k/v [HK, KV, D] fp16, mask
@@ -256,12 +272,7 @@ def flash_attn(q, k, v, mask, scale: float, softcap: float = 0.0, nsplit: int = 
     HK, KV, DV = v.shape
     if out is None:
         out = torch.empty((T, H, DV), dtype=torch.float32, device=q.device)
-    a = FaArgs(q.data_ptr(), q.stride(1), q.stride(0),
-               k.data_ptr(), k.stride(1), k.stride(0),
-               v.data_ptr(), v.stride(1), v.stride(0),
-               mask.data_ptr() if mask is not None else None, mask.stride(0) if mask is not None else 0,
-               out.data_ptr(), out.stride(1), out.stride(0),
-               D, DV, T, H, KV, HK, scale, max_bias, softcap)
+    a = _fa_args(q, k, v, mask, out, scale, softcap, max_bias)
     need = int(lib().mi355x_flash_attn_workspace(ctypes.byref(a), nsplit))
     if need and (workspace is None or workspace.numel() < need):
         workspace = torch.empty(need, dtype=torch.uint8, device=q.device)
