@@ -815,7 +815,8 @@ def moe_bench(args):
     tot_us = tot_bytes = 0.0
     for i, (name, N, K, ne11) in enumerate((("gate/up", FF, DM, 1), ("down", DM, FF, U))):
         P = synth_q4k(E * N, K, 0x5EED0000 + 65 + i)
-        copies = [mx.upload_weight(mx.Q4_K, P, E * N, K) for _ in range(3)]
+        # the layout the backend caches Q4_K expert stacks in (Q4_K regrouped by 32 rows)
+        copies = [mx.upload_weight(mx.Q4_K_X, P, E * N, K) for _ in range(3)]
         X = torch.randn(T, ne11, K, device="cuda")
         out = torch.empty(T, U, N, device="cuda")
         ws = torch.empty(1 << 26, dtype=torch.uint8, device="cuda")
@@ -824,7 +825,7 @@ def moe_bench(args):
         def run():
             w = copies[cyc[0] % 3]
             cyc[0] += 1
-            mx.mul_mat_id(mx.Q4_K, w, E, N, K, X, idt, out=out, workspace=ws)
+            mx.mul_mat_id(mx.Q4_K_X, w, E, N, K, X, idt, out=out, workspace=ws)
         for _ in range(3):
             run()
         torch.cuda.synchronize()

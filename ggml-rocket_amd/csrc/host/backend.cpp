@@ -482,6 +482,7 @@ int build_weight(Ctx * c, int t, const void * src, int64_t rows, int64_t K, int 
         TRY(mi355x_convert_f16(t, c->wstage.p, rows * K, (uint16_t *)c->wconv.p, c->stream));
         return mi355x_weight_f16_tiled(MI355X_F16, c->wconv.p, rows, K, (uint16_t *)dst, c->stream);
     }
+    if (lay == MI355X_Q4_K_X) return mi355x_weight_pack(lay, c->wstage.p, rows, K, dst, c->stream);
     if (lay != MI355X_F16 && lay != MI355X_F16_T) return mi355x_weight_pack(t, c->wstage.p, rows, K, dst, c->stream);
     // -> fp16: from the HBM layout, built first when that differs from the ggml one
     const void * q = c->wstage.p;
@@ -496,9 +497,13 @@ int build_weight(Ctx * c, int t, const void * src, int64_t rows, int64_t K, int 
 
 // A weight in device form: from the cache, or built into it, or (no key / over budget) built
 // into per-call scratch. `resident` tells which.
-int get_weight(Ctx * c, const mi355x_tensor * a, int64_t rows, int64_t K, bool want_f16, bool tiled_ok, bool moe,
-               DevBuf & scratch, WEntry & out, bool & resident) {
-    const int lay = dev_layout(a->type, want_f16, tiled_ok, K);
+int get_weight(Ctx * c, const mi355x_tensor * a, int64_t rows, int64_t K, bool want_f16, bool tiled_ok,
+               int64_t moe_n, DevBuf & scratch, WEntry & out, bool & resident) {
+    const bool moe = moe_n > 0;   // an expert stack of experts with moe_n rows each
+    int lay = dev_layout(a->type, want_f16, tiled_ok, K);
+    // Q4_K experts of whole 32-row groups take the regrouped layout, whose 32-row slabs the
+    // expert GEMM loads as contiguous bytes
+    if (moe && lay == MI355X_Q4_K && moe_n % 32 == 0) lay = MI355X_Q4_K_X;
     const int64_t dbytes = mi355x_weight_bytes(lay, rows, K);
     if (dbytes < 0) return MI355X_E_ARG;
     CacheOutcome & oc = c->outcome[moe ? USE_MOE : (lay == MI355X_F16 || lay == MI355X_F16_T) ? USE_F16 : USE_QUANT];
@@ -583,7 +588,7 @@ int mul_mat_device(Ctx * c, const std::vector<mi355x_tensor *> & grp, bool want_
     for (size_t i = 0; i < grp.size(); i++) {
         const mi355x_tensor * a = grp[i]->src[0];
         bool res = false;
-        TRY(get_weight(c, a, a->ne[1], K, want_f16, true, false, c->wscratch[i], ws[i], res));
+        TRY(get_weight(c, a, a->ne[1], K, want_f16, true, 0, c->wscratch[i], ws[i], res));
         all_resident = all_resident && res;
         outs[i].w_dev = ws[i].dev;
         outs[i].rows_total = a->ne[1];
@@ -723,7 +728,7 @@ int mul_mat_id_device(Ctx * c, mi355x_tensor * dst, bool & resident) {
     panel.ne[1] = N * E;
     panel.ne[2] = 1;
     WEntry w;
-    TRY(get_weight(c, &panel, N * E, K, false, false, true, c->moe_wscratch, w, resident));
+    TRY(get_weight(c, &panel, N * E, K, false, false, N, c->moe_wscratch, w, resident));
     const size_t bb = (size_t)T * ne11 * K * 4, ib = (size_t)T * U * 4, ob = (size_t)T * U * N * 4;
     TRY(c->moe_b.ensure(bb));
     TRY(c->moe_ids.ensure(ib));

@@ -297,6 +297,29 @@ moe_gemm_kernel(MoeArgs a) {
         }
 }
 
+// ggml Q4_K blocks -> T_Q4_KX: one thread per 16-byte chunk of a source block (the header, then
+// eight chunks of nibbles: quarter (c - 1) / 2, half (c - 1) % 2).
+__global__ void __launch_bounds__(256) pack_q4kx_kernel(const uint8_t * __restrict__ src, int64_t rows, int64_t nblk,
+                                                        uint8_t * __restrict__ dst) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= rows * nblk * 9) return;
+    const int c = (int)(i % 9);
+    const int64_t rb = i / 9, row = rb / nblk, blk = rb % nblk;
+    const u32x4 v = *(const u32x4 *)(src + rb * 144 + 16 * c);
+    uint8_t * b = dst + q4kx_block(row, blk, nblk);
+    const int r = (int)(row % Q4KX_GROUP);
+    uint8_t * d = c == 0 ? b + 16 * r : b + 16 * Q4KX_GROUP + 32 * Q4KX_GROUP * ((c - 1) / 2) + 32 * r + 16 * ((c - 1) % 2);
+    *(u32x4 *)d = v;
+}
+
+hipError_t launch_pack_q4kx(const void * src, int64_t rows, int64_t K, void * dst, hipStream_t st) {
+    const int64_t n = rows * (K / 256) * 9;
+    if (n <= 0) return hipSuccess;
+    hipLaunchKernelGGL(pack_q4kx_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, (const uint8_t *)src, rows,
+                       K / 256, (uint8_t *)dst);
+    return hipGetLastError();
+}
+
 int moe_max_tiles(int T, int U, int E) { return (T * U + MOE_BM - 1) / MOE_BM + E; }
 
 hipError_t launch_moe(int wt, const MoeArgs & a, hipStream_t st) {
@@ -318,6 +341,7 @@ hipError_t launch_moe(int wt, const MoeArgs & a, hipStream_t st) {
         case T_Q4_0: hipLaunchKernelGGL(moe_gemm_kernel<T_Q4_0>, dim3((unsigned)nb), dim3(MOE_THREADS), lds, st, a); break;
         case T_Q5_K: hipLaunchKernelGGL(moe_gemm_kernel<T_Q5_K>, dim3((unsigned)nb), dim3(MOE_THREADS), lds, st, a); break;
         case T_Q4_K: hipLaunchKernelGGL(moe_gemm_kernel<T_Q4_K>, dim3((unsigned)nb), dim3(MOE_THREADS), lds, st, a); break;
+        case T_Q4_KX: hipLaunchKernelGGL(moe_gemm_kernel<T_Q4_KX>, dim3((unsigned)nb), dim3(MOE_THREADS), lds, st, a); break;
         case T_Q6_K: hipLaunchKernelGGL(moe_gemm_kernel<T_Q6_K>, dim3((unsigned)nb), dim3(MOE_THREADS), lds, st, a); break;
         case T_MXFP4: hipLaunchKernelGGL(moe_gemm_kernel<T_MXFP4>, dim3((unsigned)nb), dim3(MOE_THREADS), lds, st, a); break;
         default: return hipErrorInvalidValue;

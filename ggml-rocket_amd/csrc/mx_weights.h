@@ -46,6 +46,7 @@ __host__ __device__ inline int64_t packed_weight_bytes(int wt, int64_t rows, int
         case T_MXFP4: return rows * (K / 32) * 17;
         case T_Q4_0: return rows * (K / 32) * 18;
         case T_Q5_K: return rows * (K / 256) * 176;
+        case T_Q4_KX: return rows % 32 ? -1 : rows * (K / 256) * 144;
         default: return -1;
     }
 }
@@ -403,6 +404,26 @@ template <> struct WLoad<T_Q4_K> {
         out[3] = u32x4{hi[4], hi[5], hi[6], hi[7]};
         run0 = 16 * u;
         run1 = 32 + 16 * u;
+    }
+};
+
+// Q4_K regrouped by 32 rows (T_Q4_KX): per (32-row group, 256-value block) 4608 bytes, the 32
+// headers (16 B each, row order) then per 64-value quarter j the 32 rows' 32 nibble bytes. The
+// same decode as Q4_K; lanes that take consecutive rows read consecutive bytes.
+constexpr int Q4KX_GROUP = 32;
+__host__ __device__ inline int64_t q4kx_block(int64_t row, int64_t blk, int64_t nblk) {
+    return ((row / Q4KX_GROUP) * nblk + blk) * (Q4KX_GROUP * 144);
+}
+template <> struct WLoad<T_Q4_KX> : WLoad<T_Q4_K> {
+    __device__ __forceinline__ void load(const uint8_t * W, int64_t rows, int64_t K, int64_t row,
+                                         int64_t k0, int u, bool ok_row) {
+        const int64_t blk = k0 / 256;
+        j = (int)((k0 % 256) / 64);
+        ok = ok_row;
+        const uint8_t * b = W + q4kx_block(row, blk, K / 256);
+        const int r = (int)(row % Q4KX_GROUP);
+        hdr = *(const u32x4 *)(b + 16 * r);
+        qs = *(const u32x4 *)(b + 16 * Q4KX_GROUP + 32 * Q4KX_GROUP * j + 32 * r + 16 * u);
     }
 };
 

@@ -47,7 +47,14 @@ enum mi355x_wtype { MI355X_F16 = 1, MI355X_Q4_0 = 2, MI355X_Q8_0 = 8, MI355X_Q4_
                      * tile (r/16, k/32) at element ((r/16)*(K/32) + k/32)*512; rows padded to a
                      * multiple of 16 (padding never read). The resident fp16 form the GEMM streams
                      * fastest: each 64-lane load instruction reads one whole tile. */
-                    MI355X_F16_T = 0x101 };
+                    MI355X_F16_T = 0x101,
+                    /* not a ggml type: Q4_K blocks of [rows][K] (rows % 32 == 0) regrouped by 32
+                     * rows, for expert stacks (mi355x_mul_mat_id only): for each group of 32 rows
+                     * and 256-value block, the 32 rows' 16-byte headers (d, dmin, scales), then
+                     * for each 64-value quarter the 32 rows' 32 bytes of nibbles. Same bytes as
+                     * Q4_K; a wave's loads of a quarter are one contiguous KiB. Built from ggml
+                     * Q4_K blocks by mi355x_weight_pack. */
+                    MI355X_Q4_K_X = 0x10C };
 
 typedef struct mi355x_device_info {
     char name[64];              /* e.g. "gfx950" */

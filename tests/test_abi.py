@@ -61,3 +61,21 @@ def test_ggml_adapter_defines_the_public_api():
     L = mx.lib()
     used = set(re.findall(r"\b(mi355x_backend_\w+)\s*\(", src))
     assert used and all(hasattr(L, n) for n in used), sorted(n for n in used if not hasattr(L, n))
+
+
+def test_q4k_x_layout_argument_checks():
+    """The expert-stack layout Q4_K_X: the same byte count as Q4_K for whole 32-row groups, no size
+    otherwise; its pack rejects partial groups, K off the 256-value blocks and in-place use before
+    touching the device (argument checks only: no GPU needed)."""
+    import ctypes
+    import ggml_mi355x as mx
+    L = mx.lib()
+    assert mx.weight_bytes(mx.Q4_K_X, 64, 512) == mx.weight_bytes(mx.Q4_K, 64, 512) == 64 * 2 * 144
+    assert mx.weight_bytes(mx.Q4_K_X, 33, 512) == -1
+    assert mx.weight_bytes(mx.Q4_K_X, 64, 320) == -1
+    buf_a = ctypes.create_string_buffer(64 * 2 * 144 + 16)
+    buf_b = ctypes.create_string_buffer(64 * 2 * 144 + 16)
+    a, b = ctypes.addressof(buf_a) + (-ctypes.addressof(buf_a)) % 16, ctypes.addressof(buf_b) + (-ctypes.addressof(buf_b)) % 16
+    assert L.mi355x_weight_pack(mx.Q4_K_X, ctypes.c_void_p(a), 33, 512, ctypes.c_void_p(b), None) == mx.E_ARG
+    assert L.mi355x_weight_pack(mx.Q4_K_X, ctypes.c_void_p(a), 64, 320, ctypes.c_void_p(b), None) == mx.E_ARG
+    assert L.mi355x_weight_pack(mx.Q4_K_X, ctypes.c_void_p(a), 64, 512, ctypes.c_void_p(a), None) == mx.E_ARG

@@ -144,8 +144,24 @@ def test_moe_bad_id_flags_error(mx):
     assert compare(ref[mask], o[mask])["range_err"] <= 1e-2
 
 
+@pytest.mark.parametrize("K,N,E,ne11,U,T", [(1024, 128, 8, 1, 2, 64), (2048, 96, 8, 2, 2, 66), (768, 2048, 4, 8, 2, 40)])
+def test_moe_q4k_x_layout(mx, K, N, E, ne11, U, T):
+    """Q4_K expert stacks regrouped by 32 rows (Q4_K_X) give the same bits as the ggml block layout
+    (same decode, same MFMA order; only where the bytes sit differs), and meet the oracle's bars;
+    N = 96 leaves a partial 128-column block."""
+    P = expert_payload(O.Q4_K, E, N, K)
+    X = make_input(T, ne11, K)
+    ids = make_ids(T, U, E)
+    base, _ = run(mx, O.Q4_K, P, E, N, K, X, ids)
+    got, _ = run(mx, mx.Q4_K_X, P, E, N, K, X, ids)
+    assert np.array_equal(base.view(np.uint32), got.view(np.uint32))
+    ref = O.mul_mat_id(O.Q4_K, P, K, N, E, X, ne11, ids)
+    check_bars(ref, got, N, 0.9990, f"moe Q4_K_X K={K} N={N} T={T}")
+
+
+@pytest.mark.parametrize("layout", ["q4_k", "q4_k_x"])
 @pytest.mark.parametrize("proj", ["gate", "up", "down"])
-def test_moe_baseline_shape(mx, proj):
+def test_moe_baseline_shape(mx, proj, layout):
     """128 experts, top-8 of a softmax over N(0,1) router logits, 512 tokens, d_model 2048,
     expert FFN 768; expert weights Q4_K from N(0,0.02), activations N(0,1)."""
     E, T, U, D, F = 128, 512, 8, 2048, 768
@@ -158,7 +174,7 @@ def test_moe_baseline_shape(mx, proj):
     W = O.fill_normal((E, N, K), seed, 0.0, 0.02)
     P = O.quantize(O.Q4_K, W)
     X = O.fill_normal((T, ne11, K), seed + 8)
-    got, _ = run(mx, O.Q4_K, P, E, N, K, X, ids)
+    got, _ = run(mx, O.Q4_K if layout == "q4_k" else mx.Q4_K_X, P, E, N, K, X, ids)
     # the oracle on a sample of 64 tokens (every slot of each)
     toks = np.unique(np.linspace(0, T - 1, 64).astype(int))
     ref = O.mul_mat_id(O.Q4_K, P, K, N, E, np.ascontiguousarray(X[toks]), ne11, np.ascontiguousarray(ids[toks]))
