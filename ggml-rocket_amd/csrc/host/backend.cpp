@@ -298,6 +298,7 @@ struct mi355x_backend {
 
     DevBuf act, a16, scales, out, part, wstage, wconv, fa_q, fa_k, fa_v, fa_m, fa_o, fa_ws, moe_b, moe_ids, moe_o, moe_ws;
     DevBuf wscratch[4], moe_wscratch;   // per-call weights: unnamed, or over the cache budget
+    DevBuf w16;                         // the decode-first form's tiled fp16 weights of one call
 
     std::unordered_map<std::string, WEntry> wcache;
     size_t cache_used = 0, cache_budget = 0;
@@ -598,11 +599,28 @@ int mul_mat_device(Ctx * c, const std::vector<mi355x_tensor *> & grp, bool want_
         outs[i].ldc = ntot;
         col += a->ne[1];
     }
+    // Q8_0 / Q6_K weights at the shapes where one decode pass plus the fp16 GEMM is faster than
+    // decoding inside the GEMM: each member decoded into tiled fp16 scratch first
+    int gtype = ws[0].dev_type;
+    bool same = true;
+    for (auto & w : ws) same = same && w.dev_type == gtype;
+    if (same && mi355x_mul_mat_decode_first(gtype, M, ntot, K) == 1) {
+        std::vector<size_t> off(grp.size() + 1, 0);
+        for (size_t i = 0; i < grp.size(); i++)
+            off[i + 1] = off[i] + (((size_t)mi355x_weight_bytes(MI355X_F16_T, outs[i].N, K) + 255) & ~(size_t)255);
+        TRY(c->w16.ensure(off.back()));
+        for (size_t i = 0; i < grp.size(); i++) {
+            uint16_t * w16 = (uint16_t *)((char *)c->w16.p + off[i]);
+            TRY(mi355x_weight_f16_tiled(gtype, outs[i].w_dev, outs[i].N, K, w16, c->stream));
+            outs[i].w_dev = w16;
+        }
+        gtype = MI355X_F16_T;
+    }
     // K-split partials, summed in a fixed order (reproducible results); a two-way split adds
     // into the outputs, which the activation pack then clears in the same launch
-    const size_t pbytes = mi355x_gemm_workspace(ws[0].dev_type, M, K, outs, (int)grp.size());
+    const size_t pbytes = mi355x_gemm_workspace(gtype, M, K, outs, (int)grp.size());
     if (pbytes) TRY(c->part.ensure(pbytes));
-    const int acc = mi355x_gemm_accumulates(ws[0].dev_type, M, K, outs, (int)grp.size(), pbytes);
+    const int acc = mi355x_gemm_accumulates(gtype, M, K, outs, (int)grp.size(), pbytes);
     if (acc < 0) return acc;
     // src1 from the attention this call just computed (same host bytes, row-major F32): its
     // device copy; otherwise uploaded
@@ -613,7 +631,7 @@ int mul_mat_device(Ctx * c, const std::vector<mi355x_tensor *> & grp, bool want_
         act = (const float *)c->fa_mirror.dev;
     else
         TRY(h2d(c, c->act.p, b->data, (size_t)M * K * 4));
-    const int tiled = ws[0].dev_type == MI355X_F16_T;
+    const int tiled = gtype == MI355X_F16_T;
     if (acc)   // the outputs are the ntot columns of c->out
         TRY(mi355x_pack_act_clear(tiled, act, K, M, K, (uint16_t *)c->a16.p, (float *)c->scales.p, (float *)c->out.p,
                                   ntot, ntot, c->stream));
@@ -621,7 +639,7 @@ int mul_mat_device(Ctx * c, const std::vector<mi355x_tensor *> & grp, bool want_
         TRY(mi355x_pack_act_tiled(act, K, M, K, (uint16_t *)c->a16.p, (float *)c->scales.p, c->stream));
     else
         TRY(mi355x_pack_act(act, K, M, K, (uint16_t *)c->a16.p, (float *)c->scales.p, c->stream));
-    TRY(mi355x_gemm_ws(ws[0].dev_type, (const uint16_t *)c->a16.p, (const float *)c->scales.p, M, K, outs,
+    TRY(mi355x_gemm_ws(gtype, (const uint16_t *)c->a16.p, (const float *)c->scales.p, M, K, outs,
                        (int)grp.size(), pbytes ? c->part.p : nullptr, pbytes, acc ? MI355X_GEMM_OUT_ZEROED : 0,
                        c->stream));
     // dst[i] is [N_i, M] contiguous: one member takes the output as is; a group's outputs come

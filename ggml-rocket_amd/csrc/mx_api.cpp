@@ -244,10 +244,35 @@ static size_t mul_mat_part_offset(int64_t M, int64_t K) {
     return (mi355x_mul_mat_workspace(M, K) + 255) & ~(size_t)255;
 }
 
+// Q8_0 and Q6_K weights at M >= 512 run faster decoded once per call into tiled fp16 (one
+// pass over the weight) and multiplied by the fp16 GEMM than decoded inside the GEMM by its
+// register-staged kernel, whose decode sits on every tile's load path: measured per call on
+// MI355X with cold weights, 1.13-1.35x at M 512 and 1.27-1.78x at M 2048 over N, K in {3072,
+// 8192}; not Q8_0 at M 512 with N < K (the fp16 GEMM's few output tiles there: 0.92x), nor M 128
+// and below (the decode pass costs more than the GEMM saves), nor Q4_K, whose all-DMA decode
+// kernel stays within 10% of the two-pass form. Same fp16 weights and activations either way.
+static bool mul_mat_decode_first(int wtype, int64_t M, int64_t N, int64_t K) {
+    if (K % 64 || M < 512) return false;
+    if (wtype == mx::T_Q6_K) return true;
+    return wtype == mx::T_Q8_0 && (N >= K || M >= 1024);
+}
+
+MI355X_API int mi355x_mul_mat_decode_first(int wtype, int64_t M, int64_t N, int64_t K) {
+    return known_wtype(wtype) && N > 0 && K > 0 && mul_mat_decode_first(wtype, M, N, K) ? 1 : 0;
+}
+
+// The tiled fp16 weight of the decode-first form sits right after the pack; the K-split
+// partials after it.
+static size_t mul_mat_w16_bytes(int64_t N, int64_t K) {
+    return ((size_t)mi355x_weight_bytes(mx::T_F16T, N, K) + 255) & ~(size_t)255;
+}
+
 MI355X_API size_t mi355x_mul_mat_workspace_for(int wtype, int64_t N, int64_t K, int64_t M) {
     const size_t need = mi355x_mul_mat_workspace(M, K);
     if (need == 0) return 0;
     const mi355x_gemm_out o = {nullptr, N, 0, N, nullptr, N};
+    if (known_wtype(wtype) && N > 0 && mul_mat_decode_first(wtype, M, N, K))
+        return mul_mat_part_offset(M, K) + mul_mat_w16_bytes(N, K) + mi355x_gemm_workspace(mx::T_F16T, M, K, &o, 1);
     const size_t part = mi355x_gemm_workspace(wtype, M, K, &o, 1);
     return part ? mul_mat_part_offset(M, K) + part : need;
 }
@@ -262,10 +287,23 @@ MI355X_API int mi355x_mul_mat(int wtype, const void * w_dev, int64_t N, int64_t 
     if (!workspace_dev || workspace_bytes < need) return MI355X_E_NOMEM;
     uint16_t * a16 = (uint16_t *)workspace_dev;
     float * scales = (float *)((char *)workspace_dev + mul_mat_a16_bytes(M, K));
-    // the room past the pack holds K-split partials
-    const size_t poff = mul_mat_part_offset(M, K);
+    // the room past the pack holds the decode-first form's fp16 weight, if it runs, then K-split
+    // partials
+    size_t poff = mul_mat_part_offset(M, K);
+    uint16_t * w16 = nullptr;
+    if (known_wtype(wtype) && N > 0 && N <= INT32_MAX && mul_mat_decode_first(wtype, M, N, K) &&
+        workspace_bytes >= poff + mul_mat_w16_bytes(N, K)) {
+        w16 = (uint16_t *)((char *)workspace_dev + poff);
+        poff += mul_mat_w16_bytes(N, K);
+    }
     void * part = workspace_bytes > poff ? (char *)workspace_dev + poff : nullptr;
     const size_t part_bytes = part ? workspace_bytes - poff : 0;
+    if (w16) {   // checks the weight's type, K and alignment like any other call of it
+        const int st = mi355x_weight_f16_tiled(wtype, w_dev, N, K, w16, stream);
+        if (st != MI355X_OK) return st;
+        wtype = mx::T_F16T;
+        w_dev = w16;
+    }
     // a GEMM that adds a two-way K split into dst has it cleared by the pack, in the same launch
     bool zero = false;
     if ((known_wtype(wtype) || wtype == mx::T_F16T) && K > 0 && K <= INT32_MAX && M <= INT32_MAX && N > 0 &&

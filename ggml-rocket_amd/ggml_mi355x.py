@@ -97,6 +97,8 @@ def lib():
     L.mi355x_mul_mat_workspace.argtypes = [i64, i64]
     L.mi355x_mul_mat_workspace_for.restype = sz
     L.mi355x_mul_mat_workspace_for.argtypes = [i32, i64, i64, i64]
+    L.mi355x_mul_mat_decode_first.restype = i32
+    L.mi355x_mul_mat_decode_first.argtypes = [i32, i64, i64, i64]
     L.mi355x_mul_mat.argtypes = [i32, vp, i64, i64, vp, i64, i64, vp, i64, vp, sz, vp]
     _bind_optional(L)
     _lib = L

@@ -79,3 +79,27 @@ def test_q4k_x_layout_argument_checks():
     assert L.mi355x_weight_pack(mx.Q4_K_X, ctypes.c_void_p(a), 33, 512, ctypes.c_void_p(b), None) == mx.E_ARG
     assert L.mi355x_weight_pack(mx.Q4_K_X, ctypes.c_void_p(a), 64, 320, ctypes.c_void_p(b), None) == mx.E_ARG
     assert L.mi355x_weight_pack(mx.Q4_K_X, ctypes.c_void_p(a), 64, 512, ctypes.c_void_p(a), None) == mx.E_ARG
+
+
+def test_mul_mat_workspace_sizes_the_decode_first_weight():
+    """mi355x_mul_mat_workspace_for makes room for the tiled fp16 weight where the decode-first
+    form runs (Q6_K at M >= 512; Q8_0 at M >= 1024, or at M >= 512 with N >= K) and elsewhere
+    sizes the pack and the in-GEMM decode's split partials only (host-side sizing: no GPU
+    needed)."""
+    import ggml_mi355x as mx
+    L = mx.lib()
+    for wt, M, N, K, first in [(mx.Q6_K, 512, 1024, 3072, True), (mx.Q6_K, 128, 1024, 3072, False),
+                               (mx.Q8_0, 512, 3072, 1024, True), (mx.Q8_0, 512, 1024, 3072, False),
+                               (mx.Q8_0, 1024, 1024, 3072, True), (mx.Q4_K, 2048, 1024, 3072, False)]:
+        pack = int(L.mi355x_mul_mat_workspace(M, K))
+        poff = (pack + 255) // 256 * 256
+        arr = (mx.GemmOut * 1)()
+        arr[0] = mx.GemmOut(0, N, 0, N, 0, N)
+        part_f16t = int(L.mi355x_gemm_workspace(mx.F16_T, M, K, arr, 1))
+        part_own = int(L.mi355x_gemm_workspace(wt, M, K, arr, 1))
+        ws = int(L.mi355x_mul_mat_workspace_for(wt, N, K, M))
+        assert L.mi355x_mul_mat_decode_first(wt, M, N, K) == int(first)
+        if first:
+            assert ws == poff + (mx.weight_bytes(mx.F16_T, N, K) + 255) // 256 * 256 + part_f16t, (wt, M, N, K)
+        else:
+            assert ws == (poff + part_own if part_own else pack), (wt, M, N, K)

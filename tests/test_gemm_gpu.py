@@ -153,6 +153,39 @@ def test_mul_mat_quant_sweep(mx, K, N, M, wtype):
     _assert_bars(ref, got[rows], len(rows), N, f"{O.TYPE_NAMES[wtype]} K={K} N={N} M={M}")
 
 
+@pytest.mark.parametrize("wtype,M,N,K", [(O.Q6_K, 512, 768, 1024), (O.Q8_0, 1024, 512, 2048),
+                                         (O.Q8_0, 512, 1024, 512)])
+def test_mul_mat_decode_first(mx, wtype, M, N, K):
+    """Q6_K / Q8_0 at M >= 512: with mi355x_mul_mat_workspace_for bytes the weight is decoded once
+    into tiled fp16 in the workspace and multiplied by the fp16 GEMM; with only the pack's bytes it
+    is decoded inside the GEMM. Both forms meet the oracle's bars and agree with each other to
+    fp32 summation order (same fp16 weights and activations)."""
+    import ctypes
+    import torch
+    W = O.fill_normal((N, K), 0x5EED0100 + wtype, 0.0, 0.02)
+    Xf = O.fill_normal((M, K), 0x5EED0200 + M)
+    Q = O.quantize(wtype, W)
+    w = mx.upload_weight(wtype, Q, N, K)
+    L = mx.lib()
+    x = _dev(Xf)
+    outs = []
+    for nbytes in (int(L.mi355x_mul_mat_workspace_for(wtype, N, K, M)), int(L.mi355x_mul_mat_workspace(M, K))):
+        ws = torch.empty(nbytes, dtype=torch.uint8, device="cuda")
+        out = torch.full((M, N), float("nan"), dtype=torch.float32, device="cuda")
+        mx.check(L.mi355x_mul_mat(wtype, ctypes.c_void_p(w.data_ptr()), N, K, ctypes.c_void_p(x.data_ptr()), K, M,
+                                  ctypes.c_void_p(out.data_ptr()), N, ctypes.c_void_p(ws.data_ptr()), nbytes,
+                                  mx.stream_handle()), "mul_mat")
+        torch.cuda.synchronize()
+        outs.append(out.cpu().numpy())
+    first, in_gemm = outs
+    assert int(L.mi355x_mul_mat_workspace_for(wtype, N, K, M)) >= int(L.mi355x_mul_mat_workspace(M, K)) + 2 * N * K
+    rows = np.unique(np.linspace(0, M - 1, 48).astype(int))
+    ref = O.mul_mat(wtype, Q, Xf[rows], N, K)
+    _assert_bars(ref, first[rows], len(rows), N, f"{O.TYPE_NAMES[wtype]} decode-first M={M}")
+    _assert_bars(ref, in_gemm[rows], len(rows), N, f"{O.TYPE_NAMES[wtype]} in-GEMM decode M={M}")
+    assert np.abs(first - in_gemm).max() <= 1e-5 * np.abs(in_gemm).max()
+
+
 @pytest.mark.parametrize("Ns", [(4096, 4096), (4096, 2048, 2048)])
 def test_fused_group(mx, Ns):
     """test-rocket-matmul.cpp:259-314: members sharing src1 in one launch over concatenated N."""
