@@ -127,12 +127,18 @@ __global__ void __launch_bounds__(MOE_SORT_THREADS) moe_sort_kernel(MoeArgs a) {
 // K slabs ahead of the MFMAs, so an HBM round trip has R - 1 slabs of work to hide behind before
 // its data is decoded. 128-column blocks: 768 of them (128 experts x 6 column blocks of a
 // 768-wide gate/up) are one round of three blocks per CU over 256 CUs.
-// Register stages of slab lookahead: four where they fit in the three-wave register budget
-// without spilling, three for the formats whose stage is wider (F16, Q5_K, Q6_K).
-template <int WT> constexpr int moe_stages() { return (WT == T_F16 || WT == T_Q6_K || WT == T_Q5_K) ? 3 : 4; }
+// Waves per SIMD and register stages of slab lookahead: Q4_K (both layouts) and Q8_0 run four
+// waves a SIMD with two stages (128 registers), measured 1-12% faster than three waves with four
+// stages, most on the down projection's 2048 blocks; the other formats measured within 2% either
+// way and keep three waves with four stages, or three where the stage is wider (F16, Q5_K, Q6_K;
+// Q6_K would spill at four waves).
+template <int WT> constexpr int moe_waves() { return (WT == T_Q4_K || WT == T_Q4_KX || WT == T_Q8_0) ? 4 : 3; }
+template <int WT> constexpr int moe_stages() {
+    return moe_waves<WT>() == 4 ? 2 : (WT == T_F16 || WT == T_Q6_K || WT == T_Q5_K) ? 3 : 4;
+}
 
 template <int WT>
-__global__ void __launch_bounds__(MOE_THREADS) __attribute__((amdgpu_waves_per_eu(3, 3)))
+__global__ void __launch_bounds__(MOE_THREADS) __attribute__((amdgpu_waves_per_eu(moe_waves<WT>(), moe_waves<WT>())))
 moe_gemm_kernel(MoeArgs a) {
     constexpr int R = moe_stages<WT>();
     extern __shared__ __align__(16) uint8_t smem[];
