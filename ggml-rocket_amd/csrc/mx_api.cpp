@@ -244,17 +244,18 @@ static size_t mul_mat_part_offset(int64_t M, int64_t K) {
     return (mi355x_mul_mat_workspace(M, K) + 255) & ~(size_t)255;
 }
 
-// Q8_0 and Q6_K weights at M >= 512 run faster decoded once per call into tiled fp16 (one
-// pass over the weight) and multiplied by the fp16 GEMM than decoded inside the GEMM by its
-// register-staged kernel, whose decode sits on every tile's load path: measured per call on
-// MI355X with cold weights, 1.13-1.35x at M 512 and 1.27-1.78x at M 2048 over N, K in {3072,
-// 8192}; not Q8_0 at M 512 with N < K (the fp16 GEMM's few output tiles there: 0.92x), nor M 128
-// and below (the decode pass costs more than the GEMM saves), nor Q4_K, whose all-DMA decode
-// kernel stays within 10% of the two-pass form. Same fp16 weights and activations either way.
+// Weights of the register-staged decode kernel run faster at M >= 512 decoded once per call into
+// tiled fp16 (one pass over the weight) and multiplied by the fp16 GEMM than decoded inside the
+// GEMM, where the decode sits on every tile's load path. Measured per call on MI355X with cold
+// weights over N, K in {3072, 4096, 8192, 14336}: Q6_K, Q5_K and MXFP4 1.06-1.48x at M 512 and
+// 1.24-1.91x at M 2048; Q8_0 and Q4_0 1.08-1.15x at M 512 with N >= K, 0.92-0.99x with N < K (the
+// fp16 GEMM's few output tiles there), 1.19-1.52x at M 2048. Not M 128 and below (the decode pass
+// costs more than the GEMM saves), nor Q4_K, whose all-DMA decode kernel is 0.83-1.38x of the
+// two-pass form depending on the shape. Same fp16 weights and activations either way.
 static bool mul_mat_decode_first(int wtype, int64_t M, int64_t N, int64_t K) {
     if (K % 64 || M < 512) return false;
-    if (wtype == mx::T_Q6_K) return true;
-    return wtype == mx::T_Q8_0 && (N >= K || M >= 1024);
+    if (wtype == mx::T_Q6_K || wtype == mx::T_Q5_K || wtype == mx::T_MXFP4) return true;
+    return (wtype == mx::T_Q8_0 || wtype == mx::T_Q4_0) && (N >= K || M >= 1024);
 }
 
 MI355X_API int mi355x_mul_mat_decode_first(int wtype, int64_t M, int64_t N, int64_t K) {

@@ -178,8 +178,9 @@ MI355X_API int mi355x_gemm_accumulates(int wtype, int64_t M, int64_t K, const mi
 
 /* 1 if a MUL_MAT of M rows with this weight layout and N x K weight runs faster in the
  * decode-first form (the weight decoded once into tiled fp16, mi355x_weight_f16_tiled, then
- * multiplied as MI355X_F16_T) than decoded inside the GEMM, else 0: MI355X_Q6_K at M >= 512,
- * MI355X_Q8_0 at M >= 1024 or at M >= 512 with N >= K, K % 64 == 0 (measured on MI355X).
+ * multiplied as MI355X_F16_T) than decoded inside the GEMM, else 0: Q6_K, Q5_K and MXFP4
+ * weights at M >= 512, Q8_0 and Q4_0 at M >= 1024 or at M >= 512 with N >= K, K % 64 == 0
+ * (measured on MI355X; Q4_K keeps its in-GEMM decode).
  * No counterpart in the reference, whose per-call fp16 route always decodes first. */
 MI355X_API int mi355x_mul_mat_decode_first(int wtype, int64_t M, int64_t N, int64_t K);
 
@@ -188,7 +189,7 @@ MI355X_API size_t mi355x_mul_mat_workspace(int64_t M, int64_t K);
 
 /* Workspace bytes with which mi355x_mul_mat runs its fastest form for this shape: the pack,
  * then (from the next 256-byte boundary) the decode-first form's tiled fp16 weight where that
- * form runs (MI355X_Q8_0 / MI355X_Q6_K weights at M >= 512, see mi355x_mul_mat), then the split
+ * form runs (mi355x_mul_mat_decode_first), then the split
  * partials mi355x_gemm_workspace names. */
 MI355X_API size_t mi355x_mul_mat_workspace_for(int wtype, int64_t N, int64_t K, int64_t M);
 
@@ -196,8 +197,8 @@ MI355X_API size_t mi355x_mul_mat_workspace_for(int wtype, int64_t N, int64_t K, 
  * then mi355x_gemm_ws, the activation pack at the start of `workspace_dev` and the K-split
  * partials in the bytes past it (mi355x_mul_mat_workspace_for sizes both; with only
  * mi355x_mul_mat_workspace bytes the split is at most two ways). Reproducible as mi355x_gemm_ws.
- * Decode-first form: Q6_K weights at M >= 512 and Q8_0 weights at M >= 1024, or at M >= 512
- * with N >= K (K % 64 == 0), are decoded once per call into tiled fp16 in the workspace
+ * Decode-first form: where mi355x_mul_mat_decode_first says so, the weight is decoded once per
+ * call into tiled fp16 in the workspace
  * (mi355x_weight_f16_tiled) and multiplied as MI355X_F16_T, when the workspace holds that
  * weight; the same fp16 weights and activations as the in-GEMM decode, faster at those shapes.
  * The whole MUL_MAT of ggml-rocket.cpp:4548-4871 on device. */

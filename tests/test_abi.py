@@ -83,14 +83,17 @@ def test_q4k_x_layout_argument_checks():
 
 def test_mul_mat_workspace_sizes_the_decode_first_weight():
     """mi355x_mul_mat_workspace_for makes room for the tiled fp16 weight where the decode-first
-    form runs (Q6_K at M >= 512; Q8_0 at M >= 1024, or at M >= 512 with N >= K) and elsewhere
+    form runs (Q6_K / Q5_K / MXFP4 at M >= 512; Q8_0 / Q4_0 at M >= 1024, or at M >= 512 with
+    N >= K) and elsewhere
     sizes the pack and the in-GEMM decode's split partials only (host-side sizing: no GPU
     needed)."""
     import ggml_mi355x as mx
     L = mx.lib()
     for wt, M, N, K, first in [(mx.Q6_K, 512, 1024, 3072, True), (mx.Q6_K, 128, 1024, 3072, False),
                                (mx.Q8_0, 512, 3072, 1024, True), (mx.Q8_0, 512, 1024, 3072, False),
-                               (mx.Q8_0, 1024, 1024, 3072, True), (mx.Q4_K, 2048, 1024, 3072, False)]:
+                               (mx.Q8_0, 1024, 1024, 3072, True), (mx.Q4_K, 2048, 1024, 3072, False),
+                               (mx.Q5_K, 512, 1024, 3072, True), (mx.MXFP4, 512, 1024, 3072, True),
+                               (mx.Q4_0, 512, 1024, 3072, False), (mx.Q4_0, 512, 3072, 1024, True)]:
         pack = int(L.mi355x_mul_mat_workspace(M, K))
         poff = (pack + 255) // 256 * 256
         arr = (mx.GemmOut * 1)()
