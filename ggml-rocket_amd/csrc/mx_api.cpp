@@ -250,11 +250,15 @@ static size_t mul_mat_part_offset(int64_t M, int64_t K) {
 // weights over N, K in {3072, 4096, 8192, 14336}: Q6_K, Q5_K and MXFP4 1.06-1.48x at M 512 and
 // 1.24-1.91x at M 2048; Q8_0 and Q4_0 1.08-1.15x at M 512 with N >= K, 0.92-0.99x with N < K (the
 // fp16 GEMM's few output tiles there), 1.19-1.52x at M 2048. Not M 128 and below (the decode pass
-// costs more than the GEMM saves), nor Q4_K, whose all-DMA decode kernel is 0.83-1.38x of the
-// two-pass form depending on the shape. Same fp16 weights and activations either way.
+// costs more than the GEMM saves). Q4_K's all-DMA decode kernel is 0.83-1.38x of the two-pass
+// form depending on the shape: the two-pass form wins where N >= K and the fp16 weight is at most
+// 64 MB (1.02-1.38x, e.g. 1.20x for N 6144, K 4096 at M 512), and loses on larger panels, whose
+// fp16 form no longer stays in the 256 MB last-level cache (0.83x for N 28672, K 4096 at M 512).
+// Same fp16 weights and activations either way.
 static bool mul_mat_decode_first(int wtype, int64_t M, int64_t N, int64_t K) {
     if (K % 64 || M < 512) return false;
     if (wtype == mx::T_Q6_K || wtype == mx::T_Q5_K || wtype == mx::T_MXFP4) return true;
+    if (wtype == mx::T_Q4_K) return N >= K && N * K <= ((int64_t)1 << 25);
     return (wtype == mx::T_Q8_0 || wtype == mx::T_Q4_0) && (N >= K || M >= 1024);
 }
 

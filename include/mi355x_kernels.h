@@ -179,8 +179,8 @@ MI355X_API int mi355x_gemm_accumulates(int wtype, int64_t M, int64_t K, const mi
 /* 1 if a MUL_MAT of M rows with this weight layout and N x K weight runs faster in the
  * decode-first form (the weight decoded once into tiled fp16, mi355x_weight_f16_tiled, then
  * multiplied as MI355X_F16_T) than decoded inside the GEMM, else 0: Q6_K, Q5_K and MXFP4
- * weights at M >= 512, Q8_0 and Q4_0 at M >= 1024 or at M >= 512 with N >= K, K % 64 == 0
- * (measured on MI355X; Q4_K keeps its in-GEMM decode).
+ * weights at M >= 512, Q8_0 and Q4_0 at M >= 1024 or at M >= 512 with N >= K, Q4_K at M >= 512
+ * with N >= K and N * K <= 2^25, K % 64 == 0 (measured on MI355X).
  * No counterpart in the reference, whose per-call fp16 route always decodes first. */
 MI355X_API int mi355x_mul_mat_decode_first(int wtype, int64_t M, int64_t N, int64_t K);
 

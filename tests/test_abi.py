@@ -92,6 +92,7 @@ def test_mul_mat_workspace_sizes_the_decode_first_weight():
     for wt, M, N, K, first in [(mx.Q6_K, 512, 1024, 3072, True), (mx.Q6_K, 128, 1024, 3072, False),
                                (mx.Q8_0, 512, 3072, 1024, True), (mx.Q8_0, 512, 1024, 3072, False),
                                (mx.Q8_0, 1024, 1024, 3072, True), (mx.Q4_K, 2048, 1024, 3072, False),
+                               (mx.Q4_K, 512, 6144, 4096, True), (mx.Q4_K, 512, 28672, 4096, False),
                                (mx.Q5_K, 512, 1024, 3072, True), (mx.MXFP4, 512, 1024, 3072, True),
                                (mx.Q4_0, 512, 1024, 3072, False), (mx.Q4_0, 512, 3072, 1024, True)]:
         pack = int(L.mi355x_mul_mat_workspace(M, K))
