@@ -16,7 +16,9 @@ host buffers (PCIe-inclusive) is reported beside it under "host_path".
 
 Routes: "prepacked-q" (default; the reference's ROCKET_QUANT_RESIDENT route): each Q4_K weight
 is decoded once to an fp16 HBM copy and the GEMMs read fp16. "mt": the GEMMs read the Q4_K
-blocks and dequantize them in LDS on every call.
+blocks and dequantize them in LDS on every call (the backend's mt route instead decodes the
+smaller panels, qkv and o, to fp16 scratch first where mi355x_mul_mat_decode_first says so; this
+step keeps the in-GEMM decode for all four).
 
 Prints ONE JSON line (rank 0). `value` is tokens/s of the whole step; `roofline` is the dominant
 kernel's (the GEMM) live HIP-event figure; `cpu_baseline` is the CPU oracle timed on a bounded
