@@ -123,7 +123,8 @@ def test_fused_groups(be, Ns):
                                          (3840, 256, 128, O.Q5_K),
                                          # M 512: the mt route's decode-first form (Q6_K; Q8_0 with N >= K)
                                          (512, 256, 512, O.Q6_K), (512, 768, 512, O.Q8_0),
-                                         (512, 256, 512, O.Q5_K), (512, 256, 512, O.MXFP4)])
+                                         (512, 256, 512, O.Q5_K), (512, 256, 512, O.MXFP4),
+                                         (512, 512, 512, O.Q4_K), (512, 512, 512, O.Q4_0)])
 @pytest.mark.parametrize("resident", [0, 1])
 def test_matmul_quant(be, K, N, M, wtype, resident):
     i = np.arange(N * K, dtype=np.float32)
