@@ -156,7 +156,10 @@ def test_mul_mat_quant_sweep(mx, K, N, M, wtype):
 @pytest.mark.parametrize("wtype,M,N,K", [(O.Q6_K, 512, 768, 1024), (O.Q8_0, 1024, 512, 2048),
                                          (O.Q8_0, 512, 1024, 512), (O.Q5_K, 512, 384, 768),
                                          (O.MXFP4, 512, 256, 512), (O.Q4_0, 512, 512, 256),
-                                         (O.Q4_K, 512, 512, 256)])
+                                         (O.Q4_K, 512, 512, 256),
+                                         # ragged: M off the 16-row groups of the tiled pack, N off the
+                                         # 32 / 128-row tiles (N % 16 == 0, as every MUL_MAT here takes)
+                                         (O.Q6_K, 520, 112, 256), (O.Q8_0, 530, 208, 192)])
 def test_mul_mat_decode_first(mx, wtype, M, N, K):
     """Q6_K / Q5_K / MXFP4 / Q8_0 / Q4_0 / Q4_K at M >= 512: with mi355x_mul_mat_workspace_for bytes the weight is decoded once
     into tiled fp16 in the workspace and multiplied by the fp16 GEMM; with only the pack's bytes it
