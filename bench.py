@@ -740,11 +740,12 @@ def configs_bench(args, subset=False):
     W = (np.random.default_rng(0x5EED0000 + 16).standard_normal((8192, 2048), dtype=np.float32) * 0.02)
     mul_mat_case("MUL_MAT F16 N=8192 K=2048", mx.F16, mx.F16_T, W.astype(np.float16).view(np.uint16),
                  8192, 2048, [512])
-    # quantized sweep, decoded inside the GEMM (the per-call route); the default bench line
-    # carries one shape of it (Q4_K, K 3072, N 8192)
+    # quantized sweep, the weight decoded per call (inside the GEMM, or first into tiled fp16 where
+    # mi355x_mul_mat_decode_first says so); the default bench line carries one shape of it for
+    # each type (K 3072, N 8192)
     for ti, (wt, tn) in enumerate(((mx.Q8_0, "Q8_0"), (mx.Q4_K, "Q4_K"), (mx.Q6_K, "Q6_K"))):
         for si, (K, N) in enumerate(((3072, 3072), (3072, 8192), (8192, 3072))):
-            if subset and (wt, K, N) != (mx.Q4_K, 3072, 8192):
+            if subset and (K, N) != (3072, 8192):
                 continue
             P = synth_blocks(wt, N, K, 0x5EED0000 + 32 + 4 * ti + si)
             mul_mat_case(f"MUL_MAT {tn} N={N} K={K}", wt, wt, P, N, K, [32, 128, 512, 2048])
