@@ -627,12 +627,46 @@ def host_path(args):
             if st != 0:
                 raise RuntimeError(f"graph_compute status {st}")
 
+    keys = ("bytes_up", "bytes_down", "up_copy_s", "up_wait_s", "down_copy_s", "down_wait_s")
+
+    def run_split():
+        """One more pass, each call's wall time and host-side copy accounting summed per group of
+        the layer ({Q,K,V}, {attention, O}, {gate,up}, {down})."""
+        per = [dict(calls=0, wall_s=0.0, **{k: 0.0 for k in keys}) for _ in range(4)]
+        for i, nodes in enumerate(calls):
+            h0 = be.host_stats()
+            t0 = time.perf_counter()
+            if be.compute(nodes) != 0:
+                raise RuntimeError("graph_compute failed")
+            dt = time.perf_counter() - t0
+            h1 = be.host_stats()
+            p = per[i % 4]
+            p["calls"] += 1
+            p["wall_s"] += dt
+            for k in keys:
+                p[k] += h1[k] - h0[k]
+        return per
+
     t0 = time.time()
     run()                                       # builds the HBM weight cache
     first_s = time.time() - t0
     t0 = time.time()
+    h0 = be.host_stats()
     run()
     sec = time.time() - t0
+    h1 = be.host_stats()
+    split = run_split()
+    link = pinned_link_rate()
+    names = ["qkv", "attn+o", "gate_up", "down"]
+    per_call = {}
+    for n, p in zip(names, split):
+        c = max(p["calls"], 1)
+        mb = (p["bytes_up"] + p["bytes_down"]) / c / 1e6
+        per_call[n] = {"ms": round(p["wall_s"] / c * 1e3, 3), "MB_up": round(p["bytes_up"] / c / 1e6, 2),
+                       "MB_down": round(p["bytes_down"] / c / 1e6, 2),
+                       "link_floor_ms": round(mb / link["GBps_one_way"], 3) if link else None,
+                       **{k.replace("_s", "_ms"): round(p[k] / c * 1e3, 3) for k in keys[2:]}}
+    bytes_step = (h1["bytes_up"] - h0["bytes_up"]) + (h1["bytes_down"] - h0["bytes_down"])
     fb = be.cpu_fallbacks()
     routes = {r: be.route_ops(r) for r in ("prepacked-q", "fused-resident", "fa", "mt", "fused")}
     be.free()
@@ -646,10 +680,50 @@ def host_path(args):
                       "layers": L, "d_model": d_model, "ffn": ffn, "heads": nh, "kv_heads": nkv,
                       "route": "prepacked-q (QUANT_RESIDENT)"},
            "first_pass_s": round(first_s, 2), "host_setup_s": round(setup_s, 1), "cpu_fallbacks": fb,
+           "GB_per_prefill": round(bytes_step / 1e9, 2), "pinned_link": link,
+           "link_floor_tok_s": round(TOKENS / (bytes_step / (link["GBps_one_way"] * 1e9)), 1) if link else None,
+           "fa_mirror_hits": h1["fa_mirror_hits"] - h0["fa_mirror_hits"],
+           "per_call": per_call,
            "routes": routes,
            "scope": "the backend's ops only: FLASH_ATTN_EXT at n_kv < FLASH_ATTN_MIN_KV and every op "
                     "the backend does not claim run on the host CPU and are not timed"}
     return out
+
+
+def pinned_link_rate(mb=256):
+    """Pinned host <-> device copy rate on this box (torch: pinned host tensors, HIP events):
+    each direction alone, then both at once. The floor of the host-buffer path is its bytes at
+    the one-way rate (the box's link does not run both directions at full rate together)."""
+    import torch
+    if not torch.cuda.is_available():
+        return None
+    n = mb << 20
+    h = torch.empty(n, dtype=torch.uint8, pin_memory=True)
+    h2 = torch.empty(n, dtype=torch.uint8, pin_memory=True)
+    d = torch.empty(n, dtype=torch.uint8, device="cuda")
+    d2 = torch.empty(n, dtype=torch.uint8, device="cuda")
+    s1, s2 = torch.cuda.Stream(), torch.cuda.Stream()
+
+    def timed(fn):
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        fn()
+        torch.cuda.synchronize()
+        return time.perf_counter() - t0
+
+    for _ in range(2):
+        up = timed(lambda: d.copy_(h, non_blocking=True))
+        down = timed(lambda: h.copy_(d, non_blocking=True))
+
+    def both():
+        with torch.cuda.stream(s1):
+            d.copy_(h, non_blocking=True)
+        with torch.cuda.stream(s2):
+            h2.copy_(d2, non_blocking=True)
+    both_s = timed(both)
+    return {"GBps_up": round(n / up / 1e9, 1), "GBps_down": round(n / down / 1e9, 1),
+            "GBps_one_way": round(2 * n / (up + down) / 1e9, 1), "GBps_both_at_once": round(2 * n / both_s / 1e9, 1),
+            "MB": mb}
 
 
 def graph_time_us(fn_of_i, n_calls, reps=3):

@@ -17,8 +17,11 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <immintrin.h>
+
 #include <algorithm>
 #include <atomic>
+#include <chrono>
 #include <condition_variable>
 #include <functional>
 #include <map>
@@ -88,149 +91,205 @@ private:
     long resting_ = 0;  // calls left in the current rest
 };
 
-// A grow-only device buffer.
+// A grow-only device buffer of one backend, allocated and freed in the order of that backend's
+// stream (the device's stream-ordered pool): a buffer that grows releases its old bytes after
+// the work already queued on the stream has read them, and neither waits for nor holds up
+// other streams or other backends (hipFree would synchronize the whole device first).
 struct DevBuf {
     void * p = nullptr;
     size_t cap = 0;
-    int ensure(size_t n) {
+    hipStream_t owner = nullptr;   // the stream p was allocated on
+    int ensure(size_t n, hipStream_t s) {
         if (n <= cap) return MI355X_OK;
-        if (p) {
-            (void)hipDeviceSynchronize();   // queued work may still read the old buffer
-            (void)hipFree(p);
-        }
+        if (p) (void)hipFreeAsync(p, owner);
         p = nullptr;
         cap = 0;
         const size_t want = (n + ((size_t)1 << 20) - 1) & ~(((size_t)1 << 20) - 1);
-        if (hipMalloc(&p, want) != hipSuccess) {
+        if (hipMallocAsync(&p, want, s) != hipSuccess) {
             (void)hipGetLastError();
             p = nullptr;
             return MI355X_E_DEVICE;
         }
+        owner = s;
         cap = want;
         return MI355X_OK;
     }
+    // after the owner stream has been synchronized
     void release() {
-        if (p) (void)hipFree(p);
+        if (p) (void)hipFreeAsync(p, owner);
         p = nullptr;
         cap = 0;
     }
 };
 
-// Host copy workers: one memcpy (or any job over disjoint parts) split across n threads, the
-// caller being one of them. Persistent threads, because a copy of one staging chunk takes about
-// as long as starting a thread.
+// n bytes from src to dst with non-temporal (streaming) 32-byte stores: the destination lines
+// are written whole without being read first, as a plain memcpy of cache-sized parts does, and
+// go to DRAM, where the DMA engine (a staging slot) or the host's next reader (a tensor larger
+// than the caches) takes them from anyway. That is a third less memory traffic per copied byte.
+__attribute__((target("avx2"))) void stream_copy_avx2(void * dst, const void * src, size_t n) {
+    char * d = (char *)dst;
+    const char * s = (const char *)src;
+    size_t head = (32 - ((uintptr_t)d & 31)) & 31;
+    if (head > n) head = n;
+    memcpy(d, s, head);
+    d += head;
+    s += head;
+    n -= head;
+    const size_t body = n & ~(size_t)127;
+    for (size_t i = 0; i < body; i += 128) {
+        const __m256i x0 = _mm256_loadu_si256((const __m256i *)(s + i));
+        const __m256i x1 = _mm256_loadu_si256((const __m256i *)(s + i + 32));
+        const __m256i x2 = _mm256_loadu_si256((const __m256i *)(s + i + 64));
+        const __m256i x3 = _mm256_loadu_si256((const __m256i *)(s + i + 96));
+        _mm256_stream_si256((__m256i *)(d + i), x0);
+        _mm256_stream_si256((__m256i *)(d + i + 32), x1);
+        _mm256_stream_si256((__m256i *)(d + i + 64), x2);
+        _mm256_stream_si256((__m256i *)(d + i + 96), x3);
+    }
+    _mm_sfence();   // the streamed lines are visible before anyone is told the copy is done
+    memcpy(d + body, s + body, n - body);
+}
+
+bool stream_copy_ok() {
+    static const bool ok = [] {
+        if (const char * e = getenv("MI355X_COPY_NT"))
+            if (atoi(e) == 0) return false;
+        return __builtin_cpu_supports("avx2") != 0;
+    }();
+    return ok;
+}
+
+void copy_bytes(void * dst, const void * src, size_t n) {
+    if (n >= 4096 && stream_copy_ok()) stream_copy_avx2(dst, src, n);
+    else memcpy(dst, src, n);
+}
+
+// Host copy workers: one copy (or any job over disjoint parts) split across n threads, the
+// caller being one of them. Persistent threads, because a copy of one staging piece takes about
+// as long as starting a thread; after a job a worker keeps polling for the next one for
+// `spin_us` before it sleeps, since during a graph_compute call the next piece comes within
+// tens of microseconds and waking a sleeping thread costs about as long.
 class CopyPool {
 public:
-    explicit CopyPool(int n, size_t min_part) : min_part_(min_part) {
+    CopyPool(int n, size_t min_part, int spin_us) : min_part_(min_part), spin_us_(spin_us) {
         for (int i = 1; i < n; i++) th_.emplace_back([this] { work(); });
     }
     ~CopyPool() {
         {
             std::lock_guard<std::mutex> lk(mu_);
-            stop_ = true;
+            stop_.store(true);
         }
         cv_.notify_all();
         for (auto & t : th_) t.join();
     }
     int threads() const { return (int)th_.size() + 1; }
+    size_t min_part() const { return min_part_; }
     // part(i) for i in [0, parts), spread over the workers and the calling thread
     void run(int parts, const std::function<void(int)> & part) {
         if (th_.empty() || parts <= 1) {
             for (int i = 0; i < parts; i++) part(i);
             return;
         }
-        {
-            std::lock_guard<std::mutex> lk(mu_);
-            job_ = &part;
-            parts_ = parts;
-            next_.store(0);
-            left_ = parts;
-            gen_++;
+        Job j;
+        j.fn = &part;
+        j.parts = parts;
+        j.left.store(parts);
+        j.gen = ++published_;
+        cur_.store(&j);
+        gen_.store(j.gen);
+        if (sleepers_.load() > 0) {
+            { std::lock_guard<std::mutex> lk(mu_); }
+            cv_.notify_all();
         }
-        cv_.notify_all();
-        drain();
-        std::unique_lock<std::mutex> lk(mu_);
-        done_.wait(lk, [this] { return left_ == 0; });
-        job_ = nullptr;
+        drain(&j);
+        while (j.left.load() > 0) __builtin_ia32_pause();
+        cur_.store(nullptr);
+        while (busy_.load() > 0) __builtin_ia32_pause();   // no worker still holds &j
     }
     void copy(void * dst, const void * src, size_t n) {
-        const int parts = (int)std::min<size_t>((size_t)threads(), (n + min_part_ - 1) / min_part_);
-        const size_t per = ((n + parts - 1) / parts + 63) & ~(size_t)63;
+        const int parts = (int)std::max<size_t>(1, std::min<size_t>((size_t)threads(), n / min_part_));
+        const size_t per = ((n + parts - 1) / parts + 127) & ~(size_t)127;
         run(parts, [&](int i) {
             const size_t o = (size_t)i * per;
-            if (o < n) memcpy((char *)dst + o, (const char *)src + o, std::min(per, n - o));
+            if (o < n) copy_bytes((char *)dst + o, (const char *)src + o, std::min(per, n - o));
         });
     }
 
 private:
-    void drain() {
+    struct Job {
+        const std::function<void(int)> * fn = nullptr;
+        int parts = 0;
+        uint64_t gen = 0;
+        std::atomic<int> next{0};
+        std::atomic<int> left{0};
+    };
+    static void drain(Job * j) {
         for (;;) {
-            const int i = next_.fetch_add(1);
-            if (i >= parts_) return;
-            (*job_)(i);
-            std::lock_guard<std::mutex> lk(mu_);
-            if (--left_ == 0) done_.notify_all();
+            const int i = j->next.fetch_add(1);
+            if (i >= j->parts) return;
+            (*j->fn)(i);
+            j->left.fetch_sub(1);
         }
     }
     void work() {
         uint64_t seen = 0;
         for (;;) {
-            {
-                std::unique_lock<std::mutex> lk(mu_);
-                cv_.wait(lk, [&] { return stop_ || gen_ != seen; });
-                if (stop_) return;
-                seen = gen_;
+            const auto t0 = std::chrono::steady_clock::now();
+            int polls = 0;
+            while (gen_.load() == seen && !stop_.load()) {
+                __builtin_ia32_pause();
+                if (++polls < 256) continue;
+                polls = 0;
+                if (std::chrono::steady_clock::now() - t0 > std::chrono::microseconds(spin_us_)) {
+                    std::unique_lock<std::mutex> lk(mu_);
+                    sleepers_.fetch_add(1);
+                    cv_.wait(lk, [&] { return stop_.load() || gen_.load() != seen; });
+                    sleepers_.fetch_sub(1);
+                }
             }
-            drain();
+            if (stop_.load()) return;
+            busy_.fetch_add(1);
+            seen = gen_.load();
+            Job * j = cur_.load();
+            if (j && j->gen == seen) drain(j);
+            busy_.fetch_sub(1);
         }
     }
     const size_t min_part_;   // smallest part one worker copies
+    const int spin_us_;
     std::vector<std::thread> th_;
     std::mutex mu_;
-    std::condition_variable cv_, done_;
-    const std::function<void(int)> * job_ = nullptr;
-    int parts_ = 0, left_ = 0;
-    std::atomic<int> next_{0};
-    uint64_t gen_ = 0;
-    bool stop_ = false;
+    std::condition_variable cv_;
+    std::atomic<Job *> cur_{nullptr};
+    std::atomic<uint64_t> gen_{0};
+    std::atomic<int> busy_{0}, sleepers_{0};
+    std::atomic<bool> stop_{false};
+    uint64_t published_ = 0;
 };
 
-// Pinned staging for the host <-> device copies of graph_compute. Host tensors are pageable
-// (ggml's CPU buffers), and a copy from pageable memory crawls through the runtime's own small
-// bounce buffer. A large copy is cut into CHUNK-sized pieces that cycle through NSLOT pinned
-// slots: the copy workers fill (or drain) one slot while the DMA engine moves another. Slots are
-// reused only after the event of their last DMA has completed, and the ring continues from one
-// copy to the next. Measured on the 8B-shape layer's transfers (8-60 MB operands): chunks of 2 to
-// 16 MB and 4 to 8 slots perform alike (within 5%); below 2 MB, or with copy parts under 512 KB,
-// the per-chunk wake-ups of the copy workers and event waits cost more than the overlap gains.
-struct Stager {
+// Pinned staging of one copy direction. Host tensors are pageable (ggml's CPU buffers), and a
+// copy from pageable memory crawls through the runtime's own small bounce buffer, so every copy
+// passes through `nslot` pinned slots of `chunk` bytes: the copy workers fill (or drain) one slot
+// while the DMA engine moves another. A slot is reused only after the event of its last DMA has
+// completed. Uploads and downloads have a ring each, so neither waits for the other's slots.
+struct Ring {
     static constexpr int MAX_SLOT = 16;
-    size_t CHUNK = (size_t)8 << 20;   // MI355X_STAGE_CHUNK_KB overrides (tuning)
-    int NSLOT = 4;                    // MI355X_STAGE_SLOTS overrides (tuning), <= MAX_SLOT
+    size_t chunk = 0;
+    int nslot = 0;
     void * slot[MAX_SLOT] = {};
     hipEvent_t ev[MAX_SLOT] = {};
     bool pending[MAX_SLOT] = {};
-    int next = 0;    // the slot the next chunk of an upload takes
-    bool ready = false;
-    int init() {
-        if (ready) return MI355X_OK;
-        if (const char * e = getenv("MI355X_STAGE_CHUNK_KB")) {
-            const long v = atol(e);
-            if (v >= 64 && v <= (64 << 10)) CHUNK = (size_t)v << 10;
-        }
-        if (const char * e = getenv("MI355X_STAGE_SLOTS")) {
-            const int v = atoi(e);
-            if (v >= 2 && v <= MAX_SLOT) NSLOT = v;
-        }
-        for (int i = 0; i < NSLOT; i++) {
-            if (hipHostMalloc(&slot[i], CHUNK, hipHostMallocDefault) != hipSuccess ||
+    int init(size_t ch, int n) {
+        chunk = ch;
+        nslot = n;
+        for (int i = 0; i < n; i++) {
+            if (hipHostMalloc(&slot[i], ch, hipHostMallocDefault) != hipSuccess ||
                 hipEventCreateWithFlags(&ev[i], hipEventDisableTiming) != hipSuccess) {
                 (void)hipGetLastError();
                 release();
                 return MI355X_E_DEVICE;
             }
         }
-        ready = true;
         return MI355X_OK;
     }
     // wait until slot i's last DMA is done
@@ -248,9 +307,49 @@ struct Stager {
             ev[i] = nullptr;
             pending[i] = false;
         }
-        ready = false;
+        nslot = 0;
     }
 };
+
+// Rows of a device matrix to be copied into contiguous host rows once the compute-stream event
+// `after` has passed. `buf` is the device buffer the rows are in, `op` the queued op they belong
+// to.
+struct DlItem {
+    const char * dev;
+    size_t pitch;       // bytes between device rows
+    char * host;        // host rows
+    size_t hpitch;      // bytes between host rows
+    size_t width;       // bytes copied per row
+    int64_t rows;
+    const void * buf;
+    hipEvent_t after;
+    int op;
+};
+struct DlPiece {
+    int item;
+    int64_t r0, r1;
+};
+// An op whose outputs are queued: the first of its pieces, and how to compute it on the CPU if
+// the device cannot deliver them.
+struct DlOp {
+    size_t first_piece;
+    std::function<void()> redo;
+    RouteHealth * brk;
+    const char * route;
+};
+
+// Host-side accounting of the copies (mi355x_backend_host_stats).
+struct HostStats {
+    long calls = 0, fa_mirror_hits = 0, redone = 0;
+    double bytes_up = 0, bytes_down = 0;
+    double wall_s = 0, up_copy_s = 0, up_wait_s = 0, down_copy_s = 0, down_wait_s = 0;
+};
+
+double now_s() {
+    timespec t;
+    clock_gettime(CLOCK_MONOTONIC, &t);
+    return (double)t.tv_sec + 1e-9 * (double)t.tv_nsec;
+}
 
 struct WEntry {
     void * dev = nullptr;
@@ -299,6 +398,7 @@ struct mi355x_backend {
     DevBuf act, a16, scales, out, part, wstage, wconv, fa_q, fa_k, fa_v, fa_m, fa_o, fa_ws, moe_b, moe_ids, moe_o, moe_ws;
     DevBuf wscratch[4], moe_wscratch;   // per-call weights: unnamed, or over the cache budget
     DevBuf w16;                         // the decode-first form's tiled fp16 weights of one call
+    size_t w16_peak = 0;                // its largest size (outside the cache budget)
 
     std::unordered_map<std::string, WEntry> wcache;
     size_t cache_used = 0, cache_budget = 0;
@@ -313,7 +413,27 @@ struct mi355x_backend {
 
     RouteHealth brk_gemm, brk_fa, brk_moe;
 
-    Stager stage;                        // pinned slots of the host <-> device copies
+    // Host <-> device copies. Uploads run on `stream`, in order before the kernels that read
+    // them; downloads on `dstream`, queued by the ops (dl_*) and drained while later ops of the
+    // call upload and compute, and entirely before graph_compute returns.
+    hipStream_t dstream = nullptr;
+    hipStream_t ustream = nullptr;       // a row-chunked MUL_MAT's activation uploads
+    int row_chunk = -1;                  // rows per chunk of such a MUL_MAT (-1: by link bytes, 0: one)
+    Ring up, down;                       // pinned slots of each direction
+    bool staging_ready = false;
+    int up_next = 0;                     // the upload slot the next piece takes
+    size_t up_piece = 0;                 // size of the next upload piece (grows within an op)
+    size_t first_piece = 0, last_piece = 0;
+    std::vector<DlItem> dl_items;
+    std::vector<DlPiece> dl_pieces;
+    std::vector<DlOp> dl_ops;
+    size_t dl_issued = 0, dl_drained = 0;
+    int dl_waited_item = -1;             // the item whose event dstream last waited on
+    bool dl_broken = false;              // a piece failed while polled (dl_drain then recomputes)
+    std::vector<hipEvent_t> evpool;      // compute-stream events of queued outputs
+    size_t ev_used = 0;
+    int inject_drain = 0;                // test hook: the next n drained pieces report a failure
+    HostStats hs;
     std::unique_ptr<CopyPool> pool;      // n_threads copy workers, started with the device
 };
 
@@ -345,100 +465,320 @@ bool ensure_device(Ctx * c) {
     return true;
 }
 
-int sync(Ctx * c) {
-    return hipStreamSynchronize(c->stream) == hipSuccess ? MI355X_OK : MI355X_E_DEVICE;
-}
-
 #define TRY_RC(x) do { const int _r = (x); if (_r != MI355X_OK) return _r; } while (0)
 
-// Copies below STAGE_MIN bytes go straight from pageable memory (the runtime's path is fine
-// there); larger ones through the pinned slots.
-constexpr size_t STAGE_MIN = (size_t)1 << 20;
+// The copy pipeline's shape: `nslot` slots of `chunk` bytes per direction; an op's uploads start
+// with a piece of `first_piece` bytes that doubles up to the slot size, so its first DMA starts
+// after a short host copy rather than a whole slot's; each queued output ends with pieces that
+// halve down to `last_piece`, so the host copy left after its last DMA lands is short. Host copies
+// of POOL_MIN bytes or more are split over the copy workers (parts of at least COPY_PART);
+// smaller ones run on the calling thread.
+constexpr size_t POOL_MIN = (size_t)512 << 10;
+constexpr int64_t CHUNK_LINK_BYTES = (int64_t)8 << 20;
+constexpr size_t COPY_PART = (size_t)256 << 10;
 
+size_t env_kb(const char * name, size_t dflt, size_t lo, size_t hi) {
+    if (const char * e = getenv(name)) {
+        const long v = atol(e);
+        if (v >= (long)(lo >> 10) && v <= (long)(hi >> 10)) return (size_t)v << 10;
+    }
+    return dflt;
+}
+
+// The staging slots, the copy workers and the download stream, made on first use. Without them
+// no device op runs (the op falls back to the CPU).
 bool staging_on(Ctx * c) {
+    if (c->staging_ready) return true;
     if (!c->pool) {
-        size_t part = (size_t)1 << 20;   // MI355X_COPY_PART_KB overrides (tuning)
-        if (const char * e = getenv("MI355X_COPY_PART_KB")) {
-            const long v = atol(e);
-            if (v >= 16 && v <= (64 << 10)) part = (size_t)v << 10;
+        int spin = 300;   // microseconds a copy worker polls for the next job before it sleeps
+        if (const char * e = getenv("MI355X_COPY_SPIN_US")) spin = std::max(0, std::min(atoi(e), 100000));
+        c->pool.reset(new CopyPool(c->n_threads, env_kb("MI355X_COPY_PART_KB", COPY_PART, 16 << 10, 64 << 20), spin));
+    }
+    // rows per chunk of a MUL_MAT whose activations are uploaded: -1 sizes chunks by their link
+    // bytes, 0 runs one chunk, n > 0 forces n rows (a multiple of 16)
+    c->row_chunk = -1;
+    if (const char * e = getenv("MI355X_ROW_CHUNK")) c->row_chunk = std::max(0, atoi(e)) / 16 * 16;
+    const size_t chunk = env_kb("MI355X_STAGE_CHUNK_KB", (size_t)8 << 20, 64 << 10, (size_t)64 << 20);
+    int nslot = 4;
+    if (const char * e = getenv("MI355X_STAGE_SLOTS")) {
+        const int v = atoi(e);
+        if (v >= 2 && v <= Ring::MAX_SLOT) nslot = v;
+    }
+    c->first_piece = env_kb("MI355X_FIRST_PIECE_KB", (size_t)1 << 20, 64 << 10, chunk);
+    c->last_piece = env_kb("MI355X_LAST_PIECE_KB", (size_t)1 << 20, 64 << 10, chunk);
+    if (!c->dstream && hipStreamCreateWithFlags(&c->dstream, hipStreamNonBlocking) != hipSuccess) {
+        (void)hipGetLastError();
+        c->dstream = nullptr;
+        return false;
+    }
+    if (!c->ustream && hipStreamCreateWithFlags(&c->ustream, hipStreamNonBlocking) != hipSuccess) {
+        (void)hipGetLastError();
+        c->ustream = nullptr;
+        return false;
+    }
+    if (c->up.init(chunk, nslot) != MI355X_OK) return false;
+    if (c->down.init(chunk, nslot) != MI355X_OK) {
+        c->up.release();
+        return false;
+    }
+    c->up_piece = c->first_piece;
+    c->staging_ready = true;
+    return true;
+}
+
+void host_copy(Ctx * c, void * dst, const void * src, size_t n) {
+    if (n >= POOL_MIN) c->pool->copy(dst, src, n);
+    else copy_bytes(dst, src, n);
+}
+
+// whether an event has passed, without waiting (a not-ready answer leaves no error behind for
+// the next launch's error check)
+bool passed(hipEvent_t e) {
+    const hipError_t r = hipEventQuery(e);
+    if (r == hipErrorNotReady) {
+        (void)hipGetLastError();
+        return false;
+    }
+    return true;
+}
+
+// ---- the download queue -------------------------------------------------------------------
+// An op queues the rows of its outputs with the compute-stream event after which they are final,
+// and returns; the pieces are copied into the download slots on `dstream` and out of them by the
+// host while later ops of the call upload and compute. Everything queued is delivered before
+// graph_compute returns, before the host reads bytes a queued piece has yet to write, and before
+// an op writes or regrows a device buffer a queued piece still reads.
+
+// An event recorded on stream `st` now (reused once the queue has been drained).
+hipEvent_t mark_event_on(Ctx * c, hipStream_t st) {
+    if (c->ev_used == c->evpool.size()) {
+        hipEvent_t e = nullptr;
+        if (hipEventCreateWithFlags(&e, hipEventDisableTiming) != hipSuccess) {
+            (void)hipGetLastError();
+            return nullptr;
         }
-        c->pool.reset(new CopyPool(c->n_threads, part));
+        c->evpool.push_back(e);
     }
-    return c->stage.init() == MI355X_OK;
+    hipEvent_t e = c->evpool[c->ev_used];
+    if (hipEventRecord(e, st) != hipSuccess) return nullptr;
+    c->ev_used++;
+    return e;
 }
 
-// host -> device, enqueued on the stream; the host buffer may be reused once this returns
-int h2d(Ctx * c, void * dst, const void * src, size_t n) {
-    if (!n) return MI355X_OK;
-    if (n < STAGE_MIN || !staging_on(c))
-        return hipMemcpyAsync(dst, src, n, hipMemcpyHostToDevice, c->stream) == hipSuccess ? MI355X_OK
-                                                                                          : MI355X_E_DEVICE;
-    Stager & S = c->stage;
-    for (size_t o = 0; o < n; o += S.CHUNK) {
-        const int k = S.next;
-        S.next = (S.next + 1) % S.NSLOT;
-        const size_t len = std::min(S.CHUNK, n - o);
-        TRY_RC(S.settle(k));
-        c->pool->copy(S.slot[k], (const char *)src + o, len);
-        if (hipMemcpyAsync((char *)dst + o, S.slot[k], len, hipMemcpyHostToDevice, c->stream) != hipSuccess ||
-            hipEventRecord(S.ev[k], c->stream) != hipSuccess)
-            return MI355X_E_DEVICE;
-        S.pending[k] = true;
-    }
-    return MI355X_OK;
+hipEvent_t mark_event(Ctx * c) { return mark_event_on(c, c->stream); }
+
+int dl_op(Ctx * c, std::function<void()> redo, RouteHealth * brk, const char * route) {
+    c->dl_ops.push_back({c->dl_pieces.size(), std::move(redo), brk, route});
+    return (int)c->dl_ops.size() - 1;
 }
 
-// Rows [0, rows) of a device matrix with row pitch `pitch` bytes, `width` bytes used per row,
-// to host memory through the pinned slots, handing each landed block of rows to `take(r0, r1,
-// host_rows)` (host_rows = the staged rows, `width` bytes apart). Returns when all rows are in.
-int d2h_rows(Ctx * c, const void * src, size_t pitch, size_t width, int64_t rows,
-             const std::function<void(int64_t, int64_t, const char *)> & take) {
-    Stager & S = c->stage;
-    const int64_t per = std::max<int64_t>(1, (int64_t)(S.CHUNK / width));
-    const int64_t nchunk = (rows + per - 1) / per;
-    auto launch = [&](int64_t i) -> int {
-        const int k = (int)(i % S.NSLOT);
-        const int64_t r0 = i * per, r1 = std::min(rows, r0 + per);
-        const hipError_t e = pitch == width
-            ? hipMemcpyAsync(S.slot[k], (const char *)src + r0 * pitch, (size_t)(r1 - r0) * width,
-                             hipMemcpyDeviceToHost, c->stream)
-            : hipMemcpy2DAsync(S.slot[k], width, (const char *)src + r0 * pitch, pitch, width, (size_t)(r1 - r0),
-                               hipMemcpyDeviceToHost, c->stream);
-        if (e != hipSuccess || hipEventRecord(S.ev[k], c->stream) != hipSuccess) return MI355X_E_DEVICE;
-        S.pending[k] = true;
-        return MI355X_OK;
-    };
-    for (int64_t i = 0; i < std::min<int64_t>(nchunk, S.NSLOT); i++) TRY_RC(launch(i));
-    for (int64_t i = 0; i < nchunk; i++) {
-        const int k = (int)(i % S.NSLOT);
-        TRY_RC(S.settle(k));
-        const int64_t r0 = i * per, r1 = std::min(rows, r0 + per);
-        take(r0, r1, (const char *)S.slot[k]);
-        if (i + S.NSLOT < nchunk) TRY_RC(launch(i + S.NSLOT));
+// `rows` rows of `width` bytes, `pitch` apart at `dev` (inside device buffer `buf`), to host rows
+// `hpitch` apart at `host`, once `after` has passed.
+void dl_rows(Ctx * c, int op, const void * dev, size_t pitch, void * host, size_t hpitch, size_t width, int64_t rows,
+             const void * buf, hipEvent_t after, bool shrink = true) {
+    if (rows <= 0 || !width) return;
+    const size_t chunk = c->down.chunk;
+    if (width > chunk) {   // rows wider than a slot: column slices of at most a slot
+        for (size_t o = 0; o < width; o += chunk)
+            dl_rows(c, op, (const char *)dev + o, pitch, (char *)host + o, hpitch, std::min(chunk, width - o), rows,
+                    buf, after, shrink);
+        return;
     }
-    return MI355X_OK;
+    if (pitch == width && hpitch == width && rows > 1 && width < ((size_t)64 << 10)) {
+        // contiguous on both sides: copied as 64 KB rows, so pieces can be cut finely
+        const size_t n = (size_t)rows * width, W = (size_t)1 << 16;
+        const int64_t full = (int64_t)(n / W);
+        dl_rows(c, op, dev, W, host, W, W, full, buf, after, shrink && n % W == 0);
+        if (n % W)
+            dl_rows(c, op, (const char *)dev + full * W, n % W, (char *)host + full * W, n % W, n % W, 1, buf, after,
+                    shrink);
+        return;
+    }
+    const int item = (int)c->dl_items.size();
+    c->dl_items.push_back({(const char *)dev, pitch, (char *)host, hpitch, width, rows, buf, after, op});
+    // piece sizes from the end: last_piece, doubling up to the slot size (or whole slots)
+    const size_t first = c->dl_pieces.size();
+    size_t target = shrink ? c->last_piece : chunk;
+    for (int64_t r1 = rows; r1 > 0;) {
+        const int64_t per = std::max<int64_t>(1, (int64_t)(std::min(target, chunk) / width));
+        const int64_t r0 = std::max<int64_t>(0, r1 - per);
+        c->dl_pieces.push_back({item, r0, r1});
+        r1 = r0;
+        target = std::min(target * 2, chunk);
+    }
+    std::reverse(c->dl_pieces.begin() + (ptrdiff_t)first, c->dl_pieces.end());
+    c->hs.bytes_down += (double)width * (double)rows;
 }
 
-// device -> host; returns when the bytes are in `dst` (it synchronizes on the copies)
-int d2h(Ctx * c, void * dst, const void * src, size_t n) {
-    if (!n) return MI355X_OK;
-    if (n < STAGE_MIN || !staging_on(c)) {
-        if (hipMemcpyAsync(dst, src, n, hipMemcpyDeviceToHost, c->stream) != hipSuccess) return MI355X_E_DEVICE;
-        return hipStreamSynchronize(c->stream) == hipSuccess ? MI355X_OK : MI355X_E_DEVICE;
-    }
-    const size_t W = 1 << 16;   // stage as rows of 64 KB (+ one short tail)
+// n contiguous bytes, as rows of 64 KB and a short last row
+void dl_bytes(Ctx * c, int op, const void * dev, void * host, size_t n, const void * buf, hipEvent_t after) {
+    const size_t W = (size_t)1 << 16;
     const int64_t full = (int64_t)(n / W);
-    TRY_RC(d2h_rows(c, src, W, W, full, [&](int64_t r0, int64_t r1, const char * h) {
-        c->pool->copy((char *)dst + r0 * W, h, (size_t)(r1 - r0) * W);
-    }));
-    if (n % W) {
-        if (hipMemcpyAsync((char *)dst + full * W, (const char *)src + full * W, n % W, hipMemcpyDeviceToHost,
-                           c->stream) != hipSuccess)
-            return MI355X_E_DEVICE;
-        return hipStreamSynchronize(c->stream) == hipSuccess ? MI355X_OK : MI355X_E_DEVICE;
+    dl_rows(c, op, dev, W, host, W, W, full, buf, after, n % W == 0);
+    if (n % W) dl_rows(c, op, (const char *)dev + full * W, n % W, (char *)host + full * W, n % W, n % W, 1, buf, after);
+}
+
+// Starts the DMAs of queued pieces into free download slots.
+int dl_issue(Ctx * c) {
+    Ring & R = c->down;
+    while (c->dl_issued < c->dl_pieces.size() && c->dl_issued < c->dl_drained + (size_t)R.nslot) {
+        const DlPiece & p = c->dl_pieces[c->dl_issued];
+        const DlItem & it = c->dl_items[(size_t)p.item];
+        const int k = (int)(c->dl_issued % (size_t)R.nslot);   // its previous piece has been drained
+        if (p.item != c->dl_waited_item) {
+            if (it.after && hipStreamWaitEvent(c->dstream, it.after, 0) != hipSuccess) return MI355X_E_DEVICE;
+            c->dl_waited_item = p.item;
+        }
+        const size_t rows = (size_t)(p.r1 - p.r0);
+        const char * src = it.dev + (size_t)p.r0 * it.pitch;
+        const hipError_t e =
+            it.pitch == it.width
+                ? hipMemcpyAsync(R.slot[k], src, rows * it.width, hipMemcpyDeviceToHost, c->dstream)
+                : hipMemcpy2DAsync(R.slot[k], it.width, src, it.pitch, it.width, rows, hipMemcpyDeviceToHost, c->dstream);
+        if (e != hipSuccess || hipEventRecord(R.ev[k], c->dstream) != hipSuccess) return MI355X_E_DEVICE;
+        R.pending[k] = true;
+        c->dl_issued++;
     }
     return MI355X_OK;
 }
+
+// Copies the oldest issued piece out of its slot once its DMA has landed.
+int dl_drain_one(Ctx * c) {
+    Ring & R = c->down;
+    const DlPiece & p = c->dl_pieces[c->dl_drained];
+    const DlItem & it = c->dl_items[(size_t)p.item];
+    const int k = (int)(c->dl_drained % (size_t)R.nslot);
+    const double t0 = now_s();
+    const int rc = R.settle(k);
+    const double t1 = now_s();
+    c->hs.down_wait_s += t1 - t0;
+    if (rc != MI355X_OK) return rc;
+    if (c->inject_drain > 0) {
+        c->inject_drain--;
+        return MI355X_E_DEVICE;
+    }
+    const int64_t rows = p.r1 - p.r0;
+    char * h = it.host + (size_t)p.r0 * it.hpitch;
+    const char * s = (const char *)R.slot[k];
+    if (it.hpitch == it.width) {
+        host_copy(c, h, s, (size_t)rows * it.width);
+    } else {
+        const int parts = (int)std::min<int64_t>(c->pool->threads(),
+                                                 std::max<int64_t>(1, (int64_t)((size_t)rows * it.width / COPY_PART)));
+        c->pool->run(parts, [&](int pi) {
+            for (int64_t r = rows * pi / parts; r < rows * (pi + 1) / parts; r++)
+                memcpy(h + (size_t)r * it.hpitch, s + (size_t)r * it.width, it.width);
+        });
+    }
+    c->hs.down_copy_s += now_s() - t1;
+    c->dl_drained++;
+    return MI355X_OK;
+}
+
+// Copies out the issued pieces whose DMA has landed, without waiting for the others. A piece
+// that fails here marks the queue broken, which the next dl_drain handles.
+void dl_poll(Ctx * c) {
+    while (!c->dl_broken && c->dl_drained < c->dl_issued) {
+        const int k = (int)(c->dl_drained % (size_t)c->down.nslot);
+        if (c->down.pending[k] && !passed(c->down.ev[k])) break;
+        if (dl_drain_one(c) != MI355X_OK || dl_issue(c) != MI355X_OK) c->dl_broken = true;
+    }
+}
+
+void dl_reset(Ctx * c) {
+    c->dl_broken = false;
+    c->dl_items.clear();
+    c->dl_pieces.clear();
+    c->dl_ops.clear();
+    c->dl_issued = c->dl_drained = 0;
+    c->dl_waited_item = -1;
+    c->ev_used = 0;
+}
+
+// Delivers everything queued. The op whose piece the device could not deliver is computed again
+// on the CPU (a device failure on its route), and so is every op queued after it, since those
+// may have read its device result.
+void dl_drain(Ctx * c) {
+    int rc = c->dl_broken ? MI355X_E_DEVICE : MI355X_OK;
+    while (rc == MI355X_OK && c->dl_drained < c->dl_pieces.size()) {
+        rc = dl_issue(c);
+        if (rc == MI355X_OK) rc = dl_drain_one(c);
+    }
+    if (rc != MI355X_OK && c->dl_drained < c->dl_pieces.size()) {
+        const size_t bad = (size_t)c->dl_items[(size_t)c->dl_pieces[c->dl_drained].item].op;
+        for (int i = 0; i < Ring::MAX_SLOT; i++)
+            if (c->down.pending[i]) {
+                (void)hipEventSynchronize(c->down.ev[i]);
+                c->down.pending[i] = false;
+            }
+        (void)hipGetLastError();
+        for (size_t o = bad; o < c->dl_ops.size(); o++) {
+            DlOp & op = c->dl_ops[o];
+            logw("%s: its device result could not be copied back; computed on the CPU\n", op.route);
+            op.brk->failures++;
+            op.redo();
+            c->n_cpu_fallbacks++;
+            c->hs.redone++;
+        }
+    }
+    dl_reset(c);
+}
+
+// whether a queued piece has yet to write host bytes in [p, p + n)
+bool dl_writes_host(const Ctx * c, const void * p, size_t n) {
+    if (c->dl_drained == c->dl_pieces.size() || !p || !n) return false;
+    const char * a = (const char *)p;
+    for (size_t i = (size_t)c->dl_pieces[c->dl_drained].item; i < c->dl_items.size(); i++) {
+        const DlItem & it = c->dl_items[i];
+        const char * h = it.host;
+        const char * e = h + (size_t)(it.rows - 1) * it.hpitch + it.width;
+        if (a < e && h < a + n) return true;
+    }
+    return false;
+}
+
+// whether a queued piece still reads device buffer `buf`
+bool dl_reads_buf(const Ctx * c, const void * buf) {
+    if (c->dl_drained == c->dl_pieces.size() || !buf) return false;
+    for (size_t i = (size_t)c->dl_pieces[c->dl_drained].item; i < c->dl_items.size(); i++)
+        if (c->dl_items[i].buf == buf) return true;
+    return false;
+}
+
+// host -> device on stream `st`, through the upload slots; the host bytes may be reused once
+// this returns
+int upload_on(Ctx * c, hipStream_t st, void * dst, const void * src, size_t n) {
+    if (!n) return MI355X_OK;
+    if (!staging_on(c)) return MI355X_E_DEVICE;
+    if (dl_writes_host(c, src, n)) dl_drain(c);
+    Ring & R = c->up;
+    for (size_t o = 0; o < n;) {
+        const size_t len = std::min(std::min(c->up_piece, R.chunk), n - o);
+        const int k = c->up_next;
+        c->up_next = (k + 1) % R.nslot;
+        const double t0 = now_s();
+        TRY_RC(R.settle(k));
+        const double t1 = now_s();
+        host_copy(c, R.slot[k], (const char *)src + o, len);
+        c->hs.up_wait_s += t1 - t0;
+        c->hs.up_copy_s += now_s() - t1;
+        if (hipMemcpyAsync((char *)dst + o, R.slot[k], len, hipMemcpyHostToDevice, st) != hipSuccess ||
+            hipEventRecord(R.ev[k], st) != hipSuccess)
+            return MI355X_E_DEVICE;
+        R.pending[k] = true;
+        o += len;
+        c->up_piece = std::min(c->up_piece * 2, R.chunk);
+        if (c->dl_issued > c->dl_drained) dl_poll(c);   // results that landed meanwhile
+    }
+    c->hs.bytes_up += (double)n;
+    return MI355X_OK;
+}
+
+// host -> device on the compute stream, ahead of the kernels that read it
+int upload(Ctx * c, void * dst, const void * src, size_t n) { return upload_on(c, c->stream, dst, src, n); }
+
+// the start of a device op: its uploads begin with a short piece again
+void begin_op(Ctx * c) { c->up_piece = c->first_piece; }
 
 #define TRY(x) do { const int _rc = (x); if (_rc != MI355X_OK) return _rc; } while (0)
 
@@ -474,12 +814,12 @@ int build_weight(Ctx * c, int t, const void * src, int64_t rows, int64_t K, int 
         return build_weight(c, MI355X_TYPE_F32, f.data(), rows, K, lay, dst);
     }
     const size_t raw = (size_t)row_bytes(t, K) * (size_t)rows;
-    if ((t == MI355X_TYPE_F16 || t == MI355X_TYPE_Q4_K || t == MI355X_TYPE_Q5_K) && lay == t) return h2d(c, dst, src, raw);
-    TRY(c->wstage.ensure(raw));
-    TRY(h2d(c, c->wstage.p, src, raw));
+    if ((t == MI355X_TYPE_F16 || t == MI355X_TYPE_Q4_K || t == MI355X_TYPE_Q5_K) && lay == t) return upload(c, dst, src, raw);
+    TRY(c->wstage.ensure(raw, c->stream));
+    TRY(upload(c, c->wstage.p, src, raw));
     if (t == MI355X_TYPE_F32 || t == MI355X_TYPE_BF16) {
         if (lay == MI355X_F16) return mi355x_convert_f16(t, c->wstage.p, rows * K, (uint16_t *)dst, c->stream);
-        TRY(c->wconv.ensure((size_t)rows * K * 2));
+        TRY(c->wconv.ensure((size_t)rows * K * 2, c->stream));
         TRY(mi355x_convert_f16(t, c->wstage.p, rows * K, (uint16_t *)c->wconv.p, c->stream));
         return mi355x_weight_f16_tiled(MI355X_F16, c->wconv.p, rows, K, (uint16_t *)dst, c->stream);
     }
@@ -488,7 +828,7 @@ int build_weight(Ctx * c, int t, const void * src, int64_t rows, int64_t K, int 
     // -> fp16: from the HBM layout, built first when that differs from the ggml one
     const void * q = c->wstage.p;
     if (t == MI355X_TYPE_Q4_0 || t == MI355X_TYPE_Q8_0 || t == MI355X_TYPE_Q6_K || t == MI355X_TYPE_MXFP4) {
-        TRY(c->wconv.ensure(raw));
+        TRY(c->wconv.ensure(raw, c->stream));
         TRY(mi355x_weight_pack(t, c->wstage.p, rows, K, c->wconv.p, c->stream));
         q = c->wconv.p;
     }
@@ -560,7 +900,7 @@ int get_weight(Ctx * c, const mi355x_tensor * a, int64_t rows, int64_t K, bool w
         oc.streamed.insert(key);
     }
     oc.per_call++;
-    TRY(scratch.ensure((size_t)dbytes));
+    TRY(scratch.ensure((size_t)dbytes, c->stream));
     TRY(build_weight(c, a->type, a->data, rows, K, lay, scratch.p));
     out.dev = scratch.p;
     out.bytes = (size_t)dbytes;
@@ -573,15 +913,17 @@ int get_weight(Ctx * c, const mi355x_tensor * a, int64_t rows, int64_t K, bool w
 
 // ---- MUL_MAT (one node or a fused group sharing src1) ---------------------------------------
 int mul_mat_device(Ctx * c, const std::vector<mi355x_tensor *> & grp, bool want_f16, bool & all_resident) {
-    if (!ensure_device(c)) return MI355X_E_DEVICE;
+    if (!ensure_device(c) || !staging_on(c)) return MI355X_E_DEVICE;
+    begin_op(c);
+    if (dl_reads_buf(c, c->out.p)) dl_drain(c);   // out is rewritten (and may regrow) below
     const mi355x_tensor * b = grp[0]->src[1];
     const int64_t K = b->ne[0], M = b->ne[1] * b->ne[2] * b->ne[3];
-    TRY(c->act.ensure((size_t)M * K * 4));
-    TRY(c->a16.ensure((size_t)((M + 15) / 16 * 16) * K * 2));
-    TRY(c->scales.ensure((size_t)M * 4));
+    TRY(c->act.ensure((size_t)M * K * 4, c->stream));
+    TRY(c->a16.ensure((size_t)((M + 15) / 16 * 16) * K * 2, c->stream));
+    TRY(c->scales.ensure((size_t)M * 4, c->stream));
     int64_t ntot = 0;
     for (auto * d : grp) ntot += d->src[0]->ne[1];
-    TRY(c->out.ensure((size_t)M * ntot * 4));
+    TRY(c->out.ensure((size_t)M * ntot * 4, c->stream));
     std::vector<WEntry> ws(grp.size());
     all_resident = true;
     mi355x_gemm_out outs[4];
@@ -595,12 +937,14 @@ int mul_mat_device(Ctx * c, const std::vector<mi355x_tensor *> & grp, bool want_
         outs[i].rows_total = a->ne[1];
         outs[i].row0 = 0;
         outs[i].N = a->ne[1];
-        outs[i].c_dev = (float *)c->out.p + col;
-        outs[i].ldc = ntot;
+        outs[i].c_dev = (float *)c->out.p + M * col;   // member i's [M][N_i], so it comes back in one run
+        outs[i].ldc = a->ne[1];
         col += a->ne[1];
     }
-    // Q8_0 / Q6_K weights at the shapes where one decode pass plus the fp16 GEMM is faster than
-    // decoding inside the GEMM: each member decoded into tiled fp16 scratch first
+    // Quantized weights (Q4_0, Q8_0, Q4_K, Q5_K, Q6_K, MXFP4) at the shapes where one decode
+    // pass plus the fp16 GEMM is faster than decoding inside the GEMM
+    // (mi355x_mul_mat_decode_first): each member decoded into tiled fp16 scratch first. That
+    // scratch lives outside the weight cache's budget; its peak size is in the teardown report.
     int gtype = ws[0].dev_type;
     bool same = true;
     for (auto & w : ws) same = same && w.dev_type == gtype;
@@ -608,7 +952,8 @@ int mul_mat_device(Ctx * c, const std::vector<mi355x_tensor *> & grp, bool want_
         std::vector<size_t> off(grp.size() + 1, 0);
         for (size_t i = 0; i < grp.size(); i++)
             off[i + 1] = off[i] + (((size_t)mi355x_weight_bytes(MI355X_F16_T, outs[i].N, K) + 255) & ~(size_t)255);
-        TRY(c->w16.ensure(off.back()));
+        TRY(c->w16.ensure(off.back(), c->stream));
+        c->w16_peak = std::max(c->w16_peak, c->w16.cap);
         for (size_t i = 0; i < grp.size(); i++) {
             uint16_t * w16 = (uint16_t *)((char *)c->w16.p + off[i]);
             TRY(mi355x_weight_f16_tiled(gtype, outs[i].w_dev, outs[i].N, K, w16, c->stream));
@@ -616,85 +961,124 @@ int mul_mat_device(Ctx * c, const std::vector<mi355x_tensor *> & grp, bool want_
         }
         gtype = MI355X_F16_T;
     }
-    // K-split partials, summed in a fixed order (reproducible results); a two-way split adds
-    // into the outputs, which the activation pack then clears in the same launch
-    const size_t pbytes = mi355x_gemm_workspace(gtype, M, K, outs, (int)grp.size());
-    if (pbytes) TRY(c->part.ensure(pbytes));
-    const int acc = mi355x_gemm_accumulates(gtype, M, K, outs, (int)grp.size(), pbytes);
-    if (acc < 0) return acc;
     // src1 from the attention this call just computed (same host bytes, row-major F32): its
     // device copy; otherwise uploaded
     const float * act = (const float *)c->act.p;
     const bool dense = b->type == MI355X_TYPE_F32 && b->nb[0] == 4 && b->nb[1] == (size_t)K * 4 &&
                        b->nb[2] == b->nb[1] * (size_t)b->ne[1] && b->nb[3] == b->nb[2] * (size_t)b->ne[2];
-    if (dense && c->fa_mirror.dev && b->data == c->fa_mirror.host && (size_t)M * K * 4 <= c->fa_mirror.bytes)
+    const bool mirrored = dense && c->fa_mirror.dev && b->data == c->fa_mirror.host &&
+                          (size_t)M * K * 4 <= c->fa_mirror.bytes;
+    if (mirrored) {
         act = (const float *)c->fa_mirror.dev;
-    else
-        TRY(h2d(c, c->act.p, b->data, (size_t)M * K * 4));
-    const int tiled = gtype == MI355X_F16_T;
-    if (acc)   // the outputs are the ntot columns of c->out
-        TRY(mi355x_pack_act_clear(tiled, act, K, M, K, (uint16_t *)c->a16.p, (float *)c->scales.p, (float *)c->out.p,
-                                  ntot, ntot, c->stream));
-    else if (tiled)
-        TRY(mi355x_pack_act_tiled(act, K, M, K, (uint16_t *)c->a16.p, (float *)c->scales.p, c->stream));
-    else
-        TRY(mi355x_pack_act(act, K, M, K, (uint16_t *)c->a16.p, (float *)c->scales.p, c->stream));
-    TRY(mi355x_gemm_ws(gtype, (const uint16_t *)c->a16.p, (const float *)c->scales.p, M, K, outs,
-                       (int)grp.size(), pbytes ? c->part.p : nullptr, pbytes, acc ? MI355X_GEMM_OUT_ZEROED : 0,
-                       c->stream));
-    // dst[i] is [N_i, M] contiguous: one member takes the output as is; a group's outputs come
-    // back as whole rows of the concatenated [M][ntot] and are split into the members' column
-    // blocks on the host
-    if (grp.size() == 1) {
-        TRY(d2h(c, grp[0]->data, c->out.p, (size_t)M * ntot * 4));
-        return sync(c);
+        c->hs.fa_mirror_hits++;
     }
-    if ((size_t)M * ntot * 4 < STAGE_MIN || !staging_on(c) || (size_t)ntot * 4 > c->stage.CHUNK) {
-        col = 0;
-        for (auto * d : grp) {
-            const int64_t N = d->src[0]->ne[1];
-            if (hipMemcpy2DAsync(d->data, (size_t)N * 4, (const float *)c->out.p + col, (size_t)ntot * 4,
-                                 (size_t)N * 4, (size_t)M, hipMemcpyDeviceToHost, c->stream) != hipSuccess)
-                return MI355X_E_DEVICE;
-            col += N;
+    // Uploaded activations run in chunks of row_chunk rows: chunk j's rows go up on the upload
+    // stream while chunk j-1 is packed and multiplied on the compute stream and the result rows of
+    // earlier chunks come back, so the link, the kernels and the host copies overlap. The upload
+    // stream first waits for the compute stream's earlier readers of the activation buffer.
+    // By default a chunk carries about CHUNK_LINK_BYTES over the link (its activations up, its
+    // results down), in 128-row steps: measured on the 8B-shape layer's calls at M 512, that is
+    // 256-row chunks for Q/K/V (40 KB a row; 128-row chunks made its narrow GEMMs slower than the
+    // overlap gained), 128 for gate/up (128 KB a row) and down (73 KB a row).
+    int64_t R = M;
+    if (!mirrored && c->row_chunk > 0) {
+        R = c->row_chunk;
+    } else if (!mirrored && c->row_chunk < 0) {
+        const int64_t per_row = K * 4 + ntot * 4;
+        R = std::max<int64_t>(128, (CHUNK_LINK_BYTES / per_row + 127) / 128 * 128);
+    }
+    if (M < 2 * R) R = M;
+    const int n_out = (int)grp.size();
+    auto chunk_outs = [&](int64_t r0, mi355x_gemm_out * o) {
+        for (int i = 0; i < n_out; i++) {
+            o[i] = outs[i];
+            o[i].c_dev = outs[i].c_dev + r0 * outs[i].ldc;
         }
-        return sync(c);
+    };
+    // K-split partials, summed in a fixed order (reproducible results), sized for the largest
+    // chunk; a two-way split adds into the outputs, which the activation pack then clears in the
+    // same launch
+    size_t pmax = 0;
+    for (const int64_t m : {R, M % R}) {
+        if (!m) continue;
+        mi355x_gemm_out o[4];
+        chunk_outs(0, o);
+        pmax = std::max(pmax, mi355x_gemm_workspace(gtype, m, K, o, n_out));
     }
-    TRY(d2h_rows(c, c->out.p, (size_t)ntot * 4, (size_t)ntot * 4, M, [&](int64_t r0, int64_t r1, const char * h) {
-        const int64_t nr = r1 - r0;
-        const int parts = (int)std::min<int64_t>(c->pool->threads(), nr);
-        c->pool->run(parts, [&](int pi) {
-            for (int64_t r = r0 + nr * pi / parts; r < r0 + nr * (pi + 1) / parts; r++) {
-                int64_t cc = 0;
-                for (auto * d : grp) {
-                    const int64_t N = d->src[0]->ne[1];
-                    memcpy((char *)d->data + (size_t)r * N * 4, h + (size_t)(r - r0) * ntot * 4 + (size_t)cc * 4,
-                           (size_t)N * 4);
-                    cc += N;
-                }
+    if (pmax) TRY(c->part.ensure(pmax, c->stream));
+    if (R < M) {
+        hipEvent_t ready = mark_event(c);
+        if (!ready || hipStreamWaitEvent(c->ustream, ready, 0) != hipSuccess) return MI355X_E_DEVICE;
+    }
+    const int tiled = gtype == MI355X_F16_T;
+    const int op = dl_op(c, [grp] { for (auto * d : grp) cpu_mul_mat(d); }, &c->brk_gemm, "MUL_MAT");
+    for (int64_t r0 = 0; r0 < M; r0 += R) {
+        const int64_t m = std::min(R, M - r0);
+        mi355x_gemm_out o[4];
+        chunk_outs(r0, o);
+        const size_t pbytes = mi355x_gemm_workspace(gtype, m, K, o, n_out);
+        const int acc = mi355x_gemm_accumulates(gtype, m, K, o, n_out, pbytes);
+        if (acc < 0) return acc;
+        if (!mirrored) {
+            const size_t xb = (size_t)m * K * 4;
+            float * x = (float *)c->act.p + r0 * K;
+            if (R < M) {
+                TRY(upload_on(c, c->ustream, x, (const char *)b->data + (size_t)r0 * K * 4, xb));
+                hipEvent_t up = mark_event_on(c, c->ustream);
+                if (!up || hipStreamWaitEvent(c->stream, up, 0) != hipSuccess) return MI355X_E_DEVICE;
+            } else {
+                TRY(upload(c, x, b->data, xb));
             }
-        });
-    }));
-    return sync(c);
+        }
+        const float * x = act + r0 * K;
+        uint16_t * a16 = (uint16_t *)c->a16.p + r0 * K;   // row r0 (a multiple of 16) of either layout
+        float * sc = (float *)c->scales.p + r0;
+        if (acc && n_out == 1) {   // the pack clears the output rows the split adds into
+            TRY(mi355x_pack_act_clear(tiled, x, K, m, K, a16, sc, o[0].c_dev, o[0].ldc, o[0].N, c->stream));
+        } else {
+            for (int i = 0; acc && i < n_out; i++)   // a group's outputs are separate blocks
+                if (hipMemsetAsync(o[i].c_dev, 0, (size_t)m * (size_t)o[i].N * 4, c->stream) != hipSuccess)
+                    return MI355X_E_DEVICE;
+            if (tiled) TRY(mi355x_pack_act_tiled(x, K, m, K, a16, sc, c->stream));
+            else TRY(mi355x_pack_act(x, K, m, K, a16, sc, c->stream));
+        }
+        TRY(mi355x_gemm_ws(gtype, a16, sc, m, K, o, n_out, pbytes ? c->part.p : nullptr, pbytes,
+                           acc ? MI355X_GEMM_OUT_ZEROED : 0, c->stream));
+        // dst[i] is [N_i, M] contiguous, as member i's output block: these rows are queued for
+        // download behind the GEMM, ending in short pieces after the op's last chunk only
+        hipEvent_t done = mark_event(c);
+        if (!done) return MI355X_E_DEVICE;
+        const bool last = r0 + m == M;
+        for (int i = 0; i < n_out; i++) {
+            const size_t w = (size_t)o[i].N * 4;
+            dl_rows(c, op, o[i].c_dev, w, (float *)grp[(size_t)i]->data + r0 * o[i].N, w, w, m, c->out.p, done,
+                    last && i == n_out - 1);
+        }
+        TRY(dl_issue(c));
+        if (R < M) dl_poll(c);
+    }
+    return MI355X_OK;
 }
 
 // ---- FLASH_ATTN_EXT ---------------------------------------------------------------------------
 int flash_attn_device(Ctx * c, mi355x_tensor * dst) {
-    if (!ensure_device(c)) return MI355X_E_DEVICE;
+    if (!ensure_device(c) || !staging_on(c)) return MI355X_E_DEVICE;
+    begin_op(c);
+    if (dl_reads_buf(c, c->fa_o.p)) dl_drain(c);   // fa_o is rewritten (and may regrow) below
     const mi355x_tensor * q = dst->src[0];
     const mi355x_tensor * k = dst->src[1];
     const mi355x_tensor * v = dst->src[2];
     const mi355x_tensor * m = dst->src[3];
     const size_t qb = nbytes(q), kb = nbytes(k), vb = nbytes(v), mb = m ? nbytes(m) : 0, ob = nbytes(dst);
-    TRY(c->fa_q.ensure(qb));
-    TRY(c->fa_k.ensure(kb));
-    TRY(c->fa_v.ensure(vb));
-    if (m) TRY(c->fa_m.ensure(mb));
-    TRY(c->fa_o.ensure(ob));
-    TRY(h2d(c, c->fa_q.p, q->data, qb));
-    TRY(h2d(c, c->fa_k.p, k->data, kb));
-    TRY(h2d(c, c->fa_v.p, v->data, vb));
-    if (m) TRY(h2d(c, c->fa_m.p, m->data, mb));
+    TRY(c->fa_q.ensure(qb, c->stream));
+    TRY(c->fa_k.ensure(kb, c->stream));
+    TRY(c->fa_v.ensure(vb, c->stream));
+    if (m) TRY(c->fa_m.ensure(mb, c->stream));
+    TRY(c->fa_o.ensure(ob, c->stream));
+    TRY(upload(c, c->fa_q.p, q->data, qb));
+    TRY(upload(c, c->fa_k.p, k->data, kb));
+    TRY(upload(c, c->fa_v.p, v->data, vb));
+    if (m) TRY(upload(c, c->fa_m.p, m->data, mb));
     mi355x_fa_args a;
     memset(&a, 0, sizeof a);
     a.q_dev = (const float *)c->fa_q.p;
@@ -721,21 +1105,25 @@ int flash_attn_device(Ctx * c, mi355x_tensor * dst) {
     memcpy(&a.max_bias, &dst->op_params[1], 4);
     memcpy(&a.softcap, &dst->op_params[2], 4);
     const size_t ws = mi355x_flash_attn_workspace(&a, 0);
-    if (ws) TRY(c->fa_ws.ensure(ws));
+    if (ws) TRY(c->fa_ws.ensure(ws, c->stream));
     TRY(mi355x_flash_attn(&a, 0, ws ? c->fa_ws.p : nullptr, ws, c->stream));
-    TRY(d2h(c, dst->data, c->fa_o.p, ob));
-    TRY(sync(c));
+    hipEvent_t done = mark_event(c);
+    if (!done) return MI355X_E_DEVICE;
+    const int op = dl_op(c, [dst] { cpu_flash_attn(dst); }, &c->brk_fa, "FLASH_ATTN_EXT");
+    dl_bytes(c, op, c->fa_o.p, dst->data, ob, c->fa_o.p, done);
     if (c->mirror_ok) {
         c->fa_mirror.host = dst->data;
         c->fa_mirror.bytes = ob;
         c->fa_mirror.dev = c->fa_o.p;
     }
-    return MI355X_OK;
+    return dl_issue(c);
 }
 
 // ---- MUL_MAT_ID -------------------------------------------------------------------------------
 int mul_mat_id_device(Ctx * c, mi355x_tensor * dst, bool & resident) {
-    if (!ensure_device(c)) return MI355X_E_DEVICE;
+    if (!ensure_device(c) || !staging_on(c)) return MI355X_E_DEVICE;
+    begin_op(c);
+    if (dl_reads_buf(c, c->moe_o.p)) dl_drain(c);   // moe_o is rewritten (and may regrow) below
     const mi355x_tensor * as = dst->src[0];
     const mi355x_tensor * b = dst->src[1];
     const mi355x_tensor * ids = dst->src[2];
@@ -748,16 +1136,16 @@ int mul_mat_id_device(Ctx * c, mi355x_tensor * dst, bool & resident) {
     WEntry w;
     TRY(get_weight(c, &panel, N * E, K, false, false, N, c->moe_wscratch, w, resident));
     const size_t bb = (size_t)T * ne11 * K * 4, ib = (size_t)T * U * 4, ob = (size_t)T * U * N * 4;
-    TRY(c->moe_b.ensure(bb));
-    TRY(c->moe_ids.ensure(ib));
-    TRY(c->moe_o.ensure(ob));
-    TRY(h2d(c, c->moe_b.p, b->data, bb));
+    TRY(c->moe_b.ensure(bb, c->stream));
+    TRY(c->moe_ids.ensure(ib, c->stream));
+    TRY(c->moe_o.ensure(ob, c->stream));
+    TRY(upload(c, c->moe_b.p, b->data, bb));
     // ids may be a strided view: pack it to [T][U] on the host side of the copy
     std::vector<int32_t> idh((size_t)T * U);
     for (int64_t t = 0; t < T; t++)
         for (int64_t s = 0; s < U; s++)
             idh[t * U + s] = *(const int32_t *)((const char *)ids->data + t * ids->nb[1] + s * ids->nb[0]);
-    TRY(h2d(c, c->moe_ids.p, idh.data(), ib));
+    TRY(upload(c, c->moe_ids.p, idh.data(), ib));
     mi355x_moe_args a;
     memset(&a, 0, sizeof a);
     a.wtype = w.dev_type;
@@ -778,10 +1166,13 @@ int mul_mat_id_device(Ctx * c, mi355x_tensor * dst, bool & resident) {
     a.dst_nb1 = N;
     a.dst_nb2 = U * N;
     const size_t ws = mi355x_mul_mat_id_workspace(&a);
-    TRY(c->moe_ws.ensure(ws));
+    TRY(c->moe_ws.ensure(ws, c->stream));
     TRY(mi355x_mul_mat_id(&a, c->moe_ws.p, ws, nullptr, c->stream));
-    TRY(d2h(c, dst->data, c->moe_o.p, ob));
-    return sync(c);
+    hipEvent_t done = mark_event(c);
+    if (!done) return MI355X_E_DEVICE;
+    const int op = dl_op(c, [dst] { cpu_mul_mat_id(dst); }, &c->brk_moe, "MUL_MAT_ID");
+    dl_bytes(c, op, c->moe_o.p, dst->data, ob, c->moe_o.p, done);
+    return dl_issue(c);
 }
 
 // Runs a device job under a breaker; on a device failure (or an open breaker) runs `fallback`.
@@ -799,6 +1190,7 @@ void guarded(Ctx * c, RouteHealth & brk, const char * route, Dev && dev, Fb && f
         brk.record(rc, route);
     }
     if (rc != MI355X_OK) {
+        dl_drain(c);   // the CPU reads host bytes that queued outputs may still have to write
         fallback();
         c->n_cpu_fallbacks++;
     }
@@ -848,6 +1240,27 @@ MI355X_API void mi355x_backend_get_memory(size_t * fr, size_t * tot) {
     if (tot) *tot = t;
 }
 
+MI355X_API void mi355x_backend_get_host_memory(size_t * fr, size_t * tot) {
+    size_t total = 0, avail = 0;
+    if (FILE * f = fopen("/proc/meminfo", "r")) {
+        char line[256];
+        int found = 0;
+        while (found < 2 && fgets(line, sizeof line, f)) {
+            unsigned long long kb = 0;
+            if (sscanf(line, "MemTotal: %llu kB", &kb) == 1) {
+                total = (size_t)kb << 10;
+                found++;
+            } else if (sscanf(line, "MemAvailable: %llu kB", &kb) == 1) {
+                avail = (size_t)kb << 10;
+                found++;
+            }
+        }
+        fclose(f);
+    }
+    if (fr) *fr = std::min(avail, total);
+    if (tot) *tot = total;
+}
+
 MI355X_API mi355x_backend_t mi355x_backend_init(void) {
     Ctx * c = new Ctx();
     int nt = knob_int("N_THREADS", 5);
@@ -888,6 +1301,14 @@ void report_residency(const Ctx * c) {
     }
 }
 
+// The decode-first scratch: per-call HBM beside the cache budget, so a run near that budget
+// can see where the rest went.
+void report_scratch(const Ctx * c) {
+    if (c->w16_peak)
+        logi("[dq-scratch] per-call fp16 decode of quantized weights peaked at %.1f MB of HBM, outside the "
+             "%.0f MB cache budget\n", (double)c->w16_peak / (1 << 20), (double)c->cache_budget / (1 << 20));
+}
+
 // The teardown line of the route counters (ops completed per route, CPU fallbacks), so a run
 // through a host that cannot call the counter API (llama-bench) still shows where ops ran.
 void report_routes(const Ctx * c) {
@@ -908,17 +1329,36 @@ void report_routes(const Ctx * c) {
 MI355X_API void mi355x_backend_free(mi355x_backend_t c) {
     if (!c) return;
     if (c->stream) (void)hipStreamSynchronize(c->stream);
-    c->stage.release();
+    if (c->dstream) (void)hipStreamSynchronize(c->dstream);
+    c->up.release();
+    c->down.release();
+    for (hipEvent_t e : c->evpool) (void)hipEventDestroy(e);
+    c->evpool.clear();
+    if (c->dstream) (void)hipStreamDestroy(c->dstream);
+    if (c->ustream) {
+        (void)hipStreamSynchronize(c->ustream);
+        (void)hipStreamDestroy(c->ustream);
+    }
     c->pool.reset();
     for (auto & kv : c->wcache) (void)hipFree(kv.second.dev);
     report_residency(c);
+    report_scratch(c);
     report_routes(c);
     c->wcache.clear();
     for (DevBuf * b : {&c->act, &c->a16, &c->scales, &c->out, &c->part, &c->wstage, &c->wconv, &c->fa_q, &c->fa_k, &c->fa_v,
                        &c->fa_m, &c->fa_o, &c->fa_ws, &c->moe_b, &c->moe_ids, &c->moe_o, &c->moe_ws,
-                       &c->wscratch[0], &c->wscratch[1], &c->wscratch[2], &c->wscratch[3], &c->moe_wscratch})
+                       &c->wscratch[0], &c->wscratch[1], &c->wscratch[2], &c->wscratch[3], &c->moe_wscratch, &c->w16})
         b->release();
-    if (c->stream) (void)hipStreamDestroy(c->stream);
+    if (c->stream) {
+        (void)hipStreamSynchronize(c->stream);   // the stream-ordered frees above
+        (void)hipStreamDestroy(c->stream);
+        // hand the freed bytes back to the device rather than keeping them in its pool
+        int dev = 0;
+        hipMemPool_t mp = nullptr;
+        if (hipGetDevice(&dev) == hipSuccess && hipDeviceGetDefaultMemPool(&mp, dev) == hipSuccess && mp)
+            (void)hipMemPoolTrimTo(mp, 0);
+        (void)hipGetLastError();
+    }
     for (const auto & k : c->moe_claimed) moe_preflight_release(k);
     moe_preflight_close();
     c->guid[0] = c->guid[1] = 0;
@@ -980,8 +1420,29 @@ MI355X_API void mi355x_backend_route_stats(mi355x_backend_t c, const char * g, l
 }
 
 MI355X_API void mi355x_backend_inject_faults(mi355x_backend_t c, const char * g, int n) {
+    if (mi355x_backend_is(c) && g && !strcmp(g, "copyback")) {
+        c->inject_drain = n < 0 ? 0 : n;
+        return;
+    }
     RouteHealth * b = breaker_of(c, g);
     if (b) b->inject = n < 0 ? 0 : n;
+}
+
+MI355X_API void mi355x_backend_host_stats(mi355x_backend_t c, mi355x_host_stats * out) {
+    if (!out) return;
+    memset(out, 0, sizeof *out);
+    if (!mi355x_backend_is(c)) return;
+    const HostStats & h = c->hs;
+    out->calls = h.calls;
+    out->fa_mirror_hits = h.fa_mirror_hits;
+    out->copyback_redone = h.redone;
+    out->bytes_up = h.bytes_up;
+    out->bytes_down = h.bytes_down;
+    out->wall_s = h.wall_s;
+    out->up_copy_s = h.up_copy_s;
+    out->up_wait_s = h.up_wait_s;
+    out->down_copy_s = h.down_copy_s;
+    out->down_wait_s = h.down_wait_s;
 }
 
 static int graph_compute_nodes(mi355x_backend_t c, mi355x_tensor * const * nodes, int n_nodes);
@@ -1030,7 +1491,20 @@ MI355X_API int mi355x_backend_graph_compute(mi355x_backend_t c, mi355x_tensor * 
     return st;
 }
 
+static int graph_compute_queued(mi355x_backend_t c, mi355x_tensor * const * nodes, int n_nodes);
+
+// Runs the nodes, then delivers every output still queued for download: each dst is written
+// when this returns, whatever the status.
 static int graph_compute_nodes(mi355x_backend_t c, mi355x_tensor * const * nodes, int n_nodes) {
+    const double t0 = now_s();
+    const int st = graph_compute_queued(c, nodes, n_nodes);
+    dl_drain(c);
+    c->hs.calls++;
+    c->hs.wall_s += now_s() - t0;
+    return st;
+}
+
+static int graph_compute_queued(mi355x_backend_t c, mi355x_tensor * const * nodes, int n_nodes) {
     c->started = true;
     c->fa_mirror = {};
     // the attention's device copy may stand in for its host bytes only if no other node of the
@@ -1096,6 +1570,7 @@ static int graph_compute_nodes(mi355x_backend_t c, mi355x_tensor * const * nodes
             case MI355X_OP_MUL_MAT_ID: {
                 const mi355x_tensor * as = node->src[0];
                 const mi355x_tensor * ids = node->src[2];
+                if (dl_writes_host(c, ids->data, nbytes(ids))) dl_drain(c);   // the ids are read here
                 // an id outside [0, n_expert) is a malformed graph (ggml-rocket.cpp:6719)
                 std::vector<bool> routed((size_t)as->ne[2], false);
                 for (int64_t t = 0; t < ids->ne[1]; t++)

@@ -6,8 +6,9 @@
 // MI355X-specific differences, each stated where it is applied:
 //   * the accumulator declaration: this device accumulates in fp32 and writes F32, so an F32 or
 //     BF16 accumulator declaration is met (the NPU route could not, 7372-7380);
-//   * the weight types: the device decodes F16, F32, BF16, Q4_0, Q8_0, Q4_K, Q5_K, Q6_K and MXFP4; other ggml quant
-//     types are declined rather than claimed and then computed on the host;
+//   * the weight types: the device decodes F16, F32, BF16, Q4_0, Q8_0, Q4_K, Q5_K, Q6_K and MXFP4;
+//     any other ggml quant type is claimed once a host decoder (ggml's to_float) is registered
+//     for it, which decodes it on the host into the fp16 weight cache, and declined otherwise;
 //   * FLASH_ATTN_EXT: head dims up to 1024 (dk % 32, dv % 8), and the strides the kernels read.
 
 #include <atomic>

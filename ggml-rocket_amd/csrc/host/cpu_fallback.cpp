@@ -8,6 +8,7 @@
 #include <string.h>
 
 #include <algorithm>
+#include <cmath>
 #include <thread>
 #include <vector>
 
@@ -171,50 +172,78 @@ void cpu_mul_mat(const mi355x_tensor * dst) {
     });
 }
 
-// The full-precision attention of ggml-rocket.cpp:5392-5442: Q read as F32, the scale, soft-cap,
-// mask and softmax in double, a fully masked row written as zeros.
+// Attention on the host in double precision, to the contract of ggml-rocket.cpp:5392-5442:
+// Q read as F32, K and V as fp16, logits = scale * q.k, soft-capped when a cap is set, plus the
+// mask; softmax in double; a query whose every key is masked gets a zero output row.
+// Work is laid out per (token, KV head): the H / HK query heads that share a KV head are scored
+// together, so each visible key and value row is widened to double once for all of them. The
+// logits are kept per head, then turned into weights against that head's largest logit and
+// folded into the value sum in key order.
 void cpu_flash_attn(const mi355x_tensor * dst) {
     const mi355x_tensor * q = dst->src[0];
     const mi355x_tensor * k = dst->src[1];
     const mi355x_tensor * v = dst->src[2];
     const mi355x_tensor * m = dst->src[3];
-    const int64_t D = q->ne[0], T = q->ne[1], H = q->ne[2], KV = k->ne[1], HK = k->ne[2], DV = v->ne[0];
-    float scale, softcap;
-    memcpy(&scale, &dst->op_params[0], 4);
-    memcpy(&softcap, &dst->op_params[2], 4);
-    const int64_t g = H / HK;
-    parallel_rows(H * T, [&](int64_t r0, int64_t r1) {
-        std::vector<double> sc((size_t)KV), acc((size_t)DV), qd((size_t)D);
-        for (int64_t r = r0; r < r1; r++) {
-            const int64_t h = r / T, t = r % T, hk = h / g;
-            const char * qr = (const char *)q->data + t * q->nb[1] + h * q->nb[2];
-            for (int64_t c = 0; c < D; c++) qd[c] = *(const float *)(qr + c * q->nb[0]);
-            double mx = -INFINITY;
-            for (int64_t j = 0; j < KV; j++) {
-                const double mv = m ? (double)h2f(*(const uint16_t *)((const char *)m->data + t * m->nb[1] + j * 2)) : 0.0;
-                if (mv == -INFINITY) { sc[j] = -INFINITY; continue; }
-                const char * kr = (const char *)k->data + j * k->nb[1] + hk * k->nb[2];
-                double d = 0.0;
-                for (int64_t c = 0; c < D; c++) d += qd[c] * (double)h2f(*(const uint16_t *)(kr + c * 2));
-                double s = d * (double)scale;
-                if (softcap != 0.0f) s = (double)softcap * tanh(s / (double)softcap);
-                sc[j] = s + mv;
-                mx = std::max(mx, sc[j]);
+    const int64_t dk = q->ne[0], n_tok = q->ne[1], n_head = q->ne[2];
+    const int64_t n_key = k->ne[1], n_kvh = k->ne[2], dv = v->ne[0];
+    const int64_t group = n_head / n_kvh;   // query heads per KV head
+    float scale_f, cap_f;
+    memcpy(&scale_f, &dst->op_params[0], 4);
+    memcpy(&cap_f, &dst->op_params[2], 4);
+    const double scale = scale_f, cap = cap_f;
+    auto widen = [](const char * row, int64_t n, double * out) {
+        for (int64_t c = 0; c < n; c++) out[c] = (double)h2f(rd16((const uint8_t *)row + 2 * c));
+    };
+    parallel_rows(n_tok * n_kvh, [&](int64_t w0, int64_t w1) {
+        std::vector<double> queries((size_t)(group * dk)), logits((size_t)(group * n_key));
+        std::vector<double> vsum((size_t)(group * dv)), top((size_t)group), total((size_t)group);
+        std::vector<double> key((size_t)dk), val((size_t)dv);
+        std::vector<int64_t> seen;   // keys the mask leaves visible, in order
+        seen.reserve((size_t)n_key);
+        for (int64_t w = w0; w < w1; w++) {
+            const int64_t tok = w / n_kvh, kvh = w % n_kvh;
+            for (int64_t i = 0; i < group; i++) {
+                const char * src = (const char *)q->data + tok * q->nb[1] + (kvh * group + i) * q->nb[2];
+                for (int64_t c = 0; c < dk; c++) queries[(size_t)(i * dk + c)] = *(const float *)(src + c * q->nb[0]);
             }
-            double sum = 0.0;
-            for (int64_t j = 0; j < KV; j++) {
-                sc[j] = (mx == -INFINITY || sc[j] == -INFINITY) ? 0.0 : exp(sc[j] - mx);
-                sum += sc[j];
+            std::fill(top.begin(), top.end(), -INFINITY);
+            seen.clear();
+            for (int64_t j = 0; j < n_key; j++) {
+                double bias = 0.0;
+                if (m) bias = (double)h2f(rd16((const uint8_t *)m->data + tok * m->nb[1] + j * 2));
+                if (std::isinf(bias) && bias < 0) continue;
+                seen.push_back(j);
+                widen((const char *)k->data + j * k->nb[1] + kvh * k->nb[2], dk, key.data());
+                for (int64_t i = 0; i < group; i++) {
+                    const double * qi = &queries[(size_t)(i * dk)];
+                    double dot = 0.0;
+                    for (int64_t c = 0; c < dk; c++) dot += qi[c] * key[(size_t)c];
+                    double x = dot * scale;
+                    if (cap != 0.0) x = cap * tanh(x / cap);
+                    x += bias;
+                    logits[(size_t)(i * n_key + j)] = x;
+                    if (x > top[(size_t)i]) top[(size_t)i] = x;
+                }
             }
-            std::fill(acc.begin(), acc.end(), 0.0);
-            for (int64_t j = 0; j < KV; j++) {
-                if (sc[j] == 0.0) continue;
-                const char * vr = (const char *)v->data + j * v->nb[1] + hk * v->nb[2];
-                for (int64_t c = 0; c < DV; c++) acc[c] += sc[j] * (double)h2f(*(const uint16_t *)(vr + c * 2));
+            std::fill(vsum.begin(), vsum.end(), 0.0);
+            std::fill(total.begin(), total.end(), 0.0);
+            for (const int64_t j : seen) {
+                widen((const char *)v->data + j * v->nb[1] + kvh * v->nb[2], dv, val.data());
+                for (int64_t i = 0; i < group; i++) {
+                    const double x = logits[(size_t)(i * n_key + j)];
+                    if (std::isinf(top[(size_t)i]) || std::isinf(x)) continue;
+                    const double p = exp(x - top[(size_t)i]);
+                    total[(size_t)i] += p;
+                    double * acc = &vsum[(size_t)(i * dv)];
+                    for (int64_t c = 0; c < dv; c++) acc[c] += p * val[(size_t)c];
+                }
             }
-            const double inv = sum > 0.0 ? 1.0 / sum : 0.0;
-            float * o = (float *)((char *)dst->data + h * dst->nb[1] + t * dst->nb[2]);
-            for (int64_t c = 0; c < DV; c++) o[c] = (float)(acc[c] * inv);
+            for (int64_t i = 0; i < group; i++) {
+                const int64_t h = kvh * group + i;
+                float * out = (float *)((char *)dst->data + h * dst->nb[1] + tok * dst->nb[2]);
+                const double t = total[(size_t)i];
+                for (int64_t c = 0; c < dv; c++) out[c] = t > 0.0 ? (float)(vsum[(size_t)(i * dv + c)] / t) : 0.0f;
+            }
         }
     });
 }

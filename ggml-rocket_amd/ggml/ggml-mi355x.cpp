@@ -39,8 +39,14 @@
 // slots to ggml_backend_buffer_type_i only, which this backend never fills: it hands out the
 // host's CPU buffer type). Designated initializers bind each function to its slot by name, so
 // a slot ggml adds compiles to NULL (unimplemented) and a renamed one fails to compile.
+// A version not yet checked warns; built with MI355X_STRICT_ABI (`make ggml STRICT_ABI=1`) it
+// is an error instead, so a CI build cannot pass on an unchecked ggml.
 #if GGML_BACKEND_API_VERSION != 2 && GGML_BACKEND_API_VERSION != 3
+#if defined(MI355X_STRICT_ABI)
+#error "ggml-mi355x: GGML_BACKEND_API_VERSION is not 2 or 3; check the three vtables against ggml-backend-impl.h and add the version"
+#else
 #warning "ggml-mi355x: the vtables are checked against GGML_BACKEND_API_VERSION 2 and 3; check ggml-backend-impl.h"
+#endif
 #endif
 
 namespace {
@@ -193,9 +199,13 @@ ggml_guid_t backend_guid() {
 const char * device_get_name(ggml_backend_dev_t) { return mi355x_backend_name(); }
 const char * device_get_description(ggml_backend_dev_t) { return mi355x_backend_description(); }
 
-// HBM of the GPU: where the weight cache and every operand live while an op runs
+// Host memory (MemAvailable / MemTotal), as the reference reports it: the device hands out the
+// host's CPU buffer type, so the model's tensors live in host pages, and llama.cpp's device
+// auto-fit sizes them against memory_free. HBM only holds the weight cache (a copy, with its own
+// budget) and per-op operands, so reporting it would let the auto-fit place more than host
+// memory holds.
 void device_get_memory(ggml_backend_dev_t, size_t * free_b, size_t * total_b) {
-    mi355x_backend_get_memory(free_b, total_b);
+    mi355x_backend_get_host_memory(free_b, total_b);
 }
 
 enum ggml_backend_dev_type device_get_type(ggml_backend_dev_t) { return GGML_BACKEND_DEVICE_TYPE_ACCEL; }

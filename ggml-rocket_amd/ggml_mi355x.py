@@ -356,6 +356,7 @@ def _bind_host(L):
     L.mi355x_backend_name.restype = ctypes.c_char_p
     L.mi355x_backend_description.restype = ctypes.c_char_p
     L.mi355x_backend_get_memory.argtypes = [ctypes.POINTER(sz), ctypes.POINTER(sz)]
+    L.mi355x_backend_get_host_memory.argtypes = [ctypes.POINTER(sz), ctypes.POINTER(sz)]
     L.mi355x_backend_supports_op.restype = ctypes.c_bool
     L.mi355x_backend_supports_op.argtypes = [pt]
     L.mi355x_backend_offload_op.restype = ctypes.c_bool
@@ -378,6 +379,7 @@ def _bind_host(L):
     L.mi355x_backend_route_stats.argtypes = [vp, ctypes.c_char_p, ctypes.POINTER(lng), ctypes.POINTER(lng),
                                                   ctypes.POINTER(lng)]
     L.mi355x_backend_inject_faults.argtypes = [vp, ctypes.c_char_p, i32]
+    L.mi355x_backend_host_stats.argtypes = [vp, ctypes.POINTER(HostStats)]
     L.mi355x_backend_weight_key.argtypes = [pt, ctypes.c_char_p, i32]
     L.mi355x_backend_register_weight_source.argtypes = [pt, vp, sz]
     L.mi355x_backend_parse_mb.restype = ctypes.c_bool
@@ -386,6 +388,14 @@ def _bind_host(L):
     L.mi355x_backend_set_to_float.argtypes = [i32, ctypes.c_int64, ctypes.c_int64, TO_FLOAT_FN]
     L._host_bound = True
     return L
+
+
+class HostStats(ctypes.Structure):
+    """mi355x_host_stats: where graph_compute's time goes on the host."""
+    _fields_ = [("calls", ctypes.c_long), ("fa_mirror_hits", ctypes.c_long), ("copyback_redone", ctypes.c_long),
+                ("bytes_up", ctypes.c_double), ("bytes_down", ctypes.c_double), ("wall_s", ctypes.c_double),
+                ("up_copy_s", ctypes.c_double), ("up_wait_s", ctypes.c_double), ("down_copy_s", ctypes.c_double),
+                ("down_wait_s", ctypes.c_double)]
 
 
 def host():
@@ -527,6 +537,11 @@ class Backend:
 
     def inject_faults(self, group, n):
         self.L.mi355x_backend_inject_faults(self.h, group.encode(), n)
+
+    def host_stats(self):
+        st = HostStats()
+        self.L.mi355x_backend_host_stats(self.h, ctypes.byref(st))
+        return {name: getattr(st, name) for name, _ in HostStats._fields_}
 
 
 _registered = {}

@@ -87,6 +87,12 @@ MI355X_API const char * mi355x_backend_name(void);
 MI355X_API const char * mi355x_backend_description(void);
 /* HBM free / total of the current device (0 / 0 without one). */
 MI355X_API void mi355x_backend_get_memory(size_t * free, size_t * total);
+/* Host memory, MemAvailable / MemTotal of /proc/meminfo in bytes (0 / 0 if unreadable; free is
+ * never above total). What the ggml device reports as its memory, as
+ * ggml_backend_rocket_device_get_memory does (ggml-rocket.cpp:7277-7293): the device hands the
+ * host's CPU buffer type out, so the model's tensors (and llama.cpp's device auto-fit, which
+ * reads memory_free) live in host pages; the HBM weight cache is a copy of them. */
+MI355X_API void mi355x_backend_get_host_memory(size_t * free, size_t * total);
 
 /* Placement hooks. Pure functions of the op's metadata; no backend instance is needed.
  * supports_op: the claim rules of ggml-rocket.cpp:7415-7772 (MUL_MAT 7424-7496, precision
@@ -153,8 +159,29 @@ MI355X_API void mi355x_backend_route_stats(mi355x_backend_t backend, const char 
                                                 long * attempts, long * failures, long * bypassed);
 
 /* Host-side fault injection for tests: the next `n` device attempts of route group `group`
- * ("gemm", "fa", "moe") report a device failure without launching anything. */
+ * ("gemm", "fa", "moe") report a device failure without launching anything; with group
+ * "copyback", the next `n` pieces of device results copied back to host memory report a failure
+ * after their copy has completed (the op is then computed on the CPU, with every op of the call
+ * queued after it). */
 MI355X_API void mi355x_backend_inject_faults(mi355x_backend_t backend, const char * group, int n);
+
+/* Where graph_compute's time goes on the host (cumulative over the backend's life; no reference
+ * counterpart): operands reach the device through pinned upload slots on the compute stream and
+ * results come back through pinned download slots on a copy stream, queued behind the kernels
+ * that produce them and delivered while later ops of the call run. */
+typedef struct mi355x_host_stats {
+    long calls;              /* graph_compute calls */
+    long fa_mirror_hits;     /* MUL_MATs that read a FLASH_ATTN_EXT result of the same call from
+                              * its device copy instead of uploading it */
+    long copyback_redone;    /* ops recomputed on the CPU because their result could not be copied back */
+    double bytes_up, bytes_down;   /* host <-> device bytes of operands and results (weights included) */
+    double wall_s;           /* time inside graph_compute */
+    double up_copy_s;        /* host copies into upload slots */
+    double up_wait_s;        /* waits for an upload slot's previous DMA */
+    double down_copy_s;      /* host copies out of download slots */
+    double down_wait_s;      /* waits for a download slot's DMA (and the kernels before it) */
+} mi355x_host_stats;
+MI355X_API void mi355x_backend_host_stats(mi355x_backend_t backend, mi355x_host_stats * out);
 
 /* The weight-cache key of a weight tensor (ggml-rocket.cpp:4154-4222): its name without this
  * backend's "MI355X#...#<idx>" copy grammar, plus "@" and a 64-bit fingerprint of sixteen

@@ -107,3 +107,60 @@ def test_mul_mat_workspace_sizes_the_decode_first_weight():
             assert ws == poff + (mx.weight_bytes(mx.F16_T, N, K) + 255) // 256 * 256 + part_f16t, (wt, M, N, K)
         else:
             assert ws == (poff + part_own if part_own else pack), (wt, M, N, K)
+
+
+def test_host_memory_matches_meminfo():
+    """The ggml device reports host memory (MemAvailable / MemTotal), as
+    ggml_backend_rocket_device_get_memory does (ggml-rocket.cpp:7277-7293), through the host
+    layer's mi355x_backend_get_host_memory; the adapter's device slot calls it."""
+    L = mx.lib()
+    mx._bind_host(L)
+    fr, tot = ctypes.c_size_t(0), ctypes.c_size_t(0)
+    L.mi355x_backend_get_host_memory(ctypes.byref(fr), ctypes.byref(tot))
+    info = {}
+    for line in open("/proc/meminfo"):
+        k, v = line.split(":", 1)
+        info[k] = int(v.split()[0]) * 1024
+    assert tot.value == info["MemTotal"]
+    assert 0 < fr.value <= tot.value
+    # MemAvailable moves between the two reads; it is the same order of magnitude
+    assert abs(fr.value - info["MemAvailable"]) < max(info["MemAvailable"] // 4, 1 << 30)
+    src = open(ADAPTER).read()
+    body = src[src.index("void device_get_memory("):]
+    body = body[:body.index("}")]
+    assert "mi355x_backend_get_host_memory(" in body
+
+
+def test_strict_abi_turns_an_unchecked_version_into_an_error(tmp_path):
+    """The adapter's version guard, preprocessed on its own: versions 2 and 3 pass; another
+    version warns, and is a compile error under MI355X_STRICT_ABI, which `make ggml STRICT_ABI=1`
+    defines (the reference's GGML_ROCKET_STRICT_ABI, ggml-rocket.cpp:7216-7225)."""
+    import subprocess
+    src = open(ADAPTER).read()
+    a = src.index("#if GGML_BACKEND_API_VERSION != 2")
+    lines = src[a:].splitlines(keepends=True)
+    depth, guard = 0, []
+    for l in lines:
+        t = l.strip()
+        if t.startswith("#if"):
+            depth += 1
+        elif t.startswith("#endif"):
+            depth -= 1
+        guard.append(l)
+        if depth == 0:
+            break
+    f = tmp_path / "guard.c"
+    f.write_text("".join(guard) + "int x;\n")
+
+    def cc(*defs):
+        return subprocess.run(["gcc", "-fsyntax-only", *defs, str(f)], capture_output=True, text=True)
+
+    for v in ("2", "3"):
+        r = cc(f"-DGGML_BACKEND_API_VERSION={v}", "-DMI355X_STRICT_ABI")
+        assert r.returncode == 0 and "warning" not in r.stderr, r.stderr
+    r = cc("-DGGML_BACKEND_API_VERSION=4")
+    assert r.returncode == 0 and "warning" in r.stderr
+    r = cc("-DGGML_BACKEND_API_VERSION=4", "-DMI355X_STRICT_ABI")
+    assert r.returncode != 0 and "error" in r.stderr
+    mk = open(os.path.join(ROOT, "ggml-rocket_amd", "Makefile")).read()
+    assert "-DMI355X_STRICT_ABI" in mk and "$(ADAPTER_DEFS)" in mk

@@ -102,7 +102,9 @@ def test_bench_host_path_from_gguf(torch_cuda, model):
     print(out, flush=True)
     assert out["cpu_fallbacks"] == 0 and out["value"] > 0
     assert out["config"]["d_model"] == 256 and out["config"]["layers"] == 2
-    # two passes (cache fill, then timed) x 4 micro-batches x 2 layers: Q/K/V and gate/up fused
-    # (5 ops), O and down (2); FLASH_ATTN_EXT in the 3 micro-batches with n_kv >= 1024
+    # three passes (cache fill, timed, per-call split) x 4 micro-batches x 2 layers: Q/K/V and
+    # gate/up fused (5 ops), O and down (2); FLASH_ATTN_EXT in the 3 micro-batches with
+    # n_kv >= 1024, whose O reads the attention's device copy
     r = out["routes"]
-    assert r["fused-resident"] == 2 * 4 * 2 * 5 and r["prepacked-q"] == 2 * 4 * 2 * 2 and r["fa"] == 2 * 3 * 2
+    assert r["fused-resident"] == 3 * 4 * 2 * 5 and r["prepacked-q"] == 3 * 4 * 2 * 2 and r["fa"] == 3 * 3 * 2
+    assert out["fa_mirror_hits"] == 3 * 2 and sum(c["MB_up"] + c["MB_down"] for c in out["per_call"].values()) > 0

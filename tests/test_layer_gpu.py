@@ -92,6 +92,9 @@ def test_8b_layer_through_graph_compute(layer, resident):
     else:
         assert routes["fused"] == 5 and routes["mt"] == 2 and routes["fa"] == 1
     assert be.route_ops() == 8
+    hs = be.host_stats()
+    print(f"  host stats {hs}", flush=True)
+    assert hs["fa_mirror_hits"] == 1 and hs["calls"] == 4 and hs["copyback_redone"] == 0
 
     got = {n: g.get(t, np.float32, (T, SHAPES[n][0])) for n, t in mm.items()}
     for n in ("q", "k", "v", "gate", "up"):
