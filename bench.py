@@ -133,6 +133,10 @@ def parse():
     p.add_argument("--moe", action="store_true",
                    help="time MUL_MAT_ID at the 128-expert / top-8 / 512-token / d 2048 / FFN 768 Q4_K "
                         "shape (gate/up and down, cold expert stacks) and print one JSON line")
+    p.add_argument("--mul-mat", default=None, metavar="TYPE,N,K,M",
+                   help="time one single-op MUL_MAT (e.g. Q4_K,8192,3072,128) through mi355x_mul_mat as the "
+                        "--configs sweep does, 64 replayed calls, and print one JSON line (for kernel traces "
+                        "of one shape)")
     p.add_argument("--pmc-probe", action="store_true",
                    help="for hardware-counter runs: launch each distinct op of one layer once, "
                         "eagerly, then a plain 1 GiB device copy (the calibration kernel), and exit")
@@ -276,7 +280,9 @@ class Prefill:
         self._pack(x, K, clear=outs[0][2] if acc else None)
         self._gemm(K, outs, flops, zeroed=acc)
 
-    def _fa(self, u):
+    def _fa(self, u, first=True):
+        """The attention of micro-batch u; `first` for the micro-batch's first layer, which
+        classifies the shared KQ mask's tiles into the workspace for the later layers."""
         n_kv = UBATCH * (u + 1)
         mx = self.mx
         q = self.qo.view(UBATCH, NH, HD).permute(1, 0, 2)
@@ -284,19 +290,20 @@ class Prefill:
         v = self.vc[:n_kv].permute(1, 0, 2)
         m = self.masks[u]
         out = self.attn.view(UBATCH, NH, HD)
-        self._ev("fa", lambda: mx.flash_attn(q, k, v, m, 1.0 / math.sqrt(HD), out=out, workspace=self.fa_ws))
+        self._ev("fa", lambda: mx.flash_attn(q, k, v, m, 1.0 / math.sqrt(HD), out=out, workspace=self.fa_ws,
+                                             classes_ready=not first))
         self.flops["fa"] += 4.0 * NH * UBATCH * n_kv * HD
 
     def step(self):
         sh = self.shapes
         for u in range(TOKENS // UBATCH):
-            for lw in self.layers:
+            for li, lw in enumerate(self.layers):
                 M = UBATCH
                 self._mm(self.x, D_MODEL, [(lw["q"], sh["q"][0], self.qo), (lw["k"], sh["k"][0], self.ko),
                                            (lw["v"], sh["v"][0], self.vo)],
                          2.0 * M * D_MODEL * (D_MODEL + 2 * NKV * HD))
                 if UBATCH * (u + 1) >= self.fa_min_kv:
-                    self._fa(u)
+                    self._fa(u, first=li == 0)
                 self._mm(self.attn, D_MODEL, [(lw["o"], D_MODEL, self.oo)], 2.0 * M * D_MODEL * D_MODEL)
                 self._mm(self.x, D_MODEL, [(lw["gate"], FFN, self.go), (lw["up"], FFN, self.uo)],
                          2.0 * M * D_MODEL * 2 * FFN)
@@ -414,7 +421,7 @@ def time_ops(pf, reps=32):
     ]
     for u in range(TOKENS // UBATCH):
         kind = "fa" if UBATCH * (u + 1) >= pf.fa_min_kv else "fa-declined"
-        ops.append((kind, 4.0 * NH * UBATCH * UBATCH * (u + 1) * HD, L_LAYERS, (lambda i, uu=u: pf._fa(uu))))
+        ops.append((kind, 4.0 * NH * UBATCH * UBATCH * (u + 1) * HD, L_LAYERS, (lambda i, uu=u: pf._fa(uu, first=i == 0))))
     pf.reset_counters(False)
     out = []
     for kind, flops, per_step, fn in ops:
@@ -770,6 +777,28 @@ def synth_blocks(wtype, N, K, seed):
     return blk.reshape(-1)
 
 
+def mul_mat_one(spec):
+    """One quantized MUL_MAT shape of the single-op sweep, alone: same weights, same rotation over
+    weight copies, same entry point and workspace as configs_bench."""
+    import numpy as np
+    import torch
+    import ggml_mi355x as mx
+    tn, N, K, M = spec.split(",")
+    N, K, M = int(N), int(K), int(M)
+    wt = {"Q8_0": mx.Q8_0, "Q4_K": mx.Q4_K, "Q6_K": mx.Q6_K, "Q4_0": mx.Q4_0, "Q5_K": mx.Q5_K, "MXFP4": mx.MXFP4}[tn]
+    P = synth_blocks(wt, N, K, 0x5EED0000 + 64)
+    w0 = mx.upload_weight(wt, P, N, K)
+    ncopy = max(3, min(64, math.ceil(320e6 / w0.numel())))
+    ws = [w0] + [w0.clone() for _ in range(ncopy - 1)]
+    x = torch.randn(M, K, device="cuda")
+    out = torch.empty(M, N, device="cuda")
+    wsp = torch.empty(max(1, int(mx.lib().mi355x_mul_mat_workspace_for(wt, N, K, M))), dtype=torch.uint8, device="cuda")
+    us = graph_time_us(lambda i: mx.mul_mat(wt, ws[i % ncopy], N, K, x, out, wsp), max(ncopy, 64))
+    nbytes = P.nbytes + M * K * 4 + M * N * 4
+    return {"case": f"MUL_MAT {tn} N={N} K={K} M={M}", "us": round(us, 2), "tflops": round(2.0 * M * N * K / us / 1e6, 1),
+            "GBps": round(nbytes / us / 1e3, 1), "decode_first": int(mx.lib().mi355x_mul_mat_decode_first(wt, M, N, K))}
+
+
 def configs_bench(args, subset=False):
     """The single-op configurations, each through the C ABI entry the backend uses for it and
     against the roofline that bounds it (arithmetic intensity against the 2.5 PFLOP/s / 8 TB/s
@@ -955,6 +984,9 @@ def main():
         sys.exit(2)
     import torch
     torch.cuda.set_device(0)
+    if args.mul_mat:
+        print(json.dumps(mul_mat_one(args.mul_mat)), flush=True)
+        return
     if args.pmc_probe:
         pmc_probe(Prefill(args.route, 1))
         return

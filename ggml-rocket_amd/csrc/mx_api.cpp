@@ -484,6 +484,12 @@ MI355X_API size_t mi355x_flash_attn_workspace(const mi355x_fa_args * a, int nspl
 
 MI355X_API int mi355x_flash_attn(const mi355x_fa_args * a, int nsplit,
                                  void * workspace_dev, size_t workspace_bytes, void * stream) {
+    return mi355x_flash_attn_ex(a, nsplit, 0, workspace_dev, workspace_bytes, stream);
+}
+
+MI355X_API int mi355x_flash_attn_ex(const mi355x_fa_args * a, int nsplit, int flags,
+                                    void * workspace_dev, size_t workspace_bytes, void * stream) {
+    if (flags & ~MI355X_FA_CLASSES_READY) return MI355X_E_ARG;
     const int st = fa_check(a);
     if (st != MI355X_OK) return st;
     if (a->T == 0) return MI355X_OK;
@@ -520,7 +526,7 @@ MI355X_API int mi355x_flash_attn(const mi355x_fa_args * a, int nsplit,
         f.part_o = (float *)(ws + L.po);
         f.part_ml = (float *)(ws + L.pml);
     }
-    return hip_status(mx::launch_fa(f, S(stream)));
+    return hip_status(mx::launch_fa(f, !(flags & MI355X_FA_CLASSES_READY), S(stream)));
 }
 
 // ---- MUL_MAT_ID -------------------------------------------------------------------------------

@@ -11,7 +11,8 @@
 // never leave fp32 registers (there is no fp16 score surface to overflow), P is rounded to fp16
 // for the P.V MFMA, both contractions accumulate in fp32.
 //
-// One op is two launches:
+// One op is two launches (one when the caller says the workspace already holds the classes of
+// this mask, e.g. for every layer after the first of a micro-batch, which all share one mask):
 //   fa_prep   the mask tile classes (per 32-query x 64-key tile: every key masked / no key
 //             masked / mixed), and 16 zero bytes (the K and V source of padded head dims).
 //   fa        a block is 4 tasks, each 32 query rows of one head, all 4 on one KV head (GQA
@@ -916,10 +917,12 @@ static hipError_t fa_launch_main(const FaArgs & a, int nb, hipStream_t st) {
 }
 
 template <int DK, int DV>
-static hipError_t fa_launch_all(const FaArgs & a, int nb, hipStream_t st) {
-    hipLaunchKernelGGL(fa_prep_kernel, dim3(fa_prep_blocks(a)), dim3(256), 0, st, a);
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return e;
+static hipError_t fa_launch_all(const FaArgs & a, int nb, bool prep, hipStream_t st) {
+    hipError_t e = hipSuccess;
+    if (prep) {
+        hipLaunchKernelGGL(fa_prep_kernel, dim3(fa_prep_blocks(a)), dim3(256), 0, st, a);
+        if ((e = hipGetLastError()) != hipSuccess) return e;
+    }
     if constexpr (DV <= 128) {
         if (a.tasks == 2)
             e = a.softcap != 0.0f ? fa_launch_main<DK, DV, 2, true>(a, nb, st) : fa_launch_main<DK, DV, 2, false>(a, nb, st);
@@ -935,14 +938,14 @@ static hipError_t fa_launch_all(const FaArgs & a, int nb, hipStream_t st) {
     return hipGetLastError();
 }
 
-hipError_t launch_fa(const FaArgs & a, hipStream_t st) {
+hipError_t launch_fa(const FaArgs & a, bool prep, hipStream_t st) {
     if (!fa_tasks_ok(a.DV, a.tasks)) return hipErrorInvalidValue;
     const int nb = fa_blocks_per_split(a) * a.nsplit;
     if (nb <= 0) return hipSuccess;
-    if (a.D == 64 && a.DV == 64) return fa_launch_all<64, 64>(a, nb, st);
-    if (a.D == 128 && a.DV == 128) return fa_launch_all<128, 128>(a, nb, st);
-    if (a.D == 192 && a.DV == 128) return fa_launch_all<192, 128>(a, nb, st);
-    if (a.D == 256 && a.DV == 256) return fa_launch_all<256, 256>(a, nb, st);
+    if (a.D == 64 && a.DV == 64) return fa_launch_all<64, 64>(a, nb, prep, st);
+    if (a.D == 128 && a.DV == 128) return fa_launch_all<128, 128>(a, nb, prep, st);
+    if (a.D == 192 && a.DV == 128) return fa_launch_all<192, 128>(a, nb, prep, st);
+    if (a.D == 256 && a.DV == 256) return fa_launch_all<256, 256>(a, nb, prep, st);
     return hipErrorInvalidValue;
 }
 

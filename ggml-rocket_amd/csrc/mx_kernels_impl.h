@@ -110,7 +110,7 @@ int fa_blocks_per_split(const FaArgs & a);   // for a.tasks
 int fa_prep_blocks(const FaArgs & a);
 bool fa_dims_supported(int dk, int dv);   // fa_pad_dims: dk, dv <= 256, multiples of 8
 size_t fa_max_kv(int dk, int dv);          // the longest KV range one launch takes
-hipError_t launch_fa(const FaArgs & a, hipStream_t st);
+hipError_t launch_fa(const FaArgs & a, bool prep, hipStream_t st);
 
 // zc (optional): an F32 output [M][ldzc] whose first zn columns the pack also clears
 hipError_t launch_pack_act(const float * X, int64_t ldx, int M, int K, uint16_t * A16, int64_t lda,

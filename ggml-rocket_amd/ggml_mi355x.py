@@ -115,6 +115,7 @@ def _bind_optional(L):
         L.mi355x_flash_attn_workspace.restype = sz
         L.mi355x_flash_attn_workspace.argtypes = [pa, i32]
         L.mi355x_flash_attn.argtypes = [pa, i32, vp, sz, vp]
+        L.mi355x_flash_attn_ex.argtypes = [pa, i32, i32, vp, sz, vp]
     if hasattr(L, "mi355x_mul_mat_noalloc"):
         L.mi355x_mul_mat_noalloc.argtypes = [i32, vp, i64, i64, vp, i64, i64, vp, i64, vp]
     if hasattr(L, "mi355x_mul_mat_id"):
@@ -267,10 +268,14 @@ def flash_attn_workspace(q, k, v, mask, out, scale: float = 1.0, softcap: float 
     return int(lib().mi355x_flash_attn_workspace(ctypes.byref(_fa_args(q, k, v, mask, out, scale, softcap)), nsplit))
 
 
+FA_CLASSES_READY = 1
+
+
 def flash_attn(q, k, v, mask, scale: float, softcap: float = 0.0, nsplit: int = 0, out=None,
-               workspace=None, max_bias: float = 0.0):
+               workspace=None, max_bias: float = 0.0, classes_ready: bool = False):
     """q [H, T, D] f32 (any strides with unit last-dim stride), k/v [HK, KV, D] fp16, mask
-    [T', KV'] fp16 or None. Returns dst [T, H, D] f32."""
+    [T', KV'] fp16 or None. Returns dst [T, H, D] f32. classes_ready: `workspace` holds the mask
+    classes of an earlier call with the same mask, shapes and split (mi355x_flash_attn_ex)."""
     torch = _torch()
     H, T, D = q.shape
     HK, KV, DV = v.shape
@@ -281,7 +286,10 @@ def flash_attn(q, k, v, mask, scale: float, softcap: float = 0.0, nsplit: int = 
     if need and (workspace is None or workspace.numel() < need):
         workspace = torch.empty(need, dtype=torch.uint8, device=q.device)
     wp = workspace.data_ptr() if need else None
-    check(lib().mi355x_flash_attn(ctypes.byref(a), nsplit, wp, need, stream_handle()), "flash_attn")
+    if classes_ready and workspace is None:
+        raise MI355XError("flash_attn: classes_ready needs the workspace of the call that classified the mask")
+    flags = FA_CLASSES_READY if classes_ready else 0
+    check(lib().mi355x_flash_attn_ex(ctypes.byref(a), nsplit, flags, wp, need, stream_handle()), "flash_attn")
     return out
 
 

@@ -212,15 +212,20 @@ MI355X_API int mi355x_mul_mat(int wtype, const void * w_dev, int64_t N, int64_t 
 
 /* mi355x_mul_mat without a workspace argument: no counterpart in the reference. For callers
  * that cannot allocate device memory (code under HIP graph capture, tight serving loops,
- * harnesses that forbid hipMalloc). The activation pack lives in a file-scope device array of
+ * harnesses that forbid hipMalloc). The workspace lives in a file-scope device array of
  * MI355X_NOALLOC_SCRATCH_BYTES per GPU, held until the process ends; the call allocates nothing
  * and frees nothing. Limit: mi355x_mul_mat_workspace(M, K) <= MI355X_NOALLOC_SCRATCH_BYTES
  * (e.g. M 2048 at K 14336), else MI355X_E_NOMEM with a message. Every call on one GPU shares
  * that GPU's array: calls that overlap on one GPU (two streams, two threads) race and must be
  * serialized by the caller. The first call on a device resolves the array's address there
- * (make it outside a stream capture); later calls may be captured. Same results as
- * mi355x_mul_mat given MI355X_NOALLOC_SCRATCH_BYTES of workspace (K-split partials use the
- * scratch past the pack). */
+ * (make it outside a stream capture); later calls may be captured. It computes exactly what
+ * mi355x_mul_mat computes given MI355X_NOALLOC_SCRATCH_BYTES of workspace: the scratch holds
+ * the activation pack, then, where the decode-first form runs (mi355x_mul_mat_decode_first) and
+ * the pack plus the tiled fp16 weight fit, that weight, and the K-split partials in what is left.
+ * So the form depends on the fit: a quantized weight whose fp16 image does not fit beside the
+ * pack (e.g. Q6_K 8192 x 4096 at M 512: 4 MiB + 64 MiB) is decoded inside the GEMM here while
+ * mi355x_mul_mat with mi355x_mul_mat_workspace_for bytes decodes it first; both forms meet the
+ * same MUL_MAT bars, but their bits can differ in the last place. */
 MI355X_API int mi355x_mul_mat_noalloc(int wtype, const void * w_dev, int64_t N, int64_t K,
                                       const float * x_dev, int64_t ldx, int64_t M,
                                       float * dst_dev, int64_t ldd, void * stream);
@@ -267,6 +272,16 @@ MI355X_API size_t mi355x_flash_attn_workspace(const mi355x_fa_args * a, int nspl
  * surface exists here, the range fallback rocket_fa_ref_f32 (5617-5626) as well. */
 MI355X_API int mi355x_flash_attn(const mi355x_fa_args * a, int nsplit,
                                  void * workspace_dev, size_t workspace_bytes, void * stream);
+
+/* mi355x_flash_attn with flags. MI355X_FA_CLASSES_READY: skip the prep pass, because this
+ * workspace already holds its results for this mask -- written by an earlier call on the same
+ * stream with the same mask bytes, T, KV, head dims and split (nsplit as resolved), and not
+ * overwritten since. A graph's layers share one KQ mask per micro-batch, so the first attention
+ * of the micro-batch classifies the mask tiles and the others reuse them. The flag is ignored for
+ * head dims past 256. No counterpart in the reference (its NPU path has no prep pass). */
+#define MI355X_FA_CLASSES_READY 1
+MI355X_API int mi355x_flash_attn_ex(const mi355x_fa_args * a, int nsplit, int flags,
+                                    void * workspace_dev, size_t workspace_bytes, void * stream);
 
 /* ---- MUL_MAT_ID --------------------------------------------------------------------------- */
 

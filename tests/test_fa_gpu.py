@@ -284,3 +284,38 @@ def test_fa_wide_mla_prefill_chunked(mx):
     r = compare(want, got[idx])
     print(f"wide MLA prefill sampled rows: {r}")
     assert r["nonfinite"] == 0 and r["max_abs"] <= 2e-2 and r["range_err"] <= 1e-2, r
+
+
+@pytest.mark.parametrize("nsplit", [1, 3])
+def test_fa_classes_ready_reuses_the_mask_classes(mx, nsplit):
+    """mi355x_flash_attn_ex with MI355X_FA_CLASSES_READY: the layers of a micro-batch share one
+    mask, so the first call classifies its tiles into the workspace and later calls with other
+    Q / K / V skip that pass. Each reusing call gives the same bits as a call that classifies the
+    mask itself, with a causal mask holding all three tile classes and a fully masked row, split
+    and unsplit; the first call's own result matches the oracle."""
+    import torch
+    D, T, H, KV, HK = 128, 200, 8, 700, 2
+    M = causal_mask(T, KV)
+    M[17, :] = -np.inf
+    M16 = O.f32_to_f16_bits(M)
+    m = torch.from_numpy(M16.view(np.float16)).cuda()
+    scale = 1.0 / np.sqrt(D)
+    ws = None
+    for layer in range(3):
+        Q = O.fill_normal((H, T, D), 0x9100 + layer)
+        K, V = O.fill_normal((HK, KV, D), 0x9110 + layer), O.fill_normal((HK, KV, D), 0x9120 + layer)
+        K16, V16 = O.f32_to_f16_bits(K), O.f32_to_f16_bits(V)
+        q = torch.from_numpy(np.ascontiguousarray(Q)).cuda()
+        k = torch.from_numpy(K16.view(np.float16)).cuda()
+        v = torch.from_numpy(V16.view(np.float16)).cuda()
+        if ws is None:
+            ws = torch.empty(mx.flash_attn_workspace(q, k, v, m, torch.empty((T, H, D), device="cuda"), scale,
+                                                     nsplit=nsplit), dtype=torch.uint8, device="cuda")
+        fresh = mx.flash_attn(q, k, v, m, scale, nsplit=nsplit).cpu().numpy()
+        got = mx.flash_attn(q, k, v, m, scale, nsplit=nsplit, workspace=ws, classes_ready=layer > 0)
+        torch.cuda.synchronize()
+        got = got.cpu().numpy()
+        assert np.array_equal(got, fresh), (layer, nsplit)
+        if layer == 0:
+            want = O.flash_attn(Q, K16, V16, M16, scale)
+            assert np.all(got[17] == 0.0) and float(np.abs(got - want).max()) <= 2e-2

@@ -45,6 +45,32 @@ def test_noalloc_matches_mul_mat(torch_cuda):
         assert r["nbad"] == 0 and r["range_err"] <= 1e-2 and worst_col_cos(ref, g) >= 0.999
 
 
+def test_noalloc_when_the_decoded_weight_does_not_fit(torch_cuda):
+    """Q6_K 8192 x 4096 at M 512: mi355x_mul_mat with mi355x_mul_mat_workspace_for bytes decodes
+    the weight into tiled fp16 first (4 MiB of pack + 64 MiB of fp16 weight), which the 64 MiB
+    static scratch cannot hold, so the no-allocation entry decodes inside the GEMM instead. Both
+    forms against the oracle's fp64 GEMM on sampled rows, with the MUL_MAT bars (not bit equality:
+    the two forms round in a different order)."""
+    torch = torch_cuda
+    L = mx.lib()
+    wt, N, K, M = O.Q6_K, 8192, 4096, 512
+    assert L.mi355x_mul_mat_decode_first(wt, M, N, K) == 1
+    assert int(L.mi355x_mul_mat_workspace_for(wt, N, K, M)) > (64 << 20) >= int(L.mi355x_mul_mat_workspace(M, K))
+    P, X, w, x = _case(torch, wt, N, K, M, 9300)
+    got = torch.full((M, N), float("nan"), device="cuda")
+    st = mx.mul_mat_noalloc(wt, w, N, K, x, got)
+    assert st == mx.OK, mx.status_str(st)
+    first = mx.mul_mat(wt, w, N, K, x)
+    torch.cuda.synchronize()
+    rows = np.sort(np.random.default_rng(93).choice(M, 40, replace=False))
+    ref = O.mul_mat(wt, P, X[rows], N, K)
+    for label, out in (("noalloc (in-GEMM decode)", got), ("mul_mat (decode first)", first)):
+        g = out.cpu().numpy()[rows]
+        r = compare(ref, g)
+        print(f"{label}: nbad={r['nbad']} range_err={r['range_err']:.3g}", flush=True)
+        assert np.isfinite(g).all() and r["nbad"] == 0 and r["range_err"] <= 1e-2 and worst_col_cos(ref, g) >= 0.999
+
+
 def test_noalloc_refuses_past_scratch(torch_cuda):
     torch = torch_cuda
     K, N = 14336, 256
