@@ -1152,6 +1152,277 @@ gemm_q4k_kernel(GemmArgs args) {
     }
 }
 
+// ---------------------------------------------------------------------------------------------
+// Skinny GEMM with the weight staged by LDS DMA (M <= 128; Q4_K, Q8_0 and Q6_K weights).
+//
+// The register-staged skinny kernel above keeps one K group of weight in flight per wave beside
+// the one it multiplies, so a block that owns a few groups pays an HBM round trip for nearly each
+// of them. Here the bytes go from HBM into LDS by global_load_lds_dwordx4, which holds them
+// without registers: a ring of NS stages, each one K group (CH 64-deep chunks) of the activation
+// slice and of the weight, NS - 1 groups requested ahead of the one multiplied. A lane's weight
+// item (decoder item g of chunk c of weight row r, as in the register kernel) arrives as NP
+// 16-byte pieces, each DMA'd by the lane that decodes it, to LDS slot
+// ((c * NP + p) * NW + wave) * 1 KB + 16 * lane, so the weight ring is private to its wave; the
+// few bytes of an item that are not 16-byte pieces (a Q8_0 block's scale, a Q6_K block's scales
+// and d) come as the aligned 16 bytes of their plane that hold them, so no register ring (whose
+// loads the compiler would wait for in full at the loop's back edge) is needed. The activation slice is shared by the
+// block's waves and lands XOR-swizzled as in the register kernel: each lane fetches the chunk
+// that belongs at its slot. Per group: wait for this wave's DMA of the group (every group issues
+// the same count, past the block's last group the last one is fetched again, so the count is a
+// constant), one barrier (the slice is complete, and every wave is done with the stage about to
+// be refilled), the DMA of group + NS - 1, then the group's decode and MFMAs.
+// Same decoders, same fp16 products and the same K order per output as the register kernel.
+// ---------------------------------------------------------------------------------------------
+template <int WT> struct SkPieces;
+
+// The aligned 16 bytes of a plane of 2-byte values that hold value `idx` (a plane starts 16-byte
+// aligned and, with N % 16 == 0, spans a whole number of 16-byte chunks, so the chunk is inside
+// it), and the value from that chunk.
+__device__ __forceinline__ const uint8_t * chunk_of16(const uint8_t * plane, int64_t idx) {
+    return plane + ((2 * idx) & ~(int64_t)15);
+}
+// word i (0..3) of c by selects: a runtime index into a vector would go through scratch memory
+__device__ __forceinline__ uint32_t word_of(const u32x4 & c, int i) {
+    const uint32_t lo = (i & 1) ? c[1] : c[0], hi = (i & 1) ? c[3] : c[2];
+    return (i & 2) ? hi : lo;
+}
+__device__ __forceinline__ uint16_t half_in_chunk(const u32x4 & c, int64_t idx) {
+    const int o = (int)((2 * idx) & 15);
+    return (uint16_t)(word_of(c, o >> 2) >> (8 * (o & 3)));
+}
+
+template <> struct SkPieces<T_Q4_K> {   // the block header and this item's 16 bytes of nibbles
+    static constexpr int NP = 2;
+    __device__ static const uint8_t * piece(const uint8_t * W, int64_t rows, int64_t K, int64_t row, int64_t k0,
+                                            int u, int p) {
+        const uint8_t * b = W + (row * (K / 256) + k0 / 256) * 144;
+        return p == 0 ? b : b + 16 + 32 * ((k0 % 256) / 64) + 16 * u;
+    }
+    __device__ static void item(WLoad<T_Q4_K> & w, const u32x4 (&pc)[NP], int64_t, int64_t, int64_t row, int64_t k0,
+                                int, bool ok) {
+        w.hdr = pc[0];
+        w.qs = pc[1];
+        w.j = (int)((k0 % 256) / 64);
+        w.ok = ok;
+    }
+};
+
+template <> struct SkPieces<T_Q8_0> {   // the item's 32 quants and the chunk holding its scale
+    static constexpr int NP = 3;
+    // the item's first value, k0 + 32 u, clamped to 0 past K (the item is then masked)
+    __device__ static int64_t kk(int64_t K, int64_t k0, int u) {
+        const int64_t k = k0 + 32 * u;
+        return k < K ? k : 0;
+    }
+    __device__ static const uint8_t * piece(const uint8_t * W, int64_t rows, int64_t K, int64_t row, int64_t k0,
+                                            int u, int p) {
+        if (p < 2) return W + row * K + kk(K, k0, u) + 16 * p;
+        return chunk_of16(W + rows * K, row * (K / 32) + kk(K, k0, u) / 32);
+    }
+    __device__ static void item(WLoad<T_Q8_0> & w, const u32x4 (&pc)[NP], int64_t rows, int64_t K, int64_t row,
+                                int64_t k0, int u, bool ok) {
+        w.q[0] = pc[0];
+        w.q[1] = pc[1];
+        w.d = half_in_chunk(pc[2], row * (K / 32) + kk(K, k0, u) / 32);
+        w.ok = ok;
+    }
+};
+
+template <> struct SkPieces<T_Q6_K> {   // ql (two runs), qh, the block's 16 scales, the chunk holding d
+    static constexpr int NP = 5;
+    __device__ static const uint8_t * piece(const uint8_t * W, int64_t rows, int64_t K, int64_t row, int64_t k0,
+                                            int u, int p) {
+        const int64_t blk = k0 / 256;
+        const int h = (int)((k0 % 256) / 64) >> 1, l0 = 16 * u;
+        if (p < 2) return W + row * (K / 2) + blk * 128 + 64 * h + l0 + 32 * p;
+        if (p == 2) return W + rows * (K / 2) + row * (K / 4) + blk * 64 + 32 * h + l0;
+        const uint8_t * sc = W + rows * (K / 2) + rows * (K / 4);
+        if (p == 3) return sc + row * (K / 16) + blk * 16;
+        return chunk_of16(sc + rows * (K / 16), row * (K / 256) + blk);
+    }
+    __device__ static void item(WLoad<T_Q6_K> & w, const u32x4 (&pc)[NP], int64_t rows, int64_t K, int64_t row,
+                                int64_t k0, int u, bool ok) {
+        const int64_t blk = k0 / 256;
+        const int q4 = (int)((k0 % 256) / 64), h = q4 >> 1, hi = q4 & 1;
+        w.qla = pc[0];
+        w.qlb = pc[1];
+        w.qh = pc[2];
+        // scales 8h + u + 4hi and that + 2 of the block (sub-blocks (l/16) + {0,2} or + {4,6})
+        const int i0 = 8 * h + u + 4 * hi;
+        const uint32_t s0 = (word_of(pc[3], i0 >> 2) >> (8 * (i0 & 3))) & 0xFFu;
+        const uint32_t s1 = (word_of(pc[3], (i0 + 2) >> 2) >> (8 * ((i0 + 2) & 3))) & 0xFFu;
+        w.sc = s0 | (s1 << 8);
+        w.d = half_in_chunk(pc[4], row * (K / 256) + blk);
+        w.hi = hi;
+        w.ok = ok;
+    }
+};
+
+template <int WT, int MT, int CH, int NS>
+struct SkDmaCfg {
+    static constexpr int NW = SK_NW, THREADS = NW * WAVE;
+    static constexpr int NP = SkPieces<WT>::NP;
+    static constexpr int CPR = 8 * CH;                    // 16-byte chunks per activation row of the slice
+    static constexpr int A_BYTES = 32 * MT * CPR * 16;    // the slice [32 MT][64 CH] fp16
+    static constexpr int PA = A_BYTES / (THREADS * 16);   // activation DMA per wave per group
+    static constexpr int W_BYTES = CH * NP * NW * 1024;   // every wave's pieces of the group
+    static constexpr int STAGE = A_BYTES + W_BYTES;
+    static constexpr int LDS = NS * STAGE;
+    static constexpr int PER = PA + CH * NP;              // DMA per wave per group
+    static_assert(PA >= 1 && PA * THREADS * 16 == A_BYTES, "slice split");
+    static_assert(NS >= 2 && NS <= 4 && LDS <= 160 * 1024, "LDS");
+};
+
+// One block a CU (its ring takes most of the LDS), so one wave a SIMD: the whole register file is
+// the wave's.
+template <int WT, int MT, int CH, int NS>
+__global__ void __launch_bounds__(SK_NW * WAVE)
+__attribute__((amdgpu_waves_per_eu(1, 1)))
+gemm_skinny_dma_kernel(GemmArgs args, int groups_per_block) {
+    using C = SkDmaCfg<WT, MT, CH, NS>;
+    using P = SkPieces<WT>;
+    constexpr int NW = C::NW, CPR = C::CPR, NP = C::NP;
+    extern __shared__ __align__(16) uint8_t smem[];
+
+    const int t = threadIdx.x, lane = t % WAVE, wave = t / WAVE;
+    const int wave_s = __builtin_amdgcn_readfirstlane(wave);
+    const int lr = lane % 32, lg = lane / 32;
+    const int ks = args.ksplit;
+    const int split = blockIdx.x % ks;
+    const int nt = blockIdx.x / ks;
+    int g = 0;
+#pragma unroll
+    for (int i = 1; i < GEMM_MAX_GROUPS; i++)
+        if (i < args.ng && nt >= args.g[i].ntile_begin) g = i;
+    GemmGroup G;
+    G.W = args.g[0].W; G.rows_total = args.g[0].rows_total; G.row0 = args.g[0].row0; G.N = args.g[0].N;
+    G.C = args.g[0].C; G.ldc = args.g[0].ldc; G.ntile_begin = args.g[0].ntile_begin;
+#pragma unroll
+    for (int i = 1; i < GEMM_MAX_GROUPS; i++)
+        if (i == g) {
+            G.W = args.g[i].W; G.rows_total = args.g[i].rows_total; G.row0 = args.g[i].row0; G.N = args.g[i].N;
+            G.C = args.g[i].C; G.ldc = args.g[i].ldc; G.ntile_begin = args.g[i].ntile_begin;
+        }
+    split_target(args, g, split, G.C, G.ldc);
+    const int n = (nt - G.ntile_begin) * (32 * NW) + 32 * wave + lr;   // this lane's weight row
+    const bool okn = n < G.N;
+    const int64_t row = G.row0 + (okn ? n : G.N - 1);
+    const int K = args.K;
+    const int nchunks = (K + 63) / 64;
+    const int ngroups = (nchunks + CH - 1) / CH;
+    const int gb = split * groups_per_block;
+    const int gn = max(0, min(ngroups, gb + groups_per_block) - gb);
+    const int glast = gb + max(gn, 1) - 1;
+    const uint8_t * W = (const uint8_t *)G.W;
+
+    // activation DMA sources: slot q of the slice holds row q / CPR, logical chunk
+    // (q % CPR) ^ (row & 7); rows past M read the last row and k past K the row's first chunk
+    // (finite values, multiplied by zero weights or never stored)
+    const uint16_t * asrc[C::PA];
+    int acol[C::PA];
+#pragma unroll
+    for (int i = 0; i < C::PA; i++) {
+        const int q = (i * NW + wave) * WAVE + lane;
+        const int r = q / CPR, c = (q % CPR) ^ (r & 7);
+        asrc[i] = args.A + (int64_t)min(r, args.M - 1) * args.lda;
+        acol[i] = 8 * c;
+    }
+    // group grp (clamped to the block's last) into stage st
+    auto issue = [&](int grp, int st) __attribute__((always_inline)) {
+        const int gg = min(grp, glast);
+        uint8_t * base = smem + st * C::STAGE;
+        const int64_t kb = (int64_t)gg * CH * 64;
+#pragma unroll
+        for (int i = 0; i < C::PA; i++) {
+            const int64_t k = kb + acol[i];
+            dma16(asrc[i] + (k < K ? k : 0), base + (i * NW + wave_s) * 1024);
+        }
+#pragma unroll
+        for (int c = 0; c < CH; c++) {
+            const int cc = min(gg * CH + c, nchunks - 1);
+            const int64_t k0 = (int64_t)cc * 64;
+#pragma unroll
+            for (int p = 0; p < NP; p++)
+                dma16(P::piece(W, G.rows_total, K, row, k0, lg, p),
+                      base + C::A_BYTES + ((c * NP + p) * NW + wave_s) * 1024);
+        }
+    };
+
+    float16v acc[MT][1];
+#pragma unroll
+    for (int i = 0; i < MT; i++)
+#pragma unroll
+        for (int e = 0; e < 16; e++) acc[i][0][e] = 0.0f;
+    auto compute = [&](int grp, int st) __attribute__((always_inline)) {
+        const uint8_t * base = smem + st * C::STAGE;
+#pragma unroll
+        for (int c = 0; c < CH; c++) {
+            const int cc = grp * CH + c;
+            u32x4 pc[NP];
+#pragma unroll
+            for (int p = 0; p < NP; p++)
+                pc[p] = *(const u32x4 *)(base + C::A_BYTES + ((c * NP + p) * NW + wave) * 1024 + 16 * lane);
+            WLoad<WT> w;
+            P::item(w, pc, G.rows_total, K, row, (int64_t)min(cc, nchunks - 1) * 64, lg,
+                    okn && cc < nchunks && (WT != T_Q8_0 || (int64_t)cc * 64 + 32 * lg < K));
+            u32x4 b[4];
+            int run0, run1;
+            w.decode_fast(lg, b, run0, run1);
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                const int ch = 8 * c + (q < 2 ? run0 + 8 * q : run1 + 8 * (q - 2)) / 8;   // slice chunk
+                const half8 bf = __builtin_bit_cast(half8, b[q]);
+#pragma unroll
+                for (int i = 0; i < MT; i++) {
+                    const int r = 32 * i + lr;
+                    const half8 af = *(const half8 *)(base + (r * CPR + (ch ^ (r & 7))) * 16);
+                    acc[i][0] = mfma32(af, bf, acc[i][0]);
+                }
+            }
+        }
+    };
+
+    if (gn > 0) {
+#pragma unroll
+        for (int q = 0; q < NS - 1; q++) issue(gb + q, q);
+        // step j: group gb + j from stage j % NS; the DMA of group gb + j + NS - 1 into the stage
+        // group gb + j - 1 used. Unrolled by NS so the register ring's indices are constants.
+        auto step = [&](int j, auto Sc) __attribute__((always_inline)) {
+            constexpr int S = decltype(Sc)::value;
+            wait_vm_lgkm0<(NS - 2) * C::PER>();
+            __builtin_amdgcn_s_barrier();
+            issue(gb + j + NS - 1, (S + NS - 1) % NS);
+            compute(gb + j, S);
+        };
+        int j = 0;
+        for (; j + NS <= gn; j += NS) {
+            step(j, std::integral_constant<int, 0>());
+            step(j + 1, std::integral_constant<int, 1>());
+            if constexpr (NS > 2) step(j + 2, std::integral_constant<int, 2 % NS>());
+            if constexpr (NS > 3) step(j + 3, std::integral_constant<int, 3 % NS>());
+        }
+        const int left = gn - j;
+        if (left > 0) step(j, std::integral_constant<int, 0>());
+        if (left > 1) step(j + 1, std::integral_constant<int, 1 % NS>());
+        if constexpr (NS > 2) if (left > 2) step(j + 2, std::integral_constant<int, 2 % NS>());
+        wait_vm_lgkm0<0>();   // no DMA may still be writing this block's LDS when it exits
+    }
+
+    scale_rows(acc, args.scales, 0, lg, args.M);
+    if (!okn || gn == 0) return;
+#pragma unroll
+    for (int i = 0; i < MT; i++) {
+#pragma unroll
+        for (int e = 0; e < 16; e++) {
+            const int r = i * 32 + 8 * (e / 4) + 4 * lg + (e % 4);
+            if (r >= args.M) continue;
+            float * p = G.C + (int64_t)r * G.ldc + n;
+            if (ks == 1 || args.part) *p = acc[i][0][e];
+            else unsafeAtomicAdd(p, acc[i][0][e]);
+        }
+    }
+}
+
 // The K-split partials summed in split order, C_g[r][n] = P[0][r][pcol_g + n] + P[1][..] + ...:
 // one thread per 4 columns of a partial row (every group's N and pcol are multiples of 16).
 __global__ void __launch_bounds__(256) reduce_splits_kernel(GemmArgs a, int ks) {
@@ -1634,6 +1905,68 @@ static bool use_skinny(int wt, const GemmArgs & a) {
 
 static int skinny_ch(int M) { return M <= 64 ? 4 : 2; }
 
+// The LDS-DMA skinny kernel (Q4_K, Q8_0, Q6_K): chunk depth CH and ring depth NS per weight type
+// and 32-row M tile, the deepest ring of whole groups that fits in LDS (MI355X_SKINNY_DMA=0
+// selects the register-staged kernel, for comparison).
+// Where it is faster (measured at N 3072-8192, K 3072-8192 on MI355X): Q6_K at every M (M 128:
+// 39.4 against 43.2 us at 8192 x 3072) and Q8_0 past 64 rows; Q4_K, and Q8_0 up to 64 rows, keep
+// the register kernel, which is as fast or faster there (Q4_K M 32: 19.1 against 21.8 us), being
+// bound by its decode and address VALU work rather than by the weight bytes in flight.
+// MI355X_SKINNY_DMA=1 forces this kernel for the three types, 0 the register one (tests).
+// The scale chunks it reads stay inside their planes when every panel's row count is a multiple
+// of 16 (the planes then span whole 16-byte chunks); other panels take the register kernel.
+static bool skinny_dma(int wt, const GemmArgs & a) {
+    if (!(wt == T_Q4_K || wt == T_Q8_0 || wt == T_Q6_K)) return false;
+    const char * e = getenv("MI355X_SKINNY_DMA");
+    const int force = (e && *e) ? atoi(e) : -1;
+    if (force == 0) return false;
+    if (force < 0 && !(wt == T_Q6_K || (wt == T_Q8_0 && a.M > 64))) return false;
+    for (int i = 0; i < a.ng; i++)
+        if (a.g[i].rows_total % 16 != 0) return false;
+    return true;
+}
+static int skinny_dma_ch(int wt, int M) {
+    const int mt = (M + 31) / 32;
+    if (wt == T_Q6_K) return mt <= 1 ? 2 : 1;
+    if (wt == T_Q8_0) return mt <= 2 ? 2 : 1;
+    return mt <= 1 ? 4 : 2;
+}
+static int skinny_chunk_depth(int wt, const GemmArgs & a) {
+    return skinny_dma(wt, a) ? skinny_dma_ch(wt, a.M) : skinny_ch(a.M);
+}
+
+template <int WT, int MT, int CH, int NS>
+static hipError_t launch_skinny_dma1(const GemmArgs & a, int nblocks, int gpb, hipStream_t st) {
+    using C = SkDmaCfg<WT, MT, CH, NS>;
+    auto kern = gemm_skinny_dma_kernel<WT, MT, CH, NS>;
+    static bool attr = false;
+    if (!attr) {
+        const hipError_t e = hipFuncSetAttribute((const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize, C::LDS);
+        if (e != hipSuccess) return e;
+        attr = true;
+    }
+    hipLaunchKernelGGL(kern, dim3(nblocks), dim3(C::THREADS), C::LDS, st, a, gpb);
+    return hipGetLastError();
+}
+
+template <int WT>
+static hipError_t launch_skinny_dma(const GemmArgs & a, int nblocks, int gpb, hipStream_t st) {
+    const int mt = (a.M + 31) / 32;
+    if constexpr (WT == T_Q6_K) {
+        if (mt == 1) return launch_skinny_dma1<WT, 1, 2, 3>(a, nblocks, gpb, st);
+        if (mt == 2) return launch_skinny_dma1<WT, 2, 1, 4>(a, nblocks, gpb, st);
+        return launch_skinny_dma1<WT, 4, 1, 4>(a, nblocks, gpb, st);
+    } else if constexpr (WT == T_Q8_0) {
+        if (mt == 1) return launch_skinny_dma1<WT, 1, 2, 4>(a, nblocks, gpb, st);
+        if (mt == 2) return launch_skinny_dma1<WT, 2, 2, 3>(a, nblocks, gpb, st);
+        return launch_skinny_dma1<WT, 4, 1, 4>(a, nblocks, gpb, st);
+    } else {
+        if (mt == 1) return launch_skinny_dma1<WT, 1, 4, 3>(a, nblocks, gpb, st);
+        if (mt == 2) return launch_skinny_dma1<WT, 2, 2, 4>(a, nblocks, gpb, st);
+        return launch_skinny_dma1<WT, 4, 2, 3>(a, nblocks, gpb, st);
+    }
+}
+
 static int skinny_ntiles(const GemmArgs & a) {
     int nt = 0;
     for (int i = 0; i < a.ng; i++) nt += (a.g[i].N + 32 * SK_NW - 1) / (32 * SK_NW);
@@ -1641,8 +1974,9 @@ static int skinny_ntiles(const GemmArgs & a) {
 }
 
 // K groups per block (the split count is ceil(groups / that)), at most `cap` splits
-static int skinny_gpb(const GemmArgs & a, int cap) {
-    const int ngroups = ((a.K + 63) / 64 + skinny_ch(a.M) - 1) / skinny_ch(a.M);
+static int skinny_gpb(int wt, const GemmArgs & a, int cap) {
+    const int ch = skinny_chunk_depth(wt, a);
+    const int ngroups = ((a.K + 63) / 64 + ch - 1) / ch;
     double blocks = 240.0;
     if (const char * e = getenv("MI355X_SKINNY_BLOCKS")) {   // tuning override
         const int v = atoi(e);
@@ -1688,8 +2022,9 @@ static GemmPlan plan_gemm(int wt, const GemmArgs & a, int cap) {
     if (use_skinny(wt, a)) {
         p.skinny = true;
         p.cfg = SKINNY_CFG;
-        p.gpb = skinny_gpb(a, cap);
-        const int ngroups = ((a.K + 63) / 64 + skinny_ch(a.M) - 1) / skinny_ch(a.M);
+        p.gpb = skinny_gpb(wt, a, cap);
+        const int ch = skinny_chunk_depth(wt, a);
+        const int ngroups = ((a.K + 63) / 64 + ch - 1) / ch;
         p.ks = (ngroups + p.gpb - 1) / p.gpb;
         return p;
     }
@@ -1737,11 +2072,14 @@ hipError_t launch_gemm(int wt, const GemmArgs & a_in, int /*unused*/, hipStream_
     if (p.skinny) {
         switch (wt) {
             case T_F16: e = launch_skinny<T_F16>(a, nblocks, p.gpb, st); break;
-            case T_Q8_0: e = launch_skinny<T_Q8_0>(a, nblocks, p.gpb, st); break;
+            case T_Q8_0: e = skinny_dma(wt, a) ? launch_skinny_dma<T_Q8_0>(a, nblocks, p.gpb, st)
+                                            : launch_skinny<T_Q8_0>(a, nblocks, p.gpb, st); break;
             case T_Q4_0: e = launch_skinny<T_Q4_0>(a, nblocks, p.gpb, st); break;
-            case T_Q4_K: e = launch_skinny<T_Q4_K>(a, nblocks, p.gpb, st); break;
+            case T_Q4_K: e = skinny_dma(wt, a) ? launch_skinny_dma<T_Q4_K>(a, nblocks, p.gpb, st)
+                                            : launch_skinny<T_Q4_K>(a, nblocks, p.gpb, st); break;
             case T_Q5_K: e = launch_skinny<T_Q5_K>(a, nblocks, p.gpb, st); break;
-            case T_Q6_K: e = launch_skinny<T_Q6_K>(a, nblocks, p.gpb, st); break;
+            case T_Q6_K: e = skinny_dma(wt, a) ? launch_skinny_dma<T_Q6_K>(a, nblocks, p.gpb, st)
+                                            : launch_skinny<T_Q6_K>(a, nblocks, p.gpb, st); break;
             case T_MXFP4: e = launch_skinny<T_MXFP4>(a, nblocks, p.gpb, st); break;
             default: break;
         }

@@ -384,6 +384,36 @@ def test_skinny_mul_mat(mx, wtype, M):
     _assert_bars(ref, got[:, :N], M, N, f"skinny {O.TYPE_NAMES[wtype]} M={M}")
 
 
+@pytest.mark.parametrize("M", [1, 32, 64, 100, 128])
+@pytest.mark.parametrize("wtype", [O.Q8_0, O.Q4_K, O.Q6_K])
+def test_skinny_dma_matches_register_kernel(mx, monkeypatch, wtype, M):
+    """The skinny kernel with the weight staged by LDS DMA (Q8_0, Q4_K, Q6_K) against the
+    register-staged one (MI355X_SKINNY_DMA=0) on the same packed activations: both walk the same
+    64-deep chunks in the same order with the same decoders, so where their K splits coincide
+    (one split: K within one block's groups) the bits are equal; the DMA form also meets the
+    oracle bars. N 400 (ragged against the 128-row block), K with a 32-value tail for Q8_0."""
+    import torch
+    K = 1024 if wtype in SUPER_BLOCK else 1056
+    N = 400
+    W = O.fill_normal((N, K), 990 + wtype, 0.0, 0.02)
+    Xf = O.fill_normal((M, K), 991 + M)
+    P = O.quantize(wtype, W)
+    w = mx.upload_weight(wtype, P, N, K)
+    a16, sc = mx.pack_act(_dev(Xf))
+    got = {}
+    for dma in ("1", "0"):
+        monkeypatch.setenv("MI355X_SKINNY_DMA", dma)
+        monkeypatch.setenv("MI355X_SKINNY_BLOCKS", "4")   # one K split: the whole K in each block
+        c = torch.full((M, N), float("nan"), dtype=torch.float32, device="cuda")
+        mx.gemm(wtype, a16, sc, K, [(w, N, 0, N, c)])
+        torch.cuda.synchronize()
+        got[dma] = c.cpu().numpy()
+    assert np.isfinite(got["1"]).all()
+    assert np.array_equal(got["1"], got["0"]), float(np.abs(got["1"] - got["0"]).max())
+    _assert_bars(O.mul_mat(wtype, P, Xf, N, K), got["1"], M, N, f"skinny dma {O.TYPE_NAMES[wtype]} M={M}",
+                 cos_floor=0.999 if M >= 8 else -1.0)
+
+
 @pytest.mark.parametrize("wtype", SKINNY_TYPES)
 def test_skinny_gemm_fused_nan_outputs(mx, wtype):
     import torch
