@@ -799,7 +799,7 @@ def mul_mat_one(spec):
             "GBps": round(nbytes / us / 1e3, 1), "decode_first": int(mx.lib().mi355x_mul_mat_decode_first(wt, M, N, K))}
 
 
-def configs_bench(args, subset=False):
+def configs_bench(args, subset=False, print_line=True):
     """The single-op configurations, each through the C ABI entry the backend uses for it and
     against the roofline that bounds it (arithmetic intensity against the 2.5 PFLOP/s / 8 TB/s
     ridge of ~312 FLOP/byte). MUL_MAT: mi355x_mul_mat (activation pack + GEMM) on an HBM-resident
@@ -892,7 +892,7 @@ def configs_bench(args, subset=False):
            {"tflops_causal_visible": round(visible / us / 1e6, 1)})
     del q, kc, m, out, wsp
     torch.cuda.empty_cache()
-    if subset:
+    if subset or not print_line:
         return cases
     print(json.dumps({
         "metric": "single-op configurations vs their rooflines (MI355X peaks: 2.5 PFLOP/s fp16, 8 TB/s)",
@@ -1109,7 +1109,7 @@ def main():
         del pf
         torch.cuda.empty_cache()
         t0 = time.time()
-        res["configs"] = configs_bench(args, subset=True)
+        res["configs"] = configs_bench(args, print_line=False)
         moe = moe_bench(args)
         res["configs"]["MUL_MAT_ID 128e top-8 Q4_K"] = {
             "GBps": moe["value"], "frac": moe["roofline"]["frac"], "bound": "hbm", "ops": moe["ops"]}

@@ -111,6 +111,40 @@ __device__ __forceinline__ float wave_sum(float v) {
     return v;
 }
 
+// One activation row of up to PACK_WAVE_K values packed by one wave: x / s as fp16 and s = the
+// row's max |x| (1 for a zero row), rounded as the block-per-row pack does (the product rounded
+// to f32, then to fp16). The max comes from lane exchanges alone, with all of the row's loads in
+// flight at once. Row-major output at A16 + m * lda, or (TL) the tiled layout over K.
+constexpr int PACK_WAVE_VEC = 16;                       // float4 a lane
+constexpr int PACK_WAVE_K = WAVE * PACK_WAVE_VEC * 4;   // 4096 values
+template <bool TL>
+__device__ __forceinline__ void pack_row_wave(const float * x, int m, int K, uint16_t * A16, int64_t lda,
+                                              float * scales, int lane) {
+    const int n4 = K / 4;
+    float4v v[PACK_WAVE_VEC];
+    float amax = 0.0f;
+#pragma unroll
+    for (int i = 0; i < PACK_WAVE_VEC; i++) {
+        const int c = lane + i * WAVE;
+        v[i] = c < n4 ? *(const float4v *)(x + 4 * c) : float4v{0, 0, 0, 0};
+        amax = fmaxf(amax, fmaxf(fmaxf(fabsf(v[i][0]), fabsf(v[i][1])), fmaxf(fabsf(v[i][2]), fabsf(v[i][3]))));
+    }
+    amax = wave_max(amax);
+    const float s = amax > 0.0f ? amax : 1.0f;
+    const float inv = 1.0f / s;
+#pragma unroll
+    for (int i = 0; i < PACK_WAVE_VEC; i++) {
+        const int c = lane + i * WAVE;
+        if (c < n4) {
+            u32x2 o;
+            o[0] = pack2h(mul_rn(v[i][0], inv), mul_rn(v[i][1], inv));
+            o[1] = pack2h(mul_rn(v[i][2], inv), mul_rn(v[i][3], inv));
+            *(u32x2 *)(TL ? A16 + tiled_index(m, 4 * c, K) : A16 + (int64_t)m * lda + 4 * c) = o;
+        }
+    }
+    if (lane == 0) scales[m] = s;
+}
+
 // Blocks are handed to the 8 XCDs round-robin by linear id. Renumber so that each XCD gets a
 // contiguous run of logical ids (XCD x takes ids [x q + min(x, r), ...) of its q or q + 1
 // blocks, q = n / 8, r = n % 8; a bijection for any n): work items that share an operand panel

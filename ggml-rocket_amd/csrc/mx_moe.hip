@@ -8,7 +8,8 @@
 //   1. pack_act converts each distinct activation row b[t][i] (T * ne11 of them) to fp16 with
 //      its per-row scale, once, however many experts read it;
 //   2. moe_sort buckets the rows by expert (counting sort in LDS) and writes a work list of
-//      (expert, first row) tiles of MOE_BM rows;
+//      (expert, first row) tiles of MOE_BM rows; steps 1 and 2 share one launch (moe_prep) when
+//      the rows fit a one-wave pack;
 //   3. moe_gemm runs every (tile, N block) pair in ONE launch: it gathers the tile's activation
 //      rows by index, streams that expert's weight panel through the same fused-dequant LDS
 //      staging as the dense GEMM, and scatters each output row to dst[t][s]. Blocks past the
@@ -60,8 +61,11 @@ __device__ __forceinline__ int2 block_scan2(int & x, int & y, int2 * wsum) {
 
 // One block: counts the (token, slot) rows of every expert, lays the experts' rows out
 // contiguously (bucket offsets off[e]) and lists the tiles of MOE_BM rows as (expert, first row).
-// Both prefix sums run across the block; rows are placed with LDS cursors.
-__global__ void __launch_bounds__(MOE_SORT_THREADS) moe_sort_kernel(MoeArgs a) {
+// Both prefix sums run across the block; rows are placed with LDS cursors. A thread keeps the
+// first SORT_KEEP ids it reads in registers for the placement pass, so up to
+// SORT_KEEP * MOE_SORT_THREADS rows are read from memory once.
+constexpr int SORT_KEEP = 8;
+__device__ __forceinline__ void moe_sort_block(const MoeArgs & a) {
     extern __shared__ __align__(16) int32_t sh[];
     int32_t * cnt = sh;              // [E] rows per expert, then the placement cursor
     __shared__ int32_t bad;
@@ -71,12 +75,24 @@ __global__ void __launch_bounds__(MOE_SORT_THREADS) moe_sort_kernel(MoeArgs a) {
     for (int e = t; e < a.E; e += MOE_SORT_THREADS) cnt[e] = 0;
     if (t == 0) bad = 0;
     __syncthreads();
-    for (int r = t; r < R; r += MOE_SORT_THREADS) {
+    auto id_of = [&](int r) {
         const int tok = r / a.U, s = r % a.U;
-        const int e = a.ids[(int64_t)tok * a.ids_nb1 + (int64_t)s * a.ids_nb0];
+        return a.ids[(int64_t)tok * a.ids_nb1 + (int64_t)s * a.ids_nb0];
+    };
+    int keep[SORT_KEEP];
+#pragma unroll
+    for (int i = 0; i < SORT_KEEP; i++) {
+        const int r = t + i * MOE_SORT_THREADS;
+        keep[i] = r < R ? id_of(r) : -1;
+    }
+    auto count = [&](int e) {
         if (e < 0 || e >= a.E) atomicOr(&bad, 1);
         else atomicAdd(&cnt[e], 1);
-    }
+    };
+#pragma unroll
+    for (int i = 0; i < SORT_KEEP; i++)
+        if (t + i * MOE_SORT_THREADS < R) count(keep[i]);
+    for (int r = t + SORT_KEEP * MOE_SORT_THREADS; r < R; r += MOE_SORT_THREADS) count(id_of(r));
     __syncthreads();
     // thread t owns experts [t * per, (t + 1) * per)
     const int per = (a.E + MOE_SORT_THREADS - 1) / MOE_SORT_THREADS;
@@ -103,13 +119,32 @@ __global__ void __launch_bounds__(MOE_SORT_THREADS) moe_sort_kernel(MoeArgs a) {
         a.err[0] = bad;
     }
     __syncthreads();
-    for (int r = t; r < R; r += MOE_SORT_THREADS) {
-        const int tok = r / a.U, s = r % a.U;
-        const int e = a.ids[(int64_t)tok * a.ids_nb1 + (int64_t)s * a.ids_nb0];
-        if (e < 0 || e >= a.E) continue;
+    auto place = [&](int r, int e) {
+        if (e < 0 || e >= a.E) return;
         const int p = atomicAdd(&cnt[e], 1);
         a.rows[p] = r;
+    };
+#pragma unroll
+    for (int i = 0; i < SORT_KEEP; i++) {
+        const int r = t + i * MOE_SORT_THREADS;
+        if (r < R) place(r, keep[i]);
     }
+    for (int r = t + SORT_KEEP * MOE_SORT_THREADS; r < R; r += MOE_SORT_THREADS) place(r, id_of(r));
+}
+
+__global__ void __launch_bounds__(MOE_SORT_THREADS) moe_sort_kernel(MoeArgs a) { moe_sort_block(a); }
+
+// The op's two passes before the GEMM in one launch, since neither needs the other: block 0
+// buckets the rows, every other block packs MOE_SORT_THREADS / WAVE distinct activation rows,
+// one wave a row (rows of at most PACK_WAVE_K values).
+__global__ void __launch_bounds__(MOE_SORT_THREADS) moe_prep_kernel(MoeArgs a) {
+    if (blockIdx.x == 0) {
+        moe_sort_block(a);
+        return;
+    }
+    const int m = (blockIdx.x - 1) * (MOE_SORT_THREADS / WAVE) + threadIdx.x / WAVE;
+    if (m >= a.T * a.ne11) return;   // the whole wave
+    pack_row_wave<false>(a.b + (int64_t)m * a.b_nb1, m, a.K, a.a16, a.K, a.scales, threadIdx.x % WAVE);
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -330,11 +365,19 @@ int moe_max_tiles(int T, int U, int E) { return (T * U + MOE_BM - 1) / MOE_BM + 
 
 hipError_t launch_moe(int wt, const MoeArgs & a, hipStream_t st) {
     const int R = a.T * a.U;
-    // 1. pack the distinct activation rows
-    hipError_t e = launch_pack_act(a.b, a.b_nb1, a.T * a.ne11, a.K, a.a16, a.K, a.scales, st);
-    if (e != hipSuccess) return e;
-    // 2. bucket
-    hipLaunchKernelGGL(moe_sort_kernel, dim3(1), dim3(MOE_SORT_THREADS), (size_t)a.E * sizeof(int32_t), st, a);
+    // 1. pack the distinct activation rows and 2. bucket the rows by expert: one launch when the
+    // rows fit the one-wave pack, else the block-per-row pack, then the bucketing
+    hipError_t e = hipSuccess;
+    const int prows = a.T * a.ne11;
+    constexpr int RPB = MOE_SORT_THREADS / WAVE;
+    if (a.K <= PACK_WAVE_K) {
+        hipLaunchKernelGGL(moe_prep_kernel, dim3(1 + (prows + RPB - 1) / RPB), dim3(MOE_SORT_THREADS),
+                           (size_t)a.E * sizeof(int32_t), st, a);
+    } else {
+        e = launch_pack_act(a.b, a.b_nb1, prows, a.K, a.a16, a.K, a.scales, st);
+        if (e != hipSuccess) return e;
+        hipLaunchKernelGGL(moe_sort_kernel, dim3(1), dim3(MOE_SORT_THREADS), (size_t)a.E * sizeof(int32_t), st, a);
+    }
     e = hipGetLastError();
     if (e != hipSuccess || R == 0) return e;
     // 3. grouped GEMM over an upper bound of tiles

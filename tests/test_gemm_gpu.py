@@ -58,6 +58,46 @@ def test_pack_act_bitexact(mx):
     assert np.array_equal(got_a, want_a)
 
 
+@pytest.mark.parametrize("K", [4, 764, 2048, 4096, 4100, 14336])
+@pytest.mark.parametrize("form", ["wave", "block"])
+@pytest.mark.parametrize("tiled", [False, True])
+def test_pack_act_forms_bitexact(mx, monkeypatch, K, form, tiled):
+    """Both forms of the activation pack (one wave a row up to 4096 values, one block a row past
+    that or with MI355X_PACK_WAVE_K=0) against the oracle's pack, row-major and tiled, with an
+    outlier row, a zero row and a value past fp16 range; the clearing variant leaves exactly the
+    columns it is asked to clear at zero."""
+    import torch
+    if tiled and K % 32:
+        pytest.skip("the tiled layout needs K % 32 == 0")
+    monkeypatch.setenv("MI355X_PACK_WAVE_K", "4096" if form == "wave" else "0")
+    M = 37
+    X = O.fill_normal((M, K), 8 + K)
+    X[3] *= 3000.0
+    X[5] = 0.0
+    X[9, K // 2] = 1e6
+    a16, sc = mx.pack_act(_dev(X), tiled=tiled)
+    want_a, want_s = O.pack_act(X)
+    got = a16.cpu().numpy().view(np.uint16)
+    if tiled:   # tile (r / 16, k / 32) of 16 x 32 values, row-major inside
+        rows = got.shape[0]
+        got = got.reshape(rows // 16, K // 32, 16, 32).transpose(0, 2, 1, 3).reshape(rows, K)[:M]
+    assert np.array_equal(sc.cpu().numpy(), want_s)
+    assert np.array_equal(got, want_a)
+    if not tiled:
+        L = mx.lib()
+        a2 = torch.empty((M, K), dtype=torch.float16, device="cuda")
+        s2 = torch.empty((M,), dtype=torch.float32, device="cuda")
+        z = torch.full((M, 40), 7.0, device="cuda")
+        x = _dev(X)
+        st = L.mi355x_pack_act_clear(0, mx._ptr(x), K, M, K, mx._ptr(a2), mx._ptr(s2), mx._ptr(z), 40, 33,
+                                     mx.stream_handle())
+        assert st == mx.OK
+        torch.cuda.synchronize()
+        zz = z.cpu().numpy()
+        assert np.all(zz[:, :33] == 0.0) and np.all(zz[:, 33:] == 7.0)
+        assert np.array_equal(a2.cpu().numpy().view(np.uint16), want_a)
+
+
 @pytest.mark.parametrize("wtype", [O.F16, O.Q8_0, O.Q4_0, O.Q4_K, O.Q5_K, O.Q6_K, O.MXFP4])
 def test_dequant_f16_bitexact(mx, wtype):
     N, K = 96, 1024
