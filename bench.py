@@ -634,7 +634,8 @@ def host_path(args):
             if st != 0:
                 raise RuntimeError(f"graph_compute status {st}")
 
-    keys = ("bytes_up", "bytes_down", "up_copy_s", "up_wait_s", "down_copy_s", "down_wait_s")
+    keys = ("bytes_up", "bytes_down", "pieces_up", "pieces_down", "up_copy_s", "up_wait_s", "down_copy_s",
+            "down_wait_s", "copy_api_s", "weight_s")
 
     def run_split():
         """One more pass, each call's wall time and host-side copy accounting summed per group of
@@ -672,7 +673,8 @@ def host_path(args):
         per_call[n] = {"ms": round(p["wall_s"] / c * 1e3, 3), "MB_up": round(p["bytes_up"] / c / 1e6, 2),
                        "MB_down": round(p["bytes_down"] / c / 1e6, 2),
                        "link_floor_ms": round(mb / link["GBps_one_way"], 3) if link else None,
-                       **{k.replace("_s", "_ms"): round(p[k] / c * 1e3, 3) for k in keys[2:]}}
+                       "pieces": round((p["pieces_up"] + p["pieces_down"]) / c, 1),
+                       **{k.replace("_s", "_ms"): round(p[k] / c * 1e3, 3) for k in keys[4:]}}
     bytes_step = (h1["bytes_up"] - h0["bytes_up"]) + (h1["bytes_down"] - h0["bytes_down"])
     fb = be.cpu_fallbacks()
     routes = {r: be.route_ops(r) for r in ("prepacked-q", "fused-resident", "fa", "mt", "fused")}

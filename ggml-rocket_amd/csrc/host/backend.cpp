@@ -340,9 +340,11 @@ struct DlOp {
 
 // Host-side accounting of the copies (mi355x_backend_host_stats).
 struct HostStats {
-    long calls = 0, fa_mirror_hits = 0, redone = 0;
+    long calls = 0, fa_mirror_hits = 0, redone = 0, pieces_up = 0, pieces_down = 0;
     double bytes_up = 0, bytes_down = 0;
     double wall_s = 0, up_copy_s = 0, up_wait_s = 0, down_copy_s = 0, down_wait_s = 0;
+    double copy_api_s = 0;   // enqueueing the copies (hipMemcpy*Async, event records and waits)
+    double weight_s = 0;     // finding (or building) the weights in the HBM cache
 };
 
 double now_s() {
@@ -621,6 +623,12 @@ void dl_bytes(Ctx * c, int op, const void * dev, void * host, size_t n, const vo
 // Starts the DMAs of queued pieces into free download slots.
 int dl_issue(Ctx * c) {
     Ring & R = c->down;
+    const double t0 = now_s();
+    struct Account {
+        Ctx * c;
+        double t0;
+        ~Account() { c->hs.copy_api_s += now_s() - t0; }
+    } account{c, t0};
     while (c->dl_issued < c->dl_pieces.size() && c->dl_issued < c->dl_drained + (size_t)R.nslot) {
         const DlPiece & p = c->dl_pieces[c->dl_issued];
         const DlItem & it = c->dl_items[(size_t)p.item];
@@ -638,6 +646,7 @@ int dl_issue(Ctx * c) {
         if (e != hipSuccess || hipEventRecord(R.ev[k], c->dstream) != hipSuccess) return MI355X_E_DEVICE;
         R.pending[k] = true;
         c->dl_issued++;
+        c->hs.pieces_down++;
     }
     return MI355X_OK;
 }
@@ -760,11 +769,14 @@ int upload_on(Ctx * c, hipStream_t st, void * dst, const void * src, size_t n) {
         TRY_RC(R.settle(k));
         const double t1 = now_s();
         host_copy(c, R.slot[k], (const char *)src + o, len);
+        const double t2 = now_s();
         c->hs.up_wait_s += t1 - t0;
-        c->hs.up_copy_s += now_s() - t1;
+        c->hs.up_copy_s += t2 - t1;
         if (hipMemcpyAsync((char *)dst + o, R.slot[k], len, hipMemcpyHostToDevice, st) != hipSuccess ||
             hipEventRecord(R.ev[k], st) != hipSuccess)
             return MI355X_E_DEVICE;
+        c->hs.copy_api_s += now_s() - t2;
+        c->hs.pieces_up++;
         R.pending[k] = true;
         o += len;
         c->up_piece = std::min(c->up_piece * 2, R.chunk);
@@ -931,7 +943,9 @@ int mul_mat_device(Ctx * c, const std::vector<mi355x_tensor *> & grp, bool want_
     for (size_t i = 0; i < grp.size(); i++) {
         const mi355x_tensor * a = grp[i]->src[0];
         bool res = false;
+        const double tw = now_s();
         TRY(get_weight(c, a, a->ne[1], K, want_f16, true, 0, c->wscratch[i], ws[i], res));
+        c->hs.weight_s += now_s() - tw;
         all_resident = all_resident && res;
         outs[i].w_dev = ws[i].dev;
         outs[i].rows_total = a->ne[1];
@@ -1443,6 +1457,10 @@ MI355X_API void mi355x_backend_host_stats(mi355x_backend_t c, mi355x_host_stats 
     out->up_wait_s = h.up_wait_s;
     out->down_copy_s = h.down_copy_s;
     out->down_wait_s = h.down_wait_s;
+    out->copy_api_s = h.copy_api_s;
+    out->weight_s = h.weight_s;
+    out->pieces_up = h.pieces_up;
+    out->pieces_down = h.pieces_down;
 }
 
 static int graph_compute_nodes(mi355x_backend_t c, mi355x_tensor * const * nodes, int n_nodes);

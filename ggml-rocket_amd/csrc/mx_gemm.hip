@@ -749,6 +749,11 @@ gemm_f16_kernel(GemmArgs args) {
 // with it the vmcnt of every wait, is a per-column constant; the body below is instantiated once
 // per column width, and both instances meet at the same barriers (one before the loop, one per
 // stage).
+// Where a column's B rows of one stage are not a whole number of DMA instructions per wave of
+// that column (96 rows x 32 K: 6 KB for four waves), all eight waves share the B tile instead:
+// instruction i (1 KB, 1024 / RB rows) goes to wave i % 8, and the waves whose last slot has no
+// real instruction fetch the last real chunk again into a 1 KB LDS slot nobody reads, so every
+// wave issues the same number of DMA instructions a stage and the wait counts stay constants.
 // ---------------------------------------------------------------------------------------------
 template <int BM_, int BN0, int BN1, int DK, int NS>
 struct ColsCfg {
@@ -756,12 +761,17 @@ struct ColsCfg {
     static constexpr int BM = BM_, BN = BN0 + BN1, TM = BM / WGM, MI = TM / 32;
     static constexpr int CH = DK / 8, RPW = 16 / CH, RB = DK * 2, NSTAGES = NS;
     static constexpr int A_BYTES = BM * RB, B_BYTES = BN * RB, STAGE = A_BYTES + B_BYTES;
-    static constexpr int LDS = NS * STAGE;
+    static constexpr bool PERCOL = (BN0 * RB) % (4 * 1024) == 0 && (BN1 * RB) % (4 * 1024) == 0;
+    static constexpr int NBI = B_BYTES / 1024;                       // B DMA instructions a stage
+    static constexpr int PBW = (NBI + NW - 1) / NW;                  // per wave when shared
+    static constexpr int RING = NS * STAGE;
+    static constexpr int LDS = RING + (PERCOL ? 0 : (NW * PBW - NBI) * 1024);
     static constexpr int PA = A_BYTES / (THREADS * 16);
+    static constexpr int PER_MAX = PA + (PERCOL ? BN0 * RB / 4096 : PBW);
     static_assert(MI >= 1 && TM % 32 == 0 && BN0 % 32 == 0 && BN1 % 32 == 0 && BN0 % 16 == 0, "wave tile");
     static_assert(PA * THREADS * 16 == A_BYTES, "A DMA split");
-    static_assert((BN0 * RB) % (4 * 1024) == 0 && (BN1 * RB) % (4 * 1024) == 0, "B DMA split");
-    static_assert(NS >= 2 && (NS - 1) * (PA + BN0 * RB / 4096) <= 63, "vmcnt range");
+    static_assert(B_BYTES % 1024 == 0, "B DMA split");
+    static_assert(NS >= 2 && (NS - 1) * PER_MAX <= 63, "vmcnt range");
     static_assert(LDS <= 160 * 1024, "LDS");
 };
 
@@ -780,7 +790,7 @@ template <class C, int TNW, int COL0, bool TL>
 __device__ __forceinline__ void cols_body(const uint16_t * __restrict__ Ap, const float * __restrict__ scales,
                                           int64_t lda, int M, int K, ColsTile tb, uint8_t * smem, int wm) {
     constexpr int DK = C::RB / 2, NS = C::NSTAGES, NJ = TNW / 32;
-    constexpr int PB = TNW * C::RB / 4096;        // this column's B DMA per wave
+    constexpr int PB = C::PERCOL ? TNW * C::RB / 4096 : C::PBW;   // this wave's B DMA a stage
     constexpr int PER = C::PA + PB;
     const int t = threadIdx.x, lane = t % WAVE, wave = t / WAVE;
     const uint16_t * W = tb.W;
@@ -802,12 +812,21 @@ __device__ __forceinline__ void cols_body(const uint16_t * __restrict__ Ap, cons
     }
 #pragma unroll
     for (int q = 0; q < PB; q++) {
-        // rows COL0 .. COL0 + TNW of the B tile, fetched by this column's four waves; COL0 is a
-        // multiple of 16, so the swizzle of a row depends on its offset inside the column only
-        const int slot = (q * 4 + wm) * WAVE + lane;
-        const int r = slot / C::CH, c = (slot % C::CH) ^ ((r / C::RPW) & (C::CH - 1));
-        const int64_t row = row0 + min(n0 + COL0 + r, N - 1), k = 8 * c;
-        bsrc[q] = W + (TL ? tiled_index(row, k, K) : row * K + k);
+        if constexpr (C::PERCOL) {
+            // rows COL0 .. COL0 + TNW of the B tile, fetched by this column's four waves; COL0 is a
+            // multiple of 16, so the swizzle of a row depends on its offset inside the column only
+            const int slot = (q * 4 + wm) * WAVE + lane;
+            const int r = slot / C::CH, c = (slot % C::CH) ^ ((r / C::RPW) & (C::CH - 1));
+            const int64_t row = row0 + min(n0 + COL0 + r, N - 1), k = 8 * c;
+            bsrc[q] = W + (TL ? tiled_index(row, k, K) : row * K + k);
+        } else {
+            // instruction q * 8 + wave of the whole B tile (rows of both columns in order; the
+            // swizzle is the same, since BN0 is a multiple of 16)
+            const int slot = min(q * C::NW + wave, C::NBI - 1) * WAVE + lane;
+            const int r = slot / C::CH, c = (slot % C::CH) ^ ((r / C::RPW) & (C::CH - 1));
+            const int64_t row = row0 + min(n0 + r, N - 1), k = 8 * c;
+            bsrc[q] = W + (TL ? tiled_index(row, k, K) : row * K + k);
+        }
     }
     const int wave_s = __builtin_amdgcn_readfirstlane(wave), wm_s = __builtin_amdgcn_readfirstlane(wm);
     auto issue = [&](int s) {
@@ -817,7 +836,14 @@ __device__ __forceinline__ void cols_body(const uint16_t * __restrict__ Ap, cons
 #pragma unroll
         for (int q = 0; q < C::PA; q++) dma16(asrc[q] + off, st + (q * C::NW + wave_s) * 1024);
 #pragma unroll
-        for (int q = 0; q < PB; q++) dma16(bsrc[q] + off, st + C::A_BYTES + COL0 * C::RB + (q * 4 + wm_s) * 1024);
+        for (int q = 0; q < PB; q++) {
+            if constexpr (C::PERCOL) {
+                dma16(bsrc[q] + off, st + C::A_BYTES + COL0 * C::RB + (q * 4 + wm_s) * 1024);
+            } else {
+                const int gi = q * C::NW + wave_s;
+                dma16(bsrc[q] + off, gi < C::NBI ? st + C::A_BYTES + gi * 1024 : smem + C::RING + (gi - C::NBI) * 1024);
+            }
+        }
     };
 
     float16v acc[C::MI][NJ];
@@ -1646,21 +1672,23 @@ hipError_t launch_pack_act_tiled(const float * X, int64_t ldx, int M, int K, uin
 // forces one (for tuning and for the tests, which run every configuration).
 //   0-3  register-staged kernel with the weight decoded into LDS: every weight type.
 //   4-15 LDS-DMA kernel: fp16 weights only (row-major or tiled); 15 has wave columns of two
-//        widths (gemm_f16_cols_kernel).
+//        widths (gemm_f16_cols_kernel), 21 and 22 are that tile with 32-deep stages, three or
+//        four of them in flight where 15 has one of 64 (the 256 x 224 tile's DMA waits are
+//        what bounds it).
 //   16-19 Q4_K with every operand by DMA (gemm_q4k_kernel), K % 256 == 0; 18 and 19 split K
-//        (q4k_split). choose_cfg prices a launch from two rates: a block's
-//        own pace, rounds * (ov_us + MFMA work of a block / tf_cu) (pipeline fill and epilogue,
-//        then its per-CU MFMA rate), and the aggregate rate at which the L2s feed the CUs for
-//        that tile shape, L2->CU bytes of all blocks / bw (bigger tiles fetch less per FLOP but
-//        keep fewer bytes in flight per CU). The two overlap, so the estimate is their 4-norm
-//        (pace^4 + feed^4)^(1/4), which follows the measured transition between the regimes
-//        better than the max; a split-K launch adds zc microseconds per MB of output (the zero
-//        fill and the second addend's atomics). The four were fitted per configuration to
-//        measurements on tiled weights at M = 128-2048, N = 1024-28672, K = 2880-14336, each
-//        launch on a weight panel no earlier launch left in the caches: mean error 3-9% per
-//        configuration, and over 50 shapes the chosen configurations cost 0.3% more than the
-//        best measured ones.
-enum CfgKind { REG = 0, DMA = 1, Q4KDMA = 2 };
+//        (q4k_split). 20 is the skinny kernel's id (use_skinny), not a tile configuration.
+// choose_cfg prices a launch from two rates: a block's own pace, rounds * (ov_us + MFMA work
+// of a block / tf_cu) (pipeline fill and epilogue, then its per-CU MFMA rate), and the
+// aggregate rate at which the L2s feed the CUs for that tile shape, L2->CU bytes of all blocks
+// / bw (bigger tiles fetch less per FLOP but keep fewer bytes in flight per CU). The two
+// overlap, so the estimate is their 4-norm (pace^4 + feed^4)^(1/4), which follows the measured
+// transition between the regimes better than the max; a split-K launch adds zc microseconds per
+// MB of output (the zero fill and the second addend's atomics). The four were fitted per
+// configuration to measurements on tiled weights at M = 128-2048, N = 1024-28672,
+// K = 2880-14336, each launch on a weight panel no earlier launch left in the caches: mean
+// error 1-9% per configuration, and over 50 shapes the chosen configurations cost 0.3-0.4%
+// more than the best measured ones.
+enum CfgKind { REG = 0, DMA = 1, Q4KDMA = 2, NONE = 3 };
 struct CfgDesc {
     int kind;        // REG: gemm_kernel, DMA: gemm_f16_kernel / _cols, Q4KDMA: gemm_q4k_kernel
     int bm, bn, ksplit;
@@ -1670,7 +1698,7 @@ struct CfgDesc {
     double bw;       // aggregate L2 -> CU TB/s
     double zc;       // split-K: microseconds per MB of output
 };
-static const CfgDesc kCfgs[] = {
+static constexpr CfgDesc kCfgs[] = {
     {REG, 128, 128, 1, 0, 0.0, 0.0, 0.0, 0.0},        // 0: 4 waves of 64x64
     {REG, 128, 128, 2, 0, 0.0, 0.0, 0.0, 0.0},        // 1: same, K split (launcher-sized, >= 2)
     {REG, 256, 128, 1, 0, 0.0, 0.0, 0.0, 0.0},        // 2: 4 waves of 128x64
@@ -1691,6 +1719,9 @@ static const CfgDesc kCfgs[] = {
     {Q4KDMA, 128, 256, 1, 64, 0.0, 0.0, 0.0, 0.0}, // 17: Q4_K by DMA, 8 waves of 64x64
     {Q4KDMA, 256, 256, 2, 64, 0.0, 0.0, 0.0, 0.0}, // 18: as 16, K split (launcher-sized, >= 2)
     {Q4KDMA, 128, 256, 2, 64, 0.0, 0.0, 0.0, 0.0}, // 19: as 17, K split (launcher-sized, >= 2)
+    {NONE, 0, 0, 1, 0, 0.0, 0.0, 0.0, 0.0},        // 20: the skinny kernel (not a tile configuration)
+    {DMA, 256, 224, 1, 32, 7.06, 9.9, 9.18, 0.00},   // 21: as 15, 4 stages of 32
+    {DMA, 256, 224, 1, 32, 6.77, 9.7, 9.15, 0.00},   // 22: as 15, 5 stages of 32
 };
 constexpr int FIRST_DMA_CFG = 4;
 constexpr int N_CFGS = sizeof(kCfgs) / sizeof(kCfgs[0]);
@@ -1755,6 +1786,8 @@ template <bool TL>
 static hipError_t launch_dma_cfg(int cfg, const GemmArgs & a, int nblocks, hipStream_t st) {
     switch (cfg) {
         case 15: return launch_cols<256, 128, 96, 64, 2, TL>(a, nblocks, st);
+        case 21: return launch_cols<256, 128, 96, 32, 4, TL>(a, nblocks, st);
+        case 22: return launch_cols<256, 128, 96, 32, 5, TL>(a, nblocks, st);
         case 4: return launch_f16<256, 256, 4, 2, 64, 2, 1, TL>(a, nblocks, st);
         case 5: return launch_f16<128, 128, 4, 2, 64, 4, 1, TL>(a, nblocks, st);
         case 6: return launch_f16<64, 128, 2, 2, 128, 3, 1, TL>(a, nblocks, st);
@@ -1853,6 +1886,7 @@ static int q4k_split(const GemmArgs & a, int bm, int bn, int cap) {
 
 static bool cfg_fits(int c, int wt, int K) {
     const CfgDesc & d = kCfgs[c];
+    if (d.kind == NONE) return false;
     if (d.kind == REG) return wt != T_F16T;
     if (d.kind == Q4KDMA) return wt == T_Q4_K && K % 256 == 0;
     if ((wt != T_F16 && wt != T_F16T) || K % d.dk) return false;
@@ -1931,7 +1965,8 @@ __global__ void zero_rows_kernel(GemmArgs args);
 // K split aims at ~240 blocks, about one per CU: fewer leave weight bytes unrequested, more add
 // atomic traffic (the fastest splits measured for Q4_K / Q8_0 at M 32-128, N 3072-14336,
 // K 3072-14336 launch 144-256 blocks).
-constexpr int SKINNY_CFG = N_CFGS;
+constexpr int SKINNY_CFG = 20;
+static_assert(kCfgs[SKINNY_CFG].kind == NONE, "the skinny kernel's id");
 
 // Row-major fp16 weights also have the DMA kernels: past M = 32 those win unless K is deep for
 // the output width (measured at M 32-128; at M 128, K 14336 x N 4096: 50 us skinny, 60 us DMA;

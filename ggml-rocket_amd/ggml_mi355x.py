@@ -403,7 +403,8 @@ class HostStats(ctypes.Structure):
     _fields_ = [("calls", ctypes.c_long), ("fa_mirror_hits", ctypes.c_long), ("copyback_redone", ctypes.c_long),
                 ("bytes_up", ctypes.c_double), ("bytes_down", ctypes.c_double), ("wall_s", ctypes.c_double),
                 ("up_copy_s", ctypes.c_double), ("up_wait_s", ctypes.c_double), ("down_copy_s", ctypes.c_double),
-                ("down_wait_s", ctypes.c_double)]
+                ("down_wait_s", ctypes.c_double), ("copy_api_s", ctypes.c_double), ("weight_s", ctypes.c_double),
+                ("pieces_up", ctypes.c_long), ("pieces_down", ctypes.c_long)]
 
 
 def host():

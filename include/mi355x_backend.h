@@ -180,6 +180,9 @@ typedef struct mi355x_host_stats {
     double up_wait_s;        /* waits for an upload slot's previous DMA */
     double down_copy_s;      /* host copies out of download slots */
     double down_wait_s;      /* waits for a download slot's DMA (and the kernels before it) */
+    double copy_api_s;       /* enqueueing the copies: the HIP copy, event-record and stream-wait calls */
+    double weight_s;         /* finding MUL_MAT weights in the HBM cache (or building them) */
+    long pieces_up, pieces_down;   /* staged copies issued in each direction */
 } mi355x_host_stats;
 MI355X_API void mi355x_backend_host_stats(mi355x_backend_t backend, mi355x_host_stats * out);
 

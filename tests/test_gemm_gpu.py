@@ -306,25 +306,27 @@ def test_pack_act_tiled_bitexact(mx):
 
 
 # Every tile configuration of mi355x_gemm, forced through MI355X_GEMM_CFG, on a ragged fused
-# launch (M and both N not multiples of any tile). Configurations 4-15 are the LDS-DMA kernels,
+# launch (M and both N not multiples of any tile). Configurations 0-3 are the register-staged
+# kernel (every weight layout but the tiled fp16 one); 4-15, 21 and 22 the LDS-DMA kernels,
 # which take fp16 weights only, row-major (F16) or tiled (F16_T); 16-19 the Q4_K kernel with
-# every operand by DMA (K % 256 == 0, Q4_K only).
-N_GEMM_CFGS = 20
-FIRST_DMA_CFG = 4
-FIRST_QDMA_CFG = 16
+# every operand by DMA (K % 256 == 0, Q4_K only). 20 is the skinny kernel (M <= 128), covered
+# by its own tests.
+REG_CFGS = list(range(0, 4))
+DMA_CFGS = list(range(4, 16)) + [21, 22]
+QDMA_CFGS = list(range(16, 20))
 F16_T = 0x101
 QUANT = (O.Q4_K, O.MXFP4, O.Q8_0, O.Q6_K, O.Q4_0, O.Q5_K)
 
 
-@pytest.mark.parametrize("cfg", list(range(N_GEMM_CFGS)))
+@pytest.mark.parametrize("cfg", REG_CFGS + DMA_CFGS + QDMA_CFGS)
 @pytest.mark.parametrize("wtype", [O.F16, O.Q4_K, F16_T, O.MXFP4, O.Q8_0, O.Q6_K, O.Q4_0, O.Q5_K])
 def test_gemm_every_tile_config(mx, monkeypatch, cfg, wtype):
     import torch
-    if FIRST_DMA_CFG <= cfg < FIRST_QDMA_CFG and wtype in QUANT:
+    if cfg in DMA_CFGS and wtype in QUANT:
         pytest.skip("the LDS-DMA configurations take fp16 weights only")
-    if cfg < FIRST_DMA_CFG and wtype == F16_T:
+    if cfg in REG_CFGS and wtype == F16_T:
         pytest.skip("the register-staged configurations do not read the tiled layout")
-    if cfg >= FIRST_QDMA_CFG and wtype != O.Q4_K:
+    if cfg in QDMA_CFGS and wtype != O.Q4_K:
         pytest.skip("the all-DMA configurations take Q4_K weights only")
     monkeypatch.setenv("MI355X_GEMM_CFG", str(cfg))
     K, M, Ns = 1280, 300, (528, 144)
