@@ -769,13 +769,15 @@ def synth_blocks(wtype, N, K, seed):
     import numpy as np
     if wtype == 12:
         return synth_q4k(N, K, seed)
-    bs, bb = {8: (32, 34), 14: (256, 210)}[wtype]
+    bs, bb = {8: (32, 34), 14: (256, 210), 39: (32, 17)}[wtype]
     blk = np.random.default_rng(seed).integers(0, 256, size=(N * K // bs, bb), dtype=np.uint8)
     d = np.array([0.0005], dtype=np.float16).view(np.uint8)
     if wtype == 8:
         blk[:, 0:2] = d
-    else:
+    elif wtype == 14:
         blk[:, 208:210] = d
+    else:
+        blk[:, 0] = 118   # MXFP4: the E8M0 block scale 2^-9, then 16 bytes of FP4 codes
     return blk.reshape(-1)
 
 
@@ -919,12 +921,38 @@ def moe_bench(args):
     logits = np.random.default_rng(0x5EED0000 + 64).standard_normal((T, E), dtype=np.float32)
     ids = np.argsort(-logits, axis=1, kind="stable")[:, :U].astype(np.int32)   # softmax is monotone
     idt = torch.from_numpy(ids).cuda()
+    # each stack in the layout the backend caches it in: Q4_K, Q8_0 and MXFP4 regrouped by 32
+    # rows, Q6_K in its split planes
+    main = moe_stack(args, mx.Q4_K_X, lambda n, k, seed: synth_q4k(n, k, seed), E, U, T, DM, FF, idt)
+    others = {}
+    if not getattr(args, "quick", False):
+        for tn, lay, wt in (("Q8_0", mx.Q8_0_X, mx.Q8_0), ("Q6_K", mx.Q6_K, mx.Q6_K), ("MXFP4", mx.MXFP4_X, mx.MXFP4)):
+            others[tn] = moe_stack(args, lay, lambda n, k, seed, wt=wt: synth_blocks(wt, n, k, seed),
+                                   E, U, T, DM, FF, idt)
+    gbs = main["GBps"]
+    return {
+        "metric": "MUL_MAT_ID expert GEMM GB/s (128 experts, top-8, 512 tok, d 2048, FFN 768, Q4_K)",
+        "value": gbs, "unit": "GB/s", "n_gpus": 1, "higher_is_better": True,
+        "dtype": "f16", "data": "synthetic (Q4_K experts from N(0,0.02), random-code Q8_0 / Q6_K / MXFP4 "
+                                "experts, N(0,1) activations and router logits)",
+        "config": {"workload": "MoE prefill expert GEMMs: gate/up and down, cold expert stacks",
+                   "experts": E, "top_k": U, "tokens": T, "d_model": DM, "ffn": FF},
+        "ops": main["ops"],
+        "roofline": {"bound": "hbm", "achieved": gbs, "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                     "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": None},
+        "other_stacks": others,
+    }
+
+
+def moe_stack(args, wt, synth, E, U, T, DM, FF, idt):
+    """Times gate/up and down of one expert-stack weight type (see moe_bench)."""
+    import torch
+    import ggml_mi355x as mx
     ops = {}
     tot_us = tot_bytes = 0.0
     for i, (name, N, K, ne11) in enumerate((("gate/up", FF, DM, 1), ("down", DM, FF, U))):
-        P = synth_q4k(E * N, K, 0x5EED0000 + 65 + i)
-        # the layout the backend caches Q4_K expert stacks in (Q4_K regrouped by 32 rows)
-        copies = [mx.upload_weight(mx.Q4_K_X, P, E * N, K) for _ in range(3)]
+        P = synth(E * N, K, 0x5EED0000 + 65 + i)
+        copies = [mx.upload_weight(wt, P, E * N, K) for _ in range(3)]
         X = torch.randn(T, ne11, K, device="cuda")
         out = torch.empty(T, U, N, device="cuda")
         ws = torch.empty(1 << 26, dtype=torch.uint8, device="cuda")
@@ -933,7 +961,7 @@ def moe_bench(args):
         def run():
             w = copies[cyc[0] % 3]
             cyc[0] += 1
-            mx.mul_mat_id(mx.Q4_K_X, w, E, N, K, X, idt, out=out, workspace=ws)
+            mx.mul_mat_id(wt, w, E, N, K, X, idt, out=out, workspace=ws)
         for _ in range(3):
             run()
         torch.cuda.synchronize()
@@ -966,16 +994,7 @@ def moe_bench(args):
         del copies, X, out, ws, g
         torch.cuda.empty_cache()
     gbs = tot_bytes / tot_us / 1e3
-    return {
-        "metric": "MUL_MAT_ID expert GEMM GB/s (128 experts, top-8, 512 tok, d 2048, FFN 768, Q4_K)",
-        "value": round(gbs, 1), "unit": "GB/s", "n_gpus": 1, "higher_is_better": True,
-        "dtype": "f16", "data": "synthetic (Q4_K experts from N(0,0.02), N(0,1) activations and router logits)",
-        "config": {"workload": "MoE prefill expert GEMMs: gate/up and down, cold expert stacks",
-                   "experts": E, "top_k": U, "tokens": T, "d_model": DM, "ffn": FF},
-        "ops": ops,
-        "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                     "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": None},
-    }
+    return {"GBps": round(gbs, 1), "frac": round(gbs / PEAK_HBM_GBS, 4), "ops": ops}
 
 
 def main():
@@ -1115,6 +1134,8 @@ def main():
         moe = moe_bench(args)
         res["configs"]["MUL_MAT_ID 128e top-8 Q4_K"] = {
             "GBps": moe["value"], "frac": moe["roofline"]["frac"], "bound": "hbm", "ops": moe["ops"]}
+        for tn, st in moe["other_stacks"].items():
+            res["configs"][f"MUL_MAT_ID 128e top-8 {tn}"] = {"bound": "hbm", **st}
         res["configs_s"] = round(time.time() - t0, 1)
         t0 = time.time()
         res["host_path"] = host_path(args)

@@ -835,7 +835,8 @@ int build_weight(Ctx * c, int t, const void * src, int64_t rows, int64_t K, int 
         TRY(mi355x_convert_f16(t, c->wstage.p, rows * K, (uint16_t *)c->wconv.p, c->stream));
         return mi355x_weight_f16_tiled(MI355X_F16, c->wconv.p, rows, K, (uint16_t *)dst, c->stream);
     }
-    if (lay == MI355X_Q4_K_X) return mi355x_weight_pack(lay, c->wstage.p, rows, K, dst, c->stream);
+    if (lay == MI355X_Q4_K_X || lay == MI355X_Q8_0_X || lay == MI355X_MXFP4_X)
+        return mi355x_weight_pack(lay, c->wstage.p, rows, K, dst, c->stream);
     if (lay != MI355X_F16 && lay != MI355X_F16_T) return mi355x_weight_pack(t, c->wstage.p, rows, K, dst, c->stream);
     // -> fp16: from the HBM layout, built first when that differs from the ggml one
     const void * q = c->wstage.p;
@@ -854,9 +855,13 @@ int get_weight(Ctx * c, const mi355x_tensor * a, int64_t rows, int64_t K, bool w
                int64_t moe_n, DevBuf & scratch, WEntry & out, bool & resident) {
     const bool moe = moe_n > 0;   // an expert stack of experts with moe_n rows each
     int lay = dev_layout(a->type, want_f16, tiled_ok, K);
-    // Q4_K experts of whole 32-row groups take the regrouped layout, whose 32-row slabs the
-    // expert GEMM loads as contiguous bytes
-    if (moe && lay == MI355X_Q4_K && moe_n % 32 == 0) lay = MI355X_Q4_K_X;
+    // Q4_K, Q8_0 and MXFP4 experts of whole 32-row groups take the regrouped layouts, whose
+    // 32-row slabs the expert GEMM loads as contiguous bytes
+    if (moe && moe_n % 32 == 0) {
+        if (lay == MI355X_Q4_K) lay = MI355X_Q4_K_X;
+        else if (lay == MI355X_Q8_0) lay = MI355X_Q8_0_X;
+        else if (lay == MI355X_MXFP4) lay = MI355X_MXFP4_X;
+    }
     const int64_t dbytes = mi355x_weight_bytes(lay, rows, K);
     if (dbytes < 0) return MI355X_E_ARG;
     CacheOutcome & oc = c->outcome[moe ? USE_MOE : (lay == MI355X_F16 || lay == MI355X_F16_T) ? USE_F16 : USE_QUANT];

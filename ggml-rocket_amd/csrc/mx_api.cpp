@@ -30,12 +30,15 @@ inline bool known_wtype(int wt) {
            wt == mx::T_Q6_K || wt == mx::T_MXFP4;
 }
 
-// the expert-stack layouts: every weight type, and Q4_K regrouped by 32 rows
-inline bool known_moe_wtype(int wt) { return known_wtype(wt) || wt == mx::T_Q4_KX; }
+// the layouts regrouped by 32 rows, built from ggml blocks for expert stacks
+inline bool x32_wtype(int wt) { return wt == mx::T_Q4_KX || wt == mx::T_Q8_0X || wt == mx::T_MXFP4X; }
+
+// the expert-stack layouts: every weight type, and the regrouped ones
+inline bool known_moe_wtype(int wt) { return known_wtype(wt) || x32_wtype(wt); }
 
 inline int64_t blck(int wt) {
     if (wt == mx::T_Q4_K || wt == mx::T_Q4_KX || wt == mx::T_Q5_K || wt == mx::T_Q6_K) return 256;
-    return (wt == mx::T_Q8_0 || wt == mx::T_Q4_0 || wt == mx::T_MXFP4) ? 32 : 1;
+    return (wt == mx::T_Q8_0 || wt == mx::T_Q8_0X || wt == mx::T_Q4_0 || wt == mx::T_MXFP4 || wt == mx::T_MXFP4X) ? 32 : 1;
 }
 
 inline bool aligned(const void * p, size_t a) { return ((uintptr_t)p % a) == 0; }
@@ -79,18 +82,22 @@ MI355X_API int mi355x_get_device_info(mi355x_device_info * out) {
 
 MI355X_API int64_t mi355x_weight_bytes(int wtype, int64_t rows, int64_t K) {
     if (wtype == mx::T_F16T) return (rows < 0 || K <= 0 || K % 32) ? -1 : mx::packed_weight_bytes(wtype, rows, K);
-    if (wtype == mx::T_Q4_KX) return (rows < 0 || K <= 0 || K % 256) ? -1 : mx::packed_weight_bytes(wtype, rows, K);
+    if (x32_wtype(wtype)) return (rows < 0 || K <= 0 || K % blck(wtype)) ? -1 : mx::packed_weight_bytes(wtype, rows, K);
     if (!known_wtype(wtype) || rows < 0 || K <= 0 || K % blck(wtype)) return -1;
     return mx::packed_weight_bytes(wtype, rows, K);
 }
 
 MI355X_API int mi355x_weight_pack(int wtype, const void * src_dev, int64_t rows, int64_t K,
                                   void * dst_dev, void * stream) {
-    if (wtype == mx::T_Q4_KX) {   // from ggml Q4_K blocks; a regrouping, so never in place
-        if (rows < 0 || rows % 32 || K <= 0 || K % 256) return MI355X_E_ARG;
+    if (x32_wtype(wtype)) {   // from ggml blocks; a regrouping, so never in place
+        if (rows < 0 || rows % 32 || K <= 0 || K % blck(wtype)) return MI355X_E_ARG;
         if (rows == 0) return MI355X_OK;
-        if (!src_dev || !dst_dev || src_dev == dst_dev || !aligned(src_dev, 16) || !aligned(dst_dev, 16)) return MI355X_E_ARG;
-        return hip_status(mx::launch_pack_q4kx(src_dev, rows, K, dst_dev, S(stream)));
+        if (!src_dev || !dst_dev || src_dev == dst_dev || !aligned(dst_dev, 16)) return MI355X_E_ARG;
+        if (wtype == mx::T_Q4_KX) {
+            if (!aligned(src_dev, 16)) return MI355X_E_ARG;
+            return hip_status(mx::launch_pack_q4kx(src_dev, rows, K, dst_dev, S(stream)));
+        }
+        return hip_status(mx::launch_pack_x32(wtype, src_dev, rows, K, dst_dev, S(stream)));
     }
     if (!known_wtype(wtype) || rows < 0 || K <= 0 || K % blck(wtype) || K % 32) return MI355X_E_ARG;
     if (rows == 0) return MI355X_OK;
@@ -569,7 +576,7 @@ MI355X_API int mi355x_mul_mat_id(const mi355x_moe_args * a, void * workspace_dev
     MoeLayout L;
     if (!moe_layout(a, L)) return MI355X_E_ARG;
     if (!known_moe_wtype(a->wtype) || a->K % 32 || a->K % blck(a->wtype) || a->N % 16) return MI355X_E_ARG;
-    if (a->wtype == mx::T_Q4_KX && a->N % 32) return MI355X_E_ARG;   // experts are whole 32-row groups
+    if (x32_wtype(a->wtype) && a->N % 32) return MI355X_E_ARG;   // experts are whole 32-row groups
     if (!a->as_dev || !a->b_dev || !a->ids_dev || !a->dst_dev || !aligned(a->as_dev, 16) || !aligned(a->b_dev, 16))
         return MI355X_E_ARG;
     if (a->b_nb1 < a->K || a->b_nb1 % 4 || a->b_nb2 != a->ne11 * a->b_nb1) return MI355X_E_ARG;

@@ -167,7 +167,9 @@ __global__ void __launch_bounds__(MOE_SORT_THREADS) moe_prep_kernel(MoeArgs a) {
 // stages, most on the down projection's 2048 blocks; the other formats measured within 2% either
 // way and keep three waves with four stages, or three where the stage is wider (F16, Q5_K, Q6_K;
 // Q6_K would spill at four waves).
-template <int WT> constexpr int moe_waves() { return (WT == T_Q4_K || WT == T_Q4_KX || WT == T_Q8_0) ? 4 : 3; }
+template <int WT> constexpr int moe_waves() {
+    return (WT == T_Q4_K || WT == T_Q4_KX || WT == T_Q8_0 || WT == T_Q8_0X) ? 4 : 3;
+}
 template <int WT> constexpr int moe_stages() {
     return moe_waves<WT>() == 4 ? 2 : (WT == T_F16 || WT == T_Q6_K || WT == T_Q5_K) ? 3 : 4;
 }
@@ -361,6 +363,41 @@ hipError_t launch_pack_q4kx(const void * src, int64_t rows, int64_t K, void * ds
     return hipGetLastError();
 }
 
+// ggml Q8_0 (34-byte) or MXFP4 (17-byte) blocks -> T_Q8_0X / T_MXFP4X: one thread per source
+// block; the blocks are only 2- or 1-byte aligned, so the quants move as bytes gathered into
+// words (a one-time layout build of an expert stack, bound by HBM either way).
+template <bool Q8>
+__global__ void __launch_bounds__(256) pack_x32_kernel(const uint8_t * __restrict__ src, int64_t rows, int64_t nblk,
+                                                       uint8_t * __restrict__ dst) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= rows * nblk) return;
+    constexpr int BB = Q8 ? 34 : 17, QB = Q8 ? 32 : 16, Q0 = Q8 ? 2 : 1;
+    const uint8_t * b = src + i * BB;
+    const int64_t x = x32_index(i / nblk, i % nblk, nblk);
+    uint32_t * q = (uint32_t *)(dst + x * QB);
+#pragma unroll
+    for (int w = 0; w < QB / 4; w++)
+        q[w] = (uint32_t)b[Q0 + 4 * w] | ((uint32_t)b[Q0 + 4 * w + 1] << 8) | ((uint32_t)b[Q0 + 4 * w + 2] << 16) |
+               ((uint32_t)b[Q0 + 4 * w + 3] << 24);
+    uint8_t * scales = dst + rows * nblk * QB;
+    if (Q8) {
+        scales[2 * x] = b[0];
+        scales[2 * x + 1] = b[1];
+    } else {
+        scales[x] = b[0];
+    }
+}
+
+hipError_t launch_pack_x32(int wt, const void * src, int64_t rows, int64_t K, void * dst, hipStream_t st) {
+    const int64_t n = rows * (K / 32);
+    if (n <= 0) return hipSuccess;
+    const dim3 grid((unsigned)((n + 255) / 256));
+    if (wt == T_Q8_0X) hipLaunchKernelGGL(pack_x32_kernel<true>, grid, dim3(256), 0, st, (const uint8_t *)src, rows, K / 32, (uint8_t *)dst);
+    else if (wt == T_MXFP4X) hipLaunchKernelGGL(pack_x32_kernel<false>, grid, dim3(256), 0, st, (const uint8_t *)src, rows, K / 32, (uint8_t *)dst);
+    else return hipErrorInvalidValue;
+    return hipGetLastError();
+}
+
 int moe_max_tiles(int T, int U, int E) { return (T * U + MOE_BM - 1) / MOE_BM + E; }
 
 hipError_t launch_moe(int wt, const MoeArgs & a, hipStream_t st) {
@@ -393,6 +430,8 @@ hipError_t launch_moe(int wt, const MoeArgs & a, hipStream_t st) {
         case T_Q4_KX: hipLaunchKernelGGL(moe_gemm_kernel<T_Q4_KX>, dim3((unsigned)nb), dim3(MOE_THREADS), lds, st, a); break;
         case T_Q6_K: hipLaunchKernelGGL(moe_gemm_kernel<T_Q6_K>, dim3((unsigned)nb), dim3(MOE_THREADS), lds, st, a); break;
         case T_MXFP4: hipLaunchKernelGGL(moe_gemm_kernel<T_MXFP4>, dim3((unsigned)nb), dim3(MOE_THREADS), lds, st, a); break;
+        case T_Q8_0X: hipLaunchKernelGGL(moe_gemm_kernel<T_Q8_0X>, dim3((unsigned)nb), dim3(MOE_THREADS), lds, st, a); break;
+        case T_MXFP4X: hipLaunchKernelGGL(moe_gemm_kernel<T_MXFP4X>, dim3((unsigned)nb), dim3(MOE_THREADS), lds, st, a); break;
         default: return hipErrorInvalidValue;
     }
     return hipGetLastError();

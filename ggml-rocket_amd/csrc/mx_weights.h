@@ -47,6 +47,8 @@ __host__ __device__ inline int64_t packed_weight_bytes(int wt, int64_t rows, int
         case T_Q4_0: return rows * (K / 32) * 18;
         case T_Q5_K: return rows * (K / 256) * 176;
         case T_Q4_KX: return rows % 32 ? -1 : rows * (K / 256) * 144;
+        case T_Q8_0X: return rows % 32 ? -1 : rows * K + rows * (K / 32) * 2;
+        case T_MXFP4X: return rows % 32 ? -1 : rows * (K / 32) * 17;
         default: return -1;
     }
 }
@@ -424,6 +426,39 @@ template <> struct WLoad<T_Q4_KX> : WLoad<T_Q4_K> {
         const int r = (int)(row % Q4KX_GROUP);
         hdr = *(const u32x4 *)(b + 16 * r);
         qs = *(const u32x4 *)(b + 16 * Q4KX_GROUP + 32 * Q4KX_GROUP * j + 32 * r + 16 * u);
+    }
+};
+
+// Q8_0 and MXFP4 regrouped by 32 rows (T_Q8_0X, T_MXFP4X): the two planes of the split layouts,
+// each ordered by (32-row group, 32-value block) and, inside, by row: per group and block the 32
+// rows' quants (Q8_0: 32 bytes each, 1 KiB; MXFP4: 16 bytes each, 512 B), and in the second plane
+// the 32 rows' scales (Q8_0: fp16, 64 B; MXFP4: the E8M0 byte, 32 B). The same decode as the
+// split layouts; lanes that take consecutive rows read consecutive bytes.
+__host__ __device__ inline int64_t x32_index(int64_t row, int64_t blk, int64_t nblk) {
+    return ((row / 32) * nblk + blk) * 32 + row % 32;
+}
+template <> struct WLoad<T_Q8_0X> : WLoad<T_Q8_0> {
+    __device__ __forceinline__ void load(const uint8_t * W, int64_t rows, int64_t K, int64_t row,
+                                         int64_t k0, int u, bool ok_row) {
+        int64_t k = k0 + 32 * u;
+        ok = ok_row && k < K;
+        k = k < K ? k : 0;
+        const int64_t x = x32_index(row, k / 32, K / 32);
+        const u32x4 * p = (const u32x4 *)(W + x * 32);
+        q[0] = p[0];
+        q[1] = p[1];
+        d = ((const uint16_t *)(W + rows * K))[x];
+    }
+};
+template <> struct WLoad<T_MXFP4X> : WLoad<T_MXFP4> {
+    __device__ __forceinline__ void load(const uint8_t * W, int64_t rows, int64_t K, int64_t row,
+                                         int64_t k0, int u, bool ok_row) {
+        int64_t k = k0 + 32 * u;
+        ok = ok_row && k < K;
+        k = k < K ? k : 0;
+        const int64_t x = x32_index(row, k / 32, K / 32);
+        qs = *(const u32x4 *)(W + x * 16);
+        e = W[rows * (K / 2) + x];
     }
 };
 

@@ -54,7 +54,15 @@ enum mi355x_wtype { MI355X_F16 = 1, MI355X_Q4_0 = 2, MI355X_Q8_0 = 8, MI355X_Q4_
                      * for each 64-value quarter the 32 rows' 32 bytes of nibbles. Same bytes as
                      * Q4_K; a wave's loads of a quarter are one contiguous KiB. Built from ggml
                      * Q4_K blocks by mi355x_weight_pack. */
-                    MI355X_Q4_K_X = 0x10C };
+                    MI355X_Q4_K_X = 0x10C,
+                    /* not ggml types: Q8_0 / MXFP4 blocks of [rows][K] (rows % 32 == 0) regrouped
+                     * by 32 rows, for expert stacks (mi355x_mul_mat_id only). Two planes, each in
+                     * (32-row group, 32-value block, row) order: the quants (Q8_0: 32 int8 a
+                     * block, MXFP4: 16 bytes of FP4 codes), then the block scales (Q8_0: fp16 d,
+                     * MXFP4: the E8M0 byte). Same bytes as the ggml blocks; a wave's quant load
+                     * of a block is 1 KiB (Q8_0) or 512 B (MXFP4) of consecutive bytes. Built from
+                     * ggml blocks by mi355x_weight_pack. */
+                    MI355X_Q8_0_X = 0x108, MI355X_MXFP4_X = 0x127 };
 
 typedef struct mi355x_device_info {
     char name[64];              /* e.g. "gfx950" */

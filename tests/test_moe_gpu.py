@@ -144,19 +144,24 @@ def test_moe_bad_id_flags_error(mx):
     assert compare(ref[mask], o[mask])["range_err"] <= 1e-2
 
 
+X32_LAYOUTS = [("Q4_K", "Q4_K_X"), ("Q8_0", "Q8_0_X"), ("MXFP4", "MXFP4_X")]
+
+
+@pytest.mark.parametrize("base_name,x_name", X32_LAYOUTS)
 @pytest.mark.parametrize("K,N,E,ne11,U,T", [(1024, 128, 8, 1, 2, 64), (2048, 96, 8, 2, 2, 66), (768, 2048, 4, 8, 2, 40)])
-def test_moe_q4k_x_layout(mx, K, N, E, ne11, U, T):
-    """Q4_K expert stacks regrouped by 32 rows (Q4_K_X) give the same bits as the ggml block layout
-    (same decode, same MFMA order; only where the bytes sit differs), and meet the oracle's bars;
-    N = 96 leaves a partial 128-column block."""
-    P = expert_payload(O.Q4_K, E, N, K)
+def test_moe_x32_layout(mx, K, N, E, ne11, U, T, base_name, x_name):
+    """Expert stacks regrouped by 32 rows (Q4_K_X, Q8_0_X, MXFP4_X) give the same bits as the
+    layout of their base type (same decode, same MFMA order; only where the bytes sit differs),
+    and meet the oracle's bars; N = 96 leaves a partial 128-column block."""
+    wt = getattr(O, base_name)
+    P = expert_payload(wt, E, N, K)
     X = make_input(T, ne11, K)
     ids = make_ids(T, U, E)
-    base, _ = run(mx, O.Q4_K, P, E, N, K, X, ids)
-    got, _ = run(mx, mx.Q4_K_X, P, E, N, K, X, ids)
+    base, _ = run(mx, wt, P, E, N, K, X, ids)
+    got, _ = run(mx, getattr(mx, x_name), P, E, N, K, X, ids)
     assert np.array_equal(base.view(np.uint32), got.view(np.uint32))
-    ref = O.mul_mat_id(O.Q4_K, P, K, N, E, X, ne11, ids)
-    check_bars(ref, got, N, 0.9990, f"moe Q4_K_X K={K} N={N} T={T}")
+    ref = O.mul_mat_id(wt, P, K, N, E, X, ne11, ids)
+    check_bars(ref, got, N, 0.9990, f"moe {x_name} K={K} N={N} T={T}")
 
 
 @pytest.mark.parametrize("layout", ["q4_k", "q4_k_x"])
