@@ -921,12 +921,11 @@ def moe_bench(args):
     logits = np.random.default_rng(0x5EED0000 + 64).standard_normal((T, E), dtype=np.float32)
     ids = np.argsort(-logits, axis=1, kind="stable")[:, :U].astype(np.int32)   # softmax is monotone
     idt = torch.from_numpy(ids).cuda()
-    # each stack in the layout the backend caches it in: Q4_K, Q8_0 and MXFP4 regrouped by 32
-    # rows, Q6_K in its split planes
+    # each stack in the layout the backend caches it in: regrouped by 32 rows
     main = moe_stack(args, mx.Q4_K_X, lambda n, k, seed: synth_q4k(n, k, seed), E, U, T, DM, FF, idt)
     others = {}
     if not getattr(args, "quick", False):
-        for tn, lay, wt in (("Q8_0", mx.Q8_0_X, mx.Q8_0), ("Q6_K", mx.Q6_K, mx.Q6_K), ("MXFP4", mx.MXFP4_X, mx.MXFP4)):
+        for tn, lay, wt in (("Q8_0", mx.Q8_0_X, mx.Q8_0), ("Q6_K", mx.Q6_K_X, mx.Q6_K), ("MXFP4", mx.MXFP4_X, mx.MXFP4)):
             others[tn] = moe_stack(args, lay, lambda n, k, seed, wt=wt: synth_blocks(wt, n, k, seed),
                                    E, U, T, DM, FF, idt)
     gbs = main["GBps"]

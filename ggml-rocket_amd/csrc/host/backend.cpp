@@ -835,7 +835,7 @@ int build_weight(Ctx * c, int t, const void * src, int64_t rows, int64_t K, int 
         TRY(mi355x_convert_f16(t, c->wstage.p, rows * K, (uint16_t *)c->wconv.p, c->stream));
         return mi355x_weight_f16_tiled(MI355X_F16, c->wconv.p, rows, K, (uint16_t *)dst, c->stream);
     }
-    if (lay == MI355X_Q4_K_X || lay == MI355X_Q8_0_X || lay == MI355X_MXFP4_X)
+    if (lay == MI355X_Q4_K_X || lay == MI355X_Q8_0_X || lay == MI355X_Q6_K_X || lay == MI355X_MXFP4_X)
         return mi355x_weight_pack(lay, c->wstage.p, rows, K, dst, c->stream);
     if (lay != MI355X_F16 && lay != MI355X_F16_T) return mi355x_weight_pack(t, c->wstage.p, rows, K, dst, c->stream);
     // -> fp16: from the HBM layout, built first when that differs from the ggml one
@@ -855,11 +855,12 @@ int get_weight(Ctx * c, const mi355x_tensor * a, int64_t rows, int64_t K, bool w
                int64_t moe_n, DevBuf & scratch, WEntry & out, bool & resident) {
     const bool moe = moe_n > 0;   // an expert stack of experts with moe_n rows each
     int lay = dev_layout(a->type, want_f16, tiled_ok, K);
-    // Q4_K, Q8_0 and MXFP4 experts of whole 32-row groups take the regrouped layouts, whose
-    // 32-row slabs the expert GEMM loads as contiguous bytes
+    // Q4_K, Q8_0, Q6_K and MXFP4 experts of whole 32-row groups take the regrouped layouts,
+    // whose 32-row slabs the expert GEMM loads as contiguous bytes
     if (moe && moe_n % 32 == 0) {
         if (lay == MI355X_Q4_K) lay = MI355X_Q4_K_X;
         else if (lay == MI355X_Q8_0) lay = MI355X_Q8_0_X;
+        else if (lay == MI355X_Q6_K) lay = MI355X_Q6_K_X;
         else if (lay == MI355X_MXFP4) lay = MI355X_MXFP4_X;
     }
     const int64_t dbytes = mi355x_weight_bytes(lay, rows, K);

@@ -31,13 +31,13 @@ inline bool known_wtype(int wt) {
 }
 
 // the layouts regrouped by 32 rows, built from ggml blocks for expert stacks
-inline bool x32_wtype(int wt) { return wt == mx::T_Q4_KX || wt == mx::T_Q8_0X || wt == mx::T_MXFP4X; }
+inline bool x32_wtype(int wt) { return wt == mx::T_Q4_KX || wt == mx::T_Q8_0X || wt == mx::T_Q6_KX || wt == mx::T_MXFP4X; }
 
 // the expert-stack layouts: every weight type, and the regrouped ones
 inline bool known_moe_wtype(int wt) { return known_wtype(wt) || x32_wtype(wt); }
 
 inline int64_t blck(int wt) {
-    if (wt == mx::T_Q4_K || wt == mx::T_Q4_KX || wt == mx::T_Q5_K || wt == mx::T_Q6_K) return 256;
+    if (wt == mx::T_Q4_K || wt == mx::T_Q4_KX || wt == mx::T_Q5_K || wt == mx::T_Q6_K || wt == mx::T_Q6_KX) return 256;
     return (wt == mx::T_Q8_0 || wt == mx::T_Q8_0X || wt == mx::T_Q4_0 || wt == mx::T_MXFP4 || wt == mx::T_MXFP4X) ? 32 : 1;
 }
 

@@ -20,11 +20,11 @@ constexpr int WAVE = 64;
 
 // ggml type ids (ggml.h enum ggml_type) for the weight formats this path decodes, and layouts of
 // this library's own, which are no ggml types: T_F16T, tiled fp16 (tiled_index below), and the
-// expert-stack layouts regrouped by 32 rows, T_Q4_KX, T_Q8_0X and T_MXFP4X (WLoad<T_Q4_KX> etc.
-// in mx_weights.h).
+// expert-stack layouts regrouped by 32 rows, T_Q4_KX, T_Q8_0X, T_Q6_KX and T_MXFP4X
+// (WLoad<T_Q4_KX> etc. in mx_weights.h).
 enum : int { T_F32 = 0, T_F16 = 1, T_Q4_0 = 2, T_Q8_0 = 8, T_Q4_K = 12, T_Q5_K = 13, T_Q6_K = 14, T_I32 = 26,
              T_BF16 = 30, T_MXFP4 = 39,
-             T_F16T = 0x101, T_Q4_KX = 0x10C, T_Q8_0X = 0x108, T_MXFP4X = 0x127 };
+             T_F16T = 0x101, T_Q4_KX = 0x10C, T_Q8_0X = 0x108, T_Q6_KX = 0x10E, T_MXFP4X = 0x127 };
 
 // The tiled fp16 layout of a [rows][K] matrix (K % 32 == 0): 16 x 32 tiles of 1 KB, row-major
 // inside, tile (row / 16, k / 32) at ((row / 16) * (K / 32) + k / 32) * 512 values; rows padded to

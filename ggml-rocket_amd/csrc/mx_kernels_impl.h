@@ -102,7 +102,7 @@ struct MoeArgs {
 
 int moe_max_tiles(int T, int U, int E);
 hipError_t launch_pack_q4kx(const void * src, int64_t rows, int64_t K, void * dst, hipStream_t st);   // rows % 32 == 0
-hipError_t launch_pack_x32(int wt, const void * src, int64_t rows, int64_t K, void * dst, hipStream_t st);   // T_Q8_0X, T_MXFP4X
+hipError_t launch_pack_x32(int wt, const void * src, int64_t rows, int64_t K, void * dst, hipStream_t st);   // T_Q8_0X, T_Q6_KX, T_MXFP4X
 hipError_t launch_moe(int wt, const MoeArgs & a, hipStream_t st);
 
 // FaArgs::tasks: 4 for every build, 2 for DV <= 128

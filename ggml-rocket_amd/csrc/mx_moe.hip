@@ -168,10 +168,10 @@ __global__ void __launch_bounds__(MOE_SORT_THREADS) moe_prep_kernel(MoeArgs a) {
 // way and keep three waves with four stages, or three where the stage is wider (F16, Q5_K, Q6_K;
 // Q6_K would spill at four waves).
 template <int WT> constexpr int moe_waves() {
-    return (WT == T_Q4_K || WT == T_Q4_KX || WT == T_Q8_0 || WT == T_Q8_0X) ? 4 : 3;
+    return (WT == T_Q4_K || WT == T_Q4_KX || WT == T_Q8_0 || WT == T_Q8_0X || WT == T_MXFP4 || WT == T_MXFP4X) ? 4 : 3;
 }
 template <int WT> constexpr int moe_stages() {
-    return moe_waves<WT>() == 4 ? 2 : (WT == T_F16 || WT == T_Q6_K || WT == T_Q5_K) ? 3 : 4;
+    return moe_waves<WT>() == 4 ? 2 : (WT == T_F16 || WT == T_Q6_K || WT == T_Q6_KX || WT == T_Q5_K) ? 3 : 4;
 }
 
 template <int WT>
@@ -388,7 +388,39 @@ __global__ void __launch_bounds__(256) pack_x32_kernel(const uint8_t * __restric
     }
 }
 
+// ggml Q6_K blocks (210 bytes: ql[128] qh[64] scales[16] d) -> T_Q6_KX: one thread per source
+// block, bytes gathered into words as above.
+__global__ void __launch_bounds__(256) pack_q6kx_kernel(const uint8_t * __restrict__ src, int64_t rows, int64_t K,
+                                                        uint8_t * __restrict__ dst) {
+    const int64_t nblk = K / 256;
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= rows * nblk) return;
+    const uint8_t * b = src + i * 210;
+    const Q6kxPlanes p = q6kx_planes(rows, K, i / nblk, i % nblk);
+    auto word = [&](int o) {
+        return (uint32_t)b[o] | ((uint32_t)b[o + 1] << 8) | ((uint32_t)b[o + 2] << 16) | ((uint32_t)b[o + 3] << 24);
+    };
+    auto chunk = [&](int o, uint8_t * d) {
+#pragma unroll
+        for (int w = 0; w < 4; w++) ((uint32_t *)d)[w] = word(o + 4 * w);
+    };
+#pragma unroll
+    for (int c = 0; c < 8; c++) chunk(16 * c, dst + p.ql + (c * 32 + p.r) * 16);
+#pragma unroll
+    for (int c = 0; c < 4; c++) chunk(128 + 16 * c, dst + p.qh + (c * 32 + p.r) * 16);
+    chunk(192, dst + p.sc + p.r * 16);
+    dst[p.d + 2 * p.r] = b[208];
+    dst[p.d + 2 * p.r + 1] = b[209];
+}
+
 hipError_t launch_pack_x32(int wt, const void * src, int64_t rows, int64_t K, void * dst, hipStream_t st) {
+    if (wt == T_Q6_KX) {
+        const int64_t n = rows * (K / 256);
+        if (n <= 0) return hipSuccess;
+        hipLaunchKernelGGL(pack_q6kx_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, (const uint8_t *)src, rows, K,
+                           (uint8_t *)dst);
+        return hipGetLastError();
+    }
     const int64_t n = rows * (K / 32);
     if (n <= 0) return hipSuccess;
     const dim3 grid((unsigned)((n + 255) / 256));
@@ -432,6 +464,7 @@ hipError_t launch_moe(int wt, const MoeArgs & a, hipStream_t st) {
         case T_MXFP4: hipLaunchKernelGGL(moe_gemm_kernel<T_MXFP4>, dim3((unsigned)nb), dim3(MOE_THREADS), lds, st, a); break;
         case T_Q8_0X: hipLaunchKernelGGL(moe_gemm_kernel<T_Q8_0X>, dim3((unsigned)nb), dim3(MOE_THREADS), lds, st, a); break;
         case T_MXFP4X: hipLaunchKernelGGL(moe_gemm_kernel<T_MXFP4X>, dim3((unsigned)nb), dim3(MOE_THREADS), lds, st, a); break;
+        case T_Q6_KX: hipLaunchKernelGGL(moe_gemm_kernel<T_Q6_KX>, dim3((unsigned)nb), dim3(MOE_THREADS), lds, st, a); break;
         default: return hipErrorInvalidValue;
     }
     return hipGetLastError();

@@ -49,6 +49,7 @@ __host__ __device__ inline int64_t packed_weight_bytes(int wt, int64_t rows, int
         case T_Q4_KX: return rows % 32 ? -1 : rows * (K / 256) * 144;
         case T_Q8_0X: return rows % 32 ? -1 : rows * K + rows * (K / 32) * 2;
         case T_MXFP4X: return rows % 32 ? -1 : rows * (K / 32) * 17;
+        case T_Q6_KX: return rows % 32 ? -1 : rows * (K / 256) * 210;
         default: return -1;
     }
 }
@@ -192,8 +193,41 @@ template <> struct WLoad<T_MXFP4> {
         qs = *(const u32x4 *)(W + row * (K / 2) + k / 2);
         e = W[rows * (K / 2) + row * (K / 32) + k / 32];
     }
+    // packed: a code's three magnitude bits moved to fp16 bits 11-9 and its sign to bit 15 read
+    // as fp16 are the doubled E2M1 value times 2^-15 exactly (0 and 1 land in the subnormals: 0
+    // and 2^-15). Two packed multiplies by powers of two scale that by 2^(e-113) = 2^15 * 2^(e-128):
+    // first by 2^a, a = clamp(e - 113, 0, 15), exact (a result of at most two significant bits
+    // between 2^-15 and 12), then by 2^(e-113-a), which rounds the exact product once, as the exact
+    // decode's f32 product and fp16 rounding do. So the values are the exact decode's for every
+    // e < 144; a block scale of 2^16 or more (every nonzero weight past the fp16 range) gives
+    // finite values instead of infinities. A masked item multiplies by zero.
     __device__ __forceinline__ void decode_fast(int u, u32x4 out[4], int & run0, int & run1) const {
-        decode(u, out, run0, run1);
+        const int s = (int)e - 113;
+        const int a = s < 0 ? 0 : (s > 15 ? 15 : s);
+        const int b = s - a;                           // -113 .. 127
+        const uint32_t ha = (uint32_t)(a + 15) << 10;  // 2^a, a normal fp16
+        // 2^b: normal for b >= -14, subnormal down to -24, below that a zero (as the product
+        // would round to); b > 15 only for e >= 144, held at 2^15
+        const uint32_t hb = !ok ? 0u
+                          : b >= -14 ? (uint32_t)((b > 15 ? 15 : b) + 15) << 10
+                          : b >= -24 ? 1u << (b + 24) : 0u;
+        const half2v DA = h2_of(ha * 0x10001u), DB = h2_of(hb * 0x10001u);
+        uint32_t o[16];
+#pragma unroll
+        for (int w = 0; w < 4; w++) {
+            const uint32_t x = qs[w];
+            // per byte: magnitude << 1 in bits 3-1 and the sign in bit 7 (the fp16 high byte)
+            const uint32_t lo = ((x << 1) & 0x0E0E0E0Eu) | ((x << 4) & 0x80808080u);
+            const uint32_t hi = ((x >> 3) & 0x0E0E0E0Eu) | (x & 0x80808080u);
+            o[2 * w] = u_of(h2_of(__builtin_amdgcn_perm(0u, lo, 0x010C000Cu)) * DA * DB);       // 4w, 4w+1
+            o[2 * w + 1] = u_of(h2_of(__builtin_amdgcn_perm(0u, lo, 0x030C020Cu)) * DA * DB);   // 4w+2, 4w+3
+            o[8 + 2 * w] = u_of(h2_of(__builtin_amdgcn_perm(0u, hi, 0x010C000Cu)) * DA * DB);   // 16+4w ...
+            o[8 + 2 * w + 1] = u_of(h2_of(__builtin_amdgcn_perm(0u, hi, 0x030C020Cu)) * DA * DB);
+        }
+#pragma unroll
+        for (int i = 0; i < 4; i++) out[i] = u32x4{o[4 * i], o[4 * i + 1], o[4 * i + 2], o[4 * i + 3]};
+        run0 = 32 * u;
+        run1 = 32 * u + 16;
     }
     __device__ __forceinline__ void decode(int u, u32x4 out[4], int & run0, int & run1) const {
         // 2^(e-128) from its bits: a subnormal for e < 2
@@ -488,8 +522,31 @@ template <> struct WLoad<T_Q6_K> {
         sc = (uint32_t)(uint8_t)scp[i0] | ((uint32_t)(uint8_t)scp[i0 + 2] << 8);
         d = *dp;
     }
+    // packed: the 6-bit codes assembled four bytes at a time (nibble of ql, two bits of qh),
+    // each placed under 1024 (magic_pair), less 1024 + 32, times the sub-block scale d * sc
+    // rounded to fp16 (zero where the item is masked)
     __device__ __forceinline__ void decode_fast(int u, u32x4 out[4], int & run0, int & run1) const {
-        decode(u, out, run0, run1);
+        const float df = h2f_bits(d);
+        const half2v DA = splat_h(ok ? df * (float)(int8_t)(sc & 0xFFu) : 0.0f);
+        const half2v DB = splat_h(ok ? df * (float)(int8_t)((sc >> 8) & 0xFFu) : 0.0f);
+        const half2v OFF = {(_Float16)-1056.0f, (_Float16)-1056.0f};
+        const int sn = 4 * hi;
+        uint32_t a[8], b[8];
+#pragma unroll
+        for (int w = 0; w < 4; w++) {
+            const uint32_t va = ((qla[w] >> sn) & 0x0F0F0F0Fu) | (((qh[w] >> sn) & 0x03030303u) << 4);
+            const uint32_t vb = ((qlb[w] >> sn) & 0x0F0F0F0Fu) | (((qh[w] >> (sn + 2)) & 0x03030303u) << 4);
+            a[2 * w] = u_of((magic_pair(va, PERM_B01) + OFF) * DA);
+            a[2 * w + 1] = u_of((magic_pair(va, PERM_B23) + OFF) * DA);
+            b[2 * w] = u_of((magic_pair(vb, PERM_B01) + OFF) * DB);
+            b[2 * w + 1] = u_of((magic_pair(vb, PERM_B23) + OFF) * DB);
+        }
+        out[0] = u32x4{a[0], a[1], a[2], a[3]};
+        out[1] = u32x4{a[4], a[5], a[6], a[7]};
+        out[2] = u32x4{b[0], b[1], b[2], b[3]};
+        out[3] = u32x4{b[4], b[5], b[6], b[7]};
+        run0 = 16 * u;
+        run1 = 32 + 16 * u;
     }
     __device__ __forceinline__ void decode(int u, u32x4 out[4], int & run0, int & run1) const {
         const float df = h2f_bits(d);
@@ -525,6 +582,38 @@ template <> struct WLoad<T_Q6_K> {
         zero_out(ok, out);
         run0 = 16 * u;
         run1 = 32 + 16 * u;
+    }
+};
+
+// Q6_K regrouped by 32 rows (T_Q6_KX): the four planes of the split layout, each ordered by
+// (32-row group, 256-value block) and, inside, so that the 32 rows' pieces a wave loads together
+// are consecutive: ql as [16-byte chunk (8)][row (32)] (4 KiB a group-block), qh as [chunk (4)]
+// [row] (2 KiB), scales as [row][16 bytes] (512 B), d as [row] (64 B). The same decode as Q6_K.
+struct Q6kxPlanes {
+    int64_t ql, qh, sc, d;   // byte offsets of the row's group-block in each plane
+    int r;
+};
+__host__ __device__ inline Q6kxPlanes q6kx_planes(int64_t rows, int64_t K, int64_t row, int64_t blk) {
+    const int64_t gb = (row / 32) * (K / 256) + blk;
+    return {gb * 4096, rows * (K / 2) + gb * 2048, rows * (K / 2) + rows * (K / 4) + gb * 512,
+            rows * (K / 2) + rows * (K / 4) + rows * (K / 16) + gb * 64, (int)(row % 32)};
+}
+template <> struct WLoad<T_Q6_KX> : WLoad<T_Q6_K> {
+    __device__ __forceinline__ void load(const uint8_t * W, int64_t rows, int64_t K, int64_t row,
+                                         int64_t k0, int u, bool ok_row) {
+        const int64_t blk = k0 / 256;
+        const int q4 = (int)((k0 % 256) / 64);
+        const int h = q4 >> 1;
+        hi = q4 & 1;
+        ok = ok_row;
+        const Q6kxPlanes p = q6kx_planes(rows, K, row, blk);
+        qla = *(const u32x4 *)(W + p.ql + ((4 * h + u) * 32 + p.r) * 16);
+        qlb = *(const u32x4 *)(W + p.ql + ((4 * h + 2 + u) * 32 + p.r) * 16);
+        qh = *(const u32x4 *)(W + p.qh + ((2 * h + u) * 32 + p.r) * 16);
+        // scales u + 4 hi and u + 4 hi + 2 of the half h: bytes u and u + 2 of one word
+        const uint32_t sw = *(const uint32_t *)(W + p.sc + p.r * 16 + 8 * h + 4 * hi);
+        sc = ((sw >> (8 * u)) & 0xFFu) | (((sw >> (8 * u + 16)) & 0xFFu) << 8);
+        d = *(const uint16_t *)(W + p.d + 2 * p.r);
     }
 };
 

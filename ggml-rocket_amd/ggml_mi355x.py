@@ -22,6 +22,7 @@ F16_T = 0x101   # the library's tiled fp16 layout (16 x 32 tiles of 1 KB); not a
 Q4_K_X = 0x10C  # Q4_K blocks regrouped by 32 rows, for expert stacks (MUL_MAT_ID); not a ggml type
 Q8_0_X = 0x108  # Q8_0 blocks regrouped by 32 rows (quant plane, then scale plane); expert stacks only
 MXFP4_X = 0x127  # MXFP4 blocks regrouped by 32 rows, as Q8_0_X; expert stacks only
+Q6_K_X = 0x10E  # Q6_K blocks regrouped by 32 rows (four planes); expert stacks only
 OK, E_ARG, E_DEVICE, E_UNSUPPORTED, E_NOMEM, E_IDS = 0, -1, -2, -3, -4, -5   # mi355x_status
 BLOCK = {F16: 1, F32: 1, BF16: 1, Q8_0: 32, Q4_0: 32, Q4_K: 256, Q5_K: 256, Q6_K: 256, MXFP4: 32}
 TYPE_SIZE = {F16: 2, F32: 4, BF16: 2, Q8_0: 34, Q4_0: 18, Q4_K: 144, Q5_K: 176, Q6_K: 210, MXFP4: 17}
@@ -168,8 +169,8 @@ def weight_bytes(wtype: int, rows: int, K: int) -> int:
 
 def upload_weight(wtype: int, payload, rows: int, K: int, device="cuda"):
     """A ggml payload (numpy uint8 / uint16 / torch) -> its HBM layout, as a uint8 device tensor.
-    Q4_K_X, Q8_0_X and MXFP4_X take the ggml blocks of their base type (rows % 32 == 0) and
-    regroup them."""
+    Q4_K_X, Q8_0_X, Q6_K_X and MXFP4_X take the ggml blocks of their base type (rows % 32 == 0)
+    and regroup them."""
     torch = _torch()
     import numpy as np
     if isinstance(payload, np.ndarray):

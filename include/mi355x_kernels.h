@@ -62,7 +62,13 @@ enum mi355x_wtype { MI355X_F16 = 1, MI355X_Q4_0 = 2, MI355X_Q8_0 = 8, MI355X_Q4_
                      * MXFP4: the E8M0 byte). Same bytes as the ggml blocks; a wave's quant load
                      * of a block is 1 KiB (Q8_0) or 512 B (MXFP4) of consecutive bytes. Built from
                      * ggml blocks by mi355x_weight_pack. */
-                    MI355X_Q8_0_X = 0x108, MI355X_MXFP4_X = 0x127 };
+                    MI355X_Q8_0_X = 0x108, MI355X_MXFP4_X = 0x127,
+                    /* not a ggml type: Q6_K blocks of [rows][K] (rows % 32 == 0) regrouped by 32
+                     * rows, for expert stacks (mi355x_mul_mat_id only): the four planes ql, qh,
+                     * scales, d, each in (32-row group, 256-value block) order, ql and qh as
+                     * [16-byte chunk][row], scales as [row][16 bytes], d as [row]. Same bytes as
+                     * the ggml blocks. Built from ggml Q6_K blocks by mi355x_weight_pack. */
+                    MI355X_Q6_K_X = 0x10E };
 
 typedef struct mi355x_device_info {
     char name[64];              /* e.g. "gfx950" */

@@ -83,20 +83,20 @@ def test_q4k_x_layout_argument_checks():
     assert L.mi355x_weight_pack(mx.Q4_K_X, ctypes.c_void_p(a), 64, 512, ctypes.c_void_p(a), None) == mx.E_ARG
 
 
-@pytest.mark.parametrize("x,base,bs", [("Q8_0_X", "Q8_0", 34), ("MXFP4_X", "MXFP4", 17)])
+@pytest.mark.parametrize("x,base,bs", [("Q8_0_X", "Q8_0", 34), ("MXFP4_X", "MXFP4", 17), ("Q6_K_X", "Q6_K", 210 / 8)])
 def test_x32_layout_argument_checks(x, base, bs):
-    """Q8_0_X and MXFP4_X: the ggml byte count for whole 32-row groups of whole 32-value blocks, no
-    size otherwise; the pack rejects partial groups, partial blocks and in-place use before
-    touching the device (argument checks only: no GPU needed)."""
+    """Q8_0_X, MXFP4_X and Q6_K_X: the ggml byte count for whole 32-row groups of whole blocks
+    (bs: bytes per 32 values), no size otherwise; the pack rejects partial groups, partial blocks
+    and in-place use before touching the device (argument checks only: no GPU needed)."""
     import ctypes
     import ggml_mi355x as mx
     L = mx.lib()
     xt, bt = getattr(mx, x), getattr(mx, base)
-    assert mx.weight_bytes(xt, 64, 512) == mx.weight_bytes(bt, 64, 512) == 64 * 16 * bs
+    assert mx.weight_bytes(xt, 64, 512) == mx.weight_bytes(bt, 64, 512) == int(64 * 16 * bs)
     assert mx.weight_bytes(xt, 33, 512) == -1
     assert mx.weight_bytes(xt, 64, 48) == -1
-    buf_a = ctypes.create_string_buffer(64 * 16 * bs + 16)
-    buf_b = ctypes.create_string_buffer(64 * 16 * bs + 16)
+    buf_a = ctypes.create_string_buffer(int(64 * 16 * bs) + 16)
+    buf_b = ctypes.create_string_buffer(int(64 * 16 * bs) + 16)
     a, b = ctypes.addressof(buf_a) + (-ctypes.addressof(buf_a)) % 16, ctypes.addressof(buf_b) + (-ctypes.addressof(buf_b)) % 16
     assert L.mi355x_weight_pack(xt, ctypes.c_void_p(a), 33, 512, ctypes.c_void_p(b), None) == mx.E_ARG
     assert L.mi355x_weight_pack(xt, ctypes.c_void_p(a), 64, 48, ctypes.c_void_p(b), None) == mx.E_ARG

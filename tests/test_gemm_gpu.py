@@ -426,6 +426,37 @@ def test_skinny_mul_mat(mx, wtype, M):
     _assert_bars(ref, got[:, :N], M, N, f"skinny {O.TYPE_NAMES[wtype]} M={M}")
 
 
+def test_mxfp4_fast_decode_is_exact(mx, monkeypatch):
+    """The skinny kernel's packed MXFP4 decoder gives the exact decode's fp16 values for block
+    scales 2^(e-127), e in 80..140 (below 89 every value rounds to zero, to 104 the products are
+    fp16 subnormals, past 128 the scale takes two steps; 140 keeps 12 x 2^(e-128) finite, since an
+    infinite weight would turn the zero products of the row into NaN): with one-hot activation
+    rows (pack scale 1, every other product zero, so the K split's partial sums are exact),
+    out[m][n] is the decoded weight W[n][k_m], compared with the oracle's dequantization to fp16
+    (as values: a zero weight of either sign sums to +0). The one-hot positions take both
+    nibbles of a byte (weights j and j + 16 of a block) and every block."""
+    import torch
+    N, K = 256, 512
+    nblk = K // 32
+    rng = np.random.default_rng(1234)
+    blocks = rng.integers(0, 256, size=(N, nblk, 17), dtype=np.uint8)
+    blocks[:, :, 0] = (80 + (np.arange(N * nblk).reshape(N, nblk) * 7) % 61).astype(np.uint8)
+    payload = blocks.reshape(-1)
+    want = O.f16_bits_to_f32(O.dequantize_f16(O.MXFP4, payload, K))
+    ks = np.array([32 * (m % nblk) + (m * 5) % 32 for m in range(64)])
+    X = np.zeros((64, K), np.float32)
+    X[np.arange(64), ks] = 1.0
+    monkeypatch.setenv("MI355X_GEMM_CFG", "20")
+    w = mx.upload_weight(O.MXFP4, payload, N, K)
+    out = mx.mul_mat(O.MXFP4, w, N, K, _dev(X))
+    torch.cuda.synchronize()
+    got = out.cpu().numpy()
+    ref = want[:, ks].T
+    assert np.isfinite(ref).all()
+    bad = np.argwhere(got != ref)
+    assert len(bad) == 0, [(int(m), int(n), float(got[m, n]), float(ref[m, n])) for m, n in bad[:8]]
+
+
 @pytest.mark.parametrize("M", [1, 32, 64, 100, 128])
 @pytest.mark.parametrize("wtype", [O.Q8_0, O.Q4_K, O.Q6_K])
 def test_skinny_dma_matches_register_kernel(mx, monkeypatch, wtype, M):

@@ -144,13 +144,13 @@ def test_moe_bad_id_flags_error(mx):
     assert compare(ref[mask], o[mask])["range_err"] <= 1e-2
 
 
-X32_LAYOUTS = [("Q4_K", "Q4_K_X"), ("Q8_0", "Q8_0_X"), ("MXFP4", "MXFP4_X")]
+X32_LAYOUTS = [("Q4_K", "Q4_K_X"), ("Q8_0", "Q8_0_X"), ("Q6_K", "Q6_K_X"), ("MXFP4", "MXFP4_X")]
 
 
 @pytest.mark.parametrize("base_name,x_name", X32_LAYOUTS)
 @pytest.mark.parametrize("K,N,E,ne11,U,T", [(1024, 128, 8, 1, 2, 64), (2048, 96, 8, 2, 2, 66), (768, 2048, 4, 8, 2, 40)])
 def test_moe_x32_layout(mx, K, N, E, ne11, U, T, base_name, x_name):
-    """Expert stacks regrouped by 32 rows (Q4_K_X, Q8_0_X, MXFP4_X) give the same bits as the
+    """Expert stacks regrouped by 32 rows (Q4_K_X, Q8_0_X, Q6_K_X, MXFP4_X) give the same bits as the
     layout of their base type (same decode, same MFMA order; only where the bytes sit differs),
     and meet the oracle's bars; N = 96 leaves a partial 128-column block."""
     wt = getattr(O, base_name)
