@@ -1674,7 +1674,7 @@ hipError_t launch_pack_act_tiled(const float * X, int64_t ldx, int M, int K, uin
 //   4-15 LDS-DMA kernel: fp16 weights only (row-major or tiled); 15 has wave columns of two
 //        widths (gemm_f16_cols_kernel), 21 and 22 are that tile with 32-deep stages, three or
 //        four of them in flight where 15 has one of 64 (the 256 x 224 tile's DMA waits are
-//        what bounds it).
+//        what bounds it); 23 and 24 are 8 and 14 with eight 32-deep stages.
 //   16-19 Q4_K with every operand by DMA (gemm_q4k_kernel), K % 256 == 0; 18 and 19 split K
 //        (q4k_split). 20 is the skinny kernel's id (use_skinny), not a tile configuration.
 // choose_cfg prices a launch from two rates: a block's own pace, rounds * (ov_us + MFMA work
@@ -1686,8 +1686,8 @@ hipError_t launch_pack_act_tiled(const float * X, int64_t ldx, int M, int K, uin
 // MB of output (the zero fill and the second addend's atomics). The four were fitted per
 // configuration to measurements on tiled weights at M = 128-2048, N = 1024-28672,
 // K = 2880-14336, each launch on a weight panel no earlier launch left in the caches: mean
-// error 1-9% per configuration, and over 50 shapes the chosen configurations cost 0.3-0.4%
-// more than the best measured ones.
+// error 2-9% per configuration, and over 50 shapes the chosen configurations cost 0.6% more
+// than the best measured ones.
 enum CfgKind { REG = 0, DMA = 1, Q4KDMA = 2, NONE = 3 };
 struct CfgDesc {
     int kind;        // REG: gemm_kernel, DMA: gemm_f16_kernel / _cols, Q4KDMA: gemm_q4k_kernel
@@ -1703,25 +1703,27 @@ static constexpr CfgDesc kCfgs[] = {
     {REG, 128, 128, 2, 0, 0.0, 0.0, 0.0, 0.0},        // 1: same, K split (launcher-sized, >= 2)
     {REG, 256, 128, 1, 0, 0.0, 0.0, 0.0, 0.0},        // 2: 4 waves of 128x64
     {REG, 128, 256, 1, 0, 0.0, 0.0, 0.0, 0.0},        // 3: 4 waves of 64x128
-    {DMA, 256, 256, 1, 64, 6.31, 5.6, 8.23, 0.00},   // 4: 8 waves of 64x128, 2 stages of 64
-    {DMA, 128, 128, 1, 64, 3.99, 0.0, 13.35, 0.00},  // 5: 8 waves of 32x64, 4 stages of 64
-    {DMA, 64, 128, 1, 128, 2.73, 5.1, 17.03, 0.00},  // 6: 4 waves of 32x64, 3 stages of 128
-    {DMA, 128, 64, 1, 128, 2.88, 5.3, 17.64, 0.00},  // 7: 4 waves of 64x32, 3 stages of 128
-    {DMA, 128, 128, 2, 64, 3.44, 0.0, 38.45, 1.70},  // 8: as 5, K split in two
-    {DMA, 64, 128, 2, 128, 2.54, 6.8, 40.00, 0.60},  // 9: as 6, K split in two
-    {DMA, 128, 128, 1, 32, 4.34, 0.0, 13.23, 0.00},  // 10: 8 waves of 32x64, 4 stages of 32 (any K)
-    {DMA, 128, 128, 1, 32, 4.29, 0.0, 13.28, 0.00},  // 11: 8 waves of 32x64, 8 stages of 32
-    {DMA, 256, 128, 1, 64, 5.60, 8.8, 11.29, 0.00},  // 12: 8 waves of 64x64, 3 stages of 64
-    {DMA, 128, 256, 1, 64, 5.27, 4.9, 11.57, 0.00},  // 13: 8 waves of 64x64, 3 stages of 64
-    {DMA, 64, 128, 1, 64, 2.53, 1.7, 18.04, 0.00},   // 14: 4 waves of 32x64, 6 stages of 64
-    {DMA, 256, 224, 1, 64, 5.73, 0.5, 8.77, 0.00},   // 15: 8 waves of 64x128 and 64x96, 2 stages of 64
+    {DMA, 256, 256, 1, 64, 6.30, 6.0, 8.05, 0.00},   // 4: 8 waves of 64x128, 2 stages of 64
+    {DMA, 128, 128, 1, 64, 4.03, 0.0, 13.00, 0.00},  // 5: 8 waves of 32x64, 4 stages of 64
+    {DMA, 64, 128, 1, 128, 2.75, 5.0, 16.32, 0.00},  // 6: 4 waves of 32x64, 3 stages of 128
+    {DMA, 128, 64, 1, 128, 2.92, 5.9, 16.88, 0.00},  // 7: 4 waves of 64x32, 3 stages of 128
+    {DMA, 128, 128, 2, 64, 3.52, 0.0, 25.17, 1.76},  // 8: as 5, K split in two
+    {DMA, 64, 128, 2, 128, 2.50, 6.3, 40.00, 0.69},  // 9: as 6, K split in two
+    {DMA, 128, 128, 1, 32, 4.43, 0.0, 13.05, 0.00},  // 10: 8 waves of 32x64, 4 stages of 32 (any K)
+    {DMA, 128, 128, 1, 32, 4.35, 0.0, 13.10, 0.00},  // 11: 8 waves of 32x64, 8 stages of 32
+    {DMA, 256, 128, 1, 64, 5.62, 8.6, 10.70, 0.00},  // 12: 8 waves of 64x64, 3 stages of 64
+    {DMA, 128, 256, 1, 64, 5.33, 6.9, 10.85, 0.00},  // 13: 8 waves of 64x64, 3 stages of 64
+    {DMA, 64, 128, 1, 64, 2.60, 2.3, 17.23, 0.00},   // 14: 4 waves of 32x64, 6 stages of 64
+    {DMA, 256, 224, 1, 64, 5.70, 0.0, 8.88, 0.00},   // 15: 8 waves of 64x128 and 64x96, 2 stages of 64
     {Q4KDMA, 256, 256, 1, 64, 0.0, 0.0, 0.0, 0.0}, // 16: Q4_K by DMA, 8 waves of 64x128
     {Q4KDMA, 128, 256, 1, 64, 0.0, 0.0, 0.0, 0.0}, // 17: Q4_K by DMA, 8 waves of 64x64
     {Q4KDMA, 256, 256, 2, 64, 0.0, 0.0, 0.0, 0.0}, // 18: as 16, K split (launcher-sized, >= 2)
     {Q4KDMA, 128, 256, 2, 64, 0.0, 0.0, 0.0, 0.0}, // 19: as 17, K split (launcher-sized, >= 2)
     {NONE, 0, 0, 1, 0, 0.0, 0.0, 0.0, 0.0},        // 20: the skinny kernel (not a tile configuration)
-    {DMA, 256, 224, 1, 32, 7.06, 9.9, 9.18, 0.00},   // 21: as 15, 4 stages of 32
-    {DMA, 256, 224, 1, 32, 6.77, 9.7, 9.15, 0.00},   // 22: as 15, 5 stages of 32
+    {DMA, 256, 224, 1, 32, 7.07, 10.7, 9.00, 0.00},   // 21: as 15, 4 stages of 32
+    {DMA, 256, 224, 1, 32, 6.78, 10.1, 8.73, 0.00},   // 22: as 15, 5 stages of 32
+    {DMA, 128, 128, 2, 32, 3.59, 0.0, 17.89, 1.65},   // 23: as 8, 8 stages of 32
+    {DMA, 64, 128, 1, 32, 2.70, 1.4, 17.12, 0.00},    // 24: as 14, 8 stages of 32
 };
 constexpr int FIRST_DMA_CFG = 4;
 constexpr int N_CFGS = sizeof(kCfgs) / sizeof(kCfgs[0]);
@@ -1788,6 +1790,8 @@ static hipError_t launch_dma_cfg(int cfg, const GemmArgs & a, int nblocks, hipSt
         case 15: return launch_cols<256, 128, 96, 64, 2, TL>(a, nblocks, st);
         case 21: return launch_cols<256, 128, 96, 32, 4, TL>(a, nblocks, st);
         case 22: return launch_cols<256, 128, 96, 32, 5, TL>(a, nblocks, st);
+        case 23: return launch_f16<128, 128, 4, 2, 32, 8, 2, TL>(a, nblocks, st);
+        case 24: return launch_f16<64, 128, 2, 2, 32, 8, 1, TL>(a, nblocks, st);
         case 4: return launch_f16<256, 256, 4, 2, 64, 2, 1, TL>(a, nblocks, st);
         case 5: return launch_f16<128, 128, 4, 2, 64, 4, 1, TL>(a, nblocks, st);
         case 6: return launch_f16<64, 128, 2, 2, 128, 3, 1, TL>(a, nblocks, st);

@@ -307,12 +307,12 @@ def test_pack_act_tiled_bitexact(mx):
 
 # Every tile configuration of mi355x_gemm, forced through MI355X_GEMM_CFG, on a ragged fused
 # launch (M and both N not multiples of any tile). Configurations 0-3 are the register-staged
-# kernel (every weight layout but the tiled fp16 one); 4-15, 21 and 22 the LDS-DMA kernels,
+# kernel (every weight layout but the tiled fp16 one); 4-15 and 21-24 the LDS-DMA kernels,
 # which take fp16 weights only, row-major (F16) or tiled (F16_T); 16-19 the Q4_K kernel with
 # every operand by DMA (K % 256 == 0, Q4_K only). 20 is the skinny kernel (M <= 128), covered
 # by its own tests.
 REG_CFGS = list(range(0, 4))
-DMA_CFGS = list(range(4, 16)) + [21, 22]
+DMA_CFGS = list(range(4, 16)) + [21, 22, 23, 24]
 QDMA_CFGS = list(range(16, 20))
 F16_T = 0x101
 QUANT = (O.Q4_K, O.MXFP4, O.Q8_0, O.Q6_K, O.Q4_0, O.Q5_K)
