@@ -352,6 +352,75 @@ fa_kernel(FaArgs a) {
             }
         }
     }
+    // DMA sources: K and V rows (keys, clamped to the last key); chunks past dk / dv, padding,
+    // read the zero bytes for every key (row stride 0)
+    const uint16_t * ksrc[C::PK];
+    uint32_t kreal = 0, vreal = 0;   // bit q: source q is a real column (else the zero bytes)
+    const uint16_t * vsrc[C::PV];
+#pragma unroll
+    for (int q = 0; q < C::PK; q++) {
+        const int slot = (q * C::WAVES + wave) * WAVE + lane;
+        const int r = slot / C::KCH, c = C::kchunk_inv(r, slot % C::KCH);
+        const bool real = 8 * c < a.dk;
+        kreal |= (uint32_t)real << q;
+        ksrc[q] = real ? a.k + (int64_t)hk * a.k_nb2 + 8 * c + (int64_t)r * a.k_nb1 : a.kzero;   // + key offset per tile
+    }
+#pragma unroll
+    for (int q = 0; q < C::PV; q++) {
+        const int slot = (q * C::WAVES + wave) * WAVE + lane;
+        const int r = slot / C::VCH, c = (slot % C::VCH) ^ C::vswz(r);
+        const bool real = 8 * c < a.dv;
+        vreal |= (uint32_t)real << q;
+        vsrc[q] = real ? a.v + (int64_t)hk * a.v_nb2 + 8 * c + (int64_t)r * a.v_nb1 : a.kzero;   // + key offset per tile
+    }
+    const int kv_last = max(a.KV - 1, 0);
+    // tile i of the range starting at key tile dma_t0 (dma_nt tiles) into ring buffer i % FA_NS;
+    // past the last tile the last one is fetched again into the buffer just freed (nobody reads
+    // it), so every step issues the same DMA count
+    int dma_t0 = 0, dma_nt = 2;
+    auto issue = [&](int i) {
+        uint8_t * st = smem + (i % FA_NS) * C::STAGE;
+        i = min(i, max(dma_nt - 1, 0));
+        const int j0 = (dma_t0 + i) * FA_BKV;
+        if (j0 + FA_BKV <= a.KV) {
+            // every key of the tile exists: one scalar row offset for the whole wave, added to
+            // the real sources only
+            const int64_t ko = (int64_t)j0 * a.k_nb1, vo = (int64_t)j0 * a.v_nb1;
+#pragma unroll
+            for (int q = 0; q < C::PK; q++)
+                fa_dma16(ksrc[q] + ((kreal >> q) & 1u ? ko : 0), st + (q * C::WAVES + wave_s) * 1024);
+#pragma unroll
+            for (int q = 0; q < C::PV; q++)
+                fa_dma16(vsrc[q] + ((vreal >> q) & 1u ? vo : 0), st + C::K_BYTES + (q * C::WAVES + wave_s) * 1024);
+            return;
+        }
+#pragma unroll
+        for (int q = 0; q < C::PK; q++) {
+            const int slot = (q * C::WAVES + wave) * WAVE + lane;
+            const int r = slot / C::KCH;
+            const int64_t jr = (int64_t)min(j0 + r, kv_last) - r;
+            fa_dma16(ksrc[q] + ((kreal >> q) & 1u ? jr * a.k_nb1 : 0), st + (q * C::WAVES + wave_s) * 1024);
+        }
+#pragma unroll
+        for (int q = 0; q < C::PV; q++) {
+            const int slot = (q * C::WAVES + wave) * WAVE + lane;
+            const int r = slot / C::VCH;
+            const int64_t jr = (int64_t)min(j0 + r, kv_last) - r;
+            fa_dma16(vsrc[q] + ((vreal >> q) & 1u ? jr * a.v_nb1 : 0), st + C::K_BYTES + (q * C::WAVES + wave_s) * 1024);
+        }
+    };
+
+    // The first two key tiles are requested now, before the mask classes say where the block's
+    // range starts: with one KV split the range almost always starts at key tile 0 (a causal
+    // mask hides no leading key from any query), and then the tiles' HBM round trip runs under
+    // the class scan and the Q conversion instead of after them. Stages 0 and 1 are free (the Q
+    // hand-over uses 2 and 3, the class rows sit behind the ring). A guess that turns out wrong
+    // waits for these tiles to land and requests the real ones.
+    const bool spec = a.nsplit == 1 && a.KV >= 1;
+    if (spec) {
+        issue(0);
+        issue(1);
+    }
     // Parity-0 waves issue first on their SIMD: both waves of a SIMD reach each step's score
     // MFMAs together, and the priority lets one run them while the other waits, so afterwards
     // one wave's softmax overlaps the other's MFMAs instead of both competing for each unit.
@@ -426,6 +495,12 @@ fa_kernel(FaArgs a) {
     const int tile0 = lo + split * per;
     const int tile1 = min(hi, tile0 + per);
     const int ntl = max(0, tile1 - tile0);
+    dma_t0 = tile0;
+    dma_nt = ntl;
+    // the guessed tiles are the real tiles 0 and 1 when the range starts at key tile 0 (a tile
+    // past the range's end is never read); otherwise they land before their stages are refilled
+    const bool spec_ok = spec && tile0 == 0;
+    if (spec && !spec_ok) fa_wait_vm_lgkm0<0>();
 
     float16v o[DBLK];
 #pragma unroll
@@ -438,62 +513,6 @@ fa_kernel(FaArgs a) {
     const uint16_t * mrow = (a.mask && qok) ? a.mask + (int64_t)tq * a.mask_nb1 : nullptr;
     // this task's class row, copied into LDS behind the ring by the range scan above
     const uint8_t * cls_w = smem + C::LDS + (qt - qt_first) * a.cls_stride;
-
-    // DMA sources: K and V rows (keys, clamped to the last key); chunks past dk / dv, padding,
-    // read the zero bytes for every key (row stride 0)
-    const uint16_t * ksrc[C::PK];
-    uint32_t kreal = 0, vreal = 0;   // bit q: source q is a real column (else the zero bytes)
-    const uint16_t * vsrc[C::PV];
-#pragma unroll
-    for (int q = 0; q < C::PK; q++) {
-        const int slot = (q * C::WAVES + wave) * WAVE + lane;
-        const int r = slot / C::KCH, c = C::kchunk_inv(r, slot % C::KCH);
-        const bool real = 8 * c < a.dk;
-        kreal |= (uint32_t)real << q;
-        ksrc[q] = real ? a.k + (int64_t)hk * a.k_nb2 + 8 * c + (int64_t)r * a.k_nb1 : a.kzero;   // + key offset per tile
-    }
-#pragma unroll
-    for (int q = 0; q < C::PV; q++) {
-        const int slot = (q * C::WAVES + wave) * WAVE + lane;
-        const int r = slot / C::VCH, c = (slot % C::VCH) ^ C::vswz(r);
-        const bool real = 8 * c < a.dv;
-        vreal |= (uint32_t)real << q;
-        vsrc[q] = real ? a.v + (int64_t)hk * a.v_nb2 + 8 * c + (int64_t)r * a.v_nb1 : a.kzero;   // + key offset per tile
-    }
-    const int kv_last = max(a.KV - 1, 0);
-    // tile i into ring buffer i % FA_NS; past the last tile the last one is fetched again into
-    // the buffer just freed (nobody reads it), so every step issues the same DMA count
-    auto issue = [&](int i) {
-        uint8_t * st = smem + (i % FA_NS) * C::STAGE;
-        i = min(i, max(ntl - 1, 0));
-        const int j0 = (tile0 + i) * FA_BKV;
-        if (j0 + FA_BKV <= a.KV) {
-            // every key of the tile exists: one scalar row offset for the whole wave, added to
-            // the real sources only
-            const int64_t ko = (int64_t)j0 * a.k_nb1, vo = (int64_t)j0 * a.v_nb1;
-#pragma unroll
-            for (int q = 0; q < C::PK; q++)
-                fa_dma16(ksrc[q] + ((kreal >> q) & 1u ? ko : 0), st + (q * C::WAVES + wave_s) * 1024);
-#pragma unroll
-            for (int q = 0; q < C::PV; q++)
-                fa_dma16(vsrc[q] + ((vreal >> q) & 1u ? vo : 0), st + C::K_BYTES + (q * C::WAVES + wave_s) * 1024);
-            return;
-        }
-#pragma unroll
-        for (int q = 0; q < C::PK; q++) {
-            const int slot = (q * C::WAVES + wave) * WAVE + lane;
-            const int r = slot / C::KCH;
-            const int64_t jr = (int64_t)min(j0 + r, kv_last) - r;
-            fa_dma16(ksrc[q] + ((kreal >> q) & 1u ? jr * a.k_nb1 : 0), st + (q * C::WAVES + wave_s) * 1024);
-        }
-#pragma unroll
-        for (int q = 0; q < C::PV; q++) {
-            const int slot = (q * C::WAVES + wave) * WAVE + lane;
-            const int r = slot / C::VCH;
-            const int64_t jr = (int64_t)min(j0 + r, kv_last) - r;
-            fa_dma16(vsrc[q] + ((vreal >> q) & 1u ? jr * a.v_nb1 : 0), st + C::K_BYTES + (q * C::WAVES + wave_s) * 1024);
-        }
-    };
 
     // V^T fragments by ds_read_b64_tr_b16, which gives lane i of each 16-lane group element e =
     // element i % 4 of the group's source lane 4e + i / 4. Source lane s of group gq points at
@@ -514,8 +533,10 @@ fa_kernel(FaArgs a) {
     // (the same query rows), and both land in the ring during the step before.
     const int nsteps = (ntl + 1) / 2;
     if (ntl > 0) {
-        issue(0);
-        issue(1);
+        if (!spec_ok) {
+            issue(0);
+            issue(1);
+        }
         if constexpr (!QSHARE)
 #pragma unroll
             for (int p = 2; p < FA_NS; p++) issue(p);
