@@ -261,12 +261,14 @@ static size_t mul_mat_part_offset(int64_t M, int64_t K) {
 // form depending on the shape: the two-pass form wins where N >= K and the fp16 weight is at most
 // 64 MB (1.02-1.38x, e.g. 1.20x for N 6144, K 4096 at M 512), and loses on larger panels, whose
 // fp16 form no longer stays in the 256 MB last-level cache (0.83x for N 28672, K 4096 at M 512).
-// Same fp16 weights and activations either way.
+// Q8_0 with whole 256-value blocks has an all-DMA kernel of its own, which wins at M < 1024 but
+// on one kind of shape (mx::q8_0_decode_first). Same fp16 weights and activations either way.
 static bool mul_mat_decode_first(int wtype, int64_t M, int64_t N, int64_t K) {
     if (K % 64 || M < 512) return false;
     if (wtype == mx::T_Q6_K || wtype == mx::T_Q5_K || wtype == mx::T_MXFP4) return true;
     if (wtype == mx::T_Q4_K) return N >= K && N * K <= ((int64_t)1 << 25);
-    return (wtype == mx::T_Q8_0 || wtype == mx::T_Q4_0) && (N >= K || M >= 1024);
+    if (wtype == mx::T_Q8_0) return mx::q8_0_decode_first(M, N, K);
+    return wtype == mx::T_Q4_0 && (N >= K || M >= 1024);
 }
 
 MI355X_API int mi355x_mul_mat_decode_first(int wtype, int64_t M, int64_t N, int64_t K) {

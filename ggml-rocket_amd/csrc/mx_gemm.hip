@@ -981,22 +981,31 @@ gemm_f16_cols_kernel(GemmArgs args) {
 //     LDS writes, one barrier, the first fragments of s+1, then the DMA of the activations of
 //     s+2, the nibbles of s+3 and, when s % 4 == 1, the header of the next block; the rest of the
 //     step's MFMAs run under these.
-// DMA instructions retire in order, so each wait counts the ones issued after its target:
-//   before the decode in stage s:  PA + 1, or PA + 2 when s % 4 == 2 (a header was issued last)
-//   at the end of stage s:         1, or 2 when s % 4 == 2.
+// DMA instructions retire in order, so each wait counts the ones issued after its target (QD =
+// the quant DMA instructions a thread issues per stage, 1 for Q4_K):
+//   before the decode in stage s:  PA + QD, or PA + QD + 1 when s % 4 == 2 (a header was issued last)
+//   at the end of stage s:         QD, or QD + 1 when s % 4 == 2.
 // K % 256 == 0; a K split (args.ksplit) divides whole blocks. Past the last stage the last one
 // is fetched and decoded again into the free buffers, so every stage issues the same DMA.
+//
+// The same pipeline takes Q8_0 weights in their split layout (int8 quants [rows][K], then fp16 d
+// [rows][K/32]): a thread's 32 values are 32 quant bytes (QD = 2 instructions, the Q ring twice as
+// wide) and the "header" of 256 values is the row's 8 block scales, 16 bytes as for Q4_K. The
+// decode is Q8_0's packed one (exact: the int8 code under 1024, less the offset, times d rounds
+// the exact product once). The wider Q ring leaves room for the 128 x 256 tile only.
 // ---------------------------------------------------------------------------------------------
-template <int BM, int WGM, int WGN>
+template <int WT, int BM, int WGM, int WGN>
 struct Q4kCfg {
     static constexpr int BN = 256, NW = WGM * WGN, THREADS = WAVE * NW;
     static constexpr int TM = BM / WGM, TN = BN / WGN, MI = TM / 32, NJ = TN / 32;
     static constexpr int DK = 64, RB = 128;                         // 8 chunks of 16 bytes a row
+    static constexpr int QD = WT == T_Q8_0 ? 2 : 1;                 // quant DMA per thread and stage
     static constexpr int A_BYTES = BM * RB, B_BYTES = BN * RB;
-    static constexpr int Q_BYTES = BN * 32, H_BYTES = BN * 16;
+    static constexpr int Q_BYTES = BN * 32 * QD, H_BYTES = BN * 16;
     static constexpr int OFF_B = 2 * A_BYTES, OFF_Q = OFF_B + 2 * B_BYTES, OFF_H = OFF_Q + 3 * Q_BYTES;
     static constexpr int LDS = OFF_H + 2 * H_BYTES;
     static constexpr int PA = A_BYTES / (THREADS * 16);             // activation DMA per wave
+    static_assert(WT == T_Q4_K || WT == T_Q8_0, "weight type");
     static_assert(NW == 8 && THREADS == 2 * BN, "one (row, half) item per thread");
     static_assert(MI >= 1 && NJ >= 1 && TM % 32 == 0 && TN % 32 == 0, "wave tile");
     static_assert(PA >= 1 && PA * THREADS * 16 == A_BYTES, "DMA split");
@@ -1010,11 +1019,11 @@ __device__ __forceinline__ void wait_vm() {
     __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
 }
 
-template <int BM, int WGM, int WGN>
+template <int WT, int BM, int WGM, int WGN>
 __global__ void __launch_bounds__(WAVE * WGM * WGN)
 __attribute__((amdgpu_waves_per_eu(2, 2)))
 gemm_q4k_kernel(GemmArgs args) {
-    using C = Q4kCfg<BM, WGM, WGN>;
+    using C = Q4kCfg<WT, BM, WGM, WGN>;
     extern __shared__ __align__(16) uint8_t smem[];
     const int t = threadIdx.x, lane = t % WAVE, wave = t / WAVE;
     const int wm = wave / WGN, wn = wave % WGN;
@@ -1029,7 +1038,7 @@ gemm_q4k_kernel(GemmArgs args) {
     for (int i = 1; i < GEMM_MAX_GROUPS; i++)
         if (i < args.ng && nt >= args.g[i].ntile_begin) g = i;
     const uint8_t * W = (const uint8_t *)args.g[0].W;
-    int64_t row0 = args.g[0].row0;
+    int64_t row0 = args.g[0].row0, rows_total = args.g[0].rows_total;
     int N = args.g[0].N, ntb = args.g[0].ntile_begin;
     float * Cp = args.g[0].C;
     int64_t ldc = args.g[0].ldc;
@@ -1038,11 +1047,12 @@ gemm_q4k_kernel(GemmArgs args) {
         if (i == g) {
             W = (const uint8_t *)args.g[i].W; row0 = args.g[i].row0; N = args.g[i].N;
             ntb = args.g[i].ntile_begin; Cp = args.g[i].C; ldc = args.g[i].ldc;
+            rows_total = args.g[i].rows_total;
         }
     split_target(args, g, split, Cp, ldc);
     const int n0 = (nt - ntb) * C::BN, m0 = mt * BM;
     const int M = args.M, K = args.K;
-    const int nsb = K / 256;                                   // Q4_K blocks a row
+    const int nsb = K / 256;                                   // 256-value blocks a row
     const int per = (nsb + ks - 1) / ks;
     const int sb0 = split * per;
     const int nk = 4 * max(0, min(nsb, sb0 + per) - sb0);      // stages of this split
@@ -1056,11 +1066,22 @@ gemm_q4k_kernel(GemmArgs args) {
         const int r = slot / 8, c = (slot % 8) ^ ((r / 2) & 7);
         asrc[q] = args.A + (int64_t)min(m0 + r, M - 1) * args.lda + (int64_t)sb0 * 256 + 8 * c;
     }
-    // weight DMA: the nibbles of item t (row t/2, half t%2) and, for lanes 0-31, the header of
-    // row 32 * wave + lane; rows past N read the last row (their outputs are never stored)
-    const int64_t rowb = (int64_t)(K / 256) * 144;
-    const uint8_t * qsrc = W + (row0 + min(n0 + t / 2, N - 1)) * rowb + (int64_t)sb0 * 144 + 16 + 16 * (t % 2);
-    const uint8_t * hsrc = W + (row0 + min(n0 + 32 * wave + lane % 32, N - 1)) * rowb + (int64_t)sb0 * 144;
+    // weight DMA: the quants of item t (row t/2, half t%2) and, for lanes 0-31, the header of
+    // row 32 * wave + lane; rows past N read the last row (their outputs are never stored).
+    // Q4_K: per block qs_blk bytes apart, the header at the block's start, the nibbles of
+    // quarter j at 16 + 32 j; Q8_0: the quants at 64 bytes a stage, the 8 scales of a block
+    // 16 bytes apart in the scale plane.
+    const int64_t qrow = row0 + min(n0 + t / 2, N - 1), hrow = row0 + min(n0 + 32 * wave + lane % 32, N - 1);
+    const uint8_t * qsrc;
+    const uint8_t * hsrc;
+    if constexpr (WT == T_Q4_K) {
+        const int64_t rowb = (int64_t)(K / 256) * 144;
+        qsrc = W + qrow * rowb + (int64_t)sb0 * 144 + 16 + 16 * (t % 2);
+        hsrc = W + hrow * rowb + (int64_t)sb0 * 144;
+    } else {
+        qsrc = W + qrow * K + (int64_t)sb0 * 256 + 32 * (t % 2);
+        hsrc = W + rows_total * K + (hrow * (K / 32) + (int64_t)sb0 * 8) * 2;
+    }
     const int wave_s = __builtin_amdgcn_readfirstlane(wave);
 
     auto issue_a = [&](int s) {
@@ -1069,25 +1090,42 @@ gemm_q4k_kernel(GemmArgs args) {
 #pragma unroll
         for (int q = 0; q < C::PA; q++) dma16(asrc[q] + off, st + (q * C::NW + wave_s) * 1024);
     };
+    // the quant DMA of item t lands at (q * THREADS + t) * 16 of its Q stage, q < QD
     auto issue_q = [&](int s) {
         const int sc = min(s, nk - 1);
-        dma16(qsrc + (sc / 4) * 144 + 32 * (sc % 4), smem + C::OFF_Q + (s % 3) * C::Q_BYTES + wave_s * 1024);
+        const uint8_t * src = WT == T_Q4_K ? qsrc + (sc / 4) * 144 + 32 * (sc % 4) : qsrc + (int64_t)sc * 64;
+#pragma unroll
+        for (int q = 0; q < C::QD; q++)
+            dma16(src + 16 * q, smem + C::OFF_Q + (s % 3) * C::Q_BYTES + (q * C::NW + wave_s) * 1024);
     };
     auto issue_h = [&](int b) {
         const int bc = min(b, nk / 4 - 1);
-        if (lane < 32) dma16(hsrc + bc * 144, smem + C::OFF_H + (b & 1) * C::H_BYTES + wave_s * 512);
+        if (lane < 32)
+            dma16(hsrc + (WT == T_Q4_K ? bc * 144 : bc * 16), smem + C::OFF_H + (b & 1) * C::H_BYTES + wave_s * 512);
     };
     // decode the item of stage s (J = s % 4) into B buffer s & 1
     auto decode = [&](int s, auto Jc) {
         constexpr int J = decltype(Jc)::value;
-        WLoad<T_Q4_K> w;
-        w.hdr = *(const u32x4 *)(smem + C::OFF_H + ((s / 4) & 1) * C::H_BYTES + (t / 2) * 16);
-        w.qs = *(const u32x4 *)(smem + C::OFF_Q + (s % 3) * C::Q_BYTES + t * 16);
-        w.j = J;
-        w.ok = true;
+        const u32x4 hdr = *(const u32x4 *)(smem + C::OFF_H + ((s / 4) & 1) * C::H_BYTES + (t / 2) * 16);
+        const uint8_t * qs = smem + C::OFF_Q + (s % 3) * C::Q_BYTES + t * 16;
         u32x4 out[4];
         int run0, run1;
-        w.decode(t % 2, out, run0, run1);
+        if constexpr (WT == T_Q4_K) {
+            WLoad<T_Q4_K> w;
+            w.hdr = hdr;
+            w.qs = *(const u32x4 *)qs;
+            w.j = J;
+            w.ok = true;
+            w.decode(t % 2, out, run0, run1);
+        } else {
+            // block 2 J + half of the 256 values: its scale is half (t % 2) of word J
+            WLoad<T_Q8_0> w;
+            w.q[0] = *(const u32x4 *)qs;
+            w.q[1] = *(const u32x4 *)(qs + C::THREADS * 16);
+            w.d = (uint16_t)(hdr[J] >> (16 * (t % 2)));
+            w.ok = true;
+            w.decode_fast(t % 2, out, run0, run1);
+        }
         uint8_t * bs = smem + C::OFF_B + (s & 1) * C::B_BYTES;
         const int r = t / 2;
         *(u32x4 *)(bs + swz<8>(r, run0 / 8)) = out[0];
@@ -1143,12 +1181,12 @@ gemm_q4k_kernel(GemmArgs args) {
                 __builtin_amdgcn_sched_barrier(0);
             }
             if (kstep == kd) {
-                wait_vm<C::PA + (J == 2 ? 2 : 1)>();
+                wait_vm<C::PA + C::QD + (J == 2 ? 1 : 0)>();
                 decode(s + 1, std::integral_constant<int, (J + 1) % 4>());
                 __builtin_amdgcn_sched_barrier(0);
             }
             if (kstep + 1 == KST) {
-                wait_vm_lgkm0<J == 2 ? 2 : 1>();
+                wait_vm_lgkm0<C::QD + (J == 2 ? 1 : 0)>();
                 __builtin_amdgcn_s_barrier();
                 read_frags(s + 1, 0, G);
                 __builtin_amdgcn_sched_barrier(0);
@@ -1175,7 +1213,7 @@ gemm_q4k_kernel(GemmArgs args) {
         issue_a(1);
         issue_q(2);
         __builtin_amdgcn_sched_barrier(0);
-        wait_vm_lgkm0<C::PA + 2>();   // this wave's LDS writes; the DMA stays in flight
+        wait_vm_lgkm0<C::PA + 2 * C::QD>();   // this wave's LDS writes; the DMA stays in flight
         __builtin_amdgcn_s_barrier();
         read_frags(0, 0, f0);
         __builtin_amdgcn_sched_barrier(0);
@@ -1770,10 +1808,10 @@ static hipError_t launch_cols(const GemmArgs & a, int nblocks, hipStream_t st) {
     return hipGetLastError();
 }
 
-template <int BM, int WGM, int WGN>
+template <int WT, int BM, int WGM, int WGN>
 static hipError_t launch_q4k(const GemmArgs & a, int nblocks, hipStream_t st) {
-    using C = Q4kCfg<BM, WGM, WGN>;
-    auto kern = gemm_q4k_kernel<BM, WGM, WGN>;
+    using C = Q4kCfg<WT, BM, WGM, WGN>;
+    auto kern = gemm_q4k_kernel<WT, BM, WGM, WGN>;
     static bool attr = false;
     if (!attr) {
         hipError_t e = hipFuncSetAttribute((const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize, C::LDS);
@@ -1810,11 +1848,19 @@ static hipError_t launch_dma_cfg(int cfg, const GemmArgs & a, int nblocks, hipSt
 template <int WT>
 static hipError_t launch_cfg(int cfg, const GemmArgs & a, int nblocks, hipStream_t st) {
     if (kCfgs[cfg].kind == Q4KDMA) {
-        if constexpr (WT != T_Q4_K) return hipErrorInvalidValue;
-        else switch (cfg) {
-            case 16: case 18: return launch_q4k<256, 4, 2>(a, nblocks, st);
-            case 17: case 19: return launch_q4k<128, 2, 4>(a, nblocks, st);
-            default: return hipErrorInvalidValue;
+        if constexpr (WT == T_Q4_K) {
+            switch (cfg) {
+                case 16: case 18: return launch_q4k<T_Q4_K, 256, 4, 2>(a, nblocks, st);
+                case 17: case 19: return launch_q4k<T_Q4_K, 128, 2, 4>(a, nblocks, st);
+                default: return hipErrorInvalidValue;
+            }
+        } else if constexpr (WT == T_Q8_0) {
+            switch (cfg) {
+                case 17: case 19: return launch_q4k<T_Q8_0, 128, 2, 4>(a, nblocks, st);
+                default: return hipErrorInvalidValue;
+            }
+        } else {
+            return hipErrorInvalidValue;
         }
     }
     if (kCfgs[cfg].kind == DMA) {
@@ -1892,7 +1938,7 @@ static bool cfg_fits(int c, int wt, int K) {
     const CfgDesc & d = kCfgs[c];
     if (d.kind == NONE) return false;
     if (d.kind == REG) return wt != T_F16T;
-    if (d.kind == Q4KDMA) return wt == T_Q4_K && K % 256 == 0;
+    if (d.kind == Q4KDMA) return (wt == T_Q4_K || (wt == T_Q8_0 && d.bm == 128)) && K % 256 == 0;
     if ((wt != T_F16 && wt != T_F16T) || K % d.dk) return false;
     return d.ksplit == 1 || K / d.dk >= 2;
 }
@@ -1944,6 +1990,15 @@ static int choose_cfg(int wt, const GemmArgs & a) {
         if ((int64_t)a.K >= 2 * tiles_n_cols(a)) return a.M <= 1024 ? 19 : 18;
         if (tiles_of(a, 256, 256) >= fill) return 16;
         if (tiles_of(a, 128, 256) >= fill) return 17;
+    }
+    // Q8_0 with whole blocks: the all-DMA kernel on its 128 x 256 tiles, K split where K is deep
+    // for the output width or the tiles fill less than half the chip. Measured at M 512 and 2048
+    // for N x K in {3072, 8192} x {3072, 8192} and the 8B shapes 14336 x 4096 / 4096 x 14336, the
+    // pick is the faster of the two, and 1.1-1.6x faster than the register-staged kernel.
+    if (wt == T_Q8_0 && a.K % 256 == 0) {
+        const int fill = (cus * 7 + 9) / 10;
+        if (((int64_t)a.K >= 2 * tiles_n_cols(a) && a.M <= 1024) || tiles_of(a, 128, 256) < fill / 2) return 19;
+        return 17;
     }
     // a skinny output: split K (see reg_split); otherwise the unsplit tile with the best fill
     if (reg_split_est(a) >= 1.5 && (a.K / BK) >= 8) return 1;
@@ -2113,6 +2168,19 @@ static GemmPlan plan_gemm(int wt, const GemmArgs & a, int cap) {
     p.ks = p.cfg == 1 ? reg_split(a, cap)
          : (d.kind == Q4KDMA && d.ksplit > 1) ? q4k_split(a, d.bm, d.bn, cap) : d.ksplit;
     return p;
+}
+
+// Q8_0 at M < 1024 with whole 256-value blocks runs the all-DMA kernel (choose_cfg) faster than
+// the decode-first form (the whole weight decoded to tiled fp16, then the fp16 GEMM) except where
+// N >= K, the weight has more than 2^24 values and its 128 x 256 tiles leave more than 30% of the
+// chip idle (8192 x 3072 at M 512: 71.2 against 66.0 us); at M >= 1024 the decode-first form is
+// as fast or faster (its weight decoded once, against once per 128-row M tile), e.g. 14336 x 4096
+// at M 2048: 296 against 366 us.
+bool q8_0_decode_first(int64_t M, int64_t N, int64_t K) {
+    if (M >= 1024) return true;
+    if (K % 256) return N >= K;
+    const int64_t tiles = ((M + 127) / 128) * ((N + 255) / 256);
+    return N >= K && N * K > ((int64_t)1 << 24) && tiles < (cu_count() * 7 + 9) / 10;
 }
 
 size_t gemm_split_bytes(int wt, const GemmArgs & a) {

@@ -130,6 +130,7 @@ hipError_t launch_gemm(int wt, const GemmArgs & a, int n_tiles_total, hipStream_
 bool gemm_accumulates(int wt, const GemmArgs & a, size_t part_bytes);
 // partial workspace bytes of the launch's fastest K split (0 if it splits two ways or less)
 size_t gemm_split_bytes(int wt, const GemmArgs & a);
+bool q8_0_decode_first(int64_t M, int64_t N, int64_t K);   // mi355x_mul_mat's form for Q8_0
 hipError_t launch_dequant_f16(int wt, const void * W, int64_t rows, int64_t K, uint16_t * out, hipStream_t st);
 hipError_t launch_f16_tiled(int wt, const void * W, int64_t rows, int64_t K, uint16_t * out, hipStream_t st);
 hipError_t launch_pack_weight(int wt, const void * src, int64_t rows, int64_t K, void * dst, hipStream_t st);

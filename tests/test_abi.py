@@ -105,14 +105,17 @@ def test_x32_layout_argument_checks(x, base, bs):
 
 def test_mul_mat_workspace_sizes_the_decode_first_weight():
     """mi355x_mul_mat_workspace_for makes room for the tiled fp16 weight where the decode-first
-    form runs (Q6_K / Q5_K / MXFP4 at M >= 512; Q8_0 / Q4_0 at M >= 1024, or at M >= 512 with
-    N >= K) and elsewhere
-    sizes the pack and the in-GEMM decode's split partials only (host-side sizing: no GPU
-    needed)."""
+    form runs (Q6_K / Q5_K / MXFP4 at M >= 512; Q4_0 at M >= 1024, or at M >= 512 with N >= K;
+    Q8_0 at M >= 1024, and at M 512 only where N >= K, N * K > 2^24 and the all-DMA kernel's
+    128 x 256 tiles leave part of the chip idle, or with K off the 256-value blocks where N >= K)
+    and elsewhere sizes the pack and the in-GEMM decode's split partials only (host-side sizing:
+    no GPU needed)."""
     import ggml_mi355x as mx
     L = mx.lib()
     for wt, M, N, K, first in [(mx.Q6_K, 512, 1024, 3072, True), (mx.Q6_K, 128, 1024, 3072, False),
-                               (mx.Q8_0, 512, 3072, 1024, True), (mx.Q8_0, 512, 1024, 3072, False),
+                               (mx.Q8_0, 512, 3072, 1024, False), (mx.Q8_0, 512, 1024, 3072, False),
+                               (mx.Q8_0, 512, 8192, 3072, True), (mx.Q8_0, 512, 14336, 4096, False),
+                               (mx.Q8_0, 512, 3072, 1088, True),
                                (mx.Q8_0, 1024, 1024, 3072, True), (mx.Q4_K, 2048, 1024, 3072, False),
                                (mx.Q4_K, 512, 6144, 4096, True), (mx.Q4_K, 512, 28672, 4096, False),
                                (mx.Q5_K, 512, 1024, 3072, True), (mx.MXFP4, 512, 1024, 3072, True),

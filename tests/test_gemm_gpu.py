@@ -194,7 +194,7 @@ def test_mul_mat_quant_sweep(mx, K, N, M, wtype):
 
 
 @pytest.mark.parametrize("wtype,M,N,K", [(O.Q6_K, 512, 768, 1024), (O.Q8_0, 1024, 512, 2048),
-                                         (O.Q8_0, 512, 1024, 512), (O.Q5_K, 512, 384, 768),
+                                         (O.Q8_0, 512, 8192, 3072), (O.Q5_K, 512, 384, 768),
                                          (O.MXFP4, 512, 256, 512), (O.Q4_0, 512, 512, 256),
                                          (O.Q4_K, 512, 512, 256),
                                          # ragged: M off the 16-row groups of the tiled pack, N off the
@@ -308,8 +308,8 @@ def test_pack_act_tiled_bitexact(mx):
 # Every tile configuration of mi355x_gemm, forced through MI355X_GEMM_CFG, on a ragged fused
 # launch (M and both N not multiples of any tile). Configurations 0-3 are the register-staged
 # kernel (every weight layout but the tiled fp16 one); 4-15 and 21-24 the LDS-DMA kernels,
-# which take fp16 weights only, row-major (F16) or tiled (F16_T); 16-19 the Q4_K kernel with
-# every operand by DMA (K % 256 == 0, Q4_K only). 20 is the skinny kernel (M <= 128), covered
+# which take fp16 weights only, row-major (F16) or tiled (F16_T); 16-19 the kernel with every
+# operand by DMA (K % 256 == 0; Q4_K, and Q8_0 on the 128 x 256 tiles 17 and 19). 20 is the skinny kernel (M <= 128), covered
 # by its own tests.
 REG_CFGS = list(range(0, 4))
 DMA_CFGS = list(range(4, 16)) + [21, 22, 23, 24]
@@ -326,8 +326,8 @@ def test_gemm_every_tile_config(mx, monkeypatch, cfg, wtype):
         pytest.skip("the LDS-DMA configurations take fp16 weights only")
     if cfg in REG_CFGS and wtype == F16_T:
         pytest.skip("the register-staged configurations do not read the tiled layout")
-    if cfg in QDMA_CFGS and wtype != O.Q4_K:
-        pytest.skip("the all-DMA configurations take Q4_K weights only")
+    if cfg in QDMA_CFGS and wtype != O.Q4_K and not (wtype == O.Q8_0 and cfg in (17, 19)):
+        pytest.skip("the all-DMA configurations take Q4_K weights, and Q8_0 on the 128-row tiles")
     monkeypatch.setenv("MI355X_GEMM_CFG", str(cfg))
     K, M, Ns = 1280, 300, (528, 144)
     Xf = O.fill_normal((M, K), 900 + cfg)
