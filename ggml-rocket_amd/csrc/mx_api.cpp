@@ -543,7 +543,7 @@ MI355X_API int mi355x_flash_attn_ex(const mi355x_fa_args * a, int nsplit, int fl
 namespace {
 
 struct MoeLayout {
-    size_t a16, scales, off, rows, tiles, n_tiles, err, total;
+    size_t a16, scales, off, rows, tiles, n_tiles, err, zero, total;
 };
 
 inline size_t up256(size_t x) { return (x + 255) & ~(size_t)255; }
@@ -562,6 +562,7 @@ bool moe_layout(const mi355x_moe_args * a, MoeLayout & L) {
     L.tiles = o;   o += up256(tiles * 8);
     L.n_tiles = o; o += 256;
     L.err = o;     o += 256;
+    L.zero = o;    o += 256;
     L.total = o;
     return true;
 }
@@ -578,7 +579,8 @@ MI355X_API int mi355x_mul_mat_id(const mi355x_moe_args * a, void * workspace_dev
     MoeLayout L;
     if (!moe_layout(a, L)) return MI355X_E_ARG;
     if (!known_moe_wtype(a->wtype) || a->K % 32 || a->K % blck(a->wtype) || a->N % 16) return MI355X_E_ARG;
-    if (x32_wtype(a->wtype) && a->N % 32) return MI355X_E_ARG;   // experts are whole 32-row groups
+    // experts are whole 32-row groups, each plane's share of one expert under 2^31 bytes
+    if (x32_wtype(a->wtype) && (a->N % 32 || a->N * a->K > ((int64_t)1 << 31))) return MI355X_E_ARG;
     if (!a->as_dev || !a->b_dev || !a->ids_dev || !a->dst_dev || !aligned(a->as_dev, 16) || !aligned(a->b_dev, 16))
         return MI355X_E_ARG;
     if (a->b_nb1 < a->K || a->b_nb1 % 4 || a->b_nb2 != a->ne11 * a->b_nb1) return MI355X_E_ARG;
@@ -601,6 +603,7 @@ MI355X_API int mi355x_mul_mat_id(const mi355x_moe_args * a, void * workspace_dev
     m.tiles = (int32_t *)(ws + L.tiles);
     m.n_tiles = (int32_t *)(ws + L.n_tiles);
     m.err = err_dev ? err_dev : (int32_t *)(ws + L.err);
+    m.zero = (uint16_t *)(ws + L.zero);
     return hip_status(mx::launch_moe(a->wtype, m, S(stream)));
 }
 

@@ -98,6 +98,7 @@ struct MoeArgs {
     int32_t * tiles;           // [2*max_tiles] (expert, first row)
     int32_t * n_tiles;         // [1]
     int32_t * err;             // [1] set when an id is out of range
+    uint16_t * zero;           // [64] zeros (written by the bucketing pass), read for k past K
 };
 
 int moe_max_tiles(int T, int U, int E);

@@ -72,6 +72,7 @@ __device__ __forceinline__ void moe_sort_block(const MoeArgs & a) {
     __shared__ int2 wsum[MOE_SORT_THREADS / WAVE];
     const int t = threadIdx.x;
     const int R = a.T * a.U;
+    if (t < 8) ((u32x4 *)a.zero)[t] = u32x4{0, 0, 0, 0};
     for (int e = t; e < a.E; e += MOE_SORT_THREADS) cnt[e] = 0;
     if (t == 0) bad = 0;
     __syncthreads();
@@ -174,6 +175,35 @@ template <int WT> constexpr int moe_stages() {
     return moe_waves<WT>() == 4 ? 2 : (WT == T_F16 || WT == T_Q6_K || WT == T_Q6_KX || WT == T_Q5_K) ? 3 : 4;
 }
 
+template <int WT> constexpr bool moe_x32() { return WT == T_Q4_KX || WT == T_Q8_0X || WT == T_Q6_KX || WT == T_MXFP4X; }
+// formats whose K may end half-way through a 64-deep slab (32-value blocks)
+template <int WT> constexpr bool moe_k_tail() {
+    return !(WT == T_Q4_K || WT == T_Q4_KX || WT == T_Q5_K || WT == T_Q6_K || WT == T_Q6_KX);
+}
+
+// A lane's weight loads: the row-strided formats keep the lane's panel row and half; the
+// regrouped layouts keep WLoad's Lane (a block-uniform base and fixed lane offsets).
+template <int WT, bool X = moe_x32<WT>()> struct MoeLane {
+    int64_t row;
+    int u;
+    __device__ __forceinline__ void init(const MoeArgs & a, int e, int nloc, int u_) {
+        row = (int64_t)e * a.N + nloc;
+        u = u_;
+    }
+    __device__ __forceinline__ void load(WLoad<WT> & w, const MoeArgs & a, int64_t k0, bool ok) const {
+        w.load((const uint8_t *)a.w, (int64_t)a.E * a.N, a.K, row, k0, u, ok);
+    }
+};
+template <int WT> struct MoeLane<WT, true> {
+    typename WLoad<WT>::Lane l;
+    __device__ __forceinline__ void init(const MoeArgs & a, int e, int nloc, int u) {
+        l = WLoad<WT>::lane((const uint8_t *)a.w, (int64_t)a.E * a.N, a.K, (int64_t)e * a.N, nloc, u);
+    }
+    __device__ __forceinline__ void load(WLoad<WT> & w, const MoeArgs & a, int64_t k0, bool ok) const {
+        w.load(l, a.K, k0, ok);
+    }
+};
+
 template <int WT>
 __global__ void __launch_bounds__(MOE_THREADS) __attribute__((amdgpu_waves_per_eu(moe_waves<WT>(), moe_waves<WT>())))
 moe_gemm_kernel(MoeArgs a) {
@@ -215,15 +245,16 @@ moe_gemm_kernel(MoeArgs a) {
 
     const int K = a.K;
     const int n0 = nt * MOE_BN;
-    const uint8_t * W = (const uint8_t *)a.w;
-    const int64_t rows_total = (int64_t)a.E * a.N;
     const int lr = lane % 32, lg = lane / 32;
     const int wr = wave * 32 + lr, wu = lg;   // this lane's weight row (output column) in the block, and its half
-    const int64_t wrow = (int64_t)e * a.N + min(n0 + wr, a.N - 1);   // clamped: loads are unconditional
     const bool wok = n0 + wr < a.N;
-    // A: thread t stages rows t / 8 and 32 + t / 8, chunk t % 8
+    MoeLane<WT> wl;
+    wl.init(a, e, min(n0 + wr, a.N - 1), wu);   // clamped: loads are unconditional
+    // A: thread t stages rows t / 8 and 32 + t / 8, chunk t % 8. A pad row reads packed row 0:
+    // MFMA output row i depends on A row i alone, and pad rows' outputs are never stored.
     const int ar = t / 8, ac = t % 8;
-    const int arow0 = act_row(ar), arow1 = act_row(ar + 32);
+    const uint16_t * ap0 = a.a16 + (int64_t)max(act_row(ar), 0) * K + 8 * ac;
+    const uint16_t * ap1 = a.a16 + (int64_t)max(act_row(ar + 32), 0) * K + 8 * ac;
 
     float16v acc[2];
 #pragma unroll
@@ -233,32 +264,31 @@ moe_gemm_kernel(MoeArgs a) {
 
     struct Stage {
         u32x4 a0, a1;
-        bool ok0, ok1;   // activation chunk real (else stored as zero)
         WLoad<WT> w;
     };
-    // Pad rows and k past K load from a valid address and are zeroed at the LDS store: a branch
-    // around the load, or a select right after it, would make the compiler wait for the newest
-    // loads at the join and cut the register stages' lookahead to one.
-    auto load_a = [&](int arow, int64_t k0, bool & ok) -> u32x4 {
-        const int64_t k = k0 + 8 * ac;
-        ok = arow >= 0 && k < K;
-        return *(const u32x4 *)(a.a16 + (ok ? (int64_t)arow * K + k : 0));
+    // Past K (the last slab of a K that ends half-way through it) a chunk reads the zero block;
+    // the weights there decode to zero as well. A branch around a load, or a select on its
+    // value, would make the compiler wait for the newest loads at the join and cut the register
+    // stages' lookahead to one, so the address is what is chosen.
+    auto load_a = [&](const uint16_t * ap, int64_t k0) -> u32x4 {
+        const uint16_t * p = ap + k0;
+        if constexpr (moe_k_tail<WT>()) p = k0 + 8 * ac < K ? p : a.zero + 8 * ac;
+        return *(const u32x4 *)p;
     };
     const int nk = (K + MOE_BK - 1) / MOE_BK;
     auto load = [&](Stage & g, int kt) {
         const int64_t k0 = (int64_t)min(kt, nk - 1) * MOE_BK;   // past the end: a repeat nobody uses
-        g.a0 = load_a(arow0, k0, g.ok0);
-        g.a1 = load_a(arow1, k0, g.ok1);
-        g.w.load(W, rows_total, K, wrow, k0, wu, wok);
+        g.a0 = load_a(ap0, k0);
+        g.a1 = load_a(ap1, k0);
+        wl.load(g.w, a, k0, wok);
     };
     // the lane's B operand of the next slab to multiply (four runs of 8 fp16 weights) and the
     // slab's 8-k chunk each run holds
     u32x4 bq[4];
     int kc[4];
     auto store = [&](uint8_t * st, const Stage & g) {
-        const u32x4 z = {0, 0, 0, 0};
-        *(u32x4 *)(st + swz<8>(ar, ac)) = g.ok0 ? g.a0 : z;
-        *(u32x4 *)(st + swz<8>(ar + 32, ac)) = g.ok1 ? g.a1 : z;
+        *(u32x4 *)(st + swz<8>(ar, ac)) = g.a0;
+        *(u32x4 *)(st + swz<8>(ar + 32, ac)) = g.a1;
         int r0, r1;
         g.w.decode_fast(wu, bq, r0, r1);
         kc[0] = r0 / 8;
@@ -272,12 +302,8 @@ moe_gemm_kernel(MoeArgs a) {
 #pragma unroll
         for (int ks = 0; ks < MOE_BK / 16; ks++) {
             const half8 bf = __builtin_bit_cast(half8, bq[ks]);
-            const half8 a0 = *(const half8 *)(st + swz<8>(lr, kc[ks]));
-            acc[0] = mfma32(a0, bf, acc[0]);
-            if (two) {
-                const half8 a1 = *(const half8 *)(st + swz<8>(32 + lr, kc[ks]));
-                acc[1] = mfma32(a1, bf, acc[1]);
-            }
+            acc[0] = mfma32(*(const half8 *)(st + swz<8>(lr, kc[ks])), bf, acc[0]);
+            if (two) acc[1] = mfma32(*(const half8 *)(st + swz<8>(32 + lr, kc[ks])), bf, acc[1]);
         }
     };
 

@@ -450,16 +450,30 @@ constexpr int Q4KX_GROUP = 32;
 __host__ __device__ inline int64_t q4kx_block(int64_t row, int64_t blk, int64_t nblk) {
     return ((row / Q4KX_GROUP) * nblk + blk) * (Q4KX_GROUP * 144);
 }
+// The regrouped layouts are loaded through a Lane, the loop-invariant part of a lane's loads:
+// the expert's first group-block in each plane (block-uniform, so it lives in scalar registers)
+// and the 32-bit byte offsets of the lane's pieces from there (an expert is whole 32-row groups,
+// and the host keeps an expert's share of a plane under 2^31 bytes). A slab's load then adds a
+// block-uniform slab offset to the base and the fixed lane offset, with no per-lane address
+// arithmetic in the loop. `row0` is the expert's first row, `nloc` the lane's row inside it.
 template <> struct WLoad<T_Q4_KX> : WLoad<T_Q4_K> {
-    __device__ __forceinline__ void load(const uint8_t * W, int64_t rows, int64_t K, int64_t row,
-                                         int64_t k0, int u, bool ok_row) {
-        const int64_t blk = k0 / 256;
+    struct Lane {
+        const uint8_t * base;
+        uint32_t oh, oq;   // the row's header and its quant bytes of quarter 0, half u
+    };
+    __device__ __forceinline__ static Lane lane(const uint8_t * W, int64_t rows, int64_t K, int64_t row0, int nloc,
+                                                int u) {
+        const int64_t nblk = K / 256;
+        const uint32_t g = (uint32_t)(nloc / Q4KX_GROUP) * (uint32_t)nblk * (uint32_t)(Q4KX_GROUP * 144);
+        const int r = nloc % Q4KX_GROUP;
+        return {W + q4kx_block(row0, 0, nblk), g + 16u * r, g + 16u * Q4KX_GROUP + 32u * r + 16u * u};
+    }
+    __device__ __forceinline__ void load(const Lane & L, int64_t K, int64_t k0, bool ok_row) {
         j = (int)((k0 % 256) / 64);
         ok = ok_row;
-        const uint8_t * b = W + q4kx_block(row, blk, K / 256);
-        const int r = (int)(row % Q4KX_GROUP);
-        hdr = *(const u32x4 *)(b + 16 * r);
-        qs = *(const u32x4 *)(b + 16 * Q4KX_GROUP + 32 * Q4KX_GROUP * j + 32 * r + 16 * u);
+        const uint8_t * b = L.base + (k0 / 256) * (Q4KX_GROUP * 144);
+        hdr = *(const u32x4 *)(b + L.oh);
+        qs = *(const u32x4 *)((b + 32 * Q4KX_GROUP * j) + L.oq);
     }
 };
 
@@ -471,28 +485,49 @@ template <> struct WLoad<T_Q4_KX> : WLoad<T_Q4_K> {
 __host__ __device__ inline int64_t x32_index(int64_t row, int64_t blk, int64_t nblk) {
     return ((row / 32) * nblk + blk) * 32 + row % 32;
 }
+// A lane's item is block k0 / 32 + u; in the last slab of a K that is an odd number of blocks
+// the u = 1 item lies past K: it reads block k0 / 32 of its row (lane offsets o*0) and decodes to
+// zero.
 template <> struct WLoad<T_Q8_0X> : WLoad<T_Q8_0> {
-    __device__ __forceinline__ void load(const uint8_t * W, int64_t rows, int64_t K, int64_t row,
-                                         int64_t k0, int u, bool ok_row) {
-        int64_t k = k0 + 32 * u;
-        ok = ok_row && k < K;
-        k = k < K ? k : 0;
-        const int64_t x = x32_index(row, k / 32, K / 32);
-        const u32x4 * p = (const u32x4 *)(W + x * 32);
+    struct Lane {
+        const uint8_t * qb, * sb;   // the expert's first group-block of quants and of scales
+        uint32_t oq, os, oq0, os0;
+        int u;
+    };
+    __device__ __forceinline__ static Lane lane(const uint8_t * W, int64_t rows, int64_t K, int64_t row0, int nloc,
+                                                int u) {
+        const int64_t nblk = K / 32, x0 = x32_index(row0, 0, nblk);
+        const uint32_t gb = (uint32_t)(nloc / 32) * (uint32_t)nblk, r = (uint32_t)(nloc % 32);
+        const uint32_t oq0 = (gb * 32 + r) * 32, os0 = (gb * 32 + r) * 2;
+        return {W + x0 * 32, W + rows * K + x0 * 2, oq0 + 1024u * u, os0 + 64u * u, oq0, os0, u};
+    }
+    __device__ __forceinline__ void load(const Lane & L, int64_t K, int64_t k0, bool ok_row) {
+        ok = ok_row && k0 + 32 * L.u < K;
+        const int64_t b0 = k0 / 32;
+        const u32x4 * p = (const u32x4 *)((L.qb + b0 * 1024) + (ok ? L.oq : L.oq0));
         q[0] = p[0];
         q[1] = p[1];
-        d = ((const uint16_t *)(W + rows * K))[x];
+        d = *(const uint16_t *)((L.sb + b0 * 64) + (ok ? L.os : L.os0));
     }
 };
 template <> struct WLoad<T_MXFP4X> : WLoad<T_MXFP4> {
-    __device__ __forceinline__ void load(const uint8_t * W, int64_t rows, int64_t K, int64_t row,
-                                         int64_t k0, int u, bool ok_row) {
-        int64_t k = k0 + 32 * u;
-        ok = ok_row && k < K;
-        k = k < K ? k : 0;
-        const int64_t x = x32_index(row, k / 32, K / 32);
-        qs = *(const u32x4 *)(W + x * 16);
-        e = W[rows * (K / 2) + x];
+    struct Lane {
+        const uint8_t * qb, * sb;
+        uint32_t oq, os, oq0, os0;
+        int u;
+    };
+    __device__ __forceinline__ static Lane lane(const uint8_t * W, int64_t rows, int64_t K, int64_t row0, int nloc,
+                                                int u) {
+        const int64_t nblk = K / 32, x0 = x32_index(row0, 0, nblk);
+        const uint32_t gb = (uint32_t)(nloc / 32) * (uint32_t)nblk, r = (uint32_t)(nloc % 32);
+        const uint32_t oq0 = (gb * 32 + r) * 16, os0 = gb * 32 + r;
+        return {W + x0 * 16, W + rows * (K / 2) + x0, oq0 + 512u * u, os0 + 32u * u, oq0, os0, u};
+    }
+    __device__ __forceinline__ void load(const Lane & L, int64_t K, int64_t k0, bool ok_row) {
+        ok = ok_row && k0 + 32 * L.u < K;
+        const int64_t b0 = k0 / 32;
+        qs = *(const u32x4 *)((L.qb + b0 * 512) + (ok ? L.oq : L.oq0));
+        e = *((L.sb + b0 * 32) + (ok ? L.os : L.os0));
     }
 };
 
@@ -599,21 +634,32 @@ __host__ __device__ inline Q6kxPlanes q6kx_planes(int64_t rows, int64_t K, int64
             rows * (K / 2) + rows * (K / 4) + rows * (K / 16) + gb * 64, (int)(row % 32)};
 }
 template <> struct WLoad<T_Q6_KX> : WLoad<T_Q6_K> {
-    __device__ __forceinline__ void load(const uint8_t * W, int64_t rows, int64_t K, int64_t row,
-                                         int64_t k0, int u, bool ok_row) {
+    struct Lane {
+        const uint8_t * ql, * qh, * sc, * d;   // the expert's first group-block in each plane
+        uint32_t oql, oqh, osc, od;
+        uint32_t sel;   // byte permute taking scale bytes u and u + 2 of a scale word
+    };
+    __device__ __forceinline__ static Lane lane(const uint8_t * W, int64_t rows, int64_t K, int64_t row0, int nloc,
+                                                int u) {
+        const Q6kxPlanes p = q6kx_planes(rows, K, row0, 0);
+        const uint32_t gb = (uint32_t)(nloc / 32) * (uint32_t)(K / 256), r = (uint32_t)(nloc % 32);
+        return {W + p.ql, W + p.qh, W + p.sc, W + p.d, gb * 4096 + (32u * u + r) * 16, gb * 2048 + (32u * u + r) * 16,
+                gb * 512 + r * 16, gb * 64 + 2 * r, 0x0C0C0000u | ((uint32_t)(u + 2) << 8) | (uint32_t)u};
+    }
+    __device__ __forceinline__ void load(const Lane & L, int64_t K, int64_t k0, bool ok_row) {
         const int64_t blk = k0 / 256;
         const int q4 = (int)((k0 % 256) / 64);
         const int h = q4 >> 1;
         hi = q4 & 1;
         ok = ok_row;
-        const Q6kxPlanes p = q6kx_planes(rows, K, row, blk);
-        qla = *(const u32x4 *)(W + p.ql + ((4 * h + u) * 32 + p.r) * 16);
-        qlb = *(const u32x4 *)(W + p.ql + ((4 * h + 2 + u) * 32 + p.r) * 16);
-        qh = *(const u32x4 *)(W + p.qh + ((2 * h + u) * 32 + p.r) * 16);
+        const uint8_t * pl = L.ql + blk * 4096 + h * 2048;
+        qla = *(const u32x4 *)(pl + L.oql);
+        qlb = *(const u32x4 *)((pl + 1024) + L.oql);
+        qh = *(const u32x4 *)((L.qh + blk * 2048 + h * 1024) + L.oqh);
         // scales u + 4 hi and u + 4 hi + 2 of the half h: bytes u and u + 2 of one word
-        const uint32_t sw = *(const uint32_t *)(W + p.sc + p.r * 16 + 8 * h + 4 * hi);
-        sc = ((sw >> (8 * u)) & 0xFFu) | (((sw >> (8 * u + 16)) & 0xFFu) << 8);
-        d = *(const uint16_t *)(W + p.d + 2 * p.r);
+        const uint32_t sw = *(const uint32_t *)((L.sc + blk * 512 + 8 * h + 4 * hi) + L.osc);
+        sc = __builtin_amdgcn_perm(0u, sw, L.sel);
+        d = *(const uint16_t *)((L.d + blk * 64) + L.od);
     }
 };
 

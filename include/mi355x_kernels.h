@@ -317,7 +317,8 @@ MI355X_API size_t mi355x_mul_mat_id_workspace(const mi355x_moe_args * a);
  * are bucketed by expert on the device, and one grouped launch runs every (expert tile, N block)
  * with the expert's weight dequantized in LDS. An id outside [0, n_expert) leaves its row
  * unwritten and sets *err_dev (a device int32, may be NULL) to 1; the host-buffer path checks ids
- * before calling. K % 32 == 0 and a whole number of blocks, N % 16 == 0.
+ * before calling. K % 32 == 0 and a whole number of blocks, N % 16 == 0; for the layouts
+ * regrouped by 32 rows (MI355X_*_X) N % 32 == 0 and N * K <= 2^31 (one expert's weights).
  * Replaces the per-expert loop of ggml-rocket.cpp:6783-6941 and its device calls
  * rocket_matmul_int8_prepacked_gw (6833) / rocket_matmul_fp16_mt (6922). */
 MI355X_API int mi355x_mul_mat_id(const mi355x_moe_args * a, void * workspace_dev, size_t workspace_bytes,
