@@ -103,6 +103,21 @@ def test_x32_layout_argument_checks(x, base, bs):
     assert L.mi355x_weight_pack(xt, ctypes.c_void_p(a), 64, 512, ctypes.c_void_p(a), None) == mx.E_ARG
 
 
+def test_mul_mat_id_regrouped_layout_limits():
+    """mi355x_mul_mat_id takes the regrouped expert layouts for experts of whole 32-row groups
+    whose N * K fits 2^31 (the kernel's 32-bit offsets inside an expert), and refuses the rest
+    before touching the device (argument checks only: no GPU needed)."""
+    import ctypes
+    import ggml_mi355x as mx
+    L = mx.lib()
+    fake = ctypes.c_void_p(1 << 20)   # 16-byte aligned, never dereferenced on these paths
+    for x in ("Q4_K_X", "Q8_0_X", "Q6_K_X", "MXFP4_X"):
+        for N, K in [(48, 4096), (1 << 16, (1 << 15) + 256)]:
+            a = mx.MoeArgs(getattr(mx, x), fake, 8, N, K, fake, 1, K, K, fake, 2, 1, 2, 4, fake, N, 2 * N)
+            ws = L.mi355x_mul_mat_id_workspace(ctypes.byref(a))
+            assert L.mi355x_mul_mat_id(ctypes.byref(a), fake, ws, None, None) == mx.E_ARG, (x, N, K)
+
+
 def test_mul_mat_workspace_sizes_the_decode_first_weight():
     """mi355x_mul_mat_workspace_for makes room for the tiled fp16 weight where the decode-first
     form runs (Q6_K / Q5_K / MXFP4 at M >= 512; Q4_0 at M >= 1024, or at M >= 512 with N >= K;
