@@ -164,6 +164,24 @@ def test_moe_x32_layout(mx, K, N, E, ne11, U, T, base_name, x_name):
     check_bars(ref, got, N, 0.9990, f"moe {x_name} K={K} N={N} T={T}")
 
 
+@pytest.mark.parametrize("base_name,x_name", [("F16", None), ("Q4_0", None), ("Q8_0", "Q8_0_X"), ("MXFP4", "MXFP4_X")])
+def test_moe_k_ending_mid_slab(mx, base_name, x_name):
+    """K = 1056 ends half-way through the expert GEMM's last 64-deep slab (32-value blocks): the
+    chunks past K read zeros and the weights there decode to zero, in the row-strided layouts and
+    the regrouped ones alike (the same bits), within the oracle's bars."""
+    K, N, E, ne11, U, T = 1056, 64, 8, 2, 2, 40
+    wt = getattr(O, base_name)
+    P = expert_payload(wt, E, N, K)
+    X = make_input(T, ne11, K)
+    ids = make_ids(T, U, E)
+    base, _ = run(mx, wt, P, E, N, K, X, ids)
+    ref = O.mul_mat_id(wt, P, K, N, E, X, ne11, ids)
+    check_bars(ref, base, N, 0.9985, f"moe {base_name} K={K}")
+    if x_name:
+        got, _ = run(mx, getattr(mx, x_name), P, E, N, K, X, ids)
+        assert np.array_equal(base.view(np.uint32), got.view(np.uint32))
+
+
 @pytest.mark.parametrize("layout", ["q4_k", "q4_k_x"])
 @pytest.mark.parametrize("proj", ["gate", "up", "down"])
 def test_moe_baseline_shape(mx, proj, layout):
