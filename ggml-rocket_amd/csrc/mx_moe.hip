@@ -163,11 +163,12 @@ __global__ void __launch_bounds__(MOE_SORT_THREADS) moe_prep_kernel(MoeArgs a) {
 // K slabs ahead of the MFMAs, so an HBM round trip has R - 1 slabs of work to hide behind before
 // its data is decoded. 128-column blocks: 768 of them (128 experts x 6 column blocks of a
 // 768-wide gate/up) are one round of three blocks per CU over 256 CUs.
-// Waves per SIMD and register stages of slab lookahead: Q4_K (both layouts) and Q8_0 run four
-// waves a SIMD with two stages (128 registers), measured 1-12% faster than three waves with four
-// stages, most on the down projection's 2048 blocks; the other formats measured within 2% either
-// way and keep three waves with four stages, or three where the stage is wider (F16, Q5_K, Q6_K;
-// Q6_K would spill at four waves).
+// Waves per SIMD and register stages of slab lookahead: Q4_K, Q8_0 and MXFP4 (each in both
+// layouts) run four waves a SIMD with two stages (128 registers), measured 1-12% faster than
+// three waves with four stages, most on the down projection's 2048 blocks (MXFP4 since its packed
+// decoder fits); the other formats keep three waves with four stages, or three where the stage
+// is wider (F16, Q5_K, Q6_K; Q6_K would spill at four waves, and three stages at four waves
+// spill for every format).
 template <int WT> constexpr int moe_waves() {
     return (WT == T_Q4_K || WT == T_Q4_KX || WT == T_Q8_0 || WT == T_Q8_0X || WT == T_MXFP4 || WT == T_MXFP4X) ? 4 : 3;
 }
